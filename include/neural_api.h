@@ -1,0 +1,276 @@
+/*
+ * neural_api.h -- C ABI of libneural_hip.so, the MI355X (gfx950) implementation
+ * of Neural-Assembly's tensor hot path.
+ *
+ * Drop-in for the reference's neural_api.h on this path: same names, argument
+ * meaning, error codes and ownership rules, so the reference's ctypes layer
+ * (pyneural/core.py) can bind this library instead of libneural.so.  Each
+ * declaration names the reference interface it replaces (paths relative to
+ * the Neural-Assembly tree).  Declarations marked NEW have no reference
+ * counterpart; they are additive.
+ *
+ * Memory model (differs from the all-host reference):
+ *   - Tensors created by the library keep their data in device memory (HBM).
+ *     neural_tensor_data() / neural_buffer_info() return a host pointer and
+ *     synchronise device -> host first.  The pointer is valid for host reads
+ *     and writes until the next library call that takes the tensor; the next
+ *     such call uploads the host copy.  (The reference Python layer calls
+ *     neural_tensor_data() right before every memmove, which fits this.)
+ *   - neural_tensor_from_buffer() accepts a host pointer (kept host-
+ *     authoritative: uploaded before and written back after every call) or a
+ *     device pointer (used in place, no copies).
+ *   - Raw-pointer entry points (quantize_*, calibrate_*, *_has_nan, ...) accept
+ *     host or device pointers; host buffers are staged through HBM.
+ *   - Calls are stream-ordered on one HIP stream; results that come back by
+ *     value or through host pointers are synchronised before return.
+ */
+#ifndef NEURAL_HIP_API_H
+#define NEURAL_HIP_API_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+#if defined(__GNUC__)
+#pragma GCC visibility push(default)
+#endif
+
+/* Error codes: neural_api.h:15-35 (error.asm:11-29). */
+typedef enum {
+    NEURAL_OK                   = 0,
+    NEURAL_ERR_NULL_POINTER     = 1,
+    NEURAL_ERR_OUT_OF_MEMORY    = 2,
+    NEURAL_ERR_INVALID_ARGUMENT = 3,
+    NEURAL_ERR_SHAPE_MISMATCH   = 4,
+    NEURAL_ERR_DTYPE_MISMATCH   = 5,
+    NEURAL_ERR_FILE_NOT_FOUND   = 6,
+    NEURAL_ERR_FILE_READ        = 7,
+    NEURAL_ERR_FILE_WRITE       = 8,
+    NEURAL_ERR_PARSE_ERROR      = 9,
+    NEURAL_ERR_INVALID_CONFIG   = 10,
+    NEURAL_ERR_TENSOR_TOO_LARGE = 11,
+    NEURAL_ERR_INVALID_DTYPE    = 12,
+    NEURAL_ERR_DIM_MISMATCH     = 13,
+    NEURAL_ERR_NOT_IMPLEMENTED  = 14,
+    NEURAL_ERR_INTERNAL         = 15,
+    NEURAL_ERR_GRAD_CHECK       = 16,
+    NEURAL_ERR_NAN_DETECTED     = 17,
+    NEURAL_ERR_INF_DETECTED     = 18
+} NeuralError;
+
+/* dtype codes: neural_api.h:41-44. */
+typedef enum { NEURAL_DTYPE_FLOAT32 = 0, NEURAL_DTYPE_FLOAT64 = 1 } NeuralDtype;
+
+/* Opaque 64-byte tensor descriptor.  Offsets 0..39 keep the reference layout
+ * (tensor.asm:7-24): data@0, ndim@8, shape@16, stride@24 (bytes, the unit
+ * neural_tensor_stride() reports), dtype@32, flags@36. */
+typedef struct NeuralTensor NeuralTensor;
+
+/* ---- Framework / errors --------------------------------------------------- */
+int         neural_init(void);                       /* neural_api.h:68  (neural_api.asm:297-331) */
+void        neural_shutdown(void);                   /* neural_api.h:73 */
+const char *neural_version(void);                    /* neural_api.h:79 */
+void        neural_clear_error(void);                /* neural_api.h:88 */
+int         neural_get_last_error(void);             /* neural_api.h:94 (thread-local here; global at neural_api.asm:56) */
+const char *neural_get_error_message(int error_code);/* neural_api.h:101 (error.asm:32-50) */
+
+/* ---- Tensor API: neural_api.h:130-302, neural_api.asm:392-967,2293-2426 ---- */
+NeuralTensor   *neural_tensor_create(const uint64_t *shape, uint64_t ndim, int dtype);   /* neural_api.h:130 */
+NeuralTensor   *neural_tensor_zeros(const uint64_t *shape, uint64_t ndim, int dtype);    /* neural_api.h:139 */
+NeuralTensor   *neural_tensor_ones(const uint64_t *shape, uint64_t ndim, int dtype);     /* neural_api.h:148 */
+NeuralTensor   *neural_tensor_from_data(const void *data, const uint64_t *shape,
+                                        uint64_t ndim, int dtype);                       /* neural_api.h:167 */
+NeuralTensor   *neural_tensor_from_buffer(void *buffer, const uint64_t *shape, uint64_t ndim,
+                                          int dtype, const int64_t *strides);            /* neural_api.h:183 */
+const int64_t  *neural_tensor_stride(NeuralTensor *tensor);                              /* neural_api.h:190 */
+int             neural_tensor_is_contiguous(NeuralTensor *tensor);                       /* neural_api.h:197 */
+NeuralTensor   *neural_tensor_make_contiguous(NeuralTensor *tensor);                     /* neural_api.h:204 */
+
+/* neural_api.h:209-217; layout: data@0 itemsize@8 ndim@16 shape@24 strides@32
+ * readonly@40 format@44 (neural_api.asm:840-890). */
+typedef struct {
+    void           *data;
+    uint64_t        itemsize;
+    uint64_t        ndim;
+    const uint64_t *shape;
+    const int64_t  *strides;
+    int             readonly;
+    char            format[8];
+} NeuralBufferInfo;
+int             neural_buffer_info(NeuralTensor *tensor, NeuralBufferInfo *info);        /* neural_api.h:229 */
+
+void            neural_tensor_free(NeuralTensor *tensor);                                /* neural_api.h:235 */
+void           *neural_tensor_data(NeuralTensor *tensor);                                /* neural_api.h:242 */
+uint64_t        neural_tensor_ndim(NeuralTensor *tensor);                                /* neural_api.h:249 */
+const uint64_t *neural_tensor_shape(NeuralTensor *tensor);                               /* neural_api.h:256 */
+uint64_t        neural_tensor_numel(NeuralTensor *tensor);                               /* neural_api.h:263 */
+int             neural_tensor_dtype(NeuralTensor *tensor);                               /* neural_api.h:270 */
+uint64_t        neural_tensor_bytes(NeuralTensor *tensor);                               /* neural_api.h:277 */
+int             neural_tensor_fill(NeuralTensor *tensor, double value);                  /* neural_api.h:285 (tensor.asm:531-589) */
+int             neural_tensor_copy(NeuralTensor *dst, const NeuralTensor *src);          /* neural_api.h:293 (neural_api.asm:905-967) */
+NeuralTensor   *neural_tensor_reshape(NeuralTensor *tensor, const uint64_t *new_shape,
+                                      uint64_t new_ndim);                                /* neural_api.h:302 (tensor.asm:600-680) */
+
+/* NEW: explicit transfers and the device address, for callers that manage
+ * their own host buffers or hand the data to other HIP code. */
+int   neural_tensor_upload(NeuralTensor *tensor, const void *host_src, uint64_t bytes);
+int   neural_tensor_download(NeuralTensor *tensor, void *host_dst, uint64_t bytes);
+void *neural_tensor_device_data(NeuralTensor *tensor);
+
+/* ---- Elementwise / broadcast: neural_api.h:315-349, math_kernels.asm:66-945 */
+/* Shapes: equal element counts run flat (the reference loop, math_kernels.asm:
+ * 105-131); otherwise numpy broadcasting over up to 4 dims, honouring strides. */
+int neural_add(NeuralTensor *out, const NeuralTensor *a, const NeuralTensor *b);  /* neural_api.h:315, ew_add  math_kernels.asm:66 */
+int neural_sub(NeuralTensor *out, const NeuralTensor *a, const NeuralTensor *b);  /* neural_api.h:324, ew_sub  math_kernels.asm:182 */
+int neural_mul(NeuralTensor *out, const NeuralTensor *a, const NeuralTensor *b);  /* neural_api.h:333, ew_mul  math_kernels.asm:292 */
+int neural_div(NeuralTensor *out, const NeuralTensor *a, const NeuralTensor *b);  /* neural_api.h:342, ew_div  math_kernels.asm:402 */
+int neural_maximum(NeuralTensor *out, const NeuralTensor *a, const NeuralTensor *b); /* ew_max math_kernels.asm:730 */
+int neural_scalar_add(NeuralTensor *out, const NeuralTensor *a, double s);        /* ew_scalar_add math_kernels.asm:516 */
+int neural_scalar_mul(NeuralTensor *out, const NeuralTensor *a, double s);        /* ew_scalar_mul math_kernels.asm:625 */
+int neural_neg(NeuralTensor *out, const NeuralTensor *a);                         /* ew_neg math_kernels.asm:843 */
+/* Row-broadcast bias add out[i,j] = x[i,j] + bias[j]: nn_layers.asm:472-539. */
+int neural_bias_add(NeuralTensor *out, const NeuralTensor *x, const NeuralTensor *bias);
+
+/* Raw-pointer f32 kernels of simd.asm:190-784, destination first as there
+ * (host or device pointers; the reference returns void, these return 0 or an
+ * error code). */
+int   simd_add_f32(float *dst, const float *a, const float *b, uint64_t n);       /* simd.asm:190 */
+int   simd_mul_f32(float *dst, const float *a, const float *b, uint64_t n);       /* simd.asm:316 */
+int   simd_fma_f32(float *dst, const float *a, const float *b, const float *c,
+                   uint64_t n);                                                   /* simd.asm:436 (fused a*b+c) */
+float simd_dot_f32(const float *a, const float *b, uint64_t n);                   /* simd.asm:551 */
+float simd_sum_f32(const float *a, uint64_t n);                                   /* simd.asm:684 */
+
+/* ---- Reductions ------------------------------------------------------------- */
+/* neural_sum / neural_mean: neural_api.h:359,367 (stubs returning 14 at
+ * neural_api.asm:2446-2454; implemented here).  Result in double. */
+int neural_sum(const NeuralTensor *tensor, double *result);
+int neural_mean(const NeuralTensor *tensor, double *result);
+/* NEW full-tensor max (running-max semantics of activations.asm:888-895) and
+ * argmax (tensor_argmax, main.asm:3598-3640). */
+int neural_max(const NeuralTensor *tensor, double *result);
+int neural_argmax(const NeuralTensor *tensor, int64_t *result);
+/* reduce_sum / reduce_mean (math_kernels.asm:956-1264): axis -1 = all,
+ * 0 = column sums of a 2-D tensor, 1 = row sums; other ranks reduce the
+ * last dim when axis == ndim-1, else all.  Mean divides each output by its
+ * own count (the asm divides only out[0] by the total, math_kernels.asm:
+ * 1232-1256). */
+int neural_reduce_sum(const NeuralTensor *in, int64_t axis, NeuralTensor *out);
+int neural_reduce_mean(const NeuralTensor *in, int64_t axis, NeuralTensor *out);
+/* NEW row max (running maxss over the row, activations.asm:888-895) and row
+ * argmax (main.asm:3245-3270) over the last dim; indices are int64 written to
+ * a host or device pointer with rows entries. */
+int neural_reduce_max(const NeuralTensor *in, int64_t axis, NeuralTensor *out);
+int neural_reduce_argmax(const NeuralTensor *in, int64_t axis, int64_t *out_indices);
+
+/* ---- Activations -------------------------------------------------------------- */
+int neural_relu(NeuralTensor *out, const NeuralTensor *input);      /* neural_api.h:379, node_relu activations.asm:114-200 */
+int neural_sigmoid(NeuralTensor *out, const NeuralTensor *input);   /* neural_api.h:387, node_sigmoid activations.asm:318-413 */
+int neural_tanh(NeuralTensor *out, const NeuralTensor *input);      /* neural_api.h:395 */
+int neural_softmax(NeuralTensor *out, const NeuralTensor *input);   /* neural_api.h:403, node_softmax activations.asm:761-987 */
+/* NEW log-softmax rows, formula of metrics_losses.c:47-64. */
+int neural_log_softmax(NeuralTensor *out, const NeuralTensor *input);
+int neural_gelu(NeuralTensor *out, const NeuralTensor *input);                    /* neural_api.h:412 */
+int neural_leaky_relu(NeuralTensor *out, const NeuralTensor *input, double alpha);/* neural_api.h:421 */
+int neural_elu(NeuralTensor *out, const NeuralTensor *input, double alpha);       /* neural_api.h:431 */
+int neural_selu(NeuralTensor *out, const NeuralTensor *input);                    /* neural_api.h:441 */
+int neural_swish(NeuralTensor *out, const NeuralTensor *input);                   /* neural_api.h:450 */
+int neural_mish(NeuralTensor *out, const NeuralTensor *input);                    /* neural_api.h:459 */
+int neural_hardswish(NeuralTensor *out, const NeuralTensor *input);               /* neural_api.h:468 */
+int neural_softplus(NeuralTensor *out, const NeuralTensor *input);                /* neural_api.h:477 */
+int neural_hardtanh(NeuralTensor *out, const NeuralTensor *input);                /* neural_api.h:486 */
+/* Tensor-level activations (neural_api.h:494-503, activations_c.c:124-158). */
+int act_tanh(void *out, const void *in);
+int act_gelu(void *out, const void *in);
+int act_leaky_relu(void *out, const void *in, double alpha);
+int act_elu(void *out, const void *in, double alpha);
+int act_selu(void *out, const void *in);
+int act_swish(void *out, const void *in);
+int act_mish(void *out, const void *in);
+int act_hardswish(void *out, const void *in);
+int act_softplus(void *out, const void *in);
+int act_hardtanh(void *out, const void *in);
+
+/* ---- Optimizers: neural_api.h:510-517, optimizers_c.c:135-562 ----------------- */
+void   *opt_sgd_create(double lr, double momentum);                                   /* optimizers_c.c:135 */
+void   *opt_adam_create(double lr, double beta1, double beta2, double epsilon);       /* optimizers_c.c:145 */
+void   *opt_adamw_create(double lr, double beta1, double beta2, double epsilon,
+                         double weight_decay);                                        /* optimizers_c.c:158 */
+int     opt_step(void *opt, void **params, void **grads, int64_t n);                  /* optimizers_c.c:353 */
+void    opt_free(void *opt);                                                          /* optimizers_c.c:370 */
+double  opt_get_lr(void *opt);                                                        /* optimizers_c.c:378 */
+void    opt_set_lr(void *opt, double lr);                                             /* optimizers_c.c:384 */
+int64_t opt_state_bytes(void *opt);                                                   /* optimizers_c.c:398 */
+int     opt_state_export(void *opt, void *buffer, int64_t size);                      /* optimizers_c.c:417 */
+int     opt_state_import(void *opt, const void *buffer, int64_t size);                /* optimizers_c.c:480 */
+
+/* ---- INT8 quantization: neural_api.h:1008-1065, quantize.c:39-269 ------------- */
+/* Same 40-byte layout as the reference (scale@0 zero_point@8 min_val@16
+ * max_val@24 symmetric@32). */
+typedef struct {
+    double  scale;
+    int32_t zero_point;
+    double  min_val;
+    double  max_val;
+    int     symmetric;
+} QuantParams;
+int    calibrate_minmax(const double *data, int64_t n, int symmetric, QuantParams *out); /* quantize.c:52 */
+int    quantize_tensor(const double *data, int8_t *out, int64_t n, const QuantParams *p);/* quantize.c:144 */
+int    dequantize_tensor(const int8_t *data, double *out, int64_t n, const QuantParams *p);/* quantize.c:163 */
+double quantization_error(const double *original, int64_t n, const QuantParams *p);   /* quantize.c:222 */
+double quantization_snr(const double *original, int64_t n, const QuantParams *p);     /* quantize.c:247 */
+/* NEW fp32 variants (input widened to double exactly; same arithmetic). */
+int    calibrate_minmax_f32(const float *data, int64_t n, int symmetric, QuantParams *out);
+int    quantize_tensor_f32(const float *data, int8_t *out, int64_t n, const QuantParams *p);
+int    dequantize_tensor_f32(const int8_t *data, float *out, int64_t n, const QuantParams *p);
+double quantization_error_f32(const float *original, int64_t n, const QuantParams *p);
+double quantization_snr_f32(const float *original, int64_t n, const QuantParams *p);
+/* NEW device-resident pipeline: params are produced and consumed in device
+ * memory (no host round trip between calibration and quantization). */
+int    calibrate_minmax_f32_dev(const float *data, int64_t n, int symmetric, QuantParams *dev_params);
+int    quantize_tensor_f32_dev(const float *data, int8_t *out, int64_t n, const QuantParams *dev_params);
+int    dequantize_tensor_f32_dev(const int8_t *data, float *out, int64_t n, const QuantParams *dev_params);
+
+/* ---- Training ops: training_ops.asm:544-696 (neural_api.asm:2786-2791) -------- */
+int   neural_tensor_has_nan(const float *data, uint64_t n);      /* training_ops.asm:544 */
+int   neural_tensor_has_inf(const float *data, uint64_t n);      /* training_ops.asm:585 */
+float neural_tensor_grad_l2_norm(const float *data, uint64_t n); /* training_ops.asm:636 */
+/* NEW fused single pass: NaN flag, Inf flag and sum of squares (double). */
+int   neural_scan_nan_inf_l2(const float *data, uint64_t n, int *has_nan, int *has_inf,
+                             double *sumsq);
+/* NEW tensor-level forms (no host round trip for device-resident tensors). */
+int   neural_tensor_scan(NeuralTensor *t, int *has_nan, int *has_inf, double *sumsq);
+
+/* ---- 2-D f64 tensor ops: neural_api.h:1273-1305, tensor_ops.c:15-148 ---------- */
+int tensor_concat_2d(const double *a, const double *b, int64_t rows_a, int64_t cols_a,
+                     int64_t rows_b, int64_t cols_b, int64_t axis, double *out,
+                     int64_t *out_rows, int64_t *out_cols);
+int tensor_split_2d(const double *in, int64_t rows, int64_t cols, int64_t axis,
+                    int64_t split_index, double *out_a, double *out_b, int64_t *rows_a,
+                    int64_t *cols_a, int64_t *rows_b, int64_t *cols_b);
+int tensor_pad_2d(const double *in, int64_t in_rows, int64_t in_cols, int64_t pad_top,
+                  int64_t pad_bottom, int64_t pad_left, int64_t pad_right, double pad_value,
+                  double *out, int64_t *out_rows, int64_t *out_cols);
+int tensor_transpose2d_array(const double *in, int64_t rows, int64_t cols, double *out);
+
+/* ---- HIP runtime controls (NEW) ------------------------------------------------- */
+/* Use an existing HIP stream (e.g. torch.cuda.current_stream().cuda_stream) for
+ * all later launches; NULL restores the library's own stream.  The previous
+ * stream is synchronised first. */
+int   neural_hip_set_stream(void *hip_stream);
+void *neural_hip_get_stream(void);
+int   neural_hip_synchronize(void);
+/* Release cached device blocks back to the driver. */
+int   neural_hip_empty_cache(void);
+/* Device ordinal, compute-unit count and device name of the active GPU. */
+int   neural_hip_device_info(int *ordinal, int *num_cus, char *name, int name_len);
+
+#if defined(__GNUC__)
+#pragma GCC visibility pop
+#endif
+#ifdef __cplusplus
+}
+#endif
+#endif /* NEURAL_HIP_API_H */

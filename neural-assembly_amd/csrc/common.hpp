@@ -1,0 +1,171 @@
+// common.hpp -- shared runtime types and device helpers for libneural_hip.so.
+//
+// One process-wide runtime (device, stream, caching allocator, reduction
+// workspace) plus the 64-byte NeuralTensor descriptor whose first 40 bytes keep
+// the reference layout (tensor.asm:7-24).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <cstring>
+
+#include "../../include/neural_api.h"
+
+// ---------------------------------------------------------------------------
+// Tensor descriptor
+// ---------------------------------------------------------------------------
+
+// flags@36 keep the reference bits (tensor.asm:29-31).
+enum : int32_t { NT_OWN_DATA = 1, NT_OWN_META = 2 };
+
+// Where the authoritative bytes live.
+enum : int32_t { ST_DEVICE = 0, ST_HOST = 1, ST_SYNCED = 2 };
+
+// What the data pointer at offset 0 is.
+//   KIND_OWNED     library allocation: device buffer + lazily synced host mirror
+//   KIND_EXT_HOST  caller's host buffer (from_buffer): host is authoritative,
+//                  a device shadow is refreshed before and written back after use
+//   KIND_EXT_DEV   caller's device buffer (from_buffer): used in place
+//   KIND_VIEW      reshape view of another tensor (shares its storage)
+enum : int32_t { KIND_OWNED = 0, KIND_EXT_HOST = 1, KIND_EXT_DEV = 2, KIND_VIEW = 3 };
+
+struct Storage;
+
+struct NeuralTensor {
+    void     *data;    // 0   host-visible pointer to element 0 (device address for KIND_EXT_DEV)
+    int64_t   ndim;    // 8
+    int64_t  *shape;   // 16
+    int64_t  *stride;  // 24  byte strides
+    int32_t   dtype;   // 32  0 f32, 1 f64
+    int32_t   flags;   // 36
+    void     *dev;     // 40  device address of element 0
+    int32_t   kind;    // 48
+    int32_t   rsv;     // 52
+    Storage  *st;      // 56  shared storage record
+};
+static_assert(sizeof(NeuralTensor) == 64, "NeuralTensor must stay 64 bytes");
+static_assert(offsetof(NeuralTensor, dtype) == 32, "dtype offset");
+static_assert(offsetof(NeuralTensor, flags) == 36, "flags offset");
+
+// Storage shared between a tensor and its reshape views.  Byte span [lo, hi)
+// relative to element 0 covers every element the strides can reach.
+struct Storage {
+    int      refs;
+    int32_t  state;      // ST_*
+    int32_t  kind;       // KIND_OWNED / KIND_EXT_HOST / KIND_EXT_DEV
+    void    *host;       // mirror (owned) or caller buffer at element 0
+    void    *dev_block;  // device allocation (owned or shadow); null for EXT_DEV
+    size_t   dev_bytes;
+    int64_t  lo, hi;     // byte span relative to element 0
+    bool     host_owned; // host mirror allocated by us
+};
+
+namespace nh {
+
+// ---------------------------------------------------------------------------
+// Runtime
+// ---------------------------------------------------------------------------
+int          ensure_init();              // NEURAL_OK or error code (lazy init)
+hipStream_t  stream();                   // active stream
+int          num_cus();
+int          set_error(int code);        // stores thread-local last error, returns code
+int          hip_fail(hipError_t e);     // maps a HIP error to NEURAL_ERR_* and records it
+
+void        *dev_alloc(size_t bytes);    // caching allocator (stream-ordered reuse)
+void         dev_free(void *p);
+
+// Per-runtime device workspace for multi-block reductions: partial results
+// plus a self-resetting completion counter (the last block sets it back to 0).
+struct Workspace {
+    void         *partials;    // kMaxPartials * 64 bytes
+    unsigned int *counter;     // kCounters counters, all zero between calls
+    void         *result;      // 256 bytes of small results
+};
+constexpr int kMaxPartials = 4096;
+constexpr int kCounters = 64;
+Workspace   &workspace();
+
+// Raw pointer classification for the pointer-taking entry points.
+bool         is_device_ptr(const void *p);
+
+// Stage a caller pointer into device memory.  For device pointers the
+// pointer itself is used; for host pointers a device block is allocated and
+// (when upload) filled.  finish() copies back (when download) and frees.
+struct Staged {
+    void  *dev = nullptr;
+    void  *host = nullptr;
+    size_t bytes = 0;
+    bool   owned = false;
+    int    open(const void *p, size_t nbytes, bool upload);
+    int    finish(bool download);
+    ~Staged();
+};
+
+// Tensor coherence
+int64_t      numel(const NeuralTensor *t);
+size_t       elem_size(int dtype);
+bool         is_contiguous(const NeuralTensor *t);
+int          check_tensor(const NeuralTensor *t);   // null / dtype validation
+// Make the device copy current and return its element-0 address.
+int          dev_read(const NeuralTensor *t, const void **p);
+// Prepare for a write; `full` = every element will be overwritten.
+int          dev_write(NeuralTensor *t, void **p, bool full);
+// After kernels that wrote `t` were enqueued: mark/propagate.
+int          dev_written(NeuralTensor *t);
+
+// Launch helpers
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+int          check_launch();                         // hipGetLastError -> error code
+int          sync();                                 // synchronise the active stream
+
+}  // namespace nh
+
+// ---------------------------------------------------------------------------
+// Device helpers
+// ---------------------------------------------------------------------------
+
+#define NH_DEV __device__ __forceinline__
+
+// Wave64 butterfly reductions; fixed pairing, so results are deterministic.
+template <typename T>
+NH_DEV T wave_sum(T v)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+template <typename T>
+NH_DEV T wave_max_ignore_nan(T v)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        T o = __shfl_xor(v, off, 64);
+        v = (v != v) ? o : ((o != o) ? v : (o > v ? o : v));
+    }
+    return v;
+}
+
+// 128-bit vector load/store helpers.
+template <typename T> struct Vec16;
+template <> struct Vec16<float>  { using type = float4;  static constexpr int n = 4; };
+template <> struct Vec16<double> { using type = double2; static constexpr int n = 2; };
+
+NH_DEV float  vget(const float4 &v, int i)  { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+NH_DEV double vget(const double2 &v, int i) { return i == 0 ? v.x : v.y; }
+NH_DEV void   vset(float4 &v, int i, float x)   { if (i == 0) v.x = x; else if (i == 1) v.y = x; else if (i == 2) v.z = x; else v.w = x; }
+NH_DEV void   vset(double2 &v, int i, double x) { if (i == 0) v.x = x; else v.y = x; }
+
+// Error-return helper for host code.
+#define NH_TRY(expr)                          \
+    do {                                      \
+        int rc__ = (expr);                    \
+        if (rc__ != NEURAL_OK) return rc__;   \
+    } while (0)
+#define NH_HIP(expr)                                   \
+    do {                                               \
+        hipError_t e__ = (expr);                       \
+        if (e__ != hipSuccess) return nh::hip_fail(e__); \
+    } while (0)

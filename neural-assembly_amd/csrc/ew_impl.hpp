@@ -1,0 +1,257 @@
+// ew_impl.hpp -- streaming elementwise machinery for gfx950.
+//
+// Flat kernels move 128-bit vectors (float4 / double2): each 256-lane block
+// owns a contiguous tile of 256*U vectors, issues all U loads per operand
+// before any store, and block 0 finishes the n % VN tail.  Inputs that are
+// not 16-byte aligned take the scalar variant.  Strided / broadcast operands
+// (up to 4 dims after merging) take the N-D kernel with per-element index
+// decomposition.
+#pragma once
+
+#include "common.hpp"
+
+namespace nh {
+
+constexpr int kBlock = 256;
+constexpr int kUnroll = 4;
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ---- flat binary ----------------------------------------------------------
+template <typename T, typename Op>
+__global__ __launch_bounds__(kBlock) void k_map2_flat(const T *__restrict__ a, const T *__restrict__ b,
+                                                      T *__restrict__ o, int64_t n, Op op)
+{
+    using V = typename Vec16<T>::type;
+    constexpr int VN = Vec16<T>::n;
+    const int64_t nv = n / VN;
+    const V *av = reinterpret_cast<const V *>(a);
+    const V *bv = reinterpret_cast<const V *>(b);
+    V *ov = reinterpret_cast<V *>(o);
+    const int64_t base = int64_t(blockIdx.x) * (kBlock * kUnroll) + threadIdx.x;
+    V ra[kUnroll], rb[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {
+        const int64_t i = base + int64_t(u) * kBlock;
+        if (i < nv) { ra[u] = av[i]; rb[u] = bv[i]; }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {
+        const int64_t i = base + int64_t(u) * kBlock;
+        if (i < nv) {
+            V r;
+#pragma unroll
+            for (int k = 0; k < VN; k++) vset(r, k, op(vget(ra[u], k), vget(rb[u], k)));
+            ov[i] = r;
+        }
+    }
+    if (blockIdx.x == 0) {
+        const int64_t j = nv * VN + threadIdx.x;
+        if (j < n) o[j] = op(a[j], b[j]);
+    }
+}
+
+template <typename T, typename Op>
+__global__ __launch_bounds__(kBlock) void k_map2_flat_scalar(const T *a, const T *b, T *o, int64_t n, Op op)
+{
+    const int64_t stride = int64_t(gridDim.x) * kBlock;
+    for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) o[i] = op(a[i], b[i]);
+}
+
+// ---- flat unary (same element width in and out) ----------------------------
+template <typename T, typename F>
+__global__ __launch_bounds__(kBlock) void k_map1_flat(const T *__restrict__ a, T *__restrict__ o, int64_t n, F f)
+{
+    using V = typename Vec16<T>::type;
+    constexpr int VN = Vec16<T>::n;
+    const int64_t nv = n / VN;
+    const V *av = reinterpret_cast<const V *>(a);
+    V *ov = reinterpret_cast<V *>(o);
+    const int64_t base = int64_t(blockIdx.x) * (kBlock * kUnroll) + threadIdx.x;
+    V ra[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {
+        const int64_t i = base + int64_t(u) * kBlock;
+        if (i < nv) ra[u] = av[i];
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {
+        const int64_t i = base + int64_t(u) * kBlock;
+        if (i < nv) {
+            V r;
+#pragma unroll
+            for (int k = 0; k < VN; k++) vset(r, k, f(vget(ra[u], k)));
+            ov[i] = r;
+        }
+    }
+    if (blockIdx.x == 0) {
+        const int64_t j = nv * VN + threadIdx.x;
+        if (j < n) o[j] = f(a[j]);
+    }
+}
+
+template <typename T, typename F>
+__global__ __launch_bounds__(kBlock) void k_map1_flat_scalar(const T *a, T *o, int64_t n, F f)
+{
+    const int64_t stride = int64_t(gridDim.x) * kBlock;
+    for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) o[i] = f(a[i]);
+}
+
+// ---- row broadcast: o[r, c] = op(a[r, c], b[c]) -----------------------------
+// Rows on grid.x (ROWS per block), 256 column vectors on grid.y; the bias
+// vector stays in registers while the block walks its rows.
+constexpr int kRowsPerBlock = 8;
+
+template <typename T, typename Op>
+__global__ __launch_bounds__(kBlock) void k_rowbcast(const T *__restrict__ a, const T *__restrict__ b,
+                                                     T *__restrict__ o, int64_t rows, int64_t cols, Op op)
+{
+    using V = typename Vec16<T>::type;
+    constexpr int VN = Vec16<T>::n;
+    const int64_t ncv = cols / VN;
+    const int64_t cv = int64_t(blockIdx.y) * kBlock + threadIdx.x;
+    if (cv >= ncv) return;
+    const V bb = reinterpret_cast<const V *>(b)[cv];
+    const int64_t r0 = int64_t(blockIdx.x) * kRowsPerBlock;
+    V ra[kRowsPerBlock];
+#pragma unroll
+    for (int u = 0; u < kRowsPerBlock; u++) {
+        const int64_t r = r0 + u;
+        if (r < rows) ra[u] = reinterpret_cast<const V *>(a + r * cols)[cv];
+    }
+#pragma unroll
+    for (int u = 0; u < kRowsPerBlock; u++) {
+        const int64_t r = r0 + u;
+        if (r < rows) {
+            V res;
+#pragma unroll
+            for (int k = 0; k < VN; k++) vset(res, k, op(vget(ra[u], k), vget(bb, k)));
+            reinterpret_cast<V *>(o + r * cols)[cv] = res;
+        }
+    }
+}
+
+// ---- N-D strided / broadcast (<= 4 dims, element strides) --------------------
+struct ND4 {
+    int64_t shape[4];
+    int64_t so[4], sa[4], sb[4];
+};
+
+NH_DEV void nd_offsets(const ND4 &d, int64_t idx, int64_t &oo, int64_t &oa, int64_t &ob)
+{
+    int64_t i3 = idx % d.shape[3];
+    int64_t r = idx / d.shape[3];
+    int64_t i2 = r % d.shape[2];
+    r /= d.shape[2];
+    int64_t i1 = r % d.shape[1];
+    int64_t i0 = r / d.shape[1];
+    oo = i0 * d.so[0] + i1 * d.so[1] + i2 * d.so[2] + i3 * d.so[3];
+    oa = i0 * d.sa[0] + i1 * d.sa[1] + i2 * d.sa[2] + i3 * d.sa[3];
+    ob = i0 * d.sb[0] + i1 * d.sb[1] + i2 * d.sb[2] + i3 * d.sb[3];
+}
+
+template <typename T, typename Op>
+__global__ __launch_bounds__(kBlock) void k_map2_nd(const T *a, const T *b, T *o, int64_t n, ND4 d, Op op)
+{
+    const int64_t stride = int64_t(gridDim.x) * kBlock;
+    for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+        int64_t oo, oa, ob;
+        nd_offsets(d, i, oo, oa, ob);
+        o[oo] = op(a[oa], b[ob]);
+    }
+}
+
+template <typename T, typename F>
+__global__ __launch_bounds__(kBlock) void k_map1_nd(const T *a, T *o, int64_t n, ND4 d, F f)
+{
+    const int64_t stride = int64_t(gridDim.x) * kBlock;
+    for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+        int64_t oo, oa, ob;
+        nd_offsets(d, i, oo, oa, ob);
+        o[oo] = f(a[oa]);
+    }
+}
+
+// ---- host-side launch helpers ---------------------------------------------------
+
+inline unsigned flat_grid(int64_t n, int vn)
+{
+    const int64_t nv = n / vn;
+    int64_t g = ceil_div(nv, int64_t(kBlock) * kUnroll);
+    return unsigned(g < 1 ? 1 : g);
+}
+
+inline unsigned strided_grid(int64_t n)
+{
+    int64_t g = ceil_div(n, kBlock);
+    const int64_t cap = int64_t(num_cus()) * 16;
+    if (g > cap) g = cap;
+    return unsigned(g < 1 ? 1 : g);
+}
+
+template <typename T, typename Op>
+int launch_map2_flat(const T *a, const T *b, T *o, int64_t n, Op op)
+{
+    if (n <= 0) return NEURAL_OK;
+    if (aligned16(a) && aligned16(b) && aligned16(o))
+        hipLaunchKernelGGL((k_map2_flat<T, Op>), dim3(flat_grid(n, Vec16<T>::n)), dim3(kBlock), 0, stream(), a, b, o, n, op);
+    else
+        hipLaunchKernelGGL((k_map2_flat_scalar<T, Op>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(), a, b, o, n, op);
+    return check_launch();
+}
+
+template <typename T, typename F>
+int launch_map1_flat(const T *a, T *o, int64_t n, F f)
+{
+    if (n <= 0) return NEURAL_OK;
+    if (aligned16(a) && aligned16(o))
+        hipLaunchKernelGGL((k_map1_flat<T, F>), dim3(flat_grid(n, Vec16<T>::n)), dim3(kBlock), 0, stream(), a, o, n, f);
+    else
+        hipLaunchKernelGGL((k_map1_flat_scalar<T, F>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(), a, o, n, f);
+    return check_launch();
+}
+
+// Broadcast layout of up to three operands against the output shape.
+// Returns NEURAL_OK and fills `d` (element strides, merged and left-padded to
+// 4 dims), or SHAPE_MISMATCH / DIM_MISMATCH.
+int build_nd(const NeuralTensor *out, const NeuralTensor *a, const NeuralTensor *b, ND4 &d);
+
+// Unary op over tensors (contiguous fast path, else N-D); `in` and `out`
+// must have the same dtype and element count.
+template <typename F32, typename F64>
+int run_unary(NeuralTensor *out, const NeuralTensor *in, F32 f32, F64 f64)
+{
+    NH_TRY(ensure_init());
+    if (!out || !in) return set_error(NEURAL_ERR_NULL_POINTER);
+    NH_TRY(check_tensor(in));
+    NH_TRY(check_tensor(out));
+    if (in->dtype != out->dtype) return set_error(NEURAL_ERR_DTYPE_MISMATCH);
+    const int64_t n = numel(in);
+    if (numel(out) != n) return set_error(NEURAL_ERR_SHAPE_MISMATCH);
+    if (n == 0) return set_error(NEURAL_OK);
+    const void *src = nullptr;
+    void *dst = nullptr;
+    NH_TRY(dev_read(in, &src));
+    const bool flat = is_contiguous(in) && is_contiguous(out);
+    NH_TRY(dev_write(out, &dst, is_contiguous(out)));
+    if (flat) {
+        if (in->dtype == NEURAL_DTYPE_FLOAT32)
+            NH_TRY(launch_map1_flat(static_cast<const float *>(src), static_cast<float *>(dst), n, f32));
+        else
+            NH_TRY(launch_map1_flat(static_cast<const double *>(src), static_cast<double *>(dst), n, f64));
+    } else {
+        ND4 d;
+        NH_TRY(build_nd(out, in, nullptr, d));
+        if (in->dtype == NEURAL_DTYPE_FLOAT32)
+            hipLaunchKernelGGL((k_map1_nd<float, F32>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(),
+                               static_cast<const float *>(src), static_cast<float *>(dst), n, d, f32);
+        else
+            hipLaunchKernelGGL((k_map1_nd<double, F64>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(),
+                               static_cast<const double *>(src), static_cast<double *>(dst), n, d, f64);
+        NH_TRY(check_launch());
+    }
+    NH_TRY(dev_written(out));
+    return set_error(NEURAL_OK);
+}
+
+}  // namespace nh

@@ -1,0 +1,482 @@
+// optim.hip -- SGD / Adam / AdamW with device-resident float64 moments.
+//
+// Reference: optimizers_c.c:64-562.  The handle keeps the hyper-parameters,
+// the step count and per-parameter float64 moment buffers that are allocated
+// (zeroed) on the first step and sized by numel(param).  Here the buffers
+// live in HBM and each step is one fused kernel per parameter tensor that
+// reads param, grad, m, v once and writes param, m, v once.
+//
+// Per-element arithmetic is the reference's, in double, in the same order,
+// without FMA contraction; the bias corrections bc1 = 1 - pow(beta1, t),
+// bc2 = 1 - pow(beta2, t) are computed on the host with libm pow as in
+// optimizers_c.c:258-260,302-304 and passed in, so params, m and v match the
+// reference bit for bit.
+//
+// OPTS state blob (optimizers_c.c:84-100,391-562): 80-byte header, then
+// int64 sizes, then f64 velocities (SGD) or all m followed by all v.
+#include <cmath>
+#include <cstdlib>
+#include <vector>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace nh {
+
+enum { OPT_SGD = 0, OPT_ADAM = 1, OPT_ADAMW = 2 };
+
+struct OptHandle {
+    int type;
+    double lr, momentum, beta1, beta2, eps, wd;
+    int64_t t;
+    int64_t n_params;
+    std::vector<int64_t> sizes;
+    std::vector<double *> m, v, vel;  // device buffers
+};
+
+struct OptStateHeader {
+    uint32_t magic;
+    uint32_t version;
+    int32_t type;
+    int32_t reserved;
+    int64_t n_params;
+    double lr, momentum, beta1, beta2, epsilon, weight_decay;
+    int64_t t;
+};
+static_assert(sizeof(OptStateHeader) == 80, "OPTS header is 80 bytes");
+constexpr uint32_t kOptsMagic = 0x5354504Fu;  // 'OPTS'
+constexpr uint32_t kOptsVersion = 1u;
+
+static void free_moments(OptHandle *o)
+{
+    for (double *p : o->m) dev_free(p);
+    for (double *p : o->v) dev_free(p);
+    for (double *p : o->vel) dev_free(p);
+    o->m.clear();
+    o->v.clear();
+    o->vel.clear();
+    o->sizes.clear();
+    o->n_params = 0;
+}
+
+static double *alloc_zeroed(int64_t n)
+{
+    double *p = static_cast<double *>(dev_alloc(size_t(n > 0 ? n : 1) * sizeof(double)));
+    if (p && n > 0 && launch_fill(p, NEURAL_DTYPE_FLOAT64, n, 0.0) != NEURAL_OK) {
+        dev_free(p);
+        return nullptr;
+    }
+    return p;
+}
+
+// ---- kernels -------------------------------------------------------------------------
+
+struct AdamArgs {
+    double lr, b1, b2, eps, wd, bc1, bc2;
+};
+
+// adamw_step_impl f32 body (optimizers_c.c:313-330).
+NH_DEV float adamw_f32(float pd, float gd, double &m, double &v, const AdamArgs &a)
+{
+    double param = double(pd);
+    const double grad = double(gd);
+    param -= a.lr * a.wd * param;
+    m = a.b1 * m + (1.0 - a.b1) * grad;
+    v = a.b2 * v + (1.0 - a.b2) * grad * grad;
+    const double mh = m / a.bc1;
+    const double vh = v / a.bc2;
+    param -= a.lr * mh / (sqrt(vh) + a.eps);
+    return float(param);
+}
+
+NH_DEV double adamw_f64(double pd, double gd, double &m, double &v, const AdamArgs &a)
+{
+    double param = pd;
+    param -= a.lr * a.wd * param;
+    m = a.b1 * m + (1.0 - a.b1) * gd;
+    v = a.b2 * v + (1.0 - a.b2) * gd * gd;
+    const double mh = m / a.bc1;
+    const double vh = v / a.bc2;
+    param -= a.lr * mh / (sqrt(vh) + a.eps);
+    return param;
+}
+
+// adam_step_impl (optimizers_c.c:270-291): the f32 step is rounded to float and
+// subtracted in float.
+NH_DEV float adam_f32(float pd, float gd, double &m, double &v, const AdamArgs &a)
+{
+    const double grad = double(gd);
+    m = a.b1 * m + (1.0 - a.b1) * grad;
+    v = a.b2 * v + (1.0 - a.b2) * grad * grad;
+    const double mh = m / a.bc1;
+    const double vh = v / a.bc2;
+    return pd - float(a.lr * mh / (sqrt(vh) + a.eps));
+}
+
+NH_DEV double adam_f64(double pd, double gd, double &m, double &v, const AdamArgs &a)
+{
+    m = a.b1 * m + (1.0 - a.b1) * gd;
+    v = a.b2 * v + (1.0 - a.b2) * gd * gd;
+    const double mh = m / a.bc1;
+    const double vh = v / a.bc2;
+    return pd - a.lr * mh / (sqrt(vh) + a.eps);
+}
+
+constexpr int kOBlock = 256;
+
+// Four f32 elements per thread-step: float4 param/grad, 2x double2 m and v.
+template <bool W>
+__global__ __launch_bounds__(kOBlock) void k_adam_f32(float *__restrict__ p, const float *__restrict__ g,
+                                                      double *__restrict__ m, double *__restrict__ v, int64_t n,
+                                                      AdamArgs a)
+{
+    const int64_t n4 = n / 4;
+    const int64_t stride = int64_t(gridDim.x) * kOBlock;
+    for (int64_t i = int64_t(blockIdx.x) * kOBlock + threadIdx.x; i < n4; i += stride) {
+        float4 pv = reinterpret_cast<float4 *>(p)[i];
+        const float4 gv = reinterpret_cast<const float4 *>(g)[i];
+        double2 m0 = reinterpret_cast<double2 *>(m)[2 * i], m1 = reinterpret_cast<double2 *>(m)[2 * i + 1];
+        double2 v0 = reinterpret_cast<double2 *>(v)[2 * i], v1 = reinterpret_cast<double2 *>(v)[2 * i + 1];
+        if (W) {
+            pv.x = adamw_f32(pv.x, gv.x, m0.x, v0.x, a);
+            pv.y = adamw_f32(pv.y, gv.y, m0.y, v0.y, a);
+            pv.z = adamw_f32(pv.z, gv.z, m1.x, v1.x, a);
+            pv.w = adamw_f32(pv.w, gv.w, m1.y, v1.y, a);
+        } else {
+            pv.x = adam_f32(pv.x, gv.x, m0.x, v0.x, a);
+            pv.y = adam_f32(pv.y, gv.y, m0.y, v0.y, a);
+            pv.z = adam_f32(pv.z, gv.z, m1.x, v1.x, a);
+            pv.w = adam_f32(pv.w, gv.w, m1.y, v1.y, a);
+        }
+        reinterpret_cast<float4 *>(p)[i] = pv;
+        reinterpret_cast<double2 *>(m)[2 * i] = m0;
+        reinterpret_cast<double2 *>(m)[2 * i + 1] = m1;
+        reinterpret_cast<double2 *>(v)[2 * i] = v0;
+        reinterpret_cast<double2 *>(v)[2 * i + 1] = v1;
+    }
+    if (blockIdx.x == 0) {
+        const int64_t j = n4 * 4 + threadIdx.x;
+        if (j < n) p[j] = W ? adamw_f32(p[j], g[j], m[j], v[j], a) : adam_f32(p[j], g[j], m[j], v[j], a);
+    }
+}
+
+template <bool W>
+__global__ __launch_bounds__(kOBlock) void k_adam_f32_scalar(float *p, const float *g, double *m, double *v,
+                                                             int64_t n, AdamArgs a)
+{
+    const int64_t stride = int64_t(gridDim.x) * kOBlock;
+    for (int64_t j = int64_t(blockIdx.x) * kOBlock + threadIdx.x; j < n; j += stride)
+        p[j] = W ? adamw_f32(p[j], g[j], m[j], v[j], a) : adam_f32(p[j], g[j], m[j], v[j], a);
+}
+
+template <bool W>
+__global__ __launch_bounds__(kOBlock) void k_adam_f64(double *p, const double *g, double *m, double *v, int64_t n,
+                                                      AdamArgs a)
+{
+    const int64_t stride = int64_t(gridDim.x) * kOBlock;
+    for (int64_t j = int64_t(blockIdx.x) * kOBlock + threadIdx.x; j < n; j += stride)
+        p[j] = W ? adamw_f64(p[j], g[j], m[j], v[j], a) : adam_f64(p[j], g[j], m[j], v[j], a);
+}
+
+// sgd_step_impl (optimizers_c.c:218-249).
+__global__ __launch_bounds__(kOBlock) void k_sgd_f32(float *p, const float *g, double *vel, int64_t n, double lr,
+                                                     double mom)
+{
+    const int64_t stride = int64_t(gridDim.x) * kOBlock;
+    for (int64_t j = int64_t(blockIdx.x) * kOBlock + threadIdx.x; j < n; j += stride) {
+        const double grad = double(g[j]);
+        const double nv = mom * vel[j] + grad;
+        vel[j] = nv;
+        p[j] = p[j] - float(lr * nv);
+    }
+}
+
+__global__ __launch_bounds__(kOBlock) void k_sgd_f64(double *p, const double *g, double *vel, int64_t n, double lr,
+                                                     double mom)
+{
+    const int64_t stride = int64_t(gridDim.x) * kOBlock;
+    for (int64_t j = int64_t(blockIdx.x) * kOBlock + threadIdx.x; j < n; j += stride) {
+        const double nv = mom * vel[j] + g[j];
+        vel[j] = nv;
+        p[j] -= lr * nv;
+    }
+}
+
+inline unsigned o_grid(int64_t work)
+{
+    int64_t g = ceil_div(work, kOBlock);
+    const int64_t cap = int64_t(num_cus()) * 16;
+    if (g > cap) g = cap;
+    return unsigned(g < 1 ? 1 : g);
+}
+
+static int step_param(OptHandle *o, size_t i, NeuralTensor *p, const NeuralTensor *g, const AdamArgs &a)
+{
+    const int64_t sz = o->sizes[i];
+    if (!p || !g) return set_error(NEURAL_ERR_NULL_POINTER);
+    NH_TRY(check_tensor(p));
+    if (g->dtype != p->dtype) return set_error(NEURAL_ERR_DTYPE_MISMATCH);
+    if (numel(p) != sz || numel(g) != sz) return set_error(NEURAL_ERR_SHAPE_MISMATCH);
+    if (!is_contiguous(p) || !is_contiguous(g)) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
+    if (sz == 0) return NEURAL_OK;
+    const void *gp = nullptr;
+    const void *pr = nullptr;
+    void *pw = nullptr;
+    NH_TRY(dev_read(g, &gp));
+    NH_TRY(dev_read(p, &pr));
+    NH_TRY(dev_write(p, &pw, false));
+    if (o->type == OPT_SGD) {
+        if (p->dtype == NEURAL_DTYPE_FLOAT32)
+            hipLaunchKernelGGL(k_sgd_f32, dim3(o_grid(sz)), dim3(kOBlock), 0, stream(), static_cast<float *>(pw),
+                               static_cast<const float *>(gp), o->vel[i], sz, o->lr, o->momentum);
+        else
+            hipLaunchKernelGGL(k_sgd_f64, dim3(o_grid(sz)), dim3(kOBlock), 0, stream(), static_cast<double *>(pw),
+                               static_cast<const double *>(gp), o->vel[i], sz, o->lr, o->momentum);
+    } else {
+        const bool w = o->type == OPT_ADAMW;
+        if (p->dtype == NEURAL_DTYPE_FLOAT32) {
+            float *P = static_cast<float *>(pw);
+            const float *G = static_cast<const float *>(gp);
+            const bool vec = ((reinterpret_cast<uintptr_t>(P) | reinterpret_cast<uintptr_t>(G)) & 15u) == 0;
+            if (vec) {
+                if (w) hipLaunchKernelGGL(k_adam_f32<true>, dim3(o_grid(sz / 4)), dim3(kOBlock), 0, stream(), P, G, o->m[i], o->v[i], sz, a);
+                else hipLaunchKernelGGL(k_adam_f32<false>, dim3(o_grid(sz / 4)), dim3(kOBlock), 0, stream(), P, G, o->m[i], o->v[i], sz, a);
+            } else {
+                if (w) hipLaunchKernelGGL(k_adam_f32_scalar<true>, dim3(o_grid(sz)), dim3(kOBlock), 0, stream(), P, G, o->m[i], o->v[i], sz, a);
+                else hipLaunchKernelGGL(k_adam_f32_scalar<false>, dim3(o_grid(sz)), dim3(kOBlock), 0, stream(), P, G, o->m[i], o->v[i], sz, a);
+            }
+        } else {
+            double *P = static_cast<double *>(pw);
+            const double *G = static_cast<const double *>(gp);
+            if (w) hipLaunchKernelGGL(k_adam_f64<true>, dim3(o_grid(sz)), dim3(kOBlock), 0, stream(), P, G, o->m[i], o->v[i], sz, a);
+            else hipLaunchKernelGGL(k_adam_f64<false>, dim3(o_grid(sz)), dim3(kOBlock), 0, stream(), P, G, o->m[i], o->v[i], sz, a);
+        }
+    }
+    NH_TRY(check_launch());
+    NH_TRY(dev_written(p));
+    return NEURAL_OK;
+}
+
+static OptHandle *make(int type)
+{
+    if (ensure_init() != NEURAL_OK) return nullptr;
+    OptHandle *o = new (std::nothrow) OptHandle();
+    if (!o) return nullptr;
+    o->type = type;
+    o->lr = o->momentum = o->beta1 = o->beta2 = o->eps = o->wd = 0.0;
+    o->t = 0;
+    o->n_params = 0;
+    return o;
+}
+
+static int64_t total_elems(const OptHandle *o)
+{
+    int64_t t = 0;
+    for (int64_t s : o->sizes) {
+        if (s < 0) return -1;
+        t += s;
+    }
+    return t;
+}
+
+}  // namespace nh
+
+using namespace nh;
+
+extern "C" {
+
+void *opt_sgd_create(double lr, double momentum)
+{
+    OptHandle *o = make(OPT_SGD);
+    if (o) { o->lr = lr; o->momentum = momentum; }
+    return o;
+}
+
+void *opt_adam_create(double lr, double beta1, double beta2, double epsilon)
+{
+    OptHandle *o = make(OPT_ADAM);
+    if (o) { o->lr = lr; o->beta1 = beta1; o->beta2 = beta2; o->eps = epsilon; o->wd = 0.0; }
+    return o;
+}
+
+void *opt_adamw_create(double lr, double beta1, double beta2, double epsilon, double weight_decay)
+{
+    OptHandle *o = make(OPT_ADAMW);
+    if (o) { o->lr = lr; o->beta1 = beta1; o->beta2 = beta2; o->eps = epsilon; o->wd = weight_decay; }
+    return o;
+}
+
+// opt_step (optimizers_c.c:353-368): NULL -> 1; n < 0 or n != first-call count -> 3.
+int opt_step(void *opt, void **params, void **grads, int64_t n)
+{
+    if (!opt || !params || !grads) return set_error(NEURAL_ERR_NULL_POINTER);
+    NH_TRY(ensure_init());
+    OptHandle *o = static_cast<OptHandle *>(opt);
+    if (n < 0) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
+    if (o->n_params > 0 && n != o->n_params) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
+    if (o->type < OPT_SGD || o->type > OPT_ADAMW) return set_error(NEURAL_ERR_NULL_POINTER);
+    if (o->n_params == 0 && n > 0) {
+        // Lazy moment allocation on the first step (optimizers_c.c:179-212).
+        o->n_params = n;
+        o->sizes.resize(size_t(n));
+        for (int64_t i = 0; i < n; i++) {
+            const NeuralTensor *p = static_cast<const NeuralTensor *>(params[i]);
+            const int64_t sz = p ? numel(p) : 0;
+            o->sizes[size_t(i)] = sz;
+            if (o->type == OPT_SGD) {
+                double *b = alloc_zeroed(sz);
+                if (!b) { free_moments(o); return set_error(NEURAL_ERR_OUT_OF_MEMORY); }
+                o->vel.push_back(b);
+            } else {
+                double *bm = alloc_zeroed(sz), *bv = alloc_zeroed(sz);
+                if (!bm || !bv) { dev_free(bm); dev_free(bv); free_moments(o); return set_error(NEURAL_ERR_OUT_OF_MEMORY); }
+                o->m.push_back(bm);
+                o->v.push_back(bv);
+            }
+        }
+    }
+    AdamArgs a{o->lr, o->beta1, o->beta2, o->eps, o->wd, 0.0, 0.0};
+    if (o->type != OPT_SGD) {
+        o->t++;
+        a.bc1 = 1.0 - std::pow(o->beta1, double(o->t));
+        a.bc2 = 1.0 - std::pow(o->beta2, double(o->t));
+    }
+    for (int64_t i = 0; i < n; i++)
+        NH_TRY(step_param(o, size_t(i), static_cast<NeuralTensor *>(params[i]),
+                          static_cast<const NeuralTensor *>(grads[i]), a));
+    return set_error(NEURAL_OK);
+}
+
+void opt_free(void *opt)
+{
+    if (!opt) return;
+    OptHandle *o = static_cast<OptHandle *>(opt);
+    if (ensure_init() == NEURAL_OK) (void)sync();
+    free_moments(o);
+    delete o;
+}
+
+double opt_get_lr(void *opt) { return opt ? static_cast<OptHandle *>(opt)->lr : 0.0; }
+
+void opt_set_lr(void *opt, double lr)
+{
+    if (opt) static_cast<OptHandle *>(opt)->lr = lr;
+}
+
+int64_t opt_state_bytes(void *opt)
+{
+    if (!opt) return 0;
+    const OptHandle *o = static_cast<const OptHandle *>(opt);
+    int64_t total = int64_t(sizeof(OptStateHeader)) + o->n_params * int64_t(sizeof(int64_t));
+    const int64_t e = total_elems(o);
+    if (e < 0) return 0;
+    if (o->type == OPT_SGD) total += e * int64_t(sizeof(double));
+    else total += 2 * e * int64_t(sizeof(double));
+    return total;
+}
+
+int opt_state_export(void *opt, void *buffer, int64_t size)
+{
+    if (!opt || !buffer || size <= 0) return set_error(NEURAL_ERR_NULL_POINTER);
+    NH_TRY(ensure_init());
+    OptHandle *o = static_cast<OptHandle *>(opt);
+    const int64_t need = opt_state_bytes(opt);
+    if (need <= 0 || size < need) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
+    OptStateHeader h;
+    std::memset(&h, 0, sizeof(h));
+    h.magic = kOptsMagic;
+    h.version = kOptsVersion;
+    h.type = o->type;
+    h.n_params = o->n_params;
+    h.lr = o->lr;
+    h.momentum = o->momentum;
+    h.beta1 = o->beta1;
+    h.beta2 = o->beta2;
+    h.epsilon = o->eps;
+    h.weight_decay = o->wd;
+    h.t = o->t;
+    uint8_t *p = static_cast<uint8_t *>(buffer);
+    std::memcpy(p, &h, sizeof(h));
+    p += sizeof(h);
+    if (o->n_params > 0) {
+        std::memcpy(p, o->sizes.data(), size_t(o->n_params) * sizeof(int64_t));
+        p += size_t(o->n_params) * sizeof(int64_t);
+    }
+    auto dump = [&](std::vector<double *> &bufs) -> int {
+        for (size_t i = 0; i < bufs.size(); i++) {
+            const int64_t n = o->sizes[i];
+            if (n <= 0) continue;
+            NH_HIP(hipMemcpyAsync(p, bufs[i], size_t(n) * sizeof(double), hipMemcpyDeviceToHost, stream()));
+            p += size_t(n) * sizeof(double);
+        }
+        return NEURAL_OK;
+    };
+    if (o->type == OPT_SGD) NH_TRY(dump(o->vel));
+    else {
+        NH_TRY(dump(o->m));
+        NH_TRY(dump(o->v));
+    }
+    NH_TRY(sync());
+    return set_error(NEURAL_OK);
+}
+
+int opt_state_import(void *opt, const void *buffer, int64_t size)
+{
+    if (!opt || !buffer || size <= 0) return set_error(NEURAL_ERR_NULL_POINTER);
+    NH_TRY(ensure_init());
+    OptHandle *o = static_cast<OptHandle *>(opt);
+    if (size < int64_t(sizeof(OptStateHeader))) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
+    const uint8_t *base = static_cast<const uint8_t *>(buffer);
+    const uint8_t *p = base;
+    OptStateHeader h;
+    std::memcpy(&h, p, sizeof(h));
+    p += sizeof(h);
+    if (h.magic != kOptsMagic || h.version != kOptsVersion) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
+    if (h.type != o->type || h.n_params < 0) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
+    NH_TRY(sync());
+    free_moments(o);
+    o->lr = h.lr;
+    o->momentum = h.momentum;
+    o->beta1 = h.beta1;
+    o->beta2 = h.beta2;
+    o->eps = h.epsilon;
+    o->wd = h.weight_decay;
+    o->t = h.t;
+    if (h.n_params == 0) return set_error(NEURAL_OK);
+    const int64_t sizes_bytes = h.n_params * int64_t(sizeof(int64_t));
+    if ((p - base) + sizes_bytes > size) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
+    o->n_params = h.n_params;
+    o->sizes.resize(size_t(h.n_params));
+    std::memcpy(o->sizes.data(), p, size_t(sizes_bytes));
+    p += sizes_bytes;
+    auto load = [&](std::vector<double *> &bufs) -> int {
+        for (int64_t i = 0; i < o->n_params; i++) {
+            const int64_t n = o->sizes[size_t(i)];
+            if (n < 0) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
+            double *d = static_cast<double *>(dev_alloc(size_t(n > 0 ? n : 1) * sizeof(double)));
+            if (!d) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
+            bufs.push_back(d);
+            if (n == 0) continue;
+            const int64_t bytes = n * int64_t(sizeof(double));
+            if ((p - base) + bytes > size) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
+            NH_HIP(hipMemcpyAsync(d, p, size_t(bytes), hipMemcpyHostToDevice, stream()));
+            p += bytes;
+        }
+        return NEURAL_OK;
+    };
+    int rc = NEURAL_OK;
+    if (o->type == OPT_SGD) rc = load(o->vel);
+    else {
+        rc = load(o->m);
+        if (rc == NEURAL_OK) rc = load(o->v);
+    }
+    if (rc != NEURAL_OK) {
+        (void)sync();
+        free_moments(o);
+        return rc;
+    }
+    NH_TRY(sync());
+    return set_error(NEURAL_OK);
+}
+
+}  // extern "C"

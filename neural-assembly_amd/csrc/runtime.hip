@@ -1,0 +1,811 @@
+// runtime.hip -- device/stream/allocator runtime and the tensor C ABI.
+//
+// Replaces the reference's host runtime for this path: tensor.asm (descriptor,
+// create/free/fill/copy/reshape), mem.asm (allocation), error.asm (codes and
+// messages) and the tensor exports of neural_api.asm:297-967,2293-2426.
+// Tensor bytes live in HBM; the host copy is a mirror synchronised at
+// neural_tensor_data() (see the memory-model note in include/neural_api.h).
+#include <cstdio>
+#include <cstdlib>
+#include <mutex>
+#include <new>
+#include <unordered_map>
+#include <vector>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace nh {
+
+namespace {
+
+struct Runtime {
+    std::mutex mu;
+    bool inited = false;
+    int init_rc = NEURAL_OK;
+    int device = 0;
+    int cus = 0;
+    char name[256] = {0};
+    hipStream_t own = nullptr;
+    hipStream_t active = nullptr;
+    std::unordered_map<size_t, std::vector<void *>> cache;  // size class -> free blocks
+    std::unordered_map<void *, size_t> live;                // block -> size class
+    Workspace ws{};
+};
+
+Runtime &R()
+{
+    static Runtime *r = new Runtime();  // never destroyed: kernels may outlive static dtors
+    return *r;
+}
+
+thread_local int t_last_error = NEURAL_OK;
+thread_local bool t_device_set = false;
+
+size_t size_class(size_t b)
+{
+    if (b <= 512) return 512;
+    if (b < (size_t(1) << 20)) return (b + 4095) & ~size_t(4095);
+    const size_t g = size_t(2) << 20;
+    return (b + g - 1) & ~(g - 1);
+}
+
+void release_cache_locked(Runtime &r)
+{
+    for (auto &kv : r.cache)
+        for (void *p : kv.second) (void)hipFree(p);
+    r.cache.clear();
+}
+
+}  // namespace
+
+int set_error(int code)
+{
+    t_last_error = code;
+    return code;
+}
+
+int hip_fail(hipError_t e)
+{
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
+    if (std::getenv("NEURAL_HIP_VERBOSE"))
+        std::fprintf(stderr, "libneural_hip: HIP error %d (%s)\n", int(e), hipGetErrorString(e));
+    return set_error(NEURAL_ERR_INTERNAL);
+}
+
+int ensure_init()
+{
+    Runtime &r = R();
+    if (!r.inited) {
+        std::lock_guard<std::mutex> g(r.mu);
+        if (!r.inited) {
+            int count = 0;
+            hipError_t e = hipGetDeviceCount(&count);
+            if (e != hipSuccess || count <= 0) {
+                (void)hipGetLastError();
+                std::fprintf(stderr, "libneural_hip: no HIP device available (%s)\n",
+                             e == hipSuccess ? "device count 0" : hipGetErrorString(e));
+                r.init_rc = NEURAL_ERR_INTERNAL;
+                return set_error(r.init_rc);
+            }
+            const char *dv = std::getenv("NEURAL_HIP_DEVICE");
+            r.device = dv ? std::atoi(dv) : 0;
+            if (r.device < 0 || r.device >= count) r.device = 0;
+            hipDeviceProp_t prop;
+            if (hipSetDevice(r.device) != hipSuccess || hipGetDeviceProperties(&prop, r.device) != hipSuccess) {
+                r.init_rc = NEURAL_ERR_INTERNAL;
+                return set_error(r.init_rc);
+            }
+            r.cus = prop.multiProcessorCount;
+            std::snprintf(r.name, sizeof(r.name), "%s", prop.gcnArchName);
+            if (hipStreamCreateWithFlags(&r.own, hipStreamNonBlocking) != hipSuccess) {
+                r.init_rc = NEURAL_ERR_INTERNAL;
+                return set_error(r.init_rc);
+            }
+            r.active = r.own;
+            // Reduction workspace; counters start at zero and every kernel that
+            // uses one leaves it at zero.
+            if (hipMalloc(&r.ws.partials, size_t(kMaxPartials) * 64) != hipSuccess ||
+                hipMalloc((void **)&r.ws.counter, sizeof(unsigned) * kCounters) != hipSuccess ||
+                hipMalloc(&r.ws.result, 256) != hipSuccess ||
+                hipMemset(r.ws.counter, 0, sizeof(unsigned) * kCounters) != hipSuccess ||
+                hipDeviceSynchronize() != hipSuccess) {
+                r.init_rc = NEURAL_ERR_OUT_OF_MEMORY;
+                return set_error(r.init_rc);
+            }
+            r.inited = true;
+            t_device_set = true;
+        }
+    }
+    if (r.init_rc != NEURAL_OK) return set_error(r.init_rc);
+    if (!t_device_set) {
+        (void)hipSetDevice(r.device);
+        t_device_set = true;
+    }
+    return NEURAL_OK;
+}
+
+hipStream_t stream() { return R().active; }
+int num_cus() { return R().cus; }
+Workspace &workspace() { return R().ws; }
+
+void *dev_alloc(size_t bytes)
+{
+    Runtime &r = R();
+    const size_t cls = size_class(bytes);
+    std::lock_guard<std::mutex> g(r.mu);
+    auto it = r.cache.find(cls);
+    if (it != r.cache.end() && !it->second.empty()) {
+        void *p = it->second.back();
+        it->second.pop_back();
+        r.live[p] = cls;
+        return p;
+    }
+    void *p = nullptr;
+    if (hipMalloc(&p, cls) != hipSuccess) {
+        (void)hipGetLastError();
+        // Give cached blocks back and retry once; outstanding work may still
+        // read them, so drain the stream first.
+        (void)hipStreamSynchronize(r.active);
+        release_cache_locked(r);
+        if (hipMalloc(&p, cls) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+    }
+    r.live[p] = cls;
+    return p;
+}
+
+void dev_free(void *p)
+{
+    if (!p) return;
+    Runtime &r = R();
+    std::lock_guard<std::mutex> g(r.mu);
+    auto it = r.live.find(p);
+    if (it == r.live.end()) return;
+    // Stream-ordered reuse: every later use of this block is enqueued on the
+    // same stream after the work that may still read it.
+    r.cache[it->second].push_back(p);
+    r.live.erase(it);
+}
+
+bool is_device_ptr(const void *p)
+{
+    if (!p) return false;
+    hipPointerAttribute_t a;
+    if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return a.type == hipMemoryTypeDevice || a.type == hipMemoryTypeManaged;
+}
+
+int check_launch()
+{
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? NEURAL_OK : hip_fail(e);
+}
+
+int sync()
+{
+    NH_HIP(hipStreamSynchronize(stream()));
+    return NEURAL_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Staging of caller pointers
+// ---------------------------------------------------------------------------
+
+int Staged::open(const void *p, size_t nbytes, bool upload)
+{
+    bytes = nbytes;
+    host = const_cast<void *>(p);
+    if (is_device_ptr(p)) {
+        dev = const_cast<void *>(p);
+        owned = false;
+        return NEURAL_OK;
+    }
+    dev = dev_alloc(nbytes ? nbytes : 1);
+    if (!dev) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
+    owned = true;
+    if (upload && nbytes) NH_HIP(hipMemcpyAsync(dev, p, nbytes, hipMemcpyHostToDevice, stream()));
+    return NEURAL_OK;
+}
+
+int Staged::finish(bool download)
+{
+    if (owned && download && bytes)
+        NH_HIP(hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, stream()));
+    if (owned) {
+        NH_TRY(sync());
+        dev_free(dev);
+        dev = nullptr;
+        owned = false;
+    }
+    return NEURAL_OK;
+}
+
+Staged::~Staged()
+{
+    if (owned && dev) {
+        (void)hipStreamSynchronize(stream());
+        dev_free(dev);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Tensor helpers
+// ---------------------------------------------------------------------------
+
+size_t elem_size(int dtype) { return dtype == NEURAL_DTYPE_FLOAT64 ? 8 : 4; }
+
+int64_t numel(const NeuralTensor *t)
+{
+    if (!t) return 0;
+    int64_t n = 1;
+    for (int64_t i = 0; i < t->ndim; i++) n *= t->shape[i];
+    return n;
+}
+
+bool is_contiguous(const NeuralTensor *t)
+{
+    int64_t expect = int64_t(elem_size(t->dtype));
+    for (int64_t i = t->ndim - 1; i >= 0; i--) {
+        if (t->shape[i] != 1 && t->stride[i] != expect) return false;
+        expect *= t->shape[i];
+    }
+    return true;
+}
+
+int check_tensor(const NeuralTensor *t)
+{
+    if (!t) return set_error(NEURAL_ERR_NULL_POINTER);
+    if (t->dtype != NEURAL_DTYPE_FLOAT32 && t->dtype != NEURAL_DTYPE_FLOAT64)
+        return set_error(NEURAL_ERR_INVALID_DTYPE);
+    return NEURAL_OK;
+}
+
+static int upload_span(Storage *s, const NeuralTensor *t)
+{
+    const int64_t span = s->hi - s->lo;
+    if (span <= 0) return NEURAL_OK;
+    char *host0 = static_cast<char *>(s->host) + s->lo;
+    NH_HIP(hipMemcpyAsync(s->dev_block, host0, size_t(span), hipMemcpyHostToDevice, stream()));
+    (void)t;
+    return NEURAL_OK;
+}
+
+static int download_span(Storage *s)
+{
+    const int64_t span = s->hi - s->lo;
+    if (span <= 0) return NEURAL_OK;
+    char *host0 = static_cast<char *>(s->host) + s->lo;
+    NH_HIP(hipMemcpyAsync(host0, s->dev_block, size_t(span), hipMemcpyDeviceToHost, stream()));
+    NH_TRY(sync());
+    return NEURAL_OK;
+}
+
+int dev_read(const NeuralTensor *t, const void **p)
+{
+    Storage *s = t->st;
+    if (s->kind == KIND_EXT_HOST || (s->kind == KIND_OWNED && s->state == ST_HOST)) {
+        NH_TRY(upload_span(s, t));
+        if (s->kind == KIND_OWNED) s->state = ST_SYNCED;
+    }
+    *p = t->dev;
+    return NEURAL_OK;
+}
+
+int dev_write(NeuralTensor *t, void **p, bool full)
+{
+    Storage *s = t->st;
+    const bool whole = full && (s->hi - s->lo) == int64_t(numel(t) * elem_size(t->dtype));
+    if (s->kind == KIND_EXT_HOST || (s->kind == KIND_OWNED && s->state == ST_HOST)) {
+        // Partial writes (or views that do not cover the storage) must keep
+        // the bytes they do not touch.
+        if (!whole) NH_TRY(upload_span(s, t));
+    }
+    *p = t->dev;
+    return NEURAL_OK;
+}
+
+int dev_written(NeuralTensor *t)
+{
+    Storage *s = t->st;
+    if (s->kind == KIND_OWNED) s->state = ST_DEVICE;
+    else if (s->kind == KIND_EXT_HOST) NH_TRY(download_span(s));
+    return NEURAL_OK;
+}
+
+// Make the host bytes current and hand them to the caller (map for host
+// access): the next device use re-uploads them.
+static void *host_map(NeuralTensor *t)
+{
+    Storage *s = t->st;
+    if (s->kind == KIND_OWNED) {
+        if (s->state == ST_DEVICE) {
+            if (download_span(s) != NEURAL_OK) return nullptr;
+        }
+        s->state = ST_HOST;
+    }
+    return t->data;
+}
+
+}  // namespace nh
+
+using namespace nh;
+
+// ---------------------------------------------------------------------------
+// Tensor construction
+// ---------------------------------------------------------------------------
+
+namespace {
+
+const char *k_messages[] = {
+    "no error",
+    "null pointer argument",
+    "out of memory (device or host)",
+    "invalid argument",
+    "tensor shapes do not match",
+    "tensor dtypes do not match",
+    "file not found",
+    "file read failed",
+    "file write failed",
+    "parse error",
+    "invalid configuration",
+    "tensor too large",
+    "invalid dtype (expected 0=float32 or 1=float64)",
+    "dimension mismatch (more than 4 broadcast dims, or bad axis)",
+    "not implemented",
+    "internal error (HIP runtime or kernel launch failed)",
+    "gradient check failed",
+    "NaN detected",
+    "Inf detected",
+};
+
+void fill_contig_strides(NeuralTensor *t)
+{
+    int64_t s = int64_t(elem_size(t->dtype));
+    for (int64_t i = t->ndim - 1; i >= 0; i--) {
+        t->stride[i] = s;
+        s *= t->shape[i];
+    }
+}
+
+NeuralTensor *alloc_desc(int64_t ndim, int dtype)
+{
+    NeuralTensor *t = static_cast<NeuralTensor *>(std::calloc(1, sizeof(NeuralTensor)));
+    if (!t) return nullptr;
+    t->ndim = ndim;
+    t->dtype = dtype;
+    const int64_t nd = ndim > 0 ? ndim : 1;
+    t->shape = static_cast<int64_t *>(std::calloc(size_t(nd), sizeof(int64_t)));
+    t->stride = static_cast<int64_t *>(std::calloc(size_t(nd), sizeof(int64_t)));
+    if (!t->shape || !t->stride) {
+        std::free(t->shape);
+        std::free(t->stride);
+        std::free(t);
+        return nullptr;
+    }
+    return t;
+}
+
+void free_desc(NeuralTensor *t)
+{
+    std::free(t->shape);
+    std::free(t->stride);
+    std::free(t);
+}
+
+void storage_release(Storage *s)
+{
+    if (!s || --s->refs > 0) return;
+    // Stream-ordered reuse makes an immediate return to the cache safe.
+    if (s->dev_block) dev_free(s->dev_block);
+    if (s->host_owned) std::free(s->host);
+    delete s;
+}
+
+// Byte span [lo, hi) reachable from element 0 through the strides.
+void span_of(const NeuralTensor *t, int64_t *lo, int64_t *hi)
+{
+    int64_t a = 0, b = 0;
+    for (int64_t i = 0; i < t->ndim; i++) {
+        if (t->shape[i] == 0) { *lo = 0; *hi = 0; return; }
+        const int64_t ext = (t->shape[i] - 1) * t->stride[i];
+        if (ext < 0) a += ext; else b += ext;
+    }
+    *lo = a;
+    *hi = b + int64_t(elem_size(t->dtype));
+}
+
+NeuralTensor *create_owned(const uint64_t *shape, uint64_t ndim, int dtype, bool zero)
+{
+    if (ensure_init() != NEURAL_OK) return nullptr;
+    if (ndim > 0 && !shape) { set_error(NEURAL_ERR_NULL_POINTER); return nullptr; }
+    if (dtype != NEURAL_DTYPE_FLOAT32 && dtype != NEURAL_DTYPE_FLOAT64) {
+        set_error(NEURAL_ERR_INVALID_DTYPE);
+        return nullptr;
+    }
+    NeuralTensor *t = alloc_desc(int64_t(ndim), dtype);
+    if (!t) { set_error(NEURAL_ERR_OUT_OF_MEMORY); return nullptr; }
+    int64_t n = 1;
+    for (uint64_t i = 0; i < ndim; i++) {
+        t->shape[i] = int64_t(shape[i]);
+        n *= int64_t(shape[i]);
+    }
+    fill_contig_strides(t);
+    const size_t bytes = size_t(n) * elem_size(dtype);
+    Storage *s = new (std::nothrow) Storage();
+    void *host = nullptr;
+    if (s && posix_memalign(&host, 64, bytes ? bytes : 64) != 0) host = nullptr;
+    void *dev = s ? dev_alloc(bytes ? bytes : 64) : nullptr;
+    if (!s || !host || !dev) {
+        std::free(host);
+        dev_free(dev);
+        delete s;
+        free_desc(t);
+        set_error(NEURAL_ERR_OUT_OF_MEMORY);
+        return nullptr;
+    }
+    s->refs = 1;
+    s->kind = KIND_OWNED;
+    s->state = ST_DEVICE;
+    s->host = host;
+    s->host_owned = true;
+    s->dev_block = dev;
+    s->dev_bytes = bytes;
+    s->lo = 0;
+    s->hi = int64_t(bytes);
+    t->data = host;
+    t->dev = dev;
+    t->kind = KIND_OWNED;
+    t->flags = NT_OWN_DATA | NT_OWN_META;
+    t->st = s;
+    // tensor_create zero-fills every new tensor (tensor.asm:326-329); the
+    // fill runs in HBM.
+    (void)zero;
+    if (bytes && launch_fill(dev, dtype, n, 0.0) != NEURAL_OK) {
+        neural_tensor_free(t);
+        return nullptr;
+    }
+    set_error(NEURAL_OK);
+    return t;
+}
+
+}  // namespace
+
+extern "C" {
+
+int neural_init(void) { return ensure_init(); }
+
+void neural_shutdown(void)
+{
+    Runtime &r = R();
+    if (!r.inited) return;
+    (void)hipStreamSynchronize(r.active);
+    std::lock_guard<std::mutex> g(r.mu);
+    release_cache_locked(r);
+}
+
+const char *neural_version(void) { return "neural-hip 1.0 (gfx950)"; }
+
+void neural_clear_error(void) { t_last_error = NEURAL_OK; }
+
+int neural_get_last_error(void) { return t_last_error; }
+
+const char *neural_get_error_message(int code)
+{
+    if (code < 0 || code > 18) return "unknown error";
+    return k_messages[code];
+}
+
+NeuralTensor *neural_tensor_create(const uint64_t *shape, uint64_t ndim, int dtype)
+{
+    return create_owned(shape, ndim, dtype, true);
+}
+
+NeuralTensor *neural_tensor_zeros(const uint64_t *shape, uint64_t ndim, int dtype)
+{
+    return create_owned(shape, ndim, dtype, true);
+}
+
+// The reference passes 1.0f bits where a double is expected and so fills with
+// ~0 (neural_api.asm:517-519); this fills with 1.0.
+NeuralTensor *neural_tensor_ones(const uint64_t *shape, uint64_t ndim, int dtype)
+{
+    NeuralTensor *t = create_owned(shape, ndim, dtype, false);
+    if (t && neural_tensor_fill(t, 1.0) != NEURAL_OK) {
+        neural_tensor_free(t);
+        return nullptr;
+    }
+    return t;
+}
+
+NeuralTensor *neural_tensor_from_data(const void *data, const uint64_t *shape, uint64_t ndim, int dtype)
+{
+    if (!data) { set_error(NEURAL_ERR_NULL_POINTER); return nullptr; }
+    NeuralTensor *t = create_owned(shape, ndim, dtype, false);
+    if (!t) return nullptr;
+    const size_t bytes = size_t(numel(t)) * elem_size(dtype);
+    Staged src;
+    if (bytes && (src.open(data, bytes, true) != NEURAL_OK ||
+                  hipMemcpyAsync(t->dev, src.dev, bytes, hipMemcpyDeviceToDevice, stream()) != hipSuccess ||
+                  src.finish(false) != NEURAL_OK)) {
+        neural_tensor_free(t);
+        set_error(NEURAL_ERR_INTERNAL);
+        return nullptr;
+    }
+    return t;
+}
+
+// Zero-copy wrap (neural_api.asm:2293-2426).  The reference marks the buffer
+// FLAG_OWN_DATA (neural_api.asm:2393) and so frees the caller's memory in
+// tensor_free; here the caller keeps ownership (flags = OWN_META only).
+NeuralTensor *neural_tensor_from_buffer(void *buffer, const uint64_t *shape, uint64_t ndim, int dtype,
+                                        const int64_t *strides)
+{
+    if (ensure_init() != NEURAL_OK) return nullptr;
+    if (!buffer || !shape) { set_error(NEURAL_ERR_NULL_POINTER); return nullptr; }
+    if (dtype != NEURAL_DTYPE_FLOAT32 && dtype != NEURAL_DTYPE_FLOAT64) {
+        set_error(NEURAL_ERR_INVALID_DTYPE);
+        return nullptr;
+    }
+    NeuralTensor *t = alloc_desc(int64_t(ndim), dtype);
+    if (!t) { set_error(NEURAL_ERR_OUT_OF_MEMORY); return nullptr; }
+    for (uint64_t i = 0; i < ndim; i++) t->shape[i] = int64_t(shape[i]);
+    if (strides) for (uint64_t i = 0; i < ndim; i++) t->stride[i] = strides[i];
+    else fill_contig_strides(t);
+    Storage *s = new (std::nothrow) Storage();
+    if (!s) { free_desc(t); set_error(NEURAL_ERR_OUT_OF_MEMORY); return nullptr; }
+    s->refs = 1;
+    s->host = buffer;
+    s->host_owned = false;
+    span_of(t, &s->lo, &s->hi);
+    t->data = buffer;
+    t->flags = NT_OWN_META;
+    t->st = s;
+    if (is_device_ptr(buffer)) {
+        s->kind = KIND_EXT_DEV;
+        s->state = ST_DEVICE;
+        t->dev = buffer;
+    } else {
+        s->kind = KIND_EXT_HOST;
+        s->state = ST_HOST;
+        const int64_t span = s->hi - s->lo;
+        s->dev_block = dev_alloc(size_t(span > 0 ? span : 64));
+        s->dev_bytes = size_t(span > 0 ? span : 0);
+        if (!s->dev_block) {
+            delete s;
+            free_desc(t);
+            set_error(NEURAL_ERR_OUT_OF_MEMORY);
+            return nullptr;
+        }
+        t->dev = static_cast<char *>(s->dev_block) - s->lo;
+    }
+    t->kind = s->kind;
+    set_error(NEURAL_OK);
+    return t;
+}
+
+const int64_t *neural_tensor_stride(NeuralTensor *t) { return t ? t->stride : nullptr; }
+
+int neural_tensor_is_contiguous(NeuralTensor *t)
+{
+    if (!t) { set_error(NEURAL_ERR_NULL_POINTER); return -1; }
+    return nh::is_contiguous(t) ? 1 : 0;
+}
+
+NeuralTensor *neural_tensor_make_contiguous(NeuralTensor *t)
+{
+    if (!t) { set_error(NEURAL_ERR_NULL_POINTER); return nullptr; }
+    if (nh::is_contiguous(t)) return t;
+    std::vector<uint64_t> shp(size_t(t->ndim));
+    for (int64_t i = 0; i < t->ndim; i++) shp[size_t(i)] = uint64_t(t->shape[i]);
+    NeuralTensor *o = neural_tensor_create(shp.data(), uint64_t(t->ndim), t->dtype);
+    if (!o) return nullptr;
+    if (neural_tensor_copy(o, t) != NEURAL_OK) {
+        neural_tensor_free(o);
+        return nullptr;
+    }
+    return o;
+}
+
+int neural_buffer_info(NeuralTensor *t, NeuralBufferInfo *info)
+{
+    if (!t || !info) return set_error(NEURAL_ERR_NULL_POINTER);
+    void *p = host_map(t);
+    if (!p && numel(t) > 0) return set_error(NEURAL_ERR_INTERNAL);
+    std::memset(info, 0, sizeof(*info));
+    info->data = p;
+    info->itemsize = elem_size(t->dtype);
+    info->ndim = uint64_t(t->ndim);
+    info->shape = reinterpret_cast<const uint64_t *>(t->shape);
+    info->strides = t->stride;
+    info->readonly = 0;
+    info->format[0] = t->dtype == NEURAL_DTYPE_FLOAT64 ? 'd' : 'f';
+    return set_error(NEURAL_OK);
+}
+
+void neural_tensor_free(NeuralTensor *t)
+{
+    if (!t) return;
+    storage_release(t->st);
+    free_desc(t);
+}
+
+void *neural_tensor_data(NeuralTensor *t)
+{
+    if (!t) return nullptr;
+    return host_map(t);
+}
+
+uint64_t neural_tensor_ndim(NeuralTensor *t) { return t ? uint64_t(t->ndim) : 0; }
+
+const uint64_t *neural_tensor_shape(NeuralTensor *t)
+{
+    return t ? reinterpret_cast<const uint64_t *>(t->shape) : nullptr;
+}
+
+uint64_t neural_tensor_numel(NeuralTensor *t) { return t ? uint64_t(numel(t)) : 0; }
+
+int neural_tensor_dtype(NeuralTensor *t) { return t ? t->dtype : -1; }
+
+uint64_t neural_tensor_bytes(NeuralTensor *t)
+{
+    return t ? uint64_t(numel(t)) * elem_size(t->dtype) : 0;
+}
+
+// tensor_fill (tensor.asm:531-589): the double value is rounded to float once
+// for f32 tensors.  Strided tensors fill every addressed element.
+int neural_tensor_fill(NeuralTensor *t, double value)
+{
+    NH_TRY(ensure_init());
+    NH_TRY(check_tensor(t));
+    const int64_t n = numel(t);
+    if (n == 0) return set_error(NEURAL_OK);
+    void *d = nullptr;
+    const bool contig = nh::is_contiguous(t);
+    NH_TRY(dev_write(t, &d, contig));
+    if (contig) {
+        NH_TRY(launch_fill(d, t->dtype, n, value));
+    } else {
+        NH_TRY(launch_fill_strided(d, t->dtype, t->shape, t->stride, int(t->ndim), value));
+    }
+    NH_TRY(dev_written(t));
+    return set_error(NEURAL_OK);
+}
+
+// neural_tensor_copy (neural_api.asm:905-967): dtype must match (5) and
+// element counts must match (4); copies in logical (row-major) order.
+int neural_tensor_copy(NeuralTensor *dst, const NeuralTensor *src)
+{
+    NH_TRY(ensure_init());
+    if (!dst || !src) return set_error(NEURAL_ERR_NULL_POINTER);
+    if (dst->dtype != src->dtype) return set_error(NEURAL_ERR_DTYPE_MISMATCH);
+    const int64_t n = numel(dst);
+    if (n != numel(src)) return set_error(NEURAL_ERR_SHAPE_MISMATCH);
+    if (n == 0) return set_error(NEURAL_OK);
+    const void *s = nullptr;
+    void *d = nullptr;
+    NH_TRY(dev_read(src, &s));
+    const bool dc = nh::is_contiguous(dst), sc = nh::is_contiguous(src);
+    NH_TRY(dev_write(dst, &d, dc));
+    const size_t es = elem_size(dst->dtype);
+    if (dc && sc) {
+        NH_HIP(hipMemcpyAsync(d, s, size_t(n) * es, hipMemcpyDeviceToDevice, stream()));
+    } else {
+        NH_TRY(launch_copy_nd(d, dst->shape, dst->stride, int(dst->ndim), s, src->shape, src->stride,
+                              int(src->ndim), int(es)));
+    }
+    NH_TRY(dev_written(dst));
+    return set_error(NEURAL_OK);
+}
+
+// tensor_reshape (tensor.asm:600-680): element counts must match (4); the
+// result is a view sharing storage (OWN_META only).  Non-contiguous inputs
+// are rejected with 3 (the reference views them anyway and mislabels strides).
+NeuralTensor *neural_tensor_reshape(NeuralTensor *t, const uint64_t *new_shape, uint64_t new_ndim)
+{
+    if (!t || (new_ndim > 0 && !new_shape)) { set_error(NEURAL_ERR_NULL_POINTER); return nullptr; }
+    int64_t n = 1;
+    for (uint64_t i = 0; i < new_ndim; i++) n *= int64_t(new_shape[i]);
+    if (n != numel(t)) { set_error(NEURAL_ERR_SHAPE_MISMATCH); return nullptr; }
+    if (!nh::is_contiguous(t)) { set_error(NEURAL_ERR_INVALID_ARGUMENT); return nullptr; }
+    NeuralTensor *v = alloc_desc(int64_t(new_ndim), t->dtype);
+    if (!v) { set_error(NEURAL_ERR_OUT_OF_MEMORY); return nullptr; }
+    for (uint64_t i = 0; i < new_ndim; i++) v->shape[i] = int64_t(new_shape[i]);
+    fill_contig_strides(v);
+    v->data = t->data;
+    v->dev = t->dev;
+    v->kind = KIND_VIEW;
+    v->flags = NT_OWN_META;
+    v->st = t->st;
+    t->st->refs++;
+    set_error(NEURAL_OK);
+    return v;
+}
+
+int neural_tensor_upload(NeuralTensor *t, const void *host_src, uint64_t bytes)
+{
+    NH_TRY(ensure_init());
+    if (!t || !host_src) return set_error(NEURAL_ERR_NULL_POINTER);
+    if (bytes != neural_tensor_bytes(t) || !nh::is_contiguous(t)) return set_error(NEURAL_ERR_SHAPE_MISMATCH);
+    void *d = nullptr;
+    NH_TRY(dev_write(t, &d, true));
+    NH_HIP(hipMemcpyAsync(d, host_src, bytes, hipMemcpyHostToDevice, stream()));
+    NH_TRY(sync());
+    NH_TRY(dev_written(t));
+    return set_error(NEURAL_OK);
+}
+
+int neural_tensor_download(NeuralTensor *t, void *host_dst, uint64_t bytes)
+{
+    NH_TRY(ensure_init());
+    if (!t || !host_dst) return set_error(NEURAL_ERR_NULL_POINTER);
+    if (bytes != neural_tensor_bytes(t) || !nh::is_contiguous(t)) return set_error(NEURAL_ERR_SHAPE_MISMATCH);
+    const void *s = nullptr;
+    NH_TRY(dev_read(t, &s));
+    NH_HIP(hipMemcpyAsync(host_dst, s, bytes, hipMemcpyDeviceToHost, stream()));
+    NH_TRY(sync());
+    return set_error(NEURAL_OK);
+}
+
+void *neural_tensor_device_data(NeuralTensor *t)
+{
+    if (!t) return nullptr;
+    const void *p = nullptr;
+    if (dev_read(t, &p) != NEURAL_OK) return nullptr;
+    // The caller may write through the device address: device copy is now
+    // authoritative.
+    if (t->st->kind == KIND_OWNED) t->st->state = ST_DEVICE;
+    return const_cast<void *>(p);
+}
+
+int neural_hip_set_stream(void *s)
+{
+    NH_TRY(ensure_init());
+    Runtime &r = R();
+    hipStream_t next = s ? static_cast<hipStream_t>(s) : r.own;
+    if (next != r.active) {
+        NH_HIP(hipStreamSynchronize(r.active));
+        r.active = next;
+    }
+    return set_error(NEURAL_OK);
+}
+
+void *neural_hip_get_stream(void)
+{
+    if (ensure_init() != NEURAL_OK) return nullptr;
+    return static_cast<void *>(R().active);
+}
+
+int neural_hip_synchronize(void)
+{
+    NH_TRY(ensure_init());
+    NH_TRY(sync());
+    return set_error(NEURAL_OK);
+}
+
+int neural_hip_empty_cache(void)
+{
+    NH_TRY(ensure_init());
+    Runtime &r = R();
+    NH_HIP(hipStreamSynchronize(r.active));
+    std::lock_guard<std::mutex> g(r.mu);
+    release_cache_locked(r);
+    return set_error(NEURAL_OK);
+}
+
+int neural_hip_device_info(int *ordinal, int *cus, char *name, int name_len)
+{
+    NH_TRY(ensure_init());
+    Runtime &r = R();
+    if (ordinal) *ordinal = r.device;
+    if (cus) *cus = r.cus;
+    if (name && name_len > 0) std::snprintf(name, size_t(name_len), "%s", r.name);
+    return set_error(NEURAL_OK);
+}
+
+}  // extern "C"

@@ -1,0 +1,756 @@
+/*
+ * neural_oracle.c -- CPU restatement of the Neural-Assembly tensor hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker, never the product).  See
+ * neural_oracle.h for what pins each function.  Build: oracle/Makefile,
+ * -O2 -std=c11 -ffp-contract=off, no -ffast-math, no -march (SSE2 only, as
+ * the reference's own C flags in Makefile:12).
+ *
+ * Reference paths below are relative to the Neural-Assembly source tree.
+ */
+#include "neural_oracle.h"
+
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------ */
+/* Elementwise: src/asm/math_kernels.asm:66-945                              */
+/* ------------------------------------------------------------------------ */
+
+/* ew_add/sub/mul/div/max (math_kernels.asm:66-507,730-835): out[i] = a[i] op b[i]
+ * over the flat element range.  vmaxps/maxss return the second operand
+ * unless the first is strictly greater, so max(a,b) = (a > b) ? a : b. */
+void ora_ew_f32(int op, const float *a, const float *b, float *out, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++) {
+        float x = a[i], y = b[i];
+        switch (op) {
+        case ORA_ADD: out[i] = x + y; break;
+        case ORA_SUB: out[i] = x - y; break;
+        case ORA_MUL: out[i] = x * y; break;
+        case ORA_DIV: out[i] = x / y; break;
+        default:      out[i] = (x > y) ? x : y; break;
+        }
+    }
+}
+
+void ora_ew_f64(int op, const double *a, const double *b, double *out, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++) {
+        double x = a[i], y = b[i];
+        switch (op) {
+        case ORA_ADD: out[i] = x + y; break;
+        case ORA_SUB: out[i] = x - y; break;
+        case ORA_MUL: out[i] = x * y; break;
+        case ORA_DIV: out[i] = x / y; break;
+        default:      out[i] = (x > y) ? x : y; break;
+        }
+    }
+}
+
+/* ew_scalar_add / ew_scalar_mul (math_kernels.asm:516-725): the scalar arrives
+ * as a double and is rounded to float once (cvtsd2ss, :544/:653) for f32. */
+void ora_scalar_f32(int op, const float *a, double s, float *out, int64_t n)
+{
+    float sf = (float)s;
+    for (int64_t i = 0; i < n; i++)
+        out[i] = (op == ORA_ADD) ? a[i] + sf : a[i] * sf;
+}
+
+void ora_scalar_f64(int op, const double *a, double s, double *out, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++)
+        out[i] = (op == ORA_ADD) ? a[i] + s : a[i] * s;
+}
+
+/* ew_neg (math_kernels.asm:843-945): xor with the sign-bit mask, which also
+ * flips the sign of NaNs and zeros. */
+void ora_neg_f32(const float *a, float *out, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++) {
+        uint32_t u;
+        memcpy(&u, &a[i], 4);
+        u ^= 0x80000000u;
+        memcpy(&out[i], &u, 4);
+    }
+}
+
+void ora_neg_f64(const double *a, double *out, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++) {
+        uint64_t u;
+        memcpy(&u, &a[i], 8);
+        u ^= 0x8000000000000000ull;
+        memcpy(&out[i], &u, 8);
+    }
+}
+
+/* node_relu (activations.asm:153-171): maxss x, 0 -> (x > 0) ? x : +0.0, so
+ * NaN -> +0 and -0 -> +0. */
+void ora_relu_f32(const float *a, float *out, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++) out[i] = (a[i] > 0.0f) ? a[i] : 0.0f;
+}
+
+void ora_relu_f64(const double *a, double *out, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++) out[i] = (a[i] > 0.0) ? a[i] : 0.0;
+}
+
+/* Row-broadcast bias add inside linear_forward_fn (nn_layers.asm:472-539):
+ * out[i*cols + j] = mm[i*cols + j] + bias[j]. */
+void ora_bias_add_f32(const float *x, const float *b, float *out, int64_t rows, int64_t cols)
+{
+    for (int64_t i = 0; i < rows; i++)
+        for (int64_t j = 0; j < cols; j++)
+            out[i * cols + j] = x[i * cols + j] + b[j];
+}
+
+void ora_bias_add_f64(const double *x, const double *b, double *out, int64_t rows, int64_t cols)
+{
+    for (int64_t i = 0; i < rows; i++)
+        for (int64_t j = 0; j < cols; j++)
+            out[i * cols + j] = x[i * cols + j] + b[j];
+}
+
+/* ------------------------------------------------------------------------ */
+/* Reductions: src/asm/math_kernels.asm:956-1264, main.asm:3245-3292,3598-3640 */
+/* ------------------------------------------------------------------------ */
+
+/* reduce_sum axis=-1, f32 (math_kernels.asm:1124-1161): eight running lanes
+ * (vaddps), then (l0+l4),(l1+l5),(l2+l6),(l3+l7) (vextractf128 + vaddps),
+ * two vhaddps -> ((s0+s1)+(s2+s3)), then the n%8 tail added one by one.
+ * With n < 8 the vector block is skipped and the tail starts from 0. */
+float ora_sum_ref_f32(const float *x, int64_t n)
+{
+    float l[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int64_t nv = n / 8;
+    for (int64_t i = 0; i < nv; i++)
+        for (int k = 0; k < 8; k++) l[k] = l[k] + x[i * 8 + k];
+    float acc = 0.0f;
+    if (nv > 0) {
+        float s0 = l[0] + l[4], s1 = l[1] + l[5], s2 = l[2] + l[6], s3 = l[3] + l[7];
+        acc = (s0 + s1) + (s2 + s3);
+    }
+    for (int64_t i = nv * 8; i < n; i++) acc = acc + x[i];
+    return acc;
+}
+
+/* reduce_sum axis=-1, f64 (math_kernels.asm:1163-1196): four lanes,
+ * (l0+l2),(l1+l3), one vhaddpd, then the n%4 tail. */
+double ora_sum_ref_f64(const double *x, int64_t n)
+{
+    double l[4] = {0, 0, 0, 0};
+    int64_t nv = n / 4;
+    for (int64_t i = 0; i < nv; i++)
+        for (int k = 0; k < 4; k++) l[k] = l[k] + x[i * 4 + k];
+    double acc = 0.0;
+    if (nv > 0) acc = (l[0] + l[2]) + (l[1] + l[3]);
+    for (int64_t i = nv * 4; i < n; i++) acc = acc + x[i];
+    return acc;
+}
+
+/* Neumaier-compensated double sum: the "fp64-exact" value the reduction
+ * contract compares against (error below 2^-104 * sum|x| plus one final
+ * rounding; f32 inputs are exact in double). */
+#define NEUMAIER(T, x, n, out)                                           \
+    do {                                                                 \
+        double s_ = 0.0, c_ = 0.0;                                       \
+        for (int64_t i_ = 0; i_ < (n); i_++) {                           \
+            double v_ = (double)(x)[i_];                                 \
+            double t_ = s_ + v_;                                         \
+            if (fabs(s_) >= fabs(v_)) c_ += (s_ - t_) + v_;              \
+            else c_ += (v_ - t_) + s_;                                   \
+            s_ = t_;                                                     \
+        }                                                                \
+        (out) = s_ + c_;                                                 \
+    } while (0)
+
+double ora_sum_exact_f32(const float *x, int64_t n) { double r; NEUMAIER(float, x, n, r); return r; }
+double ora_sum_exact_f64(const double *x, int64_t n) { double r; NEUMAIER(double, x, n, r); return r; }
+
+void ora_rowsum_exact_f32(const float *x, int64_t rows, int64_t cols, double *out)
+{
+    for (int64_t i = 0; i < rows; i++) NEUMAIER(float, x + i * cols, cols, out[i]);
+}
+
+void ora_rowsum_exact_f64(const double *x, int64_t rows, int64_t cols, double *out)
+{
+    for (int64_t i = 0; i < rows; i++) NEUMAIER(double, x + i * cols, cols, out[i]);
+}
+
+/* reduce_sum axis=1 (math_kernels.asm:1061-1107): one strictly sequential
+ * scalar accumulator per row, starting at +0. */
+void ora_rowsum_ref_f32(const float *x, int64_t rows, int64_t cols, float *out)
+{
+    for (int64_t i = 0; i < rows; i++) {
+        float acc = 0.0f;
+        for (int64_t j = 0; j < cols; j++) acc = acc + x[i * cols + j];
+        out[i] = acc;
+    }
+}
+
+void ora_rowsum_ref_f64(const double *x, int64_t rows, int64_t cols, double *out)
+{
+    for (int64_t i = 0; i < rows; i++) {
+        double acc = 0.0;
+        for (int64_t j = 0; j < cols; j++) acc = acc + x[i * cols + j];
+        out[i] = acc;
+    }
+}
+
+/* reduce_sum axis=0 (math_kernels.asm:995-1058): zero out[cols], then add the
+ * rows in order. */
+void ora_colsum_ref_f32(const float *x, int64_t rows, int64_t cols, float *out)
+{
+    for (int64_t j = 0; j < cols; j++) out[j] = 0.0f;
+    for (int64_t i = 0; i < rows; i++)
+        for (int64_t j = 0; j < cols; j++) out[j] = x[i * cols + j] + out[j];
+}
+
+void ora_colsum_ref_f64(const double *x, int64_t rows, int64_t cols, double *out)
+{
+    for (int64_t j = 0; j < cols; j++) out[j] = 0.0;
+    for (int64_t i = 0; i < rows; i++)
+        for (int64_t j = 0; j < cols; j++) out[j] = x[i * cols + j] + out[j];
+}
+
+/* Running max as the softmax max pass does it (activations.asm:815-823 f64,
+ * 888-895 f32): m = x0; m = maxss(m, x_j) = (m > x_j) ? m : x_j. */
+float ora_max_chain_f32(const float *x, int64_t n)
+{
+    float m = x[0];
+    for (int64_t j = 1; j < n; j++) m = (m > x[j]) ? m : x[j];
+    return m;
+}
+
+double ora_max_chain_f64(const double *x, int64_t n)
+{
+    double m = x[0];
+    for (int64_t j = 1; j < n; j++) m = (m > x[j]) ? m : x[j];
+    return m;
+}
+
+void ora_rowmax_chain_f32(const float *x, int64_t rows, int64_t cols, float *out)
+{
+    for (int64_t i = 0; i < rows; i++) out[i] = ora_max_chain_f32(x + i * cols, cols);
+}
+
+void ora_rowmax_chain_f64(const double *x, int64_t rows, int64_t cols, double *out)
+{
+    for (int64_t i = 0; i < rows; i++) out[i] = ora_max_chain_f64(x + i * cols, cols);
+}
+
+/* tensor_argmax (main.asm:3598-3640) and the per-row argmax of
+ * calculate_batch_accuracy (main.asm:3245-3270): idx = 0, m = x0; comiss/jbe
+ * updates only when x_j > m (ordered), so ties keep the first index and NaNs
+ * never win. */
+int64_t ora_argmax_f32(const float *x, int64_t n)
+{
+    int64_t idx = 0;
+    float m = x[0];
+    for (int64_t j = 1; j < n; j++)
+        if (x[j] > m) { m = x[j]; idx = j; }
+    return idx;
+}
+
+int64_t ora_argmax_f64(const double *x, int64_t n)
+{
+    int64_t idx = 0;
+    double m = x[0];
+    for (int64_t j = 1; j < n; j++)
+        if (x[j] > m) { m = x[j]; idx = j; }
+    return idx;
+}
+
+void ora_rowargmax_f32(const float *x, int64_t rows, int64_t cols, int64_t *out)
+{
+    for (int64_t i = 0; i < rows; i++) out[i] = ora_argmax_f32(x + i * cols, cols);
+}
+
+void ora_rowargmax_f64(const double *x, int64_t rows, int64_t cols, int64_t *out)
+{
+    for (int64_t i = 0; i < rows; i++) out[i] = ora_argmax_f64(x + i * cols, cols);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Softmax / log-softmax rows                                                */
+/* ------------------------------------------------------------------------ */
+
+/* node_softmax, f32 (activations.asm:874-952), intended semantics (the asm
+ * keeps max and sum in one stack slot, :900/:927-929): m = running maxss;
+ * e_j = (float)exp((double)x_j - (double)m); s = sequential float sum of e_j;
+ * y_j = e_j / s in float. */
+void ora_softmax_rows_f32(const float *x, int64_t rows, int64_t cols, float *out)
+{
+    for (int64_t i = 0; i < rows; i++) {
+        const float *r = x + i * cols;
+        float *o = out + i * cols;
+        float m = ora_max_chain_f32(r, cols);
+        float s = 0.0f;
+        for (int64_t j = 0; j < cols; j++) {
+            float e = (float)exp((double)r[j] - (double)m);
+            o[j] = e;
+            s = s + e;
+        }
+        for (int64_t j = 0; j < cols; j++) o[j] = o[j] / s;
+    }
+}
+
+/* node_softmax, f64 (activations.asm:800-871): m = running maxsd;
+ * e_j = exp(x_j - m); s = sequential sum; y_j = e_j / s. */
+void ora_softmax_rows_f64(const double *x, int64_t rows, int64_t cols, double *out)
+{
+    for (int64_t i = 0; i < rows; i++) {
+        const double *r = x + i * cols;
+        double *o = out + i * cols;
+        double m = ora_max_chain_f64(r, cols);
+        double s = 0.0;
+        for (int64_t j = 0; j < cols; j++) {
+            double e = exp(r[j] - m);
+            o[j] = e;
+            s = s + e;
+        }
+        for (int64_t j = 0; j < cols; j++) o[j] = o[j] / s;
+    }
+}
+
+/* Log-softmax rows, formula of label_smoothing_ce_forward
+ * (src/c/metrics_losses.c:47-64), in double: m = max (strict >, first wins),
+ * L = log(sum_c exp(x_c - m)) sequential, y_c = (x_c - m) - L.  f32 tensors
+ * widen on load and round the double result once. */
+void ora_log_softmax_rows_f64(const double *x, int64_t rows, int64_t cols, double *out)
+{
+    for (int64_t i = 0; i < rows; i++) {
+        const double *r = x + i * cols;
+        double m = r[0];
+        for (int64_t c = 1; c < cols; c++) if (r[c] > m) m = r[c];
+        double lse = 0.0;
+        for (int64_t c = 0; c < cols; c++) lse += exp(r[c] - m);
+        lse = log(lse);
+        for (int64_t c = 0; c < cols; c++) out[i * cols + c] = (r[c] - m) - lse;
+    }
+}
+
+void ora_log_softmax_rows_f32(const float *x, int64_t rows, int64_t cols, float *out)
+{
+    for (int64_t i = 0; i < rows; i++) {
+        const float *r = x + i * cols;
+        double m = (double)r[0];
+        for (int64_t c = 1; c < cols; c++) if ((double)r[c] > m) m = (double)r[c];
+        double lse = 0.0;
+        for (int64_t c = 0; c < cols; c++) lse += exp((double)r[c] - m);
+        lse = log(lse);
+        for (int64_t c = 0; c < cols; c++) out[i * cols + c] = (float)(((double)r[c] - m) - lse);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Activations: src/c/activations_c.c:63-158 (double math, one rounding to   */
+/* float for f32 tensors); sigmoid: activations.asm:352-413                  */
+/* ------------------------------------------------------------------------ */
+
+static const double K_GELU = 0.7978845608028654;
+static const double K_SELU_L = 1.0507009873554804934193349852946;
+static const double K_SELU_A = 1.6732632423543772848170429916717;
+
+static double act_eval(int which, double x, double alpha)
+{
+    switch (which) {
+    case ORA_TANH:       return tanh(x);
+    case ORA_GELU:       return 0.5 * x * (1.0 + tanh(K_GELU * (x + 0.044715 * x * x * x)));
+    case ORA_LEAKY_RELU: return x >= 0 ? x : alpha * x;
+    case ORA_ELU:        return x > 0 ? x : alpha * (exp(x) - 1.0);
+    case ORA_SELU:       return x > 0 ? K_SELU_L * x : K_SELU_L * K_SELU_A * (exp(x) - 1.0);
+    case ORA_SWISH:      return x / (1.0 + exp(-x));
+    case ORA_MISH:       return x * tanh(log(1.0 + exp(x)));
+    case ORA_HARDSWISH:  return x <= -3.0 ? 0.0 : (x >= 3.0 ? x : x * (x + 3.0) / 6.0);
+    case ORA_SOFTPLUS:   return log(1.0 + exp(x));
+    case ORA_HARDTANH:   return x < -1.0 ? -1.0 : (x > 1.0 ? 1.0 : x);
+    default:             return 1.0 / (1.0 + exp(x * -1.0));
+    }
+}
+
+void ora_act_f32(int which, const float *in, float *out, int64_t n, double alpha)
+{
+    for (int64_t i = 0; i < n; i++) out[i] = (float)act_eval(which, (double)in[i], alpha);
+}
+
+void ora_act_f64(int which, const double *in, double *out, int64_t n, double alpha)
+{
+    for (int64_t i = 0; i < n; i++) out[i] = act_eval(which, in[i], alpha);
+}
+
+/* ------------------------------------------------------------------------ */
+/* INT8 quantization: src/c/quantize.c:39-84,144-174,222-269                 */
+/* ------------------------------------------------------------------------ */
+
+/* (int32_t)round(v) as gcc emits it on x86-64: libm round, then cvttsd2si,
+ * which yields INT32_MIN for NaN and for values outside int32 range. */
+static int32_t x86_round_to_i32(double v)
+{
+    double r = round(v);
+    if (!(r > -2147483649.0 && r < 2147483648.0)) return INT32_MIN;
+    return (int32_t)r;
+}
+
+/* q = (int32)round(x * inv_scale) + zp with the x86 wrap-around add, then the
+ * clamp to [-128, 127] (quantize.c:151-156). */
+static int8_t quant_one(double x, double inv_scale, int32_t zp)
+{
+    int32_t q = (int32_t)((uint32_t)x86_round_to_i32(x * inv_scale) + (uint32_t)zp);
+    if (q < -128) q = -128;
+    if (q > 127) q = 127;
+    return (int8_t)q;
+}
+
+/* Scalar epilogue of calibrate_minmax (quantize.c:62-82). */
+static void minmax_params(double mn, double mx, int symmetric, OraQuantParams *out)
+{
+    if (symmetric) {
+        double am = fmax(fabs(mn), fabs(mx));
+        if (am < 1e-30) am = 1e-30;
+        out->scale = am / 127.0;
+        out->zero_point = 0;
+        out->min_val = -am;
+        out->max_val = am;
+        out->symmetric = 1;
+    } else {
+        if (mn == mx) { mn -= 0.5; mx += 0.5; }
+        out->scale = (mx - mn) / 255.0;
+        if (out->scale < 1e-30) out->scale = 1e-30;
+        out->zero_point = x86_round_to_i32(-128.0 - mn / out->scale);
+        if (out->zero_point < -128) out->zero_point = -128;
+        if (out->zero_point > 127) out->zero_point = 127;
+        out->min_val = mn;
+        out->max_val = mx;
+        out->symmetric = 0;
+    }
+}
+
+/* calibrate_minmax (quantize.c:52-60): strict-compare running min/max from
+ * d[0] (NaNs are skipped unless d[0] is NaN). */
+int ora_calibrate_minmax(const double *d, int64_t n, int symmetric, OraQuantParams *out)
+{
+    if (!d || n <= 0 || !out) return -1;
+    double mn = d[0], mx = d[0];
+    for (int64_t i = 1; i < n; i++) {
+        if (d[i] < mn) mn = d[i];
+        if (d[i] > mx) mx = d[i];
+    }
+    minmax_params(mn, mx, symmetric, out);
+    return 0;
+}
+
+int ora_calibrate_minmax_f32(const float *d, int64_t n, int symmetric, OraQuantParams *out)
+{
+    if (!d || n <= 0 || !out) return -1;
+    double mn = d[0], mx = d[0];
+    for (int64_t i = 1; i < n; i++) {
+        double v = (double)d[i];
+        if (v < mn) mn = v;
+        if (v > mx) mx = v;
+    }
+    minmax_params(mn, mx, symmetric, out);
+    return 0;
+}
+
+/* quantize_tensor (quantize.c:144-158). */
+int ora_quantize(const double *d, int8_t *out, int64_t n, const OraQuantParams *p)
+{
+    if (!d || !out || n <= 0 || !p) return -1;
+    double inv = 1.0 / p->scale;
+    for (int64_t i = 0; i < n; i++) out[i] = quant_one(d[i], inv, p->zero_point);
+    return 0;
+}
+
+int ora_quantize_f32(const float *d, int8_t *out, int64_t n, const OraQuantParams *p)
+{
+    if (!d || !out || n <= 0 || !p) return -1;
+    double inv = 1.0 / p->scale;
+    for (int64_t i = 0; i < n; i++) out[i] = quant_one((double)d[i], inv, p->zero_point);
+    return 0;
+}
+
+/* dequantize_tensor (quantize.c:163-174): ((double)q - (double)zp) * scale. */
+int ora_dequantize(const int8_t *q, double *out, int64_t n, const OraQuantParams *p)
+{
+    if (!q || !out || n <= 0 || !p) return -1;
+    for (int64_t i = 0; i < n; i++) out[i] = ((double)q[i] - (double)p->zero_point) * p->scale;
+    return 0;
+}
+
+int ora_dequantize_f32(const int8_t *q, float *out, int64_t n, const OraQuantParams *p)
+{
+    if (!q || !out || n <= 0 || !p) return -1;
+    for (int64_t i = 0; i < n; i++)
+        out[i] = (float)(((double)q[i] - (double)p->zero_point) * p->scale);
+    return 0;
+}
+
+/* quantization_error / quantization_snr (quantize.c:222-269): fused
+ * quantize -> dequantize -> squared error, sequential double sums. */
+#define QERR_BODY(T)                                                       \
+    double inv = 1.0 / p->scale, sig = 0.0, noise = 0.0;                   \
+    for (int64_t i = 0; i < n; i++) {                                      \
+        double x = (double)d[i];                                           \
+        sig += x * x;                                                      \
+        int8_t q = quant_one(x, inv, p->zero_point);                       \
+        double rec = ((double)q - (double)p->zero_point) * p->scale;       \
+        double diff = x - rec;                                             \
+        noise += diff * diff;                                              \
+    }
+
+double ora_quant_error(const double *d, int64_t n, const OraQuantParams *p)
+{
+    if (!d || n <= 0 || !p) return -1.0;
+    QERR_BODY(double)
+    (void)sig;
+    return noise / (double)n;
+}
+
+double ora_quant_snr(const double *d, int64_t n, const OraQuantParams *p)
+{
+    if (!d || n <= 0 || !p) return -1.0;
+    QERR_BODY(double)
+    if (noise < 1e-30) return 999.0;
+    return 10.0 * log10(sig / noise);
+}
+
+double ora_quant_error_f32(const float *d, int64_t n, const OraQuantParams *p)
+{
+    if (!d || n <= 0 || !p) return -1.0;
+    QERR_BODY(float)
+    (void)sig;
+    return noise / (double)n;
+}
+
+double ora_quant_snr_f32(const float *d, int64_t n, const OraQuantParams *p)
+{
+    if (!d || n <= 0 || !p) return -1.0;
+    QERR_BODY(float)
+    if (noise < 1e-30) return 999.0;
+    return 10.0 * log10(sig / noise);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Optimizers: src/c/optimizers_c.c:218-348                                  */
+/* ------------------------------------------------------------------------ */
+
+/* bc = 1 - pow(beta, t) (optimizers_c.c:258-260, 302-304). */
+double ora_bias_correction(double beta, int64_t t) { return 1.0 - pow(beta, (double)t); }
+
+/* sgd_step_impl (optimizers_c.c:218-249). */
+void ora_sgd_f32(float *p, const float *g, double *vel, int64_t n, double lr, double mom)
+{
+    for (int64_t j = 0; j < n; j++) {
+        double grad = (double)g[j];
+        vel[j] = mom * vel[j] + grad;
+        p[j] -= (float)(lr * vel[j]);
+    }
+}
+
+void ora_sgd_f64(double *p, const double *g, double *vel, int64_t n, double lr, double mom)
+{
+    for (int64_t j = 0; j < n; j++) {
+        vel[j] = mom * vel[j] + g[j];
+        p[j] -= lr * vel[j];
+    }
+}
+
+/* adam_step_impl (optimizers_c.c:251-293): the f32 update is subtracted in
+ * float after one rounding of the double step. */
+void ora_adam_f32(float *p, const float *g, double *m, double *v, int64_t n, double lr,
+                  double b1, double b2, double eps, double bc1, double bc2)
+{
+    for (int64_t j = 0; j < n; j++) {
+        double grad = (double)g[j];
+        m[j] = b1 * m[j] + (1.0 - b1) * grad;
+        v[j] = b2 * v[j] + (1.0 - b2) * grad * grad;
+        double mh = m[j] / bc1;
+        double vh = v[j] / bc2;
+        p[j] -= (float)(lr * mh / (sqrt(vh) + eps));
+    }
+}
+
+void ora_adam_f64(double *p, const double *g, double *m, double *v, int64_t n, double lr,
+                  double b1, double b2, double eps, double bc1, double bc2)
+{
+    for (int64_t j = 0; j < n; j++) {
+        double grad = g[j];
+        m[j] = b1 * m[j] + (1.0 - b1) * grad;
+        v[j] = b2 * v[j] + (1.0 - b2) * grad * grad;
+        double mh = m[j] / bc1;
+        double vh = v[j] / bc2;
+        p[j] -= lr * mh / (sqrt(vh) + eps);
+    }
+}
+
+/* adamw_step_impl (optimizers_c.c:295-348): decoupled decay on the double
+ * copy of the parameter, then the Adam step, one rounding at the end. */
+void ora_adamw_f32(float *p, const float *g, double *m, double *v, int64_t n, double lr,
+                   double b1, double b2, double eps, double wd, double bc1, double bc2)
+{
+    for (int64_t j = 0; j < n; j++) {
+        double param = (double)p[j];
+        double grad = (double)g[j];
+        param -= lr * wd * param;
+        m[j] = b1 * m[j] + (1.0 - b1) * grad;
+        v[j] = b2 * v[j] + (1.0 - b2) * grad * grad;
+        double mh = m[j] / bc1;
+        double vh = v[j] / bc2;
+        param -= lr * mh / (sqrt(vh) + eps);
+        p[j] = (float)param;
+    }
+}
+
+void ora_adamw_f64(double *p, const double *g, double *m, double *v, int64_t n, double lr,
+                   double b1, double b2, double eps, double wd, double bc1, double bc2)
+{
+    for (int64_t j = 0; j < n; j++) {
+        double param = p[j];
+        double grad = g[j];
+        param -= lr * wd * param;
+        m[j] = b1 * m[j] + (1.0 - b1) * grad;
+        v[j] = b2 * v[j] + (1.0 - b2) * grad * grad;
+        double mh = m[j] / bc1;
+        double vh = v[j] / bc2;
+        param -= lr * mh / (sqrt(vh) + eps);
+        p[j] = param;
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* NaN / Inf scans and the L2 norm: src/asm/training_ops.asm:544-696         */
+/* ------------------------------------------------------------------------ */
+
+/* tensor_has_nan (training_ops.asm:544-574): ucomiss x,x unordered. */
+int ora_has_nan_f32(const float *x, uint64_t n)
+{
+    if (!x || n == 0) return 0;
+    for (uint64_t i = 0; i < n; i++) if (x[i] != x[i]) return 1;
+    return 0;
+}
+
+/* tensor_has_inf (training_ops.asm:585-621): (bits & 0x7fffffff) == 0x7f800000. */
+int ora_has_inf_f32(const float *x, uint64_t n)
+{
+    if (!x || n == 0) return 0;
+    for (uint64_t i = 0; i < n; i++) {
+        uint32_t u;
+        memcpy(&u, &x[i], 4);
+        if ((u & 0x7fffffffu) == 0x7f800000u) return 1;
+    }
+    return 0;
+}
+
+/* tensor_grad_l2_norm (training_ops.asm:636-696): four float lanes of x*x
+ * (mulps/addps), then (l0+l2)+(l1+l3) (movhlps/addps/shufps/addss), then the
+ * n%4 tail squared and added one by one, then sqrtss. */
+float ora_l2_ref_f32(const float *x, uint64_t n)
+{
+    if (!x || n == 0) return 0.0f;
+    float l[4] = {0, 0, 0, 0};
+    uint64_t nv = n / 4;
+    for (uint64_t i = 0; i < nv; i++)
+        for (int k = 0; k < 4; k++) {
+            float sq = x[i * 4 + k] * x[i * 4 + k];
+            l[k] = l[k] + sq;
+        }
+    float s = 0.0f;
+    if (nv > 0) s = (l[0] + l[2]) + (l[1] + l[3]);
+    for (uint64_t i = nv * 4; i < n; i++) {
+        float sq = x[i] * x[i];
+        s = s + sq;
+    }
+    return sqrtf(s);
+}
+
+/* Exact sum of squares in double (squares of floats are exact in double). */
+double ora_sumsq_exact_f32(const float *x, uint64_t n)
+{
+    double s = 0.0, c = 0.0;
+    for (uint64_t i = 0; i < n; i++) {
+        double v = (double)x[i] * (double)x[i];
+        double t = s + v;
+        if (fabs(s) >= fabs(v)) c += (s - t) + v;
+        else c += (v - t) + s;
+        s = t;
+    }
+    return s + c;
+}
+
+/* ------------------------------------------------------------------------ */
+/* 2-D f64 copies: src/c/tensor_ops.c:15-148                                 */
+/* ------------------------------------------------------------------------ */
+
+int ora_concat_2d(const double *a, const double *b, int64_t ra, int64_t ca, int64_t rb,
+                  int64_t cb, int64_t axis, double *out, int64_t *orows, int64_t *ocols)
+{
+    if (!a || !b || !out || !orows || !ocols) return -1;
+    if (ra <= 0 || ca <= 0 || rb <= 0 || cb <= 0) return -1;
+    if (axis == 0) {
+        if (ca != cb) return -1;
+        *orows = ra + rb;
+        *ocols = ca;
+        for (int64_t i = 0; i < ra * ca; i++) out[i] = a[i];
+        for (int64_t i = 0; i < rb * cb; i++) out[ra * ca + i] = b[i];
+        return 0;
+    }
+    if (axis != 1 || ra != rb) return -1;
+    *orows = ra;
+    *ocols = ca + cb;
+    for (int64_t r = 0; r < ra; r++) {
+        for (int64_t c = 0; c < ca; c++) out[r * (ca + cb) + c] = a[r * ca + c];
+        for (int64_t c = 0; c < cb; c++) out[r * (ca + cb) + ca + c] = b[r * cb + c];
+    }
+    return 0;
+}
+
+int ora_split_2d(const double *in, int64_t rows, int64_t cols, int64_t axis, int64_t split,
+                 double *oa, double *ob, int64_t *ra, int64_t *ca, int64_t *rb, int64_t *cb)
+{
+    if (!in || !oa || !ob || !ra || !ca || !rb || !cb) return -1;
+    if (rows <= 0 || cols <= 0) return -1;
+    if (axis == 0) {
+        if (split <= 0 || split >= rows) return -1;
+        *ra = split; *ca = cols; *rb = rows - split; *cb = cols;
+        for (int64_t i = 0; i < split * cols; i++) oa[i] = in[i];
+        for (int64_t i = 0; i < (rows - split) * cols; i++) ob[i] = in[split * cols + i];
+        return 0;
+    }
+    if (axis != 1) return -1;
+    if (split <= 0 || split >= cols) return -1;
+    *ra = rows; *ca = split; *rb = rows; *cb = cols - split;
+    for (int64_t r = 0; r < rows; r++) {
+        for (int64_t c = 0; c < split; c++) oa[r * split + c] = in[r * cols + c];
+        for (int64_t c = split; c < cols; c++) ob[r * (cols - split) + c - split] = in[r * cols + c];
+    }
+    return 0;
+}
+
+int ora_pad_2d(const double *in, int64_t rows, int64_t cols, int64_t pt, int64_t pb,
+               int64_t pl, int64_t pr, double value, double *out, int64_t *orows, int64_t *ocols)
+{
+    if (!in || !out || !orows || !ocols) return -1;
+    if (rows <= 0 || cols <= 0) return -1;
+    if (pt < 0 || pb < 0 || pl < 0 || pr < 0) return -1;
+    int64_t R = rows + pt + pb, C = cols + pl + pr;
+    *orows = R;
+    *ocols = C;
+    for (int64_t i = 0; i < R * C; i++) out[i] = value;
+    for (int64_t r = 0; r < rows; r++)
+        for (int64_t c = 0; c < cols; c++) out[(r + pt) * C + pl + c] = in[r * cols + c];
+    return 0;
+}
+
+int ora_transpose_2d(const double *in, int64_t rows, int64_t cols, double *out)
+{
+    if (!in || !out) return -1;
+    if (rows <= 0 || cols <= 0) return -1;
+    for (int64_t r = 0; r < rows; r++)
+        for (int64_t c = 0; c < cols; c++) out[c * rows + r] = in[r * cols + c];
+    return 0;
+}

@@ -1,0 +1,317 @@
+"""
+ctypes/numpy wrapper of the CPU oracle (liboracle.so) and of the reference's
+own C compiled unchanged (_ref/libneural_ref.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, as the checker.  The product (libneural_hip.so,
+pyneural) never loads it.
+"""
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ORACLE_SO = HERE / "liboracle.so"
+REF_SO = HERE / "_ref" / "libneural_ref.so"
+
+ADD, SUB, MUL, DIV, MAX = 0, 1, 2, 3, 4
+ACTS = ["tanh", "gelu", "leaky_relu", "elu", "selu", "swish", "mish", "hardswish", "softplus", "hardtanh", "sigmoid"]
+ACT_CODE = {name: i for i, name in enumerate(ACTS)}
+
+
+class QuantParams(ctypes.Structure):
+    _fields_ = [("scale", ctypes.c_double), ("zero_point", ctypes.c_int32), ("min_val", ctypes.c_double),
+                ("max_val", ctypes.c_double), ("symmetric", ctypes.c_int)]
+
+
+_lib = None
+_ref = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not ORACLE_SO.exists():
+            raise RuntimeError(f"{ORACLE_SO} missing: run `make -C oracle`")
+        _lib = ctypes.CDLL(str(ORACLE_SO))
+        _lib.ora_sum_ref_f32.restype = ctypes.c_float
+        _lib.ora_sum_ref_f64.restype = ctypes.c_double
+        for n in ("ora_sum_exact_f32", "ora_sum_exact_f64", "ora_max_chain_f64", "ora_quant_error",
+                  "ora_quant_snr", "ora_quant_error_f32", "ora_quant_snr_f32", "ora_bias_correction",
+                  "ora_sumsq_exact_f32"):
+            getattr(_lib, n).restype = ctypes.c_double
+        _lib.ora_max_chain_f32.restype = ctypes.c_float
+        _lib.ora_l2_ref_f32.restype = ctypes.c_float
+        _lib.ora_argmax_f32.restype = ctypes.c_int64
+        _lib.ora_argmax_f64.restype = ctypes.c_int64
+        _lib.ora_bias_correction.argtypes = [ctypes.c_double, ctypes.c_int64]
+    return _lib
+
+
+def ref():
+    """The reference's C (activations_c.c, quantize.c, optimizers_c.c,
+    tensor_ops.c, metrics_losses.c) built by oracle/Makefile; None if absent."""
+    global _ref
+    if _ref is None and REF_SO.exists():
+        _ref = ctypes.CDLL(str(REF_SO))
+        _ref.quantization_error.restype = ctypes.c_double
+        _ref.quantization_snr.restype = ctypes.c_double
+        _ref.opt_sgd_create.restype = ctypes.c_void_p
+        _ref.opt_adam_create.restype = ctypes.c_void_p
+        _ref.opt_adamw_create.restype = ctypes.c_void_p
+        _ref.opt_state_bytes.restype = ctypes.c_int64
+        for n in ("opt_sgd_create", "opt_adam_create", "opt_adamw_create"):
+            getattr(_ref, n).argtypes = [ctypes.c_double] * {"opt_sgd_create": 2, "opt_adam_create": 4,
+                                                            "opt_adamw_create": 5}[n]
+        _ref.opt_step.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+        _ref.opt_free.argtypes = [ctypes.c_void_p]
+        _ref.opt_state_bytes.argtypes = [ctypes.c_void_p]
+        _ref.opt_state_export.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+    return _ref
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _f64(x):
+    return ctypes.c_double(float(x))
+
+
+# ---- elementwise ----------------------------------------------------------------
+
+def ew(op, a, b):
+    out = np.empty_like(a)
+    fn = lib().ora_ew_f32 if a.dtype == np.float32 else lib().ora_ew_f64
+    fn(ctypes.c_int(op), _p(a), _p(b), _p(out), ctypes.c_int64(a.size))
+    return out
+
+
+def scalar(op, a, s):
+    out = np.empty_like(a)
+    fn = lib().ora_scalar_f32 if a.dtype == np.float32 else lib().ora_scalar_f64
+    fn(ctypes.c_int(op), _p(a), _f64(s), _p(out), ctypes.c_int64(a.size))
+    return out
+
+
+def neg(a):
+    out = np.empty_like(a)
+    (lib().ora_neg_f32 if a.dtype == np.float32 else lib().ora_neg_f64)(_p(a), _p(out), ctypes.c_int64(a.size))
+    return out
+
+
+def relu(a):
+    out = np.empty_like(a)
+    (lib().ora_relu_f32 if a.dtype == np.float32 else lib().ora_relu_f64)(_p(a), _p(out), ctypes.c_int64(a.size))
+    return out
+
+
+def bias_add(x, b):
+    rows, cols = x.shape
+    out = np.empty_like(x)
+    fn = lib().ora_bias_add_f32 if x.dtype == np.float32 else lib().ora_bias_add_f64
+    fn(_p(x), _p(b), _p(out), ctypes.c_int64(rows), ctypes.c_int64(cols))
+    return out
+
+
+# ---- reductions -------------------------------------------------------------------
+
+def sum_ref(x):
+    f = lib().ora_sum_ref_f32 if x.dtype == np.float32 else lib().ora_sum_ref_f64
+    return f(_p(x), ctypes.c_int64(x.size))
+
+
+def sum_exact(x):
+    f = lib().ora_sum_exact_f32 if x.dtype == np.float32 else lib().ora_sum_exact_f64
+    return f(_p(x), ctypes.c_int64(x.size))
+
+
+def rowsum_ref(x):
+    rows, cols = x.shape
+    out = np.empty(rows, dtype=x.dtype)
+    f = lib().ora_rowsum_ref_f32 if x.dtype == np.float32 else lib().ora_rowsum_ref_f64
+    f(_p(x), ctypes.c_int64(rows), ctypes.c_int64(cols), _p(out))
+    return out
+
+
+def rowsum_exact(x):
+    rows, cols = x.shape
+    out = np.empty(rows, dtype=np.float64)
+    f = lib().ora_rowsum_exact_f32 if x.dtype == np.float32 else lib().ora_rowsum_exact_f64
+    f(_p(x), ctypes.c_int64(rows), ctypes.c_int64(cols), _p(out))
+    return out
+
+
+def colsum_ref(x):
+    rows, cols = x.shape
+    out = np.empty(cols, dtype=x.dtype)
+    f = lib().ora_colsum_ref_f32 if x.dtype == np.float32 else lib().ora_colsum_ref_f64
+    f(_p(x), ctypes.c_int64(rows), ctypes.c_int64(cols), _p(out))
+    return out
+
+
+def max_chain(x):
+    f = lib().ora_max_chain_f32 if x.dtype == np.float32 else lib().ora_max_chain_f64
+    return f(_p(x), ctypes.c_int64(x.size))
+
+
+def rowmax_chain(x):
+    rows, cols = x.shape
+    out = np.empty(rows, dtype=x.dtype)
+    f = lib().ora_rowmax_chain_f32 if x.dtype == np.float32 else lib().ora_rowmax_chain_f64
+    f(_p(x), ctypes.c_int64(rows), ctypes.c_int64(cols), _p(out))
+    return out
+
+
+def argmax(x):
+    f = lib().ora_argmax_f32 if x.dtype == np.float32 else lib().ora_argmax_f64
+    return f(_p(x), ctypes.c_int64(x.size))
+
+
+def rowargmax(x):
+    rows, cols = x.shape
+    out = np.empty(rows, dtype=np.int64)
+    f = lib().ora_rowargmax_f32 if x.dtype == np.float32 else lib().ora_rowargmax_f64
+    f(_p(x), ctypes.c_int64(rows), ctypes.c_int64(cols), _p(out))
+    return out
+
+
+def softmax_rows(x, log=False):
+    rows, cols = x.shape
+    out = np.empty_like(x)
+    name = ("ora_log_softmax_rows_" if log else "ora_softmax_rows_") + ("f32" if x.dtype == np.float32 else "f64")
+    getattr(lib(), name)(_p(x), ctypes.c_int64(rows), ctypes.c_int64(cols), _p(out))
+    return out
+
+
+# ---- activations ---------------------------------------------------------------------
+
+def act(name, x, alpha=0.0):
+    out = np.empty_like(x)
+    f = lib().ora_act_f32 if x.dtype == np.float32 else lib().ora_act_f64
+    f(ctypes.c_int(ACT_CODE[name]), _p(x), _p(out), ctypes.c_int64(x.size), _f64(alpha))
+    return out
+
+
+# ---- quantization ---------------------------------------------------------------------
+
+def calibrate(x, symmetric):
+    p = QuantParams()
+    f = lib().ora_calibrate_minmax_f32 if x.dtype == np.float32 else lib().ora_calibrate_minmax
+    rc = f(_p(x), ctypes.c_int64(x.size), ctypes.c_int(1 if symmetric else 0), ctypes.byref(p))
+    assert rc == 0
+    return p
+
+
+def quantize(x, p):
+    out = np.empty(x.size, dtype=np.int8)
+    f = lib().ora_quantize_f32 if x.dtype == np.float32 else lib().ora_quantize
+    assert f(_p(x), _p(out), ctypes.c_int64(x.size), ctypes.byref(p)) == 0
+    return out
+
+
+def dequantize(q, p, dtype=np.float64):
+    out = np.empty(q.size, dtype=dtype)
+    f = lib().ora_dequantize_f32 if dtype == np.float32 else lib().ora_dequantize
+    assert f(_p(q), _p(out), ctypes.c_int64(q.size), ctypes.byref(p)) == 0
+    return out
+
+
+def quant_error(x, p):
+    f = lib().ora_quant_error_f32 if x.dtype == np.float32 else lib().ora_quant_error
+    return f(_p(x), ctypes.c_int64(x.size), ctypes.byref(p))
+
+
+def quant_snr(x, p):
+    f = lib().ora_quant_snr_f32 if x.dtype == np.float32 else lib().ora_quant_snr
+    return f(_p(x), ctypes.c_int64(x.size), ctypes.byref(p))
+
+
+# ---- optimizers ------------------------------------------------------------------------
+
+def bias_correction(beta, t):
+    return lib().ora_bias_correction(beta, t)
+
+
+def adamw_step(p, g, m, v, lr, b1, b2, eps, wd, t):
+    """In-place AdamW step number t (1-based) on numpy buffers."""
+    bc1, bc2 = bias_correction(b1, t), bias_correction(b2, t)
+    n = ctypes.c_int64(p.size)
+    args = [_f64(lr), _f64(b1), _f64(b2), _f64(eps), _f64(wd), _f64(bc1), _f64(bc2)]
+    f = lib().ora_adamw_f32 if p.dtype == np.float32 else lib().ora_adamw_f64
+    f(_p(p), _p(g), _p(m), _p(v), n, *args)
+
+
+def adam_step(p, g, m, v, lr, b1, b2, eps, t):
+    bc1, bc2 = bias_correction(b1, t), bias_correction(b2, t)
+    n = ctypes.c_int64(p.size)
+    args = [_f64(lr), _f64(b1), _f64(b2), _f64(eps), _f64(bc1), _f64(bc2)]
+    f = lib().ora_adam_f32 if p.dtype == np.float32 else lib().ora_adam_f64
+    f(_p(p), _p(g), _p(m), _p(v), n, *args)
+
+
+def sgd_step(p, g, vel, lr, mom):
+    f = lib().ora_sgd_f32 if p.dtype == np.float32 else lib().ora_sgd_f64
+    f(_p(p), _p(g), _p(vel), ctypes.c_int64(p.size), _f64(lr), _f64(mom))
+
+
+# ---- scans ------------------------------------------------------------------------------
+
+def has_nan(x):
+    return lib().ora_has_nan_f32(_p(x), ctypes.c_uint64(x.size))
+
+
+def has_inf(x):
+    return lib().ora_has_inf_f32(_p(x), ctypes.c_uint64(x.size))
+
+
+def l2_ref(x):
+    return lib().ora_l2_ref_f32(_p(x), ctypes.c_uint64(x.size))
+
+
+def sumsq_exact(x):
+    return lib().ora_sumsq_exact_f32(_p(x), ctypes.c_uint64(x.size))
+
+
+# ---- tensor ops ------------------------------------------------------------------------------
+
+def concat_2d(a, b, ra, ca, rb, cb, axis):
+    out = np.zeros((ra + rb) * (ca + cb), dtype=np.float64)
+    r, c = ctypes.c_int64(), ctypes.c_int64()
+    rc = lib().ora_concat_2d(_p(a), _p(b), ctypes.c_int64(ra), ctypes.c_int64(ca), ctypes.c_int64(rb),
+                             ctypes.c_int64(cb), ctypes.c_int64(axis), _p(out), ctypes.byref(r), ctypes.byref(c))
+    return rc, out[: r.value * c.value] if rc == 0 else None, r.value, c.value
+
+
+def transpose_2d(a, rows, cols):
+    out = np.zeros(rows * cols, dtype=np.float64)
+    rc = lib().ora_transpose_2d(_p(a), ctypes.c_int64(rows), ctypes.c_int64(cols), _p(out))
+    return rc, out
+
+
+def pad_2d(a, rows, cols, pt, pb, pl, pr, value):
+    R, C = rows + pt + pb, cols + pl + pr
+    out = np.zeros(max(R * C, 1), dtype=np.float64)
+    r, c = ctypes.c_int64(), ctypes.c_int64()
+    rc = lib().ora_pad_2d(_p(a), ctypes.c_int64(rows), ctypes.c_int64(cols), ctypes.c_int64(pt),
+                          ctypes.c_int64(pb), ctypes.c_int64(pl), ctypes.c_int64(pr), _f64(value), _p(out),
+                          ctypes.byref(r), ctypes.byref(c))
+    return rc, out[: R * C], r.value, c.value
+
+
+def split_2d(a, rows, cols, axis, split):
+    oa = np.zeros(rows * cols, dtype=np.float64)
+    ob = np.zeros(rows * cols, dtype=np.float64)
+    ra, ca, rb, cb = (ctypes.c_int64() for _ in range(4))
+    rc = lib().ora_split_2d(_p(a), ctypes.c_int64(rows), ctypes.c_int64(cols), ctypes.c_int64(axis),
+                            ctypes.c_int64(split), _p(oa), _p(ob), ctypes.byref(ra), ctypes.byref(ca),
+                            ctypes.byref(rb), ctypes.byref(cb))
+    return rc, oa[: ra.value * ca.value], ob[: rb.value * cb.value], (ra.value, ca.value, rb.value, cb.value)
+
+
+def build_info():
+    return {"oracle": str(ORACLE_SO), "ref": str(REF_SO) if REF_SO.exists() else None,
+            "pid": os.getpid()}

@@ -1,0 +1,80 @@
+"""Activation parity (activations_c.c:124-158, activations.asm:352-413).
+
+Piecewise-linear activations (leaky_relu, hardswish, hardtanh) are bit-exact.
+Transcendental ones use the same double formula: REL32 (1e-5 relative) for
+f32 outputs and REL64 (1e-12 relative + 1e-15 absolute) for f64 outputs,
+against the oracle (glibc libm) on inputs normal(0,4) with 1% set to +-30.
+"""
+
+import numpy as np
+import pytest
+
+from conftest import GPU, rel_close, same_bits
+
+pytestmark = GPU
+
+EXACT = {"leaky_relu", "hardswish", "hardtanh"}
+ACTS = ["tanh", "gelu", "leaky_relu", "elu", "selu", "swish", "mish", "hardswish", "softplus", "hardtanh", "sigmoid"]
+ALPHA = {"leaky_relu": 0.01, "elu": 1.0}
+
+
+def _inputs(dt, n=1 << 20, seed=4):
+    rng = np.random.default_rng(seed)
+    x = rng.normal(0, 4, n)
+    idx = rng.choice(n, size=n // 100, replace=False)
+    x[idx] = np.where(rng.random(idx.size) < 0.5, -30.0, 30.0)
+    x[:8] = [0.0, -0.0, 3.0, -3.0, 1.0, -1.0, 1e-310, -700.0]
+    return x.astype(dt)
+
+
+def _run(pn, name, x):
+    import ctypes
+    t = pn.Tensor.from_numpy(x)
+    out = pn.Tensor.create(t.shape, t.dtype)
+    lib = pn.core._lib
+    if name == "sigmoid":
+        rc = lib.neural_sigmoid(out._ptr, t._ptr)
+    elif name in ALPHA:
+        rc = getattr(lib, "act_" + name)(out._ptr, t._ptr, ctypes.c_double(ALPHA[name]))
+    else:
+        rc = getattr(lib, "act_" + name)(out._ptr, t._ptr)
+    assert rc == 0
+    return out.numpy()
+
+
+@pytest.mark.parametrize("name", ACTS)
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_activation(pn, ora, name, dt):
+    x = _inputs(dt)
+    got = _run(pn, name, x)
+    want = ora.act(name, x, ALPHA.get(name, 0.0))
+    if name in EXACT:
+        same_bits(got, want)
+    elif dt == np.float32:
+        rel_close(got, want, 1e-5, 0.0, name)
+    else:
+        rel_close(got, want, 1e-12, 1e-15, name)
+
+
+def test_activation_4d_nchw(pn, ora):
+    """cfg3 layout [64,64,128,128] at a reduced batch (N=2), NCHW contiguous."""
+    x = _inputs(np.float32, n=2 * 64 * 128 * 128, seed=9).reshape(2, 64, 128, 128)
+    t = pn.Tensor.from_numpy(x)
+    y = pn.GELU()(t).numpy()
+    rel_close(y, ora.act("gelu", x.ravel()).reshape(x.shape), 1e-5, 0.0, "gelu 4d")
+    y = pn.LeakyReLU(0.2)(t).numpy()
+    same_bits(y, ora.act("leaky_relu", x.ravel(), 0.2).reshape(x.shape))
+
+
+def test_modules_and_aliases(pn, ora):
+    x = _inputs(np.float64, n=4096, seed=3)
+    t = pn.Tensor.from_numpy(x)
+    for mod, name, alias in [(pn.Mish(), "mish", "neural_mish"), (pn.Softplus(), "softplus", "neural_softplus"),
+                             (pn.Swish(), "swish", "neural_swish"), (pn.SELU(), "selu", "neural_selu"),
+                             (pn.Tanh(), "tanh", "neural_tanh"), (pn.HardSwish(), "hardswish", "neural_hardswish")]:
+        want = ora.act(name, x)
+        rel_close(mod(t).numpy(), want, 1e-12, 1e-15, name)
+        out = pn.Tensor.create(t.shape, t.dtype)
+        assert getattr(pn.core._lib, alias)(out._ptr, t._ptr) == 0
+        rel_close(out.numpy(), want, 1e-12, 1e-15, alias)
+    assert pn.core._lib.act_gelu(None, t._ptr) == pn.NeuralError.NULL_POINTER

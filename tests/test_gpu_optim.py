@@ -1,0 +1,149 @@
+"""Optimizer parity (optimizers_c.c:218-562).
+
+Params and the float64 m / v (or velocity) buffers are bit-exact against the
+oracle after several steps, for f32 and f64 params, including NaN / Inf
+gradients.  The OPTS state blob matches the reference's own optimizers_c.c
+byte for byte (oracle/_ref, when built), and round-trips through import.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import GPU, same_bits
+
+pytestmark = GPU
+
+LR, B1, B2, EPS, WD = 1e-3, 0.9, 0.999, 1e-8, 0.01
+
+
+def _data(n, dt, seed, inject=False):
+    rng = np.random.default_rng(seed)
+    p = rng.normal(0, 0.02, n).astype(dt)
+    g = rng.normal(0, 1e-3, n).astype(dt)
+    if inject and n > 200:
+        idx = rng.choice(n, 96, replace=False)
+        g[idx[:32]] = np.nan
+        g[idx[32:64]] = np.inf
+        g[idx[64:]] = -np.inf
+    return p, g
+
+
+def _blob_moments(blob, sizes, nbuf):
+    off = 80 + 8 * len(sizes)
+    out = []
+    for _ in range(nbuf):
+        for s in sizes:
+            out.append(np.frombuffer(blob[off: off + 8 * s], dtype=np.float64).copy())
+            off += 8 * s
+    return out
+
+
+@pytest.mark.parametrize("kind", ["adamw", "adam", "sgd"])
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+@pytest.mark.parametrize("n", [5, 4099, 1 << 20])
+def test_steps_bit_exact(pn, ora, kind, dt, n):
+    p, g = _data(n, dt, seed=n, inject=True)
+    p2, g2 = _data(77, dt, seed=n + 1)
+    tp, tg = pn.Tensor.from_numpy(p), pn.Tensor.from_numpy(g)
+    tp2, tg2 = pn.Tensor.from_numpy(p2), pn.Tensor.from_numpy(g2)
+    if kind == "adamw":
+        opt = pn.AdamW(LR, B1, B2, EPS, WD)
+    elif kind == "adam":
+        opt = pn.Adam(LR, B1, B2, EPS)
+    else:
+        opt = pn.SGD(0.01, 0.9)
+    rp, rp2 = p.copy(), p2.copy()
+    m, v = np.zeros(n), np.zeros(n)
+    m2, v2 = np.zeros(77), np.zeros(77)
+    for t in range(1, 4):
+        opt.step([tp, tp2], [tg, tg2])
+        if kind == "adamw":
+            ora.adamw_step(rp, g, m, v, LR, B1, B2, EPS, WD, t)
+            ora.adamw_step(rp2, g2, m2, v2, LR, B1, B2, EPS, WD, t)
+        elif kind == "adam":
+            ora.adam_step(rp, g, m, v, LR, B1, B2, EPS, t)
+            ora.adam_step(rp2, g2, m2, v2, LR, B1, B2, EPS, t)
+        else:
+            ora.sgd_step(rp, g, m, 0.01, 0.9)
+            ora.sgd_step(rp2, g2, m2, 0.01, 0.9)
+    same_bits(tp.numpy(), rp)
+    same_bits(tp2.numpy(), rp2)
+    blob = opt.state_bytes()
+    if kind == "sgd":
+        got_m, got_m2 = _blob_moments(blob, [n, 77], 1)
+        same_bits(got_m, m)
+        same_bits(got_m2, m2)
+    else:
+        gm, gm2, gv, gv2 = _blob_moments(blob, [n, 77], 2)
+        same_bits(gm, m)
+        same_bits(gv, v)
+        same_bits(gm2, m2)
+        same_bits(gv2, v2)
+
+
+def test_state_roundtrip_and_reference_blob(pn, ora):
+    p, g = _data(1000, np.float32, 3)
+    tp, tg = pn.Tensor.from_numpy(p), pn.Tensor.from_numpy(g)
+    opt = pn.AdamW(LR, B1, B2, EPS, WD)
+    opt.step([tp], [tg])
+    opt.step([tp], [tg])
+    blob = opt.state_bytes()
+    assert len(blob) == 80 + 8 + 2 * 8 * 1000
+    hdr = np.frombuffer(blob[:16], dtype=np.uint32)
+    assert hdr[0] == 0x5354504F and hdr[1] == 1
+    # resume: a fresh optimizer loaded from the blob continues identically
+    opt2 = pn.AdamW(0.5, 0.5, 0.5, 0.5, 0.5)
+    opt2.load_state_bytes(blob)
+    assert opt2.lr == LR
+    tq = pn.Tensor.from_numpy(tp.numpy())
+    opt.step([tp], [tg])
+    opt2.step([tq], [tg])
+    same_bits(tq.numpy(), tp.numpy())
+    assert opt2.state_bytes() == opt.state_bytes()
+
+    ref = ora.ref()
+    if ref is None:
+        pytest.skip("oracle/_ref not built")
+
+    class TensorC(ctypes.Structure):
+        _fields_ = [("data", ctypes.c_void_p), ("ndim", ctypes.c_int64), ("shape", ctypes.POINTER(ctypes.c_int64)),
+                    ("stride", ctypes.c_void_p), ("dtype", ctypes.c_int32), ("flags", ctypes.c_int32)]
+
+    rp = p.copy()
+    shape = (ctypes.c_int64 * 1)(1000)
+    tpc = TensorC(rp.ctypes.data, 1, shape, None, 0, 0)
+    tgc = TensorC(g.ctypes.data, 1, shape, None, 0, 0)
+    h = ref.opt_adamw_create(LR, B1, B2, EPS, WD)
+    pp = (ctypes.c_void_p * 1)(ctypes.addressof(tpc))
+    gp = (ctypes.c_void_p * 1)(ctypes.addressof(tgc))
+    for _ in range(3):
+        assert ref.opt_step(h, pp, gp, 1) == 0
+    nb = ref.opt_state_bytes(h)
+    buf = (ctypes.c_uint8 * nb)()
+    assert ref.opt_state_export(h, buf, nb) == 0
+    assert bytes(buf) == opt.state_bytes(), "OPTS blob differs from the reference optimizers_c.c"
+    same_bits(tp.numpy(), rp)
+    ref.opt_free(h)
+
+
+def test_step_errors(pn):
+    opt = pn.Adam()
+    a, b = pn.Tensor.create([10]), pn.Tensor.create([10])
+    opt.step([a], [b])
+    lib = pn.core._lib
+    arr = (ctypes.c_void_p * 2)(a._ptr, b._ptr)
+    assert lib.opt_step(opt._ptr, arr, arr, 2) == pn.NeuralError.INVALID_ARGUMENT
+    assert lib.opt_step(opt._ptr, arr, arr, -1) == pn.NeuralError.INVALID_ARGUMENT
+    assert lib.opt_step(None, arr, arr, 1) == pn.NeuralError.NULL_POINTER
+    c = pn.Tensor.create([11])
+    arr1 = (ctypes.c_void_p * 1)(c._ptr)
+    assert lib.opt_step(opt._ptr, arr1, arr1, 1) == pn.NeuralError.SHAPE_MISMATCH
+    bad = bytearray(opt.state_bytes())
+    bad[0] ^= 0xFF
+    with pytest.raises(pn.NeuralException):
+        opt.load_state_bytes(bytes(bad))
+    sgd = pn.SGD()
+    with pytest.raises(pn.NeuralException):
+        sgd.load_state_bytes(opt.state_bytes())  # type mismatch -> INVALID_ARGUMENT
