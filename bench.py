@@ -60,17 +60,6 @@ def traffic_from_profile():
         return None
 
 
-class Timer:
-    """HIP-event timing on the stream the library launches on (torch's current
-    stream, handed to the library with neural_hip_set_stream)."""
-
-    def __init__(self, torch):
-        self.torch = torch
-
-    def events(self):
-        return self.torch.cuda.Event(enable_timing=True), self.torch.cuda.Event(enable_timing=True)
-
-
 def main():
     args = parse()
     if args.gpus != 1:
@@ -87,7 +76,10 @@ def main():
     from pyneural.core import _lib, _check_error
 
     pn.init()
-    stream = torch.cuda.current_stream()
+    # A dedicated (non-null) torch stream: the library launches on it and the
+    # HIP events below are recorded on it.
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
     pn.set_stream(stream.cuda_stream)
     dev = torch.device("cuda:0")
 

@@ -257,9 +257,11 @@ int tensor_transpose2d_array(const double *in, int64_t rows, int64_t cols, doubl
 
 /* ---- HIP runtime controls (NEW) ------------------------------------------------- */
 /* Use an existing HIP stream (e.g. torch.cuda.current_stream().cuda_stream) for
- * all later launches; NULL restores the library's own stream.  The previous
- * stream is synchronised first. */
+ * all later launches; NULL selects the HIP null stream.  The previous stream
+ * is synchronised first.  neural_hip_reset_stream() returns to the library's
+ * own non-blocking stream. */
 int   neural_hip_set_stream(void *hip_stream);
+int   neural_hip_reset_stream(void);
 void *neural_hip_get_stream(void);
 int   neural_hip_synchronize(void);
 /* Release cached device blocks back to the driver. */

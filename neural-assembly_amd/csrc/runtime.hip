@@ -767,10 +767,21 @@ int neural_hip_set_stream(void *s)
 {
     NH_TRY(ensure_init());
     Runtime &r = R();
-    hipStream_t next = s ? static_cast<hipStream_t>(s) : r.own;
+    hipStream_t next = static_cast<hipStream_t>(s);  // NULL = the HIP null stream
     if (next != r.active) {
         NH_HIP(hipStreamSynchronize(r.active));
         r.active = next;
+    }
+    return set_error(NEURAL_OK);
+}
+
+int neural_hip_reset_stream(void)
+{
+    NH_TRY(ensure_init());
+    Runtime &r = R();
+    if (r.active != r.own) {
+        NH_HIP(hipStreamSynchronize(r.active));
+        r.active = r.own;
     }
     return set_error(NEURAL_OK);
 }

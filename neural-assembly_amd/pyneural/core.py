@@ -74,6 +74,29 @@ def _find_library() -> str:
     return LIB_NAME
 
 
+def _preload_torch_hip():
+    """PyTorch ships its own libamdhip64.so.  Loading it first (by path,
+    without importing torch) makes this library bind to the same HIP runtime
+    (same SONAME), so torch device pointers, streams and events are valid
+    handles here whichever package the process imports first.  Set
+    NEURAL_HIP_RUNTIME=system to use the ROCm installation's runtime instead."""
+    if os.environ.get("NEURAL_HIP_RUNTIME", "") == "system":
+        return None
+    try:
+        import importlib.util
+        spec = importlib.util.find_spec("torch")
+        if spec is None or not spec.origin:
+            return None
+        p = Path(spec.origin).parent / "lib" / "libamdhip64.so"
+        if p.exists():
+            ctypes.CDLL(str(p), mode=ctypes.RTLD_GLOBAL)
+            return str(p)
+    except OSError:
+        return None
+    return None
+
+
+_hip_runtime = _preload_torch_hip()
 _lib_path = _find_library()
 try:
     _lib = ctypes.CDLL(_lib_path)
@@ -233,6 +256,7 @@ _SIGS = {
     "tensor_transpose2d_array": (_i, [_vp, _i64, _i64, _vp]),
     # HIP runtime controls
     "neural_hip_set_stream": (_i, [_vp]),
+    "neural_hip_reset_stream": (_i, []),
     "neural_hip_get_stream": (_vp, []),
     "neural_hip_synchronize": (_i, []),
     "neural_hip_empty_cache": (_i, []),
@@ -290,10 +314,13 @@ def clear_error() -> None:
 
 
 def set_stream(stream_handle) -> None:
-    """Launch on an existing HIP stream (an int handle, e.g. torch's
-    ``torch.cuda.current_stream().cuda_stream``); ``None`` restores the
-    library's own stream."""
-    _check_error(_lib.neural_hip_set_stream(stream_handle), "set_stream")
+    """Launch on an existing HIP stream: an int handle such as torch's
+    ``torch.cuda.current_stream().cuda_stream`` (0 is the HIP null stream,
+    torch's default); ``None`` returns to the library's own stream."""
+    if stream_handle is None:
+        _check_error(_lib.neural_hip_reset_stream(), "reset_stream")
+    else:
+        _check_error(_lib.neural_hip_set_stream(ctypes.c_void_p(stream_handle)), "set_stream")
 
 
 def synchronize() -> None:

@@ -26,6 +26,19 @@ def _shape_arr(shape):
     return (ctypes.c_uint64 * max(len(shape), 1))(*shape)
 
 
+def _dtype_code(dtype) -> int:
+    """NeuralDtype code from a code, a numpy dtype or a numpy scalar type."""
+    if isinstance(dtype, int):
+        return dtype
+    if HAS_NUMPY:
+        dt = np.dtype(dtype)
+        if dt == np.float32:
+            return NeuralDtype.FLOAT32
+        if dt == np.float64:
+            return NeuralDtype.FLOAT64
+    raise ValueError(f"unsupported dtype {dtype!r} (float32 or float64)")
+
+
 class Tensor:
     """Multi-dimensional float32/float64 array resident on the GPU."""
 
@@ -50,17 +63,17 @@ class Tensor:
     @classmethod
     def create(cls, shape: Sequence[int], dtype: int = NeuralDtype.FLOAT32) -> "Tensor":
         shape = tuple(int(s) for s in shape)
-        return cls._wrap(_lib.neural_tensor_create(_shape_arr(shape), len(shape), dtype))
+        return cls._wrap(_lib.neural_tensor_create(_shape_arr(shape), len(shape), _dtype_code(dtype)))
 
     @classmethod
     def zeros(cls, shape: Sequence[int], dtype: int = NeuralDtype.FLOAT32) -> "Tensor":
         shape = tuple(int(s) for s in shape)
-        return cls._wrap(_lib.neural_tensor_zeros(_shape_arr(shape), len(shape), dtype))
+        return cls._wrap(_lib.neural_tensor_zeros(_shape_arr(shape), len(shape), _dtype_code(dtype)))
 
     @classmethod
     def ones(cls, shape: Sequence[int], dtype: int = NeuralDtype.FLOAT32) -> "Tensor":
         shape = tuple(int(s) for s in shape)
-        return cls._wrap(_lib.neural_tensor_ones(_shape_arr(shape), len(shape), dtype))
+        return cls._wrap(_lib.neural_tensor_ones(_shape_arr(shape), len(shape), _dtype_code(dtype)))
 
     @classmethod
     def from_numpy(cls, arr: "np.ndarray") -> "Tensor":

@@ -96,6 +96,22 @@ def special_f64(n, rng, frac=0.01):
     return x
 
 
+_KEEP = []
+
+
+def keep(t):
+    """Pointer of a wrapper object that stays alive until the test ends (a
+    temporary's pointer would be freed before the ctypes call runs)."""
+    _KEEP.append(t)
+    return t._ptr
+
+
+@pytest.fixture(autouse=True)
+def _release_kept():
+    yield
+    _KEEP.clear()
+
+
 @pytest.fixture
 def rng():
     return np.random.default_rng(1234)

@@ -9,7 +9,7 @@ import ctypes
 import numpy as np
 import pytest
 
-from conftest import GPU, rel_close, same_bits, special_f32, special_f64
+from conftest import GPU, keep, rel_close, same_bits, special_f32, special_f64
 
 pytestmark = GPU
 
@@ -70,8 +70,8 @@ def test_bias_add(pn, ora, rng, rows, cols, dt):
     x = rng.normal(0, 3, (rows, cols)).astype(dt)
     b = rng.normal(0, 3, cols).astype(dt)
     out = pn.Tensor.create(x.shape, x.dtype)
-    pn.core._check_error(pn.core._lib.neural_bias_add(out._ptr, pn.Tensor.from_numpy(x)._ptr,
-                                                     pn.Tensor.from_numpy(b)._ptr), "bias_add")
+    pn.core._check_error(pn.core._lib.neural_bias_add(out._ptr, keep(pn.Tensor.from_numpy(x)),
+                                                     keep(pn.Tensor.from_numpy(b))), "bias_add")
     same_bits(out.numpy(), ora.bias_add(x, b))
     # same through neural_add broadcasting
     same_bits((pn.Tensor.from_numpy(x) + pn.Tensor.from_numpy(b)).numpy(), x + b)
@@ -89,8 +89,8 @@ def test_broadcast_nd(pn, rng, sa, sb):
     b = rng.normal(0, 1, sb).astype(np.float32)
     want = a / b
     out = pn.Tensor.create(want.shape, pn.float32)
-    pn.core._check_error(pn.core._lib.neural_div(out._ptr, pn.Tensor.from_numpy(a)._ptr,
-                                                pn.Tensor.from_numpy(b)._ptr), "div")
+    pn.core._check_error(pn.core._lib.neural_div(out._ptr, keep(pn.Tensor.from_numpy(a)),
+                                                keep(pn.Tensor.from_numpy(b))), "div")
     same_bits(out.numpy(), want)
 
 
@@ -111,8 +111,8 @@ def test_strided_views_torch(pn, rng):
     at = a.t()  # non-contiguous [96, 64]
     out = torch.empty(96, 64, device="cuda")
     torch.cuda.synchronize()  # torch's stream vs the library's stream
-    rc = pn.core._lib.neural_mul(pn.Tensor.from_torch(out)._ptr, pn.Tensor.from_torch(at)._ptr,
-                                 pn.Tensor.from_torch(b)._ptr)
+    rc = pn.core._lib.neural_mul(keep(pn.Tensor.from_torch(out)), keep(pn.Tensor.from_torch(at)),
+                                 keep(pn.Tensor.from_torch(b)))
     assert rc == 0
     pn.synchronize()
     want = (at.cpu().numpy() * b.cpu().numpy()).astype(np.float32)
@@ -121,8 +121,8 @@ def test_strided_views_torch(pn, rng):
     big = torch.zeros(96, 128, device="cuda")
     view = big[:, ::2]
     torch.cuda.synchronize()
-    assert pn.core._lib.neural_add(pn.Tensor.from_torch(view)._ptr, pn.Tensor.from_torch(at)._ptr,
-                                   pn.Tensor.from_torch(b)._ptr) == 0
+    assert pn.core._lib.neural_add(keep(pn.Tensor.from_torch(view)), keep(pn.Tensor.from_torch(at)),
+                                   keep(pn.Tensor.from_torch(b))) == 0
     pn.synchronize()
     same_bits(big.cpu().numpy()[:, ::2], (at.cpu().numpy() + b.cpu().numpy()).astype(np.float32))
     assert np.all(big.cpu().numpy()[:, 1::2] == 0)
@@ -182,8 +182,8 @@ def test_unaligned_and_empty(pn, ora, rng):
     a, b = base[1:], base2[3:]  # 4098 elements each, not 16-byte aligned
     out = torch.empty(4098, device="cuda")
     torch.cuda.synchronize()
-    assert pn.core._lib.neural_sub(pn.Tensor.from_torch(out)._ptr, pn.Tensor.from_torch(a)._ptr,
-                                   pn.Tensor.from_torch(b)._ptr) == 0
+    assert pn.core._lib.neural_sub(keep(pn.Tensor.from_torch(out)), keep(pn.Tensor.from_torch(a)),
+                                   keep(pn.Tensor.from_torch(b))) == 0
     pn.synchronize()
     same_bits(out.cpu().numpy(), ora.ew(ora.SUB, a.cpu().numpy(), b.cpu().numpy()))
     e = pn.Tensor.create([0])

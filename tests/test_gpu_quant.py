@@ -29,7 +29,7 @@ def _params_equal(got, want):
 def _laplace(n, seed=5):
     rng = np.random.default_rng(seed)
     x = rng.laplace(0, 1, n).astype(np.float32)
-    k = max(2, n // 1000)
+    k = min(n, max(2, n // 1000))
     idx = rng.choice(n, size=k, replace=False)
     x[idx] = np.where(np.arange(k) % 2 == 0, 50.0, -50.0).astype(np.float32)
     return x

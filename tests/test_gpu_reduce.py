@@ -13,7 +13,7 @@ import ctypes
 import numpy as np
 import pytest
 
-from conftest import GPU, same_bits
+from conftest import GPU, keep, same_bits
 
 pytestmark = GPU
 
@@ -124,7 +124,7 @@ def test_colsum_axis0(pn, ora, rows, cols):
     rng = np.random.default_rng(cols)
     x = rng.normal(0, 1, (rows, cols)).astype(np.float32)
     out = pn.Tensor.create([cols])
-    pn.core._check_error(pn.core._lib.neural_reduce_sum(pn.Tensor.from_numpy(x)._ptr, 0, out._ptr), "colsum")
+    pn.core._check_error(pn.core._lib.neural_reduce_sum(keep(pn.Tensor.from_numpy(x)), 0, out._ptr), "colsum")
     e = ora.rowsum_exact(np.ascontiguousarray(x.T))
     bound = 1e-5 * np.sum(np.abs(x.astype(np.float64)), axis=0) + np.abs(e) * 6e-8
     assert np.all(np.abs(out.numpy() - e) <= bound)
@@ -155,5 +155,5 @@ def test_strided_reduction(pn, ora, rng):
     x = at.cpu().numpy()
     assert abs(s - ora.sum_exact(np.ascontiguousarray(x))) <= 1e-12 * np.sum(np.abs(x))
     idx = np.empty(257, dtype=np.int64)
-    pn.core._check_error(pn.core._lib.neural_reduce_argmax(pn.Tensor.from_torch(at)._ptr, 1, idx.ctypes.data), "am")
+    pn.core._check_error(pn.core._lib.neural_reduce_argmax(keep(pn.Tensor.from_torch(at)), 1, idx.ctypes.data), "am")
     same_bits(idx, ora.rowargmax(np.ascontiguousarray(x)))

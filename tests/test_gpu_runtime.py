@@ -9,7 +9,7 @@ import ctypes
 import numpy as np
 import pytest
 
-from conftest import GPU, same_bits
+from conftest import GPU, keep, same_bits
 
 pytestmark = GPU
 
@@ -36,7 +36,7 @@ def test_from_buffer_host_is_authoritative(pn):
     t = pn.Tensor.from_numpy_zero_copy(arr)
     out = pn.Tensor.create([1000], pn.float64)
     pn.core._check_error(pn.core._lib.neural_relu(out._ptr, t._ptr), "relu")
-    same_bits(out.numpy(), np.maximum(arr, 0.0) * (arr > 0))
+    same_bits(out.numpy(), np.where(arr > 0, arr, 0.0))
     arr[:] = 2.0  # later host writes are picked up by the next call
     pn.core._check_error(pn.core._lib.neural_add(t._ptr, t._ptr, t._ptr), "add")  # in place, written back
     assert np.all(arr == 4.0)
@@ -102,8 +102,8 @@ def test_torch_stream_interop(pn):
         a = torch.randn(1 << 20, device="cuda")
         b = torch.randn(1 << 20, device="cuda")
         out = torch.empty_like(a)
-        assert pn.core._lib.neural_add(pn.Tensor.from_torch(out)._ptr, pn.Tensor.from_torch(a)._ptr,
-                                       pn.Tensor.from_torch(b)._ptr) == 0
+        assert pn.core._lib.neural_add(keep(pn.Tensor.from_torch(out)), keep(pn.Tensor.from_torch(a)),
+                                       keep(pn.Tensor.from_torch(b))) == 0
         same_bits(out.cpu().numpy(), a.cpu().numpy() + b.cpu().numpy())  # stream-ordered, no explicit sync
     finally:
         pn.set_stream(None)
