@@ -45,6 +45,8 @@ def parse():
     ap.add_argument("--suite", action="store_true", help="also time every kernel family (stderr table)")
     ap.add_argument("--suite-json", default=None, help="write the per-kernel table to this file")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--calib", action="store_true",
+                    help="also run a plain 256 MiB device copy (the PMC byte-counter calibration kernel)")
     return ap.parse_args()
 
 
@@ -172,6 +174,15 @@ def main():
     }
     if cpu:
         line["config"]["speedup_vs_cpu"] = round(value / cpu["value"], 1)
+
+    if args.calib:
+        # Known-size copy: FETCH_SIZE / WRITE_SIZE of this dispatch calibrate the
+        # byte counters (256 MiB read + 256 MiB written).
+        src = torch.empty(64 << 20, device=dev).uniform_()
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
 
     if args.suite:
         rows = suite(torch, pn, stream)
