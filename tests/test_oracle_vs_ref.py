@@ -1,0 +1,246 @@
+"""Pin the oracle to the reference's own C, compiled unchanged from the
+reference tree into oracle/_ref/libneural_ref.so (oracle/Makefile).
+
+Bit-for-bit on random and special inputs: activations_c.c (all ten act_*,
+f32 and f64 tensors), quantize.c (calibrate_minmax, quantize_tensor,
+dequantize_tensor, quantization_error/_snr, including NaN / Inf / huge
+values), optimizers_c.c (SGD / Adam / AdamW steps, f32 and f64, and the
+OPTS blob), tensor_ops.c (concat / split / pad / transpose and their -1
+argument checks) and the log-softmax of metrics_losses.c:47-64 (through
+label_smoothing_ce_forward with smoothing 0, which returns exactly
+-log_softmax[target]).
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import same_bits
+
+ACT_ALPHA = {"leaky_relu": 0.01, "elu": 1.0}
+ACTS = ["tanh", "gelu", "leaky_relu", "elu", "selu", "swish", "mish", "hardswish", "softplus", "hardtanh"]
+
+
+class TensorC(ctypes.Structure):
+    """The 40-byte prefix of the reference descriptor (activations_c.c:36-43)."""
+    _fields_ = [("data", ctypes.c_void_p), ("ndim", ctypes.c_int64), ("shape", ctypes.POINTER(ctypes.c_int64)),
+                ("stride", ctypes.c_void_p), ("dtype", ctypes.c_int32), ("flags", ctypes.c_int32)]
+
+
+def tensor_c(arr, keep):
+    shape = (ctypes.c_int64 * arr.ndim)(*arr.shape)
+    keep.append(shape)
+    return TensorC(arr.ctypes.data, arr.ndim, shape, None, 0 if arr.dtype == np.float32 else 1, 0)
+
+
+@pytest.fixture(scope="module")
+def ref(ora):
+    r = ora.ref()
+    if r is None:
+        pytest.skip("oracle/_ref not built (reference sources absent)")
+    return r
+
+
+def act_inputs(dt):
+    rng = np.random.default_rng(44)
+    x = rng.normal(0, 4, 200000)
+    x[rng.choice(x.size, 2000, replace=False)] = 30.0
+    x[rng.choice(x.size, 2000, replace=False)] = -30.0
+    x[:14] = [0.0, -0.0, 3.0, -3.0, 1.0, -1.0, 1e-310, -700.0, 710.0, -1e-5, np.nan, np.inf, -np.inf, 20.0]
+    return x.astype(dt)
+
+
+@pytest.mark.parametrize("name", ACTS)
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_activations_bit_exact(ora, ref, name, dt):
+    x = act_inputs(dt)
+    out = np.empty_like(x)
+    keep = []
+    ti, to = tensor_c(x, keep), tensor_c(out, keep)
+    fn = getattr(ref, "act_" + name)
+    if name in ACT_ALPHA:
+        fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_double]
+        assert fn(ctypes.addressof(to), ctypes.addressof(ti), ACT_ALPHA[name]) == 0
+    else:
+        fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        assert fn(ctypes.addressof(to), ctypes.addressof(ti)) == 0
+    same_bits(ora.act(name, x, ACT_ALPHA.get(name, 0.0)), out)
+
+
+def _ref_params(ref, x, sym):
+    p = ora_qp()
+    ref.calibrate_minmax.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
+    assert ref.calibrate_minmax(x.ctypes.data, x.size, 1 if sym else 0, ctypes.byref(p)) == 0
+    return p
+
+
+def ora_qp():
+    import ora
+    return ora.QuantParams()
+
+
+def _params_bytes(p):
+    return bytes(memoryview(p))
+
+
+def quant_inputs():
+    rng = np.random.default_rng(5)
+    x = rng.laplace(0, 1, 100000)
+    x[rng.choice(x.size, 100, replace=False)] = 50.0
+    x[rng.choice(x.size, 100, replace=False)] = -50.0
+    return x
+
+
+@pytest.mark.parametrize("sym", [True, False])
+def test_quantize_bit_exact(ora, ref, sym):
+    x = quant_inputs()
+    rp = _ref_params(ref, x, sym)
+    op = ora.calibrate(x, sym)
+    assert _params_bytes(rp)[:12] == _params_bytes(op)[:12]  # scale + zero_point
+    assert (rp.min_val, rp.max_val, rp.symmetric) == (op.min_val, op.max_val, op.symmetric)
+    # f32 input widened to double gives the same params as the double API
+    x32 = x.astype(np.float32)
+    p32 = ora.calibrate(x32, sym)
+    rp32 = _ref_params(ref, x32.astype(np.float64), sym)
+    assert (p32.scale, p32.zero_point, p32.min_val, p32.max_val) == (rp32.scale, rp32.zero_point, rp32.min_val,
+                                                                     rp32.max_val)
+    q = np.empty(x.size, dtype=np.int8)
+    ref.quantize_tensor.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    assert ref.quantize_tensor(x.ctypes.data, q.ctypes.data, x.size, ctypes.byref(rp)) == 0
+    same_bits(ora.quantize(x, op), q)
+    d = np.empty(x.size)
+    ref.dequantize_tensor.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    assert ref.dequantize_tensor(q.ctypes.data, d.ctypes.data, x.size, ctypes.byref(rp)) == 0
+    same_bits(ora.dequantize(q, op), d)
+    ref.quantization_error.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    ref.quantization_snr.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    assert ora.quant_error(x, op) == ref.quantization_error(x.ctypes.data, x.size, ctypes.byref(rp))
+    assert ora.quant_snr(x, op) == ref.quantization_snr(x.ctypes.data, x.size, ctypes.byref(rp))
+
+
+def test_quantize_special_values_bit_exact(ora, ref):
+    """NaN, +-Inf and values beyond int32 after scaling: the reference's
+    (int32_t)round() is x86 cvttsd2si (INT32_MIN), then a wrapping add."""
+    x = np.array([0.3, np.nan, np.inf, -np.inf, 1e30, -1e30, 0.0, -0.0, 2.5, -2.5, 3.5, -3.5, 1e9, -1e9])
+    ref.quantize_tensor.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    for zp in (-128, -1, 0, 1, 127):
+        for scale in (0.5, 1e-3, 7.0):
+            p = ora_qp()
+            p.scale, p.zero_point = scale, zp
+            q = np.empty(x.size, dtype=np.int8)
+            assert ref.quantize_tensor(x.ctypes.data, q.ctypes.data, x.size, ctypes.byref(p)) == 0
+            same_bits(ora.quantize(x, p), q)
+    for data in ([np.nan, 1.0, -2.0], [5.0, 5.0, 5.0], [0.0, -0.0, 0.0], [-0.0, 0.0], [1e-40, -1e-40],
+                 [3.0, np.nan, -7.0, np.inf]):
+        a = np.array(data)
+        for sym in (True, False):
+            rp, op = _ref_params(ref, a, sym), ora.calibrate(a, sym)
+            for f in ("scale", "min_val", "max_val"):
+                rv, ov = getattr(rp, f), getattr(op, f)
+                assert (np.isnan(rv) and np.isnan(ov)) or np.float64(rv).tobytes() == np.float64(ov).tobytes()
+            assert rp.zero_point == op.zero_point and rp.symmetric == op.symmetric
+
+
+@pytest.mark.parametrize("kind", ["sgd", "adam", "adamw"])
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_optimizers_bit_exact(ora, ref, kind, dt):
+    rng = np.random.default_rng(6)
+    n = 10007
+    p = rng.normal(0, 0.02, n).astype(dt)
+    g = rng.normal(0, 1e-3, n).astype(dt)
+    g[[3, 50, 900]] = [np.nan, np.inf, -np.inf]
+    rp = p.copy()
+    keep = []
+    tp, tg = tensor_c(rp, keep), tensor_c(g, keep)
+    lr, b1, b2, eps, wd, mom = 1e-3, 0.9, 0.999, 1e-8, 0.01, 0.9
+    h = {"sgd": lambda: ref.opt_sgd_create(lr, mom), "adam": lambda: ref.opt_adam_create(lr, b1, b2, eps),
+         "adamw": lambda: ref.opt_adamw_create(lr, b1, b2, eps, wd)}[kind]()
+    pp = (ctypes.c_void_p * 1)(ctypes.addressof(tp))
+    gp = (ctypes.c_void_p * 1)(ctypes.addressof(tg))
+    op = p.copy()
+    m, v = np.zeros(n), np.zeros(n)
+    for t in range(1, 5):
+        assert ref.opt_step(h, pp, gp, 1) == 0
+        if kind == "sgd":
+            ora.sgd_step(op, g, m, lr, mom)
+        elif kind == "adam":
+            ora.adam_step(op, g, m, v, lr, b1, b2, eps, t)
+        else:
+            ora.adamw_step(op, g, m, v, lr, b1, b2, eps, wd, t)
+    same_bits(op, rp)
+    nb = ref.opt_state_bytes(h)
+    buf = (ctypes.c_uint8 * nb)()
+    assert ref.opt_state_export(h, buf, nb) == 0
+    blob = bytes(buf)
+    off = 88
+    same_bits(np.frombuffer(blob[off:off + 8 * n], dtype=np.float64), m)
+    if kind != "sgd":
+        same_bits(np.frombuffer(blob[off + 8 * n:off + 16 * n], dtype=np.float64), v)
+    ref.opt_free(h)
+
+
+def test_log_softmax_through_ce(ora, ref):
+    rng = np.random.default_rng(7)
+    K = 37
+    x = rng.normal(0, 3, (4, K))
+    x[1, 5] = 40.0
+    got = ora.softmax_rows(x, log=True)
+    fn = ref.label_smoothing_ce_forward
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_double, ctypes.c_void_p]
+    for i in range(4):
+        row = np.ascontiguousarray(x[i:i + 1])
+        for c in range(K):
+            tgt = np.array([c], dtype=np.int64)
+            loss = ctypes.c_double()
+            assert fn(row.ctypes.data, tgt.ctypes.data, 1, K, 0.0, ctypes.byref(loss)) == 0
+            assert np.float64(-loss.value).tobytes() == np.float64(got[i, c]).tobytes()
+
+
+def test_tensor_ops_bit_exact(ora, ref):
+    rng = np.random.default_rng(8)
+    d = ctypes.c_double
+    i64 = ctypes.c_int64
+    P = ctypes.c_void_p
+    ref.tensor_concat_2d.argtypes = [P, P, i64, i64, i64, i64, i64, P, P, P]
+    ref.tensor_split_2d.argtypes = [P, i64, i64, i64, i64, P, P, P, P, P, P]
+    ref.tensor_pad_2d.argtypes = [P, i64, i64, i64, i64, i64, i64, d, P, P, P]
+    ref.tensor_transpose2d_array.argtypes = [P, i64, i64, P]
+    a, b = rng.normal(size=12), rng.normal(size=6)
+    for (ra, ca, rb, cb, ax) in [(3, 4, 3, 2, 1), (3, 4, 2, 4, 0), (2, 6, 3, 2, 1), (0, 4, 3, 4, 0), (3, 4, 3, 4, 2)]:
+        bb = rng.normal(size=max(rb * cb, 1))
+        aa = rng.normal(size=max(ra * ca, 1))
+        out = np.zeros(64)
+        r, c = i64(), i64()
+        rc = ref.tensor_concat_2d(aa.ctypes.data, bb.ctypes.data, ra, ca, rb, cb, ax, out.ctypes.data,
+                                  ctypes.byref(r), ctypes.byref(c))
+        orc, oo, orr, occ = ora.concat_2d(aa, bb, ra, ca, rb, cb, ax)
+        assert rc == orc
+        if rc == 0:
+            assert (r.value, c.value) == (orr, occ)
+            same_bits(oo, out[: r.value * c.value])
+    x = rng.normal(size=35)
+    for ax, sp in [(0, 2), (1, 3), (0, 0), (1, 7), (2, 1)]:
+        oa, ob = np.zeros(35), np.zeros(35)
+        dims = [i64() for _ in range(4)]
+        rc = ref.tensor_split_2d(x.ctypes.data, 5, 7, ax, sp, oa.ctypes.data, ob.ctypes.data,
+                                 *[ctypes.byref(q) for q in dims])
+        orc, wa, wb, odims = ora.split_2d(x, 5, 7, ax, sp)
+        assert rc == orc
+        if rc == 0:
+            assert tuple(q.value for q in dims) == odims
+            same_bits(wa, oa[: wa.size])
+            same_bits(wb, ob[: wb.size])
+    for pads in [(1, 2, 3, 0), (0, 0, 0, 0), (-1, 0, 0, 0)]:
+        R, C = 5 + max(pads[0], 0) + pads[1], 7 + pads[2] + pads[3]
+        out = np.zeros(max(R * C, 1))
+        r, c = i64(), i64()
+        rc = ref.tensor_pad_2d(x.ctypes.data, 5, 7, *pads, -1.5, out.ctypes.data, ctypes.byref(r), ctypes.byref(c))
+        orc, oo, orr, occ = ora.pad_2d(x, 5, 7, *pads, -1.5)
+        assert rc == orc
+        if rc == 0:
+            same_bits(oo, out[: R * C])
+    out = np.zeros(35)
+    assert ref.tensor_transpose2d_array(x.ctypes.data, 5, 7, out.ctypes.data) == 0
+    rc, oo = ora.transpose_2d(x, 5, 7)
+    same_bits(oo, out)
