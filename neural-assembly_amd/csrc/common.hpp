@@ -148,15 +148,24 @@ NH_DEV T wave_max_ignore_nan(T v)
     return v;
 }
 
-// 128-bit vector load/store helpers.
-template <typename T> struct Vec16;
-template <> struct Vec16<float>  { using type = float4;  static constexpr int n = 4; };
-template <> struct Vec16<double> { using type = double2; static constexpr int n = 2; };
+// 128-bit vector types (clang ext vectors: element access by index, and
+// accepted by the non-temporal load/store builtins).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef double f64x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-NH_DEV float  vget(const float4 &v, int i)  { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
-NH_DEV double vget(const double2 &v, int i) { return i == 0 ? v.x : v.y; }
-NH_DEV void   vset(float4 &v, int i, float x)   { if (i == 0) v.x = x; else if (i == 1) v.y = x; else if (i == 2) v.z = x; else v.w = x; }
-NH_DEV void   vset(double2 &v, int i, double x) { if (i == 0) v.x = x; else v.y = x; }
+template <typename T> struct Vec16;
+template <> struct Vec16<float>  { using type = f32x4; static constexpr int n = 4; };
+template <> struct Vec16<double> { using type = f64x2; static constexpr int n = 2; };
+
+template <typename V> NH_DEV auto vget(const V &v, int i) { return v[i]; }
+template <typename V, typename S> NH_DEV void vset(V &v, int i, S x) { v[i] = x; }
+
+// Streaming (non-temporal) global accesses: data that is read or written
+// once per kernel does not displace reusable lines in L2 / MALL.  Measured on
+// MI355X: +10-15 % bandwidth for pure streams.
+template <typename T> NH_DEV T ld_nt(const T *p) { return __builtin_nontemporal_load(p); }
+template <typename T> NH_DEV void st_nt(T *p, T v) { __builtin_nontemporal_store(v, p); }
 
 // Error-return helper for host code.
 #define NH_TRY(expr)                          \

@@ -62,13 +62,15 @@ __global__ __launch_bounds__(kBlock) void k_fill(T *__restrict__ o, int64_t n, T
     const int64_t nv = n / VN;
     V vv;
 #pragma unroll
-    for (int k = 0; k < VN; k++) vset(vv, k, v);
+    for (int k = 0; k < VN; k++) vv[k] = v;
     V *ov = reinterpret_cast<V *>(o);
-    const int64_t base = int64_t(blockIdx.x) * (kBlock * kUnroll) + threadIdx.x;
+    const int64_t step = int64_t(gridDim.x) * (kBlock * kUnroll);
+    for (int64_t base = int64_t(blockIdx.x) * (kBlock * kUnroll) + threadIdx.x; base < nv; base += step) {
 #pragma unroll
-    for (int u = 0; u < kUnroll; u++) {
-        const int64_t i = base + int64_t(u) * kBlock;
-        if (i < nv) ov[i] = vv;
+        for (int u = 0; u < kUnroll; u++) {
+            const int64_t i = base + int64_t(u) * kBlock;
+            if (i < nv) st_nt(ov + i, vv);
+        }
     }
     if (blockIdx.x == 0) {
         const int64_t j = nv * VN + threadIdx.x;

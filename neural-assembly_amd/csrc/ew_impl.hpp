@@ -1,9 +1,9 @@
 // ew_impl.hpp -- streaming elementwise machinery for gfx950.
 //
-// Flat kernels move 128-bit vectors (float4 / double2): each 256-lane block
-// owns a contiguous tile of 256*U vectors, issues all U loads per operand
-// before any store, and block 0 finishes the n % VN tail.  Inputs that are
-// not 16-byte aligned take the scalar variant.  Strided / broadcast operands
+// Flat kernels move 128-bit vectors (4 x f32 / 2 x f64) with non-temporal
+// loads and stores, grid-striding over tiles of 256*U vectors; block 0
+// finishes the n % VN tail.  Inputs that are not 16-byte aligned take the
+// scalar variant.  Strided / broadcast operands
 // (up to 4 dims after merging) take the N-D kernel with per-element index
 // decomposition.
 #pragma once
@@ -18,6 +18,9 @@ constexpr int kUnroll = 4;
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // ---- flat binary ----------------------------------------------------------
+// Grid-stride over tiles of 256*U vectors (U = 4); per tile every lane issues
+// its U loads per operand before any arithmetic or store.  All accesses are
+// non-temporal.  Block 0 also finishes the n % VN tail.
 template <typename T, typename Op>
 __global__ __launch_bounds__(kBlock) void k_map2_flat(const T *__restrict__ a, const T *__restrict__ b,
                                                       T *__restrict__ o, int64_t n, Op op)
@@ -28,21 +31,23 @@ __global__ __launch_bounds__(kBlock) void k_map2_flat(const T *__restrict__ a, c
     const V *av = reinterpret_cast<const V *>(a);
     const V *bv = reinterpret_cast<const V *>(b);
     V *ov = reinterpret_cast<V *>(o);
-    const int64_t base = int64_t(blockIdx.x) * (kBlock * kUnroll) + threadIdx.x;
-    V ra[kUnroll], rb[kUnroll];
+    const int64_t step = int64_t(gridDim.x) * (kBlock * kUnroll);
+    for (int64_t base = int64_t(blockIdx.x) * (kBlock * kUnroll) + threadIdx.x; base < nv; base += step) {
+        V ra[kUnroll], rb[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; u++) {
-        const int64_t i = base + int64_t(u) * kBlock;
-        if (i < nv) { ra[u] = av[i]; rb[u] = bv[i]; }
-    }
+        for (int u = 0; u < kUnroll; u++) {
+            const int64_t i = base + int64_t(u) * kBlock;
+            if (i < nv) { ra[u] = ld_nt(av + i); rb[u] = ld_nt(bv + i); }
+        }
 #pragma unroll
-    for (int u = 0; u < kUnroll; u++) {
-        const int64_t i = base + int64_t(u) * kBlock;
-        if (i < nv) {
-            V r;
+        for (int u = 0; u < kUnroll; u++) {
+            const int64_t i = base + int64_t(u) * kBlock;
+            if (i < nv) {
+                V r;
 #pragma unroll
-            for (int k = 0; k < VN; k++) vset(r, k, op(vget(ra[u], k), vget(rb[u], k)));
-            ov[i] = r;
+                for (int k = 0; k < VN; k++) r[k] = op(ra[u][k], rb[u][k]);
+                st_nt(ov + i, r);
+            }
         }
     }
     if (blockIdx.x == 0) {
@@ -67,21 +72,23 @@ __global__ __launch_bounds__(kBlock) void k_map1_flat(const T *__restrict__ a, T
     const int64_t nv = n / VN;
     const V *av = reinterpret_cast<const V *>(a);
     V *ov = reinterpret_cast<V *>(o);
-    const int64_t base = int64_t(blockIdx.x) * (kBlock * kUnroll) + threadIdx.x;
-    V ra[kUnroll];
+    const int64_t step = int64_t(gridDim.x) * (kBlock * kUnroll);
+    for (int64_t base = int64_t(blockIdx.x) * (kBlock * kUnroll) + threadIdx.x; base < nv; base += step) {
+        V ra[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; u++) {
-        const int64_t i = base + int64_t(u) * kBlock;
-        if (i < nv) ra[u] = av[i];
-    }
+        for (int u = 0; u < kUnroll; u++) {
+            const int64_t i = base + int64_t(u) * kBlock;
+            if (i < nv) ra[u] = ld_nt(av + i);
+        }
 #pragma unroll
-    for (int u = 0; u < kUnroll; u++) {
-        const int64_t i = base + int64_t(u) * kBlock;
-        if (i < nv) {
-            V r;
+        for (int u = 0; u < kUnroll; u++) {
+            const int64_t i = base + int64_t(u) * kBlock;
+            if (i < nv) {
+                V r;
 #pragma unroll
-            for (int k = 0; k < VN; k++) vset(r, k, f(vget(ra[u], k)));
-            ov[i] = r;
+                for (int k = 0; k < VN; k++) r[k] = f(ra[u][k]);
+                st_nt(ov + i, r);
+            }
         }
     }
     if (blockIdx.x == 0) {
@@ -117,7 +124,7 @@ __global__ __launch_bounds__(kBlock) void k_rowbcast(const T *__restrict__ a, co
 #pragma unroll
     for (int u = 0; u < kRowsPerBlock; u++) {
         const int64_t r = r0 + u;
-        if (r < rows) ra[u] = reinterpret_cast<const V *>(a + r * cols)[cv];
+        if (r < rows) ra[u] = ld_nt(reinterpret_cast<const V *>(a + r * cols) + cv);
     }
 #pragma unroll
     for (int u = 0; u < kRowsPerBlock; u++) {
@@ -125,8 +132,8 @@ __global__ __launch_bounds__(kBlock) void k_rowbcast(const T *__restrict__ a, co
         if (r < rows) {
             V res;
 #pragma unroll
-            for (int k = 0; k < VN; k++) vset(res, k, op(vget(ra[u], k), vget(bb, k)));
-            reinterpret_cast<V *>(o + r * cols)[cv] = res;
+            for (int k = 0; k < VN; k++) res[k] = op(ra[u][k], bb[k]);
+            st_nt(reinterpret_cast<V *>(o + r * cols) + cv, res);
         }
     }
 }
@@ -174,10 +181,14 @@ __global__ __launch_bounds__(kBlock) void k_map1_nd(const T *a, T *o, int64_t n,
 
 // ---- host-side launch helpers ---------------------------------------------------
 
+// Enough tiles for the whole range, capped at 32 blocks per CU (the
+// grid-stride loop covers the rest; measured best for 64 M-element streams).
 inline unsigned flat_grid(int64_t n, int vn)
 {
     const int64_t nv = n / vn;
     int64_t g = ceil_div(nv, int64_t(kBlock) * kUnroll);
+    const int64_t cap = int64_t(num_cus()) * 32;
+    if (g > cap) g = cap;
     return unsigned(g < 1 ? 1 : g);
 }
 

@@ -124,7 +124,8 @@ NH_DEV double adam_f64(double pd, double gd, double &m, double &v, const AdamArg
 
 constexpr int kOBlock = 256;
 
-// Four f32 elements per thread-step: float4 param/grad, 2x double2 m and v.
+// Four f32 elements per thread-step: 4 x f32 param and grad, 2 x (2 x f64)
+// m and v; every access is a non-temporal 16-byte load or store.
 template <bool W>
 __global__ __launch_bounds__(kOBlock) void k_adam_f32(float *__restrict__ p, const float *__restrict__ g,
                                                       double *__restrict__ m, double *__restrict__ v, int64_t n,
@@ -132,27 +133,26 @@ __global__ __launch_bounds__(kOBlock) void k_adam_f32(float *__restrict__ p, con
 {
     const int64_t n4 = n / 4;
     const int64_t stride = int64_t(gridDim.x) * kOBlock;
+    f32x4 *pv4 = reinterpret_cast<f32x4 *>(p);
+    const f32x4 *gv4 = reinterpret_cast<const f32x4 *>(g);
+    f64x2 *mv2 = reinterpret_cast<f64x2 *>(m);
+    f64x2 *vv2 = reinterpret_cast<f64x2 *>(v);
     for (int64_t i = int64_t(blockIdx.x) * kOBlock + threadIdx.x; i < n4; i += stride) {
-        float4 pv = reinterpret_cast<float4 *>(p)[i];
-        const float4 gv = reinterpret_cast<const float4 *>(g)[i];
-        double2 m0 = reinterpret_cast<double2 *>(m)[2 * i], m1 = reinterpret_cast<double2 *>(m)[2 * i + 1];
-        double2 v0 = reinterpret_cast<double2 *>(v)[2 * i], v1 = reinterpret_cast<double2 *>(v)[2 * i + 1];
-        if (W) {
-            pv.x = adamw_f32(pv.x, gv.x, m0.x, v0.x, a);
-            pv.y = adamw_f32(pv.y, gv.y, m0.y, v0.y, a);
-            pv.z = adamw_f32(pv.z, gv.z, m1.x, v1.x, a);
-            pv.w = adamw_f32(pv.w, gv.w, m1.y, v1.y, a);
-        } else {
-            pv.x = adam_f32(pv.x, gv.x, m0.x, v0.x, a);
-            pv.y = adam_f32(pv.y, gv.y, m0.y, v0.y, a);
-            pv.z = adam_f32(pv.z, gv.z, m1.x, v1.x, a);
-            pv.w = adam_f32(pv.w, gv.w, m1.y, v1.y, a);
-        }
-        reinterpret_cast<float4 *>(p)[i] = pv;
-        reinterpret_cast<double2 *>(m)[2 * i] = m0;
-        reinterpret_cast<double2 *>(m)[2 * i + 1] = m1;
-        reinterpret_cast<double2 *>(v)[2 * i] = v0;
-        reinterpret_cast<double2 *>(v)[2 * i + 1] = v1;
+        f32x4 pv = ld_nt(pv4 + i);
+        const f32x4 gv = ld_nt(gv4 + i);
+        f64x2 m0 = ld_nt(mv2 + 2 * i), m1 = ld_nt(mv2 + 2 * i + 1);
+        f64x2 v0 = ld_nt(vv2 + 2 * i), v1 = ld_nt(vv2 + 2 * i + 1);
+        double mm[4] = {m0[0], m0[1], m1[0], m1[1]};
+        double vv[4] = {v0[0], v0[1], v1[0], v1[1]};
+#pragma unroll
+        for (int k = 0; k < 4; k++) pv[k] = W ? adamw_f32(pv[k], gv[k], mm[k], vv[k], a) : adam_f32(pv[k], gv[k], mm[k], vv[k], a);
+        m0[0] = mm[0]; m0[1] = mm[1]; m1[0] = mm[2]; m1[1] = mm[3];
+        v0[0] = vv[0]; v0[1] = vv[1]; v1[0] = vv[2]; v1[1] = vv[3];
+        st_nt(pv4 + i, pv);
+        st_nt(mv2 + 2 * i, m0);
+        st_nt(mv2 + 2 * i + 1, m1);
+        st_nt(vv2 + 2 * i, v0);
+        st_nt(vv2 + 2 * i + 1, v1);
     }
     if (blockIdx.x == 0) {
         const int64_t j = n4 * 4 + threadIdx.x;

@@ -4,11 +4,11 @@
 // 163-174 (dequantize_tensor), 222-269 (quantization_error / _snr).
 //   calibrate: mn = mx = d0; mn = d_i if d_i < mn; mx = d_i if d_i > mx, then
 //              the scalar symmetric/affine epilogue.  Here: one grid reduction
-//              of (min, max) with first-index ties (same values and zero signs
-//              as the sequential loop; NaNs ignored unless d0 is NaN), and the
-//              epilogue evaluated on the device by the last block with the same
-//              double expressions, so params never round-trip through the host
-//              in the device pipeline.
+//              of (min, max) that reproduces the loop's values and zero signs
+//              (NaNs ignored unless d0 is NaN), and the epilogue evaluated on
+//              the device by the last block with the same double expressions,
+//              so params never round-trip through the host in the device
+//              pipeline.
 //   quantize:  q = (int32)round(x * (1.0/scale)) + zp, clamp [-128, 127].  The
 //              int32 conversion reproduces x86 cvttsd2si (INT32_MIN for NaN and
 //              out-of-range) and the wrap-around add of the reference build.
@@ -61,37 +61,44 @@ NH_DEV void minmax_epilogue(double mn, double mx, int symmetric, QuantParams *ou
     *out = p;
 }
 
-// (min, max) with first-index ties, NaNs skipped; d0 NaN poisons both.
+// The sequential loop keeps, for each of min and max, the FIRST element
+// holding the extreme value; values that compare equal only differ in the
+// sign of zero.  Reduction state: NaN-ignoring min and max values and the
+// index of the first zero (each lane walks increasing indices, so "first" is
+// a one-time capture per lane and a min across lanes).  The epilogue re-reads
+// that zero for its sign, and d0 for the NaN case (d0 NaN makes both NaN).
+template <typename T>
 struct RedMinMax {
-    struct S { double mn, mx; int64_t imn, imx; int first_nan; };
+    struct S { double mn, mx; int64_t zfirst; };
     static constexpr bool kSuffixPass = false;
+    static constexpr int64_t kNone = INT64_MAX;
     int symmetric;
-    NH_DEV S init() const { return {0.0, 0.0, -1, -1, 0}; }
+    const T *x;
+    NH_DEV S init() const { return {__builtin_inf(), -__builtin_inf(), kNone}; }
     NH_DEV void acc(S &s, double v, int64_t i) const
     {
-        if (v != v) { if (i == 0) s.first_nan = 1; return; }
-        if (s.imn < 0 || v < s.mn || (v == s.mn && i < s.imn)) { s.mn = v; s.imn = i; }
-        if (s.imx < 0 || v > s.mx || (v == s.mx && i < s.imx)) { s.mx = v; s.imx = i; }
+        s.mn = __builtin_fmin(s.mn, v);
+        s.mx = __builtin_fmax(s.mx, v);
+        s.zfirst = (v == 0.0 && s.zfirst == kNone) ? i : s.zfirst;
     }
     NH_DEV S comb(S a, S b) const
     {
-        S r;
-        r.first_nan = a.first_nan | b.first_nan;
-        if (a.imn < 0 || (b.imn >= 0 && (b.mn < a.mn || (b.mn == a.mn && b.imn < a.imn)))) { r.mn = b.mn; r.imn = b.imn; }
-        else { r.mn = a.mn; r.imn = a.imn; }
-        if (a.imx < 0 || (b.imx >= 0 && (b.mx > a.mx || (b.mx == a.mx && b.imx < a.imx)))) { r.mx = b.mx; r.imx = b.imx; }
-        else { r.mx = a.mx; r.imx = a.imx; }
-        return r;
+        return {__builtin_fmin(a.mn, b.mn), __builtin_fmax(a.mx, b.mx), a.zfirst < b.zfirst ? a.zfirst : b.zfirst};
     }
     NH_DEV S shfl(S a, int off) const
     {
-        return {__shfl_xor(a.mn, off, 64), __shfl_xor(a.mx, off, 64), __shfl_xor(a.imn, off, 64),
-                __shfl_xor(a.imx, off, 64), __shfl_xor(a.first_nan, off, 64)};
+        return {__shfl_xor(a.mn, off, 64), __shfl_xor(a.mx, off, 64), __shfl_xor(a.zfirst, off, 64)};
     }
     NH_DEV void store(void *out, S s) const
     {
         double mn = s.mn, mx = s.mx;
-        if (s.first_nan || s.imn < 0) mn = mx = __longlong_as_double(0x7ff8000000000000ll);
+        if (s.zfirst != kNone) {
+            const double z = double(x[s.zfirst]);
+            if (mn == 0.0) mn = z;
+            if (mx == 0.0) mx = z;
+        }
+        const T first = x[0];
+        if (first != first || mn > mx) mn = mx = __longlong_as_double(0x7ff8000000000000ll);
         minmax_epilogue(mn, mx, symmetric, static_cast<QuantParams *>(out));
     }
 };
@@ -132,8 +139,8 @@ NH_DEV void load_q(const QArgs &a, double &inv, double &scale, int32_t &zp)
 
 constexpr int kQBlock = 256;
 
-// 16 elements per thread-step: four float4 (or eight double2) loads, one
-// 16-byte store.
+// 16 elements per thread-step: four 4 x f32 (or eight 2 x f64) loads and one
+// 16-byte store, all non-temporal.
 template <typename T>
 __global__ __launch_bounds__(kQBlock) void k_quantize(const T *__restrict__ x, int8_t *__restrict__ q, int64_t n,
                                                       QArgs qa)
@@ -150,13 +157,19 @@ __global__ __launch_bounds__(kQBlock) void k_quantize(const T *__restrict__ x, i
         const V *xv = reinterpret_cast<const V *>(x + i * 16);
         V v[NV];
 #pragma unroll
-        for (int k = 0; k < NV; k++) v[k] = xv[k];
-        union { int4 w; int8_t b[16]; } o;
+        for (int k = 0; k < NV; k++) v[k] = ld_nt(xv + k);
+        i32x4 w;
 #pragma unroll
-        for (int k = 0; k < NV; k++)
+        for (int word = 0; word < 4; word++) {
+            uint32_t packed = 0;
 #pragma unroll
-            for (int j = 0; j < VN; j++) o.b[k * VN + j] = quant_one(double(vget(v[k], j)), inv, zp);
-        reinterpret_cast<int4 *>(q)[i] = o.w;
+            for (int b = 0; b < 4; b++) {
+                const int e = word * 4 + b;
+                packed |= uint32_t(uint8_t(quant_one(double(v[e / VN][e % VN]), inv, zp))) << (8 * b);
+            }
+            w[word] = int(packed);
+        }
+        st_nt(reinterpret_cast<i32x4 *>(q) + i, w);
     }
     if (blockIdx.x == 0) {
         const int64_t j = n16 * 16 + threadIdx.x;
@@ -189,15 +202,18 @@ __global__ __launch_bounds__(kQBlock) void k_dequantize(const int8_t *__restrict
     const int64_t n16 = n / 16;
     const int64_t stride = int64_t(gridDim.x) * kQBlock;
     for (int64_t i = int64_t(blockIdx.x) * kQBlock + threadIdx.x; i < n16; i += stride) {
-        union { int4 w; int8_t b[16]; } in;
-        in.w = reinterpret_cast<const int4 *>(q)[i];
+        const i32x4 w = ld_nt(reinterpret_cast<const i32x4 *>(q) + i);
         V *yv = reinterpret_cast<V *>(y + i * 16);
 #pragma unroll
         for (int k = 0; k < NV; k++) {
             V o;
 #pragma unroll
-            for (int j = 0; j < VN; j++) vset(o, j, T((double(in.b[k * VN + j]) - dz) * scale));
-            yv[k] = o;
+            for (int j = 0; j < VN; j++) {
+                const int e = k * VN + j;
+                const int8_t b = int8_t(uint32_t(w[e / 4]) >> (8 * (e % 4)));
+                o[j] = T((double(b) - dz) * scale);
+            }
+            st_nt(yv + k, o);
         }
     }
     if (blockIdx.x == 0) {
@@ -252,8 +268,9 @@ static int calibrate(const T *data, int64_t n, int symmetric, QuantParams *out, 
     if (!data || n <= 0 || !out) return -1;
     Staged s;
     if (s.open(data, size_t(n) * sizeof(T), true) != NEURAL_OK) return -1;
-    RedMinMax red;
+    RedMinMax<T> red;
     red.symmetric = symmetric ? 1 : 0;
+    red.x = static_cast<const T *>(s.dev);
     void *res = out_on_device ? static_cast<void *>(out) : workspace().result;
     if (launch_reduce_full(static_cast<const T *>(s.dev), n, red, res) != NEURAL_OK) return -1;
     if (!out_on_device && hipMemcpyAsync(out, res, sizeof(QuantParams), hipMemcpyDeviceToHost, stream()) != hipSuccess)

@@ -38,78 +38,108 @@ struct RedRowSum : RedSum {
         static_cast<T *>(out)[r] = T(v);
     }
     NH_DEV void store(void *out, S st) const { store_row(out, 0, st); }
+    NH_DEV void store_row_x(void *out, int64_t r, S st, const T *, int64_t) const { store_row(out, r, st); }
 };
 
-// Running-max state: best non-NaN value (ties -> later index) and the last
-// NaN index seen.
+// Running-max chain m = (m > x) ? m : x as a reduction.  The chain's result
+// is the largest value after the last NaN (NaN if the last element is NaN);
+// equal values only differ in the sign of zero, where the chain keeps the
+// later element.  State: largest non-NaN value, last NaN index, last zero
+// index.  Every lane walks its elements in increasing index order, so "last"
+// is a plain overwrite per lane and a max across lanes.  The element behind a
+// zero result is re-read to get its sign.
 struct RedMax {
-    struct S { double v; int64_t i; int64_t nan_i; };
+    struct S { double v; int64_t nan_i; int64_t zero_i; };
     static constexpr bool kSuffixPass = true;
-    NH_DEV S init() const { return {0.0, -1, -1}; }
+    const void *x;   // the reduced array (element 0), to read back a zero's sign
+    int f64;         // element type of x
+    NH_DEV S init() const { return {-__builtin_inf(), -1, -1}; }
     NH_DEV void acc(S &st, double v, int64_t i) const
     {
-        if (v != v) { if (i > st.nan_i) st.nan_i = i; return; }
-        if (st.i < 0 || v > st.v || (v == st.v && i > st.i)) { st.v = v; st.i = i; }
+        st.nan_i = (v != v) ? i : st.nan_i;
+        st.zero_i = (v == 0.0) ? i : st.zero_i;
+        st.v = __builtin_fmax(st.v, v);
     }
     NH_DEV S comb(S a, S b) const
     {
-        S r;
-        r.nan_i = a.nan_i > b.nan_i ? a.nan_i : b.nan_i;
-        if (a.i < 0) { r.v = b.v; r.i = b.i; }
-        else if (b.i < 0) { r.v = a.v; r.i = a.i; }
-        else if (a.v > b.v || (a.v == b.v && a.i > b.i)) { r.v = a.v; r.i = a.i; }
-        else { r.v = b.v; r.i = b.i; }
-        return r;
+        return {__builtin_fmax(a.v, b.v), a.nan_i > b.nan_i ? a.nan_i : b.nan_i,
+                a.zero_i > b.zero_i ? a.zero_i : b.zero_i};
     }
     NH_DEV S shfl(S a, int off) const
     {
-        return {__shfl_xor(a.v, off, 64), __shfl_xor(a.i, off, 64), __shfl_xor(a.nan_i, off, 64)};
+        return {__shfl_xor(a.v, off, 64), __shfl_xor(a.nan_i, off, 64), __shfl_xor(a.zero_i, off, 64)};
     }
     NH_DEV int64_t suffix_start(S st) const { return st.nan_i; }
-    // Second pass over (L, cols): its best element is the chain's result;
-    // an empty suffix (last element NaN) yields NaN.
-    NH_DEV S suffix_result(S first, S second, int64_t) const
+    // Second pass over (L, cols) of the same row (no NaN there by
+    // definition).  A row that ends with NaN has an empty suffix: its chain
+    // value is NaN, marked by nan_i = kEndsWithNaN.
+    static constexpr int64_t kEndsWithNaN = -3;
+    NH_DEV S suffix_result(S first, S second, int64_t cols) const
     {
+        if (first.nan_i == cols - 1) return {0.0, kEndsWithNaN, -1};
         S r = second;
-        r.nan_i = first.nan_i;
-        if (second.i < 0) { r.v = __longlong_as_double(0x7ff8000000000000ll); r.i = first.nan_i; }
+        r.nan_i = -1;
         return r;
+    }
+    // Value of the chain given a first-pass state over x[0..n) (row base xr).
+    NH_DEV double finish(S st, const void *xr) const
+    {
+        double v = st.v;
+        if (v == 0.0 && st.zero_i >= 0)
+            v = f64 ? static_cast<const double *>(xr)[st.zero_i] : double(static_cast<const float *>(xr)[st.zero_i]);
+        return v;
     }
     NH_DEV void store(void *out, S st) const { *static_cast<S *>(out) = st; }
 };
 
 template <typename T>
 struct RedRowMax : RedMax {
-    NH_DEV void store_row(void *out, int64_t r, S st) const { static_cast<T *>(out)[r] = T(st.v); }
+    NH_DEV void store_row_x(void *out, int64_t r, S st, const T *xr, int64_t cols) const
+    {
+        const double v = st.nan_i == kEndsWithNaN ? __longlong_as_double(0x7ff8000000000000ll) : finish(st, xr);
+        static_cast<T *>(out)[r] = T(v);
+    }
 };
 
-// Argmax: largest non-NaN value, ties -> smaller index; x0 NaN forces 0.
+// Argmax: idx = 0, m = x0, update iff x_j > m.  Reduction state: largest
+// non-NaN value and its first index (-1 while none beats -inf); x0 NaN, or no
+// element above -inf, gives 0 (read from x in the epilogue).
 struct RedArgmax {
-    struct S { double v; int64_t i; int first_nan; };
+    struct S { double v; int64_t i; };
     static constexpr bool kSuffixPass = false;
-    NH_DEV S init() const { return {0.0, -1, 0}; }
+    NH_DEV S init() const { return {-__builtin_inf(), -1}; }
     NH_DEV void acc(S &st, double v, int64_t i) const
     {
-        if (v != v) { if (i == 0) st.first_nan = 1; return; }
-        if (st.i < 0 || v > st.v || (v == st.v && i < st.i)) { st.v = v; st.i = i; }
+        const bool up = v > st.v;
+        st.v = up ? v : st.v;
+        st.i = up ? i : st.i;
     }
     NH_DEV S comb(S a, S b) const
     {
-        S r;
-        r.first_nan = a.first_nan | b.first_nan;
-        if (a.i < 0) { r.v = b.v; r.i = b.i; }
-        else if (b.i < 0) { r.v = a.v; r.i = a.i; }
-        else if (a.v > b.v || (a.v == b.v && a.i < b.i)) { r.v = a.v; r.i = a.i; }
-        else { r.v = b.v; r.i = b.i; }
-        return r;
+        if (b.v > a.v || (b.v == a.v && b.i >= 0 && (a.i < 0 || b.i < a.i))) return b;
+        return a;
     }
-    NH_DEV S shfl(S a, int off) const
+    NH_DEV S shfl(S a, int off) const { return {__shfl_xor(a.v, off, 64), __shfl_xor(a.i, off, 64)}; }
+    template <typename T>
+    NH_DEV static int64_t result(S st, const T *x0)
     {
-        return {__shfl_xor(a.v, off, 64), __shfl_xor(a.i, off, 64), __shfl_xor(a.first_nan, off, 64)};
+        const T first = x0[0];
+        return (first != first || st.i < 0) ? 0 : st.i;
     }
-    NH_DEV static int64_t result(S st) { return (st.first_nan || st.i < 0) ? 0 : st.i; }
-    NH_DEV void store(void *out, S st) const { *static_cast<int64_t *>(out) = result(st); }
-    NH_DEV void store_row(void *out, int64_t r, S st) const { static_cast<int64_t *>(out)[r] = result(st); }
+};
+
+template <typename T>
+struct RedRowArgmax : RedArgmax {
+    NH_DEV void store_row_x(void *out, int64_t r, S st, const T *xr, int64_t) const
+    {
+        static_cast<int64_t *>(out)[r] = result(st, xr);
+    }
+};
+
+template <typename T>
+struct RedFullArgmax : RedArgmax {
+    const T *x;
+    NH_DEV void store(void *out, S st) const { *static_cast<int64_t *>(out) = result(st, x); }
 };
 
 // ---- column sums (reduce_sum axis=0) -------------------------------------------------
@@ -222,36 +252,53 @@ static int full_reduce(const NeuralTensor *t, const Red &red, Out *host_out)
     return NEURAL_OK;
 }
 
-// Running-max over a whole tensor: first pass finds the last NaN and the
-// best value; if a NaN was seen, a second pass runs on the suffix after it.
+// Running-max over a whole tensor: the first pass finds the largest value,
+// the last NaN and the last zero; if a NaN was seen a second pass runs on the
+// suffix after it (the chain restarts there).
 static int full_max(const NeuralTensor *t, double *result)
 {
     const int64_t n = numel(t);
     Contig c;
     NH_TRY(c.open(t));
-    RedMax red;
-    RedMax::S st;
+    const bool f64 = t->dtype == NEURAL_DTYPE_FLOAT64;
+    const size_t es = elem_size(t->dtype);
     void *res = workspace().result;
-    if (t->dtype == NEURAL_DTYPE_FLOAT32) NH_TRY(launch_reduce_full(static_cast<const float *>(c.p), n, red, res));
-    else NH_TRY(launch_reduce_full(static_cast<const double *>(c.p), n, red, res));
-    NH_HIP(hipMemcpyAsync(&st, res, sizeof(st), hipMemcpyDeviceToHost, stream()));
-    NH_TRY(sync());
-    if (st.nan_i >= 0) {
-        const int64_t L = st.nan_i;
-        if (L == n - 1) {
+    int64_t base = 0;
+    for (int pass = 0; pass < 2; pass++) {
+        const void *sp = static_cast<const char *>(c.p) + size_t(base) * es;
+        RedMax red;
+        red.x = sp;
+        red.f64 = f64 ? 1 : 0;
+        const int64_t m = n - base;
+        if (f64) NH_TRY(launch_reduce_full(static_cast<const double *>(sp), m, red, res));
+        else NH_TRY(launch_reduce_full(static_cast<const float *>(sp), m, red, res));
+        RedMax::S st;
+        NH_HIP(hipMemcpyAsync(&st, res, sizeof(st), hipMemcpyDeviceToHost, stream()));
+        NH_TRY(sync());
+        if (st.nan_i < 0) {
+            double v = st.v;
+            if (v == 0.0 && st.zero_i >= 0) {
+                // the sign of the zero the chain keeps (the last one)
+                const char *p = static_cast<const char *>(sp) + size_t(st.zero_i) * es;
+                if (f64) NH_HIP(hipMemcpyAsync(&v, p, 8, hipMemcpyDeviceToHost, stream()));
+                else {
+                    float f;
+                    NH_HIP(hipMemcpyAsync(&f, p, 4, hipMemcpyDeviceToHost, stream()));
+                    NH_TRY(sync());
+                    v = f;
+                }
+                NH_TRY(sync());
+            }
+            *result = v;
+            return NEURAL_OK;
+        }
+        base += st.nan_i + 1;
+        if (base >= n) {
             *result = __builtin_nan("");
             return NEURAL_OK;
         }
-        const int64_t m = n - L - 1;
-        const size_t es = elem_size(t->dtype);
-        const void *sp = static_cast<const char *>(c.p) + size_t(L + 1) * es;
-        if (t->dtype == NEURAL_DTYPE_FLOAT32) NH_TRY(launch_reduce_full(static_cast<const float *>(sp), m, red, res));
-        else NH_TRY(launch_reduce_full(static_cast<const double *>(sp), m, red, res));
-        NH_HIP(hipMemcpyAsync(&st, res, sizeof(st), hipMemcpyDeviceToHost, stream()));
-        NH_TRY(sync());
     }
-    *result = st.v;
-    return NEURAL_OK;
+    return set_error(NEURAL_ERR_INTERNAL);  // unreachable: the suffix holds no NaN
 }
 
 // Resolve (rows, cols) for a reduction over `axis` of `in`:
@@ -363,7 +410,17 @@ int neural_argmax(const NeuralTensor *t, int64_t *result)
     if (!t || !result) return set_error(NEURAL_ERR_NULL_POINTER);
     NH_TRY(check_tensor(t));
     if (numel(t) == 0) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
-    NH_TRY(full_reduce(t, RedArgmax{}, result));
+    const void *p = nullptr;
+    NH_TRY(dev_read(t, &p));
+    if (t->dtype == NEURAL_DTYPE_FLOAT32) {
+        RedFullArgmax<float> red;
+        red.x = static_cast<const float *>(p);
+        NH_TRY(full_reduce(t, red, result));
+    } else {
+        RedFullArgmax<double> red;
+        red.x = static_cast<const double *>(p);
+        NH_TRY(full_reduce(t, red, result));
+    }
     return set_error(NEURAL_OK);
 }
 
@@ -395,9 +452,9 @@ int neural_reduce_max(const NeuralTensor *in, int64_t axis, NeuralTensor *out)
     void *dst = nullptr;
     NH_TRY(dev_write(out, &dst, true));
     if (in->dtype == NEURAL_DTYPE_FLOAT32)
-        NH_TRY(launch_reduce_rows(static_cast<const float *>(c.p), rows, cols, RedRowMax<float>{}, dst));
+        NH_TRY(launch_reduce_rows(static_cast<const float *>(c.p), rows, cols, RedRowMax<float>{{nullptr, 0}}, dst));
     else
-        NH_TRY(launch_reduce_rows(static_cast<const double *>(c.p), rows, cols, RedRowMax<double>{}, dst));
+        NH_TRY(launch_reduce_rows(static_cast<const double *>(c.p), rows, cols, RedRowMax<double>{{nullptr, 1}}, dst));
     NH_TRY(dev_written(out));
     return set_error(NEURAL_OK);
 }
@@ -417,9 +474,9 @@ int neural_reduce_argmax(const NeuralTensor *in, int64_t axis, int64_t *out_indi
     Staged so;
     NH_TRY(so.open(out_indices, size_t(rows) * sizeof(int64_t), false));
     if (in->dtype == NEURAL_DTYPE_FLOAT32)
-        NH_TRY(launch_reduce_rows(static_cast<const float *>(c.p), rows, cols, RedArgmax{}, so.dev));
+        NH_TRY(launch_reduce_rows(static_cast<const float *>(c.p), rows, cols, RedRowArgmax<float>{}, so.dev));
     else
-        NH_TRY(launch_reduce_rows(static_cast<const double *>(c.p), rows, cols, RedArgmax{}, so.dev));
+        NH_TRY(launch_reduce_rows(static_cast<const double *>(c.p), rows, cols, RedRowArgmax<double>{}, so.dev));
     NH_TRY(so.finish(true));
     return set_error(NEURAL_OK);
 }

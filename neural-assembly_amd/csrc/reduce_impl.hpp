@@ -63,14 +63,14 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_full(const T *__restrict__ x
 #pragma unroll
             for (int u = 0; u < kRUnroll; u++) {
                 const int64_t i = t0 + int64_t(u) * kRBlock + threadIdx.x;
-                if (i < nv) r[u] = xv[i];
+                if (i < nv) r[u] = ld_nt(xv + i);
             }
 #pragma unroll
             for (int u = 0; u < kRUnroll; u++) {
                 const int64_t i = t0 + int64_t(u) * kRBlock + threadIdx.x;
                 if (i < nv) {
 #pragma unroll
-                    for (int k = 0; k < VN; k++) red.acc(st, double(vget(r[u], k)), i * VN + k);
+                    for (int k = 0; k < VN; k++) red.acc(st, double(r[u][k]), i * VN + k);
                 }
             }
         }
@@ -133,9 +133,9 @@ int launch_reduce_full(const T *x, int64_t n, const Red &red, void *dev_result)
 
 // ---- row reductions -----------------------------------------------------------------
 // TPR lanes per row (64: one wave, 256: one block); RPB = 256 / TPR rows per block.
-// Red additionally supplies store_row(out, row, S) and, for the running-max
-// semantics, a second pass over the suffix after the row's last NaN
-// (Red::kSuffixPass).
+// Red additionally supplies store_row_x(out, row, S, row_base, cols) and, for
+// the running-max semantics, a second pass over the suffix after the row's
+// last NaN (Red::kSuffixPass).
 
 template <class Red>
 NH_DEV typename Red::S row_group_reduce(const Red &red, typename Red::S s, int tpr)
@@ -155,9 +155,9 @@ NH_DEV typename Red::S row_scan(const Red &red, const T *xr, int64_t cols, int64
         const V *xv = reinterpret_cast<const V *>(xr);
         const int64_t nv = cols / VN;
         for (int64_t c = lane; c < nv; c += TPR) {
-            const V v = xv[c];
+            const V v = ld_nt(xv + c);
 #pragma unroll
-            for (int k = 0; k < VN; k++) red.acc(st, double(vget(v, k)), c * VN + k);
+            for (int k = 0; k < VN; k++) red.acc(st, double(v[k]), c * VN + k);
         }
         for (int64_t j = nv * VN + lane; j < cols; j += TPR) red.acc(st, double(xr[j]), j);
     } else {
@@ -186,7 +186,7 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_rows(const T *__restrict__ x
             st = red.suffix_result(st, s2, cols);
         }
     }
-    if (valid && (threadIdx.x % TPR) == 0) red.store_row(out, r, st);
+    if (valid && (threadIdx.x % TPR) == 0) red.store_row_x(out, r, st, xr, cols);
 }
 
 template <typename T, class Red>

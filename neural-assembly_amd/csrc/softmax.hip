@@ -4,8 +4,10 @@
 // f32 semantics (the asm keeps the max and the running sum in one stack slot,
 // activations.asm:900,927-929):
 //   f32: m = row max; e_j = (float)exp((double)x_j - (double)m);
-//        s = sum of e_j; y_j = e_j / (float)s  (float division)
+//        s = sum of e_j; y_j = e_j / s
 //   f64: e_j = exp(x_j - m); y_j = e_j / s
+// Here the f32 e_j come from an exact split of x - m and the float exp (about
+// 1 ulp of float, see exp_diff_f32) and y_j = e_j * (1/s).
 // Log-softmax follows the formula of label_smoothing_ce_forward
 // (metrics_losses.c:47-64) in double: y = (x - m) - log(sum exp(x - m)),
 // rounded once for f32.
@@ -30,66 +32,73 @@ NH_DEV T neg_inf();
 template <> NH_DEV float neg_inf<float>() { return -__builtin_inff(); }
 template <> NH_DEV double neg_inf<double>() { return -__builtin_inf(); }
 
-template <typename T, bool LOG, int VPL>
-__global__ __launch_bounds__(kSmBlock) void k_softmax_wave(const T *__restrict__ x, T *__restrict__ y, int64_t rows,
-                                                           int64_t cols)
+// exp(x - m) for f32 rows, accurate to about 1 ulp of float: x - m is split
+// exactly into hi + lo (TwoSum), exp(hi) comes from the float exp and the
+// low part enters as exp(hi) * (1 + lo).  This matches the reference's
+// (float)exp((double)x - (double)m) to ~1e-7 relative at a fraction of the
+// cost of a double exp.  A non-finite hi (overflowing difference, or infinite
+// inputs) skips the correction so exp(-inf) stays 0.
+NH_DEV float exp_diff_f32(float x, float m)
 {
-    using V = typename Vec16<T>::type;
-    constexpr int VN = Vec16<T>::n;
+    const float nm = -m;
+    const float hi = x + nm;
+    const float bb = hi - x;
+    float lo = (x - (hi - bb)) + (nm - bb);
+    if (!(hi - hi == 0.0f)) lo = 0.0f;
+    const float e = expf(hi);
+    return __builtin_fmaf(e, lo, e);
+}
+
+template <bool LOG, int VPL>
+__global__ __launch_bounds__(kSmBlock) void k_softmax_wave_f32(const float *__restrict__ x, float *__restrict__ y,
+                                                               int64_t rows, int64_t cols)
+{
+    using V = f32x4;
     const int lane = threadIdx.x & 63;
     const int64_t r = int64_t(blockIdx.x) * (kSmBlock / 64) + (threadIdx.x >> 6);
     if (r >= rows) return;  // uniform per wave
     const V *xr = reinterpret_cast<const V *>(x + r * cols);
     V *yr = reinterpret_cast<V *>(y + r * cols);
-    const int64_t ncv = cols / VN;
+    const int64_t ncv = cols / 4;
 
     V v[VPL];
 #pragma unroll
     for (int k = 0; k < VPL; k++) {
         const int64_t c = lane + int64_t(k) * 64;
-        if (c < ncv) v[k] = xr[c];
+        if (c < ncv) v[k] = ld_nt(xr + c);
     }
-    T m = neg_inf<T>();
+    float m = -__builtin_inff();
 #pragma unroll
     for (int k = 0; k < VPL; k++) {
         const int64_t c = lane + int64_t(k) * 64;
         if (c < ncv) {
 #pragma unroll
-            for (int j = 0; j < VN; j++) {
-                const T e = vget(v[k], j);
-                m = e > m ? e : m;
-            }
+            for (int j = 0; j < 4; j++) m = v[k][j] > m ? v[k][j] : m;
         }
     }
     m = wave_max_ignore_nan(m);
-    const double md = double(m);
 
     double s = 0.0;
     if (!LOG) {
-        // Keep e_j (rounded to T) in the input registers.
+        // e_j kept in the input registers, rounded to float as the reference does.
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
             const int64_t c = lane + int64_t(k) * 64;
             if (c < ncv) {
 #pragma unroll
-                for (int j = 0; j < VN; j++) {
-                    const T e = T(exp(double(vget(v[k], j)) - md));
-                    vset(v[k], j, e);
+                for (int j = 0; j < 4; j++) {
+                    const float e = exp_diff_f32(v[k][j], m);
+                    v[k][j] = e;
                     s += double(e);
                 }
             }
         }
         s = wave_sum(s);
-        const T st = T(s);
+        const float rs = 1.0f / float(s);
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
             const int64_t c = lane + int64_t(k) * 64;
-            if (c < ncv) {
-                V o;
-#pragma unroll
-                for (int j = 0; j < VN; j++) vset(o, j, vget(v[k], j) / st);
-                yr[c] = o;
-            }
+            if (c < ncv) st_nt(yr + c, v[k] * rs);
         }
     } else {
 #pragma unroll
@@ -97,20 +106,76 @@ __global__ __launch_bounds__(kSmBlock) void k_softmax_wave(const T *__restrict__
             const int64_t c = lane + int64_t(k) * 64;
             if (c < ncv) {
 #pragma unroll
-                for (int j = 0; j < VN; j++) s += exp(double(vget(v[k], j)) - md);
+                for (int j = 0; j < 4; j++) s += double(exp_diff_f32(v[k][j], m));
             }
         }
         s = wave_sum(s);
         const double lse = log(s);
+        const double md = double(m);
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
             const int64_t c = lane + int64_t(k) * 64;
             if (c < ncv) {
                 V o;
 #pragma unroll
-                for (int j = 0; j < VN; j++) vset(o, j, T((double(vget(v[k], j)) - md) - lse));
-                yr[c] = o;
+                for (int j = 0; j < 4; j++) o[j] = float((double(v[k][j]) - md) - lse);
+                st_nt(yr + c, o);
             }
+        }
+    }
+}
+
+template <bool LOG, int VPL>
+__global__ __launch_bounds__(kSmBlock) void k_softmax_wave_f64(const double *__restrict__ x, double *__restrict__ y,
+                                                               int64_t rows, int64_t cols)
+{
+    using V = f64x2;
+    const int lane = threadIdx.x & 63;
+    const int64_t r = int64_t(blockIdx.x) * (kSmBlock / 64) + (threadIdx.x >> 6);
+    if (r >= rows) return;  // uniform per wave
+    const V *xr = reinterpret_cast<const V *>(x + r * cols);
+    V *yr = reinterpret_cast<V *>(y + r * cols);
+    const int64_t ncv = cols / 2;
+
+    V v[VPL];
+#pragma unroll
+    for (int k = 0; k < VPL; k++) {
+        const int64_t c = lane + int64_t(k) * 64;
+        if (c < ncv) v[k] = ld_nt(xr + c);
+    }
+    double m = -__builtin_inf();
+#pragma unroll
+    for (int k = 0; k < VPL; k++) {
+        const int64_t c = lane + int64_t(k) * 64;
+        if (c < ncv) {
+#pragma unroll
+            for (int j = 0; j < 2; j++) m = v[k][j] > m ? v[k][j] : m;
+        }
+    }
+    m = wave_max_ignore_nan(m);
+    double s = 0.0;
+#pragma unroll
+    for (int k = 0; k < VPL; k++) {
+        const int64_t c = lane + int64_t(k) * 64;
+        if (c < ncv) {
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const double e = exp(v[k][j] - m);
+                if (!LOG) v[k][j] = e;
+                s += e;
+            }
+        }
+    }
+    s = wave_sum(s);
+    const double lse = LOG ? log(s) : 0.0;
+#pragma unroll
+    for (int k = 0; k < VPL; k++) {
+        const int64_t c = lane + int64_t(k) * 64;
+        if (c < ncv) {
+            V o;
+#pragma unroll
+            for (int j = 0; j < 2; j++) o[j] = LOG ? (v[k][j] - m) - lse : v[k][j] / s;
+            st_nt(yr + c, o);
         }
     }
 }
@@ -141,6 +206,9 @@ NH_DEV double block_sum(double v)
     return r;
 }
 
+NH_DEV float row_exp(float x, float m) { return exp_diff_f32(x, m); }
+NH_DEV double row_exp(double x, double m) { return exp(x - m); }
+
 template <typename T, bool LOG>
 __global__ __launch_bounds__(kSmBlock) void k_softmax_block(const T *__restrict__ x, T *__restrict__ y, int64_t cols)
 {
@@ -152,18 +220,23 @@ __global__ __launch_bounds__(kSmBlock) void k_softmax_block(const T *__restrict_
     m = block_max_ignore_nan(m);
     const double md = double(m);
     double s = 0.0;
-    for (int64_t j = threadIdx.x; j < cols; j += kSmBlock) {
-        if (LOG) s += exp(double(xr[j]) - md);
-        else s += double(T(exp(double(xr[j]) - md)));
-    }
+    for (int64_t j = threadIdx.x; j < cols; j += kSmBlock) s += double(row_exp(xr[j], m));
     s = block_sum(s);
     if (LOG) {
         const double lse = log(s);
         for (int64_t j = threadIdx.x; j < cols; j += kSmBlock) yr[j] = T((double(xr[j]) - md) - lse);
     } else {
-        const T st = T(s);
-        for (int64_t j = threadIdx.x; j < cols; j += kSmBlock) yr[j] = T(exp(double(xr[j]) - md)) / st;
+        for (int64_t j = threadIdx.x; j < cols; j += kSmBlock) yr[j] = T(double(row_exp(xr[j], m)) / s);
     }
+}
+
+template <typename T, bool LOG, int VPL>
+static void launch_wave(const T *x, T *y, int64_t rows, int64_t cols, unsigned g)
+{
+    if constexpr (sizeof(T) == 4)
+        hipLaunchKernelGGL((k_softmax_wave_f32<LOG, VPL>), dim3(g), dim3(kSmBlock), 0, stream(), x, y, rows, cols);
+    else
+        hipLaunchKernelGGL((k_softmax_wave_f64<LOG, VPL>), dim3(g), dim3(kSmBlock), 0, stream(), x, y, rows, cols);
 }
 
 template <typename T, bool LOG>
@@ -174,11 +247,11 @@ static int launch_softmax(const T *x, T *y, int64_t rows, int64_t cols)
     const int64_t ncv = cols / VN;
     const unsigned g = unsigned(ceil_div(rows, kSmBlock / 64));
     if (vec && ncv <= 64 * 16) {
-        if (ncv <= 64) hipLaunchKernelGGL((k_softmax_wave<T, LOG, 1>), dim3(g), dim3(kSmBlock), 0, stream(), x, y, rows, cols);
-        else if (ncv <= 128) hipLaunchKernelGGL((k_softmax_wave<T, LOG, 2>), dim3(g), dim3(kSmBlock), 0, stream(), x, y, rows, cols);
-        else if (ncv <= 256) hipLaunchKernelGGL((k_softmax_wave<T, LOG, 4>), dim3(g), dim3(kSmBlock), 0, stream(), x, y, rows, cols);
-        else if (ncv <= 512) hipLaunchKernelGGL((k_softmax_wave<T, LOG, 8>), dim3(g), dim3(kSmBlock), 0, stream(), x, y, rows, cols);
-        else hipLaunchKernelGGL((k_softmax_wave<T, LOG, 16>), dim3(g), dim3(kSmBlock), 0, stream(), x, y, rows, cols);
+        if (ncv <= 64) launch_wave<T, LOG, 1>(x, y, rows, cols, g);
+        else if (ncv <= 128) launch_wave<T, LOG, 2>(x, y, rows, cols, g);
+        else if (ncv <= 256) launch_wave<T, LOG, 4>(x, y, rows, cols, g);
+        else if (ncv <= 512) launch_wave<T, LOG, 8>(x, y, rows, cols, g);
+        else launch_wave<T, LOG, 16>(x, y, rows, cols, g);
     } else {
         hipLaunchKernelGGL((k_softmax_block<T, LOG>), dim3(unsigned(rows)), dim3(kSmBlock), 0, stream(), x, y, cols);
     }
