@@ -261,8 +261,14 @@ def suite(torch, pn, stream):
     timeit("mul f32 64M", lambda: _check_error(_lib.neural_mul(tc._ptr, ta._ptr, tb._ptr), "mul"), 12 * n)
     timeit("relu f32 64M", lambda: _check_error(_lib.neural_relu(tc._ptr, ta._ptr), "relu"), 8 * n)
     r = ctypes.c_double()
-    timeit("sum f32 64M (incl. D2H of result)", lambda: _lib.neural_sum(ta._ptr, ctypes.byref(r)), 4 * n)
-    timeit("max f32 64M (incl. D2H of result)", lambda: _lib.neural_max(ta._ptr, ctypes.byref(r)), 4 * n)
+    one = torch.empty(1, device=dev)
+    tone = W(one)
+    timeit("sum f32 64M (device result)", lambda: _lib.neural_reduce_sum(ta._ptr, -1, tone._ptr), 4 * n)
+    timeit("max f32 64M (device result)", lambda: _lib.neural_reduce_max(ta._ptr, -1, tone._ptr), 4 * n)
+    one_i = torch.empty(1, dtype=torch.int64, device=dev)
+    timeit("argmax f32 64M (device result)",
+           lambda: _lib.neural_reduce_argmax(ta._ptr, -1, ctypes.c_void_p(one_i.data_ptr())), 4 * n)
+    timeit("sum f32 64M (host API, incl. D2H + sync)", lambda: _lib.neural_sum(ta._ptr, ctypes.byref(r)), 4 * n)
     X = torch.randn(16384, 4096, device=dev)
     bias = torch.randn(4096, device=dev)
     Y = torch.empty_like(X)

@@ -83,8 +83,8 @@ struct Workspace {
     unsigned int *counter;     // kCounters counters, all zero between calls
     void         *result;      // 256 bytes of small results
 };
-constexpr int kMaxPartials = 4096;
-constexpr int kCounters = 64;
+constexpr int kMaxPartials = 16384;
+constexpr int kCounters = 1024;
 Workspace   &workspace();
 
 // Raw pointer classification for the pointer-taking entry points.

@@ -250,7 +250,7 @@ static bool row_broadcast_case(const NeuralTensor *out, const NeuralTensor *a, c
     for (int64_t i = 0; i + 1 < b->ndim; i++)
         if (b->shape[i] != 1) return false;
     const int64_t vn = out->dtype == NEURAL_DTYPE_FLOAT32 ? 4 : 2;
-    return C % vn == 0 && (C / vn) <= int64_t(kBlock) * 65535;
+    return C % vn == 0;
 }
 
 template <typename T, typename Op>
@@ -265,11 +265,7 @@ static int launch_binary(NeuralTensor *out, const NeuralTensor *a, const NeuralT
         return launch_map2_flat(A, B, O, n, op);
     if (row_broadcast_case(out, a, b) && aligned16(A) && aligned16(B) && aligned16(O)) {
         const int64_t C = out->shape[out->ndim - 1];
-        const int64_t R = n / C;
-        const int64_t ncv = C / Vec16<T>::n;
-        dim3 grid(unsigned(ceil_div(R, kRowsPerBlock)), unsigned(ceil_div(ncv, kBlock)));
-        hipLaunchKernelGGL((k_rowbcast<T, Op>), grid, dim3(kBlock), 0, stream(), A, B, O, R, C, op);
-        return check_launch();
+        return launch_rowbcast(A, B, O, n / C, C, op);
     }
     ND4 d;
     NH_TRY(build_nd(out, a, b, d));

@@ -105,37 +105,66 @@ __global__ __launch_bounds__(kBlock) void k_map1_flat_scalar(const T *a, T *o, i
 }
 
 // ---- row broadcast: o[r, c] = op(a[r, c], b[c]) -----------------------------
-// Rows on grid.x (ROWS per block), 256 column vectors on grid.y; the bias
-// vector stays in registers while the block walks its rows.
-constexpr int kRowsPerBlock = 8;
+// The [rows, ncv]-vector array is cut into contiguous spans of kSpan vectors,
+// one per block, streamed like the flat kernel (tiles of 256 x U vectors,
+// loads before stores).  The lane's column vector index is found once by a
+// division and then advances by a fixed amount modulo the row width (d1 =
+// 256 mod ncv per unrolled vector, dU = 256*U mod ncv per tile), so the loop
+// has no division; the bias vector (a few KiB) is served from L1/L2.
+constexpr int64_t kSpan = 8192;
 
 template <typename T, typename Op>
 __global__ __launch_bounds__(kBlock) void k_rowbcast(const T *__restrict__ a, const T *__restrict__ b,
-                                                     T *__restrict__ o, int64_t rows, int64_t cols, Op op)
+                                                     T *__restrict__ o, int64_t nv, int64_t ncv, int64_t d1,
+                                                     int64_t dU, Op op)
 {
     using V = typename Vec16<T>::type;
     constexpr int VN = Vec16<T>::n;
-    const int64_t ncv = cols / VN;
-    const int64_t cv = int64_t(blockIdx.y) * kBlock + threadIdx.x;
-    if (cv >= ncv) return;
-    const V bb = reinterpret_cast<const V *>(b)[cv];
-    const int64_t r0 = int64_t(blockIdx.x) * kRowsPerBlock;
-    V ra[kRowsPerBlock];
+    const V *av = reinterpret_cast<const V *>(a);
+    const V *bv = reinterpret_cast<const V *>(b);
+    V *ov = reinterpret_cast<V *>(o);
+    const int64_t s0 = int64_t(blockIdx.x) * kSpan;
+    const int64_t end = s0 + kSpan < nv ? s0 + kSpan : nv;
+    int64_t c = (s0 + threadIdx.x) % ncv;
+    for (int64_t base = s0 + threadIdx.x; base < end; base += int64_t(kBlock) * kUnroll) {
+        V ra[kUnroll], rb[kUnroll];
+        int64_t cc = c;
 #pragma unroll
-    for (int u = 0; u < kRowsPerBlock; u++) {
-        const int64_t r = r0 + u;
-        if (r < rows) ra[u] = ld_nt(reinterpret_cast<const V *>(a + r * cols) + cv);
-    }
-#pragma unroll
-    for (int u = 0; u < kRowsPerBlock; u++) {
-        const int64_t r = r0 + u;
-        if (r < rows) {
-            V res;
-#pragma unroll
-            for (int k = 0; k < VN; k++) res[k] = op(ra[u][k], bb[k]);
-            st_nt(reinterpret_cast<V *>(o + r * cols) + cv, res);
+        for (int u = 0; u < kUnroll; u++) {
+            const int64_t i = base + int64_t(u) * kBlock;
+            if (i < end) {
+                ra[u] = ld_nt(av + i);
+                rb[u] = bv[cc];
+            }
+            cc += d1;
+            cc = cc >= ncv ? cc - ncv : cc;
         }
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++) {
+            const int64_t i = base + int64_t(u) * kBlock;
+            if (i < end) {
+                V res;
+#pragma unroll
+                for (int k = 0; k < VN; k++) res[k] = op(ra[u][k], rb[u][k]);
+                st_nt(ov + i, res);
+            }
+        }
+        c += dU;
+        c = c >= ncv ? c - ncv : c;
     }
+}
+
+template <typename T, typename Op>
+int launch_rowbcast(const T *a, const T *b, T *o, int64_t rows, int64_t cols, Op op)
+{
+    const int64_t ncv = cols / Vec16<T>::n;
+    if (rows <= 0 || ncv <= 0) return NEURAL_OK;
+    const int64_t nv = rows * ncv;
+    const int64_t d1 = int64_t(kBlock) % ncv;
+    const int64_t dU = (int64_t(kBlock) * kUnroll) % ncv;
+    hipLaunchKernelGGL((k_rowbcast<T, Op>), dim3(unsigned(ceil_div(nv, kSpan))), dim3(kBlock), 0, stream(), a, b, o,
+                       nv, ncv, d1, dU, op);
+    return check_launch();
 }
 
 // ---- N-D strided / broadcast (<= 4 dims, element strides) --------------------

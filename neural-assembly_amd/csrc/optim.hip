@@ -124,39 +124,57 @@ NH_DEV double adam_f64(double pd, double gd, double &m, double &v, const AdamArg
 
 constexpr int kOBlock = 256;
 
-// Four f32 elements per thread-step: 4 x f32 param and grad, 2 x (2 x f64)
-// m and v; every access is a non-temporal 16-byte load or store.
+// Two f32 elements per lane-unit: 8-byte param and grad, 16-byte m and v, so
+// consecutive lanes read consecutive units and every load/store instruction
+// of a wave covers one contiguous span.  Tiles of 256 lanes x U units, all
+// loads of a tile issued before any arithmetic; accesses are non-temporal.
+constexpr int kOUnroll = 4;
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
 template <bool W>
 __global__ __launch_bounds__(kOBlock) void k_adam_f32(float *__restrict__ p, const float *__restrict__ g,
                                                       double *__restrict__ m, double *__restrict__ v, int64_t n,
                                                       AdamArgs a)
 {
-    const int64_t n4 = n / 4;
-    const int64_t stride = int64_t(gridDim.x) * kOBlock;
-    f32x4 *pv4 = reinterpret_cast<f32x4 *>(p);
-    const f32x4 *gv4 = reinterpret_cast<const f32x4 *>(g);
-    f64x2 *mv2 = reinterpret_cast<f64x2 *>(m);
-    f64x2 *vv2 = reinterpret_cast<f64x2 *>(v);
-    for (int64_t i = int64_t(blockIdx.x) * kOBlock + threadIdx.x; i < n4; i += stride) {
-        f32x4 pv = ld_nt(pv4 + i);
-        const f32x4 gv = ld_nt(gv4 + i);
-        f64x2 m0 = ld_nt(mv2 + 2 * i), m1 = ld_nt(mv2 + 2 * i + 1);
-        f64x2 v0 = ld_nt(vv2 + 2 * i), v1 = ld_nt(vv2 + 2 * i + 1);
-        double mm[4] = {m0[0], m0[1], m1[0], m1[1]};
-        double vv[4] = {v0[0], v0[1], v1[0], v1[1]};
+    const int64_t n2 = n / 2;
+    f32x2 *p2 = reinterpret_cast<f32x2 *>(p);
+    const f32x2 *g2 = reinterpret_cast<const f32x2 *>(g);
+    f64x2 *m2 = reinterpret_cast<f64x2 *>(m);
+    f64x2 *v2 = reinterpret_cast<f64x2 *>(v);
+    const int64_t tile = int64_t(kOBlock) * kOUnroll;
+    for (int64_t base = int64_t(blockIdx.x) * tile + threadIdx.x; base < n2; base += int64_t(gridDim.x) * tile) {
+        f32x2 pv[kOUnroll], gv[kOUnroll];
+        f64x2 mv[kOUnroll], vv[kOUnroll];
 #pragma unroll
-        for (int k = 0; k < 4; k++) pv[k] = W ? adamw_f32(pv[k], gv[k], mm[k], vv[k], a) : adam_f32(pv[k], gv[k], mm[k], vv[k], a);
-        m0[0] = mm[0]; m0[1] = mm[1]; m1[0] = mm[2]; m1[1] = mm[3];
-        v0[0] = vv[0]; v0[1] = vv[1]; v1[0] = vv[2]; v1[1] = vv[3];
-        st_nt(pv4 + i, pv);
-        st_nt(mv2 + 2 * i, m0);
-        st_nt(mv2 + 2 * i + 1, m1);
-        st_nt(vv2 + 2 * i, v0);
-        st_nt(vv2 + 2 * i + 1, v1);
+        for (int u = 0; u < kOUnroll; u++) {
+            const int64_t i = base + int64_t(u) * kOBlock;
+            if (i < n2) {
+                pv[u] = ld_nt(p2 + i);
+                gv[u] = ld_nt(g2 + i);
+                mv[u] = ld_nt(m2 + i);
+                vv[u] = ld_nt(v2 + i);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kOUnroll; u++) {
+            const int64_t i = base + int64_t(u) * kOBlock;
+            if (i < n2) {
+#pragma unroll
+                for (int k = 0; k < 2; k++) {
+                    double mm = mv[u][k], vq = vv[u][k];
+                    pv[u][k] = W ? adamw_f32(pv[u][k], gv[u][k], mm, vq, a) : adam_f32(pv[u][k], gv[u][k], mm, vq, a);
+                    mv[u][k] = mm;
+                    vv[u][k] = vq;
+                }
+                st_nt(p2 + i, pv[u]);
+                st_nt(m2 + i, mv[u]);
+                st_nt(v2 + i, vv[u]);
+            }
+        }
     }
-    if (blockIdx.x == 0) {
-        const int64_t j = n4 * 4 + threadIdx.x;
-        if (j < n) p[j] = W ? adamw_f32(p[j], g[j], m[j], v[j], a) : adam_f32(p[j], g[j], m[j], v[j], a);
+    if (blockIdx.x == 0 && threadIdx.x == 0 && (n & 1)) {
+        const int64_t j = n - 1;
+        p[j] = W ? adamw_f32(p[j], g[j], m[j], v[j], a) : adam_f32(p[j], g[j], m[j], v[j], a);
     }
 }
 
@@ -237,10 +255,11 @@ static int step_param(OptHandle *o, size_t i, NeuralTensor *p, const NeuralTenso
         if (p->dtype == NEURAL_DTYPE_FLOAT32) {
             float *P = static_cast<float *>(pw);
             const float *G = static_cast<const float *>(gp);
-            const bool vec = ((reinterpret_cast<uintptr_t>(P) | reinterpret_cast<uintptr_t>(G)) & 15u) == 0;
+            const bool vec = ((reinterpret_cast<uintptr_t>(P) | reinterpret_cast<uintptr_t>(G)) & 7u) == 0;
             if (vec) {
-                if (w) hipLaunchKernelGGL(k_adam_f32<true>, dim3(o_grid(sz / 4)), dim3(kOBlock), 0, stream(), P, G, o->m[i], o->v[i], sz, a);
-                else hipLaunchKernelGGL(k_adam_f32<false>, dim3(o_grid(sz / 4)), dim3(kOBlock), 0, stream(), P, G, o->m[i], o->v[i], sz, a);
+                const unsigned gg = o_grid(ceil_div(sz / 2, kOUnroll));
+                if (w) hipLaunchKernelGGL(k_adam_f32<true>, dim3(gg), dim3(kOBlock), 0, stream(), P, G, o->m[i], o->v[i], sz, a);
+                else hipLaunchKernelGGL(k_adam_f32<false>, dim3(gg), dim3(kOBlock), 0, stream(), P, G, o->m[i], o->v[i], sz, a);
             } else {
                 if (w) hipLaunchKernelGGL(k_adam_f32_scalar<true>, dim3(o_grid(sz)), dim3(kOBlock), 0, stream(), P, G, o->m[i], o->v[i], sz, a);
                 else hipLaunchKernelGGL(k_adam_f32_scalar<false>, dim3(o_grid(sz)), dim3(kOBlock), 0, stream(), P, G, o->m[i], o->v[i], sz, a);

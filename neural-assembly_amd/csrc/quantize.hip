@@ -63,64 +63,73 @@ NH_DEV void minmax_epilogue(double mn, double mx, int symmetric, QuantParams *ou
 
 // The sequential loop keeps, for each of min and max, the FIRST element
 // holding the extreme value; values that compare equal only differ in the
-// sign of zero.  Reduction state: NaN-ignoring min and max values and the
-// index of the first zero (each lane walks increasing indices, so "first" is
-// a one-time capture per lane and a min across lanes).  The epilogue re-reads
-// that zero for its sign, and d0 for the NaN case (d0 NaN makes both NaN).
+// sign of zero.  Lanes keep NaN-ignoring min and max in the input's
+// precision (exact); a segment whose min or max is zero rescans itself for
+// its first zero and takes that zero's sign.  Segment summaries combine in
+// index order with the loop's strict compares, so an earlier segment wins
+// ties.  d0 NaN makes both NaN (no later compare succeeds against NaN).
 template <typename T>
 struct RedMinMax {
-    struct S { double mn, mx; int64_t zfirst; };
-    static constexpr bool kSuffixPass = false;
-    static constexpr int64_t kNone = INT64_MAX;
-    int symmetric;
-    const T *x;
-    NH_DEV S init() const { return {__builtin_inf(), -__builtin_inf(), kNone}; }
-    NH_DEV void acc(S &s, double v, int64_t i) const
+    struct L { T mn, mx; };
+    struct B { double mn, mx; };
+    int symmetric = 0;
+    NH_DEV L linit() const { return {inf_t<T>(), -inf_t<T>()}; }
+    NH_DEV void lacc(L &s, T x, int64_t) const
     {
-        s.mn = __builtin_fmin(s.mn, v);
-        s.mx = __builtin_fmax(s.mx, v);
-        s.zfirst = (v == 0.0 && s.zfirst == kNone) ? i : s.zfirst;
+        s.mn = fmin_nn(s.mn, x);
+        s.mx = fmax_nn(s.mx, x);
     }
-    NH_DEV S comb(S a, S b) const
+    NH_DEV L lcomb(L a, L b) const { return {fmin_nn(a.mn, b.mn), fmax_nn(a.mx, b.mx)}; }
+    template <int TPR>
+    NH_DEV B finish(L s, const T *row, int64_t lo, int64_t hi) const
     {
-        return {__builtin_fmin(a.mn, b.mn), __builtin_fmax(a.mx, b.mx), a.zfirst < b.zfirst ? a.zfirst : b.zfirst};
-    }
-    NH_DEV S shfl(S a, int off) const
-    {
-        return {__shfl_xor(a.mn, off, 64), __shfl_xor(a.mx, off, 64), __shfl_xor(a.zfirst, off, 64)};
-    }
-    NH_DEV void store(void *out, S s) const
-    {
-        double mn = s.mn, mx = s.mx;
-        if (s.zfirst != kNone) {
-            const double z = double(x[s.zfirst]);
-            if (mn == 0.0) mn = z;
-            if (mx == 0.0) mx = z;
+        using G = Grp<TPR>;
+        B b{double(s.mn), double(s.mx)};
+        if (s.mn == T(0) || s.mx == T(0)) {
+            int64_t fz = INT64_MAX;
+            for (int64_t j = lo + G::lane(); j < hi; j += TPR) fz = (fz == INT64_MAX && row[j] == T(0)) ? j : fz;
+            fz = G::min_i64(fz);
+            const double z = double(row[fz]);
+            if (s.mn == T(0)) b.mn = z;
+            if (s.mx == T(0)) b.mx = z;
         }
-        const T first = x[0];
+        return b;
+    }
+    NH_DEV B bident() const { return {__builtin_inf(), -__builtin_inf()}; }
+    NH_DEV B bcomb(B a, B b) const { return {b.mn < a.mn ? b.mn : a.mn, b.mx > a.mx ? b.mx : a.mx}; }
+    NH_DEV void store(void *out, int64_t, B b, const T *row, int64_t) const
+    {
+        double mn = b.mn, mx = b.mx;
+        const T first = row[0];
         if (first != first || mn > mx) mn = mx = __longlong_as_double(0x7ff8000000000000ll);
         minmax_epilogue(mn, mx, symmetric, static_cast<QuantParams *>(out));
     }
 };
 
 // Fused quantize -> dequantize -> squared error (and signal power).
+struct QErrOut { double sig, noise; };
+template <typename T>
 struct RedQErr {
-    struct S { double sig, noise; };
-    static constexpr bool kSuffixPass = false;
+    using L = QErrOut;
+    using B = QErrOut;
     double inv, scale;
     int32_t zp;
-    NH_DEV S init() const { return {0.0, 0.0}; }
-    NH_DEV void acc(S &s, double x, int64_t) const
+    NH_DEV L linit() const { return {0.0, 0.0}; }
+    NH_DEV void lacc(L &s, T xv, int64_t) const
     {
+        const double x = double(xv);
         s.sig += x * x;
         const int8_t q = quant_one(x, inv, zp);
         const double rec = (double(q) - double(zp)) * scale;
         const double d = x - rec;
         s.noise += d * d;
     }
-    NH_DEV S comb(S a, S b) const { return {a.sig + b.sig, a.noise + b.noise}; }
-    NH_DEV S shfl(S a, int off) const { return {__shfl_xor(a.sig, off, 64), __shfl_xor(a.noise, off, 64)}; }
-    NH_DEV void store(void *out, S s) const { *static_cast<S *>(out) = s; }
+    NH_DEV L lcomb(L a, L b) const { return {a.sig + b.sig, a.noise + b.noise}; }
+    template <int TPR>
+    NH_DEV B finish(L s, const T *, int64_t, int64_t) const { return s; }
+    NH_DEV B bident() const { return linit(); }
+    NH_DEV B bcomb(B a, B b) const { return lcomb(a, b); }
+    NH_DEV void store(void *out, int64_t, B b, const T *, int64_t) const { *static_cast<QErrOut *>(out) = b; }
 };
 
 // Params either by value or from device memory (device pipeline).
@@ -139,40 +148,73 @@ NH_DEV void load_q(const QArgs &a, double &inv, double &scale, int32_t &zp)
 
 constexpr int kQBlock = 256;
 
-// 16 elements per thread-step: four 4 x f32 (or eight 2 x f64) loads and one
-// 16-byte store, all non-temporal.
+// Four elements per lane-step: a 16-byte f32 load (two for f64) becomes one
+// packed 4-byte store.  Consecutive lanes take consecutive 4-element units, so
+// every load and store instruction of a wave covers one contiguous span
+// (1 KiB read, 256 B written for f32).  Tiles of 256 lanes x U units, all
+// loads of a tile issued before its stores; accesses are non-temporal.
+constexpr int kQUnroll = 4;
+
+template <typename T>
+struct Quad;  // 4 consecutive elements
+template <> struct Quad<float> {
+    f32x4 v;
+    NH_DEV static Quad load(const float *p, int64_t u) { return {ld_nt(reinterpret_cast<const f32x4 *>(p) + u)}; }
+    NH_DEV void store(float *p, int64_t u) const { st_nt(reinterpret_cast<f32x4 *>(p) + u, v); }
+    NH_DEV double get(int k) const { return double(v[k]); }
+    NH_DEV void set(int k, double x) { v[k] = float(x); }
+};
+template <> struct Quad<double> {
+    f64x2 a, b;
+    NH_DEV static Quad load(const double *p, int64_t u)
+    {
+        const f64x2 *q = reinterpret_cast<const f64x2 *>(p) + 2 * u;
+        return {ld_nt(q), ld_nt(q + 1)};
+    }
+    NH_DEV void store(double *p, int64_t u) const
+    {
+        f64x2 *q = reinterpret_cast<f64x2 *>(p) + 2 * u;
+        st_nt(q, a);
+        st_nt(q + 1, b);
+    }
+    NH_DEV double get(int k) const { return k < 2 ? a[k] : b[k - 2]; }
+    NH_DEV void set(int k, double x)
+    {
+        if (k < 2) a[k] = x;
+        else b[k - 2] = x;
+    }
+};
+
 template <typename T>
 __global__ __launch_bounds__(kQBlock) void k_quantize(const T *__restrict__ x, int8_t *__restrict__ q, int64_t n,
                                                       QArgs qa)
 {
-    using V = typename Vec16<T>::type;
-    constexpr int VN = Vec16<T>::n;
-    constexpr int NV = 16 / VN;
     double inv, scale;
     int32_t zp;
     load_q(qa, inv, scale, zp);
-    const int64_t n16 = n / 16;
-    const int64_t stride = int64_t(gridDim.x) * kQBlock;
-    for (int64_t i = int64_t(blockIdx.x) * kQBlock + threadIdx.x; i < n16; i += stride) {
-        const V *xv = reinterpret_cast<const V *>(x + i * 16);
-        V v[NV];
+    const int64_t n4 = n / 4;
+    uint32_t *q4 = reinterpret_cast<uint32_t *>(q);
+    const int64_t tile = int64_t(kQBlock) * kQUnroll;
+    for (int64_t base = int64_t(blockIdx.x) * tile + threadIdx.x; base < n4; base += int64_t(gridDim.x) * tile) {
+        Quad<T> v[kQUnroll];
 #pragma unroll
-        for (int k = 0; k < NV; k++) v[k] = ld_nt(xv + k);
-        i32x4 w;
-#pragma unroll
-        for (int word = 0; word < 4; word++) {
-            uint32_t packed = 0;
-#pragma unroll
-            for (int b = 0; b < 4; b++) {
-                const int e = word * 4 + b;
-                packed |= uint32_t(uint8_t(quant_one(double(v[e / VN][e % VN]), inv, zp))) << (8 * b);
-            }
-            w[word] = int(packed);
+        for (int u = 0; u < kQUnroll; u++) {
+            const int64_t i = base + int64_t(u) * kQBlock;
+            if (i < n4) v[u] = Quad<T>::load(x, i);
         }
-        st_nt(reinterpret_cast<i32x4 *>(q) + i, w);
+#pragma unroll
+        for (int u = 0; u < kQUnroll; u++) {
+            const int64_t i = base + int64_t(u) * kQBlock;
+            if (i < n4) {
+                uint32_t packed = 0;
+#pragma unroll
+                for (int k = 0; k < 4; k++) packed |= uint32_t(uint8_t(quant_one(v[u].get(k), inv, zp))) << (8 * k);
+                __builtin_nontemporal_store(packed, q4 + i);
+            }
+        }
     }
     if (blockIdx.x == 0) {
-        const int64_t j = n16 * 16 + threadIdx.x;
+        const int64_t j = n4 * 4 + threadIdx.x;
         if (j < n) q[j] = quant_one(double(x[j]), inv, zp);
     }
 }
@@ -192,32 +234,36 @@ template <typename T>
 __global__ __launch_bounds__(kQBlock) void k_dequantize(const int8_t *__restrict__ q, T *__restrict__ y, int64_t n,
                                                         QArgs qa)
 {
-    using V = typename Vec16<T>::type;
-    constexpr int VN = Vec16<T>::n;
-    constexpr int NV = 16 / VN;
     double inv, scale;
     int32_t zp;
     load_q(qa, inv, scale, zp);
     const double dz = double(zp);
-    const int64_t n16 = n / 16;
-    const int64_t stride = int64_t(gridDim.x) * kQBlock;
-    for (int64_t i = int64_t(blockIdx.x) * kQBlock + threadIdx.x; i < n16; i += stride) {
-        const i32x4 w = ld_nt(reinterpret_cast<const i32x4 *>(q) + i);
-        V *yv = reinterpret_cast<V *>(y + i * 16);
+    const int64_t n4 = n / 4;
+    const uint32_t *q4 = reinterpret_cast<const uint32_t *>(q);
+    const int64_t tile = int64_t(kQBlock) * kQUnroll;
+    for (int64_t base = int64_t(blockIdx.x) * tile + threadIdx.x; base < n4; base += int64_t(gridDim.x) * tile) {
+        uint32_t w[kQUnroll];
 #pragma unroll
-        for (int k = 0; k < NV; k++) {
-            V o;
+        for (int u = 0; u < kQUnroll; u++) {
+            const int64_t i = base + int64_t(u) * kQBlock;
+            if (i < n4) w[u] = __builtin_nontemporal_load(q4 + i);
+        }
 #pragma unroll
-            for (int j = 0; j < VN; j++) {
-                const int e = k * VN + j;
-                const int8_t b = int8_t(uint32_t(w[e / 4]) >> (8 * (e % 4)));
-                o[j] = T((double(b) - dz) * scale);
+        for (int u = 0; u < kQUnroll; u++) {
+            const int64_t i = base + int64_t(u) * kQBlock;
+            if (i < n4) {
+                Quad<T> o;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int8_t b = int8_t(w[u] >> (8 * k));
+                    o.set(k, (double(b) - dz) * scale);
+                }
+                o.store(y, i);
             }
-            st_nt(yv + k, o);
         }
     }
     if (blockIdx.x == 0) {
-        const int64_t j = n16 * 16 + threadIdx.x;
+        const int64_t j = n4 * 4 + threadIdx.x;
         if (j < n) y[j] = T((double(q[j]) - dz) * scale);
     }
 }
@@ -233,9 +279,11 @@ __global__ __launch_bounds__(kQBlock) void k_dequantize_scalar(const int8_t *q, 
         y[i] = T((double(q[i]) - double(zp)) * scale);
 }
 
-inline unsigned q_grid(int64_t work)
+// Enough tiles for the whole range, capped at 32 blocks per CU (the
+// grid-stride loop covers the rest).
+inline unsigned q_grid(int64_t units, int64_t per_block)
 {
-    int64_t g = ceil_div(work, kQBlock);
+    int64_t g = ceil_div(units, per_block);
     const int64_t cap = int64_t(num_cus()) * 32;
     if (g > cap) g = cap;
     return unsigned(g < 1 ? 1 : g);
@@ -244,18 +292,25 @@ inline unsigned q_grid(int64_t work)
 template <typename T>
 static int launch_quantize(const T *x, int8_t *q, int64_t n, QArgs qa)
 {
-    const bool vec = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(q)) & 15u) == 0;
-    if (vec) hipLaunchKernelGGL((k_quantize<T>), dim3(q_grid(n / 16)), dim3(kQBlock), 0, stream(), x, q, n, qa);
-    else hipLaunchKernelGGL((k_quantize_scalar<T>), dim3(q_grid(n)), dim3(kQBlock), 0, stream(), x, q, n, qa);
+    const bool vec = (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (reinterpret_cast<uintptr_t>(q) & 3u) == 0;
+    if (vec)
+        hipLaunchKernelGGL((k_quantize<T>), dim3(q_grid(n / 4, kQBlock * kQUnroll)), dim3(kQBlock), 0, stream(), x,
+                           q, n, qa);
+    else
+        hipLaunchKernelGGL((k_quantize_scalar<T>), dim3(q_grid(n, kQBlock)), dim3(kQBlock), 0, stream(), x, q, n, qa);
     return check_launch();
 }
 
 template <typename T>
 static int launch_dequantize(const int8_t *q, T *y, int64_t n, QArgs qa)
 {
-    const bool vec = ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(q)) & 15u) == 0;
-    if (vec) hipLaunchKernelGGL((k_dequantize<T>), dim3(q_grid(n / 16)), dim3(kQBlock), 0, stream(), q, y, n, qa);
-    else hipLaunchKernelGGL((k_dequantize_scalar<T>), dim3(q_grid(n)), dim3(kQBlock), 0, stream(), q, y, n, qa);
+    const bool vec = (reinterpret_cast<uintptr_t>(y) & 15u) == 0 && (reinterpret_cast<uintptr_t>(q) & 3u) == 0;
+    if (vec)
+        hipLaunchKernelGGL((k_dequantize<T>), dim3(q_grid(n / 4, kQBlock * kQUnroll)), dim3(kQBlock), 0, stream(), q,
+                           y, n, qa);
+    else
+        hipLaunchKernelGGL((k_dequantize_scalar<T>), dim3(q_grid(n, kQBlock)), dim3(kQBlock), 0, stream(), q, y, n,
+                           qa);
     return check_launch();
 }
 
@@ -270,7 +325,6 @@ static int calibrate(const T *data, int64_t n, int symmetric, QuantParams *out, 
     if (s.open(data, size_t(n) * sizeof(T), true) != NEURAL_OK) return -1;
     RedMinMax<T> red;
     red.symmetric = symmetric ? 1 : 0;
-    red.x = static_cast<const T *>(s.dev);
     void *res = out_on_device ? static_cast<void *>(out) : workspace().result;
     if (launch_reduce_full(static_cast<const T *>(s.dev), n, red, res) != NEURAL_OK) return -1;
     if (!out_on_device && hipMemcpyAsync(out, res, sizeof(QuantParams), hipMemcpyDeviceToHost, stream()) != hipSuccess)
@@ -320,11 +374,11 @@ static int qerr(const T *data, int64_t n, const QuantParams *p, double *sig, dou
     if (ensure_init() != NEURAL_OK) return -1;
     Staged s;
     if (s.open(data, size_t(n) * sizeof(T), true) != NEURAL_OK) return -1;
-    RedQErr red;
+    RedQErr<T> red;
     red.scale = p->scale;
     red.inv = 1.0 / p->scale;
     red.zp = p->zero_point;
-    RedQErr::S st;
+    QErrOut st;
     void *res = workspace().result;
     if (launch_reduce_full(static_cast<const T *>(s.dev), n, red, res) != NEURAL_OK) return -1;
     if (hipMemcpyAsync(&st, res, sizeof(st), hipMemcpyDeviceToHost, stream()) != hipSuccess) return -1;

@@ -17,129 +17,100 @@ namespace nh {
 
 // ---- reducers -------------------------------------------------------------------
 
-struct RedSum {
-    struct S { double s; };
-    static constexpr bool kSuffixPass = false;
-    NH_DEV S init() const { return {0.0}; }
-    NH_DEV void acc(S &st, double v, int64_t) const { st.s += v; }
-    NH_DEV S comb(S a, S b) const { return {a.s + b.s}; }
-    NH_DEV S shfl(S a, int off) const { return {__shfl_xor(a.s, off, 64)}; }
-    NH_DEV void store(void *out, S st) const { *static_cast<double *>(out) = st.s; }
+// Running-max chain m = (m > x) ? m : x (activations.asm:815-823,888-895).
+// Closed form: NaN if the last element is NaN, else the largest value after
+// the last NaN, the later element winning ties (which only matters for the
+// sign of zero).  Lanes keep a NaN-ignoring max and a NaN/Inf sentinel
+// (x * 0 is NaN exactly for NaN and +-Inf); a segment whose sentinel fired
+// rescans itself for its last NaN, and a zero result rescans for the last
+// zero.  Segment summary {v, nan, nonempty} composes in index order:
+// a later segment that holds a NaN replaces everything before it.
+enum { OUT_T = 0, OUT_F64 = 1 };
+template <typename T, int MODE>
+struct RedMaxChain {
+    struct L { T m, nanacc; };
+    struct B { T v; int32_t nan, nonempty; };
+    static_assert(sizeof(B) % 4 == 0, "");
+    NH_DEV L linit() const { return {-inf_t<T>(), T(0)}; }
+    NH_DEV void lacc(L &s, T x, int64_t) const
+    {
+        s.m = fmax_nn(s.m, x);
+        s.nanacc = fma_t(x, T(0), s.nanacc);
+    }
+    NH_DEV L lcomb(L a, L b) const { return {fmax_nn(a.m, b.m), a.nanacc + b.nanacc}; }
+    template <int TPR>
+    NH_DEV B finish(L s, const T *row, int64_t lo, int64_t hi) const
+    {
+        using G = Grp<TPR>;
+        B b{s.m, 0, hi > lo ? 1 : 0};
+        int64_t from = lo;
+        if (s.nanacc != s.nanacc) {
+            int64_t ln = -1;
+            for (int64_t j = lo + G::lane(); j < hi; j += TPR) ln = (row[j] != row[j]) ? j : ln;
+            ln = G::max_i64(ln);
+            if (ln >= 0) {
+                b.nan = 1;
+                if (ln == hi - 1) {
+                    b.v = qnan_t<T>();
+                    return b;
+                }
+                T m = -inf_t<T>();
+                for (int64_t j = ln + 1 + G::lane(); j < hi; j += TPR) m = fmax_nn(m, row[j]);
+                b.v = G::reduce(m, [](T a, T c) { return fmax_nn(a, c); });
+                from = ln + 1;
+            }
+        }
+        if (b.v == T(0)) {
+            int64_t lz = -1;
+            for (int64_t j = from + G::lane(); j < hi; j += TPR) lz = (row[j] == T(0)) ? j : lz;
+            lz = G::max_i64(lz);
+            b.v = row[lz];
+        }
+        return b;
+    }
+    NH_DEV B bident() const { return {T(0), 0, 0}; }
+    NH_DEV B bcomb(B a, B b) const
+    {
+        if (!b.nonempty) return a;
+        if (!a.nonempty || b.nan) return b;
+        return {(a.v > b.v) ? a.v : b.v, a.nan, 1};
+    }
+    NH_DEV void store(void *out, int64_t r, B b, const T *, int64_t) const
+    {
+        if (MODE == OUT_F64) static_cast<double *>(out)[r] = double(b.v);
+        else static_cast<T *>(out)[r] = b.v;
+    }
 };
 
-// Sum / mean written in the tensor's dtype (one rounding of the double
-// result); `div` is the element count for a mean, 1 for a sum.
+// Argmax: idx = 0, m = x0, update iff x_j > m (main.asm:3245-3292,3598-3640):
+// the first index of the largest non-NaN value, or 0 when x0 is NaN or no
+// element exceeds -inf.  Lane state {best value, its first index}; ties go to
+// the smaller index, so the combine is order-free.
 template <typename T>
-struct RedRowSum : RedSum {
-    int64_t div;
-    NH_DEV void store_row(void *out, int64_t r, S st) const
-    {
-        const double v = div > 1 ? st.s / double(div) : st.s;
-        static_cast<T *>(out)[r] = T(v);
-    }
-    NH_DEV void store(void *out, S st) const { store_row(out, 0, st); }
-    NH_DEV void store_row_x(void *out, int64_t r, S st, const T *, int64_t) const { store_row(out, r, st); }
-};
-
-// Running-max chain m = (m > x) ? m : x as a reduction.  The chain's result
-// is the largest value after the last NaN (NaN if the last element is NaN);
-// equal values only differ in the sign of zero, where the chain keeps the
-// later element.  State: largest non-NaN value, last NaN index, last zero
-// index.  Every lane walks its elements in increasing index order, so "last"
-// is a plain overwrite per lane and a max across lanes.  The element behind a
-// zero result is re-read to get its sign.
-struct RedMax {
-    struct S { double v; int64_t nan_i; int64_t zero_i; };
-    static constexpr bool kSuffixPass = true;
-    const void *x;   // the reduced array (element 0), to read back a zero's sign
-    int f64;         // element type of x
-    NH_DEV S init() const { return {-__builtin_inf(), -1, -1}; }
-    NH_DEV void acc(S &st, double v, int64_t i) const
-    {
-        st.nan_i = (v != v) ? i : st.nan_i;
-        st.zero_i = (v == 0.0) ? i : st.zero_i;
-        st.v = __builtin_fmax(st.v, v);
-    }
-    NH_DEV S comb(S a, S b) const
-    {
-        return {__builtin_fmax(a.v, b.v), a.nan_i > b.nan_i ? a.nan_i : b.nan_i,
-                a.zero_i > b.zero_i ? a.zero_i : b.zero_i};
-    }
-    NH_DEV S shfl(S a, int off) const
-    {
-        return {__shfl_xor(a.v, off, 64), __shfl_xor(a.nan_i, off, 64), __shfl_xor(a.zero_i, off, 64)};
-    }
-    NH_DEV int64_t suffix_start(S st) const { return st.nan_i; }
-    // Second pass over (L, cols) of the same row (no NaN there by
-    // definition).  A row that ends with NaN has an empty suffix: its chain
-    // value is NaN, marked by nan_i = kEndsWithNaN.
-    static constexpr int64_t kEndsWithNaN = -3;
-    NH_DEV S suffix_result(S first, S second, int64_t cols) const
-    {
-        if (first.nan_i == cols - 1) return {0.0, kEndsWithNaN, -1};
-        S r = second;
-        r.nan_i = -1;
-        return r;
-    }
-    // Value of the chain given a first-pass state over x[0..n) (row base xr).
-    NH_DEV double finish(S st, const void *xr) const
-    {
-        double v = st.v;
-        if (v == 0.0 && st.zero_i >= 0)
-            v = f64 ? static_cast<const double *>(xr)[st.zero_i] : double(static_cast<const float *>(xr)[st.zero_i]);
-        return v;
-    }
-    NH_DEV void store(void *out, S st) const { *static_cast<S *>(out) = st; }
-};
-
-template <typename T>
-struct RedRowMax : RedMax {
-    NH_DEV void store_row_x(void *out, int64_t r, S st, const T *xr, int64_t cols) const
-    {
-        const double v = st.nan_i == kEndsWithNaN ? __longlong_as_double(0x7ff8000000000000ll) : finish(st, xr);
-        static_cast<T *>(out)[r] = T(v);
-    }
-};
-
-// Argmax: idx = 0, m = x0, update iff x_j > m.  Reduction state: largest
-// non-NaN value and its first index (-1 while none beats -inf); x0 NaN, or no
-// element above -inf, gives 0 (read from x in the epilogue).
 struct RedArgmax {
-    struct S { double v; int64_t i; };
-    static constexpr bool kSuffixPass = false;
-    NH_DEV S init() const { return {-__builtin_inf(), -1}; }
-    NH_DEV void acc(S &st, double v, int64_t i) const
+    struct L { int64_t i; T v; int32_t pad[sizeof(T) == 4 ? 1 : 2]; };
+    using B = L;
+    NH_DEV L linit() const { return {-1, -inf_t<T>(), {}}; }
+    NH_DEV void lacc(L &s, T x, int64_t i) const
     {
-        const bool up = v > st.v;
-        st.v = up ? v : st.v;
-        st.i = up ? i : st.i;
+        const bool up = x > s.v;
+        s.v = up ? x : s.v;
+        s.i = up ? i : s.i;
     }
-    NH_DEV S comb(S a, S b) const
+    NH_DEV L lcomb(L a, L b) const
     {
         if (b.v > a.v || (b.v == a.v && b.i >= 0 && (a.i < 0 || b.i < a.i))) return b;
         return a;
     }
-    NH_DEV S shfl(S a, int off) const { return {__shfl_xor(a.v, off, 64), __shfl_xor(a.i, off, 64)}; }
-    template <typename T>
-    NH_DEV static int64_t result(S st, const T *x0)
+    template <int TPR>
+    NH_DEV B finish(L s, const T *, int64_t, int64_t) const { return s; }
+    NH_DEV B bident() const { return linit(); }
+    NH_DEV B bcomb(B a, B b) const { return lcomb(a, b); }
+    NH_DEV void store(void *out, int64_t r, B b, const T *row, int64_t) const
     {
-        const T first = x0[0];
-        return (first != first || st.i < 0) ? 0 : st.i;
+        const T first = row[0];
+        static_cast<int64_t *>(out)[r] = (first != first || b.i < 0) ? 0 : b.i;
     }
-};
-
-template <typename T>
-struct RedRowArgmax : RedArgmax {
-    NH_DEV void store_row_x(void *out, int64_t r, S st, const T *xr, int64_t) const
-    {
-        static_cast<int64_t *>(out)[r] = result(st, xr);
-    }
-};
-
-template <typename T>
-struct RedFullArgmax : RedArgmax {
-    const T *x;
-    NH_DEV void store(void *out, S st) const { *static_cast<int64_t *>(out) = result(st, x); }
 };
 
 // ---- column sums (reduce_sum axis=0) -------------------------------------------------
@@ -238,68 +209,26 @@ struct Contig {
     ~Contig() { if (tmp) dev_free(tmp); }
 };
 
-template <class Red, typename Out>
-static int full_reduce(const NeuralTensor *t, const Red &red, Out *host_out)
+// Whole-tensor reduction returned to the host: one launch into the
+// workspace's result area, one 8-byte copy back, one stream sync.
+template <template <typename> class RedOf, typename Out>
+static int full_to_host(const NeuralTensor *t, Out *host_out)
 {
     const int64_t n = numel(t);
     Contig c;
     NH_TRY(c.open(t));
     void *res = workspace().result;
-    if (t->dtype == NEURAL_DTYPE_FLOAT32) NH_TRY(launch_reduce_full(static_cast<const float *>(c.p), n, red, res));
-    else NH_TRY(launch_reduce_full(static_cast<const double *>(c.p), n, red, res));
+    if (t->dtype == NEURAL_DTYPE_FLOAT32)
+        NH_TRY(launch_reduce_full(static_cast<const float *>(c.p), n, RedOf<float>{}, res));
+    else
+        NH_TRY(launch_reduce_full(static_cast<const double *>(c.p), n, RedOf<double>{}, res));
     NH_HIP(hipMemcpyAsync(host_out, res, sizeof(Out), hipMemcpyDeviceToHost, stream()));
     NH_TRY(sync());
     return NEURAL_OK;
 }
 
-// Running-max over a whole tensor: the first pass finds the largest value,
-// the last NaN and the last zero; if a NaN was seen a second pass runs on the
-// suffix after it (the chain restarts there).
-static int full_max(const NeuralTensor *t, double *result)
-{
-    const int64_t n = numel(t);
-    Contig c;
-    NH_TRY(c.open(t));
-    const bool f64 = t->dtype == NEURAL_DTYPE_FLOAT64;
-    const size_t es = elem_size(t->dtype);
-    void *res = workspace().result;
-    int64_t base = 0;
-    for (int pass = 0; pass < 2; pass++) {
-        const void *sp = static_cast<const char *>(c.p) + size_t(base) * es;
-        RedMax red;
-        red.x = sp;
-        red.f64 = f64 ? 1 : 0;
-        const int64_t m = n - base;
-        if (f64) NH_TRY(launch_reduce_full(static_cast<const double *>(sp), m, red, res));
-        else NH_TRY(launch_reduce_full(static_cast<const float *>(sp), m, red, res));
-        RedMax::S st;
-        NH_HIP(hipMemcpyAsync(&st, res, sizeof(st), hipMemcpyDeviceToHost, stream()));
-        NH_TRY(sync());
-        if (st.nan_i < 0) {
-            double v = st.v;
-            if (v == 0.0 && st.zero_i >= 0) {
-                // the sign of the zero the chain keeps (the last one)
-                const char *p = static_cast<const char *>(sp) + size_t(st.zero_i) * es;
-                if (f64) NH_HIP(hipMemcpyAsync(&v, p, 8, hipMemcpyDeviceToHost, stream()));
-                else {
-                    float f;
-                    NH_HIP(hipMemcpyAsync(&f, p, 4, hipMemcpyDeviceToHost, stream()));
-                    NH_TRY(sync());
-                    v = f;
-                }
-                NH_TRY(sync());
-            }
-            *result = v;
-            return NEURAL_OK;
-        }
-        base += st.nan_i + 1;
-        if (base >= n) {
-            *result = __builtin_nan("");
-            return NEURAL_OK;
-        }
-    }
-    return set_error(NEURAL_ERR_INTERNAL);  // unreachable: the suffix holds no NaN
-}
+template <typename T> using SumF64 = RedSum<T, SUM_OUT_F64>;
+template <typename T> using MaxF64 = RedMaxChain<T, OUT_F64>;
 
 // Resolve (rows, cols) for a reduction over `axis` of `in`:
 //   kind 0 = all elements, 1 = last dim (rows x cols), 2 = columns of 2-D.
@@ -320,6 +249,14 @@ static int resolve_axis(const NeuralTensor *in, int64_t axis, int &kind, int64_t
     return NEURAL_OK;
 }
 
+template <typename T>
+static int rows_sum(const void *src, int64_t rows, int64_t cols, bool mean, void *dst)
+{
+    RedSum<T, SUM_OUT_T> red;
+    red.div = mean ? cols : 1;
+    return launch_reduce(static_cast<const T *>(src), rows, cols, cols, red, dst);
+}
+
 static int reduce_sum_mean(const NeuralTensor *in, int64_t axis, NeuralTensor *out, bool mean)
 {
     NH_TRY(ensure_init());
@@ -337,29 +274,12 @@ static int reduce_sum_mean(const NeuralTensor *in, int64_t axis, NeuralTensor *o
     NH_TRY(c.open(in));
     void *dst = nullptr;
     NH_TRY(dev_write(out, &dst, true));
-    if (kind == 0) {
-        // Whole tensor: full-grid reduction storing straight into out[0].
-        if (in->dtype == NEURAL_DTYPE_FLOAT32) {
-            RedRowSum<float> red;
-            red.div = mean ? cols : 1;
-            NH_TRY(launch_reduce_full(static_cast<const float *>(c.p), cols, red, dst));
-        } else {
-            RedRowSum<double> red;
-            red.div = mean ? cols : 1;
-            NH_TRY(launch_reduce_full(static_cast<const double *>(c.p), cols, red, dst));
-        }
-    } else if (kind == 1) {
-        if (in->dtype == NEURAL_DTYPE_FLOAT32) {
-            RedRowSum<float> red;
-            red.div = mean ? cols : 1;
-            NH_TRY(launch_reduce_rows(static_cast<const float *>(c.p), rows, cols, red, dst));
-        } else {
-            RedRowSum<double> red;
-            red.div = mean ? cols : 1;
-            NH_TRY(launch_reduce_rows(static_cast<const double *>(c.p), rows, cols, red, dst));
-        }
-    } else {
+    if (kind == 2) {
         NH_TRY(colsum(in, c.p, rows, cols, mean, dst));
+    } else {
+        // kind 0 is the whole tensor as one row
+        if (in->dtype == NEURAL_DTYPE_FLOAT32) NH_TRY(rows_sum<float>(c.p, rows, cols, mean, dst));
+        else NH_TRY(rows_sum<double>(c.p, rows, cols, mean, dst));
     }
     NH_TRY(dev_written(out));
     return set_error(NEURAL_OK);
@@ -377,7 +297,7 @@ int neural_sum(const NeuralTensor *t, double *result)
     if (!t || !result) return set_error(NEURAL_ERR_NULL_POINTER);
     NH_TRY(check_tensor(t));
     if (numel(t) == 0) { *result = 0.0; return set_error(NEURAL_OK); }
-    NH_TRY(full_reduce(t, RedSum{}, result));
+    NH_TRY(full_to_host<SumF64>(t, result));
     return set_error(NEURAL_OK);
 }
 
@@ -389,7 +309,7 @@ int neural_mean(const NeuralTensor *t, double *result)
     const int64_t n = numel(t);
     if (n == 0) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
     double s = 0.0;
-    NH_TRY(full_reduce(t, RedSum{}, &s));
+    NH_TRY(full_to_host<SumF64>(t, &s));
     *result = s / double(n);
     return set_error(NEURAL_OK);
 }
@@ -400,7 +320,7 @@ int neural_max(const NeuralTensor *t, double *result)
     if (!t || !result) return set_error(NEURAL_ERR_NULL_POINTER);
     NH_TRY(check_tensor(t));
     if (numel(t) == 0) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
-    NH_TRY(full_max(t, result));
+    NH_TRY(full_to_host<MaxF64>(t, result));
     return set_error(NEURAL_OK);
 }
 
@@ -410,17 +330,7 @@ int neural_argmax(const NeuralTensor *t, int64_t *result)
     if (!t || !result) return set_error(NEURAL_ERR_NULL_POINTER);
     NH_TRY(check_tensor(t));
     if (numel(t) == 0) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
-    const void *p = nullptr;
-    NH_TRY(dev_read(t, &p));
-    if (t->dtype == NEURAL_DTYPE_FLOAT32) {
-        RedFullArgmax<float> red;
-        red.x = static_cast<const float *>(p);
-        NH_TRY(full_reduce(t, red, result));
-    } else {
-        RedFullArgmax<double> red;
-        red.x = static_cast<const double *>(p);
-        NH_TRY(full_reduce(t, red, result));
-    }
+    NH_TRY(full_to_host<RedArgmax>(t, result));
     return set_error(NEURAL_OK);
 }
 
@@ -452,9 +362,9 @@ int neural_reduce_max(const NeuralTensor *in, int64_t axis, NeuralTensor *out)
     void *dst = nullptr;
     NH_TRY(dev_write(out, &dst, true));
     if (in->dtype == NEURAL_DTYPE_FLOAT32)
-        NH_TRY(launch_reduce_rows(static_cast<const float *>(c.p), rows, cols, RedRowMax<float>{{nullptr, 0}}, dst));
+        NH_TRY(launch_reduce(static_cast<const float *>(c.p), rows, cols, cols, RedMaxChain<float, OUT_T>{}, dst));
     else
-        NH_TRY(launch_reduce_rows(static_cast<const double *>(c.p), rows, cols, RedRowMax<double>{{nullptr, 1}}, dst));
+        NH_TRY(launch_reduce(static_cast<const double *>(c.p), rows, cols, cols, RedMaxChain<double, OUT_T>{}, dst));
     NH_TRY(dev_written(out));
     return set_error(NEURAL_OK);
 }
@@ -474,9 +384,9 @@ int neural_reduce_argmax(const NeuralTensor *in, int64_t axis, int64_t *out_indi
     Staged so;
     NH_TRY(so.open(out_indices, size_t(rows) * sizeof(int64_t), false));
     if (in->dtype == NEURAL_DTYPE_FLOAT32)
-        NH_TRY(launch_reduce_rows(static_cast<const float *>(c.p), rows, cols, RedRowArgmax<float>{}, so.dev));
+        NH_TRY(launch_reduce(static_cast<const float *>(c.p), rows, cols, cols, RedArgmax<float>{}, so.dev));
     else
-        NH_TRY(launch_reduce_rows(static_cast<const double *>(c.p), rows, cols, RedRowArgmax<double>{}, so.dev));
+        NH_TRY(launch_reduce(static_cast<const double *>(c.p), rows, cols, cols, RedArgmax<double>{}, so.dev));
     NH_TRY(so.finish(true));
     return set_error(NEURAL_OK);
 }
@@ -490,7 +400,8 @@ float simd_sum_f32(const float *a, uint64_t n)
     if (sa.open(a, size_t(n) * 4, true) != NEURAL_OK) return 0.0f;
     void *res = workspace().result;
     double s = 0.0;
-    if (launch_reduce_full(static_cast<const float *>(sa.dev), int64_t(n), RedSum{}, res) != NEURAL_OK) return 0.0f;
+    if (launch_reduce_full(static_cast<const float *>(sa.dev), int64_t(n), SumF64<float>{}, res) != NEURAL_OK)
+        return 0.0f;
     if (hipMemcpyAsync(&s, res, sizeof(s), hipMemcpyDeviceToHost, stream()) != hipSuccess || sync() != NEURAL_OK)
         return 0.0f;
     set_error(NEURAL_OK);
@@ -503,28 +414,28 @@ namespace nh {
 
 // Dot product: sum of a[i]*b[i] in double (products of floats are exact).
 __global__ __launch_bounds__(kRBlock) void k_dot_f32(const float *__restrict__ a, const float *__restrict__ b,
-                                                     int64_t n, RedSum::S *partials, unsigned *counter, double *out)
+                                                     int64_t n, double *partials, unsigned *counter, double *out)
 {
-    RedSum red;
-    RedSum::S st = red.init();
+    double s = 0.0;
     const int64_t stride = int64_t(gridDim.x) * kRBlock;
     for (int64_t i = int64_t(blockIdx.x) * kRBlock + threadIdx.x; i < n; i += stride)
-        st.s += double(a[i]) * double(b[i]);
-    st = block_reduce(red, st);
+        s = __builtin_fma(double(a[i]), double(b[i]), s);
+    const auto add = [](double x, double y) { return x + y; };
+    s = Grp<kRBlock>::reduce(s, add);
     __shared__ bool s_last;
     if (threadIdx.x == 0) {
-        partials[blockIdx.x] = st;
+        partials[blockIdx.x] = s;
         __threadfence();
         s_last = atomicAdd(counter, 1u) == gridDim.x - 1;
     }
     __syncthreads();
     if (!s_last) return;
     __threadfence();
-    RedSum::S acc = red.init();
-    for (int i = threadIdx.x; i < int(gridDim.x); i += kRBlock) acc = red.comb(acc, partials[i]);
-    acc = block_reduce(red, acc);
+    double acc = 0.0;
+    for (int i = threadIdx.x; i < int(gridDim.x); i += kRBlock) acc += partials[i];
+    acc = Grp<kRBlock>::reduce(acc, add);
     if (threadIdx.x == 0) {
-        *out = acc.s;
+        *out = acc;
         *counter = 0u;
     }
 }
@@ -540,8 +451,8 @@ extern "C" float simd_dot_f32(const float *a, const float *b, uint64_t n)
     int64_t g = ceil_div(int64_t(n), kRBlock);
     if (g > int64_t(num_cus()) * 4) g = int64_t(num_cus()) * 4;
     hipLaunchKernelGGL(k_dot_f32, dim3(unsigned(g)), dim3(kRBlock), 0, stream(), static_cast<const float *>(sa.dev),
-                       static_cast<const float *>(sb.dev), int64_t(n), static_cast<RedSum::S *>(ws.partials),
-                       ws.counter, static_cast<double *>(ws.result));
+                       static_cast<const float *>(sb.dev), int64_t(n), static_cast<double *>(ws.partials), ws.counter,
+                       static_cast<double *>(ws.result));
     double s = 0.0;
     if (check_launch() != NEURAL_OK ||
         hipMemcpyAsync(&s, ws.result, sizeof(s), hipMemcpyDeviceToHost, stream()) != hipSuccess || sync() != NEURAL_OK)

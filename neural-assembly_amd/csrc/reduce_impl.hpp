@@ -1,17 +1,34 @@
-// reduce_impl.hpp -- deterministic reductions for gfx950.
+// reduce_impl.hpp -- deterministic segmented reductions for gfx950.
 //
-// Full-tensor reductions run in one launch: a fixed grid of G blocks walks
-// the input in 128-bit vectors (grid-stride over tiles of 256*U vectors), each
-// block reduces its lanes with a wave64 butterfly plus an LDS step, writes one
-// partial, and the last block to arrive (device-scope counter) combines the G
-// partials in a fixed order and stores the result.  G, the tile walk and the
-// combine trees are fixed, so results are bitwise reproducible run to run.
+// Every reduction here is a reduction of R rows of C elements (a whole tensor
+// is one row).  A row is split into contiguous segments; each segment is
+// reduced by one group of lanes (a wave64 or a 256-lane block):
 //
-// Row reductions give each row to one wave (short rows) or one 256-lane block
-// (long rows) and reduce the same way without the cross-block step.
+//   lanes     walk the segment in 128-bit vectors (U vectors in flight per
+//             lane), keeping a small lane state in the input's own precision
+//             where that is exact (min / max / NaN tests) and in double where
+//             it is not (sums);
+//   group     combines lane states with a fixed butterfly (wave) and an LDS
+//             step (block), then `finish` turns the result into an ORDERED
+//             segment summary -- this is where rare cases (a NaN in a
+//             running-max chain, a zero whose sign matters) rescan their own
+//             segment, so the common case costs one or two VALU ops per element;
+//   segments  of one row are combined in index order by a second launch
+//             (one block per row, fixed sequential + ordered-tree combine).
+//             Two launches instead of a last-block ticket: a device-scope
+//             fence + atomic per block cost more than the whole stream at
+//             thousands of blocks (measured on MI355X).
 //
-// A reducer `Red` supplies:  S (state, <= 64 bytes, trivially copyable),
-// init(), acc(S&, double v, int64 idx), comb(S, S) (commutative), shfl(S, off).
+// Grid shapes are a pure function of (rows, cols, CU count), so results are
+// bitwise reproducible run to run.
+//
+// A reducer `Red` for element type T supplies
+//   L  lane state        L linit(); void lacc(L&, T x, int64_t i /*index in row*/);
+//                        L lcomb(L, L)   (commutative)
+//   B  segment summary   B finish<G>(L group_state, const T *row, int64_t lo, int64_t hi)
+//                        B bident(); B bcomb(B earlier, B later)
+//   store                void store(void *out, int64_t row, B, const T *row, int64_t cols)
+// L and B are trivially copyable, a multiple of 4 bytes, B at most 64 bytes.
 #pragma once
 
 #include "common.hpp"
@@ -21,188 +38,275 @@ namespace nh {
 constexpr int kRBlock = 256;
 constexpr int kRUnroll = 4;
 
-template <class Red>
-NH_DEV typename Red::S wave_reduce(const Red &red, typename Red::S s)
-{
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) s = red.comb(s, red.shfl(s, off));
-    return s;
-}
+// ---- generic cross-lane helpers ---------------------------------------------------------
 
-// Block-wide reduce; the result is valid in every thread.
-template <class Red>
-NH_DEV typename Red::S block_reduce(const Red &red, typename Red::S s)
+template <typename S>
+NH_DEV S shfl_xor_obj(const S &s, int off)
 {
-    __shared__ typename Red::S lds[kRBlock / 64];
-    s = wave_reduce(red, s);
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) lds[w] = s;
-    __syncthreads();
-    typename Red::S r = lds[0];
+    static_assert(sizeof(S) % 4 == 0, "state must be a multiple of 4 bytes");
+    constexpr int W = sizeof(S) / 4;
+    int w[W];
+    __builtin_memcpy(w, &s, sizeof(S));
 #pragma unroll
-    for (int i = 1; i < kRBlock / 64; i++) r = red.comb(r, lds[i]);
-    __syncthreads();
+    for (int k = 0; k < W; k++) w[k] = __shfl_xor(w[k], off, 64);
+    S r;
+    __builtin_memcpy(&r, w, sizeof(S));
     return r;
 }
 
-template <typename T, class Red, bool VEC>
-__global__ __launch_bounds__(kRBlock) void k_reduce_full(const T *__restrict__ x, int64_t n, Red red,
-                                                         typename Red::S *partials, unsigned *counter,
-                                                         void *result)
+template <typename S>
+NH_DEV S shfl_down_obj(const S &s, int off)
 {
-    using S = typename Red::S;
-    S st = red.init();
-    if (VEC) {
+    constexpr int W = sizeof(S) / 4;
+    int w[W];
+    __builtin_memcpy(w, &s, sizeof(S));
+#pragma unroll
+    for (int k = 0; k < W; k++) w[k] = __shfl_down(w[k], off, 64);
+    S r;
+    __builtin_memcpy(&r, w, sizeof(S));
+    return r;
+}
+
+// Group of TPR lanes (64 = one wave, 256 = the whole block).  reduce() leaves
+// the same value in every lane of the group: the butterfly pairs are fixed and
+// each pair computes comb(a, b) and comb(b, a), equal for commutative comb.
+template <int TPR>
+struct Grp {
+    static_assert(TPR == 64 || TPR == kRBlock, "a group is one wave or one block");
+    NH_DEV static int lane() { return int(threadIdx.x) % TPR; }
+    template <typename S, typename C>
+    NH_DEV static S reduce(S s, C comb)
+    {
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) s = comb(s, shfl_xor_obj(s, off));
+        if constexpr (TPR == 64) {
+            return s;
+        } else {
+            __shared__ S lds[kRBlock / 64];
+            const int w = threadIdx.x >> 6;
+            if ((threadIdx.x & 63) == 0) lds[w] = s;
+            __syncthreads();
+            S r = lds[0];
+#pragma unroll
+            for (int i = 1; i < kRBlock / 64; i++) r = comb(r, lds[i]);
+            __syncthreads();
+            return r;
+        }
+    }
+    NH_DEV static int64_t max_i64(int64_t v)
+    {
+        return reduce(v, [](int64_t a, int64_t b) { return a > b ? a : b; });
+    }
+    NH_DEV static int64_t min_i64(int64_t v)
+    {
+        return reduce(v, [](int64_t a, int64_t b) { return a < b ? a : b; });
+    }
+};
+
+// ---- the segment walk ---------------------------------------------------------------------
+
+// Reduce row elements [lo, hi) with a group of TPR lanes.  `vec` promises that
+// row is 16-byte aligned and lo is a multiple of the vector width.
+template <typename T, class Red, int TPR>
+NH_DEV typename Red::B seg_reduce(const Red &red, const T *__restrict__ row, int64_t lo, int64_t hi, bool vec)
+{
+    using L = typename Red::L;
+    using G = Grp<TPR>;
+    L st = red.linit();
+    const int lane = G::lane();
+    int64_t tail = lo;
+    if (vec) {
         using V = typename Vec16<T>::type;
         constexpr int VN = Vec16<T>::n;
-        const V *xv = reinterpret_cast<const V *>(x);
-        const int64_t nv = n / VN;
-        const int64_t tile = int64_t(kRBlock) * kRUnroll;
-        for (int64_t t0 = int64_t(blockIdx.x) * tile; t0 < nv; t0 += int64_t(gridDim.x) * tile) {
+        const V *xv = reinterpret_cast<const V *>(row);
+        const int64_t v0 = lo / VN, v1 = hi / VN;
+        for (int64_t c = v0 + lane; c < v1; c += int64_t(TPR) * kRUnroll) {
             V r[kRUnroll];
 #pragma unroll
             for (int u = 0; u < kRUnroll; u++) {
-                const int64_t i = t0 + int64_t(u) * kRBlock + threadIdx.x;
-                if (i < nv) r[u] = ld_nt(xv + i);
+                const int64_t i = c + int64_t(u) * TPR;
+                if (i < v1) r[u] = ld_nt(xv + i);
             }
 #pragma unroll
             for (int u = 0; u < kRUnroll; u++) {
-                const int64_t i = t0 + int64_t(u) * kRBlock + threadIdx.x;
-                if (i < nv) {
+                const int64_t i = c + int64_t(u) * TPR;
+                if (i < v1) {
 #pragma unroll
-                    for (int k = 0; k < VN; k++) red.acc(st, double(r[u][k]), i * VN + k);
+                    for (int k = 0; k < VN; k++) red.lacc(st, r[u][k], i * VN + k);
                 }
             }
         }
-        if (blockIdx.x == 0) {
-            const int64_t j = nv * VN + threadIdx.x;
-            if (j < n) red.acc(st, double(x[j]), j);
-        }
-    } else {
-        const int64_t stride = int64_t(gridDim.x) * kRBlock;
-        for (int64_t i = int64_t(blockIdx.x) * kRBlock + threadIdx.x; i < n; i += stride)
-            red.acc(st, double(x[i]), i);
+        tail = v1 * VN > lo ? v1 * VN : lo;
     }
-    st = block_reduce(red, st);
-
-    __shared__ bool s_last;
-    if (threadIdx.x == 0) {
-        partials[blockIdx.x] = st;
-        __threadfence();
-        const unsigned ticket = atomicAdd(counter, 1u);
-        s_last = (ticket == gridDim.x - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    S acc = red.init();
-    for (int i = threadIdx.x; i < int(gridDim.x); i += kRBlock) acc = red.comb(acc, partials[i]);
-    acc = block_reduce(red, acc);
-    if (threadIdx.x == 0) {
-        red.store(result, acc);
-        *counter = 0u;
-    }
+    for (int64_t j = tail + lane; j < hi; j += TPR) red.lacc(st, row[j], j);
+    st = G::reduce(st, [&](const L &a, const L &b) { return red.lcomb(a, b); });
+    return red.template finish<TPR>(st, row, lo, hi);
 }
 
-inline unsigned reduce_grid(int64_t n, int vn)
-{
-    const int64_t nv = n / vn;
-    int64_t g = ceil_div(nv, int64_t(kRBlock) * kRUnroll);
-    const int64_t cap = int64_t(num_cus()) * 4;
-    if (g > cap) g = cap;
-    if (g > kMaxPartials) g = kMaxPartials;
-    return unsigned(g < 1 ? 1 : g);
-}
-
-// Launch a full reduction writing Red::store(...) into `dev_result` (device).
-template <typename T, class Red>
-int launch_reduce_full(const T *x, int64_t n, const Red &red, void *dev_result)
-{
-    static_assert(sizeof(typename Red::S) <= 64, "reduction state must fit a 64-byte partial slot");
-    Workspace &ws = workspace();
-    auto *partials = static_cast<typename Red::S *>(ws.partials);
-    const bool vec = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
-    if (vec)
-        hipLaunchKernelGGL((k_reduce_full<T, Red, true>), dim3(reduce_grid(n, Vec16<T>::n)), dim3(kRBlock), 0,
-                           stream(), x, n, red, partials, ws.counter, dev_result);
-    else
-        hipLaunchKernelGGL((k_reduce_full<T, Red, false>), dim3(reduce_grid(n, 1)), dim3(kRBlock), 0, stream(), x,
-                           n, red, partials, ws.counter, dev_result);
-    return check_launch();
-}
-
-// ---- row reductions -----------------------------------------------------------------
-// TPR lanes per row (64: one wave, 256: one block); RPB = 256 / TPR rows per block.
-// Red additionally supplies store_row_x(out, row, S, row_base, cols) and, for
-// the running-max semantics, a second pass over the suffix after the row's
-// last NaN (Red::kSuffixPass).
-
+// Ordered combine of n segment summaries p[0..n) by one block; result valid
+// in thread 0.  Each thread folds a contiguous run, then an ordered tree
+// (lane l absorbs lane l+off) across the wave and the four waves in order.
 template <class Red>
-NH_DEV typename Red::S row_group_reduce(const Red &red, typename Red::S s, int tpr)
+NH_DEV typename Red::B ordered_combine(const Red &red, const typename Red::B *p, int n)
 {
-    if (tpr == 64) return wave_reduce(red, s);
-    return block_reduce(red, s);
-}
-
-template <typename T, class Red, int TPR>
-NH_DEV typename Red::S row_scan(const Red &red, const T *xr, int64_t cols, int64_t from, bool vec)
-{
-    typename Red::S st = red.init();
-    const int lane = threadIdx.x % TPR;
-    if (vec && from == 0) {
-        using V = typename Vec16<T>::type;
-        constexpr int VN = Vec16<T>::n;
-        const V *xv = reinterpret_cast<const V *>(xr);
-        const int64_t nv = cols / VN;
-        for (int64_t c = lane; c < nv; c += TPR) {
-            const V v = ld_nt(xv + c);
+    using B = typename Red::B;
+    const int t = threadIdx.x;
+    const int k = (n + kRBlock - 1) / kRBlock;
+    B s = red.bident();
+    const int a = t * k;
+    const int e = a + k < n ? a + k : n;
+    for (int i = a; i < e; i++) s = red.bcomb(s, p[i]);
+    const int lane = t & 63;
 #pragma unroll
-            for (int k = 0; k < VN; k++) red.acc(st, double(v[k]), c * VN + k);
-        }
-        for (int64_t j = nv * VN + lane; j < cols; j += TPR) red.acc(st, double(xr[j]), j);
-    } else {
-        for (int64_t j = from + lane; j < cols; j += TPR) red.acc(st, double(xr[j]), j);
+    for (int off = 1; off < 64; off <<= 1) {
+        const B o = shfl_down_obj(s, off);
+        if ((lane & (2 * off - 1)) == 0) s = red.bcomb(s, o);
     }
-    return st;
+    __shared__ B lds[kRBlock / 64];
+    if (lane == 0) lds[t >> 6] = s;
+    __syncthreads();
+    B r = lds[0];
+#pragma unroll
+    for (int i = 1; i < kRBlock / 64; i++) r = red.bcomb(r, lds[i]);
+    return r;
 }
 
+// ---- kernels --------------------------------------------------------------------------------
+
+// One group (wave or block) per row; RPB = 256 / TPR rows per block.
 template <typename T, class Red, int TPR>
 __global__ __launch_bounds__(kRBlock) void k_reduce_rows(const T *__restrict__ x, int64_t rows, int64_t cols,
-                                                         Red red, void *out, bool vec)
+                                                         int64_t ld, Red red, void *out, bool vec)
 {
     constexpr int RPB = kRBlock / TPR;
     const int64_t r = int64_t(blockIdx.x) * RPB + threadIdx.x / TPR;
-    const bool valid = r < rows;
-    const T *xr = x + (valid ? r : 0) * cols;
-    typename Red::S st = valid ? row_scan<T, Red, TPR>(red, xr, cols, 0, vec) : red.init();
-    st = row_group_reduce(red, st, TPR);
-    if constexpr (Red::kSuffixPass) {
-        // Running-max semantics: restart after the last NaN of the row.  The
-        // branch is uniform per row group (a wave, or the whole block).
-        const int64_t L = red.suffix_start(st);
-        if (L >= 0) {
-            typename Red::S s2 = valid ? row_scan<T, Red, TPR>(red, xr, cols, L + 1, false) : red.init();
-            s2 = row_group_reduce(red, s2, TPR);
-            st = red.suffix_result(st, s2, cols);
-        }
-    }
-    if (valid && (threadIdx.x % TPR) == 0) red.store_row_x(out, r, st, xr, cols);
+    if (r >= rows) return;  // uniform per group (the grid covers whole blocks only when TPR == 256)
+    const T *xr = x + r * ld;
+    const typename Red::B b = seg_reduce<T, Red, TPR>(red, xr, 0, cols, vec);
+    if (Grp<TPR>::lane() == 0) red.store(out, r, b, xr, cols);
 }
 
+// gridDim.x blocks per row (blockIdx.y = row), each reducing one contiguous
+// segment of `chunk` elements into its summary slot.  No fence or atomic: the
+// kernel boundary before k_reduce_combine publishes the summaries.
 template <typename T, class Red>
-int launch_reduce_rows(const T *x, int64_t rows, int64_t cols, const Red &red, void *out)
+__global__ __launch_bounds__(kRBlock) void k_reduce_seg(const T *__restrict__ x, int64_t cols, int64_t ld,
+                                                        int64_t chunk, Red red, typename Red::B *partials, bool vec)
 {
-    if (rows <= 0) return NEURAL_OK;
-    const bool vec = ((reinterpret_cast<uintptr_t>(x) & 15u) == 0) && (cols % Vec16<T>::n == 0);
-    if (cols <= 1024) {
-        const unsigned g = unsigned(ceil_div(rows, kRBlock / 64));
-        hipLaunchKernelGGL((k_reduce_rows<T, Red, 64>), dim3(g), dim3(kRBlock), 0, stream(), x, rows, cols, red, out,
+    const int64_t r = blockIdx.y;
+    const T *xr = x + r * ld;
+    const int64_t lo = int64_t(blockIdx.x) * chunk;
+    const int64_t hi = lo + chunk < cols ? lo + chunk : cols;
+    const typename Red::B b = seg_reduce<T, Red, kRBlock>(red, xr, lo, hi, vec);
+    if (threadIdx.x == 0) partials[r * int64_t(gridDim.x) + blockIdx.x] = b;
+}
+
+// One block per row: ordered combine of the row's gx summaries, then store.
+template <typename T, class Red>
+__global__ __launch_bounds__(kRBlock) void k_reduce_combine(const T *__restrict__ x, int64_t cols, int64_t ld,
+                                                            int gx, Red red, const typename Red::B *partials,
+                                                            void *out)
+{
+    const int64_t r = blockIdx.x;
+    const typename Red::B tot = ordered_combine(red, partials + r * gx, gx);
+    if (threadIdx.x == 0) red.store(out, r, tot, x + r * ld, cols);
+}
+
+// ---- launch policy --------------------------------------------------------------------------
+
+// Reduce `rows` rows of `cols` elements (row r at x + r*ld) and store through
+// Red::store into `out` (device memory).  Many rows: one wave (cols <= 2048)
+// or one block per row.  Few long rows: ~4 blocks per CU spread over the rows,
+// each block one contiguous segment of a multiple of 16 KiB, then the
+// one-block-per-row combine.
+template <typename T, class Red>
+int launch_reduce(const T *x, int64_t rows, int64_t cols, int64_t ld, const Red &red, void *out)
+{
+    static_assert(sizeof(typename Red::B) <= 64, "segment summary must fit a 64-byte partial slot");
+    if (rows <= 0 || cols <= 0) return NEURAL_OK;
+    constexpr int VN = Vec16<T>::n;
+    const bool vec = ((reinterpret_cast<uintptr_t>(x) & 15u) == 0) && ((ld * int64_t(sizeof(T))) % 16 == 0);
+    const int64_t cus = num_cus();
+    const int64_t want = cus * 4;  // blocks that keep every CU streaming (measured: 4/CU >= 8/CU here)
+    constexpr int64_t kGran = int64_t(kRBlock) * kRUnroll * VN;
+    int64_t gx = 1, chunk = cols;
+    if (rows < want && cols > 2 * kGran) {
+        gx = ceil_div(want, rows);
+        chunk = ceil_div(ceil_div(cols, gx), kGran) * kGran;
+        gx = ceil_div(cols, chunk);
+        const int64_t cap = kMaxPartials / rows;
+        if (gx > cap) {
+            gx = cap;
+            chunk = ceil_div(ceil_div(cols, gx), kGran) * kGran;
+            gx = ceil_div(cols, chunk);
+        }
+    }
+    if (gx > 1) {
+        auto *part = static_cast<typename Red::B *>(workspace().partials);
+        const dim3 grid{unsigned(gx), unsigned(rows), 1u};
+        hipLaunchKernelGGL((k_reduce_seg<T, Red>), grid, dim3(kRBlock), 0, stream(), x, cols, ld, chunk, red, part,
                            vec);
+        hipLaunchKernelGGL((k_reduce_combine<T, Red>), dim3(unsigned(rows)), dim3(kRBlock), 0, stream(), x, cols, ld,
+                           int(gx), red, part, out);
+    } else if (cols <= 2048) {
+        const unsigned g = unsigned(ceil_div(rows, kRBlock / 64));
+        hipLaunchKernelGGL((k_reduce_rows<T, Red, 64>), dim3(g), dim3(kRBlock), 0, stream(), x, rows, cols, ld, red,
+                           out, vec);
     } else {
-        hipLaunchKernelGGL((k_reduce_rows<T, Red, 256>), dim3(unsigned(rows)), dim3(kRBlock), 0, stream(), x, rows,
-                           cols, red, out, vec);
+        hipLaunchKernelGGL((k_reduce_rows<T, Red, kRBlock>), dim3(unsigned(rows)), dim3(kRBlock), 0, stream(), x,
+                           rows, cols, ld, red, out, vec);
     }
     return check_launch();
 }
+
+// Whole contiguous array as one row.
+template <typename T, class Red>
+int launch_reduce_full(const T *x, int64_t n, const Red &red, void *out)
+{
+    return launch_reduce(x, 1, n, n, red, out);
+}
+
+// ---- shared reducers ---------------------------------------------------------------------
+
+template <typename T> NH_DEV T fmax_nn(T a, T b);  // NaN-ignoring max
+template <> NH_DEV float fmax_nn(float a, float b) { return __builtin_fmaxf(a, b); }
+template <> NH_DEV double fmax_nn(double a, double b) { return __builtin_fmax(a, b); }
+template <typename T> NH_DEV T fmin_nn(T a, T b);
+template <> NH_DEV float fmin_nn(float a, float b) { return __builtin_fminf(a, b); }
+template <> NH_DEV double fmin_nn(double a, double b) { return __builtin_fmin(a, b); }
+template <typename T> NH_DEV T fma_t(T a, T b, T c);
+template <> NH_DEV float fma_t(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+template <> NH_DEV double fma_t(double a, double b, double c) { return __builtin_fma(a, b, c); }
+template <typename T> NH_DEV T fabs_t(T a);
+template <> NH_DEV float fabs_t(float a) { return __builtin_fabsf(a); }
+template <> NH_DEV double fabs_t(double a) { return __builtin_fabs(a); }
+template <typename T> NH_DEV T inf_t();
+template <> NH_DEV float inf_t<float>() { return __builtin_inff(); }
+template <> NH_DEV double inf_t<double>() { return __builtin_inf(); }
+template <typename T> NH_DEV T qnan_t();
+template <> NH_DEV float qnan_t<float>() { return __builtin_nanf(""); }
+template <> NH_DEV double qnan_t<double>() { return __builtin_nan(""); }
+
+// Sum accumulated in double; the store policy decides what is written.
+//   OUT_T   : out[row] = T(sum / div)          (row sums / means, whole-tensor sum into a tensor)
+//   OUT_F64 : ((double*)out)[row] = sum        (host-returned results)
+enum { SUM_OUT_T = 0, SUM_OUT_F64 = 1 };
+template <typename T, int MODE>
+struct RedSum {
+    using L = double;
+    using B = double;
+    int64_t div = 1;
+    NH_DEV L linit() const { return 0.0; }
+    NH_DEV void lacc(L &s, T x, int64_t) const { s += double(x); }
+    NH_DEV L lcomb(L a, L b) const { return a + b; }
+    template <int TPR> NH_DEV B finish(L s, const T *, int64_t, int64_t) const { return s; }
+    NH_DEV B bident() const { return 0.0; }
+    NH_DEV B bcomb(B a, B b) const { return a + b; }
+    NH_DEV void store(void *out, int64_t r, B s, const T *, int64_t) const
+    {
+        if (MODE == SUM_OUT_F64) static_cast<double *>(out)[r] = s;
+        else static_cast<T *>(out)[r] = T(div > 1 ? s / double(div) : s);
+    }
+};
 
 }  // namespace nh

@@ -12,32 +12,49 @@
 
 namespace nh {
 
+// Lane state: sum of squares in double (fused x*x + s: the square of a
+// float is exact in double, so this is the unfused sum) and the largest |x|
+// (NaN-ignoring).  A NaN makes the sum NaN and nothing else does (all terms
+// are >= 0, so no Inf - Inf); an infinity makes the largest |x| infinite.
+struct ScanOut { double ss; int32_t flags; int32_t pad; };  // flags bit 0: NaN, bit 1: Inf
+
+template <typename T>
 struct RedScan {
-    struct S { double ss; int flags; };  // bit 0: NaN seen, bit 1: Inf seen
-    static constexpr bool kSuffixPass = false;
-    NH_DEV S init() const { return {0.0, 0}; }
-    NH_DEV void acc(S &s, double v, int64_t) const
+    struct L { double ss; T amax; int32_t pad[sizeof(T) == 4 ? 1 : 2]; };
+    using B = L;
+    NH_DEV L linit() const { return {0.0, T(0), {}}; }
+    NH_DEV void lacc(L &s, T x, int64_t) const
     {
-        if (v != v) s.flags |= 1;
-        else if (__builtin_isinf(v)) s.flags |= 2;
-        s.ss += v * v;
+        const double d = double(x);
+        s.ss = __builtin_fma(d, d, s.ss);
+        s.amax = fmax_nn(s.amax, fabs_t(x));
     }
-    NH_DEV S comb(S a, S b) const { return {a.ss + b.ss, a.flags | b.flags}; }
-    NH_DEV S shfl(S a, int off) const { return {__shfl_xor(a.ss, off, 64), __shfl_xor(a.flags, off, 64)}; }
-    NH_DEV void store(void *out, S s) const { *static_cast<S *>(out) = s; }
+    NH_DEV L lcomb(L a, L b) const { return {a.ss + b.ss, fmax_nn(a.amax, b.amax), {}}; }
+    template <int TPR>
+    NH_DEV B finish(L s, const T *, int64_t, int64_t) const { return s; }
+    NH_DEV B bident() const { return linit(); }
+    NH_DEV B bcomb(B a, B b) const { return lcomb(a, b); }
+    NH_DEV void store(void *out, int64_t, B b, const T *, int64_t) const
+    {
+        ScanOut o;
+        o.ss = b.ss;
+        o.flags = (b.ss != b.ss ? 1 : 0) | (b.amax == inf_t<T>() ? 2 : 0);
+        o.pad = 0;
+        *static_cast<ScanOut *>(out) = o;
+    }
 };
 
 template <typename T>
-static int scan_dev(const T *x, int64_t n, RedScan::S *st)
+static int scan_dev(const T *x, int64_t n, ScanOut *st)
 {
     void *res = workspace().result;
-    NH_TRY(launch_reduce_full(x, n, RedScan{}, res));
+    NH_TRY(launch_reduce_full(x, n, RedScan<T>{}, res));
     NH_HIP(hipMemcpyAsync(st, res, sizeof(*st), hipMemcpyDeviceToHost, stream()));
     NH_TRY(sync());
     return NEURAL_OK;
 }
 
-static int scan_raw(const float *data, uint64_t n, RedScan::S *st)
+static int scan_raw(const float *data, uint64_t n, ScanOut *st)
 {
     NH_TRY(ensure_init());
     Staged s;
@@ -56,7 +73,7 @@ extern "C" {
 int neural_tensor_has_nan(const float *data, uint64_t n)
 {
     if (!data || n == 0) return 0;
-    RedScan::S st;
+    ScanOut st;
     if (scan_raw(data, n, &st) != NEURAL_OK) return 0;
     return (st.flags & 1) ? 1 : 0;
 }
@@ -64,7 +81,7 @@ int neural_tensor_has_nan(const float *data, uint64_t n)
 int neural_tensor_has_inf(const float *data, uint64_t n)
 {
     if (!data || n == 0) return 0;
-    RedScan::S st;
+    ScanOut st;
     if (scan_raw(data, n, &st) != NEURAL_OK) return 0;
     return (st.flags & 2) ? 1 : 0;
 }
@@ -72,7 +89,7 @@ int neural_tensor_has_inf(const float *data, uint64_t n)
 float neural_tensor_grad_l2_norm(const float *data, uint64_t n)
 {
     if (!data || n == 0) return 0.0f;
-    RedScan::S st;
+    ScanOut st;
     if (scan_raw(data, n, &st) != NEURAL_OK) return 0.0f;
     return float(std::sqrt(st.ss));
 }
@@ -80,7 +97,7 @@ float neural_tensor_grad_l2_norm(const float *data, uint64_t n)
 int neural_scan_nan_inf_l2(const float *data, uint64_t n, int *has_nan, int *has_inf, double *sumsq)
 {
     if (!data && n > 0) return set_error(NEURAL_ERR_NULL_POINTER);
-    RedScan::S st{0.0, 0};
+    ScanOut st{0.0, 0, 0};
     if (n > 0) NH_TRY(scan_raw(data, n, &st));
     if (has_nan) *has_nan = st.flags & 1;
     if (has_inf) *has_inf = (st.flags >> 1) & 1;
@@ -92,7 +109,7 @@ int neural_tensor_scan(NeuralTensor *t, int *has_nan, int *has_inf, double *sums
 {
     NH_TRY(ensure_init());
     NH_TRY(check_tensor(t));
-    RedScan::S st{0.0, 0};
+    ScanOut st{0.0, 0, 0};
     const int64_t n = numel(t);
     if (n > 0) {
         if (!is_contiguous(t)) return set_error(NEURAL_ERR_INVALID_ARGUMENT);

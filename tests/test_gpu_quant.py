@@ -139,3 +139,22 @@ def test_quantizer_class(pn, ora):
     r = np.frombuffer(bytes(qz.dequantize(q.ctypes.data, x.size)), dtype=np.float64)
     same_bits(r, ora.dequantize(q, ora.calibrate(x, True)))
     assert qz.snr(x.ctypes.data, x.size) > 30
+
+
+@pytest.mark.parametrize("first_zero", [0.0, -0.0])
+def test_calibrate_zero_extremes_large(pn, ora, first_zero):
+    """min (or max) is a zero in a tensor split over many blocks: the loop keeps
+    the FIRST zero, so its sign decides min_val / max_val bit for bit."""
+    rng = np.random.default_rng(21)
+    n = (1 << 22) + 3
+    x = np.abs(rng.laplace(0, 1, n)).astype(np.float32) + np.float32(0.5)
+    zi = np.sort(rng.choice(n, 64, replace=False))
+    x[zi] = np.where(np.arange(64) % 2 == 0, -0.0, 0.0).astype(np.float32)
+    x[zi[0]] = first_zero
+    for sym in (True, False):
+        _params_equal(_calib(pn, x, sym), ora.calibrate(x, sym))
+    y = -x  # now the max is the zero
+    for sym in (True, False):
+        _params_equal(_calib(pn, y, sym), ora.calibrate(y, sym))
+    y[rng.choice(n, 10, replace=False)] = np.nan  # NaNs after x0 are skipped
+    _params_equal(_calib(pn, y, False), ora.calibrate(y, False))

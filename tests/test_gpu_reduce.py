@@ -157,3 +157,85 @@ def test_strided_reduction(pn, ora, rng):
     idx = np.empty(257, dtype=np.int64)
     pn.core._check_error(pn.core._lib.neural_reduce_argmax(keep(pn.Tensor.from_torch(at)), 1, idx.ctypes.data), "am")
     same_bits(idx, ora.rowargmax(np.ascontiguousarray(x)))
+
+
+def _seg_cases(rng, cols):
+    """Rows long enough to be split over many blocks, with the rare cases of
+    the chain (NaN restarts, a NaN as last element, zero-sign ties, Inf) placed
+    at random and at both row ends."""
+    rows = []
+    a = rng.normal(0, 3, cols).astype(np.float32)
+    rows.append(a)
+    b = a.copy()
+    b[rng.choice(cols, 5, replace=False)] = np.nan
+    rows.append(b)
+    c = a.copy()
+    c[-1] = np.nan
+    rows.append(c)
+    d = -np.abs(a)
+    d[rng.choice(cols, 40, replace=False)] = 0.0
+    d[rng.choice(cols, 40, replace=False)] = -0.0
+    rows.append(d)
+    e = a.copy()
+    e[rng.choice(cols, 3, replace=False)] = np.inf
+    e[rng.choice(cols, 3, replace=False)] = -np.inf
+    rows.append(e)
+    f = a.copy()
+    f[0] = np.nan
+    rows.append(f)
+    g = np.full(cols, -np.inf, dtype=np.float32)
+    g[rng.choice(cols, 2, replace=False)] = np.nan
+    rows.append(g)
+    h = -np.abs(a)
+    h[cols // 2] = -0.0
+    h[cols - 1] = 0.0  # the later zero decides the sign
+    rows.append(h)
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("cols", [1 << 20, 3 * (1 << 18) + 5])
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_segmented_rows_special(pn, ora, cols, dt):
+    rng = np.random.default_rng(cols)
+    x = _seg_cases(rng, cols).astype(dt)
+    rows = x.shape[0]
+    lib = pn.core._lib
+    t = pn.Tensor.from_numpy(x)
+    out = pn.Tensor.create([rows], t.dtype)
+    pn.core._check_error(lib.neural_reduce_max(t._ptr, 1, out._ptr), "reduce_max")
+    same_bits(out.numpy(), ora.rowmax_chain(x))
+    idx = np.empty(rows, dtype=np.int64)
+    pn.core._check_error(lib.neural_reduce_argmax(t._ptr, 1, idx.ctypes.data), "reduce_argmax")
+    same_bits(idx, ora.rowargmax(x))
+    out = pn.Tensor.create([rows], t.dtype)
+    pn.core._check_error(lib.neural_reduce_sum(t._ptr, 1, out._ptr), "reduce_sum")
+    e = ora.rowsum_exact(x)
+    g = out.numpy().astype(np.float64)
+    fin = np.isfinite(e)
+    bound = 1e-5 * np.sum(np.abs(np.where(np.isfinite(x), x, 0).astype(np.float64)), axis=1)
+    assert np.all(np.abs(g[fin] - e[fin]) <= bound[fin] + np.abs(e[fin]) * 6e-8)
+    same_bits(np.isnan(g), np.isnan(e))
+    # every row on its own, as a 1-D tensor (one row split over the whole grid)
+    for r in range(rows):
+        tr = pn.Tensor.from_numpy(np.ascontiguousarray(x[r]))
+        one = pn.Tensor.create([1], t.dtype)
+        pn.core._check_error(lib.neural_reduce_max(tr._ptr, -1, one._ptr), "max 1-D")
+        same_bits(one.numpy(), ora.rowmax_chain(x[r:r + 1]))
+        got = np.array([tr.max()], dtype=dt)
+        same_bits(got, np.array([ora.max_chain(x[r])], dtype=dt))
+        assert tr.argmax() == ora.argmax(x[r])
+
+
+def test_reduce_deterministic_large(pn, ora):
+    """Same input, same grid: bitwise identical sums run to run."""
+    rng = np.random.default_rng(77)
+    x = rng.normal(0, 1, (3, 5_000_001)).astype(np.float32)
+    t = pn.Tensor.from_numpy(x)
+    outs = []
+    for _ in range(3):
+        o = pn.Tensor.create([3])
+        pn.core._check_error(pn.core._lib.neural_reduce_sum(t._ptr, 1, o._ptr), "sum")
+        outs.append(o.numpy().tobytes())
+    assert outs[0] == outs[1] == outs[2]
+    e = ora.rowsum_exact(x)
+    assert np.all(np.abs(np.frombuffer(outs[0], np.float32) - e) <= 1e-5 * np.sum(np.abs(x), axis=1) + np.abs(e) * 6e-8)
