@@ -1,11 +1,29 @@
 // activations.hip -- the ten tensor-level activations plus sigmoid.
 //
 // Formulas are those of activations_c.c:124-158 (and node_sigmoid,
-// activations.asm:352-413), evaluated in double for both dtypes and rounded
-// once to float for f32 tensors (activations_c.c:71-77), with the same
-// operation order and no FMA contraction.  exp/log/tanh are the ROCm device
-// library's double routines; the reference uses glibc's, so transcendental
-// results agree to the last few double ulps, not bit for bit.
+// activations.asm:352-413): each element is widened to double, the formula is
+// evaluated in double, and f32 tensors store one final rounding to float
+// (activations_c.c:71-77).
+//
+// The piecewise-linear ones (leaky_relu, hardswish, hardtanh) and the exp-based
+// ones (elu, selu, swish, sigmoid) evaluate the reference expression as
+// written.  tanh, gelu, mish and softplus are evaluated by closed forms built
+// on one double exp, which costs a fifth to a third of the device library's
+// double tanh / log on gfx950 (measured ~141 and ~70 FP64 instructions per
+// element for tanh and log, ~18 for exp), while keeping the two roundings of
+// the reference that decide its low-order result:
+//
+//   u = 1.0 + exp(x)   (softplus, mish): for x << 0, u - 1 is exp(x) quantized to
+//                       multiples of 2^-52; the closed forms take t = u - 1 (exact)
+//                       so the result carries the reference's quantization;
+//   1.0 + tanh(z)       (gelu, z << 0): tanh(z) rounds to a multiple of 2^-53 in
+//                       [-1, -0.5], so 1 + tanh(z) is that multiple; it is
+//                       rebuilt as rint(eps * 2^53) * 2^-53 from eps = 1 - |tanh z|
+//                       computed to double accuracy.
+//
+// Everything else matches the reference's value to a few double ulps (libm
+// differences aside), far inside the 1e-5 (f32) / 1e-12 + 1e-15 (f64) bars.
+// f32 tensors use the float-output paths below.
 #include <cmath>
 
 #include "ew_impl.hpp"
@@ -15,19 +33,232 @@ namespace nh {
 constexpr double kGelu = 0.7978845608028654;
 constexpr double kSeluL = 1.0507009873554804934193349852946;
 constexpr double kSeluA = 1.6732632423543772848170429916717;
+// ln 2 split so that k * kLn2Hi is exact for |k| < 2^20 (32 significant bits).
+constexpr double kLn2Hi = 0x1.62e42fee00000p-1;
+constexpr double kLn2Lo = 0x1.a39ef35793c76p-33;
+constexpr double kSqrtHalf = 0x1.6a09e667f3bcdp-1;
 
-struct ATanh { NH_DEV double f(double x) const { return tanh(x); } };
-struct AGelu { NH_DEV double f(double x) const { return 0.5 * x * (1.0 + tanh(kGelu * (x + 0.044715 * x * x * x))); } };
+// Natural log of u >= 1 (also +inf and NaN, returned unchanged) to about
+// 3 ulp: u = m * 2^k with m in [sqrt(1/2), sqrt(2)), log m = 2 atanh(s),
+// s = (m - 1) / (m + 1), |s| <= 0.1716, atanh by its odd power series through
+// s^19 (truncation below 2.4e-17 relative).
+NH_DEV double log_ge1(double u)
+{
+    int k;
+    double m = frexp(u, &k);
+    if (m < kSqrtHalf) {
+        m += m;
+        k -= 1;
+    }
+    const double f = m - 1.0;  // exact (Sterbenz)
+    const double s = f / (m + 1.0);
+    const double s2 = s * s;
+    double q = 1.0 / 19.0;
+    q = __builtin_fma(q, s2, 1.0 / 17.0);
+    q = __builtin_fma(q, s2, 1.0 / 15.0);
+    q = __builtin_fma(q, s2, 1.0 / 13.0);
+    q = __builtin_fma(q, s2, 1.0 / 11.0);
+    q = __builtin_fma(q, s2, 1.0 / 9.0);
+    q = __builtin_fma(q, s2, 1.0 / 7.0);
+    q = __builtin_fma(q, s2, 1.0 / 5.0);
+    q = __builtin_fma(q, s2, 1.0 / 3.0);
+    const double s_2 = s + s;
+    const double lm = __builtin_fma(s_2 * s2, q, s_2);  // 2s (1 + s^2/3 + s^4/5 + ...)
+    const double dk = double(k);
+    const double r = __builtin_fma(dk, kLn2Hi, __builtin_fma(dk, kLn2Lo, lm));
+    return (u < __builtin_inf()) ? r : u;
+}
+
+// tanh(x) = (E - 1) / (E + 1), E = exp(2|x|), with |x| clamped to 22 (where
+// the double result is already +-1); |x| < 2^-7 uses the Taylor series through
+// x^7 (truncation below 3e-19 relative; zeros keep their sign, denormals are
+// returned unchanged).
+// E - 1 is exact, so the relative error is ~1 ulp(E) / (E - 1) < 1.5e-14.
+NH_DEV double tanh_d(double x)
+{
+    const double a = __builtin_fabs(x);
+    const double x2 = x * x;
+    const double small = __builtin_copysign(
+        __builtin_fma(x * x2, __builtin_fma(x2, __builtin_fma(x2, -17.0 / 315.0, 2.0 / 15.0), -1.0 / 3.0), x), x);
+    const double c = a < 22.0 ? a : 22.0;
+    const double e = exp(c + c);
+    const double big = __builtin_copysign((e - 1.0) / (e + 1.0), x);
+    return (a < 0x1p-7 || x != x) ? small : big;
+}
+
+// 1 + tanh(z) as the reference's double tanh leaves it, from w = exp(-2|z|):
+//   z >= 0:  1 + (1 - w)/(1 + w) = 2/(1 + w)                     (no cancellation)
+//   z < 0:   eps = 1 - |tanh z| = 2w/(1 + w); while tanh z is in [-1, -0.5]
+//            it is a multiple of 2^-53, so 1 + tanh z = rint(eps * 2^53) * 2^-53
+//            (round-half-even on the multiple = round-half-even on tanh z).
+NH_DEV double one_plus_tanh(double z)
+{
+    const double w = exp(-2.0 * __builtin_fabs(z));
+    const double d = 1.0 + w;
+    if (z >= 0.0) return 2.0 / d;
+    const double eps = (w + w) / d;
+    return eps < 0.5 ? __builtin_rint(eps * 0x1p53) * 0x1p-53 : eps;
+}
+
+NH_DEV double gelu_d(double x)
+{
+    const double z = kGelu * (x + 0.044715 * x * x * x);  // activations_c.c:130-131, same order
+    return 0.5 * x * one_plus_tanh(z);
+}
+
+// softplus = log(u), u = 1.0 + exp(x) rounded as in the reference.
+NH_DEV double softplus_d(double x) { return log_ge1(1.0 + exp(x)); }
+
+// mish = x * tanh(log u) with tanh(log u) = (u^2 - 1)/(u^2 + 1):
+//   t = u - 1 <= 1:  t(2 + t) / (t(2 + t) + 2)     (t exact: the reference's rounding of u)
+//   t > 1:           1 - 2 / (u^2 + 1)             (u^2 = inf gives 1)
+NH_DEV double mish_d(double x)
+{
+    const double u = 1.0 + exp(x);
+    const double t = u - 1.0;
+    double g;
+    if (t <= 1.0) {
+        const double a = t * (2.0 + t);
+        g = a / (a + 2.0);
+    } else {
+        g = 1.0 - 2.0 / (u * u + 1.0);
+    }
+    return x * g;
+}
+
+// ---- f32 outputs ----------------------------------------------------------------
+// An f32 result only needs the reference's value to 1e-5 relative, so where the
+// reference's double roundings are invisible at that level the formula runs in
+// float (device expf / log1pf / tanhf, a few ulp), and the double closed forms
+// above take over only where the quantization shows:
+//   softplus, mish: x < -20, where 1 + exp(x) keeps fewer than 31 bits of exp(x)
+//                   (above it the quantization is < 5.4e-8 relative);
+//   gelu:           z < -10.5, where 1 + tanh(z) < 1.5e-9 is a small multiple of
+//                   2^-53 (above it the quantization is < 7.4e-8 relative);
+//   swish:          x < -80, where exp(-x) leaves float's range.
+// Inputs of magnitude below 2^-30 (where outputs can be denormal, so a second
+// rounding would show) take the double formula's linear term exactly.
+
+// exp(y) for a double y to ~1e-7 relative from the float exp: y = hi + lo
+// exactly split, exp(y) = expf(hi) * (1 + lo) (an infinite hi has no low part).
+NH_DEV float exp_split(double y)
+{
+    const float hi = float(y);
+    const float lo = (hi - hi == 0.0f) ? float(y - double(hi)) : 0.0f;  // +-inf / NaN: no low part
+    const float e = expf(hi);
+    return __builtin_fmaf(e, lo, e);
+}
+
+NH_DEV float rcp_f32(float a) { return __builtin_amdgcn_rcpf(a); }  // 1 ulp, a in [1, 2^126)
+
+// log(1 + e) for e in [0, 1] in float: 2 atanh(s), s = e / (2 + e) <= 1/3, odd
+// series through s^13 (truncation below 1.5e-8 relative).
+NH_DEV float log1p_01(float e)
+{
+    const float s = e * rcp_f32(2.0f + e);
+    const float s2 = s * s;
+    float q = 1.0f / 13.0f;
+    q = __builtin_fmaf(q, s2, 1.0f / 11.0f);
+    q = __builtin_fmaf(q, s2, 1.0f / 9.0f);
+    q = __builtin_fmaf(q, s2, 1.0f / 7.0f);
+    q = __builtin_fmaf(q, s2, 1.0f / 5.0f);
+    q = __builtin_fmaf(q, s2, 1.0f / 3.0f);
+    const float s_2 = s + s;
+    return __builtin_fmaf(s_2 * s2, q, s_2);
+}
+
+// Each f32 activation below is a head (float formula, every element, with the
+// `need` flag for the region where the reference's double rounding shows) and
+// a tail (the exact double evaluation for those elements).
+struct GeluF32 {
+    static constexpr bool kHeadTail = true;
+    NH_DEV float head(float xf, bool &need) const
+    {
+        const double x = double(xf);
+        const double z = kGelu * (x + 0.044715 * x * x * x);
+        need = z < -10.5;  // 1 + tanh(z) < 1.5e-9: a small multiple of 2^-53 in the reference
+        const float w = exp_split(-2.0 * __builtin_fabs(z));
+        const float r = rcp_f32(1.0f + w);
+        const float onept = z >= 0.0 ? 2.0f * r : (w + w) * r;
+        return (0.5f * xf) * onept;
+    }
+    NH_DEV float tail(float xf) const
+    {
+        const double x = double(xf);
+        const double z = kGelu * (x + 0.044715 * x * x * x);
+        const double w = exp(z + z);               // < 7.6e-10
+        const double eps = (w + w) * (1.0 - w);   // 2w / (1 + w) to 6e-19 relative
+        return float(0.5 * x * (__builtin_rint(eps * 0x1p53) * 0x1p-53));
+    }
+};
+
+struct SoftplusF32 {
+    static constexpr bool kHeadTail = true;
+    NH_DEV float head(float x, bool &need) const
+    {
+        need = x < -20.0f;  // 1 + exp(x) keeps < 31 bits of exp(x) in the reference
+        if (x >= 709.78271484375f) return __builtin_inff();  // the reference's double exp overflows
+        return __builtin_fmaxf(x, 0.0f) + log1p_01(expf(-__builtin_fabsf(x)));
+    }
+    NH_DEV float tail(float x) const
+    {
+        const double t = (1.0 + exp(double(x))) - 1.0;  // the reference's quantized exp(x); t < 2.1e-9
+        return float(t - 0.5 * t * t);                  // log1p(t), truncation t^3/3
+    }
+};
+
+// mish: tanh(log u) from t = u - 1: t(2+t) / (t(2+t) + 2) for t <= 1, else
+// 1 - 2/(u^2 + 1).
+NH_DEV float mish_from_t(float x, float t)
+{
+    float g;
+    if (t <= 1.0f) {
+        const float a = t * (2.0f + t);
+        g = a * rcp_f32(a + 2.0f);
+    } else {
+        const float u = 1.0f + t;
+        g = 1.0f - 2.0f * rcp_f32(__builtin_fmaf(u, u, 1.0f));
+    }
+    return x * g;
+}
+
+struct MishF32 {
+    static constexpr bool kHeadTail = true;
+    NH_DEV float head(float x, bool &need) const
+    {
+        need = x < -20.0f;
+        if (__builtin_fabsf(x) < 0x1p-30f) return float(double(x) * 0.6);  // tanh(log 2) = 0.6 in double
+        return mish_from_t(x, expf(x));
+    }
+    NH_DEV float tail(float x) const { return mish_from_t(x, float((1.0 + exp(double(x))) - 1.0)); }
+};
+
+struct SwishF32 {
+    static constexpr bool kHeadTail = true;
+    NH_DEV float head(float x, bool &need) const
+    {
+        need = x < -80.0f;  // exp(-x) leaves float's range
+        return x * rcp_f32(1.0f + expf(-x));
+    }
+    NH_DEV float tail(float x) const { return float(double(x) / (1.0 + exp(-double(x)))); }
+};
+
+// ---- functors ----------------------------------------------------------------------
+
+// Reference formula (or its closed form) in double; f32 tensors round once.
+struct ATanh { NH_DEV double f(double x) const { return tanh_d(x); } };
+struct AGelu { NH_DEV double f(double x) const { return gelu_d(x); } };
 struct ALeaky { double alpha; NH_DEV double f(double x) const { return x >= 0 ? x : alpha * x; } };
 struct AElu { double alpha; NH_DEV double f(double x) const { return x > 0 ? x : alpha * (exp(x) - 1.0); } };
 struct ASelu { NH_DEV double f(double x) const { return x > 0 ? kSeluL * x : kSeluL * kSeluA * (exp(x) - 1.0); } };
 struct ASwish { NH_DEV double f(double x) const { return x / (1.0 + exp(-x)); } };
-struct AMish { NH_DEV double f(double x) const { return x * tanh(log(1.0 + exp(x))); } };
+struct AMish { NH_DEV double f(double x) const { return mish_d(x); } };
 struct AHardswish { NH_DEV double f(double x) const { return x <= -3.0 ? 0.0 : (x >= 3.0 ? x : x * (x + 3.0) / 6.0); } };
-struct ASoftplus { NH_DEV double f(double x) const { return log(1.0 + exp(x)); } };
+struct ASoftplus { NH_DEV double f(double x) const { return softplus_d(x); } };
 struct AHardtanh { NH_DEV double f(double x) const { return x < -1.0 ? -1.0 : (x > 1.0 ? 1.0 : x); } };
 struct ASigmoid { NH_DEV double f(double x) const { return 1.0 / (1.0 + exp(x * -1.0)); } };
 
+// Elementwise functor over both dtypes from a double formula.
 template <class A>
 struct ActFn {
     A a;
@@ -35,13 +266,46 @@ struct ActFn {
     NH_DEV double operator()(double x) const { return a.f(x); }
 };
 
+// f32 functor from a head/tail pair (k_map1_f32_tail on aligned contiguous
+// tensors; per element otherwise).
+template <class H>
+struct HeadTailFn {
+    H h;
+    static constexpr bool kHeadTail = true;
+    NH_DEV float head(float x, bool &need) const { return h.head(x, need); }
+    NH_DEV float tail(float x) const { return h.tail(x); }
+    NH_DEV float operator()(float x) const
+    {
+        bool need = false;
+        const float y = h.head(x, need);
+        return need ? h.tail(x) : y;
+    }
+};
+
+// f32 functor calling a float formula directly.
+struct TanhF32Fn {
+    NH_DEV float operator()(float x) const { return tanhf(x); }
+};
+
+template <class A, class F32>
+static int act2(void *out, const void *in, F32 f32, A a = A{})
+{
+    if (!out || !in) return set_error(NEURAL_ERR_NULL_POINTER);
+    ActFn<A> f64{a};
+    return run_unary(static_cast<NeuralTensor *>(out), static_cast<const NeuralTensor *>(in), f32, f64);
+}
+
 template <class A>
 static int act(void *out, const void *in, A a = A{})
 {
-    if (!out || !in) return set_error(NEURAL_ERR_NULL_POINTER);
-    ActFn<A> f{a};
-    return run_unary(static_cast<NeuralTensor *>(out), static_cast<const NeuralTensor *>(in), f, f);
+    return act2<A>(out, in, ActFn<A>{a}, a);
 }
+
+static int act_gelu_impl(void *out, const void *in) { return act2<AGelu>(out, in, HeadTailFn<GeluF32>{}); }
+static int act_swish_impl(void *out, const void *in) { return act2<ASwish>(out, in, HeadTailFn<SwishF32>{}); }
+static int act_mish_impl(void *out, const void *in) { return act2<AMish>(out, in, HeadTailFn<MishF32>{}); }
+static int act_softplus_impl(void *out, const void *in) { return act2<ASoftplus>(out, in, HeadTailFn<SoftplusF32>{}); }
+static int act_tanh_impl(void *out, const void *in) { return act2<ATanh>(out, in, TanhF32Fn{}); }
 
 }  // namespace nh
 
@@ -49,29 +313,29 @@ using namespace nh;
 
 extern "C" {
 
-int act_tanh(void *out, const void *in) { return act<ATanh>(out, in); }
-int act_gelu(void *out, const void *in) { return act<AGelu>(out, in); }
+int act_tanh(void *out, const void *in) { return act_tanh_impl(out, in); }
+int act_gelu(void *out, const void *in) { return act_gelu_impl(out, in); }
 int act_leaky_relu(void *out, const void *in, double alpha) { return act<ALeaky>(out, in, ALeaky{alpha}); }
 int act_elu(void *out, const void *in, double alpha) { return act<AElu>(out, in, AElu{alpha}); }
 int act_selu(void *out, const void *in) { return act<ASelu>(out, in); }
-int act_swish(void *out, const void *in) { return act<ASwish>(out, in); }
-int act_mish(void *out, const void *in) { return act<AMish>(out, in); }
+int act_swish(void *out, const void *in) { return act_swish_impl(out, in); }
+int act_mish(void *out, const void *in) { return act_mish_impl(out, in); }
 int act_hardswish(void *out, const void *in) { return act<AHardswish>(out, in); }
-int act_softplus(void *out, const void *in) { return act<ASoftplus>(out, in); }
+int act_softplus(void *out, const void *in) { return act_softplus_impl(out, in); }
 int act_hardtanh(void *out, const void *in) { return act<AHardtanh>(out, in); }
 
 // Tensor-typed aliases of the header's neural_* activations
 // (neural_api.h:387-486).
 int neural_sigmoid(NeuralTensor *out, const NeuralTensor *in) { return act<ASigmoid>(out, in); }
-int neural_tanh(NeuralTensor *out, const NeuralTensor *in) { return act<ATanh>(out, in); }
-int neural_gelu(NeuralTensor *out, const NeuralTensor *in) { return act<AGelu>(out, in); }
+int neural_tanh(NeuralTensor *out, const NeuralTensor *in) { return act_tanh_impl(out, in); }
+int neural_gelu(NeuralTensor *out, const NeuralTensor *in) { return act_gelu_impl(out, in); }
 int neural_leaky_relu(NeuralTensor *out, const NeuralTensor *in, double alpha) { return act<ALeaky>(out, in, ALeaky{alpha}); }
 int neural_elu(NeuralTensor *out, const NeuralTensor *in, double alpha) { return act<AElu>(out, in, AElu{alpha}); }
 int neural_selu(NeuralTensor *out, const NeuralTensor *in) { return act<ASelu>(out, in); }
-int neural_swish(NeuralTensor *out, const NeuralTensor *in) { return act<ASwish>(out, in); }
-int neural_mish(NeuralTensor *out, const NeuralTensor *in) { return act<AMish>(out, in); }
+int neural_swish(NeuralTensor *out, const NeuralTensor *in) { return act_swish_impl(out, in); }
+int neural_mish(NeuralTensor *out, const NeuralTensor *in) { return act_mish_impl(out, in); }
 int neural_hardswish(NeuralTensor *out, const NeuralTensor *in) { return act<AHardswish>(out, in); }
-int neural_softplus(NeuralTensor *out, const NeuralTensor *in) { return act<ASoftplus>(out, in); }
+int neural_softplus(NeuralTensor *out, const NeuralTensor *in) { return act_softplus_impl(out, in); }
 int neural_hardtanh(NeuralTensor *out, const NeuralTensor *in) { return act<AHardtanh>(out, in); }
 
 }  // extern "C"

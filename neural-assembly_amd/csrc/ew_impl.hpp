@@ -8,6 +8,8 @@
 // decomposition.
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace nh {
@@ -102,6 +104,83 @@ __global__ __launch_bounds__(kBlock) void k_map1_flat_scalar(const T *a, T *o, i
 {
     const int64_t stride = int64_t(gridDim.x) * kBlock;
     for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) o[i] = f(a[i]);
+}
+
+// ---- flat unary f32 with a rare expensive path ------------------------------
+// F supplies head(x, need) -- the cheap evaluation, run for every element,
+// which also says whether the element needs the expensive one -- and
+// tail(x).  Per tile, each wave queues its `need` elements in LDS (ballot +
+// prefix count keeps them in lane/element order), runs tail() over the queue
+// 64 at a time, and reads the results back, so the tail costs one pass per 64
+// queued elements instead of one pass per element position that any lane
+// needs.  The tile loop is block-uniform; the wave's queue holds a full tile.
+constexpr int kTailUnroll = 2;  // 4 blows past 240 VGPRs (occupancy 1)
+
+template <typename F>
+__global__ __launch_bounds__(kBlock) void k_map1_f32_tail(const float *__restrict__ a, float *__restrict__ o,
+                                                          int64_t n, F f)
+{
+    constexpr int kUnroll = kTailUnroll;
+    constexpr int kPerLane = kUnroll * 4;
+    __shared__ float queue[kBlock / 64][64 * kPerLane];
+    float *wq = queue[threadIdx.x >> 6];
+    const int lane = threadIdx.x & 63;
+    const uint64_t below = __lanemask_lt();
+    const int64_t nv = n / 4;
+    const f32x4 *av = reinterpret_cast<const f32x4 *>(a);
+    f32x4 *ov = reinterpret_cast<f32x4 *>(o);
+    const int64_t tile = int64_t(kBlock) * kUnroll;
+    for (int64_t t0 = int64_t(blockIdx.x) * tile; t0 < nv; t0 += int64_t(gridDim.x) * tile) {
+        f32x4 r[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++) {
+            const int64_t i = t0 + int64_t(u) * kBlock + threadIdx.x;
+            if (i < nv) r[u] = ld_nt(av + i);
+        }
+        int cnt = 0;  // wave-uniform queue length
+        int slot[kPerLane];
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++) {
+            const bool valid = t0 + int64_t(u) * kBlock + threadIdx.x < nv;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                bool need = false;
+                const float x = r[u][k];
+                const float y = valid ? f.head(x, need) : 0.0f;
+                need = need && valid;
+                const uint64_t m = __ballot(need);
+                slot[u * 4 + k] = need ? cnt + __popcll(m & below) : -1;
+                if (need) wq[cnt + __popcll(m & below)] = x;
+                cnt += __popcll(m);
+                r[u][k] = y;
+            }
+        }
+        if (cnt > 0) {
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            for (int j = lane; j < cnt; j += 64) wq[j] = f.tail(wq[j]);
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int e = 0; e < kPerLane; e++)
+                if (slot[e] >= 0) r[e / 4][e % 4] = wq[slot[e]];
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++) {
+            const int64_t i = t0 + int64_t(u) * kBlock + threadIdx.x;
+            if (i < nv) st_nt(ov + i, r[u]);
+        }
+    }
+    if (blockIdx.x == 0) {
+        const int64_t j = nv * 4 + threadIdx.x;
+        if (j < n) {
+            bool need = false;
+            const float y = f.head(a[j], need);
+            o[j] = need ? f.tail(a[j]) : y;
+        }
+    }
 }
 
 // ---- row broadcast: o[r, c] = op(a[r, c], b[c]) -----------------------------
@@ -240,6 +319,18 @@ int launch_map2_flat(const T *a, const T *b, T *o, int64_t n, Op op)
     return check_launch();
 }
 
+// f32 head/tail variant of launch_map1_flat (contiguous, 16-byte aligned).
+template <typename F>
+int launch_map1_f32_tail(const float *a, float *o, int64_t n, F f)
+{
+    if (n <= 0) return NEURAL_OK;
+    int64_t g = ceil_div(n / 4, int64_t(kBlock) * kTailUnroll);
+    const int64_t cap = int64_t(num_cus()) * 32;
+    g = g > cap ? cap : (g < 1 ? 1 : g);
+    hipLaunchKernelGGL((k_map1_f32_tail<F>), dim3(unsigned(g)), dim3(kBlock), 0, stream(), a, o, n, f);
+    return check_launch();
+}
+
 template <typename T, typename F>
 int launch_map1_flat(const T *a, T *o, int64_t n, F f)
 {
@@ -258,6 +349,10 @@ int build_nd(const NeuralTensor *out, const NeuralTensor *a, const NeuralTensor 
 
 // Unary op over tensors (contiguous fast path, else N-D); `in` and `out`
 // must have the same dtype and element count.
+// F32 functors that declare kHeadTail provide head()/tail() for k_map1_f32_tail.
+template <typename F, typename = void> struct HasHeadTail : std::false_type {};
+template <typename F> struct HasHeadTail<F, std::void_t<decltype(F::kHeadTail)>> : std::true_type {};
+
 template <typename F32, typename F64>
 int run_unary(NeuralTensor *out, const NeuralTensor *in, F32 f32, F64 f64)
 {
@@ -275,9 +370,16 @@ int run_unary(NeuralTensor *out, const NeuralTensor *in, F32 f32, F64 f64)
     const bool flat = is_contiguous(in) && is_contiguous(out);
     NH_TRY(dev_write(out, &dst, is_contiguous(out)));
     if (flat) {
-        if (in->dtype == NEURAL_DTYPE_FLOAT32)
-            NH_TRY(launch_map1_flat(static_cast<const float *>(src), static_cast<float *>(dst), n, f32));
-        else
+        if (in->dtype == NEURAL_DTYPE_FLOAT32) {
+            const float *fs = static_cast<const float *>(src);
+            float *fd = static_cast<float *>(dst);
+            if constexpr (HasHeadTail<F32>::value) {
+                if (aligned16(fs) && aligned16(fd)) NH_TRY(launch_map1_f32_tail(fs, fd, n, f32));
+                else NH_TRY(launch_map1_flat(fs, fd, n, f32));
+            } else {
+                NH_TRY(launch_map1_flat(fs, fd, n, f32));
+            }
+        } else
             NH_TRY(launch_map1_flat(static_cast<const double *>(src), static_cast<double *>(dst), n, f64));
     } else {
         ND4 d;

@@ -78,3 +78,24 @@ def test_modules_and_aliases(pn, ora):
         assert getattr(pn.core._lib, alias)(out._ptr, t._ptr) == 0
         rel_close(out.numpy(), want, 1e-12, 1e-15, alias)
     assert pn.core._lib.act_gelu(None, t._ptr) == pn.NeuralError.NULL_POINTER
+
+
+@pytest.mark.parametrize("name", ["tanh", "gelu", "mish", "softplus", "swish", "elu", "selu", "sigmoid"])
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_activation_dense_sweep(pn, ora, name, dt):
+    """Every region of the closed forms: a dense grid over [-40, 40] (the
+    cancellation tails of softplus/mish/gelu and the clamps of tanh included),
+    the branch points, and the special values."""
+    grid = np.linspace(-40.0, 40.0, 2_000_001)
+    pts = np.array([0.0, -0.0, 2.0 ** -7, -2.0 ** -7, 22.0, -22.0, 19.06, -19.06, 1e-30, -1e-30, 1e-40, -1e-40,
+                    88.7, -88.7, 103.9, -103.9, 709.78, 709.79, -745.2, 1e30, -1e30, 3.4e38, -3.4e38,
+                    np.inf, -np.inf, np.nan])
+    x = np.concatenate([grid, pts]).astype(dt)
+    got = _run(pn, name, x)
+    want = ora.act(name, x, ALPHA.get(name, 0.0))
+    if dt == np.float32:
+        rel_close(got, want, 1e-5, 0.0, name)
+    else:
+        rel_close(got, want, 1e-12, 1e-15, name)
+    z = (want == 0) & ~np.isnan(want)
+    assert np.array_equal(np.signbit(got[z]), np.signbit(want[z])), f"{name}: sign of zero differs"
