@@ -148,6 +148,43 @@ NH_DEV T wave_max_ignore_nan(T v)
     return v;
 }
 
+// DPP-based wave64 all-reductions: quad xor-1 / xor-2 swaps, half-row and row
+// mirrors make every 16-lane row uniform in four VALU steps, then two lane
+// swizzles across rows (xor 16, xor 32).  Fixed pairing: deterministic, and
+// every lane ends with the same value.
+template <int CTRL>
+NH_DEV int dpp_i(int v) { return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true); }
+template <int CTRL>
+NH_DEV float dpp_f(float v) { return __int_as_float(dpp_i<CTRL>(__float_as_int(v))); }
+template <int CTRL>
+NH_DEV double dpp_d(double v)
+{
+    const long long b = __double_as_longlong(v);
+    const int lo = dpp_i<CTRL>(int(b)), hi = dpp_i<CTRL>(int(b >> 32));
+    return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<unsigned int>(lo));
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+NH_DEV float wave_fmax(float v)  // NaN-ignoring max over the wave
+{
+    v = __builtin_fmaxf(v, dpp_f<kDppXor1>(v));
+    v = __builtin_fmaxf(v, dpp_f<kDppXor2>(v));
+    v = __builtin_fmaxf(v, dpp_f<kDppHalfMirror>(v));
+    v = __builtin_fmaxf(v, dpp_f<kDppMirror>(v));
+    v = __builtin_fmaxf(v, __shfl_xor(v, 16, 64));
+    return __builtin_fmaxf(v, __shfl_xor(v, 32, 64));
+}
+
+NH_DEV double wave_dsum(double v)
+{
+    v += dpp_d<kDppXor1>(v);
+    v += dpp_d<kDppXor2>(v);
+    v += dpp_d<kDppHalfMirror>(v);
+    v += dpp_d<kDppMirror>(v);
+    v += __shfl_xor(v, 16, 64);
+    return v + __shfl_xor(v, 32, 64);
+}
+
 // 128-bit vector types (clang ext vectors: element access by index, and
 // accepted by the non-temporal load/store builtins).
 typedef float f32x4 __attribute__((ext_vector_type(4)));

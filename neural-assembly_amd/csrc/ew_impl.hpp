@@ -184,36 +184,47 @@ __global__ __launch_bounds__(kBlock) void k_map1_f32_tail(const float *__restric
 }
 
 // ---- row broadcast: o[r, c] = op(a[r, c], b[c]) -----------------------------
-// The [rows, ncv]-vector array is cut into contiguous spans of kSpan vectors,
-// one per block, streamed like the flat kernel (tiles of 256 x U vectors,
-// loads before stores).  The lane's column vector index is found once by a
-// division and then advances by a fixed amount modulo the row width (d1 =
-// 256 mod ncv per unrolled vector, dU = 256*U mod ncv per tile), so the loop
-// has no division; the bias vector (a few KiB) is served from L1/L2.
-constexpr int64_t kSpan = 8192;
-
-template <typename T, typename Op>
+// The [rows, ncv]-vector array is streamed like the flat kernel: grid-stride
+// over tiles of 256 x U vectors, loads before stores.  A lane's column vector
+// index is found once by a division and then advances by fixed amounts modulo
+// the row width (d1 = 256 mod ncv per unrolled vector, dS = grid stride mod ncv
+// per tile), so the loop has no division; the bias vector (a few KiB) is
+// served from L1/L2.
+template <typename T, typename Op, bool FIXED>
 __global__ __launch_bounds__(kBlock) void k_rowbcast(const T *__restrict__ a, const T *__restrict__ b,
                                                      T *__restrict__ o, int64_t nv, int64_t ncv, int64_t d1,
-                                                     int64_t dU, Op op)
+                                                     int64_t dS, Op op)
 {
+    // FIXED: dS == 0, so a lane meets the same U bias vectors on every tile;
+    // they are loaded once, before the loop.
     using V = typename Vec16<T>::type;
     constexpr int VN = Vec16<T>::n;
     const V *av = reinterpret_cast<const V *>(a);
     const V *bv = reinterpret_cast<const V *>(b);
     V *ov = reinterpret_cast<V *>(o);
-    const int64_t s0 = int64_t(blockIdx.x) * kSpan;
-    const int64_t end = s0 + kSpan < nv ? s0 + kSpan : nv;
-    int64_t c = (s0 + threadIdx.x) % ncv;
-    for (int64_t base = s0 + threadIdx.x; base < end; base += int64_t(kBlock) * kUnroll) {
-        V ra[kUnroll], rb[kUnroll];
+    const int64_t tile = int64_t(kBlock) * kUnroll;
+    const int64_t stride = int64_t(gridDim.x) * tile;
+    int64_t base = int64_t(blockIdx.x) * tile + threadIdx.x;
+    int64_t c = base % ncv;
+    V rb[kUnroll];
+    if (FIXED) {
+        int64_t cc = c;
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++) {
+            rb[u] = bv[cc];
+            cc += d1;
+            cc = cc >= ncv ? cc - ncv : cc;
+        }
+    }
+    for (; base < nv; base += stride) {
+        V ra[kUnroll];
         int64_t cc = c;
 #pragma unroll
         for (int u = 0; u < kUnroll; u++) {
             const int64_t i = base + int64_t(u) * kBlock;
-            if (i < end) {
+            if (i < nv) {
                 ra[u] = ld_nt(av + i);
-                rb[u] = bv[cc];
+                if (!FIXED) rb[u] = bv[cc];
             }
             cc += d1;
             cc = cc >= ncv ? cc - ncv : cc;
@@ -221,30 +232,18 @@ __global__ __launch_bounds__(kBlock) void k_rowbcast(const T *__restrict__ a, co
 #pragma unroll
         for (int u = 0; u < kUnroll; u++) {
             const int64_t i = base + int64_t(u) * kBlock;
-            if (i < end) {
+            if (i < nv) {
                 V res;
 #pragma unroll
                 for (int k = 0; k < VN; k++) res[k] = op(ra[u][k], rb[u][k]);
                 st_nt(ov + i, res);
             }
         }
-        c += dU;
+        c += dS;
         c = c >= ncv ? c - ncv : c;
     }
 }
 
-template <typename T, typename Op>
-int launch_rowbcast(const T *a, const T *b, T *o, int64_t rows, int64_t cols, Op op)
-{
-    const int64_t ncv = cols / Vec16<T>::n;
-    if (rows <= 0 || ncv <= 0) return NEURAL_OK;
-    const int64_t nv = rows * ncv;
-    const int64_t d1 = int64_t(kBlock) % ncv;
-    const int64_t dU = (int64_t(kBlock) * kUnroll) % ncv;
-    hipLaunchKernelGGL((k_rowbcast<T, Op>), dim3(unsigned(ceil_div(nv, kSpan))), dim3(kBlock), 0, stream(), a, b, o,
-                       nv, ncv, d1, dU, op);
-    return check_launch();
-}
 
 // ---- N-D strided / broadcast (<= 4 dims, element strides) --------------------
 struct ND4 {
@@ -306,6 +305,24 @@ inline unsigned strided_grid(int64_t n)
     const int64_t cap = int64_t(num_cus()) * 16;
     if (g > cap) g = cap;
     return unsigned(g < 1 ? 1 : g);
+}
+
+template <typename T, typename Op>
+int launch_rowbcast(const T *a, const T *b, T *o, int64_t rows, int64_t cols, Op op)
+{
+    constexpr int VN = Vec16<T>::n;
+    const int64_t ncv = cols / VN;
+    if (rows <= 0 || ncv <= 0) return NEURAL_OK;
+    const int64_t nv = rows * ncv;
+    const unsigned g = flat_grid(nv * VN, VN);
+    const int64_t d1 = int64_t(kBlock) % ncv;
+    const int64_t dS = (int64_t(g) * kBlock * kUnroll) % ncv;
+    if (dS == 0)
+        hipLaunchKernelGGL((k_rowbcast<T, Op, true>), dim3(g), dim3(kBlock), 0, stream(), a, b, o, nv, ncv, d1, dS, op);
+    else
+        hipLaunchKernelGGL((k_rowbcast<T, Op, false>), dim3(g), dim3(kBlock), 0, stream(), a, b, o, nv, ncv, d1, dS,
+                           op);
+    return check_launch();
 }
 
 template <typename T, typename Op>

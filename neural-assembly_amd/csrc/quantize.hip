@@ -26,9 +26,22 @@ NH_DEV int32_t x86_cvt_i32(double r)
     return int32_t(r);
 }
 
+// q = clamp((int32)round(x * inv) + zp, -128, 127) with the reference build's
+// x86 semantics.  For |x * inv| <= 2^30 (everything but NaN and huge
+// outliers) round() is trunc plus a +-1 step decided by the exact remainder,
+// and no int32 operation can overflow; otherwise cvttsd2si (INT32_MIN) and the
+// wrapping add are reproduced.
 NH_DEV int8_t quant_one(double x, double inv, int32_t zp)
 {
-    int32_t q = int32_t(uint32_t(x86_cvt_i32(round(x * inv))) + uint32_t(zp));
+    const double y = x * inv;
+    int32_t q;
+    if (__builtin_fabs(y) <= 0x1p30) {
+        const double t = __builtin_trunc(y);
+        const double d = y - t;  // exact
+        q = int32_t(t) + (d >= 0.5 ? 1 : 0) - (d <= -0.5 ? 1 : 0) + zp;
+    } else {
+        q = int32_t(uint32_t(x86_cvt_i32(round(y))) + uint32_t(zp));
+    }
     q = q < -128 ? -128 : q;
     q = q > 127 ? 127 : q;
     return int8_t(q);

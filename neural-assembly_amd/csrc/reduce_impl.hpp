@@ -155,7 +155,17 @@ NH_DEV typename Red::B ordered_combine(const Red &red, const typename Red::B *p,
     B s = red.bident();
     const int a = t * k;
     const int e = a + k < n ? a + k : n;
-    for (int i = a; i < e; i++) s = red.bcomb(s, p[i]);
+    // loads of a batch issued together (the fold is sequential, the loads not)
+    constexpr int kBatch = 4;
+    for (int i0 = a; i0 < e; i0 += kBatch) {
+        B buf[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; j++)
+            if (i0 + j < e) buf[j] = p[i0 + j];
+#pragma unroll
+        for (int j = 0; j < kBatch; j++)
+            if (i0 + j < e) s = red.bcomb(s, buf[j]);
+    }
     const int lane = t & 63;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {

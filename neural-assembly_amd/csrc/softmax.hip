@@ -6,8 +6,8 @@
 //   f32: m = row max; e_j = (float)exp((double)x_j - (double)m);
 //        s = sum of e_j; y_j = e_j / s
 //   f64: e_j = exp(x_j - m); y_j = e_j / s
-// Here the f32 e_j come from an exact split of x - m and the float exp (about
-// 1 ulp of float, see exp_diff_f32) and y_j = e_j * (1/s).
+// Here the f32 e_j come from the exact double difference x - m and the
+// hardware exp2 (about 1.5e-7 relative, see exp_diff_f32) and y_j = e_j * (1/s).
 // Log-softmax follows the formula of label_smoothing_ce_forward
 // (metrics_losses.c:47-64) in double: y = (x - m) - log(sum exp(x - m)),
 // rounded once for f32.
@@ -32,97 +32,101 @@ NH_DEV T neg_inf();
 template <> NH_DEV float neg_inf<float>() { return -__builtin_inff(); }
 template <> NH_DEV double neg_inf<double>() { return -__builtin_inf(); }
 
-// exp(x - m) for f32 rows, accurate to about 1 ulp of float: x - m is split
-// exactly into hi + lo (TwoSum), exp(hi) comes from the float exp and the
-// low part enters as exp(hi) * (1 + lo).  This matches the reference's
-// (float)exp((double)x - (double)m) to ~1e-7 relative at a fraction of the
-// cost of a double exp.  A non-finite hi (overflowing difference, or infinite
-// inputs) skips the correction so exp(-inf) stays 0.
-NH_DEV float exp_diff_f32(float x, float m)
+// exp(x - m) for f32 rows (x <= m, m the row max held in double): the
+// difference is exact in double; t = d * log2(e) = n + f with n = rint(t) and
+// |f| <= 1/2 exact; 2^f from the hardware exp2 of float(f) (~1 ulp), scaled by
+// 2^n.  About 1.5e-7 relative against (float)exp((double)x - (double)m) for
+// any spread of the row, at ~10 instructions.  t is clamped at -300 so that
+// exp(-inf) = 0; a NaN passes through (and makes the row's sum NaN, as in the
+// reference).
+NH_DEV float exp_diff_f32(float x, double md)
 {
-    const float nm = -m;
-    const float hi = x + nm;
-    const float bb = hi - x;
-    float lo = (x - (hi - bb)) + (nm - bb);
-    if (!(hi - hi == 0.0f)) lo = 0.0f;
-    const float e = expf(hi);
-    return __builtin_fmaf(e, lo, e);
+    double t = (double(x) - md) * 1.4426950408889634;
+    t = t < -300.0 ? -300.0 : t;
+    const double n = __builtin_rint(t);
+    const float e = __builtin_amdgcn_exp2f(float(t - n));
+    return __builtin_ldexpf(e, int(n));
 }
 
-template <bool LOG, int VPL>
-__global__ __launch_bounds__(kSmBlock) void k_softmax_wave_f32(const float *__restrict__ x, float *__restrict__ y,
-                                                               int64_t rows, int64_t cols)
+// One wave per row (RPW rows per wave: all loads of the wave's rows issued
+// before any arithmetic).
+template <bool LOG, int VPL, bool FULL>
+NH_DEV void softmax_row_f32(f32x4 (&v)[VPL], f32x4 *__restrict__ yr, int64_t ncv, int lane)
 {
-    using V = f32x4;
-    const int lane = threadIdx.x & 63;
-    const int64_t r = int64_t(blockIdx.x) * (kSmBlock / 64) + (threadIdx.x >> 6);
-    if (r >= rows) return;  // uniform per wave
-    const V *xr = reinterpret_cast<const V *>(x + r * cols);
-    V *yr = reinterpret_cast<V *>(y + r * cols);
-    const int64_t ncv = cols / 4;
-
-    V v[VPL];
-#pragma unroll
-    for (int k = 0; k < VPL; k++) {
-        const int64_t c = lane + int64_t(k) * 64;
-        if (c < ncv) v[k] = ld_nt(xr + c);
-    }
+    const auto in_row = [&](int k) { return FULL || lane + int64_t(k) * 64 < ncv; };
     float m = -__builtin_inff();
 #pragma unroll
     for (int k = 0; k < VPL; k++) {
-        const int64_t c = lane + int64_t(k) * 64;
-        if (c < ncv) {
+        if (in_row(k)) {
 #pragma unroll
-            for (int j = 0; j < 4; j++) m = v[k][j] > m ? v[k][j] : m;
+            for (int j = 0; j < 4; j++) m = __builtin_fmaxf(m, v[k][j]);
         }
     }
-    m = wave_max_ignore_nan(m);
-
+    const double md = double(wave_fmax(m));
     double s = 0.0;
     if (!LOG) {
         // e_j kept in the input registers, rounded to float as the reference does.
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
-            const int64_t c = lane + int64_t(k) * 64;
-            if (c < ncv) {
+            if (in_row(k)) {
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    const float e = exp_diff_f32(v[k][j], m);
+                    const float e = exp_diff_f32(v[k][j], md);
                     v[k][j] = e;
                     s += double(e);
                 }
             }
         }
-        s = wave_sum(s);
+        s = wave_dsum(s);
         const float rs = 1.0f / float(s);
 #pragma unroll
-        for (int k = 0; k < VPL; k++) {
-            const int64_t c = lane + int64_t(k) * 64;
-            if (c < ncv) st_nt(yr + c, v[k] * rs);
-        }
+        for (int k = 0; k < VPL; k++)
+            if (in_row(k)) st_nt(yr + lane + k * 64, v[k] * rs);
     } else {
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
-            const int64_t c = lane + int64_t(k) * 64;
-            if (c < ncv) {
+            if (in_row(k)) {
 #pragma unroll
-                for (int j = 0; j < 4; j++) s += double(exp_diff_f32(v[k][j], m));
+                for (int j = 0; j < 4; j++) s += double(exp_diff_f32(v[k][j], md));
             }
         }
-        s = wave_sum(s);
+        s = wave_dsum(s);
         const double lse = log(s);
-        const double md = double(m);
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
-            const int64_t c = lane + int64_t(k) * 64;
-            if (c < ncv) {
-                V o;
+            if (in_row(k)) {
+                f32x4 o;
 #pragma unroll
                 for (int j = 0; j < 4; j++) o[j] = float((double(v[k][j]) - md) - lse);
-                st_nt(yr + c, o);
+                st_nt(yr + lane + k * 64, o);
             }
         }
     }
+}
+
+template <bool LOG, int VPL, bool FULL, int RPW>
+__global__ __launch_bounds__(kSmBlock) void k_softmax_wave_f32(const float *__restrict__ x, float *__restrict__ y,
+                                                               int64_t rows, int64_t cols)
+{
+    using V = f32x4;
+    const int lane = threadIdx.x & 63;
+    const int64_t r0 = (int64_t(blockIdx.x) * (kSmBlock / 64) + (threadIdx.x >> 6)) * RPW;
+    if (r0 >= rows) return;  // uniform per wave
+    const int64_t ncv = cols / 4;
+    V v[RPW][VPL];
+#pragma unroll
+    for (int q = 0; q < RPW; q++) {
+        if (r0 + q < rows) {
+            const V *xr = reinterpret_cast<const V *>(x + (r0 + q) * cols);
+#pragma unroll
+            for (int k = 0; k < VPL; k++)
+                if (FULL || lane + int64_t(k) * 64 < ncv) v[q][k] = ld_nt(xr + lane + k * 64);
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < RPW; q++)
+        if (r0 + q < rows)
+            softmax_row_f32<LOG, VPL, FULL>(v[q], reinterpret_cast<V *>(y + (r0 + q) * cols), ncv, lane);
 }
 
 template <bool LOG, int VPL>
@@ -206,7 +210,7 @@ NH_DEV double block_sum(double v)
     return r;
 }
 
-NH_DEV float row_exp(float x, float m) { return exp_diff_f32(x, m); }
+NH_DEV float row_exp(float x, float m) { return exp_diff_f32(x, double(m)); }
 NH_DEV double row_exp(double x, double m) { return exp(x - m); }
 
 template <typename T, bool LOG>
@@ -233,10 +237,18 @@ __global__ __launch_bounds__(kSmBlock) void k_softmax_block(const T *__restrict_
 template <typename T, bool LOG, int VPL>
 static void launch_wave(const T *x, T *y, int64_t rows, int64_t cols, unsigned g)
 {
-    if constexpr (sizeof(T) == 4)
-        hipLaunchKernelGGL((k_softmax_wave_f32<LOG, VPL>), dim3(g), dim3(kSmBlock), 0, stream(), x, y, rows, cols);
-    else
+    if constexpr (sizeof(T) == 4) {
+        if (cols == int64_t(VPL) * 256) {
+            // (two rows per wave measured slower on MI355X: 89.7 vs 86.2 us at [65536,1024])
+            hipLaunchKernelGGL((k_softmax_wave_f32<LOG, VPL, true, 1>), dim3(g), dim3(kSmBlock), 0, stream(), x, y,
+                               rows, cols);
+        } else {
+            hipLaunchKernelGGL((k_softmax_wave_f32<LOG, VPL, false, 1>), dim3(g), dim3(kSmBlock), 0, stream(), x, y,
+                               rows, cols);
+        }
+    } else {
         hipLaunchKernelGGL((k_softmax_wave_f64<LOG, VPL>), dim3(g), dim3(kSmBlock), 0, stream(), x, y, rows, cols);
+    }
 }
 
 template <typename T, bool LOG>
