@@ -139,16 +139,6 @@ NH_DEV double mish_d(double x)
 // Inputs of magnitude below 2^-30 (where outputs can be denormal, so a second
 // rounding would show) take the double formula's linear term exactly.
 
-// exp(y) for a double y to ~1e-7 relative from the float exp: y = hi + lo
-// exactly split, exp(y) = expf(hi) * (1 + lo) (an infinite hi has no low part).
-NH_DEV float exp_split(double y)
-{
-    const float hi = float(y);
-    const float lo = (hi - hi == 0.0f) ? float(y - double(hi)) : 0.0f;  // +-inf / NaN: no low part
-    const float e = expf(hi);
-    return __builtin_fmaf(e, lo, e);
-}
-
 NH_DEV float rcp_f32(float a) { return __builtin_amdgcn_rcpf(a); }  // 1 ulp, a in [1, 2^126)
 
 // log(1 + e) for e in [0, 1] in float: 2 atanh(s), s = e / (2 + e) <= 1/3, odd
@@ -177,7 +167,7 @@ struct GeluF32 {
         const double x = double(xf);
         const double z = kGelu * (x + 0.044715 * x * x * x);
         need = z < -10.5;  // 1 + tanh(z) < 1.5e-9: a small multiple of 2^-53 in the reference
-        const float w = exp_split(-2.0 * __builtin_fabs(z));
+        const float w = exp_d2f(-2.0 * __builtin_fabs(z));
         const float r = rcp_f32(1.0f + w);
         const float onept = z >= 0.0 ? 2.0f * r : (w + w) * r;
         return (0.5f * xf) * onept;

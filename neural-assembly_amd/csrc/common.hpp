@@ -82,6 +82,7 @@ struct Workspace {
     void         *partials;    // kMaxPartials * 64 bytes
     unsigned int *counter;     // kCounters counters, all zero between calls
     void         *result;      // 256 bytes of small results
+    void         *host_result; // 256 bytes of pinned host memory: landing area for result_to_host
 };
 constexpr int kMaxPartials = 16384;
 constexpr int kCounters = 1024;
@@ -119,6 +120,9 @@ int          dev_written(NeuralTensor *t);
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 int          check_launch();                         // hipGetLastError -> error code
 int          sync();                                 // synchronise the active stream
+// Copy `bytes` (<= 256) of a device result to `dst` (host): one D2H copy into
+// the pinned landing area, a stream sync, then a host memcpy.
+int          result_to_host(void *dst, const void *dev_src, size_t bytes);
 
 }  // namespace nh
 
@@ -183,6 +187,19 @@ NH_DEV double wave_dsum(double v)
     v += dpp_d<kDppMirror>(v);
     v += __shfl_xor(v, 16, 64);
     return v + __shfl_xor(v, 32, 64);
+}
+
+// e^y as a float for a double argument y <= ~88.7: t = y * log2(e) = n + f with
+// n = rint(t) and |f| <= 1/2 exact, 2^f from the hardware exp2 of float(f)
+// (about 1 ulp), scaled by 2^n with ldexp (exact, or correctly rounded into
+// the denormal range).  About 1.5e-7 relative in ~7 instructions.  t is clamped
+// at -300 so exp(-inf) = 0; a NaN passes through.
+NH_DEV float exp_d2f(double y)
+{
+    double t = y * 1.4426950408889634;
+    t = t < -300.0 ? -300.0 : t;
+    const double n = __builtin_rint(t);
+    return __builtin_ldexpf(__builtin_amdgcn_exp2f(float(t - n)), int(n));
 }
 
 // 128-bit vector types (clang ext vectors: element access by index, and

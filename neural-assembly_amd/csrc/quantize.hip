@@ -340,9 +340,8 @@ static int calibrate(const T *data, int64_t n, int symmetric, QuantParams *out, 
     red.symmetric = symmetric ? 1 : 0;
     void *res = out_on_device ? static_cast<void *>(out) : workspace().result;
     if (launch_reduce_full(static_cast<const T *>(s.dev), n, red, res) != NEURAL_OK) return -1;
-    if (!out_on_device && hipMemcpyAsync(out, res, sizeof(QuantParams), hipMemcpyDeviceToHost, stream()) != hipSuccess)
-        return -1;
-    if (s.finish(false) != NEURAL_OK || (!out_on_device && sync() != NEURAL_OK)) return -1;
+    if (!out_on_device && result_to_host(out, res, sizeof(QuantParams)) != NEURAL_OK) return -1;
+    if (s.finish(false) != NEURAL_OK) return -1;
     set_error(NEURAL_OK);
     return 0;
 }
@@ -394,8 +393,8 @@ static int qerr(const T *data, int64_t n, const QuantParams *p, double *sig, dou
     QErrOut st;
     void *res = workspace().result;
     if (launch_reduce_full(static_cast<const T *>(s.dev), n, red, res) != NEURAL_OK) return -1;
-    if (hipMemcpyAsync(&st, res, sizeof(st), hipMemcpyDeviceToHost, stream()) != hipSuccess) return -1;
-    if (s.finish(false) != NEURAL_OK || sync() != NEURAL_OK) return -1;
+    if (result_to_host(&st, res, sizeof(st)) != NEURAL_OK) return -1;
+    if (s.finish(false) != NEURAL_OK) return -1;
     *sig = st.sig;
     *noise = st.noise;
     set_error(NEURAL_OK);

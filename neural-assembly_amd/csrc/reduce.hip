@@ -222,9 +222,7 @@ static int full_to_host(const NeuralTensor *t, Out *host_out)
         NH_TRY(launch_reduce_full(static_cast<const float *>(c.p), n, RedOf<float>{}, res));
     else
         NH_TRY(launch_reduce_full(static_cast<const double *>(c.p), n, RedOf<double>{}, res));
-    NH_HIP(hipMemcpyAsync(host_out, res, sizeof(Out), hipMemcpyDeviceToHost, stream()));
-    NH_TRY(sync());
-    return NEURAL_OK;
+    return result_to_host(host_out, res, sizeof(Out));
 }
 
 template <typename T> using SumF64 = RedSum<T, SUM_OUT_F64>;
@@ -402,8 +400,7 @@ float simd_sum_f32(const float *a, uint64_t n)
     double s = 0.0;
     if (launch_reduce_full(static_cast<const float *>(sa.dev), int64_t(n), SumF64<float>{}, res) != NEURAL_OK)
         return 0.0f;
-    if (hipMemcpyAsync(&s, res, sizeof(s), hipMemcpyDeviceToHost, stream()) != hipSuccess || sync() != NEURAL_OK)
-        return 0.0f;
+    if (result_to_host(&s, res, sizeof(s)) != NEURAL_OK) return 0.0f;
     set_error(NEURAL_OK);
     return float(s);
 }
@@ -454,9 +451,7 @@ extern "C" float simd_dot_f32(const float *a, const float *b, uint64_t n)
                        static_cast<const float *>(sb.dev), int64_t(n), static_cast<double *>(ws.partials), ws.counter,
                        static_cast<double *>(ws.result));
     double s = 0.0;
-    if (check_launch() != NEURAL_OK ||
-        hipMemcpyAsync(&s, ws.result, sizeof(s), hipMemcpyDeviceToHost, stream()) != hipSuccess || sync() != NEURAL_OK)
-        return 0.0f;
+    if (check_launch() != NEURAL_OK || result_to_host(&s, ws.result, sizeof(s)) != NEURAL_OK) return 0.0f;
     set_error(NEURAL_OK);
     return float(s);
 }

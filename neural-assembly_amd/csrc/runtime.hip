@@ -108,6 +108,7 @@ int ensure_init()
             if (hipMalloc(&r.ws.partials, size_t(kMaxPartials) * 64) != hipSuccess ||
                 hipMalloc((void **)&r.ws.counter, sizeof(unsigned) * kCounters) != hipSuccess ||
                 hipMalloc(&r.ws.result, 256) != hipSuccess ||
+                hipHostMalloc(&r.ws.host_result, 256, hipHostMallocDefault) != hipSuccess ||
                 hipMemset(r.ws.counter, 0, sizeof(unsigned) * kCounters) != hipSuccess ||
                 hipDeviceSynchronize() != hipSuccess) {
                 r.init_rc = NEURAL_ERR_OUT_OF_MEMORY;
@@ -190,6 +191,16 @@ int check_launch()
 int sync()
 {
     NH_HIP(hipStreamSynchronize(stream()));
+    return NEURAL_OK;
+}
+
+int result_to_host(void *dst, const void *dev_src, size_t bytes)
+{
+    Workspace &ws = workspace();
+    if (bytes > 256) return set_error(NEURAL_ERR_INTERNAL);
+    NH_HIP(hipMemcpyAsync(ws.host_result, dev_src, bytes, hipMemcpyDeviceToHost, stream()));
+    NH_TRY(sync());
+    std::memcpy(dst, ws.host_result, bytes);
     return NEURAL_OK;
 }
 

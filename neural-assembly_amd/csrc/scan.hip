@@ -49,9 +49,7 @@ static int scan_dev(const T *x, int64_t n, ScanOut *st)
 {
     void *res = workspace().result;
     NH_TRY(launch_reduce_full(x, n, RedScan<T>{}, res));
-    NH_HIP(hipMemcpyAsync(st, res, sizeof(*st), hipMemcpyDeviceToHost, stream()));
-    NH_TRY(sync());
-    return NEURAL_OK;
+    return result_to_host(st, res, sizeof(*st));
 }
 
 static int scan_raw(const float *data, uint64_t n, ScanOut *st)

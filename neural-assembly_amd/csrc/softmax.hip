@@ -33,20 +33,10 @@ template <> NH_DEV float neg_inf<float>() { return -__builtin_inff(); }
 template <> NH_DEV double neg_inf<double>() { return -__builtin_inf(); }
 
 // exp(x - m) for f32 rows (x <= m, m the row max held in double): the
-// difference is exact in double; t = d * log2(e) = n + f with n = rint(t) and
-// |f| <= 1/2 exact; 2^f from the hardware exp2 of float(f) (~1 ulp), scaled by
-// 2^n.  About 1.5e-7 relative against (float)exp((double)x - (double)m) for
-// any spread of the row, at ~10 instructions.  t is clamped at -300 so that
-// exp(-inf) = 0; a NaN passes through (and makes the row's sum NaN, as in the
-// reference).
-NH_DEV float exp_diff_f32(float x, double md)
-{
-    double t = (double(x) - md) * 1.4426950408889634;
-    t = t < -300.0 ? -300.0 : t;
-    const double n = __builtin_rint(t);
-    const float e = __builtin_amdgcn_exp2f(float(t - n));
-    return __builtin_ldexpf(e, int(n));
-}
+// difference is exact in double, so exp_d2f gives about 1.5e-7 relative
+// against (float)exp((double)x - (double)m) for any spread of the row.  A NaN
+// passes through and makes the row's sum NaN, as in the reference.
+NH_DEV float exp_diff_f32(float x, double md) { return exp_d2f(double(x) - md); }
 
 // One wave per row (RPW rows per wave: all loads of the wave's rows issued
 // before any arithmetic).
