@@ -11,9 +11,13 @@ achieved HBM bandwidth: algorithmic bytes (each input read once, each output
 written once) divided by the step time.
 
 Prints ONE JSON line (the driver contract) with a roofline object for the
-dominant kernel (row softmax on [65536,1024], timed live with HIP events on
-the launch stream) and a cpu_baseline object (the oracle's C restatement of
-the same step, single-threaded, on this host).
+dominant kernel (row softmax on [65536,1024], each launch inside the timed
+steps bracketed by HIP events on the launch stream; these read ~5% above the
+kernel trace's durations for the same launches, so `achieved` is
+conservative.  A back-to-back figure after the timed region is reported
+beside it; it is helped by the 256 MB Infinity Cache re-serving the input)
+and a cpu_baseline object (the oracle's C restatement of the same step,
+single-threaded, on this host).
 
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--suite]   (--suite: per-kernel table on stderr)
 """
@@ -112,7 +116,7 @@ def main():
         _check_error(_lib.neural_reduce_max(T["Y"]._ptr, 1, T["rmax"]._ptr), "row max")
         _check_error(_lib.neural_reduce_argmax(T["Y"]._ptr, 1, ctypes.c_void_p(ridx.data_ptr())), "row argmax")
         if record:
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0, e1 = ev_pairs[len(sm_times)]
             e0.record(stream)
         _check_error(_lib.neural_softmax(T["P"]._ptr, T["S"]._ptr), "softmax")
         if record:
@@ -120,6 +124,9 @@ def main():
             sm_times.append((e0, e1))
         _check_error(_lib.neural_log_softmax(T["L"]._ptr, T["S"]._ptr), "log_softmax")
 
+    # Event pairs for the roofline kernel, created before the timed region.
+    ev_pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                for _ in range(args.steps)]
     for _ in range(args.warmup):
         step(False)
     torch.cuda.synchronize()
@@ -132,6 +139,16 @@ def main():
     torch.cuda.synchronize()
     ms_per_step = t0.elapsed_time(t1) / args.steps
     sm_ms = statistics.mean(a.elapsed_time(c) for a, c in sm_times)
+    # The same kernel launched back to back (no event between launches), so the
+    # per-launch dispatch latency that the bracketing events above include is
+    # hidden: this is the kernel duration a kernel trace reports.
+    b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    b0.record(stream)
+    for _ in range(args.steps):
+        _check_error(_lib.neural_softmax(T["P"]._ptr, T["S"]._ptr), "softmax")
+    b1.record(stream)
+    torch.cuda.synchronize()
+    sm_b2b_ms = b0.elapsed_time(b1) / args.steps
 
     n1, n2 = ROWS * COLS, SROWS * SCOLS
     step_bytes = (2 * n1 * 4 + COLS * 4) + 3 * (n1 * 4 + ROWS * 4) + (n1 * 4 + ROWS * 8) + 2 * (2 * n2 * 4)
@@ -160,7 +177,7 @@ def main():
             "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 1),
         },
         "roofline": {
-            "kernel": "k_softmax_wave<float,false,4> (neural_softmax [65536,1024] f32)",
+            "kernel": "k_softmax_wave_f32<false,4,true,1> (neural_softmax [65536,1024] f32)",
             "bound": "hbm",
             "achieved": round(sm_gbs, 1),
             "peak": HBM_PEAK_GBS,
@@ -169,6 +186,8 @@ def main():
             "traffic": traffic_from_profile(),
             "avg_launch_us": round(sm_ms * 1e3, 2),
             "algorithmic_bytes": sm_bytes,
+            "backtoback_us": round(sm_b2b_ms * 1e3, 2),
+            "achieved_backtoback": round(sm_bytes / (sm_b2b_ms * 1e-3) / 1e9, 1),
         },
         "cpu_baseline": cpu,
     }
