@@ -255,6 +255,34 @@ int tensor_pad_2d(const double *in, int64_t in_rows, int64_t in_cols, int64_t pa
                   double *out, int64_t *out_rows, int64_t *out_cols);
 int tensor_transpose2d_array(const double *in, int64_t rows, int64_t cols, double *out);
 
+/* ---- Cross-entropy losses --------------------------------------------------------- */
+/* Label-smoothed cross-entropy (replaces metrics_losses.c:28-125, declared at
+ * neural_api.h:1101-1106): f64 logits [batch, num_classes], int64 targets;
+ * smoothed target (1 - a) * one_hot + a / K; loss_out = mean over rows of
+ * -sum_c target_c * log_softmax_c; grad_out = (softmax - target) / batch.
+ * Pointers may be host or device memory.  Returns 0, or -1 on NULL, batch or
+ * num_classes <= 0, smoothing outside [0, 1], or a target outside [0, K). */
+int label_smoothing_ce_forward(const double *logits, const int64_t *targets, int64_t batch_size,
+                               int64_t num_classes, double smoothing, double *loss_out);
+int label_smoothing_ce_backward(const double *logits, const int64_t *targets, int64_t batch_size,
+                                int64_t num_classes, double smoothing, double *grad_out);
+/* NEW: forward and backward in one pass over the logits (same results as the
+ * two calls above). */
+int label_smoothing_ce_fused(const double *logits, const int64_t *targets, int64_t batch_size,
+                             int64_t num_classes, double smoothing, double *loss_out, double *grad_out);
+/* NEW: the same on f32 logits (widened exactly to double, as the reference's
+ * f32 paths do), gradient rounded to float. */
+int label_smoothing_ce_fused_f32(const float *logits, const int64_t *targets, int64_t batch_size,
+                                 int64_t num_classes, double smoothing, double *loss_out, float *grad_out);
+/* Cross-entropy of softmax(prediction) (replaces neural_api.h:674,
+ * neural_api.asm:2546 -> losses.asm:315-613, intended semantics): prediction
+ * [batch, K], target [batch] holding class indices as values of the same
+ * dtype (truncated); *loss = mean over rows of -log(softmax[target] + 1e-7).
+ * NULL_POINTER / DTYPE_MISMATCH / DIM_MISMATCH (prediction not 2-D) /
+ * SHAPE_MISMATCH (target numel != batch) / INVALID_ARGUMENT (target out of
+ * range, or non-contiguous tensors). */
+int neural_cross_entropy_loss(const NeuralTensor *prediction, const NeuralTensor *target, double *loss);
+
 /* ---- HIP runtime controls (NEW) ------------------------------------------------- */
 /* Use an existing HIP stream (e.g. torch.cuda.current_stream().cuda_stream) for
  * all later launches; NULL selects the HIP null stream.  The previous stream

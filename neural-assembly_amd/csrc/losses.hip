@@ -1,0 +1,362 @@
+// losses.hip -- cross-entropy losses: label-smoothed CE forward / backward and
+// a fused forward+backward, and the tensor cross-entropy loss.
+//
+// Reference: metrics_losses.c:28-125 (label_smoothing_ce_forward/backward,
+// f64 logits, int64 targets):
+//   m = max (strict compare from row[0]); lse = log(sum_c exp(x_c - m));
+//   st_c = a/K + (c == t ? 1 - a : 0); loss_row = -sum_c st_c * ((x_c - m) - lse);
+//   loss = sum_rows / B;   grad_c = (1/B) * (exp(x_c - m) / sum - st_c)
+// and losses.asm:315-613 (cross_entropy_loss, intended semantics -- the C-ABI
+// wrapper neural_api.asm:2546-2568 passes a Tensor* where a Node* is expected
+// and never writes *loss): softmax per row, target index = truncation of the
+// target tensor's value, loss = mean_rows(-log(p_target + 1e-7)); f32 rows
+// keep the float roundings of e_j, of p_t and of each row's loss.
+//
+// One wave per row with the row in VGPRs (one HBM read; the gradient written
+// once), rows wider than the register budget take a block per row with three
+// passes.  Per-row losses land in a double buffer and are summed by the
+// segmented reduction (fixed order, deterministic); the row sums of exp use a
+// fixed wave tree instead of the reference's sequential order, so losses
+// agree to a few ulps of the row terms, not bit for bit.  An invalid target
+// sets a device flag and the call returns -1 (C API) / INVALID_ARGUMENT.
+#include <cmath>
+
+#include "reduce_impl.hpp"
+
+namespace nh {
+
+enum { CE_LS_FWD = 1, CE_LS_BWD = 2, CE_LS_FUSED = 3, CE_ASM = 4 };
+
+template <typename T>
+NH_DEV bool loss_target(const int64_t *ti, const T *tv, int64_t r, int64_t cols, int64_t &t)
+{
+    if (ti) {
+        t = ti[r];
+        return t >= 0 && t < cols;
+    }
+    const T v = tv[r];
+    if (!(v > T(-1) && v < T(cols))) return false;  // NaN fails too
+    t = int64_t(v);                                  // truncation (cvttss2si / cvttsd2si)
+    return true;
+}
+
+// e = exp(x - m) for one element: double exp for f64 rows, float-accurate for
+// f32 rows (the reference widens f32 exactly and rounds e to float).
+NH_DEV double row_exp_d(double x, double m) { return exp(x - m); }
+NH_DEV double row_exp_f(float x, double m) { return double(exp_d2f(double(x) - m)); }
+
+struct CeArgs {
+    const int64_t *tidx;   // int64 targets (label-smoothed API) or null
+    const void *tval;      // target values of the logits' dtype (tensor API) or null
+    int64_t rows, cols;
+    double alpha, inv_n;
+    double *row_loss;      // [rows] or null
+    void *grad;            // [rows, cols] or null
+    int *bad;              // set to 1 when a target is out of range
+};
+
+// Per-element work once m, s (and lse) are known.  Returns the element's loss
+// term (label-smoothed: st * log_soft) and writes the gradient element.
+template <typename T, int MODE>
+NH_DEV double ce_elem(T xv, int64_t c, int64_t t, double m, double lse, double rs, const CeArgs &a, T &g)
+{
+    const double x = double(xv);
+    const double st = a.alpha / double(a.cols) + (c == t ? 1.0 - a.alpha : 0.0);
+    double term = 0.0;
+    if (MODE == CE_LS_FWD || MODE == CE_LS_FUSED) term = st * ((x - m) - lse);
+    if (MODE == CE_LS_BWD || MODE == CE_LS_FUSED) {
+        const double e = sizeof(T) == 8 ? row_exp_d(x, m) : row_exp_f(float(xv), m);
+        g = T(a.inv_n * (e * rs - st));
+    }
+    return term;
+}
+
+template <typename T>
+NH_DEV double wave_fmax_t(T v);
+template <> NH_DEV double wave_fmax_t<float>(float v) { return double(wave_fmax(v)); }
+template <> NH_DEV double wave_fmax_t<double>(double v)
+{
+    return Grp<64>::reduce(v, [](double a, double b) { return __builtin_fmax(a, b); });
+}
+
+// One wave per row, VPL 16-byte vectors per lane (<= 64 * VPL * VN values).
+template <typename T, int VPL, int MODE>
+__global__ __launch_bounds__(256) void k_ce_wave(const T *__restrict__ x, CeArgs a, bool vec)
+{
+    using V = typename Vec16<T>::type;
+    constexpr int VN = Vec16<T>::n;
+    const int lane = threadIdx.x & 63;
+    const int64_t r = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (r >= a.rows) return;  // uniform per wave
+    const int64_t cols = a.cols;
+    const T *xr = x + r * cols;
+    V v[VPL];
+#pragma unroll
+    for (int k = 0; k < VPL; k++) {
+        const int64_t c0 = (int64_t(k) * 64 + lane) * VN;
+        if (vec) {
+            if (c0 < cols) v[k] = ld_nt(reinterpret_cast<const V *>(xr + c0));
+        } else {
+#pragma unroll
+            for (int j = 0; j < VN; j++)
+                if (c0 + j < cols) v[k][j] = xr[c0 + j];
+        }
+    }
+    T mx = -inf_t<T>();
+#pragma unroll
+    for (int k = 0; k < VPL; k++) {
+        const int64_t c0 = (int64_t(k) * 64 + lane) * VN;
+#pragma unroll
+        for (int j = 0; j < VN; j++)
+            if (c0 + j < cols) mx = fmax_nn(mx, v[k][j]);
+    }
+    const double m = wave_fmax_t<T>(mx);
+    double s = 0.0;
+#pragma unroll
+    for (int k = 0; k < VPL; k++) {
+        const int64_t c0 = (int64_t(k) * 64 + lane) * VN;
+#pragma unroll
+        for (int j = 0; j < VN; j++)
+            if (c0 + j < cols) s += sizeof(T) == 8 ? row_exp_d(double(v[k][j]), m) : row_exp_f(float(v[k][j]), m);
+    }
+    s = wave_dsum(s);
+    int64_t t = 0;
+    const bool ok = loss_target(a.tidx, static_cast<const T *>(a.tval), r, cols, t);
+    if (!ok) {
+        if (lane == 0) {
+            __hip_atomic_store(a.bad, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (a.row_loss) a.row_loss[r] = __builtin_nan("");
+        }
+        return;
+    }
+    if (MODE == CE_ASM) {
+        // p_t = e_t / sum; loss = -log(p_t + 1e-7) (f32: e_t, sum, p_t and the loss rounded to float)
+        if (lane == 0) {
+            double lt;
+            if (sizeof(T) == 4) {
+                const float et = exp_d2f(double(xr[t]) - m);
+                const float p = et / float(s);
+                lt = double(float(-log(double(p) + 1e-7)));
+            } else {
+                lt = -log(row_exp_d(double(xr[t]), m) / s + 1e-7);
+            }
+            a.row_loss[r] = lt;
+        }
+        return;
+    }
+    const double lse = log(s);
+    const double rs = 1.0 / s;
+    double acc = 0.0;
+    T *gr = static_cast<T *>(a.grad) + r * cols;
+#pragma unroll
+    for (int k = 0; k < VPL; k++) {
+        const int64_t c0 = (int64_t(k) * 64 + lane) * VN;
+        V g;
+#pragma unroll
+        for (int j = 0; j < VN; j++)
+            if (c0 + j < cols) {
+                T gj = T(0);
+                acc += ce_elem<T, MODE>(v[k][j], c0 + j, t, m, lse, rs, a, gj);
+                g[j] = gj;
+            }
+        if (MODE == CE_LS_BWD || MODE == CE_LS_FUSED) {
+            if (vec) {
+                if (c0 < cols) st_nt(reinterpret_cast<V *>(gr + c0), g);
+            } else {
+#pragma unroll
+                for (int j = 0; j < VN; j++)
+                    if (c0 + j < cols) gr[c0 + j] = g[j];
+            }
+        }
+    }
+    if (MODE == CE_LS_FWD || MODE == CE_LS_FUSED) {
+        acc = wave_dsum(acc);
+        if (lane == 0) a.row_loss[r] = -acc;
+    }
+}
+
+// Block per row (any width): max, sum of exp, then the outputs, each a pass
+// over the row.
+template <typename T, int MODE>
+__global__ __launch_bounds__(256) void k_ce_block(const T *__restrict__ x, CeArgs a)
+{
+    using G = Grp<256>;
+    const int64_t r = blockIdx.x;
+    const int64_t cols = a.cols;
+    const T *xr = x + r * cols;
+    T mx = -inf_t<T>();
+    for (int64_t c = threadIdx.x; c < cols; c += 256) mx = fmax_nn(mx, xr[c]);
+    const double m = double(G::reduce(mx, [](T p, T q) { return fmax_nn(p, q); }));
+    double s = 0.0;
+    for (int64_t c = threadIdx.x; c < cols; c += 256)
+        s += sizeof(T) == 8 ? row_exp_d(double(xr[c]), m) : row_exp_f(float(xr[c]), m);
+    s = G::reduce(s, [](double p, double q) { return p + q; });
+    int64_t t = 0;
+    const bool ok = loss_target(a.tidx, static_cast<const T *>(a.tval), r, cols, t);
+    if (!ok) {
+        if (threadIdx.x == 0) {
+            __hip_atomic_store(a.bad, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (a.row_loss) a.row_loss[r] = __builtin_nan("");
+        }
+        return;
+    }
+    if (MODE == CE_ASM) {
+        if (threadIdx.x == 0) {
+            double lt;
+            if (sizeof(T) == 4) {
+                const float et = exp_d2f(double(xr[t]) - m);
+                const float p = et / float(s);
+                lt = double(float(-log(double(p) + 1e-7)));
+            } else {
+                lt = -log(row_exp_d(double(xr[t]), m) / s + 1e-7);
+            }
+            a.row_loss[r] = lt;
+        }
+        return;
+    }
+    const double lse = log(s);
+    const double rs = 1.0 / s;
+    double acc = 0.0;
+    T *gr = static_cast<T *>(a.grad) + r * cols;
+    for (int64_t c = threadIdx.x; c < cols; c += 256) {
+        T g = T(0);
+        acc += ce_elem<T, MODE>(xr[c], c, t, m, lse, rs, a, g);
+        if (MODE == CE_LS_BWD || MODE == CE_LS_FUSED) gr[c] = g;
+    }
+    if (MODE == CE_LS_FWD || MODE == CE_LS_FUSED) {
+        acc = G::reduce(acc, [](double p, double q) { return p + q; });
+        if (threadIdx.x == 0) a.row_loss[r] = -acc;
+    }
+}
+
+template <typename T, int MODE, int VPL>
+static void launch_ce_wave(const T *x, const CeArgs &a, bool vec)
+{
+    hipLaunchKernelGGL((k_ce_wave<T, VPL, MODE>), dim3(unsigned(ceil_div(a.rows, 4))), dim3(256), 0, stream(), x, a,
+                       vec);
+}
+
+template <typename T, int MODE>
+static int launch_ce(const T *x, const CeArgs &a)
+{
+    constexpr int VN = Vec16<T>::n;
+    const bool vec = (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && a.cols % VN == 0 &&
+                     (!a.grad || (reinterpret_cast<uintptr_t>(a.grad) & 15u) == 0);
+    const int64_t per = ceil_div(a.cols, int64_t(64) * VN);  // vectors per lane
+    if (per <= 1) launch_ce_wave<T, MODE, 1>(x, a, vec);
+    else if (per <= 2) launch_ce_wave<T, MODE, 2>(x, a, vec);
+    else if (per <= 4) launch_ce_wave<T, MODE, 4>(x, a, vec);
+    else if (per <= 8) launch_ce_wave<T, MODE, 8>(x, a, vec);
+    else if (per <= 16) launch_ce_wave<T, MODE, 16>(x, a, vec);
+    else hipLaunchKernelGGL((k_ce_block<T, MODE>), dim3(unsigned(a.rows)), dim3(256), 0, stream(), x, a);
+    return check_launch();
+}
+
+// Runs MODE over [rows, cols] logits already on the device; sums the per-row
+// losses into *loss_host (mean over rows) when wanted.  Returns NEURAL_OK,
+// NEURAL_ERR_INVALID_ARGUMENT for a target out of range, or an error code.
+template <typename T, int MODE>
+static int ce_run(const T *x, const int64_t *tidx, const T *tval, int64_t rows, int64_t cols, double alpha,
+                  double *loss_host, T *grad_dev)
+{
+    Workspace &ws = workspace();
+    int *bad = static_cast<int *>(ws.result) + 32;  // flag word in the small-result area
+    NH_HIP(hipMemsetAsync(bad, 0, sizeof(int), stream()));
+    const bool want_loss = MODE != CE_LS_BWD;
+    double *row_loss = nullptr;
+    if (want_loss) {
+        row_loss = static_cast<double *>(dev_alloc(size_t(rows) * sizeof(double)));
+        if (!row_loss) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
+    }
+    CeArgs a{tidx, tval, rows, cols, alpha, 1.0 / double(rows), row_loss, grad_dev, bad};
+    int rc = launch_ce<T, MODE>(x, a);
+    if (rc == NEURAL_OK && want_loss) rc = launch_reduce_full(row_loss, rows, RedSum<double, SUM_OUT_F64>{}, ws.result);
+    struct { double sum; int pad[30]; int bad; } res;  // result area layout: sum at 0, flag at word 32
+    static_assert(sizeof(res) == 136, "");
+    if (rc == NEURAL_OK) rc = result_to_host(&res, ws.result, sizeof(res));
+    if (row_loss) dev_free(row_loss);
+    if (rc != NEURAL_OK) return rc;
+    if (res.bad) return NEURAL_ERR_INVALID_ARGUMENT;
+    if (want_loss && loss_host) *loss_host = res.sum / double(rows);
+    return NEURAL_OK;
+}
+
+// Raw-pointer label-smoothed CE (host or device pointers).
+template <typename T, int MODE>
+static int ls_ce(const T *logits, const int64_t *targets, int64_t batch, int64_t classes, double smoothing,
+                 double *loss_out, T *grad_out)
+{
+    if (ensure_init() != NEURAL_OK) return -1;
+    if (!logits || !targets) return -1;
+    if ((MODE != CE_LS_BWD && !loss_out) || (MODE != CE_LS_FWD && !grad_out)) return -1;
+    if (batch <= 0 || classes <= 0) return -1;
+    if (!(smoothing >= 0.0 && smoothing <= 1.0)) return -1;
+    const size_t n = size_t(batch) * size_t(classes);
+    Staged sx, st, sg;
+    if (sx.open(logits, n * sizeof(T), true) != NEURAL_OK || st.open(targets, size_t(batch) * 8, true) != NEURAL_OK)
+        return -1;
+    if (MODE != CE_LS_FWD && sg.open(grad_out, n * sizeof(T), false) != NEURAL_OK) return -1;
+    const int rc = ce_run<T, MODE>(static_cast<const T *>(sx.dev), static_cast<const int64_t *>(st.dev), nullptr,
+                                   batch, classes, smoothing, loss_out, static_cast<T *>(sg.dev));
+    if (rc != NEURAL_OK) return -1;
+    if (MODE != CE_LS_FWD && sg.finish(true) != NEURAL_OK) return -1;
+    set_error(NEURAL_OK);
+    return 0;
+}
+
+}  // namespace nh
+
+using namespace nh;
+
+extern "C" {
+
+int label_smoothing_ce_forward(const double *logits, const int64_t *targets, int64_t batch_size,
+                               int64_t num_classes, double smoothing, double *loss_out)
+{
+    return ls_ce<double, CE_LS_FWD>(logits, targets, batch_size, num_classes, smoothing, loss_out, nullptr);
+}
+
+int label_smoothing_ce_backward(const double *logits, const int64_t *targets, int64_t batch_size,
+                                int64_t num_classes, double smoothing, double *grad_out)
+{
+    return ls_ce<double, CE_LS_BWD>(logits, targets, batch_size, num_classes, smoothing, nullptr, grad_out);
+}
+
+int label_smoothing_ce_fused(const double *logits, const int64_t *targets, int64_t batch_size, int64_t num_classes,
+                             double smoothing, double *loss_out, double *grad_out)
+{
+    return ls_ce<double, CE_LS_FUSED>(logits, targets, batch_size, num_classes, smoothing, loss_out, grad_out);
+}
+
+int label_smoothing_ce_fused_f32(const float *logits, const int64_t *targets, int64_t batch_size,
+                                 int64_t num_classes, double smoothing, double *loss_out, float *grad_out)
+{
+    return ls_ce<float, CE_LS_FUSED>(logits, targets, batch_size, num_classes, smoothing, loss_out, grad_out);
+}
+
+int neural_cross_entropy_loss(const NeuralTensor *prediction, const NeuralTensor *target, double *loss)
+{
+    NH_TRY(ensure_init());
+    if (!prediction || !target || !loss) return set_error(NEURAL_ERR_NULL_POINTER);
+    NH_TRY(check_tensor(prediction));
+    NH_TRY(check_tensor(target));
+    if (prediction->dtype != target->dtype) return set_error(NEURAL_ERR_DTYPE_MISMATCH);
+    if (prediction->ndim != 2) return set_error(NEURAL_ERR_DIM_MISMATCH);
+    const int64_t rows = prediction->shape[0], cols = prediction->shape[1];
+    if (rows <= 0 || cols <= 0) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
+    if (numel(target) != rows) return set_error(NEURAL_ERR_SHAPE_MISMATCH);
+    if (!is_contiguous(prediction) || !is_contiguous(target)) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
+    const void *px = nullptr, *pt = nullptr;
+    NH_TRY(dev_read(prediction, &px));
+    NH_TRY(dev_read(target, &pt));
+    int rc;
+    if (prediction->dtype == NEURAL_DTYPE_FLOAT32)
+        rc = ce_run<float, CE_ASM>(static_cast<const float *>(px), nullptr, static_cast<const float *>(pt), rows, cols,
+                                   0.0, loss, nullptr);
+    else
+        rc = ce_run<double, CE_ASM>(static_cast<const double *>(px), nullptr, static_cast<const double *>(pt), rows,
+                                    cols, 0.0, loss, nullptr);
+    return set_error(rc);
+}
+
+}  // extern "C"

@@ -3,7 +3,8 @@ pyneural -- drop-in Python API for libneural_hip.so, the MI355X (gfx950)
 implementation of Neural-Assembly's tensor hot path.
 
 Public names follow the reference package for this path: Tensor, zeros,
-ones, tensor; nn.ReLU/Sigmoid/Softmax/Tanh; activations.*; Quantizer /
+ones, tensor; nn.ReLU/Sigmoid/Softmax/Tanh, nn.CrossEntropyLoss /
+LabelSmoothingCrossEntropy; activations.*; Quantizer /
 QuantParams; optim.SGD/Adam/AdamW; training.NaNDetector / grad_l2_norm;
 tensor_ops.*.
 """
@@ -12,7 +13,7 @@ from .core import (NeuralError, NeuralDtype, NeuralException, init, shutdown, ve
                    get_error_message, clear_error, set_stream, synchronize, device_info)
 from .tensor import Tensor, zeros, ones, tensor
 from . import nn, activations, optim, quantize, training, tensor_ops
-from .nn import ReLU, Sigmoid, Softmax, LogSoftmax, Tanh
+from .nn import ReLU, Sigmoid, Softmax, LogSoftmax, Tanh, CrossEntropyLoss, LabelSmoothingCrossEntropy
 from .activations import GELU, LeakyReLU, ELU, SELU, Swish, Mish, HardSwish, Softplus, HardTanh
 from .optim import SGD, Adam, AdamW
 from .quantize import Quantizer, QuantParams

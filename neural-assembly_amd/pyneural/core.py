@@ -254,6 +254,12 @@ _SIGS = {
     "tensor_split_2d": (_i, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64p, _i64p, _i64p, _i64p]),
     "tensor_pad_2d": (_i, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _d, _vp, _i64p, _i64p]),
     "tensor_transpose2d_array": (_i, [_vp, _i64, _i64, _vp]),
+    # cross-entropy losses
+    "label_smoothing_ce_forward": (_i, [_vp, _vp, _i64, _i64, _d, _dp]),
+    "label_smoothing_ce_backward": (_i, [_vp, _vp, _i64, _i64, _d, _vp]),
+    "label_smoothing_ce_fused": (_i, [_vp, _vp, _i64, _i64, _d, _dp, _vp]),
+    "label_smoothing_ce_fused_f32": (_i, [_vp, _vp, _i64, _i64, _d, _dp, _vp]),
+    "neural_cross_entropy_loss": (_i, [_vp, _vp, _dp]),
     # HIP runtime controls
     "neural_hip_set_stream": (_i, [_vp]),
     "neural_hip_reset_stream": (_i, []),

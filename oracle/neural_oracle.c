@@ -754,3 +754,116 @@ int ora_transpose_2d(const double *in, int64_t rows, int64_t cols, double *out)
         for (int64_t c = 0; c < cols; c++) out[c * rows + r] = in[r * cols + c];
     return 0;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Cross-entropy losses                                                     */
+/* ------------------------------------------------------------------------ */
+
+/* Label-smoothed cross-entropy, forward (metrics_losses.c:28-77): per row
+ * max by strict compare from row[0]; lse = log(sum exp(x - max)) in index
+ * order; sample_loss -= smooth_t * log_soft over c in index order, with
+ * smooth_t = smoothing / K (+ 1 - smoothing at the target); loss = total / B. */
+int ora_ls_ce_forward(const double *logits, const int64_t *targets, int64_t batch, int64_t classes,
+                      double smoothing, double *loss_out)
+{
+    if (!logits || !targets || !loss_out) return -1;
+    if (batch <= 0 || classes <= 0) return -1;
+    if (smoothing < 0.0 || smoothing > 1.0) return -1;
+    double total = 0.0;
+    for (int64_t i = 0; i < batch; i++) {
+        const double *row = logits + i * classes;
+        double mx = row[0];
+        for (int64_t c = 1; c < classes; c++)
+            if (row[c] > mx) mx = row[c];
+        double lse = 0.0;
+        for (int64_t c = 0; c < classes; c++) lse += exp(row[c] - mx);
+        lse = log(lse);
+        const int64_t t = targets[i];
+        if (t < 0 || t >= classes) return -1;
+        double sample = 0.0;
+        for (int64_t c = 0; c < classes; c++) {
+            const double ls = (row[c] - mx) - lse;
+            double st = smoothing / (double)classes;
+            if (c == t) st += (1.0 - smoothing);
+            sample -= st * ls;
+        }
+        total += sample;
+    }
+    *loss_out = total / (double)batch;
+    return 0;
+}
+
+/* Label-smoothed cross-entropy, backward (metrics_losses.c:80-125):
+ * grad = (1/B) * (exp(x - max) / sum - smooth_t), the division per element. */
+int ora_ls_ce_backward(const double *logits, const int64_t *targets, int64_t batch, int64_t classes,
+                       double smoothing, double *grad)
+{
+    if (!logits || !targets || !grad) return -1;
+    if (batch <= 0 || classes <= 0) return -1;
+    if (smoothing < 0.0 || smoothing > 1.0) return -1;
+    const double inv_n = 1.0 / (double)batch;
+    for (int64_t i = 0; i < batch; i++) {
+        const double *row = logits + i * classes;
+        double *g = grad + i * classes;
+        double mx = row[0];
+        for (int64_t c = 1; c < classes; c++)
+            if (row[c] > mx) mx = row[c];
+        double s = 0.0;
+        for (int64_t c = 0; c < classes; c++) {
+            g[c] = exp(row[c] - mx);
+            s += g[c];
+        }
+        for (int64_t c = 0; c < classes; c++) g[c] /= s;
+        const int64_t t = targets[i];
+        if (t < 0 || t >= classes) return -1;
+        for (int64_t c = 0; c < classes; c++) {
+            double st = smoothing / (double)classes;
+            if (c == t) st += (1.0 - smoothing);
+            g[c] = inv_n * (g[c] - st);
+        }
+    }
+    return 0;
+}
+
+/* cross_entropy_loss (losses.asm:315-613), intended semantics: per row the
+ * maxss chain from x[0] (the running max of ora_max_chain), e_j =
+ * (float)exp((double)x_j - (double)max) summed sequentially in float
+ * (addss), p = e / sum (divss); the target index is the truncation of the
+ * target tensor's float value (cvttss2si); per-row loss
+ * (float)(-log((double)p_t + 1e-7)) summed sequentially in float, divided by
+ * (float)B.  Returns -1 for a target outside [0, K). */
+int ora_ce_loss_f32(const float *x, const float *tgt, int64_t batch, int64_t classes, double *loss)
+{
+    float total = 0.0f;
+    for (int64_t i = 0; i < batch; i++) {
+        const float *row = x + i * classes;
+        const float mx = ora_max_chain_f32(row, classes);
+        float s = 0.0f;
+        for (int64_t c = 0; c < classes; c++) s += (float)exp((double)row[c] - (double)mx);
+        const int32_t t = (int32_t)tgt[i];
+        if (!(tgt[i] > -1.0f && tgt[i] < (float)classes)) return -1;
+        const float et = (float)exp((double)row[t] - (double)mx);
+        const float p = et / s;
+        total += (float)(-log((double)p + 1e-7));
+    }
+    *loss = (double)(total / (float)batch);
+    return 0;
+}
+
+/* f64 path of the same routine: exp / log in double, sums in double. */
+int ora_ce_loss_f64(const double *x, const double *tgt, int64_t batch, int64_t classes, double *loss)
+{
+    double total = 0.0;
+    for (int64_t i = 0; i < batch; i++) {
+        const double *row = x + i * classes;
+        const double mx = ora_max_chain_f64(row, classes);
+        double s = 0.0;
+        for (int64_t c = 0; c < classes; c++) s += exp(row[c] - mx);
+        if (!(tgt[i] > -1.0 && tgt[i] < (double)classes)) return -1;
+        const int64_t t = (int64_t)tgt[i];
+        const double p = exp(row[t] - mx) / s;
+        total += -log(p + 1e-7);
+    }
+    *loss = total / (double)batch;
+    return 0;
+}

@@ -125,4 +125,15 @@ int ora_pad_2d(const double *in, int64_t rows, int64_t cols, int64_t pt, int64_t
                int64_t pl, int64_t pr, double value, double *out, int64_t *orows, int64_t *ocols);
 int ora_transpose_2d(const double *in, int64_t rows, int64_t cols, double *out);
 
+/* Cross-entropy losses (metrics_losses.c:28-125, losses.asm:315-613).
+ * ora_ls_ce_*: pinned bit-exact against the reference's metrics_losses.c
+ * (oracle/_ref).  ora_ce_loss_*: pinned by a closed form (fp64 log-softmax
+ * at the target) and a small hand-checked case (tests/test_oracle_losses.py). */
+int ora_ls_ce_forward(const double *logits, const int64_t *targets, int64_t batch, int64_t classes,
+                      double smoothing, double *loss_out);
+int ora_ls_ce_backward(const double *logits, const int64_t *targets, int64_t batch, int64_t classes,
+                       double smoothing, double *grad);
+int ora_ce_loss_f32(const float *x, const float *tgt, int64_t batch, int64_t classes, double *loss);
+int ora_ce_loss_f64(const double *x, const double *tgt, int64_t batch, int64_t classes, double *loss);
+
 #endif

@@ -315,3 +315,40 @@ def split_2d(a, rows, cols, axis, split):
 def build_info():
     return {"oracle": str(ORACLE_SO), "ref": str(REF_SO) if REF_SO.exists() else None,
             "pid": os.getpid()}
+
+
+# ---- cross-entropy losses -------------------------------------------------------------
+
+def ls_ce_forward(logits, targets, smoothing, use_ref=False):
+    """Label-smoothed CE forward (metrics_losses.c:28-77); use_ref runs the
+    reference's own compiled C."""
+    b, k = logits.shape
+    x = np.ascontiguousarray(logits, dtype=np.float64)
+    t = np.ascontiguousarray(targets, dtype=np.int64)
+    out = ctypes.c_double()
+    f = getattr(ref() if use_ref else lib(), "label_smoothing_ce_forward" if use_ref else "ora_ls_ce_forward")
+    rc = f(_p(x), _p(t), ctypes.c_int64(b), ctypes.c_int64(k), ctypes.c_double(smoothing), ctypes.byref(out))
+    return rc, out.value
+
+
+def ls_ce_backward(logits, targets, smoothing, use_ref=False):
+    b, k = logits.shape
+    x = np.ascontiguousarray(logits, dtype=np.float64)
+    t = np.ascontiguousarray(targets, dtype=np.int64)
+    g = np.zeros((b, k), dtype=np.float64)
+    f = getattr(ref() if use_ref else lib(), "label_smoothing_ce_backward" if use_ref else "ora_ls_ce_backward")
+    rc = f(_p(x), _p(t), ctypes.c_int64(b), ctypes.c_int64(k), ctypes.c_double(smoothing), _p(g))
+    return rc, g
+
+
+def ce_loss(logits, target_values):
+    """cross_entropy_loss intended semantics (losses.asm:315-613): targets as
+    values of the logits' dtype, truncated to an index."""
+    b, k = logits.shape
+    x = np.ascontiguousarray(logits)
+    t = np.ascontiguousarray(target_values, dtype=x.dtype)
+    out = ctypes.c_double()
+    f = lib().ora_ce_loss_f32 if x.dtype == np.float32 else lib().ora_ce_loss_f64
+    rc = f(_p(x), _p(t), ctypes.c_int64(b), ctypes.c_int64(k), ctypes.byref(out))
+    return rc, out.value
+
