@@ -307,7 +307,29 @@ def suite(torch, pn, stream):
     tS, tP = W(S), W(P)
     timeit("softmax f32 [65536,1024]", lambda: _lib.neural_softmax(tP._ptr, tS._ptr), 8 * S.numel())
     timeit("log_softmax f32 [65536,1024]", lambda: _lib.neural_log_softmax(tP._ptr, tS._ptr), 8 * S.numel())
-    del S, P, tS, tP
+    # cross-entropy on the same [65536,1024] logits:
+    # label-smoothed forward + backward in one pass (f32 and f64 logits, int64
+    # targets), and the tensor cross_entropy_loss (reads the logits once)
+    tgt = torch.randint(0, 1024, (65536,), device=dev, dtype=torch.int64)
+    tgt_f = tgt.to(torch.float32)
+    ttf = W(tgt_f)
+    lossv = ctypes.c_double()
+    timeit("ls_ce fused fwd+bwd f32 [65536,1024]",
+           lambda: _lib.label_smoothing_ce_fused_f32(S.data_ptr(), tgt.data_ptr(), 65536, 1024, 0.1,
+                                                     ctypes.byref(lossv), P.data_ptr()), 8 * S.numel())
+    timeit("cross_entropy_loss f32 [65536,1024] (incl. D2H)",
+           lambda: _lib.neural_cross_entropy_loss(tS._ptr, ttf._ptr, ctypes.byref(lossv)), 4 * S.numel())
+    del P, tP
+    S64 = S.double()
+    G64 = torch.empty_like(S64)
+    torch.cuda.synchronize()
+    timeit("ls_ce fused fwd+bwd f64 [65536,1024]",
+           lambda: _lib.label_smoothing_ce_fused(S64.data_ptr(), tgt.data_ptr(), 65536, 1024, 0.1,
+                                                 ctypes.byref(lossv), G64.data_ptr()), 16 * S.numel())
+    timeit("ls_ce forward f64 [65536,1024] (incl. D2H)",
+           lambda: _lib.label_smoothing_ce_forward(S64.data_ptr(), tgt.data_ptr(), 65536, 1024, 0.1,
+                                                   ctypes.byref(lossv)), 8 * S.numel())
+    del S, tS, S64, G64
     # cfg3 activations
     x4 = torch.randn(64, 64, 128, 128, device=dev) * 4
     y4 = torch.empty_like(x4)

@@ -80,7 +80,10 @@ template <> NH_DEV double wave_fmax_t<double>(double v)
 }
 
 // One wave per row, VPL 16-byte vectors per lane (<= 64 * VPL * VN values).
-template <typename T, int VPL, int MODE>
+// FULL: the row is exactly 64 * VPL * VN values and 16-byte aligned, so no
+// element needs a bounds check (per-element checks around the exp turn into
+// exec-mask branches).
+template <typename T, int VPL, int MODE, bool FULL>
 __global__ __launch_bounds__(256) void k_ce_wave(const T *__restrict__ x, CeArgs a, bool vec)
 {
     using V = typename Vec16<T>::type;
@@ -94,12 +97,12 @@ __global__ __launch_bounds__(256) void k_ce_wave(const T *__restrict__ x, CeArgs
 #pragma unroll
     for (int k = 0; k < VPL; k++) {
         const int64_t c0 = (int64_t(k) * 64 + lane) * VN;
-        if (vec) {
-            if (c0 < cols) v[k] = ld_nt(reinterpret_cast<const V *>(xr + c0));
+        if (FULL || vec) {
+            if (FULL || c0 < cols) v[k] = ld_nt(reinterpret_cast<const V *>(xr + c0));
         } else {
 #pragma unroll
             for (int j = 0; j < VN; j++)
-                if (c0 + j < cols) v[k][j] = xr[c0 + j];
+                if (FULL || c0 + j < cols) v[k][j] = xr[c0 + j];
         }
     }
     T mx = -inf_t<T>();
@@ -108,16 +111,23 @@ __global__ __launch_bounds__(256) void k_ce_wave(const T *__restrict__ x, CeArgs
         const int64_t c0 = (int64_t(k) * 64 + lane) * VN;
 #pragma unroll
         for (int j = 0; j < VN; j++)
-            if (c0 + j < cols) mx = fmax_nn(mx, v[k][j]);
+            if (FULL || c0 + j < cols) mx = fmax_nn(mx, v[k][j]);
     }
     const double m = wave_fmax_t<T>(mx);
+    // e_c = exp(x_c - m), kept for the gradient (the backward modes)
+    constexpr bool KEEP = MODE == CE_LS_BWD || MODE == CE_LS_FUSED;
+    V ev[KEEP ? VPL : 1];
     double s = 0.0;
 #pragma unroll
     for (int k = 0; k < VPL; k++) {
         const int64_t c0 = (int64_t(k) * 64 + lane) * VN;
 #pragma unroll
         for (int j = 0; j < VN; j++)
-            if (c0 + j < cols) s += sizeof(T) == 8 ? row_exp_d(double(v[k][j]), m) : row_exp_f(float(v[k][j]), m);
+            if (FULL || c0 + j < cols) {
+                const double e = sizeof(T) == 8 ? row_exp_d(double(v[k][j]), m) : row_exp_f(float(v[k][j]), m);
+                if constexpr (KEEP) ev[k][j] = T(e);
+                s += e;
+            }
     }
     s = wave_dsum(s);
     int64_t t = 0;
@@ -146,6 +156,11 @@ __global__ __launch_bounds__(256) void k_ce_wave(const T *__restrict__ x, CeArgs
     }
     const double lse = log(s);
     const double rs = 1.0 / s;
+    const double st0 = a.alpha / double(cols), st1 = st0 + (1.0 - a.alpha);
+    // f32 rows: the per-element terms in float (the gradient is a float and
+    // each loss term needs ~1e-7 of itself); the loss still sums in double
+    const float mf = float(m), lsef = float(lse), rsf = float(rs), st0f = float(st0), st1f = float(st1),
+                inf_ = float(a.inv_n);
     double acc = 0.0;
     T *gr = static_cast<T *>(a.grad) + r * cols;
 #pragma unroll
@@ -154,18 +169,25 @@ __global__ __launch_bounds__(256) void k_ce_wave(const T *__restrict__ x, CeArgs
         V g;
 #pragma unroll
         for (int j = 0; j < VN; j++)
-            if (c0 + j < cols) {
-                T gj = T(0);
-                acc += ce_elem<T, MODE>(v[k][j], c0 + j, t, m, lse, rs, a, gj);
-                g[j] = gj;
+            if (FULL || c0 + j < cols) {
+                const bool at_t = c0 + j == t;
+                if constexpr (sizeof(T) == 4) {
+                    const float st = at_t ? st1f : st0f;
+                    if (MODE == CE_LS_FWD || MODE == CE_LS_FUSED) acc += double(st * ((v[k][j] - mf) - lsef));
+                    if constexpr (KEEP) g[j] = inf_ * (ev[k][j] * rsf - st);
+                } else {
+                    const double st = at_t ? st1 : st0;
+                    if (MODE == CE_LS_FWD || MODE == CE_LS_FUSED) acc += st * ((double(v[k][j]) - m) - lse);
+                    if constexpr (KEEP) g[j] = T(a.inv_n * (double(ev[k][j]) * rs - st));
+                }
             }
         if (MODE == CE_LS_BWD || MODE == CE_LS_FUSED) {
-            if (vec) {
-                if (c0 < cols) st_nt(reinterpret_cast<V *>(gr + c0), g);
+            if (FULL || vec) {
+                if (FULL || c0 < cols) st_nt(reinterpret_cast<V *>(gr + c0), g);
             } else {
 #pragma unroll
                 for (int j = 0; j < VN; j++)
-                    if (c0 + j < cols) gr[c0 + j] = g[j];
+                    if (FULL || c0 + j < cols) gr[c0 + j] = g[j];
             }
         }
     }
@@ -232,8 +254,11 @@ __global__ __launch_bounds__(256) void k_ce_block(const T *__restrict__ x, CeArg
 template <typename T, int MODE, int VPL>
 static void launch_ce_wave(const T *x, const CeArgs &a, bool vec)
 {
-    hipLaunchKernelGGL((k_ce_wave<T, VPL, MODE>), dim3(unsigned(ceil_div(a.rows, 4))), dim3(256), 0, stream(), x, a,
-                       vec);
+    const dim3 g(unsigned(ceil_div(a.rows, 4)));
+    if (vec && a.cols == int64_t(64) * VPL * Vec16<T>::n)
+        hipLaunchKernelGGL((k_ce_wave<T, VPL, MODE, true>), g, dim3(256), 0, stream(), x, a, vec);
+    else
+        hipLaunchKernelGGL((k_ce_wave<T, VPL, MODE, false>), g, dim3(256), 0, stream(), x, a, vec);
 }
 
 template <typename T, int MODE>
@@ -260,8 +285,10 @@ static int ce_run(const T *x, const int64_t *tidx, const T *tval, int64_t rows, 
                   double *loss_host, T *grad_dev)
 {
     Workspace &ws = workspace();
-    int *bad = static_cast<int *>(ws.result) + 32;  // flag word in the small-result area
-    NH_HIP(hipMemsetAsync(bad, 0, sizeof(int), stream()));
+    // Flag word in the small-result area: zero at init and between calls (a
+    // call that finds it set clears it), so the common path launches nothing
+    // to reset it.
+    int *bad = static_cast<int *>(ws.result) + 32;
     const bool want_loss = MODE != CE_LS_BWD;
     double *row_loss = nullptr;
     if (want_loss) {
@@ -276,7 +303,10 @@ static int ce_run(const T *x, const int64_t *tidx, const T *tval, int64_t rows, 
     if (rc == NEURAL_OK) rc = result_to_host(&res, ws.result, sizeof(res));
     if (row_loss) dev_free(row_loss);
     if (rc != NEURAL_OK) return rc;
-    if (res.bad) return NEURAL_ERR_INVALID_ARGUMENT;
+    if (res.bad) {
+        NH_HIP(hipMemsetAsync(bad, 0, sizeof(int), stream()));
+        return NEURAL_ERR_INVALID_ARGUMENT;
+    }
     if (want_loss && loss_host) *loss_host = res.sum / double(rows);
     return NEURAL_OK;
 }

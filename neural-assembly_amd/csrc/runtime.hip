@@ -110,6 +110,7 @@ int ensure_init()
                 hipMalloc(&r.ws.result, 256) != hipSuccess ||
                 hipHostMalloc(&r.ws.host_result, 256, hipHostMallocDefault) != hipSuccess ||
                 hipMemset(r.ws.counter, 0, sizeof(unsigned) * kCounters) != hipSuccess ||
+                hipMemset(r.ws.result, 0, 256) != hipSuccess ||
                 hipDeviceSynchronize() != hipSuccess) {
                 r.init_rc = NEURAL_ERR_OUT_OF_MEMORY;
                 return set_error(r.init_rc);
