@@ -378,6 +378,16 @@ def suite(torch, pn, stream):
     hn, hi, ss = ctypes.c_int(), ctypes.c_int(), ctypes.c_double()
     timeit("nan/inf/l2 scan f32 100M (incl. D2H)",
            lambda: _lib.neural_tensor_scan(tg._ptr, ctypes.byref(hn), ctypes.byref(hi), ctypes.byref(ss)), 4 * na)
+    # gradient clipping over the same 100M gradients (no host readback).  A
+    # negative max_norm clips on every call (scale -|max|/norm, magnitudes kept).
+    glist = (ctypes.c_void_p * 1)(tg._ptr)
+    norm0 = float(ss.value) ** 0.5
+    timeit("clip_grad_norm f32 100M, clipping (sumsq + scale)",
+           lambda: _lib.neural_clip_grad_norm_list(glist, 1, ctypes.c_double(-norm0), None), 12 * na)
+    timeit("clip_grad_norm f32 100M, below threshold (sumsq only)",
+           lambda: _lib.neural_clip_grad_norm_list(glist, 1, ctypes.c_double(1e300), None), 4 * na)
+    timeit("clip_grad_value f32 100M",
+           lambda: _lib.neural_clip_grad_value_list(glist, 1, ctypes.c_double(-1e-3), ctypes.c_double(1e-3)), 8 * na)
     return out
 
 

@@ -206,6 +206,22 @@ int64_t opt_state_bytes(void *opt);                                             
 int     opt_state_export(void *opt, void *buffer, int64_t size);                      /* optimizers_c.c:417 */
 int     opt_state_import(void *opt, const void *buffer, int64_t size);                /* optimizers_c.c:480 */
 
+/* Gradient clipping: neural_api.h:731,741 (neural_api.asm:1677-1720 ->
+ * clip_grad_norm_ / clip_grad_value_, optimizers.asm:1370-1620).  On an
+ * optimizer handle, they act on the gradient tensors passed to its latest
+ * opt_step (none before the first step: NEURAL_OK, nothing done).  Global-norm
+ * clip: norm = sqrt(sum double(g)^2); when norm > max_norm every gradient is
+ * multiplied by max_norm / norm (f32: that scale rounded to float).  Value
+ * clip: g = min(max(g, lo), hi) with SSE maxsd/minsd operand rules (a NaN
+ * gradient becomes lo); f32 bounds rounded to float. */
+int     neural_clip_grad_norm(void *optimizer, double max_norm);                     /* neural_api.h:731 */
+int     neural_clip_grad_value(void *optimizer, double min_val, double max_val);     /* neural_api.h:741 */
+/* NEW: the same on an explicit gradient list (NULL entries skipped); total_norm
+ * (may be NULL) receives the pre-clip norm -- when NULL the call does not wait
+ * for the device.  At most 16384 non-empty tensors per call. */
+int     neural_clip_grad_norm_list(NeuralTensor **grads, int64_t n, double max_norm, double *total_norm);
+int     neural_clip_grad_value_list(NeuralTensor **grads, int64_t n, double min_val, double max_val);
+
 /* ---- INT8 quantization: neural_api.h:1008-1065, quantize.c:39-269 ------------- */
 /* Same 40-byte layout as the reference (scale@0 zero_point@8 min_val@16
  * max_val@24 symmetric@32). */

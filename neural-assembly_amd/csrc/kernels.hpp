@@ -3,6 +3,8 @@
 
 #include <cstdint>
 
+struct NeuralTensor;
+
 namespace nh {
 
 // Contiguous fill of n elements (f32 stores (float)value).
@@ -14,5 +16,11 @@ int launch_fill_strided(void *dst, int dtype, const int64_t *shape, const int64_
 // shapes/byte strides, element size es).
 int launch_copy_nd(void *dst, const int64_t *dshape, const int64_t *dstride, int dndim, const void *src,
                    const int64_t *sshape, const int64_t *sstride, int sndim, int es);
+
+// Gradient clipping over a tensor list (NULL entries skipped): the global-norm
+// clip (total_norm, when non-null, receives the pre-clip norm) and the value
+// clip.  Both run on the active stream; see clip.hip.
+int clip_norm_list(NeuralTensor *const *grads, int64_t count, double max_norm, double *total_norm);
+int clip_value_list(NeuralTensor *const *grads, int64_t count, double lo, double hi);
 
 }  // namespace nh

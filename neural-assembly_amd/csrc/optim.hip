@@ -32,6 +32,7 @@ struct OptHandle {
     int64_t n_params;
     std::vector<int64_t> sizes;
     std::vector<double *> m, v, vel;  // device buffers
+    std::vector<NeuralTensor *> last_grads;  // gradient tensors of the latest opt_step
 };
 
 struct OptStateHeader {
@@ -354,6 +355,7 @@ int opt_step(void *opt, void **params, void **grads, int64_t n)
             }
         }
     }
+    o->last_grads.assign(reinterpret_cast<NeuralTensor **>(grads), reinterpret_cast<NeuralTensor **>(grads) + n);
     AdamArgs a{o->lr, o->beta1, o->beta2, o->eps, o->wd, 0.0, 0.0};
     if (o->type != OPT_SGD) {
         o->t++;
@@ -373,6 +375,31 @@ void opt_free(void *opt)
     if (ensure_init() == NEURAL_OK) (void)sync();
     free_moments(o);
     delete o;
+}
+
+// neural_clip_grad_norm / neural_clip_grad_value (neural_api.h:731,741;
+// neural_api.asm:1677-1720 -> clip_grad_norm_ / clip_grad_value_,
+// optimizers.asm:1370-1620).  The reference's optimizer holds its parameter
+// nodes and clips their gradients.  This handle learns its gradients from
+// opt_step, so it clips the gradient tensors passed to its most recent
+// opt_step (the caller keeps them alive, as the reference keeps its nodes).
+// Before the first step there are none: NEURAL_OK with nothing done, as
+// clip_grad_norm_ does for an optimizer without parameter nodes
+// (optimizers.asm:1386-1388).
+int neural_clip_grad_norm(void *opt, double max_norm)
+{
+    if (!opt) return set_error(NEURAL_ERR_NULL_POINTER);
+    OptHandle *o = static_cast<OptHandle *>(opt);
+    if (o->last_grads.empty()) return set_error(NEURAL_OK);
+    return clip_norm_list(o->last_grads.data(), int64_t(o->last_grads.size()), max_norm, nullptr);
+}
+
+int neural_clip_grad_value(void *opt, double min_val, double max_val)
+{
+    if (!opt) return set_error(NEURAL_ERR_NULL_POINTER);
+    OptHandle *o = static_cast<OptHandle *>(opt);
+    if (o->last_grads.empty()) return set_error(NEURAL_OK);
+    return clip_value_list(o->last_grads.data(), int64_t(o->last_grads.size()), min_val, max_val);
 }
 
 double opt_get_lr(void *opt) { return opt ? static_cast<OptHandle *>(opt)->lr : 0.0; }

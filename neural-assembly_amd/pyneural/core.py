@@ -229,6 +229,10 @@ _SIGS = {
     "opt_state_bytes": (_i64, [_vp]),
     "opt_state_export": (_i, [_vp, _vp, _i64]),
     "opt_state_import": (_i, [_vp, _vp, _i64]),
+    "neural_clip_grad_norm": (_i, [_vp, _d]),
+    "neural_clip_grad_value": (_i, [_vp, _d, _d]),
+    "neural_clip_grad_norm_list": (_i, [ctypes.POINTER(_vp), _i64, _d, _dp]),
+    "neural_clip_grad_value_list": (_i, [ctypes.POINTER(_vp), _i64, _d, _d]),
     # quantization
     "calibrate_minmax": (_i, [_vp, _i64, _i, _qp]),
     "quantize_tensor": (_i, [_vp, _vp, _i64, _qp]),

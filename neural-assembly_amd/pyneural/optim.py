@@ -42,6 +42,20 @@ class Optimizer:
         pp = (ctypes.c_void_p * max(n, 1))(*[p._ptr for p in params])
         gp = (ctypes.c_void_p * max(n, 1))(*[g._ptr for g in grads])
         _check_error(_lib.opt_step(self._ptr, pp, gp, n), label)
+        # The handle clips the gradients of its latest step (neural_clip_grad_*);
+        # keep those tensors alive while it may touch them.
+        self._last_grads = list(grads)
+
+    def clip_grad_norm(self, max_norm: float) -> None:
+        """Clip the gradients of the latest step by their global L2 norm
+        (neural_clip_grad_norm, optimizers.asm:1370-1516)."""
+        _check_error(_lib.neural_clip_grad_norm(self._ptr, ctypes.c_double(max_norm)), "clip_grad_norm")
+
+    def clip_grad_value(self, min_val: float, max_val: float) -> None:
+        """Clamp the gradients of the latest step to [min_val, max_val]
+        (neural_clip_grad_value, optimizers.asm:1527-1620)."""
+        _check_error(_lib.neural_clip_grad_value(self._ptr, ctypes.c_double(min_val), ctypes.c_double(max_val)),
+                     "clip_grad_value")
 
     def state_bytes(self) -> bytes:
         if not self._ptr:

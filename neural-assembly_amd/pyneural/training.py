@@ -2,7 +2,9 @@
 Training-step checks (reference ``pyneural/training.py:25-79``): NaN/Inf
 detection and the gradient L2 norm.  Both use one fused device scan of the
 tensor (``neural_tensor_scan``) instead of the reference's host pointer
-round trip.
+round trip.  Gradient clipping over a gradient list (the work the reference's
+Trainer asks of ``neural_clip_grad_norm``, training.py:267-271;
+optimizers.asm:1370-1620) runs as three device launches for the whole list.
 """
 
 import ctypes
@@ -52,3 +54,28 @@ def grad_l2_norm(tensor) -> float:
     """L2 norm of a tensor's data, rounded to float32 as the reference returns."""
     _, _, ss = _scan(tensor)
     return float(ctypes.c_float(math.sqrt(ss)).value)
+
+
+def _grad_array(grads):
+    grads = list(grads)
+    arr = (ctypes.c_void_p * max(len(grads), 1))(*[g._ptr if g is not None else None for g in grads])
+    return arr, len(grads)
+
+
+def clip_grad_norm(grads, max_norm: float) -> float:
+    """Scale every gradient by max_norm / norm when the global L2 norm exceeds
+    max_norm (clip_grad_norm_, optimizers.asm:1370-1516).  Returns the norm
+    before clipping.  None entries are skipped."""
+    arr, n = _grad_array(grads)
+    norm = ctypes.c_double()
+    _check_error(_lib.neural_clip_grad_norm_list(arr, n, ctypes.c_double(max_norm), ctypes.byref(norm)),
+                 "clip_grad_norm")
+    return norm.value
+
+
+def clip_grad_value(grads, min_val: float, max_val: float) -> None:
+    """Clamp every gradient element to [min_val, max_val] with the reference's
+    maxsd/minsd rules (clip_grad_value_, optimizers.asm:1527-1620)."""
+    arr, n = _grad_array(grads)
+    _check_error(_lib.neural_clip_grad_value_list(arr, n, ctypes.c_double(min_val), ctypes.c_double(max_val)),
+                 "clip_grad_value")

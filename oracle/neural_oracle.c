@@ -867,3 +867,72 @@ int ora_ce_loss_f64(const double *x, const double *tgt, int64_t batch, int64_t c
     *loss = total / (double)batch;
     return 0;
 }
+
+/* ---- gradient clipping ---------------------------------------------------------- */
+
+/* clip_grad_norm_ (optimizers.asm:1370-1516) over a list of gradient buffers
+ * (dtypes[i]: 0 f32, 1 f64; NULL entries skipped as the asm skips parameter
+ * nodes without a gradient, 1396-1403).  One sequential double sum of
+ * (double)g * (double)g over the list in order (mulsd + addsd, 1410-1436),
+ * sqrtsd (1444), then clip only when norm > max_norm: ucomisd + jbe
+ * (1448-1449) skips on <= and on unordered.  scale = max_norm / norm (divsd,
+ * 1452); f64 gradients g * scale (1480-1487), f32 gradients g * (float)scale
+ * in float (cvtsd2ss + mulss, 1489-1499).  Returns the pre-clip norm. */
+double ora_clip_grad_norm(void **grads, const int *dtypes, const int64_t *ns, int64_t count, double max_norm)
+{
+    double total = 0.0;
+    for (int64_t i = 0; i < count; i++) {
+        if (!grads[i]) continue;
+        if (dtypes[i] == 0) {
+            const float *g = (const float *)grads[i];
+            for (int64_t j = 0; j < ns[i]; j++) {
+                const double d = (double)g[j];
+                total += d * d;
+            }
+        } else {
+            const double *g = (const double *)grads[i];
+            for (int64_t j = 0; j < ns[i]; j++) total += g[j] * g[j];
+        }
+    }
+    const double norm = sqrt(total);
+    if (norm > max_norm) {
+        const double scale = max_norm / norm;
+        for (int64_t i = 0; i < count; i++) {
+            if (!grads[i]) continue;
+            if (dtypes[i] == 0) {
+                float *g = (float *)grads[i];
+                const float sf = (float)scale;
+                for (int64_t j = 0; j < ns[i]; j++) g[j] = g[j] * sf;
+            } else {
+                double *g = (double *)grads[i];
+                for (int64_t j = 0; j < ns[i]; j++) g[j] = g[j] * scale;
+            }
+        }
+    }
+    return norm;
+}
+
+/* clip_grad_value_ (optimizers.asm:1527-1620): maxsd then minsd, i.e.
+ * t = g > lo ? g : lo; g = t < hi ? t : hi (the SSE rule returns the second
+ * operand when the compare is false, NaN included).  f32 bounds are rounded to
+ * float first (cvtsd2ss, 1587-1591); maxsd / minsd at 1579-1581. */
+void ora_clip_grad_value(void **grads, const int *dtypes, const int64_t *ns, int64_t count, double lo, double hi)
+{
+    for (int64_t i = 0; i < count; i++) {
+        if (!grads[i]) continue;
+        if (dtypes[i] == 0) {
+            float *g = (float *)grads[i];
+            const float l = (float)lo, h = (float)hi;
+            for (int64_t j = 0; j < ns[i]; j++) {
+                const float t = g[j] > l ? g[j] : l;
+                g[j] = t < h ? t : h;
+            }
+        } else {
+            double *g = (double *)grads[i];
+            for (int64_t j = 0; j < ns[i]; j++) {
+                const double t = g[j] > lo ? g[j] : lo;
+                g[j] = t < hi ? t : hi;
+            }
+        }
+    }
+}

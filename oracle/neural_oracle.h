@@ -136,4 +136,11 @@ int ora_ls_ce_backward(const double *logits, const int64_t *targets, int64_t bat
 int ora_ce_loss_f32(const float *x, const float *tgt, int64_t batch, int64_t classes, double *loss);
 int ora_ce_loss_f64(const double *x, const double *tgt, int64_t batch, int64_t classes, double *loss);
 
+/* Gradient clipping (optimizers.asm:1370-1620).  Pinned by invariants in
+ * tests/test_oracle_clip.py: the pre-clip norm against math.fsum, the
+ * post-clip norm equal to max_norm, bitwise no-op below the threshold and for
+ * a NaN norm, hand-computed NaN / reversed-bound cases for the value clip. */
+double ora_clip_grad_norm(void **grads, const int *dtypes, const int64_t *ns, int64_t count, double max_norm);
+void   ora_clip_grad_value(void **grads, const int *dtypes, const int64_t *ns, int64_t count, double lo, double hi);
+
 #endif

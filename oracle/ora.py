@@ -352,3 +352,36 @@ def ce_loss(logits, target_values):
     rc = f(_p(x), _p(t), ctypes.c_int64(b), ctypes.c_int64(k), ctypes.byref(out))
     return rc, out.value
 
+
+
+# ---- gradient clipping -------------------------------------------------------------
+
+def _grad_lists(arrays):
+    outs = [None if a is None else np.array(a, copy=True, order="C") for a in arrays]
+    n = len(outs)
+    ptrs = (ctypes.c_void_p * max(n, 1))(*[None if a is None else a.ctypes.data for a in outs])
+    dts = (ctypes.c_int * max(n, 1))(*[1 if (a is not None and a.dtype == np.float64) else 0 for a in outs])
+    ns = (ctypes.c_int64 * max(n, 1))(*[0 if a is None else a.size for a in outs])
+    return outs, ptrs, dts, ns, n
+
+
+def clip_grad_norm(arrays, max_norm):
+    """clip_grad_norm_ (optimizers.asm:1370-1516) on copies of float32/float64
+    arrays (None entries skipped).  Returns (pre-clip norm, clipped copies)."""
+    outs, ptrs, dts, ns, n = _grad_lists(arrays)
+    f = lib().ora_clip_grad_norm
+    f.restype = ctypes.c_double
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_double]
+    norm = f(ptrs, dts, ns, n, max_norm)
+    return norm, outs
+
+
+def clip_grad_value(arrays, lo, hi):
+    """clip_grad_value_ (optimizers.asm:1527-1620) on copies; returns them."""
+    outs, ptrs, dts, ns, n = _grad_lists(arrays)
+    f = lib().ora_clip_grad_value
+    f.restype = None
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_double,
+                  ctypes.c_double]
+    f(ptrs, dts, ns, n, lo, hi)
+    return outs
