@@ -294,6 +294,19 @@ def suite(torch, pn, stream):
     tX, tbias, tY = W(X), W(bias), W(Y)
     torch.cuda.synchronize()
     timeit("bias_add f32 [16384,4096]", lambda: _lib.neural_bias_add(tY._ptr, tX._ptr, tbias._ptr), 8 * X.numel())
+    timeit("bias_add+relu fused f32 [16384,4096]",
+           lambda: _lib.neural_bias_add_act(tY._ptr, tX._ptr, tbias._ptr, 1, ctypes.c_double(0.0)), 8 * X.numel())
+    timeit("bias_add+gelu fused f32 [16384,4096]",
+           lambda: _lib.neural_bias_add_act(tY._ptr, tX._ptr, tbias._ptr, 4, ctypes.c_double(0.0)), 8 * X.numel())
+    # dropout over the 64M cfg1 vector: 4 B in + 4 B out + 1 B mask per element
+    dmask = torch.empty(n, dtype=torch.uint8, device=dev)
+    torch.cuda.synchronize()
+    timeit("dropout fwd f32 64M (p=0.5, draws + apply)",
+           lambda: _lib.neural_dropout_forward(a.data_ptr(), c.data_ptr(), dmask.data_ptr(), n, ctypes.c_float(0.5)),
+           9 * n)
+    timeit("dropout bwd f32 64M", lambda: _lib.neural_dropout_backward(a.data_ptr(), c.data_ptr(), dmask.data_ptr(), n,
+                                                                       ctypes.c_float(0.5)), 9 * n)
+    del dmask
     rs = torch.empty(16384, device=dev)
     trs = W(rs)
     timeit("row sum f32 [16384,4096]", lambda: _lib.neural_reduce_sum(tX._ptr, 1, trs._ptr), 4 * X.numel())

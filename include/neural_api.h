@@ -132,6 +132,23 @@ int neural_scalar_mul(NeuralTensor *out, const NeuralTensor *a, double s);      
 int neural_neg(NeuralTensor *out, const NeuralTensor *a);                         /* ew_neg math_kernels.asm:843 */
 /* Row-broadcast bias add out[i,j] = x[i,j] + bias[j]: nn_layers.asm:472-539. */
 int neural_bias_add(NeuralTensor *out, const NeuralTensor *x, const NeuralTensor *bias);
+/* NEW out = max(0, a + b) in one pass (addss then maxss with +0, as
+ * vec_add_relu_fusion, fusion.asm:200-226); b broadcasts as in neural_add, so
+ * a [.., C] bias gives the bias + ReLU epilogue of matmul_bias_relu_fusion
+ * (fusion.asm:110-190). */
+int neural_add_relu(NeuralTensor *out, const NeuralTensor *a, const NeuralTensor *b);
+/* NEW fused bias add + activation: out = act(x + bias) with x + bias rounded
+ * in the tensor's dtype first (nn_layers.asm:472-539, then the activation
+ * formulas of activations_c.c), bit-identical to neural_bias_add followed by
+ * the activation.  alpha is used by LEAKY_RELU and ELU. */
+typedef enum {
+    NEURAL_ACT_NONE = 0, NEURAL_ACT_RELU = 1, NEURAL_ACT_SIGMOID = 2, NEURAL_ACT_TANH = 3,
+    NEURAL_ACT_GELU = 4, NEURAL_ACT_LEAKY_RELU = 5, NEURAL_ACT_ELU = 6, NEURAL_ACT_SELU = 7,
+    NEURAL_ACT_SWISH = 8, NEURAL_ACT_MISH = 9, NEURAL_ACT_HARDSWISH = 10, NEURAL_ACT_SOFTPLUS = 11,
+    NEURAL_ACT_HARDTANH = 12
+} NeuralActivation;
+int neural_bias_add_act(NeuralTensor *out, const NeuralTensor *x, const NeuralTensor *bias, int act,
+                        double alpha);
 
 /* Raw-pointer f32 kernels of simd.asm:190-784, destination first as there
  * (host or device pointers; the reference returns void, these return 0 or an
@@ -142,6 +159,8 @@ int   simd_fma_f32(float *dst, const float *a, const float *b, const float *c,
                    uint64_t n);                                                   /* simd.asm:436 (fused a*b+c) */
 float simd_dot_f32(const float *a, const float *b, uint64_t n);                   /* simd.asm:551 */
 float simd_sum_f32(const float *a, uint64_t n);                                   /* simd.asm:684 */
+/* c[i] = max(0, a[i] + b[i]); nothing for length <= 0 (host or device pointers). */
+void  vec_add_relu_fusion(const float *a, const float *b, float *c, int64_t length);  /* fusion.asm:200 */
 
 /* ---- Reductions ------------------------------------------------------------- */
 /* neural_sum / neural_mean: neural_api.h:359,367 (stubs returning 14 at
@@ -258,6 +277,22 @@ int   neural_scan_nan_inf_l2(const float *data, uint64_t n, int *has_nan, int *h
                              double *sumsq);
 /* NEW tensor-level forms (no host round trip for device-resident tensors). */
 int   neural_tensor_scan(NeuralTensor *t, int *has_nan, int *has_inf, double *sumsq);
+
+/* Inverted dropout (training_ops.asm:718-858; neural_api.asm:2797-2803; bound
+ * at pyneural/core.py:499-515).  Forward draws one value of the library's
+ * copy of glibc's rand() stream per element: dropped when the draw is below
+ * cvtsd2si(p * 2147483647.0) (mask 0, out +0.0f), else mask 1 and
+ * out = x * (float)(1 / (1 - p)).  Backward: grad_in = mask ? grad_out * scale
+ * : +0.0f.  Host or device pointers. */
+int   neural_dropout_forward(const float *input, float *output, uint8_t *mask, uint64_t num_elements,
+                             float p);
+int   neural_dropout_backward(const float *grad_output, float *grad_input, const uint8_t *mask,
+                              uint64_t num_elements, float p);
+/* NEW: position the dropout stream as srand(seed) positions glibc's rand()
+ * (the reference seeds through srand, training_ops.asm:943); the stream
+ * starts as srand(1).  neural_dropout_draws: draws taken since the last seed. */
+int      neural_dropout_seed(uint32_t seed);
+uint64_t neural_dropout_draws(void);
 
 /* ---- 2-D f64 tensor ops: neural_api.h:1273-1305, tensor_ops.c:15-148 ---------- */
 int tensor_concat_2d(const double *a, const double *b, int64_t rows_a, int64_t cols_a,

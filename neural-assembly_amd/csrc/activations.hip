@@ -297,6 +297,56 @@ static int act_mish_impl(void *out, const void *in) { return act2<AMish>(out, in
 static int act_softplus_impl(void *out, const void *in) { return act2<ASoftplus>(out, in, HeadTailFn<SoftplusF32>{}); }
 static int act_tanh_impl(void *out, const void *in) { return act2<ATanh>(out, in, TanhF32Fn{}); }
 
+// Bias add then activation, one pass: y = act(x + b) with x + b rounded in
+// the tensor's dtype first (nn_layers.asm:472-539 then activations_c.c), so
+// the result equals neural_bias_add followed by the activation bit for bit.
+template <class F32, class F64>
+struct OpAddAct {
+    F32 f32;
+    F64 f64;
+    NH_DEV float operator()(float x, float b) const { return f32(x + b); }
+    NH_DEV double operator()(double x, double b) const { return f64(x + b); }
+};
+template <class F32, class F64>
+OpAddAct<F32, F64> add_act(F32 f32, F64 f64) { return {f32, f64}; }
+
+struct FnReluAct {
+    NH_DEV float operator()(float x) const { return x > 0.0f ? x : 0.0f; }
+    NH_DEV double operator()(double x) const { return x > 0.0 ? x : 0.0; }
+};
+struct FnIdentity {
+    template <class T> NH_DEV T operator()(T x) const { return x; }
+};
+
+static int bias_add_act(NeuralTensor *out, const NeuralTensor *x, const NeuralTensor *bias, int act, double alpha)
+{
+    if (!out || !x || !bias) return set_error(NEURAL_ERR_NULL_POINTER);
+    if (bias->ndim < 1 || x->ndim < 1 || numel(bias) != x->shape[x->ndim - 1])
+        return set_error(NEURAL_ERR_SHAPE_MISMATCH);
+    if (out->ndim != x->ndim) return set_error(NEURAL_ERR_SHAPE_MISMATCH);
+    for (int64_t i = 0; i < x->ndim; i++)
+        if (out->shape[i] != x->shape[i]) return set_error(NEURAL_ERR_SHAPE_MISMATCH);
+    switch (act) {
+    case NEURAL_ACT_NONE: return binary_api(out, x, bias, add_act(FnIdentity{}, FnIdentity{}));
+    case NEURAL_ACT_RELU: return binary_api(out, x, bias, add_act(FnReluAct{}, FnReluAct{}));
+    case NEURAL_ACT_SIGMOID: return binary_api(out, x, bias, add_act(ActFn<ASigmoid>{}, ActFn<ASigmoid>{}));
+    case NEURAL_ACT_TANH: return binary_api(out, x, bias, add_act(TanhF32Fn{}, ActFn<ATanh>{}));
+    case NEURAL_ACT_GELU: return binary_api(out, x, bias, add_act(HeadTailFn<GeluF32>{}, ActFn<AGelu>{}));
+    case NEURAL_ACT_LEAKY_RELU:
+        return binary_api(out, x, bias, add_act(ActFn<ALeaky>{ALeaky{alpha}}, ActFn<ALeaky>{ALeaky{alpha}}));
+    case NEURAL_ACT_ELU:
+        return binary_api(out, x, bias, add_act(ActFn<AElu>{AElu{alpha}}, ActFn<AElu>{AElu{alpha}}));
+    case NEURAL_ACT_SELU: return binary_api(out, x, bias, add_act(ActFn<ASelu>{}, ActFn<ASelu>{}));
+    case NEURAL_ACT_SWISH: return binary_api(out, x, bias, add_act(HeadTailFn<SwishF32>{}, ActFn<ASwish>{}));
+    case NEURAL_ACT_MISH: return binary_api(out, x, bias, add_act(HeadTailFn<MishF32>{}, ActFn<AMish>{}));
+    case NEURAL_ACT_HARDSWISH: return binary_api(out, x, bias, add_act(ActFn<AHardswish>{}, ActFn<AHardswish>{}));
+    case NEURAL_ACT_SOFTPLUS:
+        return binary_api(out, x, bias, add_act(HeadTailFn<SoftplusF32>{}, ActFn<ASoftplus>{}));
+    case NEURAL_ACT_HARDTANH: return binary_api(out, x, bias, add_act(ActFn<AHardtanh>{}, ActFn<AHardtanh>{}));
+    default: return set_error(NEURAL_ERR_INVALID_ARGUMENT);
+    }
+}
+
 }  // namespace nh
 
 using namespace nh;
@@ -327,5 +377,10 @@ int neural_mish(NeuralTensor *out, const NeuralTensor *in) { return act_mish_imp
 int neural_hardswish(NeuralTensor *out, const NeuralTensor *in) { return act<AHardswish>(out, in); }
 int neural_softplus(NeuralTensor *out, const NeuralTensor *in) { return act_softplus_impl(out, in); }
 int neural_hardtanh(NeuralTensor *out, const NeuralTensor *in) { return act<AHardtanh>(out, in); }
+
+int neural_bias_add_act(NeuralTensor *out, const NeuralTensor *x, const NeuralTensor *bias, int act, double alpha)
+{
+    return bias_add_act(out, x, bias, act, alpha);
+}
 
 }  // extern "C"

@@ -1,0 +1,523 @@
+// dropout.hip -- inverted dropout forward / backward with the reference's
+// random stream.
+//
+// Reference: dropout_forward / dropout_backward (training_ops.asm:717-858),
+// exported as neural_dropout_forward / _backward (neural_api.asm:2797-2803,
+// bound at pyneural/core.py:499-515).  Forward, per element i in order: one
+// libc rand() draw; drop when (int64)rand() < threshold with
+// threshold = cvtsd2si((double)p * 2147483647.0) (round to nearest even);
+// dropped: mask 0, out +0.0f; kept: mask 1, out = x * scale with
+// scale = (float)(1.0 / (1.0 - (double)p)).  Backward: grad_in = mask ?
+// grad_out * scale : +0.0f.
+//
+// The random stream is glibc's rand() (the reference calls it through the
+// PLT; glibc's default TYPE_3 generator, published e.g. in P. Selinger, "The
+// GLIBC pseudo-random number generator"): srand(s) fills r[0..30] with the
+// Park-Miller sequence r[i] = 16807 * r[i-1] mod (2^31 - 1) from r[0] = s
+// (s = 0 taken as 1), sets r[31..33] = r[0..2], continues
+// r[i] = r[i-31] + r[i-3] (mod 2^32), and rand() returns r[k + 344] >> 1
+// for k = 0, 1, ...  The library keeps its own stream: neural_dropout_seed(s)
+// positions it as srand(s) would (unseeded = srand(1), glibc's default), and
+// every forward call consumes n draws, so masks equal the reference's when its
+// process is at the same point of its rand() stream.
+//
+// Parallel generation on the device: the recurrence is linear, so for the
+// anchor window W = r[A .. A+30] any later value is r[A + k] = sum_m c_m W[m]
+// with c = x^k mod P(x), P(x) = x^31 - x^28 - 1, coefficients mod 2^32.
+// The n draws of a call are cut into segments of L = 992 draws (32 periods
+// of 31).  T[j] = x^(jL) mod P is a device table computed once; thread j
+// builds its starting window from T[j] and W (961 multiply-adds), then runs
+// the recurrence for its 992 draws with the 31-value ring in registers and
+// packs keep bits into 31 words.  A second, streaming kernel reads x in
+// 16-byte vectors, the 4 keep bits of each vector, and writes out and the
+// mask bytes (9 B per element).  The window after the call (r at A + n ..
+// A + n + 30) is written by the threads that generate the last 31 draws.
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace nh {
+
+constexpr int kLag = 31;                       // r[i] = r[i-31] + r[i-3]
+constexpr int kPeriods = 32;
+constexpr int64_t kSegL = int64_t(kLag) * kPeriods;   // 992 draws per thread segment
+constexpr int kSegWords = kPeriods * kLag / 32;        // 31 keep-bit words per segment
+constexpr int kDBlock = 256;
+
+// ---- polynomials mod P(x) = x^31 - x^28 - 1 over Z / 2^32 ------------------------------
+
+// a * b mod P.  x^d for d >= 31 is x^(d-3) + x^(d-31).
+NH_DEV void dpoly_mul(uint32_t (&a)[kLag], const uint32_t *__restrict__ b)
+{
+    uint32_t prod[2 * kLag - 1];
+#pragma unroll
+    for (int d = 0; d < 2 * kLag - 1; d++) prod[d] = 0u;
+#pragma unroll
+    for (int i = 0; i < kLag; i++) {
+#pragma unroll
+        for (int j = 0; j < kLag; j++) prod[i + j] += a[i] * b[j];
+    }
+#pragma unroll
+    for (int d = 2 * kLag - 2; d >= kLag; d--) {
+        prod[d - kLag] += prod[d];
+        prod[d - 3] += prod[d];
+    }
+#pragma unroll
+    for (int i = 0; i < kLag; i++) a[i] = prod[i];
+}
+
+// T[j] = x^(j*L) mod P for j in [j0, j1): square-and-multiply over the
+// host-made powers B[k] = x^(L * 2^k) mod P.
+__global__ __launch_bounds__(kDBlock) void k_jump_table(uint32_t *__restrict__ T, int64_t j0, int64_t j1,
+                                                         const uint32_t *__restrict__ B)
+{
+    const int64_t j = j0 + int64_t(blockIdx.x) * kDBlock + threadIdx.x;
+    if (j >= j1) return;
+    uint32_t c[kLag];
+#pragma unroll
+    for (int i = 0; i < kLag; i++) c[i] = i == 0 ? 1u : 0u;
+    for (int k = 0; k < 63 && (j >> k) != 0; k++)
+        if ((j >> k) & 1) dpoly_mul(c, B + k * kLag);
+#pragma unroll
+    for (int i = 0; i < kLag; i++) T[j * kLag + i] = c[i];
+}
+
+// Generate the keep bits of segment j.  W is the anchor window, Wn receives
+// the window after the call.  keep = (r >> 1) >= thr.
+template <bool TAIL>
+NH_DEV void gen_segment(uint32_t (&w)[kLag], int64_t d0, int64_t n, uint32_t thr, uint32_t *__restrict__ bits,
+                        uint32_t *__restrict__ Wn)
+{
+    uint32_t acc = 0u;
+    int i = 0;
+    for (int per = 0; per < kPeriods; per++) {
+#pragma unroll
+        for (int u = 0; u < kLag; u++) {
+            const uint32_t r = w[u] + w[(u + 28) % kLag];
+            w[u] = r;
+            acc |= uint32_t((r >> 1) >= thr) << (i & 31);
+            if constexpr (TAIL) {
+                const int64_t d = d0 + i;
+                if (d < n && d >= n - kLag) Wn[d - (n - kLag)] = r;
+            }
+            if ((i & 31) == 31) {
+                bits[i >> 5] = acc;
+                acc = 0u;
+            }
+            i++;
+        }
+    }
+}
+
+__global__ __launch_bounds__(kDBlock) void k_dropout_bits(const uint32_t *__restrict__ T, const uint32_t *__restrict__ W,
+                                                           uint32_t *__restrict__ Wn, int64_t n, int64_t nseg,
+                                                           uint32_t thr, uint32_t *__restrict__ bits)
+{
+    const int64_t j = int64_t(blockIdx.x) * kDBlock + threadIdx.x;
+    if (blockIdx.x == 0 && threadIdx.x < kLag && n + threadIdx.x < kLag)
+        Wn[threadIdx.x] = W[n + threadIdx.x];  // calls shorter than 31 draws keep part of the old window
+    if (j >= nseg) return;
+    // starting window: w[t] = r[A + jL + t] = sum_m (x^(jL+t) mod P)_m W[m]
+    uint32_t c[kLag], w[kLag];
+#pragma unroll
+    for (int i = 0; i < kLag; i++) c[i] = T[j * kLag + i];
+#pragma unroll
+    for (int t = 0; t < kLag; t++) {
+        uint32_t s = 0u;
+#pragma unroll
+        for (int m = 0; m < kLag; m++) s += c[m] * W[m];
+        w[t] = s;
+        // c <- c * x mod P
+        const uint32_t top = c[kLag - 1];
+#pragma unroll
+        for (int m = kLag - 1; m > 0; m--) c[m] = c[m - 1];
+        c[0] = top;
+        c[28] += top;
+    }
+    const int64_t d0 = j * kSegL;
+    uint32_t *b = bits + j * kSegWords;
+    if (d0 + kSegL > n - kLag) gen_segment<true>(w, d0, n, thr, b, Wn);
+    else gen_segment<false>(w, d0, n, thr, b, Wn);
+}
+
+constexpr int kDUnroll = 2;
+
+// Keep bit of draw d: segment d / L, bit d % L of its 31 words.  I = uint32_t
+// when every index fits (a division by the constant L is then a multiply-high
+// and a shift).
+template <typename I>
+NH_DEV uint32_t keep_bits(const uint32_t *__restrict__ bits, I d)
+{
+    const I seg = d / I(kSegL);
+    const I bi = d - seg * I(kSegL);
+    return bits[size_t(seg) * kSegWords + size_t(bi >> 5)] >> (bi & 31);
+}
+
+// out = keep ? x * scale : +0, mask = keep; 4 elements per lane-unit.
+template <typename I>
+__global__ __launch_bounds__(kDBlock) void k_dropout_apply(const f32x4 *__restrict__ x, f32x4 *__restrict__ out,
+                                                            uint32_t *__restrict__ mask, const uint32_t *__restrict__ bits,
+                                                            int64_t n4, float scale)
+{
+    const int64_t tile = int64_t(kDBlock) * kDUnroll;
+    for (int64_t base = int64_t(blockIdx.x) * tile + threadIdx.x; base < n4; base += int64_t(gridDim.x) * tile) {
+        f32x4 v[kDUnroll];
+        uint32_t kb[kDUnroll];
+#pragma unroll
+        for (int u = 0; u < kDUnroll; u++) {
+            const int64_t q = base + int64_t(u) * kDBlock;
+            if (q < n4) {
+                v[u] = ld_nt(x + q);
+                kb[u] = keep_bits<I>(bits, I(q * 4)) & 0xFu;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kDUnroll; u++) {
+            const int64_t q = base + int64_t(u) * kDBlock;
+            if (q < n4) {
+                f32x4 o;
+                uint32_t m = 0u;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const bool keep = (kb[u] >> k) & 1u;
+                    o[k] = keep ? v[u][k] * scale : 0.0f;
+                    m |= uint32_t(keep) << (8 * k);
+                }
+                st_nt(out + q, o);
+                st_nt(mask + q, m);
+            }
+        }
+    }
+}
+
+// Element-at-a-time form for unaligned buffers and the n % 4 tail.
+__global__ __launch_bounds__(kDBlock) void k_dropout_apply1(const float *__restrict__ x, float *__restrict__ out,
+                                                             uint8_t *__restrict__ mask,
+                                                             const uint32_t *__restrict__ bits, int64_t d0, int64_t n,
+                                                             float scale)
+{
+    for (int64_t d = d0 + int64_t(blockIdx.x) * kDBlock + threadIdx.x; d < n; d += int64_t(gridDim.x) * kDBlock) {
+        const bool keep = keep_bits<int64_t>(bits, d) & 1u;
+        out[d] = keep ? x[d] * scale : 0.0f;
+        mask[d] = keep ? 1 : 0;
+    }
+}
+
+// grad_in = mask ? grad_out * scale : +0 (any nonzero mask byte keeps).
+__global__ __launch_bounds__(kDBlock) void k_dropout_bwd(const f32x4 *__restrict__ go, f32x4 *__restrict__ gi,
+                                                          const uint32_t *__restrict__ mask, int64_t n4, float scale)
+{
+    const int64_t tile = int64_t(kDBlock) * kDUnroll;
+    for (int64_t base = int64_t(blockIdx.x) * tile + threadIdx.x; base < n4; base += int64_t(gridDim.x) * tile) {
+        f32x4 v[kDUnroll];
+        uint32_t m[kDUnroll];
+#pragma unroll
+        for (int u = 0; u < kDUnroll; u++) {
+            const int64_t q = base + int64_t(u) * kDBlock;
+            if (q < n4) {
+                v[u] = ld_nt(go + q);
+                m[u] = ld_nt(mask + q);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kDUnroll; u++) {
+            const int64_t q = base + int64_t(u) * kDBlock;
+            if (q < n4) {
+                f32x4 o;
+#pragma unroll
+                for (int k = 0; k < 4; k++) o[k] = ((m[u] >> (8 * k)) & 0xFFu) ? v[u][k] * scale : 0.0f;
+                st_nt(gi + q, o);
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(kDBlock) void k_dropout_bwd1(const float *__restrict__ go, float *__restrict__ gi,
+                                                           const uint8_t *__restrict__ mask, int64_t d0, int64_t n,
+                                                           float scale)
+{
+    for (int64_t d = d0 + int64_t(blockIdx.x) * kDBlock + threadIdx.x; d < n; d += int64_t(gridDim.x) * kDBlock)
+        gi[d] = mask[d] ? go[d] * scale : 0.0f;
+}
+
+// ---- host side ------------------------------------------------------------------------
+
+namespace {
+
+using HPoly = std::vector<uint32_t>;  // kLag coefficients
+
+HPoly hpoly_mul(const HPoly &a, const HPoly &b)
+{
+    uint32_t prod[2 * kLag - 1] = {0};
+    for (int i = 0; i < kLag; i++)
+        for (int j = 0; j < kLag; j++) prod[i + j] += a[size_t(i)] * b[size_t(j)];
+    for (int d = 2 * kLag - 2; d >= kLag; d--) {
+        prod[d - kLag] += prod[d];
+        prod[d - 3] += prod[d];
+    }
+    return HPoly(prod, prod + kLag);
+}
+
+HPoly hpoly_xpow(uint64_t k)
+{
+    HPoly r(kLag, 0u), base(kLag, 0u);
+    r[0] = 1u;
+    base[1] = 1u;  // x
+    while (k) {
+        if (k & 1) r = hpoly_mul(r, base);
+        base = hpoly_mul(base, base);
+        k >>= 1;
+    }
+    return r;
+}
+
+// glibc srand(seed) followed by the 310 discarded values: the window
+// r[313 .. 343] that precedes the first rand() output r[344].
+void seed_window(uint32_t seed, uint32_t *win)
+{
+    uint32_t r[344];
+    const uint32_t s = seed == 0 ? 1u : seed;
+    r[0] = s;
+    int32_t word = int32_t(s);
+    for (int i = 1; i < kLag; i++) {
+        // 16807 * word mod (2^31 - 1) without overflow (Schrage), as glibc does
+        const int32_t hi = word / 127773, lo = word % 127773;
+        word = 16807 * lo - 2836 * hi;
+        if (word < 0) word += 2147483647;
+        r[i] = uint32_t(word);
+    }
+    for (int i = kLag; i < 34; i++) r[i] = r[i - kLag];
+    for (int i = 34; i < 344; i++) r[i] = r[i - kLag] + r[i - 3];
+    std::memcpy(win, r + 344 - kLag, kLag * sizeof(uint32_t));
+}
+
+struct Stream {
+    std::mutex mu;
+    bool ready = false;
+    uint32_t *win[2] = {nullptr, nullptr};  // device windows (current, next)
+    int cur = 0;
+    uint32_t *table = nullptr;              // T[j], kLag words each
+    int64_t table_n = 0;
+    uint32_t *powers = nullptr;             // B[k] = x^(L 2^k) mod P, k < 63
+    uint32_t *bits = nullptr;
+    size_t bits_cap = 0;
+    uint64_t drawn = 0;                     // draws since the last seed
+};
+
+Stream &S()
+{
+    static Stream *s = new Stream();  // never destroyed: kernels may outlive static dtors
+    return *s;
+}
+
+int set_seed_locked(Stream &s, uint32_t seed)
+{
+    uint32_t w[kLag];
+    seed_window(seed, w);
+    NH_TRY(sync());
+    NH_HIP(hipMemcpy(s.win[s.cur], w, sizeof(w), hipMemcpyHostToDevice));
+    s.drawn = 0;
+    return NEURAL_OK;
+}
+
+int ensure_stream_locked(Stream &s)
+{
+    if (s.ready) return NEURAL_OK;
+    for (int i = 0; i < 2; i++) {
+        s.win[i] = static_cast<uint32_t *>(dev_alloc(kLag * sizeof(uint32_t)));
+        if (!s.win[i]) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
+    }
+    std::vector<uint32_t> B(size_t(63) * kLag);
+    HPoly p = hpoly_xpow(uint64_t(kSegL));
+    for (int k = 0; k < 63; k++) {
+        std::memcpy(B.data() + size_t(k) * kLag, p.data(), kLag * sizeof(uint32_t));
+        p = hpoly_mul(p, p);
+    }
+    s.powers = static_cast<uint32_t *>(dev_alloc(B.size() * sizeof(uint32_t)));
+    if (!s.powers) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
+    NH_HIP(hipMemcpy(s.powers, B.data(), B.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
+    s.ready = true;
+    return set_seed_locked(s, 1u);  // glibc's initial state is srand(1)
+}
+
+// Grow the jump table to cover nseg segments (doubling; old entries kept).
+int ensure_table_locked(Stream &s, int64_t nseg)
+{
+    if (nseg <= s.table_n) return NEURAL_OK;
+    int64_t cap = s.table_n > 0 ? s.table_n : 1024;
+    while (cap < nseg) cap *= 2;
+    uint32_t *t = static_cast<uint32_t *>(dev_alloc(size_t(cap) * kLag * sizeof(uint32_t)));
+    if (!t) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
+    if (s.table_n > 0)
+        NH_HIP(hipMemcpyAsync(t, s.table, size_t(s.table_n) * kLag * sizeof(uint32_t), hipMemcpyDeviceToDevice,
+                              stream()));
+    const int64_t fresh = cap - s.table_n;
+    hipLaunchKernelGGL(k_jump_table, dim3(unsigned(ceil_div(fresh, kDBlock))), dim3(kDBlock), 0, stream(), t,
+                       s.table_n, cap, s.powers);
+    NH_TRY(check_launch());
+    if (s.table) dev_free(s.table);
+    s.table = t;
+    s.table_n = cap;
+    return NEURAL_OK;
+}
+
+// cvtsd2si under the default rounding mode: nearest-even; NaN and values
+// outside int64 give the "integer indefinite" INT64_MIN.
+int64_t cvtsd2si(double v)
+{
+    if (!(v >= -0x1p63 && v < 0x1p63)) return INT64_MIN;
+    return int64_t(std::nearbyint(v));
+}
+
+float drop_scale(float p) { return float(1.0 / (1.0 - double(p))); }
+
+inline unsigned d_grid(int64_t work)
+{
+    int64_t g = ceil_div(work, kDBlock);
+    const int64_t cap = int64_t(num_cus()) * 16;
+    if (g > cap) g = cap;
+    return unsigned(g < 1 ? 1 : g);
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+static int dropout_fwd(const float *in, float *out, uint8_t *mask, uint64_t n, float p)
+{
+    if (!in || !out || !mask) return set_error(NEURAL_ERR_NULL_POINTER);
+    NH_TRY(ensure_init());
+    if (n == 0) return set_error(NEURAL_OK);
+    if (n > (uint64_t(1) << 40)) return set_error(NEURAL_ERR_TENSOR_TOO_LARGE);
+    Stream &s = S();
+    std::lock_guard<std::mutex> lock(s.mu);
+    NH_TRY(ensure_stream_locked(s));
+    const int64_t nn = int64_t(n);
+    const int64_t nseg = ceil_div(nn, kSegL);
+    NH_TRY(ensure_table_locked(s, nseg));
+    const size_t words = size_t(nseg) * kSegWords;
+    if (words > s.bits_cap) {
+        if (s.bits) dev_free(s.bits);
+        s.bits = static_cast<uint32_t *>(dev_alloc(words * sizeof(uint32_t)));
+        s.bits_cap = s.bits ? words : 0;
+        if (!s.bits) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
+    }
+    const int64_t th = cvtsd2si(double(p) * 2147483647.0);
+    const uint32_t thr = th <= 0 ? 0u : (th >= (int64_t(1) << 31) ? 0x80000000u : uint32_t(th));
+    const float scale = drop_scale(p);
+
+    Staged xi, xo, xm;
+    NH_TRY(xi.open(in, size_t(n) * 4, true));
+    NH_TRY(xo.open(out, size_t(n) * 4, false));
+    NH_TRY(xm.open(mask, size_t(n), false));
+    uint32_t *W = s.win[s.cur], *Wn = s.win[s.cur ^ 1];
+    hipLaunchKernelGGL(k_dropout_bits, dim3(unsigned(ceil_div(nseg, kDBlock))), dim3(kDBlock), 0, stream(), s.table,
+                       W, Wn, nn, nseg, thr, s.bits);
+    NH_TRY(check_launch());
+    s.cur ^= 1;
+    s.drawn += n;
+    const float *X = static_cast<const float *>(xi.dev);
+    float *O = static_cast<float *>(xo.dev);
+    uint8_t *M = static_cast<uint8_t *>(xm.dev);
+    int64_t done = 0;
+    if (aligned16(X) && aligned16(O) && (reinterpret_cast<uintptr_t>(M) & 3u) == 0) {
+        const int64_t n4 = nn / 4;
+        if (n4 > 0) {
+            if (nn < (int64_t(1) << 32))
+                hipLaunchKernelGGL(k_dropout_apply<uint32_t>, dim3(d_grid(ceil_div(n4, kDUnroll))), dim3(kDBlock), 0,
+                                   stream(), reinterpret_cast<const f32x4 *>(X), reinterpret_cast<f32x4 *>(O),
+                                   reinterpret_cast<uint32_t *>(M), s.bits, n4, scale);
+            else
+                hipLaunchKernelGGL(k_dropout_apply<int64_t>, dim3(d_grid(ceil_div(n4, kDUnroll))), dim3(kDBlock), 0,
+                                   stream(), reinterpret_cast<const f32x4 *>(X), reinterpret_cast<f32x4 *>(O),
+                                   reinterpret_cast<uint32_t *>(M), s.bits, n4, scale);
+            NH_TRY(check_launch());
+        }
+        done = n4 * 4;
+    }
+    if (done < nn) {
+        hipLaunchKernelGGL(k_dropout_apply1, dim3(d_grid(nn - done)), dim3(kDBlock), 0, stream(), X, O, M, s.bits,
+                           done, nn, scale);
+        NH_TRY(check_launch());
+    }
+    NH_TRY(xo.finish(true));
+    NH_TRY(xm.finish(true));
+    NH_TRY(xi.finish(false));
+    return set_error(NEURAL_OK);
+}
+
+static int dropout_bwd(const float *go, float *gi, const uint8_t *mask, uint64_t n, float p)
+{
+    if (!go || !gi || !mask) return set_error(NEURAL_ERR_NULL_POINTER);
+    NH_TRY(ensure_init());
+    if (n == 0) return set_error(NEURAL_OK);
+    const int64_t nn = int64_t(n);
+    const float scale = drop_scale(p);
+    Staged sg, so, sm;
+    NH_TRY(sg.open(go, size_t(n) * 4, true));
+    NH_TRY(sm.open(mask, size_t(n), true));
+    NH_TRY(so.open(gi, size_t(n) * 4, false));
+    const float *G = static_cast<const float *>(sg.dev);
+    float *O = static_cast<float *>(so.dev);
+    const uint8_t *M = static_cast<const uint8_t *>(sm.dev);
+    int64_t done = 0;
+    if (aligned16(G) && aligned16(O) && (reinterpret_cast<uintptr_t>(M) & 3u) == 0) {
+        const int64_t n4 = nn / 4;
+        if (n4 > 0) {
+            hipLaunchKernelGGL(k_dropout_bwd, dim3(d_grid(ceil_div(n4, kDUnroll))), dim3(kDBlock), 0, stream(),
+                               reinterpret_cast<const f32x4 *>(G), reinterpret_cast<f32x4 *>(O),
+                               reinterpret_cast<const uint32_t *>(M), n4, scale);
+            NH_TRY(check_launch());
+        }
+        done = n4 * 4;
+    }
+    if (done < nn) {
+        hipLaunchKernelGGL(k_dropout_bwd1, dim3(d_grid(nn - done)), dim3(kDBlock), 0, stream(), G, O, M, done, nn,
+                           scale);
+        NH_TRY(check_launch());
+    }
+    NH_TRY(so.finish(true));
+    NH_TRY(sg.finish(false));
+    NH_TRY(sm.finish(false));
+    return set_error(NEURAL_OK);
+}
+
+}  // namespace nh
+
+using namespace nh;
+
+extern "C" {
+
+int neural_dropout_forward(const float *input, float *output, uint8_t *mask, uint64_t num_elements, float p)
+{
+    return dropout_fwd(input, output, mask, num_elements, p);
+}
+
+int neural_dropout_backward(const float *grad_output, float *grad_input, const uint8_t *mask, uint64_t num_elements,
+                            float p)
+{
+    return dropout_bwd(grad_output, grad_input, mask, num_elements, p);
+}
+
+int neural_dropout_seed(uint32_t seed)
+{
+    NH_TRY(ensure_init());
+    Stream &s = S();
+    std::lock_guard<std::mutex> lock(s.mu);
+    NH_TRY(ensure_stream_locked(s));
+    NH_TRY(set_seed_locked(s, seed));
+    return set_error(NEURAL_OK);
+}
+
+uint64_t neural_dropout_draws(void)
+{
+    Stream &s = S();
+    std::lock_guard<std::mutex> lock(s.mu);
+    return s.drawn;
+}
+
+}  // extern "C"

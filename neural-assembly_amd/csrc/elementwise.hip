@@ -37,6 +37,16 @@ struct FnRelu {
     NH_DEV double operator()(double x) const { return x > 0.0 ? x : 0.0; }
 };
 
+// vec_add_relu_fusion (fusion.asm:200-226) and the bias + ReLU epilogue of
+// matmul_bias_relu_fusion (fusion.asm:110-190): addss, then maxss with +0.
+struct OpAddRelu {
+    template <class T> NH_DEV T operator()(T x, T y) const
+    {
+        const T s = x + y;
+        return s > T(0) ? s : T(0);
+    }
+};
+
 // ew_scalar_add/mul: the f32 path rounds the double scalar to float once
 // (cvtsd2ss, math_kernels.asm:544,653).
 struct FnScalarAdd {
@@ -237,64 +247,6 @@ int build_nd(const NeuralTensor *out, const NeuralTensor *a, const NeuralTensor 
     return NEURAL_OK;
 }
 
-// Is `b` a [C] (or [1,..,1,C]) contiguous vector matching the last dim of a
-// contiguous `a`/`out` pair of equal shape?
-static bool row_broadcast_case(const NeuralTensor *out, const NeuralTensor *a, const NeuralTensor *b)
-{
-    if (out->ndim < 1 || a->ndim != out->ndim || !is_contiguous(out) || !is_contiguous(a) || !is_contiguous(b))
-        return false;
-    for (int64_t i = 0; i < out->ndim; i++)
-        if (a->shape[i] != out->shape[i]) return false;
-    const int64_t C = out->shape[out->ndim - 1];
-    if (b->ndim < 1 || b->shape[b->ndim - 1] != C) return false;
-    for (int64_t i = 0; i + 1 < b->ndim; i++)
-        if (b->shape[i] != 1) return false;
-    const int64_t vn = out->dtype == NEURAL_DTYPE_FLOAT32 ? 4 : 2;
-    return C % vn == 0;
-}
-
-template <typename T, typename Op>
-static int launch_binary(NeuralTensor *out, const NeuralTensor *a, const NeuralTensor *b, const void *pa,
-                         const void *pb, void *po, Op op)
-{
-    const int64_t n = numel(out);
-    const T *A = static_cast<const T *>(pa);
-    const T *B = static_cast<const T *>(pb);
-    T *O = static_cast<T *>(po);
-    if (numel(a) == n && numel(b) == n && is_contiguous(a) && is_contiguous(b) && is_contiguous(out))
-        return launch_map2_flat(A, B, O, n, op);
-    if (row_broadcast_case(out, a, b) && aligned16(A) && aligned16(B) && aligned16(O)) {
-        const int64_t C = out->shape[out->ndim - 1];
-        return launch_rowbcast(A, B, O, n / C, C, op);
-    }
-    ND4 d;
-    NH_TRY(build_nd(out, a, b, d));
-    hipLaunchKernelGGL((k_map2_nd<T, Op>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(), A, B, O, n, d, op);
-    return check_launch();
-}
-
-template <typename Op>
-static int binary_api(NeuralTensor *out, const NeuralTensor *a, const NeuralTensor *b, Op op)
-{
-    NH_TRY(ensure_init());
-    if (!out || !a || !b) return set_error(NEURAL_ERR_NULL_POINTER);
-    NH_TRY(check_tensor(out));
-    NH_TRY(check_tensor(a));
-    NH_TRY(check_tensor(b));
-    if (a->dtype != out->dtype || b->dtype != out->dtype) return set_error(NEURAL_ERR_DTYPE_MISMATCH);
-    const int64_t n = numel(out);
-    if (n == 0) return set_error(NEURAL_OK);
-    const void *pa = nullptr, *pb = nullptr;
-    void *po = nullptr;
-    NH_TRY(dev_read(a, &pa));
-    NH_TRY(dev_read(b, &pb));
-    NH_TRY(dev_write(out, &po, is_contiguous(out)));
-    if (out->dtype == NEURAL_DTYPE_FLOAT32) NH_TRY((launch_binary<float, Op>(out, a, b, pa, pb, po, op)));
-    else NH_TRY((launch_binary<double, Op>(out, a, b, pa, pb, po, op)));
-    NH_TRY(dev_written(out));
-    return set_error(NEURAL_OK);
-}
-
 // ---- raw-pointer f32 (simd.asm) --------------------------------------------------------
 
 struct OpFma {
@@ -349,6 +301,21 @@ int neural_bias_add(NeuralTensor *out, const NeuralTensor *x, const NeuralTensor
     for (int64_t i = 0; i < out->ndim || i < x->ndim; i++)
         if (out->ndim != x->ndim || out->shape[i] != x->shape[i]) return set_error(NEURAL_ERR_SHAPE_MISMATCH);
     return binary_api(out, x, bias, OpAdd{});
+}
+
+// out = relu(a + b) in one pass; b may broadcast like neural_add's operands
+// (a [.., C] bias is the fused bias + ReLU).
+int neural_add_relu(NeuralTensor *out, const NeuralTensor *a, const NeuralTensor *b)
+{
+    return binary_api(out, a, b, OpAddRelu{});
+}
+
+// vec_add_relu_fusion (fusion.asm:200-226): c[i] = max(0, a[i] + b[i]) over
+// raw float pointers (host or device); nothing happens for length <= 0.
+void vec_add_relu_fusion(const float *a, const float *b, float *c, int64_t n)
+{
+    if (n <= 0) return;
+    (void)raw_binary_f32(c, a, b, uint64_t(n), OpAddRelu{});
 }
 
 int neural_scalar_add(NeuralTensor *out, const NeuralTensor *a, double s)

@@ -413,4 +413,64 @@ int run_unary(NeuralTensor *out, const NeuralTensor *in, F32 f32, F64 f64)
     return set_error(NEURAL_OK);
 }
 
+// Is `b` a [C] (or [1,..,1,C]) contiguous vector matching the last dim of a
+// contiguous `a`/`out` pair of equal shape?
+inline bool row_broadcast_case(const NeuralTensor *out, const NeuralTensor *a, const NeuralTensor *b)
+{
+    if (out->ndim < 1 || a->ndim != out->ndim || !is_contiguous(out) || !is_contiguous(a) || !is_contiguous(b))
+        return false;
+    for (int64_t i = 0; i < out->ndim; i++)
+        if (a->shape[i] != out->shape[i]) return false;
+    const int64_t C = out->shape[out->ndim - 1];
+    if (b->ndim < 1 || b->shape[b->ndim - 1] != C) return false;
+    for (int64_t i = 0; i + 1 < b->ndim; i++)
+        if (b->shape[i] != 1) return false;
+    const int64_t vn = out->dtype == NEURAL_DTYPE_FLOAT32 ? 4 : 2;
+    return C % vn == 0;
+}
+
+template <typename T, typename Op>
+int launch_binary(NeuralTensor *out, const NeuralTensor *a, const NeuralTensor *b, const void *pa,
+                         const void *pb, void *po, Op op)
+{
+    const int64_t n = numel(out);
+    const T *A = static_cast<const T *>(pa);
+    const T *B = static_cast<const T *>(pb);
+    T *O = static_cast<T *>(po);
+    if (numel(a) == n && numel(b) == n && is_contiguous(a) && is_contiguous(b) && is_contiguous(out))
+        return launch_map2_flat(A, B, O, n, op);
+    if (row_broadcast_case(out, a, b) && aligned16(A) && aligned16(B) && aligned16(O)) {
+        const int64_t C = out->shape[out->ndim - 1];
+        return launch_rowbcast(A, B, O, n / C, C, op);
+    }
+    ND4 d;
+    NH_TRY(build_nd(out, a, b, d));
+    hipLaunchKernelGGL((k_map2_nd<T, Op>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(), A, B, O, n, d, op);
+    return check_launch();
+}
+
+// Binary op on tensors: flat when all three are contiguous and equal in size,
+// the row-broadcast kernel for [.., C] (+) [C], else the strided N-D kernel.
+template <typename Op>
+int binary_api(NeuralTensor *out, const NeuralTensor *a, const NeuralTensor *b, Op op)
+{
+    NH_TRY(ensure_init());
+    if (!out || !a || !b) return set_error(NEURAL_ERR_NULL_POINTER);
+    NH_TRY(check_tensor(out));
+    NH_TRY(check_tensor(a));
+    NH_TRY(check_tensor(b));
+    if (a->dtype != out->dtype || b->dtype != out->dtype) return set_error(NEURAL_ERR_DTYPE_MISMATCH);
+    const int64_t n = numel(out);
+    if (n == 0) return set_error(NEURAL_OK);
+    const void *pa = nullptr, *pb = nullptr;
+    void *po = nullptr;
+    NH_TRY(dev_read(a, &pa));
+    NH_TRY(dev_read(b, &pb));
+    NH_TRY(dev_write(out, &po, is_contiguous(out)));
+    if (out->dtype == NEURAL_DTYPE_FLOAT32) NH_TRY((launch_binary<float, Op>(out, a, b, pa, pb, po, op)));
+    else NH_TRY((launch_binary<double, Op>(out, a, b, pa, pb, po, op)));
+    NH_TRY(dev_written(out));
+    return set_error(NEURAL_OK);
+}
+
 }  // namespace nh

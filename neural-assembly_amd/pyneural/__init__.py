@@ -4,7 +4,8 @@ implementation of Neural-Assembly's tensor hot path.
 
 Public names follow the reference package for this path: Tensor, zeros,
 ones, tensor; nn.ReLU/Sigmoid/Softmax/Tanh, nn.CrossEntropyLoss /
-LabelSmoothingCrossEntropy; activations.*; Quantizer /
+LabelSmoothingCrossEntropy, nn.Dropout (+ dropout_seed), fused add_relu /
+bias_add_act; activations.*; Quantizer /
 QuantParams; optim.SGD/Adam/AdamW; training.NaNDetector / grad_l2_norm /
 clip_grad_norm / clip_grad_value; save_checkpoint / load_checkpoint;
 tensor_ops.*.
@@ -14,7 +15,8 @@ from .core import (NeuralError, NeuralDtype, NeuralException, init, shutdown, ve
                    get_error_message, clear_error, set_stream, synchronize, device_info)
 from .tensor import Tensor, zeros, ones, tensor
 from . import nn, activations, optim, quantize, training, tensor_ops, checkpoint
-from .nn import ReLU, Sigmoid, Softmax, LogSoftmax, Tanh, CrossEntropyLoss, LabelSmoothingCrossEntropy
+from .nn import (ReLU, Sigmoid, Softmax, LogSoftmax, Tanh, CrossEntropyLoss, LabelSmoothingCrossEntropy, Dropout,
+                 dropout_seed, add_relu, bias_add_act)
 from .activations import GELU, LeakyReLU, ELU, SELU, Swish, Mish, HardSwish, Softplus, HardTanh
 from .optim import SGD, Adam, AdamW
 from .quantize import Quantizer, QuantParams

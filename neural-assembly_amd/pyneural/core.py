@@ -179,6 +179,9 @@ _SIGS = {
     "neural_scalar_mul": (_i, [_vp, _vp, _d]),
     "neural_neg": (_i, [_vp, _vp]),
     "neural_bias_add": (_i, [_vp, _vp, _vp]),
+    "neural_add_relu": (_i, [_vp, _vp, _vp]),
+    "neural_bias_add_act": (_i, [_vp, _vp, _vp, _i, _d]),
+    "vec_add_relu_fusion": (None, [_vp, _vp, _vp, _i64]),
     "simd_add_f32": (_i, [_vp, _vp, _vp, _u64]),
     "simd_mul_f32": (_i, [_vp, _vp, _vp, _u64]),
     "simd_fma_f32": (_i, [_vp, _vp, _vp, _vp, _u64]),
@@ -253,6 +256,10 @@ _SIGS = {
     "neural_tensor_grad_l2_norm": (_f, [_vp, _u64]),
     "neural_scan_nan_inf_l2": (_i, [_vp, _u64, _ip, _ip, _dp]),
     "neural_tensor_scan": (_i, [_vp, _ip, _ip, _dp]),
+    "neural_dropout_forward": (_i, [_vp, _vp, _vp, _u64, _f]),
+    "neural_dropout_backward": (_i, [_vp, _vp, _vp, _u64, _f]),
+    "neural_dropout_seed": (_i, [ctypes.c_uint32]),
+    "neural_dropout_draws": (_u64, []),
     # tensor ops
     "tensor_concat_2d": (_i, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _i64p, _i64p]),
     "tensor_split_2d": (_i, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64p, _i64p, _i64p, _i64p]),

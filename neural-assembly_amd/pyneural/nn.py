@@ -5,12 +5,18 @@ neural_softmax over the last dim) and Tanh (nn.py:176-190 -> act_tanh), plus
 LogSoftmax (rows, formula of metrics_losses.c:47-64).  Each allocates the
 output and makes one library call.  Loss modules: CrossEntropyLoss
 (nn.py:629-654 -> neural_cross_entropy_loss) and LabelSmoothingCrossEntropy
-(nn.py:657-751 -> label_smoothing_ce_forward / _backward).
+(nn.py:657-751 -> label_smoothing_ce_forward / _backward).  Dropout
+(nn.py:193-301 -> neural_dropout_forward / _backward) keeps its mask in device
+memory.  Fused epilogues: add_relu (vec_add_relu_fusion, fusion.asm:200-226)
+and bias_add_act (bias add of nn_layers.asm:472-539 followed by an
+activation, one pass).
 """
 
 import ctypes
 
-from .core import _lib, _check_error
+import numpy as np
+
+from .core import _lib, _check_error, NeuralDtype
 from .tensor import Tensor
 
 
@@ -175,3 +181,90 @@ class LabelSmoothingCrossEntropy(Module):
     def __repr__(self) -> str:
         return f"LabelSmoothingCrossEntropy(num_classes={self.num_classes}, smoothing={self.smoothing})"
 
+
+
+class Dropout(Module):
+    """Inverted dropout: in training, each element is zeroed with probability
+    ``p`` and the rest are scaled by ``1 / (1 - p)``; identity in eval mode.
+    Draws come from the library's copy of the C library's rand() stream (see
+    ``dropout_seed``), one per element, as the reference's kernel draws them.
+    float32 tensors only (the reference kernel reads float data)."""
+
+    def __init__(self, p: float = 0.5):
+        super().__init__()
+        if not 0.0 <= p <= 1.0:
+            raise ValueError(f"Dropout probability must be in [0, 1], got {p}")
+        self.p = p
+        self._mask = None  # device bytes, held in a float32 tensor of ceil(n / 4) words
+        self._numel = 0
+
+    @staticmethod
+    def _mask_buffer(numel: int) -> Tensor:
+        return Tensor.zeros([max((numel + 3) // 4, 1)], NeuralDtype.FLOAT32)
+
+    def forward(self, x: Tensor) -> Tensor:
+        if not self.training or self.p == 0.0:
+            out = Tensor.create(x.shape, x.dtype)
+            _check_error(_lib.neural_tensor_copy(out._ptr, x._ptr), "dropout (identity)")
+            return out
+        numel = x.numel
+        if self.p == 1.0:  # all dropped, no draws taken (reference nn.py:241-249)
+            self._mask, self._numel = self._mask_buffer(numel), numel
+            return Tensor.zeros(x.shape, x.dtype)
+        if x.dtype != NeuralDtype.FLOAT32:
+            raise TypeError("dropout works on float32 tensors")
+        src = x.contiguous()
+        out = Tensor.create(x.shape, x.dtype)
+        mask = self._mask_buffer(numel)
+        _check_error(_lib.neural_dropout_forward(src.device_ptr, out.device_ptr, mask.device_ptr, numel,
+                                                 ctypes.c_float(self.p)), "dropout forward")
+        self._mask, self._numel = mask, numel
+        return out
+
+    def backward(self, grad_output: Tensor) -> Tensor:
+        if self._mask is None:
+            raise RuntimeError("Dropout.backward called before forward")
+        go = grad_output.contiguous()
+        gi = Tensor.create(grad_output.shape, grad_output.dtype)
+        _check_error(_lib.neural_dropout_backward(go.device_ptr, gi.device_ptr, self._mask.device_ptr, self._numel,
+                                                  ctypes.c_float(self.p)), "dropout backward")
+        return gi
+
+    def mask(self) -> "np.ndarray":
+        """The last forward's keep mask (uint8, one byte per element)."""
+        if self._mask is None:
+            return np.zeros(0, dtype=np.uint8)
+        return self._mask.numpy().view(np.uint8)[: self._numel].copy()
+
+    def __repr__(self) -> str:
+        return f"Dropout(p={self.p})"
+
+
+def dropout_seed(seed: int) -> None:
+    """Position the dropout stream as srand(seed) positions the C library's
+    rand() (the stream starts as srand(1))."""
+    _check_error(_lib.neural_dropout_seed(ctypes.c_uint32(seed & 0xFFFFFFFF)), "dropout seed")
+
+
+def add_relu(a: Tensor, b: Tensor) -> Tensor:
+    """max(0, a + b) in one pass (b broadcasts, e.g. a [.., C] bias)."""
+    out = Tensor.create(a.shape, a.dtype)
+    _check_error(_lib.neural_add_relu(out._ptr, a._ptr, b._ptr), "add_relu")
+    return out
+
+
+ACTIVATIONS = {"none": 0, "relu": 1, "sigmoid": 2, "tanh": 3, "gelu": 4, "leaky_relu": 5, "elu": 6, "selu": 7,
+               "swish": 8, "mish": 9, "hardswish": 10, "softplus": 11, "hardtanh": 12}
+
+
+def bias_add_act(x: Tensor, bias: Tensor, activation: str = "relu", alpha: float = None) -> Tensor:
+    """act(x + bias) for x [.., C] and bias [C] in one pass; equal bit for bit
+    to the bias add followed by the activation.  alpha defaults to 0.01 for
+    leaky_relu and 1.0 for elu (the reference's defaults)."""
+    code = ACTIVATIONS[activation]
+    if alpha is None:
+        alpha = 0.01 if activation == "leaky_relu" else 1.0
+    out = Tensor.create(x.shape, x.dtype)
+    _check_error(_lib.neural_bias_add_act(out._ptr, x._ptr, bias._ptr, code, ctypes.c_double(alpha)),
+                 "bias_add_act")
+    return out

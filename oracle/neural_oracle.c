@@ -936,3 +936,59 @@ void ora_clip_grad_value(void **grads, const int *dtypes, const int64_t *ns, int
         }
     }
 }
+
+/* ---- dropout and the fused add + relu -------------------------------------------- */
+
+/* cvtsd2si under the default MXCSR rounding (nearest even); NaN and values
+ * outside int64 give the integer indefinite INT64_MIN. */
+static int64_t ora_cvtsd2si(double v)
+{
+    if (!(v >= -0x1p63 && v < 0x1p63)) return INT64_MIN;
+    return (int64_t)nearbyint(v);
+}
+
+void ora_srand(unsigned seed) { srand(seed); }
+
+/* dropout_forward (training_ops.asm:718-790) with the C library's rand(), as
+ * the reference calls it: p widened to double (cvtss2sd, 734);
+ * scale = (float)(1.0 / (1.0 - p)) (divsd + cvtsd2ss, 736-739); threshold =
+ * cvtsd2si(p * 2147483647.0) (743-744); per element one rand() (753),
+ * sign-extended and compared signed (757-759): r < threshold drops (mask 0,
+ * out +0.0f, 768-772), else mask 1 and out = in * scale (mulss, 762-765). */
+int ora_dropout_forward(const float *in, float *out, uint8_t *mask, uint64_t n, float p)
+{
+    const double pd = (double)p;
+    const float scale = (float)(1.0 / (1.0 - pd));
+    const int64_t th = ora_cvtsd2si(pd * 2147483647.0);
+    for (uint64_t i = 0; i < n; i++) {
+        const int64_t r = (int64_t)rand();
+        if (r < th) {
+            mask[i] = 0;
+            out[i] = 0.0f;
+        } else {
+            mask[i] = 1;
+            out[i] = in[i] * scale;
+        }
+    }
+    return 0;
+}
+
+/* dropout_backward (training_ops.asm:804-858): any nonzero mask byte keeps
+ * (movzx + test, 832-834),
+ * grad_in = grad_out * scale (mulss); else +0.0f. */
+int ora_dropout_backward(const float *go, float *gi, const uint8_t *mask, uint64_t n, float p)
+{
+    const float scale = (float)(1.0 / (1.0 - (double)p));
+    for (uint64_t i = 0; i < n; i++) gi[i] = mask[i] ? go[i] * scale : 0.0f;
+    return 0;
+}
+
+/* vec_add_relu_fusion (fusion.asm:200-226): addss then maxss with +0, i.e.
+ * s = a + b; c = s > 0 ? s : +0 (NaN and -0 give +0). */
+void ora_add_relu_f32(const float *a, const float *b, float *c, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++) {
+        const float s = a[i] + b[i];
+        c[i] = s > 0.0f ? s : 0.0f;
+    }
+}

@@ -143,4 +143,14 @@ int ora_ce_loss_f64(const double *x, const double *tgt, int64_t batch, int64_t c
 double ora_clip_grad_norm(void **grads, const int *dtypes, const int64_t *ns, int64_t count, double max_norm);
 void   ora_clip_grad_value(void **grads, const int *dtypes, const int64_t *ns, int64_t count, double lo, double hi);
 
+/* Dropout (training_ops.asm:717-858) with the C library's rand() -- the
+ * reference's own generator -- and vec_add_relu_fusion (fusion.asm:200-226).
+ * Pinned in tests/test_oracle_dropout.py: rand() against a restatement of
+ * glibc's TYPE_3 generator, hand-derived thresholds (p = 0.5 rounds half to
+ * even), keep rates, the closed forms of out and the backward. */
+void ora_srand(unsigned seed);
+int  ora_dropout_forward(const float *in, float *out, uint8_t *mask, uint64_t n, float p);
+int  ora_dropout_backward(const float *go, float *gi, const uint8_t *mask, uint64_t n, float p);
+void ora_add_relu_f32(const float *a, const float *b, float *c, int64_t n);
+
 #endif

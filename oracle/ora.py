@@ -385,3 +385,63 @@ def clip_grad_value(arrays, lo, hi):
                   ctypes.c_double]
     f(ptrs, dts, ns, n, lo, hi)
     return outs
+
+
+# ---- dropout ---------------------------------------------------------------------
+
+def glibc_rand(seed, n, skip=0):
+    """Restatement of glibc's rand() stream after srand(seed) (TYPE_3:
+    r[i] = r[i-31] + r[i-3] mod 2^32 after a Park-Miller fill and 310
+    discards; output r >> 1), draws skip .. skip + n - 1, as uint32."""
+    s = seed & 0xFFFFFFFF
+    s = s if s != 0 else 1
+    r = np.zeros(344 + skip + n, dtype=np.uint64)
+    r[0] = s
+    w = s if s < 2 ** 31 else s - 2 ** 32
+    for i in range(1, 31):
+        hi = int(w / 127773)
+        lo = w - hi * 127773
+        w = 16807 * lo - 2836 * hi
+        if w < 0:
+            w += 2147483647
+        r[i] = w
+    r[31:34] = r[0:3]
+    m = np.uint64(0xFFFFFFFF)
+    for i in range(34, 344 + skip + n):
+        r[i] = (r[i - 31] + r[i - 3]) & m
+    return (r[344 + skip:] >> np.uint64(1)).astype(np.uint32)
+
+
+def srand(seed):
+    lib().ora_srand(ctypes.c_uint(seed & 0xFFFFFFFF))
+
+
+def dropout_forward(x, p):
+    """dropout_forward with the C library's rand() from its current state."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    mask = np.empty(x.size, dtype=np.uint8)
+    f = lib().ora_dropout_forward
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_float]
+    rc = f(_p(x), _p(out), _p(mask), x.size, p)
+    return rc, out, mask
+
+
+def dropout_backward(go, mask, p):
+    go = np.ascontiguousarray(go, dtype=np.float32)
+    mask = np.ascontiguousarray(mask, dtype=np.uint8)
+    gi = np.empty_like(go)
+    f = lib().ora_dropout_backward
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_float]
+    rc = f(_p(go), _p(gi), _p(mask), go.size, p)
+    return rc, gi
+
+
+def add_relu(a, b):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    c = np.empty_like(a)
+    f = lib().ora_add_relu_f32
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+    f(_p(a), _p(b), _p(c), a.size)
+    return c

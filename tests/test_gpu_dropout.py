@@ -1,0 +1,150 @@
+"""Dropout parity (training_ops.asm:718-858) through the C-ABI.
+
+The device stream is compared with the C library's rand() itself: after
+neural_dropout_seed(s) and ora.srand(s), every forward call's mask and output
+must equal the oracle's (which calls rand() once per element, as the
+reference does) bit for bit -- across consecutive calls (the stream
+continues), for lengths around the 31-draw period and the 992-draw segment,
+for p on the threshold's rounding edge, and for host, device and unaligned
+buffers.  The backward is compared bit for bit with its closed form.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import GPU, same_bits
+
+pytestmark = GPU
+
+
+def _lib():
+    from pyneural.core import _lib
+    return _lib
+
+
+def _fwd_host(x, p):
+    out = np.empty_like(x)
+    mask = np.empty(x.size, np.uint8)
+    rc = _lib().neural_dropout_forward(x.ctypes.data, out.ctypes.data, mask.ctypes.data, x.size, ctypes.c_float(p))
+    assert rc == 0
+    return out, mask
+
+
+@pytest.mark.parametrize("seed", [1, 77, 2 ** 31 + 5])
+def test_stream_across_calls(pn, ora, seed):
+    rng = np.random.default_rng(seed & 0xFFFF)
+    assert _lib().neural_dropout_seed(ctypes.c_uint32(seed)) == 0
+    ora.srand(seed)
+    total = 0
+    for n in [1, 5, 30, 31, 32, 991, 992, 993, 1984, 100_003, 7, 65_536 * 3 + 1]:
+        x = rng.normal(0, 1, n).astype(np.float32)
+        p = 0.5 if n % 2 else 0.3
+        out, mask = _fwd_host(x, p)
+        _, wout, wmask = ora.dropout_forward(x, p)
+        same_bits(mask, wmask)
+        same_bits(out, wout)
+        total += n
+    assert _lib().neural_dropout_draws() == total
+
+
+@pytest.mark.parametrize("p", [0.0, 0.5, 0.1, 0.9, 1.0 / 3.0, 1.0, float("nan"), -0.25, 1.5])
+def test_probabilities(pn, ora, p):
+    rng = np.random.default_rng(3)
+    x = rng.normal(0, 2, 50_000).astype(np.float32)
+    x[::97] = np.nan
+    _lib().neural_dropout_seed(ctypes.c_uint32(12))
+    ora.srand(12)
+    out, mask = _fwd_host(x, p)
+    _, wout, wmask = ora.dropout_forward(x, p)
+    same_bits(mask, wmask)
+    same_bits(out, wout)
+
+
+def test_device_and_unaligned_buffers(pn, ora):
+    import torch
+    rng = np.random.default_rng(4)
+    n = 1_000_003
+    x = rng.normal(0, 1, n + 1).astype(np.float32)
+    xd = torch.from_numpy(x).cuda()
+    od = torch.empty(n + 1, device="cuda")
+    md = torch.empty(n + 4, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    _lib().neural_dropout_seed(ctypes.c_uint32(5))
+    ora.srand(5)
+    # aligned device buffers
+    assert _lib().neural_dropout_forward(xd.data_ptr(), od.data_ptr(), md.data_ptr(), n, ctypes.c_float(0.4)) == 0
+    _, wout, wmask = ora.dropout_forward(x[:n], 0.4)
+    same_bits(od.cpu().numpy()[:n], wout)
+    same_bits(md.cpu().numpy()[:n], wmask)
+    # element 1 onwards: 4-byte offset input/output, 1-byte offset mask
+    assert _lib().neural_dropout_forward(xd.data_ptr() + 4, od.data_ptr() + 4, md.data_ptr() + 1, n,
+                                         ctypes.c_float(0.4)) == 0
+    _, wout, wmask = ora.dropout_forward(x[1:], 0.4)
+    same_bits(od.cpu().numpy()[1:], wout)
+    same_bits(md.cpu().numpy()[1:n + 1], wmask)
+
+
+def test_large_stream(pn, ora):
+    # 64 M draws in one call (65 K segments) then a short continuation
+    n = 1 << 26
+    x = np.ones(n, np.float32)
+    _lib().neural_dropout_seed(ctypes.c_uint32(2024))
+    ora.srand(2024)
+    out, mask = _fwd_host(x, 0.25)
+    _, wout, wmask = ora.dropout_forward(x, 0.25)
+    same_bits(mask, wmask)
+    same_bits(out, wout)
+    out, mask = _fwd_host(x[:1000], 0.25)
+    _, wout, wmask = ora.dropout_forward(x[:1000], 0.25)
+    same_bits(mask, wmask)
+
+
+def test_backward(pn, ora):
+    rng = np.random.default_rng(6)
+    n = 300_007
+    go = rng.normal(0, 1, n).astype(np.float32)
+    go[::101] = np.inf
+    mask = rng.integers(0, 4, n).astype(np.uint8)  # any nonzero byte keeps
+    for p in [0.5, 0.2, 0.0]:
+        gi = np.empty_like(go)
+        assert _lib().neural_dropout_backward(go.ctypes.data, gi.ctypes.data, mask.ctypes.data, n,
+                                              ctypes.c_float(p)) == 0
+        _, want = ora.dropout_backward(go, mask, p)
+        same_bits(gi, want)
+
+
+def test_module(pn, ora):
+    rng = np.random.default_rng(7)
+    x = rng.normal(0, 1, (64, 257)).astype(np.float32)
+    t = pn.Tensor.from_numpy(x)
+    pn.dropout_seed(9)
+    ora.srand(9)
+    drop = pn.Dropout(0.3)
+    y = drop(t)
+    _, wout, wmask = ora.dropout_forward(x.reshape(-1), 0.3)
+    same_bits(y.numpy().reshape(-1), wout)
+    same_bits(drop.mask(), wmask)
+    g = rng.normal(0, 1, x.shape).astype(np.float32)
+    gi = drop.backward(pn.Tensor.from_numpy(g))
+    _, wg = ora.dropout_backward(g.reshape(-1), wmask, 0.3)
+    same_bits(gi.numpy().reshape(-1), wg)
+    drop.eval()
+    same_bits(drop(t).numpy(), x)
+    drop.train()
+    drop.p = 1.0
+    before = _lib().neural_dropout_draws()
+    assert not drop(t).numpy().any()
+    assert _lib().neural_dropout_draws() == before  # p == 1 takes no draws
+    with pytest.raises(ValueError):
+        pn.Dropout(1.5)
+
+
+def test_errors(pn):
+    lib = _lib()
+    buf = np.zeros(4, np.float32)
+    m = np.zeros(4, np.uint8)
+    assert lib.neural_dropout_forward(None, buf.ctypes.data, m.ctypes.data, 4, ctypes.c_float(0.5)) == 1
+    assert lib.neural_dropout_backward(buf.ctypes.data, buf.ctypes.data, None, 4, ctypes.c_float(0.5)) == 1
+    assert lib.neural_dropout_forward(buf.ctypes.data, buf.ctypes.data, m.ctypes.data, 0, ctypes.c_float(0.5)) == 0
