@@ -24,11 +24,11 @@
 // Parallel generation on the device: the recurrence is linear, so for the
 // anchor window W = r[A .. A+30] any later value is r[A + k] = sum_m c_m W[m]
 // with c = x^k mod P(x), P(x) = x^31 - x^28 - 1, coefficients mod 2^32.
-// The n draws of a call are cut into segments of L = 992 draws (32 periods
+// The n draws of a call are cut into segments of L = 248 draws (8 periods
 // of 31).  T[j] = x^(jL) mod P is a device table computed once; thread j
 // builds its starting window from T[j] and W (961 multiply-adds), then runs
-// the recurrence for its 992 draws with the 31-value ring in registers and
-// packs keep bits into 31 words.  A second, streaming kernel reads x in
+// the recurrence for its 248 draws with the 31-value ring in registers and
+// packs keep bits into 8 words.  A second, streaming kernel reads x in
 // 16-byte vectors, the 4 keep bits of each vector, and writes out and the
 // mask bytes (9 B per element).  The window after the call (r at A + n ..
 // A + n + 30) is written by the threads that generate the last 31 draws.
@@ -43,9 +43,13 @@
 namespace nh {
 
 constexpr int kLag = 31;                       // r[i] = r[i-31] + r[i-3]
-constexpr int kPeriods = 32;
-constexpr int64_t kSegL = int64_t(kLag) * kPeriods;   // 992 draws per thread segment
-constexpr int kSegWords = kPeriods * kLag / 32;        // 31 keep-bit words per segment
+// Segments of 8 periods: the jump (961 quarter-rate multiplies per segment)
+// then costs ~3/4 of the kernel, but 4 waves per SIMD hide the latencies one
+// wave cannot (measured on 64 M draws: 32 periods 68 us, 16 periods 47 us,
+// 8 periods 41 us).
+constexpr int kPeriods = 8;
+constexpr int64_t kSegL = int64_t(kLag) * kPeriods;   // 248 draws per thread segment (a multiple of 4)
+constexpr int kSegWords = int((kSegL + 31) / 32);      // keep-bit words per segment (8)
 constexpr int kDBlock = 256;
 
 // ---- polynomials mod P(x) = x^31 - x^28 - 1 over Z / 2^32 ------------------------------
@@ -87,30 +91,41 @@ __global__ __launch_bounds__(kDBlock) void k_jump_table(uint32_t *__restrict__ T
 }
 
 // Generate the keep bits of segment j.  W is the anchor window, Wn receives
-// the window after the call.  keep = (r >> 1) >= thr.
+// the window after the call.  keep = (r >> 1) >= thr, taken as the sign bit of
+// thr_m1 - (r >> 1) with thr_m1 = thr - 1 (mod 2^32; both sides fit in 32 bits,
+// and thr = 0 keeps every draw): no compare, so no chain through VCC.  One period of 31 draws
+// is unrolled (ring slots are then registers) and the period loop is not:
+// the fully unrolled segment is ~50 KB of straight-line code, and fetching it
+// cold made the kernel instruction-fetch bound (measured 4x slower).
 template <bool TAIL>
-NH_DEV void gen_segment(uint32_t (&w)[kLag], int64_t d0, int64_t n, uint32_t thr, uint32_t *__restrict__ bits,
+NH_DEV void gen_segment(uint32_t (&w)[kLag], int64_t d0, int64_t n, uint32_t thr_m1, uint32_t *__restrict__ bits,
                         uint32_t *__restrict__ Wn)
 {
-    uint32_t acc = 0u;
-    int i = 0;
+    uint64_t acc = 0u;  // pending keep bits; the low `have` are valid
+    int have = 0;
+    int word = 0;
+#pragma unroll 1
     for (int per = 0; per < kPeriods; per++) {
+        uint32_t pb = 0u;
 #pragma unroll
         for (int u = 0; u < kLag; u++) {
             const uint32_t r = w[u] + w[(u + 28) % kLag];
             w[u] = r;
-            acc |= uint32_t((r >> 1) >= thr) << (i & 31);
+            pb |= ((thr_m1 - (r >> 1)) >> (31 - u)) & (1u << u);
             if constexpr (TAIL) {
-                const int64_t d = d0 + i;
+                const int64_t d = d0 + int64_t(per) * kLag + u;
                 if (d < n && d >= n - kLag) Wn[d - (n - kLag)] = r;
             }
-            if ((i & 31) == 31) {
-                bits[i >> 5] = acc;
-                acc = 0u;
-            }
-            i++;
+        }
+        acc |= uint64_t(pb) << have;
+        have += kLag;
+        if (have >= 32) {
+            bits[word++] = uint32_t(acc);
+            acc >>= 32;
+            have -= 32;
         }
     }
+    if (have > 0) bits[word] = uint32_t(acc);  // only when L is not a multiple of 32
 }
 
 __global__ __launch_bounds__(kDBlock) void k_dropout_bits(const uint32_t *__restrict__ T, const uint32_t *__restrict__ W,
@@ -140,13 +155,13 @@ __global__ __launch_bounds__(kDBlock) void k_dropout_bits(const uint32_t *__rest
     }
     const int64_t d0 = j * kSegL;
     uint32_t *b = bits + j * kSegWords;
-    if (d0 + kSegL > n - kLag) gen_segment<true>(w, d0, n, thr, b, Wn);
-    else gen_segment<false>(w, d0, n, thr, b, Wn);
+    if (d0 + kSegL > n - kLag) gen_segment<true>(w, d0, n, thr - 1u, b, Wn);
+    else gen_segment<false>(w, d0, n, thr - 1u, b, Wn);
 }
 
 constexpr int kDUnroll = 2;
 
-// Keep bit of draw d: segment d / L, bit d % L of its 31 words.  I = uint32_t
+// Keep bit of draw d: segment d / L, bit d % L of its words.  I = uint32_t
 // when every index fits (a division by the constant L is then a multiply-high
 // and a shift).
 template <typename I>

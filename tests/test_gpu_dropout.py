@@ -4,7 +4,7 @@ The device stream is compared with the C library's rand() itself: after
 neural_dropout_seed(s) and ora.srand(s), every forward call's mask and output
 must equal the oracle's (which calls rand() once per element, as the
 reference does) bit for bit -- across consecutive calls (the stream
-continues), for lengths around the 31-draw period and the 992-draw segment,
+continues), for lengths around the 31-draw period and the 248-draw segment,
 for p on the threshold's rounding edge, and for host, device and unaligned
 buffers.  The backward is compared bit for bit with its closed form.
 """
@@ -38,7 +38,7 @@ def test_stream_across_calls(pn, ora, seed):
     assert _lib().neural_dropout_seed(ctypes.c_uint32(seed)) == 0
     ora.srand(seed)
     total = 0
-    for n in [1, 5, 30, 31, 32, 991, 992, 993, 1984, 100_003, 7, 65_536 * 3 + 1]:
+    for n in [1, 5, 30, 31, 32, 247, 248, 249, 496, 991, 992, 993, 100_003, 7, 65_536 * 3 + 1]:
         x = rng.normal(0, 1, n).astype(np.float32)
         p = 0.5 if n % 2 else 0.3
         out, mask = _fwd_host(x, p)
@@ -87,7 +87,7 @@ def test_device_and_unaligned_buffers(pn, ora):
 
 
 def test_large_stream(pn, ora):
-    # 64 M draws in one call (65 K segments) then a short continuation
+    # 64 M draws in one call (270 K segments) then a short continuation
     n = 1 << 26
     x = np.ones(n, np.float32)
     _lib().neural_dropout_seed(ctypes.c_uint32(2024))
