@@ -391,6 +391,19 @@ def suite(torch, pn, stream):
     hn, hi, ss = ctypes.c_int(), ctypes.c_int(), ctypes.c_double()
     timeit("nan/inf/l2 scan f32 100M (incl. D2H)",
            lambda: _lib.neural_tensor_scan(tg._ptr, ctypes.byref(hn), ctypes.byref(hi), ctypes.byref(ss)), 4 * na)
+    # per-feature transforms on [1M, 64] f64 (512 MB), device pointers
+    tb_rows, tb_f = 1 << 20, 64
+    tdat = torch.randn(tb_rows, tb_f, device=dev, dtype=torch.float64) * 3 + 1
+    tout = torch.empty_like(tdat)
+    tstat = [torch.empty(tb_f, device=dev, dtype=torch.float64) for _ in range(4)]
+    torch.cuda.synchronize()
+    timeit("transform_compute_stats f64 [1M,64] (mean/std/min/max)",
+           lambda: _lib.transform_compute_stats(tdat.data_ptr(), tb_rows, tb_f, *[s.data_ptr() for s in tstat]),
+           8 * tdat.numel())
+    timeit("transform_normalize f64 [1M,64]",
+           lambda: _lib.transform_normalize(tdat.data_ptr(), tout.data_ptr(), tb_rows, tb_f, tstat[0].data_ptr(),
+                                            tstat[1].data_ptr(), ctypes.c_double(1e-8)), 16 * tdat.numel())
+    del tdat, tout
     # gradient clipping over the same 100M gradients (no host readback).  A
     # negative max_norm clips on every call (scale -|max|/norm, magnitudes kept).
     glist = (ctypes.c_void_p * 1)(tg._ptr)

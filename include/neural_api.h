@@ -306,6 +306,20 @@ int tensor_pad_2d(const double *in, int64_t in_rows, int64_t in_cols, int64_t pa
                   double *out, int64_t *out_rows, int64_t *out_cols);
 int tensor_transpose2d_array(const double *in, int64_t rows, int64_t cols, double *out);
 
+/* ---- Per-feature transforms: neural_api.h:1115-1126, transforms.c:27-143 ---- */
+/* [batch, features] row-major float64, host or device pointers; 0 or -1 as
+ * the reference (NULL data / non-positive sizes).  compute_stats: any output
+ * may be NULL; min / max start at +-1e308 and keep the first of equal values;
+ * std is the population std sqrt(max(sum2/b - mean^2, 0)). */
+int transform_compute_stats(const double *data, int64_t batch_size, int64_t num_features, double *mean_out,
+                            double *std_out, double *min_out, double *max_out);          /* transforms.c:26 */
+int transform_normalize(const double *data, double *output, int64_t batch_size, int64_t num_features,
+                        const double *mean, const double *std, double eps);              /* transforms.c:69 */
+int transform_unnormalize(const double *data, double *output, int64_t batch_size, int64_t num_features,
+                          const double *mean, const double *std, double eps);            /* transforms.c:95 */
+int transform_minmax(const double *data, double *output, int64_t batch_size, int64_t num_features,
+                     const double *min_val, const double *max_val, double eps);          /* transforms.c:122 */
+
 /* ---- Cross-entropy losses --------------------------------------------------------- */
 /* Label-smoothed cross-entropy (replaces metrics_losses.c:28-125, declared at
  * neural_api.h:1101-1106): f64 logits [batch, num_classes], int64 targets;

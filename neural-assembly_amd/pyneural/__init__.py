@@ -8,13 +8,13 @@ LabelSmoothingCrossEntropy, nn.Dropout (+ dropout_seed), fused add_relu /
 bias_add_act; activations.*; Quantizer /
 QuantParams; optim.SGD/Adam/AdamW; training.NaNDetector / grad_l2_norm /
 clip_grad_norm / clip_grad_value; save_checkpoint / load_checkpoint;
-tensor_ops.*.
+transforms.Normalize / MinMaxScale / Compose / compute_stats; tensor_ops.*.
 """
 
 from .core import (NeuralError, NeuralDtype, NeuralException, init, shutdown, version, get_last_error,
                    get_error_message, clear_error, set_stream, synchronize, device_info)
 from .tensor import Tensor, zeros, ones, tensor
-from . import nn, activations, optim, quantize, training, tensor_ops, checkpoint
+from . import nn, activations, optim, quantize, training, tensor_ops, checkpoint, transforms
 from .nn import (ReLU, Sigmoid, Softmax, LogSoftmax, Tanh, CrossEntropyLoss, LabelSmoothingCrossEntropy, Dropout,
                  dropout_seed, add_relu, bias_add_act)
 from .activations import GELU, LeakyReLU, ELU, SELU, Swish, Mish, HardSwish, Softplus, HardTanh
@@ -22,6 +22,7 @@ from .optim import SGD, Adam, AdamW
 from .quantize import Quantizer, QuantParams
 from .training import NaNDetector, grad_l2_norm, clip_grad_norm, clip_grad_value
 from .checkpoint import save_checkpoint, load_checkpoint
+from .transforms import Normalize, MinMaxScale, Compose, compute_stats
 
 float32 = NeuralDtype.FLOAT32
 float64 = NeuralDtype.FLOAT64

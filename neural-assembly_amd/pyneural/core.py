@@ -256,6 +256,11 @@ _SIGS = {
     "neural_tensor_grad_l2_norm": (_f, [_vp, _u64]),
     "neural_scan_nan_inf_l2": (_i, [_vp, _u64, _ip, _ip, _dp]),
     "neural_tensor_scan": (_i, [_vp, _ip, _ip, _dp]),
+    # per-feature transforms
+    "transform_compute_stats": (_i, [_vp, _i64, _i64, _vp, _vp, _vp, _vp]),
+    "transform_normalize": (_i, [_vp, _vp, _i64, _i64, _vp, _vp, _d]),
+    "transform_unnormalize": (_i, [_vp, _vp, _i64, _i64, _vp, _vp, _d]),
+    "transform_minmax": (_i, [_vp, _vp, _i64, _i64, _vp, _vp, _d]),
     "neural_dropout_forward": (_i, [_vp, _vp, _vp, _u64, _f]),
     "neural_dropout_backward": (_i, [_vp, _vp, _vp, _u64, _f]),
     "neural_dropout_seed": (_i, [ctypes.c_uint32]),

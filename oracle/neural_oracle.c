@@ -992,3 +992,57 @@ void ora_add_relu_f32(const float *a, const float *b, float *c, int64_t n)
         c[i] = s > 0.0f ? s : 0.0f;
     }
 }
+
+/* ---- per-feature transforms (transforms.c) ----------------------------------------- */
+
+/* transform_compute_stats (transforms.c:27-62): per feature, one pass over the
+ * rows in order: sum += v, sum2 += v * v, mn starts at 1e308 and takes v only
+ * when v < mn (mx: -1e308, v > mx), so NaN never enters, the first of equal
+ * values (+0 / -0) stays, and values beyond +-1e308 leave the start value.
+ * mean = sum / b; var = sum2 / b - mean * mean, clamped at 0 (a NaN var
+ * stays NaN); std = sqrt(var).  NULL outputs are skipped. */
+int ora_transform_stats(const double *data, int64_t b, int64_t nf, double *mean, double *std, double *mn_out,
+                        double *mx_out)
+{
+    if (!data || b <= 0 || nf <= 0) return -1;
+    for (int64_t f = 0; f < nf; f++) {
+        double sum = 0.0, sum2 = 0.0, mn = 1e308, mx = -1e308;
+        for (int64_t i = 0; i < b; i++) {
+            const double v = data[i * nf + f];
+            sum += v;
+            sum2 += v * v;
+            if (v < mn) mn = v;
+            if (v > mx) mx = v;
+        }
+        const double m = sum / (double)b;
+        double var = sum2 / (double)b - m * m;
+        if (var < 0.0) var = 0.0;
+        if (mean) mean[f] = m;
+        if (std) std[f] = sqrt(var);
+        if (mn_out) mn_out[f] = mn;
+        if (mx_out) mx_out[f] = mx;
+    }
+    return 0;
+}
+
+/* transform_normalize / _unnormalize / _minmax (transforms.c:68-143):
+ * (x - mean) / (std + eps); x * (std + eps) + mean; (x - min) / (max - min + eps).
+ * mode 0, 1, 2 respectively; -1 on NULL pointers or non-positive sizes. */
+int ora_transform_apply(int mode, const double *data, double *out, int64_t b, int64_t nf, const double *p0,
+                        const double *p1, double eps)
+{
+    if (!data || !out || !p0 || !p1) return -1;
+    if (b <= 0 || nf <= 0) return -1;
+    for (int64_t i = 0; i < b; i++) {
+        for (int64_t f = 0; f < nf; f++) {
+            const int64_t idx = i * nf + f;
+            if (mode == 0) out[idx] = (data[idx] - p0[f]) / (p1[f] + eps);
+            else if (mode == 1) out[idx] = data[idx] * (p1[f] + eps) + p0[f];
+            else {
+                const double range = p1[f] - p0[f] + eps;
+                out[idx] = (data[idx] - p0[f]) / range;
+            }
+        }
+    }
+    return 0;
+}

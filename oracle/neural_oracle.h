@@ -20,10 +20,11 @@
  *     emulation of the asm order on tiny inputs and the fp64-exact value
  *     (math.fsum) within the rounding bound of the order.
  *   - ora_act_*, ora_quant*, ora_calibrate*, ora_dequant*, ora_adam*,
- *     ora_sgd*, ora_log_softmax_rows_*, ora_concat/split/pad/transpose:
- *     bit-for-bit against the reference's own C (activations_c.c,
- *     quantize.c, optimizers_c.c, metrics_losses.c, tensor_ops.c) compiled
- *     unchanged into oracle/_ref/libneural_ref.so.
+ *     ora_sgd*, ora_log_softmax_rows_*, ora_concat/split/pad/transpose,
+ *     ora_transform_*: bit-for-bit against the reference's own C
+ *     (activations_c.c, quantize.c, optimizers_c.c, metrics_losses.c,
+ *     tensor_ops.c, transforms.c) compiled unchanged into
+ *     oracle/_ref/libneural_ref.so.
  *   - ora_softmax_rows_*: fp64 closed form (numpy) within the f32 rounding
  *     bound; the f64 path also equals an unrolled numpy restatement bit for
  *     bit when the same libm exp is used.
@@ -152,5 +153,13 @@ void ora_srand(unsigned seed);
 int  ora_dropout_forward(const float *in, float *out, uint8_t *mask, uint64_t n, float p);
 int  ora_dropout_backward(const float *go, float *gi, const uint8_t *mask, uint64_t n, float p);
 void ora_add_relu_f32(const float *a, const float *b, float *c, int64_t n);
+
+/* Per-feature transforms (transforms.c:27-143): statistics and the three
+ * per-feature affine maps (mode 0 normalize, 1 unnormalize, 2 min-max).
+ * Pinned bit-exact against the reference's transforms.c (oracle/_ref). */
+int ora_transform_stats(const double *data, int64_t b, int64_t nf, double *mean, double *std, double *mn_out,
+                        double *mx_out);
+int ora_transform_apply(int mode, const double *data, double *out, int64_t b, int64_t nf, const double *p0,
+                        const double *p1, double eps);
 
 #endif

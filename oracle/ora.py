@@ -53,7 +53,8 @@ def lib():
 
 def ref():
     """The reference's C (activations_c.c, quantize.c, optimizers_c.c,
-    tensor_ops.c, metrics_losses.c) built by oracle/Makefile; None if absent."""
+    tensor_ops.c, metrics_losses.c, transforms.c) built by oracle/Makefile;
+    None if absent."""
     global _ref
     if _ref is None and REF_SO.exists():
         _ref = ctypes.CDLL(str(REF_SO))
@@ -445,3 +446,33 @@ def add_relu(a, b):
     f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
     f(_p(a), _p(b), _p(c), a.size)
     return c
+
+
+# ---- per-feature transforms ----------------------------------------------------------
+
+def transform_stats(data, use_ref=False):
+    """transform_compute_stats (transforms.c:27-62) on a [batch, features]
+    float64 array; use_ref runs the reference's own compiled C.  Returns
+    (rc, mean, std, min, max)."""
+    x = np.ascontiguousarray(data, dtype=np.float64)
+    b, nf = x.shape
+    outs = [np.zeros(nf) for _ in range(4)]
+    f = ref().transform_compute_stats if use_ref else lib().ora_transform_stats
+    rc = f(_p(x), ctypes.c_int64(b), ctypes.c_int64(nf), *[_p(o) for o in outs])
+    return (rc, *outs)
+
+
+def transform_apply(mode, data, p0, p1, eps, use_ref=False):
+    """mode 0 normalize, 1 unnormalize, 2 min-max (transforms.c:68-143)."""
+    x = np.ascontiguousarray(data, dtype=np.float64)
+    b, nf = x.shape
+    a0 = np.ascontiguousarray(p0, dtype=np.float64)
+    a1 = np.ascontiguousarray(p1, dtype=np.float64)
+    out = np.zeros_like(x)
+    if use_ref:
+        f = getattr(ref(), ["transform_normalize", "transform_unnormalize", "transform_minmax"][mode])
+        rc = f(_p(x), _p(out), ctypes.c_int64(b), ctypes.c_int64(nf), _p(a0), _p(a1), ctypes.c_double(eps))
+    else:
+        rc = lib().ora_transform_apply(ctypes.c_int(mode), _p(x), _p(out), ctypes.c_int64(b), ctypes.c_int64(nf),
+                                       _p(a0), _p(a1), ctypes.c_double(eps))
+    return rc, out
