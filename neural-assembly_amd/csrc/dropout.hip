@@ -393,7 +393,7 @@ float drop_scale(float p) { return float(1.0 / (1.0 - double(p))); }
 inline unsigned d_grid(int64_t work)
 {
     int64_t g = ceil_div(work, kDBlock);
-    const int64_t cap = int64_t(num_cus()) * 16;
+    const int64_t cap = kMaxGridBlocks;
     if (g > cap) g = cap;
     return unsigned(g < 1 ? 1 : g);
 }

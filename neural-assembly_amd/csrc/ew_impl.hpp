@@ -288,13 +288,13 @@ __global__ __launch_bounds__(kBlock) void k_map1_nd(const T *a, T *o, int64_t n,
 
 // ---- host-side launch helpers ---------------------------------------------------
 
-// Enough tiles for the whole range, capped at 32 blocks per CU (the
-// grid-stride loop covers the rest; measured best for 64 M-element streams).
+// One block per tile of the whole range (kMaxGridBlocks at most; the
+// grid-stride loop covers the rest).
 inline unsigned flat_grid(int64_t n, int vn)
 {
     const int64_t nv = n / vn;
     int64_t g = ceil_div(nv, int64_t(kBlock) * kUnroll);
-    const int64_t cap = int64_t(num_cus()) * 32;
+    const int64_t cap = kMaxGridBlocks;
     if (g > cap) g = cap;
     return unsigned(g < 1 ? 1 : g);
 }
@@ -302,7 +302,7 @@ inline unsigned flat_grid(int64_t n, int vn)
 inline unsigned strided_grid(int64_t n)
 {
     int64_t g = ceil_div(n, kBlock);
-    const int64_t cap = int64_t(num_cus()) * 16;
+    const int64_t cap = kMaxGridBlocks;
     if (g > cap) g = cap;
     return unsigned(g < 1 ? 1 : g);
 }
@@ -342,7 +342,7 @@ int launch_map1_f32_tail(const float *a, float *o, int64_t n, F f)
 {
     if (n <= 0) return NEURAL_OK;
     int64_t g = ceil_div(n / 4, int64_t(kBlock) * kTailUnroll);
-    const int64_t cap = int64_t(num_cus()) * 32;
+    const int64_t cap = kMaxGridBlocks;
     g = g > cap ? cap : (g < 1 ? 1 : g);
     hipLaunchKernelGGL((k_map1_f32_tail<F>), dim3(unsigned(g)), dim3(kBlock), 0, stream(), a, o, n, f);
     return check_launch();

@@ -297,7 +297,7 @@ __global__ __launch_bounds__(kQBlock) void k_dequantize_scalar(const int8_t *q, 
 inline unsigned q_grid(int64_t units, int64_t per_block)
 {
     int64_t g = ceil_div(units, per_block);
-    const int64_t cap = int64_t(num_cus()) * 32;
+    const int64_t cap = kMaxGridBlocks;
     if (g > cap) g = cap;
     return unsigned(g < 1 ? 1 : g);
 }

@@ -68,7 +68,7 @@ __global__ __launch_bounds__(256) void k_transpose(const double *in, double *o, 
 inline unsigned t_grid(int64_t n)
 {
     int64_t g = ceil_div(n, 256);
-    const int64_t cap = int64_t(num_cus()) * 16;
+    const int64_t cap = kMaxGridBlocks;
     if (g > cap) g = cap;
     return unsigned(g < 1 ? 1 : g);
 }

@@ -201,7 +201,7 @@ __global__ __launch_bounds__(kTBlock) void k_feat_map1(const double *__restrict_
 inline unsigned t_grid(int64_t work)
 {
     int64_t g = ceil_div(work, kTBlock);
-    const int64_t cap = int64_t(num_cus()) * 16;
+    const int64_t cap = kMaxGridBlocks;
     if (g > cap) g = cap;
     return unsigned(g < 1 ? 1 : g);
 }
