@@ -99,6 +99,13 @@ def test_large_stream(pn, ora):
     out, mask = _fwd_host(x[:1000], 0.25)
     _, wout, wmask = ora.dropout_forward(x[:1000], 0.25)
     same_bits(mask, wmask)
+    # just above the size where the keep bits are made on a second stream,
+    # with a length that is not a multiple of the chunking
+    m = (1 << 23) + 1003
+    out, mask = _fwd_host(x[:m], 0.6)
+    _, wout, wmask = ora.dropout_forward(x[:m], 0.6)
+    same_bits(mask, wmask)
+    same_bits(out, wout)
 
 
 def test_backward(pn, ora):
