@@ -21,6 +21,8 @@
 // sets a device flag and the call returns -1 (C API) / INVALID_ARGUMENT.
 #include <cmath>
 
+#include <type_traits>
+
 #include "reduce_impl.hpp"
 
 namespace nh {
@@ -93,6 +95,9 @@ __global__ __launch_bounds__(256) void k_ce_wave(const T *__restrict__ x, CeArgs
     if (r >= a.rows) return;  // uniform per wave
     const int64_t cols = a.cols;
     const T *xr = x + r * cols;
+    // the target first: its load overlaps the row's instead of following the reductions
+    int64_t t = 0;
+    const bool ok = loss_target(a.tidx, static_cast<const T *>(a.tval), r, cols, t);
     V v[VPL];
 #pragma unroll
     for (int k = 0; k < VPL; k++) {
@@ -117,7 +122,12 @@ __global__ __launch_bounds__(256) void k_ce_wave(const T *__restrict__ x, CeArgs
     // e_c = exp(x_c - m), kept for the gradient (the backward modes)
     constexpr bool KEEP = MODE == CE_LS_BWD || MODE == CE_LS_FUSED;
     V ev[KEEP ? VPL : 1];
-    double s = 0.0;
+    // Per-lane sums: double, except the f32 tensor loss, whose reference sums
+    // its float e_c in float (a lane's 16 float partial sums stay far inside
+    // that sum's own rounding); the wave sum is double either way.
+    using Acc = typename std::conditional<MODE == CE_ASM && sizeof(T) == 4, float, double>::type;
+    Acc sl = Acc(0);
+    Acc et = Acc(0);  // CE_ASM: e at the target column, in the lane that holds it
 #pragma unroll
     for (int k = 0; k < VPL; k++) {
         const int64_t c0 = (int64_t(k) * 64 + lane) * VN;
@@ -126,12 +136,11 @@ __global__ __launch_bounds__(256) void k_ce_wave(const T *__restrict__ x, CeArgs
             if (FULL || c0 + j < cols) {
                 const double e = sizeof(T) == 8 ? row_exp_d(double(v[k][j]), m) : row_exp_f(float(v[k][j]), m);
                 if constexpr (KEEP) ev[k][j] = T(e);
-                s += e;
+                if constexpr (MODE == CE_ASM) et = c0 + j == t ? Acc(e) : et;
+                sl += Acc(e);
             }
     }
-    s = wave_dsum(s);
-    int64_t t = 0;
-    const bool ok = loss_target(a.tidx, static_cast<const T *>(a.tval), r, cols, t);
+    double s = wave_dsum(double(sl));
     if (!ok) {
         if (lane == 0) {
             __hip_atomic_store(a.bad, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -140,18 +149,17 @@ __global__ __launch_bounds__(256) void k_ce_wave(const T *__restrict__ x, CeArgs
         return;
     }
     if (MODE == CE_ASM) {
-        // p_t = e_t / sum; loss = -log(p_t + 1e-7) (f32: e_t, sum, p_t and the loss rounded to float)
-        if (lane == 0) {
-            double lt;
-            if (sizeof(T) == 4) {
-                const float et = exp_d2f(double(xr[t]) - m);
-                const float p = et / float(s);
-                lt = double(float(-log(double(p) + 1e-7)));
-            } else {
-                lt = -log(row_exp_d(double(xr[t]), m) / s + 1e-7);
-            }
-            a.row_loss[r] = lt;
-        }
+        // p_t = e_t / sum (f32: e_t, sum and p_t rounded to float); the row's
+        // loss -log(p_t + 1e-7) is taken in the summing pass (RedCeLoss), where
+        // the double log runs on all lanes instead of on lane 0 of every row.
+        // e_t comes from the lane that computed it (the same value the
+        // reference's exp(x_t - m) gives), not from a second read of the row.
+        const int owner = int((t / VN) % 64);
+        const long long eb = __double_as_longlong(double(et));
+        const int lo = __builtin_amdgcn_readlane(int(eb), owner);
+        const int hi = __builtin_amdgcn_readlane(int(eb >> 32), owner);
+        const double e_t = __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<unsigned int>(lo));
+        if (lane == 0) a.row_loss[r] = sizeof(T) == 4 ? double(float(e_t) / float(s)) : e_t / s;
         return;
     }
     const double lse = log(s);
@@ -224,15 +232,8 @@ __global__ __launch_bounds__(256) void k_ce_block(const T *__restrict__ x, CeArg
     }
     if (MODE == CE_ASM) {
         if (threadIdx.x == 0) {
-            double lt;
-            if (sizeof(T) == 4) {
-                const float et = exp_d2f(double(xr[t]) - m);
-                const float p = et / float(s);
-                lt = double(float(-log(double(p) + 1e-7)));
-            } else {
-                lt = -log(row_exp_d(double(xr[t]), m) / s + 1e-7);
-            }
-            a.row_loss[r] = lt;
+            if (sizeof(T) == 4) a.row_loss[r] = double(exp_d2f(double(xr[t]) - m) / float(s));
+            else a.row_loss[r] = row_exp_d(double(xr[t]), m) / s;
         }
         return;
     }
@@ -277,6 +278,26 @@ static int launch_ce(const T *x, const CeArgs &a)
     return check_launch();
 }
 
+// Sum of the per-row losses of the tensor CE (losses.asm intended semantics):
+// the rows hold p_t, the loss term is -log(p_t + 1e-7), rounded to float for
+// f32 logits as the reference's float loss.
+template <bool F32>
+struct RedCeLoss {
+    using L = double;
+    using B = double;
+    NH_DEV L linit() const { return 0.0; }
+    NH_DEV void lacc(L &s, double p, int64_t) const
+    {
+        const double lt = -log(p + 1e-7);
+        s += F32 ? double(float(lt)) : lt;
+    }
+    NH_DEV L lcomb(L a, L b) const { return a + b; }
+    template <int TPR> NH_DEV B finish(L s, const double *, int64_t, int64_t) const { return s; }
+    NH_DEV B bident() const { return 0.0; }
+    NH_DEV B bcomb(B a, B b) const { return a + b; }
+    NH_DEV void store(void *out, int64_t r, B s, const double *, int64_t) const { static_cast<double *>(out)[r] = s; }
+};
+
 // Runs MODE over [rows, cols] logits already on the device; sums the per-row
 // losses into *loss_host (mean over rows) when wanted.  Returns NEURAL_OK,
 // NEURAL_ERR_INVALID_ARGUMENT for a target out of range, or an error code.
@@ -297,7 +318,10 @@ static int ce_run(const T *x, const int64_t *tidx, const T *tval, int64_t rows, 
     }
     CeArgs a{tidx, tval, rows, cols, alpha, 1.0 / double(rows), row_loss, grad_dev, bad};
     int rc = launch_ce<T, MODE>(x, a);
-    if (rc == NEURAL_OK && want_loss) rc = launch_reduce_full(row_loss, rows, RedSum<double, SUM_OUT_F64>{}, ws.result);
+    if (rc == NEURAL_OK && want_loss) {
+        if (MODE == CE_ASM) rc = launch_reduce_full(row_loss, rows, RedCeLoss<sizeof(T) == 4>{}, ws.result);
+        else rc = launch_reduce_full(row_loss, rows, RedSum<double, SUM_OUT_F64>{}, ws.result);
+    }
     struct { double sum; int pad[30]; int bad; } res;  // result area layout: sum at 0, flag at word 32
     static_assert(sizeof(res) == 136, "");
     if (rc == NEURAL_OK) rc = result_to_host(&res, ws.result, sizeof(res));
