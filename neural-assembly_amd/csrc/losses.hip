@@ -52,20 +52,25 @@ struct CeArgs {
     const void *tval;      // target values of the logits' dtype (tensor API) or null
     int64_t rows, cols;
     double alpha, inv_n;
-    double *row_loss;      // [rows] or null
+    double *row_loss;      // [rows] or null: p_t (tensor CE) or sum_c st_c (x_c - m) (label-smoothed)
+    double *row_s;         // [rows] or null: sum_c exp(x_c - m) (label-smoothed forward)
     void *grad;            // [rows, cols] or null
     int *bad;              // set to 1 when a target is out of range
 };
 
-// Per-element work once m, s (and lse) are known.  Returns the element's loss
-// term (label-smoothed: st * log_soft) and writes the gradient element.
+// Per-element work once m and s are known.  Returns the element's part of the
+// row loss without the log term (label-smoothed: st * (x - m)) and writes the
+// gradient element.  The row loss is -sum_c st_c ((x_c - m) - lse) =
+// lse * sum_c st_c - sum_c st_c (x_c - m); every term of the reference's sum
+// has one sign (x_c - m <= 0, lse >= 0), so the regrouping changes only the
+// last bits, and the log moves out of the row kernel into the summing pass.
 template <typename T, int MODE>
-NH_DEV double ce_elem(T xv, int64_t c, int64_t t, double m, double lse, double rs, const CeArgs &a, T &g)
+NH_DEV double ce_elem(T xv, int64_t c, int64_t t, double m, double rs, const CeArgs &a, T &g)
 {
     const double x = double(xv);
     const double st = a.alpha / double(a.cols) + (c == t ? 1.0 - a.alpha : 0.0);
     double term = 0.0;
-    if (MODE == CE_LS_FWD || MODE == CE_LS_FUSED) term = st * ((x - m) - lse);
+    if (MODE == CE_LS_FWD || MODE == CE_LS_FUSED) term = st * (x - m);
     if (MODE == CE_LS_BWD || MODE == CE_LS_FUSED) {
         const double e = sizeof(T) == 8 ? row_exp_d(x, m) : row_exp_f(float(xv), m);
         g = T(a.inv_n * (e * rs - st));
@@ -162,13 +167,11 @@ __global__ __launch_bounds__(256) void k_ce_wave(const T *__restrict__ x, CeArgs
         if (lane == 0) a.row_loss[r] = sizeof(T) == 4 ? double(float(e_t) / float(s)) : e_t / s;
         return;
     }
-    const double lse = log(s);
     const double rs = 1.0 / s;
     const double st0 = a.alpha / double(cols), st1 = st0 + (1.0 - a.alpha);
     // f32 rows: the per-element terms in float (the gradient is a float and
     // each loss term needs ~1e-7 of itself); the loss still sums in double
-    const float mf = float(m), lsef = float(lse), rsf = float(rs), st0f = float(st0), st1f = float(st1),
-                inf_ = float(a.inv_n);
+    const float mf = float(m), rsf = float(rs), st0f = float(st0), st1f = float(st1), inf_ = float(a.inv_n);
     double acc = 0.0;
     T *gr = static_cast<T *>(a.grad) + r * cols;
 #pragma unroll
@@ -181,11 +184,11 @@ __global__ __launch_bounds__(256) void k_ce_wave(const T *__restrict__ x, CeArgs
                 const bool at_t = c0 + j == t;
                 if constexpr (sizeof(T) == 4) {
                     const float st = at_t ? st1f : st0f;
-                    if (MODE == CE_LS_FWD || MODE == CE_LS_FUSED) acc += double(st * ((v[k][j] - mf) - lsef));
+                    if (MODE == CE_LS_FWD || MODE == CE_LS_FUSED) acc += double(st * (v[k][j] - mf));
                     if constexpr (KEEP) g[j] = inf_ * (ev[k][j] * rsf - st);
                 } else {
                     const double st = at_t ? st1 : st0;
-                    if (MODE == CE_LS_FWD || MODE == CE_LS_FUSED) acc += st * ((double(v[k][j]) - m) - lse);
+                    if (MODE == CE_LS_FWD || MODE == CE_LS_FUSED) acc += st * (double(v[k][j]) - m);
                     if constexpr (KEEP) g[j] = T(a.inv_n * (double(ev[k][j]) * rs - st));
                 }
             }
@@ -201,7 +204,10 @@ __global__ __launch_bounds__(256) void k_ce_wave(const T *__restrict__ x, CeArgs
     }
     if (MODE == CE_LS_FWD || MODE == CE_LS_FUSED) {
         acc = wave_dsum(acc);
-        if (lane == 0) a.row_loss[r] = -acc;
+        if (lane == 0) {
+            a.row_loss[r] = acc;
+            a.row_s[r] = s;
+        }
     }
 }
 
@@ -237,18 +243,20 @@ __global__ __launch_bounds__(256) void k_ce_block(const T *__restrict__ x, CeArg
         }
         return;
     }
-    const double lse = log(s);
     const double rs = 1.0 / s;
     double acc = 0.0;
     T *gr = static_cast<T *>(a.grad) + r * cols;
     for (int64_t c = threadIdx.x; c < cols; c += 256) {
         T g = T(0);
-        acc += ce_elem<T, MODE>(xr[c], c, t, m, lse, rs, a, g);
+        acc += ce_elem<T, MODE>(xr[c], c, t, m, rs, a, g);
         if (MODE == CE_LS_BWD || MODE == CE_LS_FUSED) gr[c] = g;
     }
     if (MODE == CE_LS_FWD || MODE == CE_LS_FUSED) {
         acc = G::reduce(acc, [](double p, double q) { return p + q; });
-        if (threadIdx.x == 0) a.row_loss[r] = -acc;
+        if (threadIdx.x == 0) {
+            a.row_loss[r] = acc;
+            a.row_s[r] = s;
+        }
     }
 }
 
@@ -298,6 +306,28 @@ struct RedCeLoss {
     NH_DEV void store(void *out, int64_t r, B s, const double *, int64_t) const { static_cast<double *>(out)[r] = s; }
 };
 
+// Sum of the label-smoothed row losses: row r holds A_r = sum_c st_c (x_c - m)
+// and s_r = sum_c exp(x_c - m); its loss is log(s_r) * S - A_r with
+// S = sum_c st_c = st0 (cols - 1) + st1.
+struct RedLsLoss {
+    using L = double;
+    using B = double;
+    const double *s;
+    double S;
+    NH_DEV L linit() const { return 0.0; }
+    NH_DEV void lacc(L &acc, double A, int64_t i) const
+    {
+        const double lse = log(s[i]);
+        const double sl = lse * S;
+        acc += sl - A;
+    }
+    NH_DEV L lcomb(L a, L b) const { return a + b; }
+    template <int TPR> NH_DEV B finish(L v, const double *, int64_t, int64_t) const { return v; }
+    NH_DEV B bident() const { return 0.0; }
+    NH_DEV B bcomb(B a, B b) const { return a + b; }
+    NH_DEV void store(void *out, int64_t r, B v, const double *, int64_t) const { static_cast<double *>(out)[r] = v; }
+};
+
 // Runs MODE over [rows, cols] logits already on the device; sums the per-row
 // losses into *loss_host (mean over rows) when wanted.  Returns NEURAL_OK,
 // NEURAL_ERR_INVALID_ARGUMENT for a target out of range, or an error code.
@@ -311,16 +341,23 @@ static int ce_run(const T *x, const int64_t *tidx, const T *tval, int64_t rows, 
     // to reset it.
     int *bad = static_cast<int *>(ws.result) + 32;
     const bool want_loss = MODE != CE_LS_BWD;
-    double *row_loss = nullptr;
+    constexpr bool kLs = MODE == CE_LS_FWD || MODE == CE_LS_FUSED;
+    double *row_loss = nullptr, *row_s = nullptr;
     if (want_loss) {
-        row_loss = static_cast<double *>(dev_alloc(size_t(rows) * sizeof(double)));
+        // one block: [rows] row values, then [rows] exp sums (label-smoothed)
+        row_loss = static_cast<double *>(dev_alloc(size_t(rows) * sizeof(double) * (kLs ? 2 : 1)));
         if (!row_loss) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
+        if (kLs) row_s = row_loss + rows;
     }
-    CeArgs a{tidx, tval, rows, cols, alpha, 1.0 / double(rows), row_loss, grad_dev, bad};
+    CeArgs a{tidx, tval, rows, cols, alpha, 1.0 / double(rows), row_loss, row_s, grad_dev, bad};
     int rc = launch_ce<T, MODE>(x, a);
     if (rc == NEURAL_OK && want_loss) {
-        if (MODE == CE_ASM) rc = launch_reduce_full(row_loss, rows, RedCeLoss<sizeof(T) == 4>{}, ws.result);
-        else rc = launch_reduce_full(row_loss, rows, RedSum<double, SUM_OUT_F64>{}, ws.result);
+        if (MODE == CE_ASM) {
+            rc = launch_reduce_full(row_loss, rows, RedCeLoss<sizeof(T) == 4>{}, ws.result);
+        } else {
+            const double st0 = alpha / double(cols), st1 = st0 + (1.0 - alpha);
+            rc = launch_reduce_full(row_loss, rows, RedLsLoss{row_s, st0 * double(cols - 1) + st1}, ws.result);
+        }
     }
     struct { double sum; int pad[30]; int bad; } res;  // result area layout: sum at 0, flag at word 32
     static_assert(sizeof(res) == 136, "");
