@@ -236,7 +236,7 @@ __global__ __launch_bounds__(kBlock) void k_rowbcast(const T *__restrict__ a, co
                 V res;
 #pragma unroll
                 for (int k = 0; k < VN; k++) res[k] = op(ra[u][k], rb[u][k]);
-                st_nt(ov + i, res);
+                ov[i] = res;
             }
         }
         c += dS;

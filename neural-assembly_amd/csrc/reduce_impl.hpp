@@ -106,8 +106,9 @@ struct Grp {
 // ---- the segment walk ---------------------------------------------------------------------
 
 // Reduce row elements [lo, hi) with a group of TPR lanes.  `vec` promises that
-// row is 16-byte aligned and lo is a multiple of the vector width.
-template <typename T, class Red, int TPR>
+// row is 16-byte aligned and lo is a multiple of the vector width.  NT: the
+// vector loads are non-temporal.
+template <typename T, class Red, int TPR, bool NT>
 NH_DEV typename Red::B seg_reduce(const Red &red, const T *__restrict__ row, int64_t lo, int64_t hi, bool vec)
 {
     using L = typename Red::L;
@@ -125,7 +126,7 @@ NH_DEV typename Red::B seg_reduce(const Red &red, const T *__restrict__ row, int
 #pragma unroll
             for (int u = 0; u < kRUnroll; u++) {
                 const int64_t i = c + int64_t(u) * TPR;
-                if (i < v1) r[u] = ld_nt(xv + i);
+                if (i < v1) r[u] = NT ? ld_nt(xv + i) : xv[i];
             }
 #pragma unroll
             for (int u = 0; u < kRUnroll; u++) {
@@ -192,7 +193,7 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_rows(const T *__restrict__ x
     const int64_t r = int64_t(blockIdx.x) * RPB + threadIdx.x / TPR;
     if (r >= rows) return;  // uniform per group (the grid covers whole blocks only when TPR == 256)
     const T *xr = x + r * ld;
-    const typename Red::B b = seg_reduce<T, Red, TPR>(red, xr, 0, cols, vec);
+    const typename Red::B b = seg_reduce<T, Red, TPR, false>(red, xr, 0, cols, vec);
     if (Grp<TPR>::lane() == 0) red.store(out, r, b, xr, cols);
 }
 
@@ -207,7 +208,7 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_seg(const T *__restrict__ x,
     const T *xr = x + r * ld;
     const int64_t lo = int64_t(blockIdx.x) * chunk;
     const int64_t hi = lo + chunk < cols ? lo + chunk : cols;
-    const typename Red::B b = seg_reduce<T, Red, kRBlock>(red, xr, lo, hi, vec);
+    const typename Red::B b = seg_reduce<T, Red, kRBlock, true>(red, xr, lo, hi, vec);
     if (threadIdx.x == 0) partials[r * int64_t(gridDim.x) + blockIdx.x] = b;
 }
 
