@@ -25,8 +25,11 @@
 // anchor window W = r[A .. A+30] any later value is r[A + k] = sum_m c_m W[m]
 // with c = x^k mod P(x), P(x) = x^31 - x^28 - 1, coefficients mod 2^32.
 // The n draws of a call are cut into segments of L = 248 draws (8 periods
-// of 31).  T[j] = x^(jL) mod P is a device table computed once; thread j
-// builds its starting window from T[j] and W (961 multiply-adds), then runs
+// of 31).  c_j = x^(jL) mod P is a device table computed once.  Segment j's
+// starting window is w_j[t] = r[A + jL + t] = sum_m c_j[m] G[m + t] with
+// G = r[A .. A+61] (the anchor window and the 31 values after it): for 64
+// segments at a time a [64 x 32] x [32 x 32] product mod 2^32, done on the
+// matrix cores (int8 MFMA over signed byte limbs, below).  Thread j then runs
 // the recurrence for its 248 draws with the 31-value ring in registers and
 // packs keep bits into 8 words.  A second, streaming kernel reads x in
 // 16-byte vectors, the 4 keep bits of each vector, and writes out and the
@@ -74,9 +77,41 @@ NH_DEV void dpoly_mul(uint32_t (&a)[kLag], const uint32_t *__restrict__ b)
     for (int i = 0; i < kLag; i++) a[i] = prod[i];
 }
 
-// T[j] = x^(j*L) mod P for j in [j0, j1): square-and-multiply over the
-// host-made powers B[k] = x^(L * 2^k) mod P.
-__global__ __launch_bounds__(kDBlock) void k_jump_table(uint32_t *__restrict__ T, int64_t j0, int64_t j1,
+// ---- the jump as an int8 matrix product ---------------------------------------------------
+//
+// A 32-bit value is split into balanced base-256 digits, v = sum_p l_p 256^p
+// (mod 2^32) with l_p in [-128, 127], so that products of digits fit the
+// signed int8 inputs of v_mfma_i32_32x32x16_i8.  For C (segments x m) and
+// H (m x t): C H = sum_{p+q <= 3} 256^(p+q) C_p H_q (mod 2^32) -- the
+// digit products with p + q >= 4 vanish mod 2^32.  Each D_s = sum_{p+q=s}
+// C_p H_q is exact in int32 (32 (s+1) terms of magnitude <= 2^14).
+// Operand layout of the 32x32x16 int8 MFMA: lane l holds row l % 32 of A
+// and column l % 32 of B, k = 8 (l / 32) + b for byte b of the 64-bit
+// operand; the 16 results of lane l are D[8 (v/4) + 4 (l/32) + v % 4][l % 32].
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+// Balanced base-256 digits of v, each as the low byte of l[p].
+__host__ __device__ inline void limbs4(uint32_t v, uint32_t (&l)[4])
+{
+    uint32_t u = v;
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const uint32_t b = u & 0xFFu;
+        l[p] = b;
+        const uint32_t sb = b >= 128u ? b - 256u : b;  // the digit, sign-extended mod 2^32
+        u = (u - sb) >> 8;
+    }
+}
+
+// Table layout: the A operands of segment j's row, wave block w = j / 64
+// (1024 64-bit words): word w*1024 + T*512 + (p*2 + c)*64 + lane holds
+// digit p of coefficients m = 16c + 8(lane/32) + b, b = 0..7, of segment
+// 64w + 32T + lane % 32 (m = 31 is padding, 0).
+constexpr int kTabWordsPerWave = 1024;
+
+// c_j = x^(j*L) mod P for j in [j0, j1), stored as MFMA A-operand digits:
+// square-and-multiply over the host-made powers B[k] = x^(L * 2^k) mod P.
+__global__ __launch_bounds__(kDBlock) void k_jump_table(uint64_t *__restrict__ TL, int64_t j0, int64_t j1,
                                                          const uint32_t *__restrict__ B)
 {
     const int64_t j = j0 + int64_t(blockIdx.x) * kDBlock + threadIdx.x;
@@ -86,8 +121,24 @@ __global__ __launch_bounds__(kDBlock) void k_jump_table(uint32_t *__restrict__ T
     for (int i = 0; i < kLag; i++) c[i] = i == 0 ? 1u : 0u;
     for (int k = 0; k < 63 && (j >> k) != 0; k++)
         if ((j >> k) & 1) dpoly_mul(c, B + k * kLag);
+    uint64_t *row = TL + (j >> 6) * kTabWordsPerWave + ((j >> 5) & 1) * 512 + (j & 31);
 #pragma unroll
-    for (int i = 0; i < kLag; i++) T[j * kLag + i] = c[i];
+    for (int h = 0; h < 2; h++) {
+#pragma unroll
+        for (int cc = 0; cc < 2; cc++) {
+            uint64_t q[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int b = 0; b < 8; b++) {
+                const int m = 16 * cc + 8 * h + b;
+                uint32_t l[4];
+                limbs4(m < kLag ? c[m] : 0u, l);
+#pragma unroll
+                for (int p = 0; p < 4; p++) q[p] |= uint64_t(l[p]) << (8 * b);
+            }
+#pragma unroll
+            for (int p = 0; p < 4; p++) row[(p * 2 + cc) * 64 + 32 * h] = q[p];
+        }
+    }
 }
 
 // Generate the keep bits of segment j.  W is the anchor window, Wn receives
@@ -128,31 +179,98 @@ NH_DEV void gen_segment(uint32_t (&w)[kLag], int64_t d0, int64_t n, uint32_t thr
     if (have > 0) bits[word] = uint32_t(acc);  // only when L is not a multiple of 32
 }
 
-__global__ __launch_bounds__(kDBlock) void k_dropout_bits(const uint32_t *__restrict__ T, const uint32_t *__restrict__ W,
-                                                           uint32_t *__restrict__ Wn, int64_t n, int64_t nseg,
-                                                           uint32_t thr, uint32_t *__restrict__ bits)
+// One thread per segment, 64 segments per wave.  X31 holds x^(31+i) mod P
+// for i < 31 (G[31 + i] = sum_m X31[i][m] W[m]).  Every wave of the grid
+// has table rows (the table covers a multiple of 256 segments >= nseg), so
+// all waves run the jump and reach every barrier; threads past nseg stop
+// before generating.
+__global__ __launch_bounds__(kDBlock) void k_dropout_bits(const uint64_t *__restrict__ TL,
+                                                           const uint32_t *__restrict__ X31,
+                                                           const uint32_t *__restrict__ W, uint32_t *__restrict__ Wn,
+                                                           int64_t n, int64_t nseg, uint32_t thr,
+                                                           uint32_t *__restrict__ bits)
 {
-    const int64_t j = int64_t(blockIdx.x) * kDBlock + threadIdx.x;
-    if (blockIdx.x == 0 && threadIdx.x < kLag && n + threadIdx.x < kLag)
-        Wn[threadIdx.x] = W[n + threadIdx.x];  // calls shorter than 31 draws keep part of the old window
-    if (j >= nseg) return;
-    // starting window: w[t] = r[A + jL + t] = sum_m (x^(jL+t) mod P)_m W[m]
-    uint32_t c[kLag], w[kLag];
-#pragma unroll
-    for (int i = 0; i < kLag; i++) c[i] = T[j * kLag + i];
-#pragma unroll
-    for (int t = 0; t < kLag; t++) {
-        uint32_t s = 0u;
-#pragma unroll
-        for (int m = 0; m < kLag; m++) s += c[m] * W[m];
-        w[t] = s;
-        // c <- c * x mod P
-        const uint32_t top = c[kLag - 1];
-#pragma unroll
-        for (int m = kLag - 1; m > 0; m--) c[m] = c[m - 1];
-        c[0] = top;
-        c[28] += top;
+    __shared__ uint32_t sG[64];
+    __shared__ uint64_t sB[8][64];
+    __shared__ uint32_t sX[kDBlock / 64][32 * kLag];  // per wave: one tile's 32 windows, row stride 31 (odd: no bank conflicts)
+    const int tid = threadIdx.x, lane = tid & 63;
+    if (blockIdx.x == 0 && tid < kLag && n + tid < kLag)
+        Wn[tid] = W[n + tid];  // calls shorter than 31 draws keep part of the old window
+    // G = r[A .. A+61] (G[62], G[63] = 0: they meet only padding coefficients)
+    if (tid < 64) {
+        uint32_t g = 0u;
+        if (tid < kLag) {
+            g = W[tid];
+        } else if (tid < 2 * kLag) {
+            for (int m = 0; m < kLag; m++) g += X31[(tid - kLag) * kLag + m] * W[m];
+        }
+        sG[tid] = g;
     }
+    __syncthreads();
+    // B operands, the same for every wave: digits of H[m][t] = G[m + t]
+    if (tid < 64) {
+        const int t = tid & 31, h = tid >> 5;
+#pragma unroll
+        for (int cc = 0; cc < 2; cc++) {
+            uint64_t q[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int b = 0; b < 8; b++) {
+                uint32_t l[4];
+                limbs4(sG[16 * cc + 8 * h + b + t], l);
+#pragma unroll
+                for (int p = 0; p < 4; p++) q[p] |= uint64_t(l[p]) << (8 * b);
+            }
+#pragma unroll
+            for (int p = 0; p < 4; p++) sB[p * 2 + cc][tid] = q[p];
+        }
+    }
+    __syncthreads();
+    long Bq[4][2];
+#pragma unroll
+    for (int p = 0; p < 4; p++)
+#pragma unroll
+        for (int cc = 0; cc < 2; cc++) Bq[p][cc] = long(sB[p * 2 + cc][lane]);
+    const int64_t wave = (int64_t(blockIdx.x) * kDBlock + tid) >> 6;
+    const uint64_t *tw = TL + wave * kTabWordsPerWave;
+    uint32_t *X = sX[tid >> 6];
+    // Two 32-segment tiles, transposed through LDS one at a time; one
+    // accumulator at a time (D_0 .. D_3 folded into `out` as they finish).
+    // Registers and LDS stay low enough for 5+ waves per SIMD, which the
+    // recurrence below needs to issue at full rate.
+    uint32_t w[kLag];
+#pragma unroll
+    for (int T = 0; T < 2; T++) {
+        long A[4][2];
+#pragma unroll
+        for (int p = 0; p < 4; p++)
+#pragma unroll
+            for (int cc = 0; cc < 2; cc++) A[p][cc] = long(tw[T * 512 + (p * 2 + cc) * 64 + lane]);
+        uint32_t out[16];
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            i32x16 d = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+            for (int p = 0; p <= s; p++)
+#pragma unroll
+                for (int cc = 0; cc < 2; cc++)
+                    d = __builtin_amdgcn_mfma_i32_32x32x16_i8(A[p][cc], Bq[s - p][cc], d, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 16; v++) out[v] = s == 0 ? uint32_t(d[v]) : out[v] + (uint32_t(d[v]) << (8 * s));
+        }
+        // result (row, t) of lane l, value v: row 8(v/4) + 4(l/32) + v%4, t = l % 32 (t = 31 is padding)
+        if ((lane & 31) < kLag) {
+#pragma unroll
+            for (int v = 0; v < 16; v++) X[(8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)) * kLag + (lane & 31)] = out[v];
+        }
+        __syncthreads();
+        if ((lane >> 5) == T) {
+#pragma unroll
+            for (int t = 0; t < kLag; t++) w[t] = X[(lane & 31) * kLag + t];
+        }
+        __syncthreads();
+    }
+    const int64_t j = wave * 64 + lane;
+    if (j >= nseg) return;
     const int64_t d0 = j * kSegL;
     uint32_t *b = bits + j * kSegWords;
     if (d0 + kSegL > n - kLag) gen_segment<true>(w, d0, n, thr - 1u, b, Wn);
@@ -315,9 +433,10 @@ struct Stream {
     bool ready = false;
     uint32_t *win[2] = {nullptr, nullptr};  // device windows (current, next)
     int cur = 0;
-    uint32_t *table = nullptr;              // T[j], kLag words each
-    int64_t table_n = 0;
+    uint64_t *table = nullptr;              // c_j = x^(jL) mod P as MFMA digits, 16 words per segment
+    int64_t table_n = 0;                    // segments covered (a power of two >= 1024)
     uint32_t *powers = nullptr;             // B[k] = x^(L 2^k) mod P, k < 63
+    uint32_t *x31 = nullptr;                // x^(31+i) mod P, i < 31
     uint32_t *bits = nullptr;
     size_t bits_cap = 0;
     uint64_t drawn = 0;                     // draws since the last seed
@@ -355,6 +474,14 @@ int ensure_stream_locked(Stream &s)
     s.powers = static_cast<uint32_t *>(dev_alloc(B.size() * sizeof(uint32_t)));
     if (!s.powers) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
     NH_HIP(hipMemcpy(s.powers, B.data(), B.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
+    std::vector<uint32_t> X(size_t(kLag) * kLag);
+    for (int i = 0; i < kLag; i++) {
+        const HPoly c = hpoly_xpow(uint64_t(kLag + i));
+        std::memcpy(X.data() + size_t(i) * kLag, c.data(), kLag * sizeof(uint32_t));
+    }
+    s.x31 = static_cast<uint32_t *>(dev_alloc(X.size() * sizeof(uint32_t)));
+    if (!s.x31) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
+    NH_HIP(hipMemcpy(s.x31, X.data(), X.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
     s.ready = true;
     return set_seed_locked(s, 1u);  // glibc's initial state is srand(1)
 }
@@ -365,10 +492,13 @@ int ensure_table_locked(Stream &s, int64_t nseg)
     if (nseg <= s.table_n) return NEURAL_OK;
     int64_t cap = s.table_n > 0 ? s.table_n : 1024;
     while (cap < nseg) cap *= 2;
-    uint32_t *t = static_cast<uint32_t *>(dev_alloc(size_t(cap) * kLag * sizeof(uint32_t)));
+    // 16 words per segment; a wave block's rows are contiguous, so the old
+    // table is a prefix of the new one
+    const size_t per_seg = kTabWordsPerWave / 64;
+    uint64_t *t = static_cast<uint64_t *>(dev_alloc(size_t(cap) * per_seg * sizeof(uint64_t)));
     if (!t) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
     if (s.table_n > 0)
-        NH_HIP(hipMemcpyAsync(t, s.table, size_t(s.table_n) * kLag * sizeof(uint32_t), hipMemcpyDeviceToDevice,
+        NH_HIP(hipMemcpyAsync(t, s.table, size_t(s.table_n) * per_seg * sizeof(uint64_t), hipMemcpyDeviceToDevice,
                               stream()));
     const int64_t fresh = cap - s.table_n;
     hipLaunchKernelGGL(k_jump_table, dim3(unsigned(ceil_div(fresh, kDBlock))), dim3(kDBlock), 0, stream(), t,
@@ -430,8 +560,10 @@ static int dropout_fwd(const float *in, float *out, uint8_t *mask, uint64_t n, f
     NH_TRY(xo.open(out, size_t(n) * 4, false));
     NH_TRY(xm.open(mask, size_t(n), false));
     uint32_t *W = s.win[s.cur], *Wn = s.win[s.cur ^ 1];
+    // the grid covers ceil(nseg / 256) * 256 <= table_n segments (table_n is a
+    // power of two >= 1024), so every wave reads existing table rows
     hipLaunchKernelGGL(k_dropout_bits, dim3(unsigned(ceil_div(nseg, kDBlock))), dim3(kDBlock), 0, stream(), s.table,
-                       W, Wn, nn, nseg, thr, s.bits);
+                       s.x31, W, Wn, nn, nseg, thr, s.bits);
     NH_TRY(check_launch());
     s.cur ^= 1;
     s.drawn += n;

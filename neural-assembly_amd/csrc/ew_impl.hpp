@@ -236,6 +236,9 @@ __global__ __launch_bounds__(kBlock) void k_rowbcast(const T *__restrict__ a, co
                 V res;
 #pragma unroll
                 for (int k = 0; k < VN; k++) res[k] = op(ra[u][k], rb[u][k]);
+                // default-policy store: measured faster than a non-temporal
+                // one here, and the row reductions that read the result next
+                // run faster after it
                 ov[i] = res;
             }
         }
