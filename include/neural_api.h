@@ -348,6 +348,164 @@ int label_smoothing_ce_fused_f32(const float *logits, const int64_t *targets, in
  * range, or non-contiguous tensors). */
 int neural_cross_entropy_loss(const NeuralTensor *prediction, const NeuralTensor *target, double *loss);
 
+/* ---- Reference entry points outside the hot path ---------------------------------
+ * The reference's Python layer binds every one of these names at import
+ * (pyneural/core.py; the line of each binding is given), so the library
+ * exports them for that loader to succeed.  The subsystems behind them
+ * (layers, recurrent cells, pooling, attention, fuzzy logic, pruning,
+ * datasets, config, metrics, TensorBoard writer, weight init, LR schedules,
+ * the asm optimizer handles, int8 matmul, percentile calibration) are outside
+ * this library's scope.  Each records NEURAL_ERR_NOT_IMPLEMENTED as the last
+ * error and returns: NEURAL_ERR_NOT_IMPLEMENTED (int neural_* functions), -1
+ * (other int and int64_t functions, the C modules' failure value), NULL
+ * (pointers), 0 (uint64_t), NaN (double).  The *_free functions and
+ * neural_optimizer_set_lr do nothing (no stub hands out an object);
+ * neural_get_simd_level / _name report that no host SIMD path exists. */
+int attention_scaled_dot_product(void *, void *, void *, void *, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, void *, void *);  /* core.py:1336 */
+int batchnorm1d_backward(void *, void *, void *, void *, void *, int64_t);  /* core.py:812 */
+int batchnorm1d_forward(void *, void *, void *, int64_t, int);  /* core.py:803 */
+int64_t batchnorm1d_num_features(void *);  /* core.py:834 */
+void *batchnorm1d_beta(void *);  /* core.py:825 */
+void *batchnorm1d_create(int64_t, double, double);  /* core.py:797 */
+void *batchnorm1d_gamma(void *);  /* core.py:822 */
+void *batchnorm1d_running_mean(void *);  /* core.py:828 */
+void *batchnorm1d_running_var(void *);  /* core.py:831 */
+void batchnorm1d_free(void *);  /* core.py:800 */
+int conv2d_layer_backward(void *, void *, void *, int64_t, int64_t, int64_t, void *, void *, void *);  /* core.py:1150 */
+int conv2d_layer_forward(void *, void *, int64_t, int64_t, int64_t, void *);  /* core.py:1140 */
+int64_t conv2d_layer_in_channels(void *);  /* core.py:1178 */
+int64_t conv2d_layer_kernel_h(void *);  /* core.py:1184 */
+int64_t conv2d_layer_kernel_w(void *);  /* core.py:1187 */
+int64_t conv2d_layer_out_channels(void *);  /* core.py:1181 */
+int64_t conv2d_layer_out_h(void *, int64_t);  /* core.py:1169 */
+int64_t conv2d_layer_out_w(void *, int64_t);  /* core.py:1172 */
+int64_t conv2d_layer_padding(void *);  /* core.py:1193 */
+int64_t conv2d_layer_stride(void *);  /* core.py:1190 */
+int64_t conv2d_layer_weight_size(void *);  /* core.py:1175 */
+int64_t conv2d_output_size(int64_t, int64_t, int64_t, int64_t);  /* core.py:1118 */
+void *conv2d_layer_bias(void *);  /* core.py:1166 */
+void *conv2d_layer_create(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int);  /* core.py:1126 */
+void *conv2d_layer_weight(void *);  /* core.py:1163 */
+void conv2d_layer_free(void *);  /* core.py:1137 */
+int embedding_backward(void *, void *, int64_t, void *, void *);  /* core.py:961 */
+int embedding_forward(void *, void *, int64_t, void *);  /* core.py:953 */
+int64_t embedding_dim(void *);  /* core.py:976 */
+int64_t embedding_num_embeddings(void *);  /* core.py:973 */
+void *embedding_create(int64_t, int64_t);  /* core.py:947 */
+void *embedding_weight(void *);  /* core.py:970 */
+void embedding_free(void *);  /* core.py:950 */
+double fuzzy_and(double, double);  /* core.py:1007 */
+double fuzzy_defuzz_bisector(void *, void *, int64_t);  /* core.py:1024 */
+double fuzzy_defuzz_centroid(void *, void *, int64_t);  /* core.py:1017 */
+double fuzzy_defuzz_mom(void *, void *, int64_t);  /* core.py:1031 */
+double fuzzy_gaussian(double, double, double);  /* core.py:999 */
+double fuzzy_not(double);  /* core.py:1013 */
+double fuzzy_or(double, double);  /* core.py:1010 */
+double fuzzy_trapezoidal(double, double, double, double, double);  /* core.py:990 */
+double fuzzy_triangular(double, double, double, double);  /* core.py:982 */
+int fuzzy_system_add_input_mf(void *, int, int, double, double, double, double);  /* core.py:1065 */
+int fuzzy_system_add_output_mf(void *, int, double, double, double, double);  /* core.py:1076 */
+int fuzzy_system_add_rule(void *, void *, void *, int, int, double);  /* core.py:1086 */
+int fuzzy_system_defuzz_method(void *);  /* core.py:1113 */
+int fuzzy_system_evaluate(void *, void *, void *);  /* core.py:1096 */
+int fuzzy_system_n_inputs(void *);  /* core.py:1104 */
+int fuzzy_system_n_rules(void *);  /* core.py:1107 */
+int fuzzy_system_resolution(void *);  /* core.py:1110 */
+int fuzzy_system_set_input_range(void *, int, double, double);  /* core.py:1050 */
+int fuzzy_system_set_output_range(void *, double, double);  /* core.py:1058 */
+void *fuzzy_system_create(int, int, int);  /* core.py:1039 */
+void fuzzy_system_free(void *);  /* core.py:1046 */
+double *gru_bias_hh(void *);  /* core.py:364 */
+double *gru_bias_ih(void *);  /* core.py:362 */
+double *gru_weight_hh(void *);  /* core.py:360 */
+double *gru_weight_ih(void *);  /* core.py:358 */
+int gru_forward(void *, double *, double *, double *, double *, int64_t, int64_t);  /* core.py:347 */
+int64_t gru_hidden_size(void *);  /* core.py:368 */
+int64_t gru_input_size(void *);  /* core.py:366 */
+void *gru_create(int64_t, int64_t);  /* core.py:341 */
+void gru_free(void *);  /* core.py:344 */
+int layernorm_backward(void *, void *, void *, void *, void *, int64_t);  /* core.py:852 */
+int layernorm_forward(void *, void *, void *, int64_t);  /* core.py:844 */
+int64_t layernorm_num_features(void *);  /* core.py:868 */
+void *layernorm_beta(void *);  /* core.py:865 */
+void *layernorm_create(int64_t, double);  /* core.py:838 */
+void *layernorm_gamma(void *);  /* core.py:862 */
+void layernorm_free(void *);  /* core.py:841 */
+double *lstm_bias_hh(void *);  /* core.py:334 */
+double *lstm_bias_ih(void *);  /* core.py:332 */
+double *lstm_weight_hh(void *);  /* core.py:330 */
+double *lstm_weight_ih(void *);  /* core.py:328 */
+int lstm_forward(void *, double *, double *, double *, double *, double *, double *, int64_t, int64_t);  /* core.py:315 */
+int64_t lstm_hidden_size(void *);  /* core.py:338 */
+int64_t lstm_input_size(void *);  /* core.py:336 */
+void *lstm_create(int64_t, int64_t);  /* core.py:309 */
+void lstm_free(void *);  /* core.py:312 */
+const char *neural_get_simd_name(void);  /* core.py:113 */
+double compute_sparsity(void *, int64_t);  /* core.py:705 */
+double compute_threshold_for_sparsity(void *, int64_t, double);  /* core.py:711 */
+int calibrate_percentile(void *, int64_t, double, int, QuantParams *);  /* core.py:745 */
+int neural_get_simd_level(void);  /* core.py:110 */
+int neural_matmul(void *, void *, void *);  /* core.py:178 */
+int neural_mse_loss(void *, void *, double *);  /* core.py:372 */
+int neural_weighted_sample_indices(void *, uint64_t, uint64_t, void *, int);  /* core.py:618 */
+int quantized_matmul(void *, void *, void *, int64_t, int64_t, int64_t, QuantParams *, QuantParams *);  /* core.py:770 */
+int roc_auc_score(void *, void *, int64_t, double *);  /* core.py:893 */
+int64_t count_nonzero(void *, int64_t);  /* core.py:708 */
+void apply_mask(void *, void *, int64_t);  /* core.py:718 */
+void *neural_adam_create(double, double, double, double);  /* core.py:243 */
+void *neural_adamw_create(double, double, double, double, double);  /* core.py:251 */
+double neural_compute_accuracy_from_matrix(void *, int);  /* core.py:450 */
+double neural_compute_class_f1(void *, int, int);  /* core.py:443 */
+double neural_compute_class_precision(void *, int, int);  /* core.py:429 */
+double neural_compute_class_recall(void *, int, int);  /* core.py:436 */
+int neural_compute_class_weights(void *, uint64_t, uint64_t, void *);  /* core.py:601 */
+int neural_compute_sample_weights(void *, uint64_t, void *, uint64_t, void *);  /* core.py:609 */
+void *neural_config_load(const char *);  /* core.py:411 */
+void neural_config_free(void *);  /* core.py:414 */
+int neural_confusion_matrix_update(void *, void *, void *, uint64_t, uint64_t);  /* core.py:420 */
+int neural_dataset_get_batch(void *, uint64_t, uint64_t, void **, void **);  /* core.py:401 */
+uint64_t neural_dataset_size(void *);  /* core.py:398 */
+void *neural_dataset_load_csv(const char *, const char *, uint64_t, uint32_t);  /* core.py:387 */
+void neural_dataset_free(void *);  /* core.py:395 */
+int neural_init_he_normal(void *, uint64_t, uint64_t, int);  /* core.py:554 */
+int neural_init_he_uniform(void *, uint64_t, uint64_t, int);  /* core.py:537 */
+int neural_init_kaiming_uniform(void *, uint64_t, uint64_t, uint64_t, int, int);  /* core.py:571 */
+int neural_init_normal_range(void *, uint64_t, float, float, int);  /* core.py:528 */
+int neural_init_uniform_range(void *, uint64_t, float, float, int);  /* core.py:519 */
+int neural_init_xavier_normal(void *, uint64_t, uint64_t, uint64_t, int);  /* core.py:562 */
+int neural_init_xavier_uniform(void *, uint64_t, uint64_t, uint64_t, int);  /* core.py:545 */
+int neural_linear_forward(void *, void *, void *);  /* core.py:229 */
+void *neural_linear_bias(void *);  /* core.py:236 */
+void *neural_linear_create(uint64_t, uint64_t, int);  /* core.py:223 */
+void *neural_linear_weight(void *);  /* core.py:233 */
+void neural_linear_free(void *);  /* core.py:226 */
+double neural_lr_cosine_annealing(double, int, int, double);  /* core.py:472 */
+double neural_lr_exponential_decay(double, int, double);  /* core.py:465 */
+double neural_lr_step_decay(double, int, int, double);  /* core.py:457 */
+double neural_optimizer_get_lr(void *);  /* core.py:588 */
+void neural_optimizer_free(void *);  /* core.py:260 */
+void neural_optimizer_set_lr(void *, double);  /* core.py:582 */
+void *neural_sgd_create(double, double);  /* core.py:240 */
+int avgpool2d_backward(void *, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, void *);  /* core.py:1242 */
+int avgpool2d_forward(void *, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, void *);  /* core.py:1228 */
+int maxpool2d_backward(void *, void *, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, void *);  /* core.py:1213 */
+int maxpool2d_forward(void *, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, void *, void *);  /* core.py:1198 */
+int64_t prune_cols(void *, int64_t, int64_t, double, void *);  /* core.py:696 */
+int64_t prune_magnitude(void *, void *, int64_t, double);  /* core.py:671 */
+int64_t prune_rows(void *, int64_t, int64_t, double, void *);  /* core.py:687 */
+int64_t prune_topk(void *, void *, int64_t, double);  /* core.py:679 */
+const char *tb_get_filepath(int);  /* core.py:667 */
+const char *tb_get_logdir(int);  /* core.py:664 */
+int tb_add_histogram_stats(int, const char *, void *, int, int64_t);  /* core.py:649 */
+int tb_add_scalar(int, const char *, float, int64_t);  /* core.py:631 */
+int tb_add_scalars(int, const char *, void *, void *, int, int64_t);  /* core.py:639 */
+int tb_close(int);  /* core.py:661 */
+int tb_create_writer(const char *);  /* core.py:628 */
+int tb_flush(int);  /* core.py:658 */
+int transformer_block_forward(void *, int64_t, int64_t, int64_t, int64_t, void *, void *, void *, void *, void *, void *, void *, void *, void *, void *, void *, void *, double, void *);  /* core.py:1352 */
+int upsample2d_nearest_backward(void *, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, void *);  /* core.py:1268 */
+int upsample2d_nearest_forward(void *, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, void *);  /* core.py:1256 */
+
 /* ---- HIP runtime controls (NEW) ------------------------------------------------- */
 /* Use an existing HIP stream (e.g. torch.cuda.current_stream().cuda_stream) for
  * all later launches; NULL selects the HIP null stream.  The previous stream

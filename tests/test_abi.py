@@ -68,3 +68,54 @@ def test_no_oracle_in_product():
             + list((ROOT / "neural-assembly_amd").rglob("*.hpp")):
         t = p.read_text()
         assert "liboracle" not in t and "import ora" not in t and "_ref/" not in t, p
+
+
+def _bound():
+    import json
+    return json.loads((ROOT / "tests" / "golden" / "reference_bound_symbols.json").read_text())
+
+
+def test_reference_loader_symbols_are_exported(lib):
+    """Every name the reference's pyneural binds at import (core.py, tensor.py;
+    list made by tests/golden/make_bound_symbols.py) resolves in this library."""
+    names = _bound()
+    assert len(names) == 215
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_out_of_scope_stubs(lib):
+    """Entry points outside the hot path answer without touching a device:
+    NOT_IMPLEMENTED / -1 / NULL / 0 / NaN, and NOT_IMPLEMENTED as last error."""
+    import math
+    ct = ctypes
+    lib.neural_get_last_error.restype = ct.c_int
+
+    def check(name, restype, argtypes, args, want):
+        f = getattr(lib, name)
+        f.restype, f.argtypes = restype, argtypes
+        got = f(*args)
+        if isinstance(want, float) and math.isnan(want):
+            assert math.isnan(got), (name, got)
+        else:
+            assert got == want, (name, got)
+        assert lib.neural_get_last_error() == 14, name
+
+    check("neural_matmul", ct.c_int, [ct.c_void_p] * 3, [None] * 3, 14)
+    check("neural_mse_loss", ct.c_int, [ct.c_void_p, ct.c_void_p, ct.POINTER(ct.c_double)], [None, None, None], 14)
+    check("layernorm_forward", ct.c_int, [ct.c_void_p] * 3 + [ct.c_int64], [None, None, None, 4], -1)
+    check("layernorm_create", ct.c_void_p, [ct.c_int64, ct.c_double], [4, 1e-5], None)
+    check("neural_sgd_create", ct.c_void_p, [ct.c_double, ct.c_double], [0.1, 0.9], None)
+    check("conv2d_output_size", ct.c_int64, [ct.c_int64] * 4, [32, 3, 1, 1], -1)
+    check("neural_dataset_size", ct.c_uint64, [ct.c_void_p], [None], 0)
+    check("compute_sparsity", ct.c_double, [ct.c_void_p, ct.c_int64], [None, 0], float("nan"))
+    check("neural_lr_step_decay", ct.c_double, [ct.c_double, ct.c_int, ct.c_int, ct.c_double], [0.1, 3, 2, 0.5],
+          float("nan"))
+    check("tb_get_logdir", ct.c_char_p, [ct.c_int], [0], None)
+    check("calibrate_percentile", ct.c_int, [ct.c_void_p, ct.c_int64, ct.c_double, ct.c_int, ct.c_void_p],
+          [None, 0, 99.9, 0, None], -1)
+    check("apply_mask", None, [ct.c_void_p, ct.c_void_p, ct.c_int64], [None, None, 0], None)
+    lib.layernorm_free.argtypes = [ct.c_void_p]
+    lib.layernorm_free(None)
+    lib.neural_get_simd_name.restype = ct.c_char_p
+    assert b"HIP" in lib.neural_get_simd_name()
