@@ -193,6 +193,9 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_rows(const T *__restrict__ x
     const int64_t r = int64_t(blockIdx.x) * RPB + threadIdx.x / TPR;
     if (r >= rows) return;  // uniform per group (the grid covers whole blocks only when TPR == 256)
     const T *xr = x + r * ld;
+    // default-policy loads: in a sequence (bias add, then several row
+    // reductions of its result, then other streams) this measured faster for
+    // the whole sequence than non-temporal ones
     const typename Red::B b = seg_reduce<T, Red, TPR, false>(red, xr, 0, cols, vec);
     if (Grp<TPR>::lane() == 0) red.store(out, r, b, xr, cols);
 }
