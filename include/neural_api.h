@@ -510,7 +510,9 @@ int upsample2d_nearest_forward(void *, int64_t, int64_t, int64_t, int64_t, int64
 /* Use an existing HIP stream (e.g. torch.cuda.current_stream().cuda_stream) for
  * all later launches; NULL selects the HIP null stream.  The previous stream
  * is synchronised first.  neural_hip_reset_stream() returns to the library's
- * own non-blocking stream. */
+ * own stream, a blocking one: it orders implicitly with the legacy null stream
+ * (torch's default stream), so kernels on it follow earlier null-stream work
+ * and later null-stream work waits for them. */
 int   neural_hip_set_stream(void *hip_stream);
 int   neural_hip_reset_stream(void);
 void *neural_hip_get_stream(void);

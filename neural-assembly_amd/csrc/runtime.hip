@@ -98,7 +98,11 @@ int ensure_init()
             }
             r.cus = prop.multiProcessorCount;
             std::snprintf(r.name, sizeof(r.name), "%s", prop.gcnArchName);
-            if (hipStreamCreateWithFlags(&r.own, hipStreamNonBlocking) != hipSuccess) {
+            // A blocking stream: it orders implicitly with the legacy null
+            // stream, which torch uses by default, so device buffers shared
+            // with torch are written and read in program order without an
+            // explicit sync on either side.
+            if (hipStreamCreateWithFlags(&r.own, hipStreamDefault) != hipSuccess) {
                 r.init_rc = NEURAL_ERR_INTERNAL;
                 return set_error(r.init_rc);
             }

@@ -983,6 +983,97 @@ int ora_dropout_backward(const float *go, float *gi, const uint8_t *mask, uint64
     return 0;
 }
 
+/* The C library's rand() n times (the process-wide stream, as the reference
+ * draws it). */
+void ora_rand_n(uint64_t n, uint32_t *out)
+{
+    for (uint64_t i = 0; i < n; i++) out[i] = (uint32_t)rand();
+}
+
+/* glibc's TYPE_3 stream at any position without stepping to it.
+ * srand(s): r[0] = s (0 taken as 1), r[i] = 16807 r[i-1] mod (2^31 - 1) for
+ * i < 31 (Schrage's method on int32, as glibc's srandom_r), r[31..33] =
+ * r[0..2], r[i] = r[i-31] + r[i-3] mod 2^32 for i >= 34; rand() number k
+ * (k = 0, 1, ...) is r[k + 344] >> 1.  The recurrence is linear with
+ * characteristic polynomial P(x) = x^31 - x^28 - 1, so with the anchor
+ * window W = r[313 .. 343], r[313 + j] = sum_m (x^j mod P)_m W[m]
+ * (coefficients mod 2^32): the window at any offset follows from
+ * x^skip mod P by square-and-multiply. */
+static void ora_pmul(uint32_t *a, const uint32_t *b) /* a = a * b mod P; b may alias a */
+{
+    uint32_t prod[61] = {0};
+    for (int i = 0; i < 31; i++)
+        for (int j = 0; j < 31; j++) prod[i + j] += a[i] * b[j];
+    for (int d = 60; d >= 31; d--) { /* x^d = x^(d-3) + x^(d-31) */
+        prod[d - 31] += prod[d];
+        prod[d - 3] += prod[d];
+    }
+    memcpy(a, prod, 31 * sizeof(uint32_t));
+}
+
+void ora_glibc_window(uint32_t seed, uint64_t skip, uint64_t n, uint32_t *out)
+{
+    uint32_t r[344];
+    r[0] = seed == 0 ? 1u : seed;
+    int32_t word = (int32_t)r[0];
+    for (int i = 1; i < 31; i++) {
+        const int32_t hi = word / 127773, lo = word % 127773;
+        word = 16807 * lo - 2836 * hi;
+        if (word < 0) word += 2147483647;
+        r[i] = (uint32_t)word;
+    }
+    for (int i = 31; i < 34; i++) r[i] = r[i - 31];
+    for (int i = 34; i < 344; i++) r[i] = r[i - 31] + r[i - 3];
+    const uint32_t *W = r + 313;
+    /* window at r[344 + skip - 31 ..]: offset j = skip + 0 .. 30 from the anchor */
+    uint32_t c[31] = {0}, base[31] = {0}, w[31];
+    c[0] = 1u;
+    base[1] = 1u;
+    for (uint64_t k = skip; k; k >>= 1) {
+        if (k & 1) ora_pmul(c, base);
+        ora_pmul(base, base);
+    }
+    for (int t = 0; t < 31; t++) {
+        uint32_t v = 0;
+        for (int m = 0; m < 31; m++) v += c[m] * W[m];
+        w[t] = v;
+        const uint32_t top = c[30]; /* c <- c * x mod P */
+        for (int m = 30; m > 0; m--) c[m] = c[m - 1];
+        c[0] = top;
+        c[28] += top;
+    }
+    for (uint64_t j = 0; j < n; j++) {
+        const int a = (int)(j % 31), b = (int)((j + 28) % 31);
+        const uint32_t v = w[a] + w[b];
+        w[a] = v;
+        out[j] = v >> 1;
+    }
+}
+
+/* ora_dropout_forward on draws skip .. skip + n - 1 after srand(seed), the
+ * draws taken from ora_glibc_window instead of the C library. */
+int ora_dropout_window(uint32_t seed, uint64_t skip, const float *in, float *out, uint8_t *mask, uint64_t n,
+                       float p)
+{
+    uint32_t *r = (uint32_t *)malloc(n * sizeof(uint32_t) + 4);
+    if (!r) return -1;
+    ora_glibc_window(seed, skip, n, r);
+    const double pd = (double)p;
+    const float scale = (float)(1.0 / (1.0 - pd));
+    const int64_t th = ora_cvtsd2si(pd * 2147483647.0);
+    for (uint64_t i = 0; i < n; i++) {
+        if ((int64_t)r[i] < th) {
+            mask[i] = 0;
+            out[i] = 0.0f;
+        } else {
+            mask[i] = 1;
+            out[i] = in[i] * scale;
+        }
+    }
+    free(r);
+    return 0;
+}
+
 /* vec_add_relu_fusion (fusion.asm:200-226): addss then maxss with +0, i.e.
  * s = a + b; c = s > 0 ? s : +0 (NaN and -0 give +0). */
 void ora_add_relu_f32(const float *a, const float *b, float *c, int64_t n)

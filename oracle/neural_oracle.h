@@ -152,6 +152,10 @@ void   ora_clip_grad_value(void **grads, const int *dtypes, const int64_t *ns, i
 void ora_srand(unsigned seed);
 int  ora_dropout_forward(const float *in, float *out, uint8_t *mask, uint64_t n, float p);
 int  ora_dropout_backward(const float *go, float *gi, const uint8_t *mask, uint64_t n, float p);
+void ora_rand_n(uint64_t n, uint32_t *out);
+void ora_glibc_window(uint32_t seed, uint64_t skip, uint64_t n, uint32_t *out);
+int  ora_dropout_window(uint32_t seed, uint64_t skip, const float *in, float *out, uint8_t *mask, uint64_t n,
+                        float p);
 void ora_add_relu_f32(const float *a, const float *b, float *c, int64_t n);
 
 /* Per-feature transforms (transforms.c:27-143): statistics and the three

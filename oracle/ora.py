@@ -438,6 +438,39 @@ def dropout_backward(go, mask, p):
     return rc, gi
 
 
+def rand_n(n):
+    """The C library's rand(), n calls from its current state, as uint32."""
+    out = np.empty(n, dtype=np.uint32)
+    f = lib().ora_rand_n
+    f.argtypes = [ctypes.c_uint64, ctypes.c_void_p]
+    f.restype = None
+    f(n, _p(out))
+    return out
+
+
+def glibc_window(seed, skip, n):
+    """rand() values skip .. skip + n - 1 after srand(seed), from the C
+    restatement with the jump x^skip mod (x^31 - x^28 - 1)."""
+    out = np.empty(n, dtype=np.uint32)
+    f = lib().ora_glibc_window
+    f.argtypes = [ctypes.c_uint32, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p]
+    f.restype = None
+    f(seed & 0xFFFFFFFF, skip, n, _p(out))
+    return out
+
+
+def dropout_window(seed, skip, x, p):
+    """dropout_forward on draws skip .. skip + x.size - 1 after srand(seed)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    mask = np.empty(x.size, dtype=np.uint8)
+    f = lib().ora_dropout_window
+    f.argtypes = [ctypes.c_uint32, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64,
+                  ctypes.c_float]
+    assert f(seed & 0xFFFFFFFF, skip, _p(x), _p(out), _p(mask), x.size, p) == 0
+    return out, mask
+
+
 def add_relu(a, b):
     a = np.ascontiguousarray(a, dtype=np.float32)
     b = np.ascontiguousarray(b, dtype=np.float32)

@@ -13,6 +13,11 @@ reference calls.  What pins it:
   - out = x * (float)(1 / (1 - p)) where kept and +0 where dropped, and the
     keep rate of a million draws within 5 sigma of 1 - p;
   - backward: any nonzero mask byte keeps.
+ora_glibc_window (positions far into the stream by the jump x^k mod
+x^31 - x^28 - 1, used to check GPU windows 2^31 draws in) is pinned against
+rand() itself (ora_rand_n) at skips up to 3 * 10^6 + 7, against ora.glibc_rand
+at skips around the 31-value period and the 344-value warm-up, and by the
+jump's composition (skip a then b equals skip a + b).
 """
 
 import ctypes
@@ -116,3 +121,34 @@ def test_add_relu():
     assert c.tolist()[:4] == [2.0, 0.0, 0.0, 0.0]
     assert c[4] == 0 and c[5] == 0 and c[6] == 0
     assert all(math.copysign(1, v) > 0 for v in c if v == 0)
+
+
+@pytest.mark.parametrize("seed", [1, 0, 2024, 2 ** 31 + 5, 2 ** 32 - 1])
+def test_jump_window_matches_rand(seed):
+    for skip, n in [(0, 1000), (1, 64), (30, 70), (31, 31), (32, 5), (313, 100), (344, 100), (12345, 700)]:
+        assert np.array_equal(ora.glibc_window(seed, skip, n), ora.glibc_rand(seed, n, skip=skip)), (seed, skip)
+    # the C library itself, three million draws in
+    k = 3_000_007
+    ora.srand(seed)
+    libc_draws = ora.rand_n(k + 500)
+    assert np.array_equal(ora.glibc_window(seed, k, 500), libc_draws[k:])
+    assert np.array_equal(ora.glibc_window(seed, 0, 500), libc_draws[:500])
+
+
+def test_jump_window_composes():
+    # x^(a+b) = x^a x^b: a window at a + b equals the window reached from the
+    # stream at a, stepped b further -- checked at offsets past 2^32
+    a, b = (1 << 32) + 12345, 999_983
+    w = ora.glibc_window(77, a, b + 300)
+    assert np.array_equal(ora.glibc_window(77, a + b, 300), w[b:])
+
+
+def test_dropout_window_matches_forward():
+    rng = np.random.default_rng(8)
+    x = rng.normal(0, 1, 5000).astype(np.float32)
+    ora.srand(31)
+    ora.rand_n(123_456)
+    rc, out, mask = ora.dropout_forward(x, 0.3)
+    wout, wmask = ora.dropout_window(31, 123_456, x, 0.3)
+    assert np.array_equal(mask, wmask)
+    assert np.array_equal(out.view(np.uint32), wout.view(np.uint32))
