@@ -330,7 +330,7 @@ def suite(torch, pn, stream):
     one_i = torch.empty(1, dtype=torch.int64, device=dev)
     timeit("argmax f32 64M (device result)",
            lambda: _lib.neural_reduce_argmax(ta._ptr, -1, ctypes.c_void_p(one_i.data_ptr())), 4 * n)
-    timeit("sum f32 64M (host API, incl. D2H + sync)", lambda: _lib.neural_sum(ta._ptr, ctypes.byref(r)), 4 * n)
+    timeit("sum f32 64M (host API, result on the host)", lambda: _lib.neural_sum(ta._ptr, ctypes.byref(r)), 4 * n)
     X = torch.randn(16384, 4096, device=dev)
     bias = torch.randn(4096, device=dev)
     Y = torch.empty_like(X)
@@ -373,7 +373,7 @@ def suite(torch, pn, stream):
     timeit("ls_ce fused fwd+bwd f32 [65536,1024]",
            lambda: _lib.label_smoothing_ce_fused_f32(S.data_ptr(), tgt.data_ptr(), 65536, 1024, 0.1,
                                                      ctypes.byref(lossv), P.data_ptr()), 8 * S.numel())
-    timeit("cross_entropy_loss f32 [65536,1024] (incl. D2H)",
+    timeit("cross_entropy_loss f32 [65536,1024] (result on the host)",
            lambda: _lib.neural_cross_entropy_loss(tS._ptr, ttf._ptr, ctypes.byref(lossv)), 4 * S.numel())
     del P, tP
     S64 = S.double()
@@ -382,7 +382,7 @@ def suite(torch, pn, stream):
     timeit("ls_ce fused fwd+bwd f64 [65536,1024]",
            lambda: _lib.label_smoothing_ce_fused(S64.data_ptr(), tgt.data_ptr(), 65536, 1024, 0.1,
                                                  ctypes.byref(lossv), G64.data_ptr()), 16 * S.numel())
-    timeit("ls_ce forward f64 [65536,1024] (incl. D2H)",
+    timeit("ls_ce forward f64 [65536,1024] (result on the host)",
            lambda: _lib.label_smoothing_ce_forward(S64.data_ptr(), tgt.data_ptr(), 65536, 1024, 0.1,
                                                    ctypes.byref(lossv)), 8 * S.numel())
     del S, tS, S64, G64
@@ -432,7 +432,7 @@ def suite(torch, pn, stream):
     opt = pn.AdamW(1e-3, 0.9, 0.999, 1e-8, 0.01)
     timeit("adamw f32 params, f64 m/v, 100M", lambda: opt.step([tp], [tg]), 44 * na)
     hn, hi, ss = ctypes.c_int(), ctypes.c_int(), ctypes.c_double()
-    timeit("nan/inf/l2 scan f32 100M (incl. D2H)",
+    timeit("nan/inf/l2 scan f32 100M (result on the host)",
            lambda: _lib.neural_tensor_scan(tg._ptr, ctypes.byref(hn), ctypes.byref(hi), ctypes.byref(ss)), 4 * na)
     # per-feature transforms on [1M, 64] f64 (512 MB), device pointers
     tb_rows, tb_f = 1 << 20, 64

@@ -82,7 +82,8 @@ struct Workspace {
     void         *partials;    // kMaxPartials * 64 bytes
     unsigned int *counter;     // kCounters counters, all zero between calls
     void         *result;      // 256 bytes of small results
-    void         *host_result; // 256 bytes of pinned host memory: landing area for result_to_host
+    void         *host_result; // 256 bytes of coherent pinned host memory (host address)
+    void         *host_result_dev; // the same bytes as kernels address them
 };
 constexpr int kMaxPartials = 16384;
 constexpr int kCounters = 1024;
@@ -129,6 +130,11 @@ int          sync();                                 // synchronise the active s
 // Copy `bytes` (<= 256) of a device result to `dst` (host): one D2H copy into
 // the pinned landing area, a stream sync, then a host memcpy.
 int          result_to_host(void *dst, const void *dev_src, size_t bytes);
+// Results that only the host reads are stored by the last kernel straight
+// into workspace().host_result_dev (coherent pinned memory): a stream sync
+// and a host memcpy, no copy command (measured: 14.9 -> 11.3 us for a
+// launch-and-return round trip).
+int          host_result_fetch(void *dst, size_t bytes);
 
 }  // namespace nh
 

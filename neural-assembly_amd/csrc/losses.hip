@@ -336,10 +336,10 @@ static int ce_run(const T *x, const int64_t *tidx, const T *tval, int64_t rows, 
                   double *loss_host, T *grad_dev)
 {
     Workspace &ws = workspace();
-    // Flag word in the small-result area: zero at init and between calls (a
-    // call that finds it set clears it), so the common path launches nothing
-    // to reset it.
-    int *bad = static_cast<int *>(ws.result) + 32;
+    // The loss sum (word 0) and the out-of-range flag (int word 32) are stored
+    // into the mapped host area.  The flag is zero at init and between calls
+    // (a call that finds it set clears it on the host).
+    int *bad = static_cast<int *>(ws.host_result_dev) + 32;
     const bool want_loss = MODE != CE_LS_BWD;
     constexpr bool kLs = MODE == CE_LS_FWD || MODE == CE_LS_FUSED;
     double *row_loss = nullptr, *row_s = nullptr;
@@ -353,19 +353,20 @@ static int ce_run(const T *x, const int64_t *tidx, const T *tval, int64_t rows, 
     int rc = launch_ce<T, MODE>(x, a);
     if (rc == NEURAL_OK && want_loss) {
         if (MODE == CE_ASM) {
-            rc = launch_reduce_full(row_loss, rows, RedCeLoss<sizeof(T) == 4>{}, ws.result);
+            rc = launch_reduce_full(row_loss, rows, RedCeLoss<sizeof(T) == 4>{}, ws.host_result_dev);
         } else {
             const double st0 = alpha / double(cols), st1 = st0 + (1.0 - alpha);
-            rc = launch_reduce_full(row_loss, rows, RedLsLoss{row_s, st0 * double(cols - 1) + st1}, ws.result);
+            rc = launch_reduce_full(row_loss, rows, RedLsLoss{row_s, st0 * double(cols - 1) + st1},
+                                    ws.host_result_dev);
         }
     }
     struct { double sum; int pad[30]; int bad; } res;  // result area layout: sum at 0, flag at word 32
     static_assert(sizeof(res) == 136, "");
-    if (rc == NEURAL_OK) rc = result_to_host(&res, ws.result, sizeof(res));
+    if (rc == NEURAL_OK) rc = host_result_fetch(&res, sizeof(res));
     if (row_loss) dev_free(row_loss);
     if (rc != NEURAL_OK) return rc;
     if (res.bad) {
-        NH_HIP(hipMemsetAsync(bad, 0, sizeof(int), stream()));
+        static_cast<int *>(ws.host_result)[32] = 0;  // the stream is idle: host_result_fetch synchronised it
         return NEURAL_ERR_INVALID_ARGUMENT;
     }
     if (want_loss && loss_host) *loss_host = res.sum / double(rows);

@@ -338,9 +338,9 @@ static int calibrate(const T *data, int64_t n, int symmetric, QuantParams *out, 
     if (s.open(data, size_t(n) * sizeof(T), true) != NEURAL_OK) return -1;
     RedMinMax<T> red;
     red.symmetric = symmetric ? 1 : 0;
-    void *res = out_on_device ? static_cast<void *>(out) : workspace().result;
+    void *res = out_on_device ? static_cast<void *>(out) : workspace().host_result_dev;
     if (launch_reduce_full(static_cast<const T *>(s.dev), n, red, res) != NEURAL_OK) return -1;
-    if (!out_on_device && result_to_host(out, res, sizeof(QuantParams)) != NEURAL_OK) return -1;
+    if (!out_on_device && host_result_fetch(out, sizeof(QuantParams)) != NEURAL_OK) return -1;
     if (s.finish(false) != NEURAL_OK) return -1;
     set_error(NEURAL_OK);
     return 0;
@@ -391,9 +391,8 @@ static int qerr(const T *data, int64_t n, const QuantParams *p, double *sig, dou
     red.inv = 1.0 / p->scale;
     red.zp = p->zero_point;
     QErrOut st;
-    void *res = workspace().result;
-    if (launch_reduce_full(static_cast<const T *>(s.dev), n, red, res) != NEURAL_OK) return -1;
-    if (result_to_host(&st, res, sizeof(st)) != NEURAL_OK) return -1;
+    if (launch_reduce_full(static_cast<const T *>(s.dev), n, red, workspace().host_result_dev) != NEURAL_OK) return -1;
+    if (host_result_fetch(&st, sizeof(st)) != NEURAL_OK) return -1;
     if (s.finish(false) != NEURAL_OK) return -1;
     *sig = st.sig;
     *noise = st.noise;

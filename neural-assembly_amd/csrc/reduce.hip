@@ -209,20 +209,20 @@ struct Contig {
     ~Contig() { if (tmp) dev_free(tmp); }
 };
 
-// Whole-tensor reduction returned to the host: one launch into the
-// workspace's result area, one 8-byte copy back, one stream sync.
+// Whole-tensor reduction returned to the host: the combine launch stores the
+// result into the mapped host area, then one stream sync.
 template <template <typename> class RedOf, typename Out>
 static int full_to_host(const NeuralTensor *t, Out *host_out)
 {
     const int64_t n = numel(t);
     Contig c;
     NH_TRY(c.open(t));
-    void *res = workspace().result;
+    void *res = workspace().host_result_dev;
     if (t->dtype == NEURAL_DTYPE_FLOAT32)
         NH_TRY(launch_reduce_full(static_cast<const float *>(c.p), n, RedOf<float>{}, res));
     else
         NH_TRY(launch_reduce_full(static_cast<const double *>(c.p), n, RedOf<double>{}, res));
-    return result_to_host(host_out, res, sizeof(Out));
+    return host_result_fetch(host_out, sizeof(Out));
 }
 
 template <typename T> using SumF64 = RedSum<T, SUM_OUT_F64>;
@@ -396,11 +396,11 @@ float simd_sum_f32(const float *a, uint64_t n)
     if (ensure_init() != NEURAL_OK || !a || n == 0) return 0.0f;
     Staged sa;
     if (sa.open(a, size_t(n) * 4, true) != NEURAL_OK) return 0.0f;
-    void *res = workspace().result;
+    void *res = workspace().host_result_dev;
     double s = 0.0;
     if (launch_reduce_full(static_cast<const float *>(sa.dev), int64_t(n), SumF64<float>{}, res) != NEURAL_OK)
         return 0.0f;
-    if (result_to_host(&s, res, sizeof(s)) != NEURAL_OK) return 0.0f;
+    if (host_result_fetch(&s, sizeof(s)) != NEURAL_OK) return 0.0f;
     set_error(NEURAL_OK);
     return float(s);
 }
@@ -449,9 +449,9 @@ extern "C" float simd_dot_f32(const float *a, const float *b, uint64_t n)
     if (g > int64_t(num_cus()) * 4) g = int64_t(num_cus()) * 4;
     hipLaunchKernelGGL(k_dot_f32, dim3(unsigned(g)), dim3(kRBlock), 0, stream(), static_cast<const float *>(sa.dev),
                        static_cast<const float *>(sb.dev), int64_t(n), static_cast<double *>(ws.partials), ws.counter,
-                       static_cast<double *>(ws.result));
+                       static_cast<double *>(ws.host_result_dev));
     double s = 0.0;
-    if (check_launch() != NEURAL_OK || result_to_host(&s, ws.result, sizeof(s)) != NEURAL_OK) return 0.0f;
+    if (check_launch() != NEURAL_OK || host_result_fetch(&s, sizeof(s)) != NEURAL_OK) return 0.0f;
     set_error(NEURAL_OK);
     return float(s);
 }

@@ -112,7 +112,9 @@ int ensure_init()
             if (hipMalloc(&r.ws.partials, size_t(kMaxPartials) * 64) != hipSuccess ||
                 hipMalloc((void **)&r.ws.counter, sizeof(unsigned) * kCounters) != hipSuccess ||
                 hipMalloc(&r.ws.result, 256) != hipSuccess ||
-                hipHostMalloc(&r.ws.host_result, 256, hipHostMallocDefault) != hipSuccess ||
+                hipHostMalloc(&r.ws.host_result, 256, hipHostMallocCoherent | hipHostMallocMapped) != hipSuccess ||
+                hipHostGetDevicePointer(&r.ws.host_result_dev, r.ws.host_result, 0) != hipSuccess ||
+                std::memset(r.ws.host_result, 0, 256) == nullptr ||
                 hipMemset(r.ws.counter, 0, sizeof(unsigned) * kCounters) != hipSuccess ||
                 hipMemset(r.ws.result, 0, 256) != hipSuccess ||
                 hipDeviceSynchronize() != hipSuccess) {
@@ -196,6 +198,14 @@ int check_launch()
 int sync()
 {
     NH_HIP(hipStreamSynchronize(stream()));
+    return NEURAL_OK;
+}
+
+int host_result_fetch(void *dst, size_t bytes)
+{
+    if (bytes > 256) return set_error(NEURAL_ERR_INTERNAL);
+    NH_TRY(sync());
+    std::memcpy(dst, workspace().host_result, bytes);
     return NEURAL_OK;
 }
 

@@ -47,9 +47,8 @@ struct RedScan {
 template <typename T>
 static int scan_dev(const T *x, int64_t n, ScanOut *st)
 {
-    void *res = workspace().result;
-    NH_TRY(launch_reduce_full(x, n, RedScan<T>{}, res));
-    return result_to_host(st, res, sizeof(*st));
+    NH_TRY(launch_reduce_full(x, n, RedScan<T>{}, workspace().host_result_dev));
+    return host_result_fetch(st, sizeof(*st));
 }
 
 static int scan_raw(const float *data, uint64_t n, ScanOut *st)
