@@ -86,18 +86,33 @@ NH_DEV double tanh_d(double x)
     return (a < 0x1p-7 || x != x) ? small : big;
 }
 
+// 1 / d for d in [1, 2]: the hardware reciprocal refined by two Newton steps
+// (each squares the relative error; the result is within an ulp or two of
+// the correctly rounded quotient, ~5 instructions instead of a division's ~12).
+NH_DEV double rcp_1_2(double d)
+{
+    double r = __builtin_amdgcn_rcp(d);
+    double e = __builtin_fma(-d, r, 1.0);
+    r = __builtin_fma(r, e, r);
+    e = __builtin_fma(-d, r, 1.0);
+    return __builtin_fma(r, e, r);
+}
+
 // 1 + tanh(z) as the reference's double tanh leaves it, from w = exp(-2|z|):
 //   z >= 0:  1 + (1 - w)/(1 + w) = 2/(1 + w)                     (no cancellation)
 //   z < 0:   eps = 1 - |tanh z| = 2w/(1 + w); while tanh z is in [-1, -0.5]
 //            it is a multiple of 2^-53, so 1 + tanh z = rint(eps * 2^53) * 2^-53
 //            (round-half-even on the multiple = round-half-even on tanh z).
+// Both sides share one reciprocal and no branch: a wave holds both signs.
+// An ulp of error in eps matters to rint only where eps * 2^53 is large, i.e.
+// where one multiple of 2^-53 is far below 1e-12 of the result.
 NH_DEV double one_plus_tanh(double z)
 {
     const double w = exp(-2.0 * __builtin_fabs(z));
-    const double d = 1.0 + w;
-    if (z >= 0.0) return 2.0 / d;
-    const double eps = (w + w) / d;
-    return eps < 0.5 ? __builtin_rint(eps * 0x1p53) * 0x1p-53 : eps;
+    const double r = rcp_1_2(1.0 + w);
+    const double eps = (w + w) * r;
+    const double q = eps < 0.5 ? __builtin_rint(eps * 0x1p53) * 0x1p-53 : eps;
+    return z >= 0.0 ? r + r : q;
 }
 
 NH_DEV double gelu_d(double x)
