@@ -42,10 +42,18 @@ NH_DEV bool loss_target(const int64_t *ti, const T *tv, int64_t r, int64_t cols,
     return true;
 }
 
-// e = exp(x - m) for one element: double exp for f64 rows, float-accurate for
-// f32 rows (the reference widens f32 exactly and rounds e to float).
+// e = exp(x - m) for one element: double exp for f64 rows; for f32 rows the
+// hardware exp2 of (x - m) * log2(e) in float (m is the row's largest float,
+// so float(m) is exact).  Relative error about (|x - m| + 1) * 1.2e-7 against
+// the reference's float rounding of the exact value: the losses built on it
+// stay within 2e-6 of the exact loss (the f32 bar), and the float gradients
+// within 1e-5.  Exact-difference double range reduction was measured ~20%
+// slower for the tensor loss kernel.
 NH_DEV double row_exp_d(double x, double m) { return exp(x - m); }
-NH_DEV double row_exp_f(float x, double m) { return double(exp_d2f(double(x) - m)); }
+NH_DEV double row_exp_f(float x, double m)
+{
+    return double(__builtin_amdgcn_exp2f((x - float(m)) * 1.4426950408889634f));
+}
 
 struct CeArgs {
     const int64_t *tidx;   // int64 targets (label-smoothed API) or null
