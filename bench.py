@@ -218,6 +218,9 @@ def main():
             "workload": "cfg2: bias-add [8192,4096]+[4096]; row sum/mean/max/argmax; softmax + log-softmax rows [65536,1024]",
             "step_bytes": step_bytes,
             "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 1),
+            # elements through the step's ops: bias add and four row reductions
+            # over [8192,4096], softmax and log-softmax over [65536,1024]
+            "elements_per_s": round((5 * n1 + 2 * n2) / (ms_per_step * 1e-3), 0),
         },
         "roofline": {
             "kernel": "k_softmax_wave_f32<false,4,true,1> (neural_softmax [65536,1024] f32)",
@@ -256,6 +259,16 @@ def main():
     print(json.dumps(line), flush=True)
 
 
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
 def cpu_baseline(X, b, S, step_bytes):
     """The oracle's C restatement of the same step (reference loop orders,
     scalar libm exp/log, -O2, one thread), on the same data copied to host."""
@@ -281,7 +294,8 @@ def cpu_baseline(X, b, S, step_bytes):
         "cores": 1,
         "kind": "port",
         "sample": f"full cfg2 step on host (oracle/liboracle.so, gcc -O2 SSE2), median of 3 = {sec:.3f} s; "
-                  f"host {os.cpu_count()} logical CPUs, 1 used (the reference never dispatches to its pool)",
+                  f"host {_cpu_model()}, {os.cpu_count()} logical CPUs, 1 used (the reference never dispatches "
+                  f"to its thread pool: pool size 1, unused)",
     }
 
 
@@ -292,7 +306,7 @@ def suite(torch, pn, stream):
     dev = torch.device("cuda:0")
     out = []
 
-    def timeit(name, fn, nbytes, reps=10, flops=None):
+    def timeit(name, fn, nbytes, reps=10, flops=None, elems=None):
         for _ in range(3):
             fn()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -305,6 +319,10 @@ def suite(torch, pn, stream):
         us = e0.elapsed_time(e1) * 1e3 / reps
         r = {"kernel": name, "us": round(us, 2), "GB/s": round(nbytes / us / 1e3, 1),
              "pct_hbm": round(100 * nbytes / us / 1e3 / HBM_PEAK_GBS, 1), "bytes": nbytes}
+        if elems:
+            r["Gelem/s"] = round(elems / us / 1e3, 2)
+        if copy_peak:
+            r["x_rocm_copy"] = round(nbytes / us / 1e3 / copy_peak[0], 3)
         if flops:
             r["fp64_TFLOPs"] = round(flops / us / 1e6, 2)
         out.append(r)
@@ -319,50 +337,56 @@ def suite(torch, pn, stream):
     c = torch.empty_like(a)
     ta, tb, tc = W(a), W(b2), W(c)
     torch.cuda.synchronize()
-    timeit("add f32 64M", lambda: _check_error(_lib.neural_add(tc._ptr, ta._ptr, tb._ptr), "add"), 12 * n)
-    timeit("mul f32 64M", lambda: _check_error(_lib.neural_mul(tc._ptr, ta._ptr, tb._ptr), "mul"), 12 * n)
-    timeit("relu f32 64M", lambda: _check_error(_lib.neural_relu(tc._ptr, ta._ptr), "relu"), 8 * n)
+    # every row is also quoted against a measured copy: torch's copy_ of the
+    # same 64M-element vector, i.e. the ROCm runtime's device-to-device copy
+    # kernel (x_rocm_copy = the row's GB/s over that copy's)
+    copy_peak = []
+    timeit("copy f32 64M (torch copy_ = ROCm runtime D2D copy kernel)", lambda: c.copy_(a), 8 * n, elems=n)
+    copy_peak.append(out[-1]["GB/s"])
+    out[-1]["x_rocm_copy"] = 1.0
+    timeit("add f32 64M", lambda: _check_error(_lib.neural_add(tc._ptr, ta._ptr, tb._ptr), "add"), 12 * n, elems=n)
+    timeit("mul f32 64M", lambda: _check_error(_lib.neural_mul(tc._ptr, ta._ptr, tb._ptr), "mul"), 12 * n, elems=n)
+    timeit("relu f32 64M", lambda: _check_error(_lib.neural_relu(tc._ptr, ta._ptr), "relu"), 8 * n, elems=n)
     r = ctypes.c_double()
     one = torch.empty(1, device=dev)
     tone = W(one)
-    timeit("sum f32 64M (device result)", lambda: _lib.neural_reduce_sum(ta._ptr, -1, tone._ptr), 4 * n)
-    timeit("max f32 64M (device result)", lambda: _lib.neural_reduce_max(ta._ptr, -1, tone._ptr), 4 * n)
+    timeit("sum f32 64M (device result)", lambda: _lib.neural_reduce_sum(ta._ptr, -1, tone._ptr), 4 * n, elems=n)
+    timeit("max f32 64M (device result)", lambda: _lib.neural_reduce_max(ta._ptr, -1, tone._ptr), 4 * n, elems=n)
     one_i = torch.empty(1, dtype=torch.int64, device=dev)
     timeit("argmax f32 64M (device result)",
-           lambda: _lib.neural_reduce_argmax(ta._ptr, -1, ctypes.c_void_p(one_i.data_ptr())), 4 * n)
-    timeit("sum f32 64M (host API, result on the host)", lambda: _lib.neural_sum(ta._ptr, ctypes.byref(r)), 4 * n)
+           lambda: _lib.neural_reduce_argmax(ta._ptr, -1, ctypes.c_void_p(one_i.data_ptr())), 4 * n, elems=n)
+    timeit("sum f32 64M (host API, result on the host)", lambda: _lib.neural_sum(ta._ptr, ctypes.byref(r)), 4 * n, elems=n)
     X = torch.randn(16384, 4096, device=dev)
     bias = torch.randn(4096, device=dev)
     Y = torch.empty_like(X)
     tX, tbias, tY = W(X), W(bias), W(Y)
     torch.cuda.synchronize()
-    timeit("bias_add f32 [16384,4096]", lambda: _lib.neural_bias_add(tY._ptr, tX._ptr, tbias._ptr), 8 * X.numel())
+    timeit("bias_add f32 [16384,4096]", lambda: _lib.neural_bias_add(tY._ptr, tX._ptr, tbias._ptr), 8 * X.numel(), elems=X.numel())
     timeit("bias_add+relu fused f32 [16384,4096]",
-           lambda: _lib.neural_bias_add_act(tY._ptr, tX._ptr, tbias._ptr, 1, ctypes.c_double(0.0)), 8 * X.numel())
+           lambda: _lib.neural_bias_add_act(tY._ptr, tX._ptr, tbias._ptr, 1, ctypes.c_double(0.0)), 8 * X.numel(), elems=X.numel())
     timeit("bias_add+gelu fused f32 [16384,4096]",
-           lambda: _lib.neural_bias_add_act(tY._ptr, tX._ptr, tbias._ptr, 4, ctypes.c_double(0.0)), 8 * X.numel())
+           lambda: _lib.neural_bias_add_act(tY._ptr, tX._ptr, tbias._ptr, 4, ctypes.c_double(0.0)), 8 * X.numel(), elems=X.numel())
     # dropout over the 64M cfg1 vector: 4 B in + 4 B out + 1 B mask per element
     dmask = torch.empty(n, dtype=torch.uint8, device=dev)
     torch.cuda.synchronize()
     timeit("dropout fwd f32 64M (p=0.5, draws + apply)",
-           lambda: _lib.neural_dropout_forward(a.data_ptr(), c.data_ptr(), dmask.data_ptr(), n, ctypes.c_float(0.5)),
-           9 * n)
+           lambda: _lib.neural_dropout_forward(a.data_ptr(), c.data_ptr(), dmask.data_ptr(), n, ctypes.c_float(0.5)), 9 * n, elems=n)
     timeit("dropout bwd f32 64M", lambda: _lib.neural_dropout_backward(a.data_ptr(), c.data_ptr(), dmask.data_ptr(), n,
-                                                                       ctypes.c_float(0.5)), 9 * n)
+                                                                       ctypes.c_float(0.5)), 9 * n, elems=n)
     del dmask
     rs = torch.empty(16384, device=dev)
     trs = W(rs)
-    timeit("row sum f32 [16384,4096]", lambda: _lib.neural_reduce_sum(tX._ptr, 1, trs._ptr), 4 * X.numel())
-    timeit("row max f32 [16384,4096]", lambda: _lib.neural_reduce_max(tX._ptr, 1, trs._ptr), 4 * X.numel())
+    timeit("row sum f32 [16384,4096]", lambda: _lib.neural_reduce_sum(tX._ptr, 1, trs._ptr), 4 * X.numel(), elems=X.numel())
+    timeit("row max f32 [16384,4096]", lambda: _lib.neural_reduce_max(tX._ptr, 1, trs._ptr), 4 * X.numel(), elems=X.numel())
     idx = torch.empty(16384, dtype=torch.int64, device=dev)
     timeit("row argmax f32 [16384,4096]",
-           lambda: _lib.neural_reduce_argmax(tX._ptr, 1, ctypes.c_void_p(idx.data_ptr())), 4 * X.numel())
+           lambda: _lib.neural_reduce_argmax(tX._ptr, 1, ctypes.c_void_p(idx.data_ptr())), 4 * X.numel(), elems=X.numel())
     del X, Y, tX, tY
     S = torch.randn(65536, 1024, device=dev) * 3
     P = torch.empty_like(S)
     tS, tP = W(S), W(P)
-    timeit("softmax f32 [65536,1024]", lambda: _lib.neural_softmax(tP._ptr, tS._ptr), 8 * S.numel())
-    timeit("log_softmax f32 [65536,1024]", lambda: _lib.neural_log_softmax(tP._ptr, tS._ptr), 8 * S.numel())
+    timeit("softmax f32 [65536,1024]", lambda: _lib.neural_softmax(tP._ptr, tS._ptr), 8 * S.numel(), elems=S.numel())
+    timeit("log_softmax f32 [65536,1024]", lambda: _lib.neural_log_softmax(tP._ptr, tS._ptr), 8 * S.numel(), elems=S.numel())
     # cross-entropy on the same [65536,1024] logits:
     # label-smoothed forward + backward in one pass (f32 and f64 logits, int64
     # targets), and the tensor cross_entropy_loss (reads the logits once)
@@ -372,19 +396,19 @@ def suite(torch, pn, stream):
     lossv = ctypes.c_double()
     timeit("ls_ce fused fwd+bwd f32 [65536,1024]",
            lambda: _lib.label_smoothing_ce_fused_f32(S.data_ptr(), tgt.data_ptr(), 65536, 1024, 0.1,
-                                                     ctypes.byref(lossv), P.data_ptr()), 8 * S.numel())
+                                                     ctypes.byref(lossv), P.data_ptr()), 8 * S.numel(), elems=S.numel())
     timeit("cross_entropy_loss f32 [65536,1024] (result on the host)",
-           lambda: _lib.neural_cross_entropy_loss(tS._ptr, ttf._ptr, ctypes.byref(lossv)), 4 * S.numel())
+           lambda: _lib.neural_cross_entropy_loss(tS._ptr, ttf._ptr, ctypes.byref(lossv)), 4 * S.numel(), elems=S.numel())
     del P, tP
     S64 = S.double()
     G64 = torch.empty_like(S64)
     torch.cuda.synchronize()
     timeit("ls_ce fused fwd+bwd f64 [65536,1024]",
            lambda: _lib.label_smoothing_ce_fused(S64.data_ptr(), tgt.data_ptr(), 65536, 1024, 0.1,
-                                                 ctypes.byref(lossv), G64.data_ptr()), 16 * S.numel())
+                                                 ctypes.byref(lossv), G64.data_ptr()), 16 * S.numel(), elems=S.numel())
     timeit("ls_ce forward f64 [65536,1024] (result on the host)",
            lambda: _lib.label_smoothing_ce_forward(S64.data_ptr(), tgt.data_ptr(), 65536, 1024, 0.1,
-                                                   ctypes.byref(lossv)), 8 * S.numel())
+                                                   ctypes.byref(lossv)), 8 * S.numel(), elems=S.numel())
     del S, tS, S64, G64
     # cfg3 activations
     x4 = torch.randn(64, 64, 128, 128, device=dev) * 4
@@ -405,7 +429,7 @@ def suite(torch, pn, stream):
                 f = (lambda fn=fn: fn(yy._ptr, xx._ptr, ctypes.c_double(0.01 if nm == "leaky_relu" else 1.0)))
             else:
                 f = (lambda fn=fn: fn(yy._ptr, xx._ptr))
-            timeit(f"act_{nm} {dt_name} [64,64,128,128]", f, bpe * ne)
+            timeit(f"act_{nm} {dt_name} [64,64,128,128]", f, bpe * ne, elems=ne)
         if dt_name == "f64":
             del x8, y8
     del x4, y4
@@ -417,11 +441,11 @@ def suite(torch, pn, stream):
     pbuf = torch.zeros(5, dtype=torch.float64, device=dev)
     torch.cuda.synchronize()
     timeit("calibrate_minmax f32 268M (device params)",
-           lambda: _lib.calibrate_minmax_f32_dev(q_in.data_ptr(), nq, 0, pbuf.data_ptr()), 4 * nq)
+           lambda: _lib.calibrate_minmax_f32_dev(q_in.data_ptr(), nq, 0, pbuf.data_ptr()), 4 * nq, elems=nq)
     timeit("quantize f32->i8 268M", lambda: _lib.quantize_tensor_f32_dev(q_in.data_ptr(), q8.data_ptr(), nq,
-                                                                       pbuf.data_ptr()), 5 * nq)
+                                                                       pbuf.data_ptr()), 5 * nq, elems=nq)
     timeit("dequantize i8->f32 268M", lambda: _lib.dequantize_tensor_f32_dev(q8.data_ptr(), dq.data_ptr(), nq,
-                                                                           pbuf.data_ptr()), 5 * nq)
+                                                                           pbuf.data_ptr()), 5 * nq, elems=nq)
     del q_in, q8, dq
     # cfg5 AdamW + scan
     na = 100_000_000
@@ -430,10 +454,10 @@ def suite(torch, pn, stream):
     tp, tg = W(p), W(gr)
     torch.cuda.synchronize()
     opt = pn.AdamW(1e-3, 0.9, 0.999, 1e-8, 0.01)
-    timeit("adamw f32 params, f64 m/v, 100M", lambda: opt.step([tp], [tg]), 44 * na)
+    timeit("adamw f32 params, f64 m/v, 100M", lambda: opt.step([tp], [tg]), 44 * na, elems=na)
     hn, hi, ss = ctypes.c_int(), ctypes.c_int(), ctypes.c_double()
     timeit("nan/inf/l2 scan f32 100M (result on the host)",
-           lambda: _lib.neural_tensor_scan(tg._ptr, ctypes.byref(hn), ctypes.byref(hi), ctypes.byref(ss)), 4 * na)
+           lambda: _lib.neural_tensor_scan(tg._ptr, ctypes.byref(hn), ctypes.byref(hi), ctypes.byref(ss)), 4 * na, elems=na)
     # per-feature transforms on [1M, 64] f64 (512 MB), device pointers
     tb_rows, tb_f = 1 << 20, 64
     tdat = torch.randn(tb_rows, tb_f, device=dev, dtype=torch.float64) * 3 + 1
@@ -441,22 +465,21 @@ def suite(torch, pn, stream):
     tstat = [torch.empty(tb_f, device=dev, dtype=torch.float64) for _ in range(4)]
     torch.cuda.synchronize()
     timeit("transform_compute_stats f64 [1M,64] (mean/std/min/max)",
-           lambda: _lib.transform_compute_stats(tdat.data_ptr(), tb_rows, tb_f, *[s.data_ptr() for s in tstat]),
-           8 * tdat.numel())
+           lambda: _lib.transform_compute_stats(tdat.data_ptr(), tb_rows, tb_f, *[s.data_ptr() for s in tstat]), 8 * tdat.numel(), elems=tdat.numel())
     timeit("transform_normalize f64 [1M,64]",
            lambda: _lib.transform_normalize(tdat.data_ptr(), tout.data_ptr(), tb_rows, tb_f, tstat[0].data_ptr(),
-                                            tstat[1].data_ptr(), ctypes.c_double(1e-8)), 16 * tdat.numel())
+                                            tstat[1].data_ptr(), ctypes.c_double(1e-8)), 16 * tdat.numel(), elems=tdat.numel())
     del tdat, tout
     # gradient clipping over the same 100M gradients (no host readback).  A
     # negative max_norm clips on every call (scale -|max|/norm, magnitudes kept).
     glist = (ctypes.c_void_p * 1)(tg._ptr)
     norm0 = float(ss.value) ** 0.5
     timeit("clip_grad_norm f32 100M, clipping (sumsq + scale)",
-           lambda: _lib.neural_clip_grad_norm_list(glist, 1, ctypes.c_double(-norm0), None), 12 * na)
+           lambda: _lib.neural_clip_grad_norm_list(glist, 1, ctypes.c_double(-norm0), None), 12 * na, elems=na)
     timeit("clip_grad_norm f32 100M, below threshold (sumsq only)",
-           lambda: _lib.neural_clip_grad_norm_list(glist, 1, ctypes.c_double(1e300), None), 4 * na)
+           lambda: _lib.neural_clip_grad_norm_list(glist, 1, ctypes.c_double(1e300), None), 4 * na, elems=na)
     timeit("clip_grad_value f32 100M",
-           lambda: _lib.neural_clip_grad_value_list(glist, 1, ctypes.c_double(-1e-3), ctypes.c_double(1e-3)), 8 * na)
+           lambda: _lib.neural_clip_grad_value_list(glist, 1, ctypes.c_double(-1e-3), ctypes.c_double(1e-3)), 8 * na, elems=na)
     return out
 
 
