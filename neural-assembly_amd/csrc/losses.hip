@@ -67,18 +67,21 @@ struct CeArgs {
 };
 
 // Per-element work once m and s are known.  Returns the element's part of the
-// row loss without the log term (label-smoothed: st * (x - m)) and writes the
-// gradient element.  The row loss is -sum_c st_c ((x_c - m) - lse) =
-// lse * sum_c st_c - sum_c st_c (x_c - m); every term of the reference's sum
-// has one sign (x_c - m <= 0, lse >= 0), so the regrouping changes only the
-// last bits, and the log moves out of the row kernel into the summing pass.
+// row loss without the log term and without its weight (label-smoothed:
+// x - m) and writes the gradient element.  The row loss is
+// -sum_c st_c ((x_c - m) - lse) = lse * sum_c st_c - A with
+// A = sum_c st_c (x_c - m) = st0 * sum_c (x_c - m) + (st1 - st0) (x_t - m)
+// (st_c = st0 off the target, st1 on it): every term of the reference's sum
+// has one sign (x_c - m <= 0, lse >= 0), and so have the two parts of A, so
+// the regrouping changes only the last bits; the log moves out of the row
+// kernel into the summing pass and the weights out of the element loop.
 template <typename T, int MODE>
 NH_DEV double ce_elem(T xv, int64_t c, int64_t t, double m, double rs, const CeArgs &a, T &g)
 {
     const double x = double(xv);
     const double st = a.alpha / double(a.cols) + (c == t ? 1.0 - a.alpha : 0.0);
     double term = 0.0;
-    if (MODE == CE_LS_FWD || MODE == CE_LS_FUSED) term = st * (x - m);
+    if (MODE == CE_LS_FWD || MODE == CE_LS_FUSED) term = x - m;
     if (MODE == CE_LS_BWD || MODE == CE_LS_FUSED) {
         const double e = sizeof(T) == 8 ? row_exp_d(x, m) : row_exp_f(float(xv), m);
         g = T(a.inv_n * (e * rs - st));
@@ -191,13 +194,11 @@ __global__ __launch_bounds__(256) void k_ce_wave(const T *__restrict__ x, CeArgs
             if (FULL || c0 + j < cols) {
                 const bool at_t = c0 + j == t;
                 if constexpr (sizeof(T) == 4) {
-                    const float st = at_t ? st1f : st0f;
-                    if (MODE == CE_LS_FWD || MODE == CE_LS_FUSED) acc += double(st * (v[k][j] - mf));
-                    if constexpr (KEEP) g[j] = inf_ * (ev[k][j] * rsf - st);
+                    if (MODE == CE_LS_FWD || MODE == CE_LS_FUSED) acc += double(v[k][j] - mf);
+                    if constexpr (KEEP) g[j] = inf_ * (ev[k][j] * rsf - (at_t ? st1f : st0f));
                 } else {
-                    const double st = at_t ? st1 : st0;
-                    if (MODE == CE_LS_FWD || MODE == CE_LS_FUSED) acc += st * (double(v[k][j]) - m);
-                    if constexpr (KEEP) g[j] = T(a.inv_n * (double(ev[k][j]) * rs - st));
+                    if (MODE == CE_LS_FWD || MODE == CE_LS_FUSED) acc += double(v[k][j]) - m;
+                    if constexpr (KEEP) g[j] = T(a.inv_n * (double(ev[k][j]) * rs - (at_t ? st1 : st0)));
                 }
             }
         if (MODE == CE_LS_BWD || MODE == CE_LS_FUSED) {
@@ -212,8 +213,27 @@ __global__ __launch_bounds__(256) void k_ce_wave(const T *__restrict__ x, CeArgs
     }
     if (MODE == CE_LS_FWD || MODE == CE_LS_FUSED) {
         acc = wave_dsum(acc);
+        // x_t from the registers of the lane that holds it: its vector k and
+        // slot j are the same for every lane, so the pick is a uniform select
+        const int kt = int(t / (64 * VN)), jt = int(t % VN), owner = int((t / VN) % 64);
+        T xl = T(0);
+#pragma unroll
+        for (int k = 0; k < VPL; k++)
+#pragma unroll
+            for (int j = 0; j < VN; j++)
+                if (k == kt && j == jt) xl = v[k][j];
+        double xv;
+        if constexpr (sizeof(T) == 4) {
+            xv = double(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(xl), owner)));
+        } else {
+            const long long xb = __double_as_longlong(double(xl));
+            const int lo = __builtin_amdgcn_readlane(int(xb), owner);
+            const int hi = __builtin_amdgcn_readlane(int(xb >> 32), owner);
+            xv = __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<unsigned int>(lo));
+        }
         if (lane == 0) {
-            a.row_loss[r] = acc;
+            const double xt = sizeof(T) == 4 ? double(float(xv) - mf) : xv - m;
+            a.row_loss[r] = st0 * acc + (st1 - st0) * xt;
             a.row_s[r] = s;
         }
     }
@@ -246,7 +266,7 @@ __global__ __launch_bounds__(256) void k_ce_block(const T *__restrict__ x, CeArg
     }
     if (MODE == CE_ASM) {
         if (threadIdx.x == 0) {
-            if (sizeof(T) == 4) a.row_loss[r] = double(exp_d2f(double(xr[t]) - m) / float(s));
+            if (sizeof(T) == 4) a.row_loss[r] = double(float(row_exp_f(float(xr[t]), m)) / float(s));
             else a.row_loss[r] = row_exp_d(double(xr[t]), m) / s;
         }
         return;
@@ -262,7 +282,9 @@ __global__ __launch_bounds__(256) void k_ce_block(const T *__restrict__ x, CeArg
     if (MODE == CE_LS_FWD || MODE == CE_LS_FUSED) {
         acc = G::reduce(acc, [](double p, double q) { return p + q; });
         if (threadIdx.x == 0) {
-            a.row_loss[r] = acc;
+            const double st0 = a.alpha / double(cols), st1 = st0 + (1.0 - a.alpha);
+            const double xt = double(xr[t]) - m;  // as ce_elem forms the other terms
+            a.row_loss[r] = st0 * acc + (st1 - st0) * xt;
             a.row_s[r] = s;
         }
     }
