@@ -145,8 +145,11 @@ NH_DEV double feat_map(double v, double a, double c, double eps)
 
 // Pairs of elements (F even, 16-byte aligned): pair p holds features f, f+1
 // with f = 2p mod F.  f advances by d1 = 512 mod F between unrolled slots and
-// by dS = 2 * stride mod F between grid-stride steps.
-template <int MODE>
+// by dS = 2 * stride mod F between grid-stride steps.  FIXED (d1 = dS = 0,
+// e.g. F = 64): a lane meets the same two features throughout, so their
+// parameters are loaded once instead of with every vector (four parameter
+// loads per 16-byte data load otherwise).
+template <int MODE, bool FIXED>
 __global__ __launch_bounds__(kTBlock) void k_feat_map2(const f64x2 *__restrict__ x, f64x2 *__restrict__ o,
                                                         int64_t n2, int64_t F, const double *__restrict__ A,
                                                         const double *__restrict__ C, double eps, int64_t d1,
@@ -155,6 +158,28 @@ __global__ __launch_bounds__(kTBlock) void k_feat_map2(const f64x2 *__restrict__
     const int64_t tile = int64_t(kTBlock) * kTUnroll;
     int64_t base = int64_t(blockIdx.x) * tile + threadIdx.x;
     int64_t fb = (2 * base) % F;
+    if constexpr (FIXED) {
+        const double a0 = A[fb], a1 = A[fb + 1], c0 = C[fb], c1 = C[fb + 1];
+        for (; base < n2; base += int64_t(gridDim.x) * tile) {
+            f64x2 v[kTUnroll];
+#pragma unroll
+            for (int u = 0; u < kTUnroll; u++) {
+                const int64_t i = base + int64_t(u) * kTBlock;
+                if (i < n2) v[u] = ld_nt(x + i);
+            }
+#pragma unroll
+            for (int u = 0; u < kTUnroll; u++) {
+                const int64_t i = base + int64_t(u) * kTBlock;
+                if (i < n2) {
+                    f64x2 r;
+                    r[0] = feat_map<MODE>(v[u][0], a0, c0, eps);
+                    r[1] = feat_map<MODE>(v[u][1], a1, c1, eps);
+                    st_nt(o + i, r);
+                }
+            }
+        }
+        return;
+    }
     for (; base < n2; base += int64_t(gridDim.x) * tile) {
         f64x2 v[kTUnroll];
         int64_t fu[kTUnroll];
@@ -266,9 +291,15 @@ static int feat_apply(const double *data, double *out, int64_t b, int64_t F, con
         const int64_t n2 = n / 2;
         const unsigned g = t_grid(ceil_div(n2, kTUnroll));
         const int64_t stride = int64_t(g) * kTBlock * kTUnroll;
-        hipLaunchKernelGGL(k_feat_map2<MODE>, dim3(g), dim3(kTBlock), 0, stream(), reinterpret_cast<const f64x2 *>(X),
-                           reinterpret_cast<f64x2 *>(O), n2, F, A, C, eps, (2 * int64_t(kTBlock)) % F,
-                           (2 * stride) % F);
+        const int64_t d1 = (2 * int64_t(kTBlock)) % F, dS = (2 * stride) % F;
+        if (d1 == 0 && dS == 0)
+            hipLaunchKernelGGL((k_feat_map2<MODE, true>), dim3(g), dim3(kTBlock), 0, stream(),
+                               reinterpret_cast<const f64x2 *>(X), reinterpret_cast<f64x2 *>(O), n2, F, A, C, eps, d1,
+                               dS);
+        else
+            hipLaunchKernelGGL((k_feat_map2<MODE, false>), dim3(g), dim3(kTBlock), 0, stream(),
+                               reinterpret_cast<const f64x2 *>(X), reinterpret_cast<f64x2 *>(O), n2, F, A, C, eps, d1,
+                               dS);
     } else {
         const unsigned g = t_grid(n);
         hipLaunchKernelGGL(k_feat_map1<MODE>, dim3(g), dim3(kTBlock), 0, stream(), X, O, n, F, A, C, eps,
