@@ -252,6 +252,13 @@ typedef struct {
     int     symmetric;
 } QuantParams;
 int    calibrate_minmax(const double *data, int64_t n, int symmetric, QuantParams *out); /* quantize.c:52 */
+/* quantized_matmul (quantize.c:191-214): C[M x N] = (double)acc * (sa * sb),
+ * acc = sum_k (A[i][k] - za)(B[k][j] - zb) in int32 (wrapping), A [M x K] and
+ * B [K x N] row-major int8; host or device pointers; 0, or -1 for NULL
+ * pointers / non-positive sizes / more than 8,388,480 rows or 1,048,560
+ * columns of A. */
+int    quantized_matmul(const int8_t *A, const int8_t *B, double *C, int64_t M, int64_t K, int64_t N,
+                        const QuantParams *params_a, const QuantParams *params_b);
 int    quantize_tensor(const double *data, int8_t *out, int64_t n, const QuantParams *p);/* quantize.c:144 */
 int    dequantize_tensor(const int8_t *data, double *out, int64_t n, const QuantParams *p);/* quantize.c:163 */
 double quantization_error(const double *original, int64_t n, const QuantParams *p);   /* quantize.c:222 */
@@ -354,7 +361,7 @@ int neural_cross_entropy_loss(const NeuralTensor *prediction, const NeuralTensor
  * exports them for that loader to succeed.  The subsystems behind them
  * (layers, recurrent cells, pooling, attention, fuzzy logic, pruning,
  * datasets, config, metrics, TensorBoard writer, weight init, LR schedules,
- * the asm optimizer handles, int8 matmul, percentile calibration) are outside
+ * the asm optimizer handles, percentile calibration) are outside
  * this library's scope.  Each records NEURAL_ERR_NOT_IMPLEMENTED as the last
  * error and returns: NEURAL_ERR_NOT_IMPLEMENTED (int neural_* functions), -1
  * (other int and int64_t functions, the C modules' failure value), NULL
@@ -448,7 +455,6 @@ int neural_get_simd_level(void);  /* core.py:110 */
 int neural_matmul(void *, void *, void *);  /* core.py:178 */
 int neural_mse_loss(void *, void *, double *);  /* core.py:372 */
 int neural_weighted_sample_indices(void *, uint64_t, uint64_t, void *, int);  /* core.py:618 */
-int quantized_matmul(void *, void *, void *, int64_t, int64_t, int64_t, QuantParams *, QuantParams *);  /* core.py:770 */
 int roc_auc_score(void *, void *, int64_t, double *);  /* core.py:893 */
 int64_t count_nonzero(void *, int64_t);  /* core.py:708 */
 void apply_mask(void *, void *, int64_t);  /* core.py:718 */

@@ -332,10 +332,6 @@ int neural_mse_loss(void *, void *, double *) {
 int neural_weighted_sample_indices(void *, uint64_t, uint64_t, void *, int) {
     return nh::set_error(NEURAL_ERR_NOT_IMPLEMENTED);
 }
-int quantized_matmul(void *, void *, void *, int64_t, int64_t, int64_t, QuantParams *, QuantParams *) {
-    nh::set_error(NEURAL_ERR_NOT_IMPLEMENTED);
-    return -1;
-}
 int roc_auc_score(void *, void *, int64_t, double *) {
     nh::set_error(NEURAL_ERR_NOT_IMPLEMENTED);
     return -1;

@@ -19,7 +19,7 @@ from .nn import (ReLU, Sigmoid, Softmax, LogSoftmax, Tanh, CrossEntropyLoss, Lab
                  dropout_seed, add_relu, bias_add_act)
 from .activations import GELU, LeakyReLU, ELU, SELU, Swish, Mish, HardSwish, Softplus, HardTanh
 from .optim import SGD, Adam, AdamW
-from .quantize import Quantizer, QuantParams
+from .quantize import Quantizer, QuantParams, quantized_matmul
 from .training import NaNDetector, grad_l2_norm, clip_grad_norm, clip_grad_value
 from .checkpoint import save_checkpoint, load_checkpoint
 from .transforms import Normalize, MinMaxScale, Compose, compute_stats

@@ -238,6 +238,7 @@ _SIGS = {
     "neural_clip_grad_value_list": (_i, [ctypes.POINTER(_vp), _i64, _d, _d]),
     # quantization
     "calibrate_minmax": (_i, [_vp, _i64, _i, _qp]),
+    "quantized_matmul": (_i, [_vp, _vp, _vp, _i64, _i64, _i64, _qp, _qp]),
     "quantize_tensor": (_i, [_vp, _vp, _i64, _qp]),
     "dequantize_tensor": (_i, [_vp, _vp, _i64, _qp]),
     "quantization_error": (_d, [_vp, _i64, _qp]),

@@ -115,6 +115,26 @@ class Quantizer:
         return f"Quantizer({mode}, {calib})"
 
 
-def quantized_matmul(*args, **kwargs):
-    """int8 GEMM is outside this library's memory-bound hot path."""
-    raise NeuralException(NeuralError.NOT_IMPLEMENTED, "quantized_matmul")
+def quantized_matmul(a_int8, b_int8, m: int, k: int, n: int, params_a: QuantParams,
+                     params_b: QuantParams) -> ctypes.Array:
+    """C[M,N] = dequant(A[M,K]) @ dequant(B[K,N]) (reference quantize.py:195-223,
+    quantize.c:191-214): the inner sum in int32, then scaled to float64, on the
+    matrix cores.  a_int8 / b_int8 are ctypes int8 arrays (or anything with a
+    buffer, e.g. numpy int8 arrays); returns a ctypes float64 array of m*n."""
+    c_out = (ctypes.c_double * (m * n))()
+    pa = params_a._to_c()
+    pb = params_b._to_c()
+    rc = core._lib.quantized_matmul(_buf_ptr(a_int8), _buf_ptr(b_int8), ctypes.addressof(c_out), ctypes.c_int64(m),
+                               ctypes.c_int64(k), ctypes.c_int64(n), ctypes.byref(pa), ctypes.byref(pb))
+    if rc != 0:
+        raise RuntimeError("Quantized matmul failed")
+    return c_out
+
+
+def _buf_ptr(a) -> int:
+    """Address of a ctypes array, a numpy array or an integer address."""
+    if isinstance(a, int):
+        return a
+    if hasattr(a, "ctypes"):
+        return a.ctypes.data
+    return ctypes.addressof(a)

@@ -937,6 +937,31 @@ void ora_clip_grad_value(void **grads, const int *dtypes, const int64_t *ns, int
     }
 }
 
+/* quantized_matmul (quantize.c:191-214): combined_scale = sa * sb;
+ * acc = sum_k ((int32)A[i][k] - za) * ((int32)B[k][j] - zb) in int32, the
+ * reference's loop order; the adds and multiplies wrap mod 2^32 (the compiled
+ * reference's behaviour; written in uint32 here so that C defines it);
+ * C[i][j] = (double)acc * combined_scale. */
+int ora_quantized_matmul(const int8_t *A, const int8_t *B, double *C, int64_t M, int64_t K, int64_t N,
+                         const OraQuantParams *pa, const OraQuantParams *pb)
+{
+    if (!A || !B || !C || !pa || !pb) return -1;
+    if (M <= 0 || K <= 0 || N <= 0) return -1;
+    const double cs = pa->scale * pb->scale;
+    const uint32_t za = (uint32_t)pa->zero_point, zb = (uint32_t)pb->zero_point;
+    for (int64_t i = 0; i < M; i++)
+        for (int64_t j = 0; j < N; j++) {
+            uint32_t acc = 0;
+            for (int64_t k = 0; k < K; k++) {
+                const uint32_t a = (uint32_t)(int32_t)A[i * K + k] - za;
+                const uint32_t b = (uint32_t)(int32_t)B[k * N + j] - zb;
+                acc += a * b;
+            }
+            C[i * N + j] = (double)(int32_t)acc * cs;
+        }
+    return 0;
+}
+
 /* ---- dropout and the fused add + relu -------------------------------------------- */
 
 /* cvtsd2si under the default MXCSR rounding (nearest even); NaN and values

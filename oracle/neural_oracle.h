@@ -149,6 +149,8 @@ void   ora_clip_grad_value(void **grads, const int *dtypes, const int64_t *ns, i
  * Pinned in tests/test_oracle_dropout.py: rand() against a restatement of
  * glibc's TYPE_3 generator, hand-derived thresholds (p = 0.5 rounds half to
  * even), keep rates, the closed forms of out and the backward. */
+int  ora_quantized_matmul(const int8_t *A, const int8_t *B, double *C, int64_t M, int64_t K, int64_t N,
+                          const OraQuantParams *pa, const OraQuantParams *pb);
 void ora_srand(unsigned seed);
 int  ora_dropout_forward(const float *in, float *out, uint8_t *mask, uint64_t n, float p);
 int  ora_dropout_backward(const float *go, float *gi, const uint8_t *mask, uint64_t n, float p);

@@ -221,6 +221,20 @@ def dequantize(q, p, dtype=np.float64):
     return out
 
 
+def quantized_matmul(a, b, m, k, n, pa, pb, use_ref=False):
+    """C [m x n] float64 of int8 a [m x k] and b [k x n] (quantize.c:191-214);
+    use_ref: the reference's own quantize.c (oracle/_ref)."""
+    a = np.ascontiguousarray(a, dtype=np.int8)
+    b = np.ascontiguousarray(b, dtype=np.int8)
+    c = np.empty(m * n, dtype=np.float64)
+    f = ref().quantized_matmul if use_ref else lib().ora_quantized_matmul
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                  ctypes.POINTER(QuantParams), ctypes.POINTER(QuantParams)]
+    rc = f(_p(a), _p(b), _p(c), m, k, n, ctypes.byref(pa), ctypes.byref(pb))
+    return rc, c.reshape(m, n)
+
+
 def quant_error(x, p):
     f = lib().ora_quant_error_f32 if x.dtype == np.float32 else lib().ora_quant_error
     return f(_p(x), ctypes.c_int64(x.size), ctypes.byref(p))

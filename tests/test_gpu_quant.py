@@ -158,3 +158,79 @@ def test_calibrate_zero_extremes_large(pn, ora, first_zero):
         _params_equal(_calib(pn, y, sym), ora.calibrate(y, sym))
     y[rng.choice(n, 10, replace=False)] = np.nan  # NaNs after x0 are skipped
     _params_equal(_calib(pn, y, False), ora.calibrate(y, False))
+
+
+# ---- quantized_matmul (quantize.c:191-214) on the matrix cores ---------------------
+
+def _qmm_params(ora, za, zb):
+    pa, pb = ora.QuantParams(), ora.QuantParams()
+    pa.scale, pa.zero_point = 0.0123, za
+    pb.scale, pb.zero_point = 3.7e-3, zb
+    return pa, pb
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (3, 5, 7), (128, 128, 128), (130, 257, 129), (64, 4096, 64),
+                                   (257, 33, 1000), (300, 1000, 500)])
+@pytest.mark.parametrize("za,zb", [(0, 0), (-128, 127), (17, -3)])
+def test_quantized_matmul_bit_exact(pn, ora, m, k, n, za, zb):
+    rng = np.random.default_rng(m + 7 * k + 13 * n + za + 1000)
+    a = rng.integers(-128, 128, (m, k), dtype=np.int64).astype(np.int8)
+    b = rng.integers(-128, 128, (k, n), dtype=np.int64).astype(np.int8)
+    pa, pb = _qmm_params(ora, za, zb)
+    got = np.empty((m, n))
+    lib = pn.core._lib
+    qa, qb = pn.core.QuantParamsC(), pn.core.QuantParamsC()
+    ctypes.memmove(ctypes.byref(qa), ctypes.byref(pa), ctypes.sizeof(qa))
+    ctypes.memmove(ctypes.byref(qb), ctypes.byref(pb), ctypes.sizeof(qb))
+    assert lib.quantized_matmul(a.ctypes.data, b.ctypes.data, got.ctypes.data, m, k, n, ctypes.byref(qa),
+                                ctypes.byref(qb)) == 0
+    rc, want = ora.quantized_matmul(a, b, m, k, n, pa, pb)
+    assert rc == 0
+    same_bits(got.reshape(-1), want.reshape(-1))
+
+
+def test_quantized_matmul_device_wrap_and_errors(pn, ora):
+    import torch
+    lib = pn.core._lib
+    # device pointers
+    rng = np.random.default_rng(5)
+    m, k, n = 200, 3000, 150
+    a = rng.integers(-128, 128, (m, k), dtype=np.int64).astype(np.int8)
+    b = rng.integers(-128, 128, (k, n), dtype=np.int64).astype(np.int8)
+    pa, pb = _qmm_params(ora, -5, 9)
+    qa, qb = pn.core.QuantParamsC(), pn.core.QuantParamsC()
+    ctypes.memmove(ctypes.byref(qa), ctypes.byref(pa), ctypes.sizeof(qa))
+    ctypes.memmove(ctypes.byref(qb), ctypes.byref(pb), ctypes.sizeof(qb))
+    da, db = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+    dc = torch.empty(m, n, dtype=torch.float64, device="cuda")
+    torch.cuda.synchronize()
+    assert lib.quantized_matmul(da.data_ptr(), db.data_ptr(), dc.data_ptr(), m, k, n, ctypes.byref(qa),
+                                ctypes.byref(qb)) == 0
+    torch.cuda.synchronize()
+    same_bits(dc.cpu().numpy().reshape(-1), ora.quantized_matmul(a, b, m, k, n, pa, pb)[1].reshape(-1))
+    # a sum past int32 wraps mod 2^32, as in the compiled reference
+    k2 = 40_000
+    a2 = np.full((3, k2), -128, dtype=np.int8)
+    a2[1, ::3] = 100
+    b2 = np.full((k2, 5), 127, dtype=np.int8)
+    b2[::7, 2] = -77
+    p1, p2 = _qmm_params(ora, 127, -128)
+    q1, q2 = pn.core.QuantParamsC(), pn.core.QuantParamsC()
+    ctypes.memmove(ctypes.byref(q1), ctypes.byref(p1), ctypes.sizeof(q1))
+    ctypes.memmove(ctypes.byref(q2), ctypes.byref(p2), ctypes.sizeof(q2))
+    got = np.empty((3, 5))
+    assert lib.quantized_matmul(a2.ctypes.data, b2.ctypes.data, got.ctypes.data, 3, k2, 5, ctypes.byref(q1),
+                                ctypes.byref(q2)) == 0
+    same_bits(got.reshape(-1), ora.quantized_matmul(a2, b2, 3, k2, 5, p1, p2)[1].reshape(-1))
+    # the Python layer (reference quantize.py:195-223): ctypes arrays in, ctypes float64 array out
+    ca = (ctypes.c_int8 * (m * k)).from_buffer_copy(a.tobytes())
+    cb = (ctypes.c_int8 * (k * n)).from_buffer_copy(b.tobytes())
+    P = pn.QuantParams(scale=pa.scale, zero_point=pa.zero_point)
+    Q = pn.QuantParams(scale=pb.scale, zero_point=pb.zero_point)
+    out = pn.quantized_matmul(ca, cb, m, k, n, P, Q)
+    same_bits(np.frombuffer(out, dtype=np.float64), ora.quantized_matmul(a, b, m, k, n, pa, pb)[1].reshape(-1))
+    # errors (0 / -1 like the reference)
+    assert lib.quantized_matmul(None, b.ctypes.data, got.ctypes.data, m, k, n, ctypes.byref(qa), ctypes.byref(qb)) == -1
+    assert lib.quantized_matmul(a.ctypes.data, b.ctypes.data, got.ctypes.data, 0, k, n, ctypes.byref(qa),
+                                ctypes.byref(qb)) == -1
+    assert lib.quantized_matmul(a.ctypes.data, b.ctypes.data, got.ctypes.data, m, k, n, None, ctypes.byref(qb)) == -1

@@ -244,3 +244,44 @@ def test_tensor_ops_bit_exact(ora, ref):
     assert ref.tensor_transpose2d_array(x.ctypes.data, 5, 7, out.ctypes.data) == 0
     rc, oo = ora.transpose_2d(x, 5, 7)
     same_bits(oo, out)
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (3, 5, 7), (16, 64, 9), (33, 130, 17)])
+@pytest.mark.parametrize("za,zb", [(0, 0), (-128, 127), (17, -3)])
+def test_quantized_matmul_matches_reference(ora, m, k, n, za, zb):
+    """ora_quantized_matmul against quantize.c:191-214 compiled unchanged."""
+    if ora.ref() is None:
+        pytest.skip("reference C build (oracle/_ref) absent")
+    rng = np.random.default_rng(m * 1000 + k + n)
+    a = rng.integers(-128, 128, (m, k), dtype=np.int64).astype(np.int8)
+    b = rng.integers(-128, 128, (k, n), dtype=np.int64).astype(np.int8)
+    pa, pb = ora.QuantParams(), ora.QuantParams()
+    pa.scale, pa.zero_point = 0.0123, za
+    pb.scale, pb.zero_point = 3.7e-3, zb
+    rc, got = ora.quantized_matmul(a, b, m, k, n, pa, pb)
+    rc2, want = ora.quantized_matmul(a, b, m, k, n, pa, pb, use_ref=True)
+    assert rc == 0 and rc2 == 0
+    assert np.array_equal(got.view(np.uint64), want.view(np.uint64))
+    # the closed form in exact integers when nothing overflows int32
+    acc = (a.astype(np.int64) - za) @ (b.astype(np.int64) - zb)
+    assert np.array_equal(got, acc.astype(np.float64) * (pa.scale * pb.scale))
+
+
+def test_quantized_matmul_wraps_like_reference(ora):
+    """A sum past int32 wraps mod 2^32 in the compiled reference and in the oracle."""
+    if ora.ref() is None:
+        pytest.skip("reference C build (oracle/_ref) absent")
+    k = 40_000  # 40,000 x 255 x 255 > 2^31
+    a = np.full((2, k), -128, dtype=np.int8)
+    b = np.full((k, 3), 127, dtype=np.int8)
+    pa, pb = ora.QuantParams(), ora.QuantParams()
+    pa.scale, pa.zero_point = 1.0, 127
+    pb.scale, pb.zero_point = 1.0, -128
+    _, got = ora.quantized_matmul(a, b, 2, k, 3, pa, pb)
+    _, want = ora.quantized_matmul(a, b, 2, k, 3, pa, pb, use_ref=True)
+    assert np.array_equal(got, want)
+    exact = -255 * 255 * k
+    wrapped = (exact + 2 ** 31) % 2 ** 32 - 2 ** 31
+    assert got[0, 0] == float(wrapped) and exact != wrapped
+    # errors
+    assert ora.quantized_matmul(a, b, 0, k, 3, pa, pb)[0] == -1
