@@ -447,6 +447,17 @@ def suite(torch, pn, stream):
     timeit("dequantize i8->f32 268M", lambda: _lib.dequantize_tensor_f32_dev(q8.data_ptr(), dq.data_ptr(), nq,
                                                                            pbuf.data_ptr()), 5 * nq, elems=nq)
     del q_in, q8, dq
+    # percentile calibration: exact radix select of two order statistics, 8 passes
+    # over the data with a host read of the histograms between passes; bytes
+    # counted as ONE read of the input (the algorithmic minimum)
+    npc = 1 << 26
+    pc_in = torch.randn(npc, device=dev, dtype=torch.float64)
+    qp = pn.core.QuantParamsC()
+    torch.cuda.synchronize()
+    timeit("calibrate_percentile f64 64M p=0.01 (result on the host)",
+           lambda: _lib.calibrate_percentile(pc_in.data_ptr(), npc, ctypes.c_double(0.01), 0, ctypes.byref(qp)),
+           8 * npc, reps=5, elems=npc)
+    del pc_in
     # cfg5 AdamW + scan
     na = 100_000_000
     p = torch.randn(na, device=dev) * 0.02

@@ -259,6 +259,12 @@ int    calibrate_minmax(const double *data, int64_t n, int symmetric, QuantParam
  * columns of A. */
 int    quantized_matmul(const int8_t *A, const int8_t *B, double *C, int64_t M, int64_t K, int64_t N,
                         const QuantParams *params_a, const QuantParams *params_b);
+/* calibrate_percentile (quantize.c:89-132): calibrate on [sorted[lo], sorted[hi]]
+ * of the data in the order of quantize.c's comparator, lo = (int64)(n p),
+ * hi = (int64)(n (1 - p)), p outside [0, 0.5] taken as 0.01; host or device
+ * data; 0, or -1 for NULL / n <= 0 / a NaN p (which the reference does not
+ * survive). */
+int    calibrate_percentile(const double *data, int64_t n, double percentile, int symmetric, QuantParams *out);
 int    quantize_tensor(const double *data, int8_t *out, int64_t n, const QuantParams *p);/* quantize.c:144 */
 int    dequantize_tensor(const int8_t *data, double *out, int64_t n, const QuantParams *p);/* quantize.c:163 */
 double quantization_error(const double *original, int64_t n, const QuantParams *p);   /* quantize.c:222 */
@@ -361,7 +367,7 @@ int neural_cross_entropy_loss(const NeuralTensor *prediction, const NeuralTensor
  * exports them for that loader to succeed.  The subsystems behind them
  * (layers, recurrent cells, pooling, attention, fuzzy logic, pruning,
  * datasets, config, metrics, TensorBoard writer, weight init, LR schedules,
- * the asm optimizer handles, percentile calibration) are outside
+ * the asm optimizer handles) are outside
  * this library's scope.  Each records NEURAL_ERR_NOT_IMPLEMENTED as the last
  * error and returns: NEURAL_ERR_NOT_IMPLEMENTED (int neural_* functions), -1
  * (other int and int64_t functions, the C modules' failure value), NULL
@@ -450,7 +456,6 @@ void lstm_free(void *);  /* core.py:312 */
 const char *neural_get_simd_name(void);  /* core.py:113 */
 double compute_sparsity(void *, int64_t);  /* core.py:705 */
 double compute_threshold_for_sparsity(void *, int64_t, double);  /* core.py:711 */
-int calibrate_percentile(void *, int64_t, double, int, QuantParams *);  /* core.py:745 */
 int neural_get_simd_level(void);  /* core.py:110 */
 int neural_matmul(void *, void *, void *);  /* core.py:178 */
 int neural_mse_loss(void *, void *, double *);  /* core.py:372 */

@@ -15,16 +15,10 @@
 //   dequantize: ((double)q - (double)zp) * scale.
 #include <cmath>
 
+#include "quant_common.hpp"
 #include "reduce_impl.hpp"
 
 namespace nh {
-
-// cvttsd2si of an already-rounded double.
-NH_DEV int32_t x86_cvt_i32(double r)
-{
-    if (!(r > -2147483649.0 && r < 2147483648.0)) return int32_t(0x80000000u);
-    return int32_t(r);
-}
 
 // q = clamp((int32)round(x * inv) + zp, -128, 127) with the reference build's
 // x86 semantics.  For |x * inv| <= 2^30 (everything but NaN and huge
@@ -47,32 +41,6 @@ NH_DEV int8_t quant_one(double x, double inv, int32_t zp)
     return int8_t(q);
 }
 
-NH_DEV void minmax_epilogue(double mn, double mx, int symmetric, QuantParams *out)
-{
-    QuantParams p;
-    p.zero_point = 0;
-    if (symmetric) {
-        double am = fmax(fabs(mn), fabs(mx));
-        if (am < 1e-30) am = 1e-30;
-        p.scale = am / 127.0;
-        p.zero_point = 0;
-        p.min_val = -am;
-        p.max_val = am;
-        p.symmetric = 1;
-    } else {
-        if (mn == mx) { mn -= 0.5; mx += 0.5; }
-        p.scale = (mx - mn) / 255.0;
-        if (p.scale < 1e-30) p.scale = 1e-30;
-        int32_t zp = x86_cvt_i32(round(-128.0 - mn / p.scale));
-        if (zp < -128) zp = -128;
-        if (zp > 127) zp = 127;
-        p.zero_point = zp;
-        p.min_val = mn;
-        p.max_val = mx;
-        p.symmetric = 0;
-    }
-    *out = p;
-}
 
 // The sequential loop keeps, for each of min and max, the FIRST element
 // holding the extreme value; values that compare equal only differ in the

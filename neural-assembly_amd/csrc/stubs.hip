@@ -316,10 +316,6 @@ double compute_threshold_for_sparsity(void *, int64_t, double) {
     nh::set_error(NEURAL_ERR_NOT_IMPLEMENTED);
     return std::numeric_limits<double>::quiet_NaN();
 }
-int calibrate_percentile(void *, int64_t, double, int, QuantParams *) {
-    nh::set_error(NEURAL_ERR_NOT_IMPLEMENTED);
-    return -1;
-}
 int neural_get_simd_level(void) {
     return 0;  // no host SIMD dispatch: the arithmetic runs on the GPU
 }

@@ -239,6 +239,7 @@ _SIGS = {
     # quantization
     "calibrate_minmax": (_i, [_vp, _i64, _i, _qp]),
     "quantized_matmul": (_i, [_vp, _vp, _vp, _i64, _i64, _i64, _qp, _qp]),
+    "calibrate_percentile": (_i, [_vp, _i64, _d, _i, _qp]),
     "quantize_tensor": (_i, [_vp, _vp, _i64, _qp]),
     "dequantize_tensor": (_i, [_vp, _vp, _i64, _qp]),
     "quantization_error": (_d, [_vp, _i64, _qp]),

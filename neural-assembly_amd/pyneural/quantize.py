@@ -63,11 +63,16 @@ class Quantizer:
         return getattr(core._lib, name + ("_f32" if self.float32 else ""))
 
     def calibrate(self, data_ptr, n: int) -> QuantParams:
-        if self.percentile > 0.0:
-            raise NeuralException(NeuralError.NOT_IMPLEMENTED, "percentile calibration")
         c_params = QuantParamsC()
-        rc = self._fn("calibrate_minmax")(ctypes.cast(data_ptr, ctypes.c_void_p), ctypes.c_int64(n),
-                                          1 if self.symmetric else 0, ctypes.byref(c_params))
+        if self.percentile > 0.0:
+            if self.float32:
+                raise NeuralException(NeuralError.NOT_IMPLEMENTED, "percentile calibration of float32 data")
+            rc = core._lib.calibrate_percentile(ctypes.cast(data_ptr, ctypes.c_void_p), ctypes.c_int64(n),
+                                                ctypes.c_double(self.percentile), 1 if self.symmetric else 0,
+                                                ctypes.byref(c_params))
+        else:
+            rc = self._fn("calibrate_minmax")(ctypes.cast(data_ptr, ctypes.c_void_p), ctypes.c_int64(n),
+                                              1 if self.symmetric else 0, ctypes.byref(c_params))
         if rc != 0:
             raise RuntimeError("Calibration failed")
         self.params = QuantParams._from_c(c_params)

@@ -937,6 +937,56 @@ void ora_clip_grad_value(void **grads, const int *dtypes, const int64_t *ns, int
     }
 }
 
+/* calibrate_percentile (quantize.c:89-132): a sorted copy by the C
+ * library's qsort with the reference's comparator (equal elements, e.g. -0
+ * and +0, keep the order qsort gives them), sorted[lo] / sorted[hi] with
+ * lo = (int64)(n p), hi = (int64)(n (1 - p)), then the minmax expressions. */
+static int ora_cmp_double_asc(const void *a, const void *b)
+{
+    const double da = *(const double *)a, db = *(const double *)b;
+    return (da > db) - (da < db);
+}
+
+int ora_calibrate_percentile(const double *data, int64_t n, double percentile, int symmetric, OraQuantParams *out)
+{
+    if (!data || n <= 0 || !out) return -1;
+    if (percentile != percentile) return -1; /* the reference reads out of bounds here */
+    if (percentile < 0.0 || percentile > 0.5) percentile = 0.01;
+    double *sorted = (double *)malloc((size_t)n * sizeof(double));
+    if (!sorted) return -1;
+    memcpy(sorted, data, (size_t)n * sizeof(double));
+    qsort(sorted, (size_t)n, sizeof(double), ora_cmp_double_asc);
+    int64_t lo_idx = (int64_t)(n * percentile);
+    int64_t hi_idx = (int64_t)(n * (1.0 - percentile));
+    if (lo_idx < 0) lo_idx = 0;
+    if (hi_idx >= n) hi_idx = n - 1;
+    double cmin = sorted[lo_idx], cmax = sorted[hi_idx];
+    free(sorted);
+    if (symmetric) {
+        double am = fmax(fabs(cmin), fabs(cmax));
+        if (am < 1e-30) am = 1e-30;
+        out->scale = am / 127.0;
+        out->zero_point = 0;
+        out->min_val = -am;
+        out->max_val = am;
+        out->symmetric = 1;
+    } else {
+        if (cmin == cmax) {
+            cmin -= 0.5;
+            cmax += 0.5;
+        }
+        out->scale = (cmax - cmin) / 255.0;
+        if (out->scale < 1e-30) out->scale = 1e-30;
+        out->zero_point = (int32_t)round(-128.0 - cmin / out->scale);
+        if (out->zero_point < -128) out->zero_point = -128;
+        if (out->zero_point > 127) out->zero_point = 127;
+        out->min_val = cmin;
+        out->max_val = cmax;
+        out->symmetric = 0;
+    }
+    return 0;
+}
+
 /* quantized_matmul (quantize.c:191-214): combined_scale = sa * sb;
  * acc = sum_k ((int32)A[i][k] - za) * ((int32)B[k][j] - zb) in int32, the
  * reference's loop order; the adds and multiplies wrap mod 2^32 (the compiled

@@ -149,6 +149,7 @@ void   ora_clip_grad_value(void **grads, const int *dtypes, const int64_t *ns, i
  * Pinned in tests/test_oracle_dropout.py: rand() against a restatement of
  * glibc's TYPE_3 generator, hand-derived thresholds (p = 0.5 rounds half to
  * even), keep rates, the closed forms of out and the backward. */
+int  ora_calibrate_percentile(const double *data, int64_t n, double percentile, int symmetric, OraQuantParams *out);
 int  ora_quantized_matmul(const int8_t *A, const int8_t *B, double *C, int64_t M, int64_t K, int64_t N,
                           const OraQuantParams *pa, const OraQuantParams *pb);
 void ora_srand(unsigned seed);

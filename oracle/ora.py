@@ -221,6 +221,18 @@ def dequantize(q, p, dtype=np.float64):
     return out
 
 
+def calibrate_percentile(x, percentile, symmetric, use_ref=False):
+    """QuantParams from calibrate_percentile (quantize.c:89-132) on float64 x;
+    use_ref: the reference's own quantize.c.  Returns (rc, params)."""
+    x = np.ascontiguousarray(x, dtype=np.float64)
+    p = QuantParams()
+    f = ref().calibrate_percentile if use_ref else lib().ora_calibrate_percentile
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_double, ctypes.c_int, ctypes.POINTER(QuantParams)]
+    rc = f(_p(x), x.size, percentile, 1 if symmetric else 0, ctypes.byref(p))
+    return rc, p
+
+
 def quantized_matmul(a, b, m, k, n, pa, pb, use_ref=False):
     """C [m x n] float64 of int8 a [m x k] and b [k x n] (quantize.c:191-214);
     use_ref: the reference's own quantize.c (oracle/_ref)."""

@@ -112,9 +112,14 @@ def test_out_of_scope_stubs(lib):
     check("neural_lr_step_decay", ct.c_double, [ct.c_double, ct.c_int, ct.c_int, ct.c_double], [0.1, 3, 2, 0.5],
           float("nan"))
     check("tb_get_logdir", ct.c_char_p, [ct.c_int], [0], None)
-    check("calibrate_percentile", ct.c_int, [ct.c_void_p, ct.c_int64, ct.c_double, ct.c_int, ct.c_void_p],
-          [None, 0, 99.9, 0, None], -1)
     check("apply_mask", None, [ct.c_void_p, ct.c_void_p, ct.c_int64], [None, None, 0], None)
+    # real entry points outside the hot path reject bad arguments before touching a device
+    lib.calibrate_percentile.restype = ct.c_int
+    lib.calibrate_percentile.argtypes = [ct.c_void_p, ct.c_int64, ct.c_double, ct.c_int, ct.c_void_p]
+    assert lib.calibrate_percentile(None, 10, 0.01, 0, None) == -1
+    lib.quantized_matmul.restype = ct.c_int
+    lib.quantized_matmul.argtypes = [ct.c_void_p] * 3 + [ct.c_int64] * 3 + [ct.c_void_p] * 2
+    assert lib.quantized_matmul(None, None, None, 1, 1, 1, None, None) == -1
     lib.layernorm_free.argtypes = [ct.c_void_p]
     lib.layernorm_free(None)
     lib.neural_get_simd_name.restype = ct.c_char_p

@@ -234,3 +234,64 @@ def test_quantized_matmul_device_wrap_and_errors(pn, ora):
     assert lib.quantized_matmul(a.ctypes.data, b.ctypes.data, got.ctypes.data, 0, k, n, ctypes.byref(qa),
                                 ctypes.byref(qb)) == -1
     assert lib.quantized_matmul(a.ctypes.data, b.ctypes.data, got.ctypes.data, m, k, n, None, ctypes.byref(qb)) == -1
+
+
+# ---- calibrate_percentile (quantize.c:89-132): radix select on the device -----------
+
+def _qp_bits(p):
+    return (np.float64(p.scale).view(np.uint64), p.zero_point, np.float64(p.min_val).view(np.uint64),
+            np.float64(p.max_val).view(np.uint64), p.symmetric)
+
+
+@pytest.mark.parametrize("sym", [0, 1])
+def test_calibrate_percentile_bit_exact(pn, ora, sym):
+    lib = pn.core._lib
+    rng = np.random.default_rng(23)
+    zeros = np.where(rng.random(3000) < 0.5, -0.0, 0.0)
+    cases = [rng.normal(0, 3, 100_003), rng.integers(-5, 6, 5000).astype(np.float64), np.array([2.5]),
+             np.array([1.0, -1.0]), np.concatenate([zeros, rng.normal(0, 1, 60)]),
+             np.concatenate([-np.abs(rng.normal(0, 1, 40)), zeros, np.abs(rng.normal(0, 1, 40))]),
+             rng.permutation(np.concatenate([zeros, rng.normal(0, 1, 200)])),
+             np.array([np.inf, -np.inf, 1e308, -1e308, 5e-324, -5e-324, 0.0, -0.0] * 50),
+             rng.laplace(0, 1, 1 << 20)]
+    for x in cases:
+        for p in [0.01, 0.05, 0.25, 0.5, 0.0, -1.0, 0.7, 1e-9]:
+            got = pn.core.QuantParamsC()
+            assert lib.calibrate_percentile(x.ctypes.data, x.size, ctypes.c_double(p), sym, ctypes.byref(got)) == 0
+            rc, want = ora.calibrate_percentile(x, p, sym)
+            assert rc == 0
+            assert _qp_bits(got) == _qp_bits(want), (x.size, p, got.min_val, want.min_val)
+
+
+def test_calibrate_percentile_device_python_and_errors(pn, ora):
+    import torch
+    lib = pn.core._lib
+    rng = np.random.default_rng(29)
+    x = rng.normal(0, 1, (1 << 24) + 17)
+    x[::1000] = 0.0
+    x[5::1000] = -0.0
+    xd = torch.from_numpy(x).cuda()
+    torch.cuda.synchronize()
+    for p in [0.001, 0.3]:
+        got = pn.core.QuantParamsC()
+        assert lib.calibrate_percentile(xd.data_ptr(), x.size, ctypes.c_double(p), 0, ctypes.byref(got)) == 0
+        assert _qp_bits(got) == _qp_bits(ora.calibrate_percentile(x, p, 0)[1])
+    # a selected rank inside a long run of mixed-sign zeros (device pointer)
+    z = np.where(rng.random(1 << 20) < 0.5, -0.0, 0.0)
+    zd = torch.from_numpy(z).cuda()
+    torch.cuda.synchronize()
+    for p in [0.01, 0.2, 0.45]:
+        got = pn.core.QuantParamsC()
+        assert lib.calibrate_percentile(zd.data_ptr(), z.size, ctypes.c_double(p), 0, ctypes.byref(got)) == 0
+        assert _qp_bits(got) == _qp_bits(ora.calibrate_percentile(z, p, 0)[1])
+    # the Python Quantizer (reference quantize.py:76-105)
+    q = pn.Quantizer(symmetric=False, percentile=0.02)
+    params = q.calibrate(x.ctypes.data, x.size)
+    want = ora.calibrate_percentile(x, 0.02, 0)[1]
+    assert (params.scale, params.zero_point, params.min_val, params.max_val) == \
+        (want.scale, want.zero_point, want.min_val, want.max_val)
+    # errors: NULL, n <= 0, NaN percentile (the reference indexes out of bounds there)
+    got = pn.core.QuantParamsC()
+    assert lib.calibrate_percentile(None, 10, ctypes.c_double(0.01), 0, ctypes.byref(got)) == -1
+    assert lib.calibrate_percentile(x.ctypes.data, 0, ctypes.c_double(0.01), 0, ctypes.byref(got)) == -1
+    assert lib.calibrate_percentile(x.ctypes.data, 10, ctypes.c_double(float("nan")), 0, ctypes.byref(got)) == -1

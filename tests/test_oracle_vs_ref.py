@@ -285,3 +285,30 @@ def test_quantized_matmul_wraps_like_reference(ora):
     assert got[0, 0] == float(wrapped) and exact != wrapped
     # errors
     assert ora.quantized_matmul(a, b, 0, k, 3, pa, pb)[0] == -1
+
+
+def _qp_tuple(p):
+    return (np.float64(p.scale).view(np.uint64), p.zero_point, np.float64(p.min_val).view(np.uint64),
+            np.float64(p.max_val).view(np.uint64), p.symmetric)
+
+
+@pytest.mark.parametrize("sym", [0, 1])
+def test_calibrate_percentile_matches_reference(ora, sym):
+    """ora_calibrate_percentile against quantize.c:89-132 compiled unchanged,
+    incl. percentiles outside [0, 0.5], ties and runs of +-0 at the selected ranks."""
+    if ora.ref() is None:
+        pytest.skip("reference C build (oracle/_ref) absent")
+    rng = np.random.default_rng(17)
+    zeros = np.where(rng.random(2000) < 0.5, -0.0, 0.0)
+    cases = [rng.normal(0, 3, 100_003), rng.integers(-5, 6, 5000).astype(np.float64), np.array([2.5]),
+             np.array([1.0, -1.0]), np.concatenate([zeros, rng.normal(0, 1, 50)]),
+             np.concatenate([-np.abs(rng.normal(0, 1, 30)), zeros, np.abs(rng.normal(0, 1, 30))]),
+             # infinite range: zero point from (int32)round(inf/inf), x86 INT32_MIN clamped to -128
+             np.array([np.inf, -np.inf, 1e308, -1e308, 5e-324, -5e-324, 0.0, -0.0] * 50)]
+    for x in cases:
+        for p in [0.01, 0.05, 0.25, 0.5, 0.0, -1.0, 0.7, 1e-9]:
+            rc, got = ora.calibrate_percentile(x, p, sym)
+            rc2, want = ora.calibrate_percentile(x, p, sym, use_ref=True)
+            assert rc == 0 and rc2 == 0
+            assert _qp_tuple(got) == _qp_tuple(want), (x.size, p)
+    assert ora.calibrate_percentile(np.ones(3), float("nan"), sym)[0] == -1
