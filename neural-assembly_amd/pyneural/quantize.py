@@ -43,12 +43,13 @@ class QuantParams:
 
 
 class Quantizer:
-    """INT8 quantizer with min/max calibration.
+    """INT8 quantizer with min/max or percentile calibration (quantize.py:60-105).
 
     Args:
         symmetric: symmetric (zero_point 0) or affine quantization.
-        percentile: percentile clipping is not provided by this library
-            (NOT_IMPLEMENTED when > 0).
+        percentile: when > 0, calibrate on the [p, 1 - p] order statistics
+            (calibrate_percentile, float64 data only; NOT_IMPLEMENTED with
+            float32=True).
         float32: inputs are float32 arrays (the library's *_f32 entry points)
             instead of the reference's float64.
     """

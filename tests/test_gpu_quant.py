@@ -295,3 +295,23 @@ def test_calibrate_percentile_device_python_and_errors(pn, ora):
     assert lib.calibrate_percentile(None, 10, ctypes.c_double(0.01), 0, ctypes.byref(got)) == -1
     assert lib.calibrate_percentile(x.ctypes.data, 0, ctypes.c_double(0.01), 0, ctypes.byref(got)) == -1
     assert lib.calibrate_percentile(x.ctypes.data, 10, ctypes.c_double(float("nan")), 0, ctypes.byref(got)) == -1
+
+
+def test_calibrate_percentile_ordered_and_duplicate_inputs(pn, ora):
+    """Inputs whose matches come in long runs (sorted, reversed) or never
+    thin out (few distinct values), where copying the matching keys out of the
+    data overflows a block's region or never starts."""
+    import torch
+    lib = pn.core._lib
+    rng = np.random.default_rng(31)
+    base = rng.normal(0, 1, (1 << 23) + 3)
+    cases = [np.sort(base), np.sort(base)[::-1].copy(), rng.integers(0, 3, 1 << 22).astype(np.float64),
+             np.full(70_001, -1.5), np.concatenate([np.sort(base[: 1 << 20]), rng.normal(0, 1, 1 << 20)])]
+    for x in cases:
+        xd = torch.from_numpy(x).cuda()
+        torch.cuda.synchronize()
+        for p in [0.01, 0.1, 0.5]:
+            for sym in (0, 1):
+                got = pn.core.QuantParamsC()
+                assert lib.calibrate_percentile(xd.data_ptr(), x.size, ctypes.c_double(p), sym, ctypes.byref(got)) == 0
+                assert _qp_bits(got) == _qp_bits(ora.calibrate_percentile(x, p, sym)[1]), (x.size, p, sym)
