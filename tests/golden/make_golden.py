@@ -26,6 +26,8 @@ import ora  # noqa: E402
 
 ACTS = ["tanh", "gelu", "leaky_relu", "elu", "selu", "swish", "mish", "hardswish", "softplus", "hardtanh"]
 ALPHA = {"leaky_relu": 0.01, "elu": 1.0}
+PCTS = (0.01, 0.3, 0.45)
+QMM_PARAMS = ((0.02, -3), (0.5, 5))  # (scale, zero_point) of A and B, affine
 
 
 class TensorC(ctypes.Structure):
@@ -93,6 +95,30 @@ def main():
         out[f"quant_{tag}_params"] = np.array([p.scale, p.zero_point, p.min_val, p.max_val, p.symmetric])
         out[f"quant_{tag}_q"] = q
         out[f"quant_{tag}_dq"] = d
+    # percentile calibration (quantize.c:89-132): sorted, 500 negatives, 300
+    # mixed-sign zeros, 1200 positives with integer ties; at p = 0.3 the low
+    # rank (600) falls inside the zeros, so min_val carries the sign of the
+    # zero that input order puts there (a -0 with this seed)
+    rng = np.random.default_rng(106)
+    xp = rng.permutation(np.concatenate([-np.abs(rng.normal(0, 2, 500)), np.where(rng.random(300) < 0.5, -0.0, 0.0),
+                                         np.abs(rng.normal(0, 2, 1100)), rng.integers(1, 4, 100).astype(np.float64)]))
+    out["pct_x"] = xp
+    rows = []
+    for pc in PCTS:
+        for sym in (1, 0):
+            rc, p = ora.calibrate_percentile(xp, pc, sym, use_ref=True)
+            assert rc == 0
+            rows.append([p.scale, p.zero_point, p.min_val, p.max_val, p.symmetric])
+    out["pct_params"] = np.array(rows)
+    # int8 product (quantize.c:191-214), affine zero points on both sides
+    qa = rng.integers(-128, 128, (7, 37)).astype(np.int8)
+    qb = rng.integers(-128, 128, (37, 5)).astype(np.int8)
+    out["qmm_a"], out["qmm_b"] = qa, qb
+    pa, pb = ora.QuantParams(), ora.QuantParams()
+    (pa.scale, pa.zero_point), (pb.scale, pb.zero_point) = QMM_PARAMS
+    rc, cq = ora.quantized_matmul(qa, qb, 7, 37, 5, pa, pb, use_ref=True)
+    assert rc == 0
+    out["qmm_c"] = cq
     # optimizers (optimizers_c.c): three steps
     for dt, tag in ((np.float32, "f32"), (np.float64, "f64")):
         rng = np.random.default_rng(102)

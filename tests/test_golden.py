@@ -26,6 +26,29 @@ def _params(ora, arr):
     return p
 
 
+PCTS = (0.01, 0.3, 0.45)                 # as in make_golden.py
+QMM_PARAMS = ((0.02, -3), (0.5, 5))
+
+
+def _pct_rows(calib):
+    """[scale, zero_point, min_val, max_val, symmetric] rows in fixture order;
+    calib(percentile, symmetric) -> (rc, params)."""
+    rows = []
+    for pc in PCTS:
+        for sym in (1, 0):
+            rc, p = calib(pc, sym)
+            assert rc == 0
+            rows.append([p.scale, p.zero_point, p.min_val, p.max_val, p.symmetric])
+    return np.array(rows)
+
+
+def _qmm_params(cls):
+    pa, pb = cls(), cls()
+    (pa.scale, pa.zero_point), (pb.scale, pb.zero_point) = QMM_PARAMS
+    pa.symmetric = pb.symmetric = 0
+    return pa, pb
+
+
 # ---- CPU: oracle vs fixtures ------------------------------------------------------------
 
 @pytest.mark.parametrize("tag", ["f32", "f64"])
@@ -56,6 +79,11 @@ def test_oracle_quant_opt_misc(ora):
             same_bits(p, G[f"opt_{kind}_{tag}_p"])
             blob = G[f"opt_{kind}_{tag}_blob"].tobytes()
             same_bits(np.frombuffer(blob[88:88 + 8 * p.size], dtype=np.float64), m)
+    same_bits(_pct_rows(lambda pc, sym: ora.calibrate_percentile(G["pct_x"], pc, sym)), G["pct_params"])
+    pa, pb = _qmm_params(ora.QuantParams)
+    rc, c = ora.quantized_matmul(G["qmm_a"], G["qmm_b"], 7, 37, 5, pa, pb)
+    assert rc == 0
+    same_bits(c, G["qmm_c"])
     same_bits(ora.softmax_rows(G["logsoftmax_x"], log=True), G["logsoftmax_y"])
     a, b = G["ew_a"], G["ew_b"]
     for name, code in (("add", ora.ADD), ("sub", ora.SUB), ("mul", ora.MUL), ("div", ora.DIV), ("max", ora.MAX)):
@@ -104,6 +132,17 @@ def test_gpu_quant_opt_golden(pn):
         d = np.empty(xq.size)
         assert lib.dequantize_tensor(q.ctypes.data, d.ctypes.data, q.size, ctypes.byref(p)) == 0
         same_bits(d, G[f"quant_{tag}_dq"])
+    x = G["pct_x"]
+
+    def calib(pc, sym):
+        p = pn.core.QuantParamsC()
+        return lib.calibrate_percentile(x.ctypes.data, x.size, ctypes.c_double(pc), sym, ctypes.byref(p)), p
+    same_bits(_pct_rows(calib), G["pct_params"])
+    pa, pb = _qmm_params(pn.core.QuantParamsC)
+    c = np.empty((7, 5))
+    assert lib.quantized_matmul(G["qmm_a"].ctypes.data, G["qmm_b"].ctypes.data, c.ctypes.data, 7, 37, 5,
+                                ctypes.byref(pa), ctypes.byref(pb)) == 0
+    same_bits(c, G["qmm_c"])
     for tag in ("f32", "f64"):
         for kind, opt in (("sgd", pn.SGD(1e-2, 0.9)), ("adam", pn.Adam(1e-3, 0.9, 0.999, 1e-8)),
                           ("adamw", pn.AdamW(1e-3, 0.9, 0.999, 1e-8, 0.01))):
