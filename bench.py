@@ -306,7 +306,7 @@ def suite(torch, pn, stream):
     dev = torch.device("cuda:0")
     out = []
 
-    def timeit(name, fn, nbytes, reps=10, flops=None, elems=None):
+    def timeit(name, fn, nbytes, reps=10, flops=None, elems=None, int8_ops=None):
         for _ in range(3):
             fn()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -325,6 +325,8 @@ def suite(torch, pn, stream):
             r["x_rocm_copy"] = round(nbytes / us / 1e3 / copy_peak[0], 3)
         if flops:
             r["fp64_TFLOPs"] = round(flops / us / 1e6, 2)
+        if int8_ops:
+            r["int8_TOPS"] = round(int8_ops / us / 1e6, 1)
         out.append(r)
         print(json.dumps(r), file=sys.stderr, flush=True)
 
@@ -458,6 +460,20 @@ def suite(torch, pn, stream):
            lambda: _lib.calibrate_percentile(pc_in.data_ptr(), npc, ctypes.c_double(0.01), 0, ctypes.byref(qp)),
            8 * npc, reps=5, elems=npc)
     del pc_in
+    # int8 product C[M,N] f64 = dequant(A) dequant(B) on the matrix cores; bytes:
+    # A + B read once, C written once (the algorithmic minimum)
+    mq = kq = nq2 = 4096
+    qa = torch.randint(-128, 128, (mq, kq), dtype=torch.int8, device=dev)
+    qb = torch.randint(-128, 128, (kq, nq2), dtype=torch.int8, device=dev)
+    qc = torch.empty(mq, nq2, dtype=torch.float64, device=dev)
+    qpa, qpb = pn.core.QuantParamsC(), pn.core.QuantParamsC()
+    qpa.scale, qpa.zero_point, qpb.scale, qpb.zero_point = 0.02, -3, 0.5, 5
+    torch.cuda.synchronize()
+    timeit("quantized_matmul int8 4096^3 -> f64 (device pointers)",
+           lambda: _lib.quantized_matmul(qa.data_ptr(), qb.data_ptr(), qc.data_ptr(), mq, kq, nq2, ctypes.byref(qpa),
+                                         ctypes.byref(qpb)), mq * kq + kq * nq2 + 8 * mq * nq2, reps=5,
+           int8_ops=2 * mq * kq * nq2)
+    del qa, qb, qc
     # cfg5 AdamW + scan
     na = 100_000_000
     p = torch.randn(na, device=dev) * 0.02

@@ -7,7 +7,8 @@
 //
 // The piecewise-linear ones (leaky_relu, hardswish, hardtanh) and the exp-based
 // ones (elu, selu, swish, sigmoid) evaluate the reference expression as
-// written.  tanh, gelu, mish and softplus are evaluated by closed forms built
+// written (f32 tensors: in float where the reference's double rounding is
+// invisible at 1e-5, see the *F32 functors).  tanh, gelu, mish and softplus are evaluated by closed forms built
 // on one double exp, which costs a fifth to a third of the device library's
 // double tanh / log on gfx950 (measured ~141 and ~70 FP64 instructions per
 // element for tanh and log, ~18 for exp), while keeping the two roundings of
@@ -251,6 +252,32 @@ struct SwishF32 {
     NH_DEV float tail(float x) const { return float(double(x) / (1.0 + exp(-double(x)))); }
 };
 
+// elu / selu, f32: x > 0 is the reference's double product; below, the
+// reference's alpha * (exp(x) - 1.0) with the float expm1.  The reference's
+// double exp(x) - 1.0 carries an absolute error of ~1.1e-16, below 1e-8
+// relative for |x| >= 2^-26, so there the float result matches it to ~2 float
+// ulps; smaller |x| (and zeros) keep the double formula.
+struct EluF32 {
+    double alpha;
+    static constexpr bool kHeadTail = true;
+    NH_DEV float head(float x, bool &need) const
+    {
+        need = x <= 0.0f && x > -0x1p-26f;
+        return x > 0.0f ? x : float(alpha * double(expm1f(x)));
+    }
+    NH_DEV float tail(float x) const { return float(alpha * (exp(double(x)) - 1.0)); }
+};
+
+struct SeluF32 {
+    static constexpr bool kHeadTail = true;
+    NH_DEV float head(float x, bool &need) const
+    {
+        need = x <= 0.0f && x > -0x1p-26f;
+        return x > 0.0f ? float(kSeluL * double(x)) : float(kSeluL * kSeluA * double(expm1f(x)));
+    }
+    NH_DEV float tail(float x) const { return float(kSeluL * kSeluA * (exp(double(x)) - 1.0)); }
+};
+
 // ---- functors ----------------------------------------------------------------------
 
 // Reference formula (or its closed form) in double; f32 tensors round once.
@@ -314,6 +341,11 @@ static int act_swish_impl(void *out, const void *in) { return act2<ASwish>(out, 
 static int act_mish_impl(void *out, const void *in) { return act2<AMish>(out, in, HeadTailFn<MishF32>{}); }
 static int act_softplus_impl(void *out, const void *in) { return act2<ASoftplus>(out, in, HeadTailFn<SoftplusF32>{}); }
 static int act_tanh_impl(void *out, const void *in) { return act2<ATanh>(out, in, TanhF32Fn{}); }
+static int act_elu_impl(void *out, const void *in, double alpha)
+{
+    return act2<AElu>(out, in, HeadTailFn<EluF32>{EluF32{alpha}}, AElu{alpha});
+}
+static int act_selu_impl(void *out, const void *in) { return act2<ASelu>(out, in, HeadTailFn<SeluF32>{}); }
 
 // Bias add then activation, one pass: y = act(x + b) with x + b rounded in
 // the tensor's dtype first (nn_layers.asm:472-539 then activations_c.c), so
@@ -353,8 +385,8 @@ static int bias_add_act(NeuralTensor *out, const NeuralTensor *x, const NeuralTe
     case NEURAL_ACT_LEAKY_RELU:
         return binary_api(out, x, bias, add_act(ActFn<ALeaky>{ALeaky{alpha}}, ActFn<ALeaky>{ALeaky{alpha}}));
     case NEURAL_ACT_ELU:
-        return binary_api(out, x, bias, add_act(ActFn<AElu>{AElu{alpha}}, ActFn<AElu>{AElu{alpha}}));
-    case NEURAL_ACT_SELU: return binary_api(out, x, bias, add_act(ActFn<ASelu>{}, ActFn<ASelu>{}));
+        return binary_api(out, x, bias, add_act(HeadTailFn<EluF32>{EluF32{alpha}}, ActFn<AElu>{AElu{alpha}}));
+    case NEURAL_ACT_SELU: return binary_api(out, x, bias, add_act(HeadTailFn<SeluF32>{}, ActFn<ASelu>{}));
     case NEURAL_ACT_SWISH: return binary_api(out, x, bias, add_act(HeadTailFn<SwishF32>{}, ActFn<ASwish>{}));
     case NEURAL_ACT_MISH: return binary_api(out, x, bias, add_act(HeadTailFn<MishF32>{}, ActFn<AMish>{}));
     case NEURAL_ACT_HARDSWISH: return binary_api(out, x, bias, add_act(ActFn<AHardswish>{}, ActFn<AHardswish>{}));
@@ -374,8 +406,8 @@ extern "C" {
 int act_tanh(void *out, const void *in) { return act_tanh_impl(out, in); }
 int act_gelu(void *out, const void *in) { return act_gelu_impl(out, in); }
 int act_leaky_relu(void *out, const void *in, double alpha) { return act<ALeaky>(out, in, ALeaky{alpha}); }
-int act_elu(void *out, const void *in, double alpha) { return act<AElu>(out, in, AElu{alpha}); }
-int act_selu(void *out, const void *in) { return act<ASelu>(out, in); }
+int act_elu(void *out, const void *in, double alpha) { return act_elu_impl(out, in, alpha); }
+int act_selu(void *out, const void *in) { return act_selu_impl(out, in); }
 int act_swish(void *out, const void *in) { return act_swish_impl(out, in); }
 int act_mish(void *out, const void *in) { return act_mish_impl(out, in); }
 int act_hardswish(void *out, const void *in) { return act<AHardswish>(out, in); }
@@ -388,8 +420,8 @@ int neural_sigmoid(NeuralTensor *out, const NeuralTensor *in) { return act<ASigm
 int neural_tanh(NeuralTensor *out, const NeuralTensor *in) { return act_tanh_impl(out, in); }
 int neural_gelu(NeuralTensor *out, const NeuralTensor *in) { return act_gelu_impl(out, in); }
 int neural_leaky_relu(NeuralTensor *out, const NeuralTensor *in, double alpha) { return act<ALeaky>(out, in, ALeaky{alpha}); }
-int neural_elu(NeuralTensor *out, const NeuralTensor *in, double alpha) { return act<AElu>(out, in, AElu{alpha}); }
-int neural_selu(NeuralTensor *out, const NeuralTensor *in) { return act<ASelu>(out, in); }
+int neural_elu(NeuralTensor *out, const NeuralTensor *in, double alpha) { return act_elu_impl(out, in, alpha); }
+int neural_selu(NeuralTensor *out, const NeuralTensor *in) { return act_selu_impl(out, in); }
 int neural_swish(NeuralTensor *out, const NeuralTensor *in) { return act_swish_impl(out, in); }
 int neural_mish(NeuralTensor *out, const NeuralTensor *in) { return act_mish_impl(out, in); }
 int neural_hardswish(NeuralTensor *out, const NeuralTensor *in) { return act<AHardswish>(out, in); }

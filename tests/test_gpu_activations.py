@@ -99,3 +99,37 @@ def test_activation_dense_sweep(pn, ora, name, dt):
         rel_close(got, want, 1e-12, 1e-15, name)
     z = (want == 0) & ~np.isnan(want)
     assert np.array_equal(np.signbit(got[z]), np.signbit(want[z])), f"{name}: sign of zero differs"
+
+
+@pytest.mark.parametrize("name,alpha", [("elu", 1.0), ("elu", 0.5), ("elu", 2.5), ("selu", 0.0)])
+def test_elu_selu_f32_small_negative(pn, ora, name, alpha):
+    """f32 elu / selu take the float expm1 below -2^-26 and the reference's
+    double exp(x) - 1.0 above it: a log sweep of negative inputs down to 1e-12
+    (where the reference's own cancellation sets the low digits), the points
+    around the switch, and the fused bias-add form of the same functors."""
+    import ctypes
+    t26 = 2.0 ** -26
+    x = np.concatenate([-np.logspace(-12, 1, 200_001), np.logspace(-12, 1, 2001),
+                        [-t26, -t26 * (1 + 2 ** -23), -t26 * (1 - 2 ** -24), -1.1 * t26, -0.9 * t26,
+                         0.0, -0.0, -88.0, -104.0, -np.inf, np.nan]]).astype(np.float32)
+    t = pn.Tensor.from_numpy(x)
+    out = pn.Tensor.create(t.shape, t.dtype)
+    lib = pn.core._lib
+    if name == "elu":
+        assert lib.act_elu(out._ptr, t._ptr, ctypes.c_double(alpha)) == 0
+    else:
+        assert lib.act_selu(out._ptr, t._ptr) == 0
+    got = out.numpy()
+    want = ora.act(name, x, alpha)
+    rel_close(got, want, 1e-5, 0.0, name)
+    z = (want == 0) & ~np.isnan(want)
+    assert np.array_equal(np.signbit(got[z]), np.signbit(want[z]))
+    # bias add + activation: x + 0 rounds to x, so the result is the same
+    x2 = x[: 4096 * 48].reshape(48, 4096) if x.size >= 4096 * 48 else None
+    if x2 is not None:
+        b = np.zeros(4096, dtype=np.float32)
+        tx, tb = pn.Tensor.from_numpy(np.ascontiguousarray(x2)), pn.Tensor.from_numpy(b)
+        o2 = pn.Tensor.create(tx.shape, tx.dtype)
+        code = 6 if name == "elu" else 7  # NEURAL_ACT_ELU / NEURAL_ACT_SELU (neural_api.h)
+        assert lib.neural_bias_add_act(o2._ptr, tx._ptr, tb._ptr, code, ctypes.c_double(alpha)) == 0
+        rel_close(o2.numpy(), want[: x2.size].reshape(x2.shape), 1e-5, 0.0, name + " fused")
