@@ -412,8 +412,11 @@ def suite(torch, pn, stream):
            lambda: _lib.label_smoothing_ce_forward(S64.data_ptr(), tgt.data_ptr(), 65536, 1024, 0.1,
                                                    ctypes.byref(lossv)), 8 * S.numel(), elems=S.numel())
     del S, tS, S64, G64
-    # cfg3 activations
+    # cfg3 activations: normal(0,4) with 1% of the values set to +-30 (saturation)
     x4 = torch.randn(64, 64, 128, 128, device=dev) * 4
+    sat = torch.randperm(x4.numel(), device=dev)[: x4.numel() // 100]
+    x4.view(-1)[sat] = 30.0 * (torch.randint(0, 2, (sat.numel(),), device=dev).float() * 2 - 1)
+    del sat
     y4 = torch.empty_like(x4)
     tx4, ty4 = W(x4), W(y4)
     ne = x4.numel()
