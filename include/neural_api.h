@@ -524,6 +524,13 @@ int upsample2d_nearest_forward(void *, int64_t, int64_t, int64_t, int64_t, int64
  * own stream, a blocking one: it orders implicitly with the legacy null stream
  * (torch's default stream), so kernels on it follow earlier null-stream work
  * and later null-stream work waits for them. */
+/* NEW (no reference counterpart; for measurement): attach two hipEvent_t to
+ * the next softmax / log-softmax kernel launch, made with
+ * hipExtLaunchKernelGGL so that hipEventElapsedTime(start, stop) is that
+ * kernel's own execution time, without the latency of separate event
+ * records around the call.  The events are used once and then cleared.
+ * Returns NEURAL_ERR_NULL_POINTER for a null event. */
+int   neural_hip_time_next_softmax(void *start_event, void *stop_event);
 int   neural_hip_set_stream(void *hip_stream);
 int   neural_hip_reset_stream(void);
 void *neural_hip_get_stream(void);

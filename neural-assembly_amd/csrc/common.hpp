@@ -69,6 +69,12 @@ namespace nh {
 // ---------------------------------------------------------------------------
 int          ensure_init();              // NEURAL_OK or error code (lazy init)
 hipStream_t  stream();                   // active stream
+// Events attached to the next softmax / log-softmax kernel launch
+// (neural_hip_time_next_softmax); take_softmax_timer() hands them out once.
+struct LaunchTimer {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+LaunchTimer  take_softmax_timer();
 int          num_cus();
 int          set_error(int code);        // stores thread-local last error, returns code
 int          hip_fail(hipError_t e);     // maps a HIP error to NEURAL_ERR_* and records it

@@ -358,6 +358,15 @@ static void *host_map(NeuralTensor *t)
     return t->data;
 }
 
+LaunchTimer g_softmax_timer;
+
+LaunchTimer take_softmax_timer()
+{
+    const LaunchTimer t = g_softmax_timer;
+    g_softmax_timer = LaunchTimer{};
+    return t;
+}
+
 }  // namespace nh
 
 using namespace nh;
@@ -809,6 +818,15 @@ int neural_hip_reset_stream(void)
         NH_HIP(hipStreamSynchronize(r.active));
         r.active = r.own;
     }
+    return set_error(NEURAL_OK);
+}
+
+int neural_hip_time_next_softmax(void *start_event, void *stop_event)
+{
+    NH_TRY(ensure_init());
+    if (!start_event || !stop_event) return set_error(NEURAL_ERR_NULL_POINTER);
+    g_softmax_timer.start = static_cast<hipEvent_t>(start_event);
+    g_softmax_timer.stop = static_cast<hipEvent_t>(stop_event);
     return set_error(NEURAL_OK);
 }
 

@@ -21,6 +21,8 @@
 // resident: one wave per row, a single HBM read and a single write.
 #include <cmath>
 
+#include <hip/hip_ext.h>
+
 #include "common.hpp"
 
 namespace nh {
@@ -224,20 +226,30 @@ __global__ __launch_bounds__(kSmBlock) void k_softmax_block(const T *__restrict_
     }
 }
 
+// With timing events pending (neural_hip_time_next_softmax) the launch
+// carries them (hipExtLaunchKernelGGL), so their elapsed time is this kernel's
+// execution; otherwise a plain launch.
+template <typename K, typename... Args>
+static void launch_timed(K kernel, unsigned g, Args... args)
+{
+    const LaunchTimer t = take_softmax_timer();
+    if (t.start)
+        hipExtLaunchKernelGGL(kernel, dim3(g), dim3(kSmBlock), 0, stream(), t.start, t.stop, 0, args...);
+    else
+        hipLaunchKernelGGL(kernel, dim3(g), dim3(kSmBlock), 0, stream(), args...);
+}
+
 template <typename T, bool LOG, int VPL>
 static void launch_wave(const T *x, T *y, int64_t rows, int64_t cols, unsigned g)
 {
     if constexpr (sizeof(T) == 4) {
-        if (cols == int64_t(VPL) * 256) {
-            // (two rows per wave measured slower on MI355X: 89.7 vs 86.2 us at [65536,1024])
-            hipLaunchKernelGGL((k_softmax_wave_f32<LOG, VPL, true, 1>), dim3(g), dim3(kSmBlock), 0, stream(), x, y,
-                               rows, cols);
-        } else {
-            hipLaunchKernelGGL((k_softmax_wave_f32<LOG, VPL, false, 1>), dim3(g), dim3(kSmBlock), 0, stream(), x, y,
-                               rows, cols);
-        }
+        // (two rows per wave measured slower on MI355X: 89.7 vs 86.2 us at [65536,1024])
+        if (cols == int64_t(VPL) * 256)
+            launch_timed(k_softmax_wave_f32<LOG, VPL, true, 1>, g, x, y, rows, cols);
+        else
+            launch_timed(k_softmax_wave_f32<LOG, VPL, false, 1>, g, x, y, rows, cols);
     } else {
-        hipLaunchKernelGGL((k_softmax_wave_f64<LOG, VPL>), dim3(g), dim3(kSmBlock), 0, stream(), x, y, rows, cols);
+        launch_timed(k_softmax_wave_f64<LOG, VPL>, g, x, y, rows, cols);
     }
 }
 
