@@ -72,3 +72,42 @@ def test_softmax_errors(pn):
     assert pn.core._lib.neural_softmax(b._ptr, a._ptr) == pn.NeuralError.DTYPE_MISMATCH
     c = pn.Tensor.create([5, 8])
     assert pn.core._lib.neural_softmax(c._ptr, a._ptr) == pn.NeuralError.SHAPE_MISMATCH
+
+
+def test_softmax_timed_launch(pn):
+    """neural_hip_time_next_softmax: the events ride on the next softmax launch
+    (elapsed time > 0, output unchanged), are used once, and a null event is
+    rejected."""
+    import ctypes
+    from pathlib import Path
+    import torch
+    hip = ctypes.CDLL(str(Path(torch.__file__).parent / "lib" / "libamdhip64.so"))
+    hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+    hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+    lib = pn.core._lib
+    rng = np.random.default_rng(41)
+    x = rng.normal(0, 3, (512, 1024)).astype(np.float32)
+    tx = pn.Tensor.from_numpy(x)
+    y_plain = pn.Tensor.create(tx.shape, tx.dtype)
+    assert lib.neural_softmax(y_plain._ptr, tx._ptr) == 0
+    s = torch.cuda.current_stream()
+    lib.neural_hip_set_stream(ctypes.c_void_p(s.cuda_stream))
+    try:
+        e0, e1 = ctypes.c_void_p(), ctypes.c_void_p()
+        assert hip.hipEventCreate(ctypes.byref(e0)) == 0 and hip.hipEventCreate(ctypes.byref(e1)) == 0
+        assert lib.neural_hip_time_next_softmax(e0, e1) == 0
+        y = pn.Tensor.create(tx.shape, tx.dtype)
+        assert lib.neural_softmax(y._ptr, tx._ptr) == 0
+        torch.cuda.synchronize()
+        ms = ctypes.c_float()
+        assert hip.hipEventElapsedTime(ctypes.byref(ms), e0, e1) == 0
+        assert ms.value > 0.0
+        assert np.array_equal(y.numpy(), y_plain.numpy())
+        assert lib.neural_softmax(y._ptr, tx._ptr) == 0  # no events pending: a plain launch
+        assert np.array_equal(y.numpy(), y_plain.numpy())
+        assert lib.neural_hip_time_next_softmax(None, e1) == pn.NeuralError.NULL_POINTER
+        hip.hipEventDestroy(e0)
+        hip.hipEventDestroy(e1)
+    finally:
+        lib.neural_hip_reset_stream()
