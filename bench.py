@@ -115,7 +115,7 @@ def main():
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "the path would shard by rows / element ranges with one scalar all-reduce per global "
-              "reduction -- see DESIGN.md", file=sys.stderr)
+              "reduction", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
@@ -389,7 +389,7 @@ def suite(torch, pn, stream):
     tS, tP = W(S), W(P)
     timeit("softmax f32 [65536,1024]", lambda: _lib.neural_softmax(tP._ptr, tS._ptr), 8 * S.numel(), elems=S.numel())
     timeit("log_softmax f32 [65536,1024]", lambda: _lib.neural_log_softmax(tP._ptr, tS._ptr), 8 * S.numel(), elems=S.numel())
-    # cross-entropy on the same [65536,1024] logits:
+    # cross-entropy on the same [65536,1024] logits (the label-smoothed and tensor CE entry points):
     # label-smoothed forward + backward in one pass (f32 and f64 logits, int64
     # targets), and the tensor cross_entropy_loss (reads the logits once)
     tgt = torch.randint(0, 1024, (65536,), device=dev, dtype=torch.int64)

@@ -9,7 +9,7 @@
  * the Neural-Assembly tree).  Declarations marked NEW have no reference
  * counterpart; they are additive.
  *
- * Memory model (differs from the all-host reference, see INTEGRATION.md):
+ * Memory model (differs from the all-host reference):
  *   - Tensors created by the library keep their data in device memory (HBM).
  *     neural_tensor_data() / neural_buffer_info() return a host pointer and
  *     synchronise device -> host first.  The pointer is valid for host reads
