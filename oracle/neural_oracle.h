@@ -97,6 +97,16 @@ int    ora_quantize_f32(const float *d, int8_t *out, int64_t n, const OraQuantPa
 int    ora_dequantize(const int8_t *q, double *out, int64_t n, const OraQuantParams *p);
 int    ora_dequantize_f32(const int8_t *q, float *out, int64_t n, const OraQuantParams *p);
 double ora_quant_error(const double *d, int64_t n, const OraQuantParams *p);
+/* calibrate_percentile (quantize.c:89-132) and quantized_matmul
+ * (quantize.c:191-214).  Pinned bit-exact against the reference's quantize.c
+ * (oracle/_ref) in tests/test_oracle_vs_ref.py -- runs of mixed-sign zeros at
+ * the selected ranks (glibc's qsort is a stable merge sort), an infinite range,
+ * percentiles outside [0, 0.5], a K = 40,000 product whose int32 sums wrap --
+ * and by the golden fixtures pct_params / qmm_c. */
+int    ora_calibrate_percentile(const double *data, int64_t n, double percentile, int symmetric,
+                                OraQuantParams *out);
+int    ora_quantized_matmul(const int8_t *A, const int8_t *B, double *C, int64_t M, int64_t K, int64_t N,
+                            const OraQuantParams *pa, const OraQuantParams *pb);
 double ora_quant_snr(const double *d, int64_t n, const OraQuantParams *p);
 double ora_quant_error_f32(const float *d, int64_t n, const OraQuantParams *p);
 double ora_quant_snr_f32(const float *d, int64_t n, const OraQuantParams *p);
@@ -149,9 +159,6 @@ void   ora_clip_grad_value(void **grads, const int *dtypes, const int64_t *ns, i
  * Pinned in tests/test_oracle_dropout.py: rand() against a restatement of
  * glibc's TYPE_3 generator, hand-derived thresholds (p = 0.5 rounds half to
  * even), keep rates, the closed forms of out and the backward. */
-int  ora_calibrate_percentile(const double *data, int64_t n, double percentile, int symmetric, OraQuantParams *out);
-int  ora_quantized_matmul(const int8_t *A, const int8_t *B, double *C, int64_t M, int64_t K, int64_t N,
-                          const OraQuantParams *pa, const OraQuantParams *pb);
 void ora_srand(unsigned seed);
 int  ora_dropout_forward(const float *in, float *out, uint8_t *mask, uint64_t n, float p);
 int  ora_dropout_backward(const float *go, float *gi, const uint8_t *mask, uint64_t n, float p);
