@@ -315,3 +315,33 @@ def test_calibrate_percentile_ordered_and_duplicate_inputs(pn, ora):
                 got = pn.core.QuantParamsC()
                 assert lib.calibrate_percentile(xd.data_ptr(), x.size, ctypes.c_double(p), sym, ctypes.byref(got)) == 0
                 assert _qp_bits(got) == _qp_bits(ora.calibrate_percentile(x, p, sym)[1]), (x.size, p, sym)
+
+
+def test_calibrate_percentile_full_size_vs_stable_sort(pn):
+    """64 M doubles (the size the library is measured at): the selected order
+    statistics equal a stable device sort's elements at lo = (int64)(n p) and
+    hi = (int64)(n (1 - p)) bit for bit -- a stable sort keeps equal values
+    (+0 / -0 included) in input order, as the reference's qsort (glibc's
+    merge sort) does -- and the affine parameters follow from them."""
+    import torch
+    lib = pn.core._lib
+    n = 1 << 26
+    g = torch.Generator(device="cuda")
+    g.manual_seed(37)
+    # N(1, 3) with 2% +0 and 2% -0: the zeros fill sorted ranks ~[0.355, 0.395] n,
+    # so p = 0.37 selects a zero (its sign: input order) and a positive value
+    x = torch.randn(n, device="cuda", dtype=torch.float64, generator=g) * 3 + 1
+    x[torch.randperm(n, device="cuda", generator=g)[: n // 50]] = 0.0
+    x[torch.randperm(n, device="cuda", generator=g)[: n // 50]] = -0.0
+    srt = torch.sort(x, stable=True).values
+    torch.cuda.synchronize()
+    assert float(srt[int(n * 0.37)]) == 0.0
+    for p in (0.001, 0.01, 0.3, 0.37):
+        lo, hi = int(n * p), int(n * (1.0 - p))
+        got = pn.core.QuantParamsC()
+        assert lib.calibrate_percentile(x.data_ptr(), n, ctypes.c_double(p), 0, ctypes.byref(got)) == 0
+        want_lo, want_hi = float(srt[lo]), float(srt[hi])
+        assert np.float64(got.min_val).view(np.uint64) == np.float64(want_lo).view(np.uint64), (p, got.min_val, want_lo)
+        assert np.float64(got.max_val).view(np.uint64) == np.float64(want_hi).view(np.uint64), (p, got.max_val, want_hi)
+        scale = (want_hi - want_lo) / 255.0
+        assert got.scale == scale
