@@ -345,3 +345,28 @@ def test_calibrate_percentile_full_size_vs_stable_sort(pn):
         assert np.float64(got.max_val).view(np.uint64) == np.float64(want_hi).view(np.uint64), (p, got.max_val, want_hi)
         scale = (want_hi - want_lo) / 255.0
         assert got.scale == scale
+
+
+def test_quantized_matmul_full_size_vs_exact_f64(pn):
+    """4096^3 (the size the product is measured at): every inner sum
+    sum_k (A - za)(B - zb) is an integer below 2^31 here (|terms| <= 255 * 255,
+    K = 4096: < 2.7e8), so a float64 device product of the shifted operands is
+    exact in any summation order; C must equal that sum * (sa * sb) bit for
+    bit, as quantize.c:191-214 forms it."""
+    import torch
+    lib = pn.core._lib
+    m = k = n = 4096
+    g = torch.Generator(device="cuda")
+    g.manual_seed(43)
+    a = torch.randint(-128, 128, (m, k), dtype=torch.int8, device="cuda", generator=g)
+    b = torch.randint(-128, 128, (k, n), dtype=torch.int8, device="cuda", generator=g)
+    c = torch.empty(m, n, dtype=torch.float64, device="cuda")
+    pa, pb = pn.core.QuantParamsC(), pn.core.QuantParamsC()
+    pa.scale, pa.zero_point, pb.scale, pb.zero_point = 0.013, -7, 0.37, 11
+    torch.cuda.synchronize()
+    assert lib.quantized_matmul(a.data_ptr(), b.data_ptr(), c.data_ptr(), m, k, n, ctypes.byref(pa),
+                                ctypes.byref(pb)) == 0
+    torch.cuda.synchronize()
+    exact = torch.matmul(a.double() - pa.zero_point, (b.double() - pb.zero_point).contiguous())
+    want = exact * (pa.scale * pb.scale)
+    assert torch.equal(c, want)
