@@ -12,13 +12,22 @@
  * so SSE2 arithmetic and no FMA contraction).
  *
  * Pinning (what each function is checked against, in tests/test_oracle_*.py):
- *   - ora_ew_*, ora_scalar_*, ora_neg_*, ora_relu_*, ora_bias_add_*,
- *     ora_has_nan/inf, ora_argmax*: IEEE-754 closed forms (numpy) plus
- *     brute force on tiny inputs and the reference unit-test values
- *     (src/asm/tests.asm:337-405,470-519).
+ *   - ora_ew_*, ora_scalar_*, ora_neg_*, ora_relu_*, ora_bias_add_f32/f64,
+ *     ora_has_nan/inf: IEEE-754 closed forms (numpy) plus the reference
+ *     unit-test values (src/asm/tests.asm:337-405,470-519).
+ *   - ora_max_chain_f32/f64, ora_rowmax_chain_*, ora_argmax_f32/f64,
+ *     ora_rowargmax_*: brute force over every array of length 1-4 drawn
+ *     from {NaN, -0, +0, 1, -1, 2} in float32 AND float64 against the
+ *     maxss/maxsd and comiss/comisd rules, plus closed forms (rightmost
+ *     maximum after the last NaN; first index of the non-NaN maximum).
  *   - ora_sum_ref_*, ora_l2_ref_f32, ora_rowsum_ref_*: a Python lane-by-lane
  *     emulation of the asm order on tiny inputs and the fp64-exact value
  *     (math.fsum) within the rounding bound of the order.
+ *   - ora_calibrate_minmax_f32, ora_quantize_f32, ora_dequantize_f32,
+ *     ora_quant_error_f32, ora_quant_snr_f32: bit-for-bit against the
+ *     reference's quantize.c run on the float32 values widened to double
+ *     (exact), incl. NaN / +-Inf / +-50 / 2^31 overflow (the dequantized
+ *     floats against (float) of the reference's double).
  *   - ora_act_*, ora_quant*, ora_calibrate*, ora_dequant*, ora_adam*,
  *     ora_sgd*, ora_log_softmax_rows_*, ora_concat/split/pad/transpose,
  *     ora_transform_*: bit-for-bit against the reference's own C

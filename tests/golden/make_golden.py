@@ -95,6 +95,33 @@ def main():
         out[f"quant_{tag}_params"] = np.array([p.scale, p.zero_point, p.min_val, p.max_val, p.symmetric])
         out[f"quant_{tag}_q"] = q
         out[f"quant_{tag}_dq"] = d
+    # float32 quantization (calibrate_minmax_f32 / quantize_tensor_f32 /
+    # dequantize_tensor_f32 / quantization_error_f32 / _snr_f32): the
+    # reference's double path run on the float32 values widened to double
+    # (exact); the dequantized fixture is (float) of the reference's double.
+    rng32 = np.random.default_rng(105)
+    xq32 = rng32.laplace(0, 1, 2048).astype(np.float32)
+    xq32[[3, 64]] = [50.0, -50.0]
+    xq32[[8, 13, 21, 34, 55, 89, 144]] = [np.nan, np.inf, -np.inf, 0.0, -0.0, 1e-45, 3.4e38]
+    xq32_clean = xq32.copy()
+    xq32_clean[[8, 13, 21, 144]] = [0.5, -0.5, 1.5, -1.5]
+    out["quant32_x"], out["quant32_x_clean"] = xq32, xq32_clean
+    w, wc = xq32.astype(np.float64), xq32_clean.astype(np.float64)
+    ref.quantization_error.argtypes = [P, ctypes.c_int64, P]
+    ref.quantization_snr.argtypes = [P, ctypes.c_int64, P]
+    for sym in (1, 0):
+        p = ora.QuantParams()
+        assert ref.calibrate_minmax(wc.ctypes.data, wc.size, sym, ctypes.byref(p)) == 0
+        q = np.empty(w.size, dtype=np.int8)
+        assert ref.quantize_tensor(w.ctypes.data, q.ctypes.data, w.size, ctypes.byref(p)) == 0
+        d = np.empty(w.size)
+        assert ref.dequantize_tensor(q.ctypes.data, d.ctypes.data, q.size, ctypes.byref(p)) == 0
+        tag = "sym" if sym else "aff"
+        out[f"quant32_{tag}_params"] = np.array([p.scale, p.zero_point, p.min_val, p.max_val, p.symmetric])
+        out[f"quant32_{tag}_q"] = q
+        out[f"quant32_{tag}_dq"] = d.astype(np.float32)
+        out[f"quant32_{tag}_err_snr"] = np.array([ref.quantization_error(wc.ctypes.data, wc.size, ctypes.byref(p)),
+                                                  ref.quantization_snr(wc.ctypes.data, wc.size, ctypes.byref(p))])
     # percentile calibration (quantize.c:89-132): sorted, 500 negatives, 300
     # mixed-sign zeros, 1200 positives with integer ties; at p = 0.3 the low
     # rank (600) falls inside the zeros, so min_val carries the sign of the

@@ -124,3 +124,113 @@ def test_out_of_scope_stubs(lib):
     lib.layernorm_free(None)
     lib.neural_get_simd_name.restype = ct.c_char_p
     assert b"HIP" in lib.neural_get_simd_name()
+
+
+# ---- signatures of the reference's bindings --------------------------------------------------
+
+def _ref_type(expr):
+    """The ctypes object a reference binding string names (ctypes.c_uint64 and
+    ctypes.c_ulong are one type on LP64, so aliases compare equal)."""
+    import sys
+    sys.path.insert(0, str(ROOT / "neural-assembly_amd"))
+    from pyneural.core import QuantParamsC, NeuralBufferInfo
+    if expr == "None":
+        return None
+    return eval(expr, {"ctypes": ctypes, "QuantParamsC": QuantParamsC, "NeuralBufferInfo": NeuralBufferInfo})
+
+
+def test_python_bindings_match_reference_signatures():
+    """Every entry point this package binds that the reference's pyneural also
+    binds has the reference's restype and argtypes (pyneural/core.py:89-1373,
+    tensor.py:40-59), so the reference's own ctypes declarations call this
+    library with the same argument widths."""
+    import sys
+    sys.path.insert(0, str(ROOT / "neural-assembly_amd"))
+    from pyneural.core import _SIGS
+    ref = _bound()
+    both = [n for n in _SIGS if n in ref]
+    assert len(both) >= 70, len(both)
+    bad = []
+    for n in both:
+        res, args = _SIGS[n]
+        want_res = _ref_type(ref[n]["restype"])
+        want_args = [_ref_type(a) for a in ref[n]["argtypes"]]
+        if res is not want_res or list(args) != want_args:
+            bad.append((n, (res, args), (want_res, want_args)))
+    assert not bad, bad
+
+
+_C_SCALARS = {
+    "int": ctypes.c_int, "int32_t": ctypes.c_int32, "int64_t": ctypes.c_int64, "uint64_t": ctypes.c_uint64,
+    "uint32_t": ctypes.c_uint32, "double": ctypes.c_double, "float": ctypes.c_float, "size_t": ctypes.c_size_t,
+}
+
+
+def _header_decls():
+    """name -> (return type text, [parameter type texts]) for every function
+    include/neural_api.h declares."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    text = re.sub(r"#[^\n]*", "", text)
+    out = {}
+    for m in re.finditer(r"([A-Za-z_][A-Za-z0-9_ \t\*]*?[\s\*])([A-Za-z_][A-Za-z0-9_]*)\s*\(([^;{}()]*)\)\s*;", text):
+        ret, name, params = m.group(1), m.group(2), m.group(3).strip()
+        ret = ret.split(";")[-1].split("}")[-1].strip()
+        plist = [] if params in ("", "void") else [p.strip() for p in params.split(",")]
+        types = []
+        for p in plist:
+            p = re.sub(r"\[\s*\]", "*", p)
+            toks = re.findall(r"[A-Za-z_][A-Za-z0-9_]*|\*", p)
+            # drop the parameter name (last identifier after the type)
+            if len(toks) >= 2 and toks[-1] != "*" and toks[-2] not in ("const",):
+                toks = toks[:-1]
+            types.append(" ".join(toks))
+        out[name] = (ret, types)
+    return out
+
+
+def _c_matches(ctext, want):
+    """A C type from the header is ABI-compatible with a ctypes binding: equal
+    scalar widths; pointers bind as c_void_p, c_char_p (char *) or
+    POINTER(T) where T is the pointee."""
+    toks = [t for t in re.findall(r"[A-Za-z_][A-Za-z0-9_]*|\*", ctext) if t not in ("const", "struct", "unsigned")]
+    npt = toks.count("*")
+    base = [t for t in toks if t != "*"]
+    base = base[0] if base else ""
+    if npt == 0:
+        if base == "void":
+            return want is None
+        return want is _C_SCALARS.get(base, object())
+    if want is ctypes.c_void_p:
+        return True
+    if want is ctypes.c_char_p:
+        return base == "char" and npt == 1
+    if hasattr(want, "_type_") and getattr(want, "__name__", "").startswith("LP_"):
+        inner = want._type_
+        if npt == 2:
+            return inner is ctypes.c_void_p
+        if base == "QuantParams":
+            return inner.__name__ == "QuantParamsC"
+        if base == "NeuralBufferInfo":
+            return inner.__name__ == "NeuralBufferInfo"
+        return inner is _C_SCALARS.get(base, object())
+    return False
+
+
+def test_header_matches_reference_signatures():
+    """Every declaration in include/neural_api.h of a name the reference's
+    pyneural binds is ABI-compatible with that binding: same argument count,
+    same scalar widths, pointers where the reference passes pointers."""
+    decls = _header_decls()
+    ref = _bound()
+    both = [n for n in ref if n in decls]
+    assert len(both) >= 70, len(both)
+    bad = []
+    for n in both:
+        ret, params = decls[n]
+        want_res = _ref_type(ref[n]["restype"])
+        want_args = [_ref_type(a) for a in ref[n]["argtypes"]]
+        ok = _c_matches(ret, want_res) and len(params) == len(want_args) and \
+            all(_c_matches(p, w) for p, w in zip(params, want_args))
+        if not ok:
+            bad.append((n, ret, params, ref[n]["restype"], ref[n]["argtypes"]))
+    assert not bad, bad

@@ -153,6 +153,43 @@ def test_gpu_quant_opt_golden(pn):
             assert opt.state_bytes() == G[f"opt_{kind}_{tag}_blob"].tobytes()
 
 
+def test_oracle_quant_f32_golden(ora):
+    """The oracle's float32 quantization functions reproduce the fixtures the
+    reference's quantize.c made from the widened values."""
+    for tag in ("sym", "aff"):
+        p = ora.calibrate(G["quant32_x_clean"], tag == "sym")
+        assert [p.scale, p.zero_point, p.min_val, p.max_val, p.symmetric] == G[f"quant32_{tag}_params"].tolist()
+        same_bits(ora.quantize(G["quant32_x"], p), G[f"quant32_{tag}_q"])
+        same_bits(ora.dequantize(G[f"quant32_{tag}_q"], p, np.float32), G[f"quant32_{tag}_dq"])
+        want_e, want_s = G[f"quant32_{tag}_err_snr"].tolist()
+        assert ora.quant_error(G["quant32_x_clean"], p) == want_e
+        assert ora.quant_snr(G["quant32_x_clean"], p) == want_s
+
+
+@GPU
+def test_gpu_quant_f32_golden(pn):
+    """The float32 entry points reproduce the fixtures quantize.c made from
+    the widened values: parameters, int8 codes and dequantized floats bit for
+    bit; error and SNR within 1e-12 relative (tree order vs the reference's
+    sequential double sum)."""
+    lib = pn.core._lib
+    for tag in ("sym", "aff"):
+        xc = G["quant32_x_clean"]
+        p = pn.core.QuantParamsC()
+        assert lib.calibrate_minmax_f32(xc.ctypes.data, xc.size, 1 if tag == "sym" else 0, ctypes.byref(p)) == 0
+        assert [p.scale, p.zero_point, p.min_val, p.max_val, p.symmetric] == G[f"quant32_{tag}_params"].tolist()
+        x = G["quant32_x"]
+        q = np.empty(x.size, dtype=np.int8)
+        assert lib.quantize_tensor_f32(x.ctypes.data, q.ctypes.data, x.size, ctypes.byref(p)) == 0
+        same_bits(q, G[f"quant32_{tag}_q"])
+        d = np.empty(x.size, dtype=np.float32)
+        assert lib.dequantize_tensor_f32(q.ctypes.data, d.ctypes.data, q.size, ctypes.byref(p)) == 0
+        same_bits(d, G[f"quant32_{tag}_dq"])
+        want_e, want_s = G[f"quant32_{tag}_err_snr"].tolist()
+        rel_close([lib.quantization_error_f32(xc.ctypes.data, xc.size, ctypes.byref(p))], [want_e], 1e-12, 0.0, "err")
+        rel_close([lib.quantization_snr_f32(xc.ctypes.data, xc.size, ctypes.byref(p))], [want_s], 1e-12, 0.0, "snr")
+
+
 @GPU
 def test_gpu_misc_golden(pn):
     lib = pn.core._lib

@@ -58,11 +58,24 @@ def test_elementwise_closed_forms(ora, rng, dt):
     assert np.signbit(ora.ew(ora.MAX, z, z[::-1].copy())[0])            # max(+0, -0) -> -0 (second operand)
 
 
-def test_bias_add_closed_form(ora, rng):
-    x = rng.normal(0, 3, (33, 77)).astype(np.float32)
-    b = rng.normal(0, 3, 77).astype(np.float32)
-    same_bits(ora.bias_add(x, b), x + b)
-    assert not np.array_equal(ora.bias_add(x, b), x + b[::-1])
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_bias_add_closed_form(ora, rng, dt):
+    """out[i,j] = x[i,j] + b[j] correctly rounded (addss / addsd,
+    nn_layers.asm:472-539): numpy's broadcast add in the same dtype, with
+    NaN, +-Inf, signed zeros and a row/column transposition planted so a
+    swapped index or a dropped row stride fails."""
+    x = rng.normal(0, 3, (33, 77)).astype(dt)
+    b = rng.normal(0, 3, 77).astype(dt)
+    x[0, :4] = [np.nan, np.inf, -0.0, 0.0]
+    b[:4] = [1.0, -np.inf, -0.0, -0.0]
+    got = ora.bias_add(x, b)
+    same_bits(got, x + b)
+    assert np.signbit(got[0, 2]) and not np.signbit(got[0, 3])  # -0 + -0 = -0, +0 + -0 = +0
+    assert np.isnan(got[0, 1])                                   # inf + -inf
+    assert not np.array_equal(got[1:], (x + b[::-1])[1:])
+    sq = rng.normal(size=(40, 40)).astype(dt)
+    bq = rng.normal(size=40).astype(dt)
+    assert not np.array_equal(ora.bias_add(sq, bq), sq + bq[:, None])  # broadcast over rows, not columns
 
 
 def _emulate_sum_f32(x):
@@ -146,7 +159,7 @@ def test_row_and_column_orders(ora, rng):
         assert e[i] == math.fsum(x[i].astype(np.float64)) or abs(e[i] - math.fsum(x[i])) < 1e-15
 
 
-POOL = np.array([np.nan, -0.0, 0.0, 1.0, -1.0, 2.0], dtype=np.float32)
+POOL = [np.nan, -0.0, 0.0, 1.0, -1.0, 2.0]
 
 
 def _chain(xs):
@@ -164,13 +177,18 @@ def _argmax(xs):
     return idx
 
 
-def test_max_argmax_brute_force(ora):
-    """Every array of length 1..4 over a pool with NaN and signed zeros."""
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_max_argmax_brute_force(ora, dt):
+    """Every array of length 1..4 over a pool with NaN and signed zeros, in
+    both dtypes: the f32 chain is activations.asm:888-895 (maxss) and
+    main.asm:3598-3640 (comiss), the f64 chain activations.asm:815-823
+    (maxsd) and the same argmax rule on doubles."""
+    pool = np.array(POOL, dtype=dt)
     for n in range(1, 5):
-        for combo in itertools.product(range(len(POOL)), repeat=n):
-            x = POOL[list(combo)].copy()
-            want = np.float32(_chain(list(x)))
-            got = np.float32(ora.max_chain(x))
+        for combo in itertools.product(range(len(pool)), repeat=n):
+            x = pool[list(combo)].copy()
+            want = dt(_chain(list(x)))
+            got = dt(ora.max_chain(x))
             assert (np.isnan(want) and np.isnan(got)) or got.tobytes() == want.tobytes(), x
             assert ora.argmax(x) == _argmax(list(x)), x
             # closed form used by the GPU reduction: after the last NaN,
@@ -191,12 +209,16 @@ def test_max_argmax_brute_force(ora):
                 assert ora.argmax(x) == -max(vals)[1]
 
 
-def test_rowwise_matches_flat(ora, rng):
-    x = rng.normal(size=(9, 31)).astype(np.float32)
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_rowwise_matches_flat(ora, rng, dt):
+    x = rng.normal(size=(9, 31)).astype(dt)
     x[2, 4] = np.nan
+    x[5, 0] = np.nan
+    x[6, :] = 0.0
+    x[6, 3] = -0.0
     rm, ra = ora.rowmax_chain(x), ora.rowargmax(x)
     for i in range(9):
-        assert np.float32(ora.max_chain(x[i].copy())).tobytes() == rm[i].tobytes()
+        assert dt(ora.max_chain(x[i].copy())).tobytes() == rm[i].tobytes()
         assert ora.argmax(x[i].copy()) == ra[i]
 
 

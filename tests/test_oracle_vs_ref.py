@@ -312,3 +312,97 @@ def test_calibrate_percentile_matches_reference(ora, sym):
             assert rc == 0 and rc2 == 0
             assert _qp_tuple(got) == _qp_tuple(want), (x.size, p)
     assert ora.calibrate_percentile(np.ones(3), float("nan"), sym)[0] == -1
+
+
+def _f32_quant_inputs(rng):
+    """cfg4-shaped float32 data: Laplace(0,1), +-50 outliers (both signs, so
+    min = -50 and max = +50 exactly), signed zeros and float32 denormals."""
+    x = rng.laplace(0, 1, 100003).astype(np.float32)
+    x[rng.choice(x.size, 120, replace=False)] = 50.0
+    x[rng.choice(x.size, 120, replace=False)] = -50.0
+    x[1:7] = [0.0, -0.0, 1e-45, -1e-45, 1.1754944e-38, -3.0e-39]
+    return x
+
+
+def _ref_call_f64(ref, name, *args):
+    f = getattr(ref, name)
+    f.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_int64, ctypes.c_void_p] if name in (
+        "quantize_tensor", "dequantize_tensor") else [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    return f(*args)
+
+
+@pytest.mark.parametrize("sym", [True, False])
+def test_f32_quant_variants_match_reference_on_widened_input(ora, ref, sym):
+    """ora_calibrate_minmax_f32 / ora_quantize_f32 / ora_dequantize_f32 /
+    ora_quant_error_f32 / ora_quant_snr_f32 against the reference's
+    quantize.c:52-84,144-174,222-269 (compiled unchanged) run on the same
+    values widened to double, which is exact: the reference API is
+    double-in, double-out; the f32 entry points read floats and write
+    (float) of the double result."""
+    x32 = _f32_quant_inputs(np.random.default_rng(50 + sym))
+    x64 = x32.astype(np.float64)
+    rp = _ref_params(ref, x64, sym)
+    op = ora.calibrate(x32, sym)
+    assert _params_bytes(op) [:12] == _params_bytes(rp)[:12]
+    assert (op.min_val, op.max_val, op.symmetric) == (rp.min_val, rp.max_val, rp.symmetric)
+    # what the mathematics fixes: +-50 both present
+    if sym:
+        assert op.scale == 50.0 / 127.0 and op.zero_point == 0 and (op.min_val, op.max_val) == (-50.0, 50.0)
+    else:
+        assert op.scale == 100.0 / 255.0 and (op.min_val, op.max_val) == (-50.0, 50.0)
+        v = -128.0 - (-50.0) / op.scale                    # C round(): half away from zero
+        assert op.zero_point == int(np.copysign(np.floor(abs(v) + 0.5), v))
+    q_ref = np.empty(x32.size, dtype=np.int8)
+    assert _ref_call_f64(ref, "quantize_tensor", x64.ctypes.data, q_ref.ctypes.data, x64.size, ctypes.byref(rp)) == 0
+    same_bits(ora.quantize(x32, op), q_ref)
+    d_ref = np.empty(x32.size)
+    assert _ref_call_f64(ref, "dequantize_tensor", q_ref.ctypes.data, d_ref.ctypes.data, x64.size,
+                         ctypes.byref(rp)) == 0
+    same_bits(ora.dequantize(q_ref, op, np.float32), d_ref.astype(np.float32))
+    ref.quantization_error.restype = ctypes.c_double
+    ref.quantization_snr.restype = ctypes.c_double
+    e_ref = _ref_call_f64(ref, "quantization_error", x64.ctypes.data, x64.size, ctypes.byref(rp))
+    s_ref = _ref_call_f64(ref, "quantization_snr", x64.ctypes.data, x64.size, ctypes.byref(rp))
+    assert ora.quant_error(x32, op) == e_ref
+    assert ora.quant_snr(x32, op) == s_ref
+    # the error is bounded by the step: |x - deq(q(x))| <= scale/2 inside the range
+    assert 0.0 < e_ref <= (op.scale / 2) ** 2
+
+
+def test_f32_quant_variants_special_values_match_reference(ora, ref):
+    """NaN, +-Inf, values whose scaled magnitude passes 2^31 (x86 cvttsd2si
+    gives INT32_MIN, then the int32 add wraps), ties at .5, float32 extremes:
+    the f32 variants equal the reference's double path on the widened
+    values, for every zero point and several scales."""
+    x32 = np.array([0.3, np.nan, np.inf, -np.inf, 3.4e38, -3.4e38, 0.0, -0.0, 2.5, -2.5, 3.5, -3.5, 1e9, -1e9,
+                    1e-45, 50.0, -50.0, 127.5, -128.5], dtype=np.float32)
+    x64 = x32.astype(np.float64)
+    for zp in (-128, -1, 0, 1, 127):
+        for scale in (0.5, 1e-3, 7.0, 50.0 / 127.0):
+            p = ora_qp()
+            p.scale, p.zero_point = scale, zp
+            q = np.empty(x32.size, dtype=np.int8)
+            assert _ref_call_f64(ref, "quantize_tensor", x64.ctypes.data, q.ctypes.data, x64.size,
+                                 ctypes.byref(p)) == 0
+            same_bits(ora.quantize(x32, p), q)
+            d = np.empty(x32.size)
+            assert _ref_call_f64(ref, "dequantize_tensor", q.ctypes.data, d.ctypes.data, x64.size,
+                                 ctypes.byref(p)) == 0
+            same_bits(ora.dequantize(q, p, np.float32), d.astype(np.float32))
+            ref.quantization_error.restype = ctypes.c_double
+            ref.quantization_snr.restype = ctypes.c_double
+            for fn, name in ((ora.quant_error, "quantization_error"), (ora.quant_snr, "quantization_snr")):
+                want = _ref_call_f64(ref, name, x64.ctypes.data, x64.size, ctypes.byref(p))
+                got = fn(x32, p)
+                assert (np.isnan(want) and np.isnan(got)) or want == got, (name, zp, scale, got, want)
+            # finite-only inputs give a finite error that both sides agree on
+            fin32 = x32[np.isfinite(x32)].copy()
+            fin64 = fin32.astype(np.float64)
+            want = _ref_call_f64(ref, "quantization_error", fin64.ctypes.data, fin64.size, ctypes.byref(p))
+            assert ora.quant_error(fin32, p) == want
+    # dequantize of every int8 code for an affine map: (float)((q - zp) * scale)
+    qs = np.arange(-128, 128, dtype=np.int8)
+    p = ora_qp()
+    p.scale, p.zero_point = 0.0123, -7
+    want = ((qs.astype(np.float64) + 7.0) * 0.0123).astype(np.float32)
+    same_bits(ora.dequantize(qs, p, np.float32), want)
