@@ -518,6 +518,15 @@ int upsample2d_nearest_backward(void *, int64_t, int64_t, int64_t, int64_t, int6
 int upsample2d_nearest_forward(void *, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, void *);  /* core.py:1256 */
 
 /* ---- HIP runtime controls (NEW) ------------------------------------------------- */
+/* Threads: every entry point may be called from several host threads at
+ * once (the reference is single-threaded; ctypes releases the GIL around
+ * each call).  The last error is per thread.  Calls that use the shared
+ * reduction workspace (whole-tensor and per-row reductions over few rows, the
+ * NaN/Inf/L2 scan, calibration, quantization error, the CE losses, gradient
+ * clipping, simd_sum/dot) hold one process-wide lock from their first launch
+ * until their result has been read back, so they serialise; everything else
+ * only shares the stream.  One tensor must not be written by one thread while
+ * another reads or writes it. */
 /* Use an existing HIP stream (e.g. torch.cuda.current_stream().cuda_stream) for
  * all later launches; NULL selects the HIP null stream.  The previous stream
  * is synchronised first.  neural_hip_reset_stream() returns to the library's
@@ -525,12 +534,17 @@ int upsample2d_nearest_forward(void *, int64_t, int64_t, int64_t, int64_t, int64
  * (torch's default stream), so kernels on it follow earlier null-stream work
  * and later null-stream work waits for them. */
 /* NEW (no reference counterpart; for measurement): attach two hipEvent_t to
- * the next softmax / log-softmax kernel launch, made with
- * hipExtLaunchKernelGGL so that hipEventElapsedTime(start, stop) is that
- * kernel's own execution time, without the latency of separate event
- * records around the call.  The events are used once and then cleared.
- * Returns NEURAL_ERR_NULL_POINTER for a null event. */
-int   neural_hip_time_next_softmax(void *start_event, void *stop_event);
+ * one later kernel launch made by the CALLING thread: the launch after the
+ * next `skip` launches (skip = 0: the next launch; the second kernel of a
+ * two-kernel call is skip = 1).  That launch is made with
+ * hipExtLaunchKernelGGL, so hipEventElapsedTime(start, stop) is that
+ * kernel's own execution time on its stream, without the latency of separate
+ * event records around the call.  The events are used once, then cleared;
+ * neural_hip_time_cancel() clears them unused.  Returns
+ * NEURAL_ERR_NULL_POINTER for a null event, NEURAL_ERR_INVALID_ARGUMENT for
+ * skip < 0. */
+int   neural_hip_time_next_launch(void *start_event, void *stop_event, int skip);
+int   neural_hip_time_cancel(void);
 int   neural_hip_set_stream(void *hip_stream);
 int   neural_hip_reset_stream(void);
 void *neural_hip_get_stream(void);

@@ -400,19 +400,20 @@ int clip_norm_list(NeuralTensor *const *grads, int64_t count, double max_norm, d
     }
     Plan p;
     NH_TRY(make_plan(g, p));
+    WsGuard wg;
     double *part = static_cast<double *>(workspace().partials);
     ClipState *st = static_cast<ClipState *>(workspace().result);
     p.with_tab([&](const auto &tab) {
         using Tab = std::decay_t<decltype(tab)>;
-        hipLaunchKernelGGL(k_clip_sumsq<Tab>, dim3(unsigned(p.blocks_sum)), dim3(kCBlock), 0, stream(), tab,
+        NH_LAUNCH(k_clip_sumsq<Tab>, dim3(unsigned(p.blocks_sum)), dim3(kCBlock), 0, stream(), tab,
                            p.count, p.chunk_sum, part);
     });
     NH_TRY(check_launch());
-    hipLaunchKernelGGL(k_clip_decide, dim3(1), dim3(kRBlock), 0, stream(), part, int(p.blocks_sum), max_norm, st);
+    NH_LAUNCH(k_clip_decide, dim3(1), dim3(kRBlock), 0, stream(), part, int(p.blocks_sum), max_norm, st);
     NH_TRY(check_launch());
     p.with_tab([&](const auto &tab) {
         using Tab = std::decay_t<decltype(tab)>;
-        hipLaunchKernelGGL(k_clip_scale<Tab>, dim3(p.grid_ew), dim3(kCBlock), 0, stream(), tab, p.count, p.chunk_ew,
+        NH_LAUNCH(k_clip_scale<Tab>, dim3(p.grid_ew), dim3(kCBlock), 0, stream(), tab, p.count, p.chunk_ew,
                            p.blocks_ew, st);
     });
     NH_TRY(check_launch());
@@ -435,7 +436,7 @@ int clip_value_list(NeuralTensor *const *grads, int64_t count, double lo, double
     NH_TRY(make_plan(g, p));
     p.with_tab([&](const auto &tab) {
         using Tab = std::decay_t<decltype(tab)>;
-        hipLaunchKernelGGL(k_clip_value<Tab>, dim3(p.grid_ew), dim3(kCBlock), 0, stream(), tab, p.count, p.chunk_ew,
+        NH_LAUNCH(k_clip_value<Tab>, dim3(p.grid_ew), dim3(kCBlock), 0, stream(), tab, p.count, p.chunk_ew,
                            p.blocks_ew, lo, hi);
     });
     NH_TRY(check_launch());

@@ -5,11 +5,13 @@
 // the reference layout (tensor.asm:7-24).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
 #include <cstdint>
 #include <cstring>
+#include <mutex>
 
 #include "../../include/neural_api.h"
 
@@ -69,12 +71,15 @@ namespace nh {
 // ---------------------------------------------------------------------------
 int          ensure_init();              // NEURAL_OK or error code (lazy init)
 hipStream_t  stream();                   // active stream
-// Events attached to the next softmax / log-softmax kernel launch
-// (neural_hip_time_next_softmax); take_softmax_timer() hands them out once.
+// A pair of events armed by neural_hip_time_next_launch on the calling
+// thread: the launch `skip` launches later carries them (see NH_LAUNCH).
 struct LaunchTimer {
     hipEvent_t start = nullptr, stop = nullptr;
+    int skip = 0;
 };
-LaunchTimer  take_softmax_timer();
+// Counts this thread's launches down; returns the events once, for the launch
+// they were armed for, and null events otherwise.
+LaunchTimer  take_launch_timer();
 int          num_cus();
 int          set_error(int code);        // stores thread-local last error, returns code
 int          hip_fail(hipError_t e);     // maps a HIP error to NEURAL_ERR_* and records it
@@ -94,6 +99,17 @@ struct Workspace {
 constexpr int kMaxPartials = 16384;
 constexpr int kCounters = 1024;
 Workspace   &workspace();
+
+// The workspace is shared by every thread of the process.  An entry point
+// that uses it holds WsGuard from its first launch that writes it until the
+// last read of it: until the host has copied a host-returned result out of
+// host_result, or, for results left in device memory, until the last kernel
+// that reads the summaries has been enqueued (later users enqueue behind it
+// on the same stream).  Recursive, so helpers may take it again.
+std::recursive_mutex &workspace_mutex();
+struct WsGuard {
+    std::lock_guard<std::recursive_mutex> g{workspace_mutex()};
+};
 
 // Raw pointer classification for the pointer-taking entry points.
 bool         is_device_ptr(const void *p);
@@ -238,6 +254,19 @@ template <typename V, typename S> NH_DEV void vset(V &v, int i, S x) { v[i] = x;
 // MI355X: +10-15 % bandwidth for pure streams.
 template <typename T> NH_DEV T ld_nt(const T *p) { return __builtin_nontemporal_load(p); }
 template <typename T> NH_DEV void st_nt(T *p, T v) { __builtin_nontemporal_store(v, p); }
+
+// Every kernel launch goes through NH_LAUNCH.  When the calling thread has
+// armed an event pair (neural_hip_time_next_launch), the launch it was armed
+// for is made with hipExtLaunchKernelGGL, which records the events around
+// this kernel's own execution on its stream; every other launch is plain.
+#define NH_LAUNCH(kernel, grid, block, shmem, strm, ...)                                            \
+    do {                                                                                            \
+        const nh::LaunchTimer t__ = nh::take_launch_timer();                                        \
+        if (t__.start)                                                                              \
+            hipExtLaunchKernelGGL(kernel, grid, block, shmem, strm, t__.start, t__.stop, 0, __VA_ARGS__); \
+        else                                                                                        \
+            hipLaunchKernelGGL(kernel, grid, block, shmem, strm, __VA_ARGS__);                      \
+    } while (0)
 
 // Error-return helper for host code.
 #define NH_TRY(expr)                          \

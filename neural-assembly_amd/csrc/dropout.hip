@@ -501,7 +501,7 @@ int ensure_table_locked(Stream &s, int64_t nseg)
         NH_HIP(hipMemcpyAsync(t, s.table, size_t(s.table_n) * per_seg * sizeof(uint64_t), hipMemcpyDeviceToDevice,
                               stream()));
     const int64_t fresh = cap - s.table_n;
-    hipLaunchKernelGGL(k_jump_table, dim3(unsigned(ceil_div(fresh, kDBlock))), dim3(kDBlock), 0, stream(), t,
+    NH_LAUNCH(k_jump_table, dim3(unsigned(ceil_div(fresh, kDBlock))), dim3(kDBlock), 0, stream(), t,
                        s.table_n, cap, s.powers);
     NH_TRY(check_launch());
     if (s.table) dev_free(s.table);
@@ -562,7 +562,7 @@ static int dropout_fwd(const float *in, float *out, uint8_t *mask, uint64_t n, f
     uint32_t *W = s.win[s.cur], *Wn = s.win[s.cur ^ 1];
     // the grid covers ceil(nseg / 256) * 256 <= table_n segments (table_n is a
     // power of two >= 1024), so every wave reads existing table rows
-    hipLaunchKernelGGL(k_dropout_bits, dim3(unsigned(ceil_div(nseg, kDBlock))), dim3(kDBlock), 0, stream(), s.table,
+    NH_LAUNCH(k_dropout_bits, dim3(unsigned(ceil_div(nseg, kDBlock))), dim3(kDBlock), 0, stream(), s.table,
                        s.x31, W, Wn, nn, nseg, thr, s.bits);
     NH_TRY(check_launch());
     s.cur ^= 1;
@@ -575,11 +575,11 @@ static int dropout_fwd(const float *in, float *out, uint8_t *mask, uint64_t n, f
         const int64_t n4 = nn / 4;
         if (n4 > 0) {
             if (nn < (int64_t(1) << 32))
-                hipLaunchKernelGGL(k_dropout_apply<uint32_t>, dim3(d_grid(ceil_div(n4, kDUnroll))), dim3(kDBlock), 0,
+                NH_LAUNCH(k_dropout_apply<uint32_t>, dim3(d_grid(ceil_div(n4, kDUnroll))), dim3(kDBlock), 0,
                                    stream(), reinterpret_cast<const f32x4 *>(X), reinterpret_cast<f32x4 *>(O),
                                    reinterpret_cast<uint32_t *>(M), s.bits, n4, scale);
             else
-                hipLaunchKernelGGL(k_dropout_apply<int64_t>, dim3(d_grid(ceil_div(n4, kDUnroll))), dim3(kDBlock), 0,
+                NH_LAUNCH(k_dropout_apply<int64_t>, dim3(d_grid(ceil_div(n4, kDUnroll))), dim3(kDBlock), 0,
                                    stream(), reinterpret_cast<const f32x4 *>(X), reinterpret_cast<f32x4 *>(O),
                                    reinterpret_cast<uint32_t *>(M), s.bits, n4, scale);
             NH_TRY(check_launch());
@@ -587,7 +587,7 @@ static int dropout_fwd(const float *in, float *out, uint8_t *mask, uint64_t n, f
         done = n4 * 4;
     }
     if (done < nn) {
-        hipLaunchKernelGGL(k_dropout_apply1, dim3(d_grid(nn - done)), dim3(kDBlock), 0, stream(), X, O, M, s.bits,
+        NH_LAUNCH(k_dropout_apply1, dim3(d_grid(nn - done)), dim3(kDBlock), 0, stream(), X, O, M, s.bits,
                            done, nn, scale);
         NH_TRY(check_launch());
     }
@@ -615,7 +615,7 @@ static int dropout_bwd(const float *go, float *gi, const uint8_t *mask, uint64_t
     if (aligned16(G) && aligned16(O) && (reinterpret_cast<uintptr_t>(M) & 3u) == 0) {
         const int64_t n4 = nn / 4;
         if (n4 > 0) {
-            hipLaunchKernelGGL(k_dropout_bwd, dim3(d_grid(ceil_div(n4, kDUnroll))), dim3(kDBlock), 0, stream(),
+            NH_LAUNCH(k_dropout_bwd, dim3(d_grid(ceil_div(n4, kDUnroll))), dim3(kDBlock), 0, stream(),
                                reinterpret_cast<const f32x4 *>(G), reinterpret_cast<f32x4 *>(O),
                                reinterpret_cast<const uint32_t *>(M), n4, scale);
             NH_TRY(check_launch());
@@ -623,7 +623,7 @@ static int dropout_bwd(const float *go, float *gi, const uint8_t *mask, uint64_t
         done = n4 * 4;
     }
     if (done < nn) {
-        hipLaunchKernelGGL(k_dropout_bwd1, dim3(d_grid(nn - done)), dim3(kDBlock), 0, stream(), G, O, M, done, nn,
+        NH_LAUNCH(k_dropout_bwd1, dim3(d_grid(nn - done)), dim3(kDBlock), 0, stream(), G, O, M, done, nn,
                            scale);
         NH_TRY(check_launch());
     }

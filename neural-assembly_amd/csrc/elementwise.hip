@@ -138,10 +138,10 @@ int launch_fill(void *dst, int dtype, int64_t n, double value)
 {
     if (n <= 0) return NEURAL_OK;
     if (dtype == NEURAL_DTYPE_FLOAT32)
-        hipLaunchKernelGGL((k_fill<float>), dim3(flat_grid(n, 4)), dim3(kBlock), 0, stream(),
+        NH_LAUNCH((k_fill<float>), dim3(flat_grid(n, 4)), dim3(kBlock), 0, stream(),
                            static_cast<float *>(dst), n, float(value));
     else
-        hipLaunchKernelGGL((k_fill<double>), dim3(flat_grid(n, 2)), dim3(kBlock), 0, stream(),
+        NH_LAUNCH((k_fill<double>), dim3(flat_grid(n, 2)), dim3(kBlock), 0, stream(),
                            static_cast<double *>(dst), n, value);
     return check_launch();
 }
@@ -155,10 +155,10 @@ int launch_fill_strided(void *dst, int dtype, const int64_t *shape, const int64_
     for (int i = 0; i < ndim; i++) n *= shape[i];
     if (n <= 0) return NEURAL_OK;
     if (dtype == NEURAL_DTYPE_FLOAT32)
-        hipLaunchKernelGGL((k_fill_nd<float>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(),
+        NH_LAUNCH((k_fill_nd<float>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(),
                            static_cast<float *>(dst), n, d, float(value));
     else
-        hipLaunchKernelGGL((k_fill_nd<double>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(),
+        NH_LAUNCH((k_fill_nd<double>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(),
                            static_cast<double *>(dst), n, d, value);
     return check_launch();
 }
@@ -173,10 +173,10 @@ int launch_copy_nd(void *dst, const int64_t *dshape, const int64_t *dstride, int
     for (int i = 0; i < dndim; i++) n *= dshape[i];
     if (n <= 0) return NEURAL_OK;
     if (es == 4)
-        hipLaunchKernelGGL((k_copy_nd<uint32_t>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(),
+        NH_LAUNCH((k_copy_nd<uint32_t>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(),
                            static_cast<uint32_t *>(dst), od, static_cast<const uint32_t *>(src), sd, n);
     else
-        hipLaunchKernelGGL((k_copy_nd<uint64_t>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(),
+        NH_LAUNCH((k_copy_nd<uint64_t>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(),
                            static_cast<uint64_t *>(dst), od, static_cast<const uint64_t *>(src), sd, n);
     return check_launch();
 }
@@ -353,7 +353,7 @@ int simd_fma_f32(float *dst, const float *a, const float *b, const float *c, uin
     NH_TRY(sb.open(b, bytes, true));
     NH_TRY(sc.open(c, bytes, true));
     NH_TRY(so.open(dst, bytes, false));
-    hipLaunchKernelGGL(k_fma_f32, dim3(strided_grid(int64_t(n))), dim3(kBlock), 0, stream(),
+    NH_LAUNCH(k_fma_f32, dim3(strided_grid(int64_t(n))), dim3(kBlock), 0, stream(),
                        static_cast<const float *>(sa.dev), static_cast<const float *>(sb.dev),
                        static_cast<const float *>(sc.dev), static_cast<float *>(so.dev), int64_t(n));
     NH_TRY(check_launch());

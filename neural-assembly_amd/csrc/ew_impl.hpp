@@ -321,9 +321,9 @@ int launch_rowbcast(const T *a, const T *b, T *o, int64_t rows, int64_t cols, Op
     const int64_t d1 = int64_t(kBlock) % ncv;
     const int64_t dS = (int64_t(g) * kBlock * kUnroll) % ncv;
     if (dS == 0)
-        hipLaunchKernelGGL((k_rowbcast<T, Op, true>), dim3(g), dim3(kBlock), 0, stream(), a, b, o, nv, ncv, d1, dS, op);
+        NH_LAUNCH((k_rowbcast<T, Op, true>), dim3(g), dim3(kBlock), 0, stream(), a, b, o, nv, ncv, d1, dS, op);
     else
-        hipLaunchKernelGGL((k_rowbcast<T, Op, false>), dim3(g), dim3(kBlock), 0, stream(), a, b, o, nv, ncv, d1, dS,
+        NH_LAUNCH((k_rowbcast<T, Op, false>), dim3(g), dim3(kBlock), 0, stream(), a, b, o, nv, ncv, d1, dS,
                            op);
     return check_launch();
 }
@@ -333,9 +333,9 @@ int launch_map2_flat(const T *a, const T *b, T *o, int64_t n, Op op)
 {
     if (n <= 0) return NEURAL_OK;
     if (aligned16(a) && aligned16(b) && aligned16(o))
-        hipLaunchKernelGGL((k_map2_flat<T, Op>), dim3(flat_grid(n, Vec16<T>::n)), dim3(kBlock), 0, stream(), a, b, o, n, op);
+        NH_LAUNCH((k_map2_flat<T, Op>), dim3(flat_grid(n, Vec16<T>::n)), dim3(kBlock), 0, stream(), a, b, o, n, op);
     else
-        hipLaunchKernelGGL((k_map2_flat_scalar<T, Op>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(), a, b, o, n, op);
+        NH_LAUNCH((k_map2_flat_scalar<T, Op>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(), a, b, o, n, op);
     return check_launch();
 }
 
@@ -347,7 +347,7 @@ int launch_map1_f32_tail(const float *a, float *o, int64_t n, F f)
     int64_t g = ceil_div(n / 4, int64_t(kBlock) * kTailUnroll);
     const int64_t cap = kMaxGridBlocks;
     g = g > cap ? cap : (g < 1 ? 1 : g);
-    hipLaunchKernelGGL((k_map1_f32_tail<F>), dim3(unsigned(g)), dim3(kBlock), 0, stream(), a, o, n, f);
+    NH_LAUNCH((k_map1_f32_tail<F>), dim3(unsigned(g)), dim3(kBlock), 0, stream(), a, o, n, f);
     return check_launch();
 }
 
@@ -356,9 +356,9 @@ int launch_map1_flat(const T *a, T *o, int64_t n, F f)
 {
     if (n <= 0) return NEURAL_OK;
     if (aligned16(a) && aligned16(o))
-        hipLaunchKernelGGL((k_map1_flat<T, F>), dim3(flat_grid(n, Vec16<T>::n)), dim3(kBlock), 0, stream(), a, o, n, f);
+        NH_LAUNCH((k_map1_flat<T, F>), dim3(flat_grid(n, Vec16<T>::n)), dim3(kBlock), 0, stream(), a, o, n, f);
     else
-        hipLaunchKernelGGL((k_map1_flat_scalar<T, F>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(), a, o, n, f);
+        NH_LAUNCH((k_map1_flat_scalar<T, F>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(), a, o, n, f);
     return check_launch();
 }
 
@@ -405,10 +405,10 @@ int run_unary(NeuralTensor *out, const NeuralTensor *in, F32 f32, F64 f64)
         ND4 d;
         NH_TRY(build_nd(out, in, nullptr, d));
         if (in->dtype == NEURAL_DTYPE_FLOAT32)
-            hipLaunchKernelGGL((k_map1_nd<float, F32>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(),
+            NH_LAUNCH((k_map1_nd<float, F32>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(),
                                static_cast<const float *>(src), static_cast<float *>(dst), n, d, f32);
         else
-            hipLaunchKernelGGL((k_map1_nd<double, F64>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(),
+            NH_LAUNCH((k_map1_nd<double, F64>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(),
                                static_cast<const double *>(src), static_cast<double *>(dst), n, d, f64);
         NH_TRY(check_launch());
     }
@@ -448,7 +448,7 @@ int launch_binary(NeuralTensor *out, const NeuralTensor *a, const NeuralTensor *
     }
     ND4 d;
     NH_TRY(build_nd(out, a, b, d));
-    hipLaunchKernelGGL((k_map2_nd<T, Op>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(), A, B, O, n, d, op);
+    NH_LAUNCH((k_map2_nd<T, Op>), dim3(strided_grid(n)), dim3(kBlock), 0, stream(), A, B, O, n, d, op);
     return check_launch();
 }
 

@@ -295,9 +295,9 @@ static void launch_ce_wave(const T *x, const CeArgs &a, bool vec)
 {
     const dim3 g(unsigned(ceil_div(a.rows, 4)));
     if (vec && a.cols == int64_t(64) * VPL * Vec16<T>::n)
-        hipLaunchKernelGGL((k_ce_wave<T, VPL, MODE, true>), g, dim3(256), 0, stream(), x, a, vec);
+        NH_LAUNCH((k_ce_wave<T, VPL, MODE, true>), g, dim3(256), 0, stream(), x, a, vec);
     else
-        hipLaunchKernelGGL((k_ce_wave<T, VPL, MODE, false>), g, dim3(256), 0, stream(), x, a, vec);
+        NH_LAUNCH((k_ce_wave<T, VPL, MODE, false>), g, dim3(256), 0, stream(), x, a, vec);
 }
 
 template <typename T, int MODE>
@@ -312,7 +312,7 @@ static int launch_ce(const T *x, const CeArgs &a)
     else if (per <= 4) launch_ce_wave<T, MODE, 4>(x, a, vec);
     else if (per <= 8) launch_ce_wave<T, MODE, 8>(x, a, vec);
     else if (per <= 16) launch_ce_wave<T, MODE, 16>(x, a, vec);
-    else hipLaunchKernelGGL((k_ce_block<T, MODE>), dim3(unsigned(a.rows)), dim3(256), 0, stream(), x, a);
+    else NH_LAUNCH((k_ce_block<T, MODE>), dim3(unsigned(a.rows)), dim3(256), 0, stream(), x, a);
     return check_launch();
 }
 
@@ -365,6 +365,7 @@ template <typename T, int MODE>
 static int ce_run(const T *x, const int64_t *tidx, const T *tval, int64_t rows, int64_t cols, double alpha,
                   double *loss_host, T *grad_dev)
 {
+    WsGuard wg;
     Workspace &ws = workspace();
     // The loss sum (word 0) and the out-of-range flag (int word 32) are stored
     // into the mapped host area.  The flag is zero at init and between calls

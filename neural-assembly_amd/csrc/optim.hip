@@ -211,23 +211,23 @@ static int step_param(OptHandle *o, size_t i, NeuralTensor *p, const NeuralTenso
     NH_TRY(dev_write(p, &pw, false));
     if (o->type == OPT_SGD) {
         if (p->dtype == NEURAL_DTYPE_FLOAT32)
-            hipLaunchKernelGGL(k_sgd_f32, dim3(o_grid(sz)), dim3(kOBlock), 0, stream(), static_cast<float *>(pw),
+            NH_LAUNCH(k_sgd_f32, dim3(o_grid(sz)), dim3(kOBlock), 0, stream(), static_cast<float *>(pw),
                                static_cast<const float *>(gp), o->vel[i], sz, o->lr, o->momentum);
         else
-            hipLaunchKernelGGL(k_sgd_f64, dim3(o_grid(sz)), dim3(kOBlock), 0, stream(), static_cast<double *>(pw),
+            NH_LAUNCH(k_sgd_f64, dim3(o_grid(sz)), dim3(kOBlock), 0, stream(), static_cast<double *>(pw),
                                static_cast<const double *>(gp), o->vel[i], sz, o->lr, o->momentum);
     } else {
         const bool w = o->type == OPT_ADAMW;
         if (p->dtype == NEURAL_DTYPE_FLOAT32) {
             float *P = static_cast<float *>(pw);
             const float *G = static_cast<const float *>(gp);
-            if (w) hipLaunchKernelGGL(k_adam_f32<true>, dim3(o_grid(sz)), dim3(kOBlock), 0, stream(), P, G, o->m[i], o->v[i], sz, a);
-            else hipLaunchKernelGGL(k_adam_f32<false>, dim3(o_grid(sz)), dim3(kOBlock), 0, stream(), P, G, o->m[i], o->v[i], sz, a);
+            if (w) NH_LAUNCH(k_adam_f32<true>, dim3(o_grid(sz)), dim3(kOBlock), 0, stream(), P, G, o->m[i], o->v[i], sz, a);
+            else NH_LAUNCH(k_adam_f32<false>, dim3(o_grid(sz)), dim3(kOBlock), 0, stream(), P, G, o->m[i], o->v[i], sz, a);
         } else {
             double *P = static_cast<double *>(pw);
             const double *G = static_cast<const double *>(gp);
-            if (w) hipLaunchKernelGGL(k_adam_f64<true>, dim3(o_grid(sz)), dim3(kOBlock), 0, stream(), P, G, o->m[i], o->v[i], sz, a);
-            else hipLaunchKernelGGL(k_adam_f64<false>, dim3(o_grid(sz)), dim3(kOBlock), 0, stream(), P, G, o->m[i], o->v[i], sz, a);
+            if (w) NH_LAUNCH(k_adam_f64<true>, dim3(o_grid(sz)), dim3(kOBlock), 0, stream(), P, G, o->m[i], o->v[i], sz, a);
+            else NH_LAUNCH(k_adam_f64<false>, dim3(o_grid(sz)), dim3(kOBlock), 0, stream(), P, G, o->m[i], o->v[i], sz, a);
         }
     }
     NH_TRY(check_launch());

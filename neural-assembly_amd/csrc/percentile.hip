@@ -405,22 +405,23 @@ static int select_ranks(const double *x, int64_t n, const int64_t r[2], uint64_t
     unsigned *cnt0 = reinterpret_cast<unsigned *>(ws + st_b + hist_b), *cnt1 = cnt0 + g;
     uint64_t *keys0 = reinterpret_cast<uint64_t *>(ws + keys_off), *keys1 = keys0 + g * R;
     static_assert(sizeof(PctResult) <= 256, "result record exceeds the host result area");
+    WsGuard wg;
     auto *res = static_cast<PctResult *>(workspace().host_result_dev);
-    hipLaunchKernelGGL(k_pct_init, dim3(1), dim3(64), 0, stream(), st, hist, r[0], r[1], n);
+    NH_LAUNCH(k_pct_init, dim3(1), dim3(64), 0, stream(), st, hist, r[0], r[1], n);
     int rc = check_launch();
     for (int pass = 0; pass < kPasses && rc == NEURAL_OK; pass++) {
-        hipLaunchKernelGGL(k_pct_pass, dim3(unsigned(g)), dim3(kPB), 0, stream(), x, n, R, pass, st, hist, keys0,
+        NH_LAUNCH(k_pct_pass, dim3(unsigned(g)), dim3(kPB), 0, stream(), x, n, R, pass, st, hist, keys0,
                            keys1, cnt0, cnt1);
         rc = check_launch();
         if (rc != NEURAL_OK) break;
         PctResult *last = pass == kPasses - 1 ? res : nullptr;
         const int nb = 1 << pass_bits(pass);
         if (nb == 4096)
-            hipLaunchKernelGGL(k_pct_select<64>, dim3(1), dim3(64), 0, stream(), st, hist, cnt0, cnt1, g, R, pass, last);
+            NH_LAUNCH(k_pct_select<64>, dim3(1), dim3(64), 0, stream(), st, hist, cnt0, cnt1, g, R, pass, last);
         else if (nb == 256)
-            hipLaunchKernelGGL(k_pct_select<4>, dim3(1), dim3(64), 0, stream(), st, hist, cnt0, cnt1, g, R, pass, last);
+            NH_LAUNCH(k_pct_select<4>, dim3(1), dim3(64), 0, stream(), st, hist, cnt0, cnt1, g, R, pass, last);
         else
-            hipLaunchKernelGGL(k_pct_select<1>, dim3(1), dim3(64), 0, stream(), st, hist, cnt0, cnt1, g, R, pass, last);
+            NH_LAUNCH(k_pct_select<1>, dim3(1), dim3(64), 0, stream(), st, hist, cnt0, cnt1, g, R, pass, last);
         rc = check_launch();
     }
     PctResult out{};
@@ -443,7 +444,7 @@ static int zero_sign(const double *x, int64_t n, int64_t j, int *sign_out)
     if (!counts) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
     int *dsign = reinterpret_cast<int *>(counts + nch);
     std::vector<unsigned> c(static_cast<size_t>(nch));
-    hipLaunchKernelGGL(k_pct_zero_count, dim3(unsigned(nch)), dim3(kPB), 0, stream(), x, n, counts);
+    NH_LAUNCH(k_pct_zero_count, dim3(unsigned(nch)), dim3(kPB), 0, stream(), x, n, counts);
     int rc = check_launch();
     if (rc == NEURAL_OK &&
         hipMemcpyAsync(c.data(), counts, size_t(nch) * sizeof(unsigned), hipMemcpyDeviceToHost, stream()) != hipSuccess)
@@ -457,7 +458,7 @@ static int zero_sign(const double *x, int64_t n, int64_t j, int *sign_out)
     int sign = 0;
     if (rc == NEURAL_OK) {
         const int64_t c0 = ch * kZChunk, c1 = c0 + kZChunk < n ? c0 + kZChunk : n;
-        hipLaunchKernelGGL(k_pct_zero_pick, dim3(1), dim3(64), 0, stream(), x, c0, c1, unsigned(j), dsign);
+        NH_LAUNCH(k_pct_zero_pick, dim3(1), dim3(64), 0, stream(), x, c0, c1, unsigned(j), dsign);
         rc = check_launch();
         if (rc == NEURAL_OK && hipMemcpyAsync(&sign, dsign, sizeof(int), hipMemcpyDeviceToHost, stream()) != hipSuccess)
             rc = NEURAL_ERR_INTERNAL;

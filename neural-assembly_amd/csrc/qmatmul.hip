@@ -199,13 +199,13 @@ static int qmatmul(const int8_t *A, const int8_t *B, double *C, int64_t M, int64
         rc = NEURAL_ERR_INTERNAL;
     const int64_t units = Kp / 16;
     if (rc == NEURAL_OK) {
-        hipLaunchKernelGGL(k_qpad_a, dim3(unsigned(ceil_div(M * units, 256))), dim3(256), 0, stream(),
+        NH_LAUNCH(k_qpad_a, dim3(unsigned(ceil_div(M * units, 256))), dim3(256), 0, stream(),
                            static_cast<const int8_t *>(sa.dev), Ap, M, K, Kp, units);
-        hipLaunchKernelGGL(k_qrowsum, dim3(unsigned(ceil_div(M, 4))), dim3(256), 0, stream(), Ap, rowA, M, Kp);
-        hipLaunchKernelGGL(k_qpad_bt, dim3(unsigned(ceil_div(N, 256)), unsigned(units)), dim3(256), 0, stream(),
+        NH_LAUNCH(k_qrowsum, dim3(unsigned(ceil_div(M, 4))), dim3(256), 0, stream(), Ap, rowA, M, Kp);
+        NH_LAUNCH(k_qpad_bt, dim3(unsigned(ceil_div(N, 256)), unsigned(units)), dim3(256), 0, stream(),
                            static_cast<const int8_t *>(sb.dev), Bt, colB, K, N, Kp);
         const double cs = pa->scale * pb->scale;  // combined_scale, quantize.c:198
-        hipLaunchKernelGGL(k_qgemm, dim3(unsigned(Np / kQT), unsigned(Mp / kQT)), dim3(256), 0, stream(), Ap, Bt,
+        NH_LAUNCH(k_qgemm, dim3(unsigned(Np / kQT), unsigned(Mp / kQT)), dim3(256), 0, stream(), Ap, Bt,
                            static_cast<double *>(sc.dev), rowA, colB, M, N, K, Kp, pa->zero_point, pb->zero_point, cs);
         rc = check_launch();
     }

@@ -275,10 +275,10 @@ static int launch_quantize(const T *x, int8_t *q, int64_t n, QArgs qa)
 {
     const bool vec = (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (reinterpret_cast<uintptr_t>(q) & 3u) == 0;
     if (vec)
-        hipLaunchKernelGGL((k_quantize<T>), dim3(q_grid(n / 4, kQBlock * kQUnroll)), dim3(kQBlock), 0, stream(), x,
+        NH_LAUNCH((k_quantize<T>), dim3(q_grid(n / 4, kQBlock * kQUnroll)), dim3(kQBlock), 0, stream(), x,
                            q, n, qa);
     else
-        hipLaunchKernelGGL((k_quantize_scalar<T>), dim3(q_grid(n, kQBlock)), dim3(kQBlock), 0, stream(), x, q, n, qa);
+        NH_LAUNCH((k_quantize_scalar<T>), dim3(q_grid(n, kQBlock)), dim3(kQBlock), 0, stream(), x, q, n, qa);
     return check_launch();
 }
 
@@ -287,10 +287,10 @@ static int launch_dequantize(const int8_t *q, T *y, int64_t n, QArgs qa)
 {
     const bool vec = (reinterpret_cast<uintptr_t>(y) & 15u) == 0 && (reinterpret_cast<uintptr_t>(q) & 3u) == 0;
     if (vec)
-        hipLaunchKernelGGL((k_dequantize<T>), dim3(q_grid(n / 4, kQBlock * kQUnroll)), dim3(kQBlock), 0, stream(), q,
+        NH_LAUNCH((k_dequantize<T>), dim3(q_grid(n / 4, kQBlock * kQUnroll)), dim3(kQBlock), 0, stream(), q,
                            y, n, qa);
     else
-        hipLaunchKernelGGL((k_dequantize_scalar<T>), dim3(q_grid(n, kQBlock)), dim3(kQBlock), 0, stream(), q, y, n,
+        NH_LAUNCH((k_dequantize_scalar<T>), dim3(q_grid(n, kQBlock)), dim3(kQBlock), 0, stream(), q, y, n,
                            qa);
     return check_launch();
 }
@@ -306,6 +306,7 @@ static int calibrate(const T *data, int64_t n, int symmetric, QuantParams *out, 
     if (s.open(data, size_t(n) * sizeof(T), true) != NEURAL_OK) return -1;
     RedMinMax<T> red;
     red.symmetric = symmetric ? 1 : 0;
+    WsGuard wg;
     void *res = out_on_device ? static_cast<void *>(out) : workspace().host_result_dev;
     if (launch_reduce_full(static_cast<const T *>(s.dev), n, red, res) != NEURAL_OK) return -1;
     if (!out_on_device && host_result_fetch(out, sizeof(QuantParams)) != NEURAL_OK) return -1;
@@ -358,6 +359,7 @@ static int qerr(const T *data, int64_t n, const QuantParams *p, double *sig, dou
     red.scale = p->scale;
     red.inv = 1.0 / p->scale;
     red.zp = p->zero_point;
+    WsGuard wg;
     QErrOut st;
     if (launch_reduce_full(static_cast<const T *>(s.dev), n, red, workspace().host_result_dev) != NEURAL_OK) return -1;
     if (host_result_fetch(&st, sizeof(st)) != NEURAL_OK) return -1;

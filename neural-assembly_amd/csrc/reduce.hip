@@ -168,17 +168,17 @@ static int colsum(const NeuralTensor *in, const void *src, int64_t rows, int64_t
     if (!part) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
     const dim3 g1{unsigned(cgroups), unsigned(nchunks), 1u};
     if (in->dtype == NEURAL_DTYPE_FLOAT32)
-        hipLaunchKernelGGL(k_colsum_stage1_f32, g1, dim3(256), 0, stream(), static_cast<const float *>(src), rows,
+        NH_LAUNCH(k_colsum_stage1_f32, g1, dim3(256), 0, stream(), static_cast<const float *>(src), rows,
                            cols, chunk, part);
     else
-        hipLaunchKernelGGL(k_colsum_stage1_f64, g1, dim3(256), 0, stream(), static_cast<const double *>(src), rows,
+        NH_LAUNCH(k_colsum_stage1_f64, g1, dim3(256), 0, stream(), static_cast<const double *>(src), rows,
                            cols, chunk, part);
     const int64_t div = mean ? rows : 1;
     if (in->dtype == NEURAL_DTYPE_FLOAT32)
-        hipLaunchKernelGGL((k_colsum_stage2<float>), dim3(unsigned(cgroups)), dim3(256), 0, stream(), part, nchunks,
+        NH_LAUNCH((k_colsum_stage2<float>), dim3(unsigned(cgroups)), dim3(256), 0, stream(), part, nchunks,
                            cols, div, static_cast<float *>(dst));
     else
-        hipLaunchKernelGGL((k_colsum_stage2<double>), dim3(unsigned(cgroups)), dim3(256), 0, stream(), part,
+        NH_LAUNCH((k_colsum_stage2<double>), dim3(unsigned(cgroups)), dim3(256), 0, stream(), part,
                            nchunks, cols, div, static_cast<double *>(dst));
     const int rc = check_launch();
     dev_free(part);
@@ -217,6 +217,7 @@ static int full_to_host(const NeuralTensor *t, Out *host_out)
     const int64_t n = numel(t);
     Contig c;
     NH_TRY(c.open(t));
+    WsGuard wg;
     void *res = workspace().host_result_dev;
     if (t->dtype == NEURAL_DTYPE_FLOAT32)
         NH_TRY(launch_reduce_full(static_cast<const float *>(c.p), n, RedOf<float>{}, res));
@@ -396,6 +397,7 @@ float simd_sum_f32(const float *a, uint64_t n)
     if (ensure_init() != NEURAL_OK || !a || n == 0) return 0.0f;
     Staged sa;
     if (sa.open(a, size_t(n) * 4, true) != NEURAL_OK) return 0.0f;
+    WsGuard wg;
     void *res = workspace().host_result_dev;
     double s = 0.0;
     if (launch_reduce_full(static_cast<const float *>(sa.dev), int64_t(n), SumF64<float>{}, res) != NEURAL_OK)
@@ -444,10 +446,11 @@ extern "C" float simd_dot_f32(const float *a, const float *b, uint64_t n)
     if (ensure_init() != NEURAL_OK || !a || !b || n == 0) return 0.0f;
     Staged sa, sb;
     if (sa.open(a, size_t(n) * 4, true) != NEURAL_OK || sb.open(b, size_t(n) * 4, true) != NEURAL_OK) return 0.0f;
+    WsGuard wg;
     Workspace &ws = workspace();
     int64_t g = ceil_div(int64_t(n), kRBlock);
     if (g > int64_t(num_cus()) * 4) g = int64_t(num_cus()) * 4;
-    hipLaunchKernelGGL(k_dot_f32, dim3(unsigned(g)), dim3(kRBlock), 0, stream(), static_cast<const float *>(sa.dev),
+    NH_LAUNCH(k_dot_f32, dim3(unsigned(g)), dim3(kRBlock), 0, stream(), static_cast<const float *>(sa.dev),
                        static_cast<const float *>(sb.dev), int64_t(n), static_cast<double *>(ws.partials), ws.counter,
                        static_cast<double *>(ws.host_result_dev));
     double s = 0.0;

@@ -258,18 +258,19 @@ int launch_reduce(const T *x, int64_t rows, int64_t cols, int64_t ld, const Red 
         }
     }
     if (gx > 1) {
+        WsGuard wg;
         auto *part = static_cast<typename Red::B *>(workspace().partials);
         const dim3 grid{unsigned(gx), unsigned(rows), 1u};
-        hipLaunchKernelGGL((k_reduce_seg<T, Red>), grid, dim3(kRBlock), 0, stream(), x, cols, ld, chunk, red, part,
+        NH_LAUNCH((k_reduce_seg<T, Red>), grid, dim3(kRBlock), 0, stream(), x, cols, ld, chunk, red, part,
                            vec);
-        hipLaunchKernelGGL((k_reduce_combine<T, Red>), dim3(unsigned(rows)), dim3(kRBlock), 0, stream(), x, cols, ld,
+        NH_LAUNCH((k_reduce_combine<T, Red>), dim3(unsigned(rows)), dim3(kRBlock), 0, stream(), x, cols, ld,
                            int(gx), red, part, out);
     } else if (cols <= 2048) {
         const unsigned g = unsigned(ceil_div(rows, kRBlock / 64));
-        hipLaunchKernelGGL((k_reduce_rows<T, Red, 64>), dim3(g), dim3(kRBlock), 0, stream(), x, rows, cols, ld, red,
+        NH_LAUNCH((k_reduce_rows<T, Red, 64>), dim3(g), dim3(kRBlock), 0, stream(), x, rows, cols, ld, red,
                            out, vec);
     } else {
-        hipLaunchKernelGGL((k_reduce_rows<T, Red, kRBlock>), dim3(unsigned(rows)), dim3(kRBlock), 0, stream(), x,
+        NH_LAUNCH((k_reduce_rows<T, Red, kRBlock>), dim3(unsigned(rows)), dim3(kRBlock), 0, stream(), x,
                            rows, cols, ld, red, out, vec);
     }
     return check_launch();

@@ -203,6 +203,7 @@ int sync()
 
 int host_result_fetch(void *dst, size_t bytes)
 {
+    WsGuard wg;
     if (bytes > 256) return set_error(NEURAL_ERR_INTERNAL);
     NH_TRY(sync());
     std::memcpy(dst, workspace().host_result, bytes);
@@ -211,6 +212,7 @@ int host_result_fetch(void *dst, size_t bytes)
 
 int result_to_host(void *dst, const void *dev_src, size_t bytes)
 {
+    WsGuard wg;
     Workspace &ws = workspace();
     if (bytes > 256) return set_error(NEURAL_ERR_INTERNAL);
     NH_HIP(hipMemcpyAsync(ws.host_result, dev_src, bytes, hipMemcpyDeviceToHost, stream()));
@@ -358,13 +360,24 @@ static void *host_map(NeuralTensor *t)
     return t->data;
 }
 
-LaunchTimer g_softmax_timer;
+thread_local LaunchTimer t_timer;
 
-LaunchTimer take_softmax_timer()
+LaunchTimer take_launch_timer()
 {
-    const LaunchTimer t = g_softmax_timer;
-    g_softmax_timer = LaunchTimer{};
+    if (!t_timer.start) return LaunchTimer{};
+    if (t_timer.skip > 0) {
+        t_timer.skip--;
+        return LaunchTimer{};
+    }
+    const LaunchTimer t = t_timer;
+    t_timer = LaunchTimer{};
     return t;
+}
+
+std::recursive_mutex &workspace_mutex()
+{
+    static std::recursive_mutex *m = new std::recursive_mutex();  // never destroyed, like the runtime
+    return *m;
 }
 
 }  // namespace nh
@@ -821,12 +834,20 @@ int neural_hip_reset_stream(void)
     return set_error(NEURAL_OK);
 }
 
-int neural_hip_time_next_softmax(void *start_event, void *stop_event)
+int neural_hip_time_next_launch(void *start_event, void *stop_event, int skip)
 {
     NH_TRY(ensure_init());
     if (!start_event || !stop_event) return set_error(NEURAL_ERR_NULL_POINTER);
-    g_softmax_timer.start = static_cast<hipEvent_t>(start_event);
-    g_softmax_timer.stop = static_cast<hipEvent_t>(stop_event);
+    if (skip < 0) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
+    t_timer.start = static_cast<hipEvent_t>(start_event);
+    t_timer.stop = static_cast<hipEvent_t>(stop_event);
+    t_timer.skip = skip;
+    return set_error(NEURAL_OK);
+}
+
+int neural_hip_time_cancel(void)
+{
+    t_timer = LaunchTimer{};
     return set_error(NEURAL_OK);
 }
 

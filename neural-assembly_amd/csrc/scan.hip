@@ -47,6 +47,7 @@ struct RedScan {
 template <typename T>
 static int scan_dev(const T *x, int64_t n, ScanOut *st)
 {
+    WsGuard wg;
     NH_TRY(launch_reduce_full(x, n, RedScan<T>{}, workspace().host_result_dev));
     return host_result_fetch(st, sizeof(*st));
 }

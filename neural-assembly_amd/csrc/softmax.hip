@@ -226,17 +226,10 @@ __global__ __launch_bounds__(kSmBlock) void k_softmax_block(const T *__restrict_
     }
 }
 
-// With timing events pending (neural_hip_time_next_softmax) the launch
-// carries them (hipExtLaunchKernelGGL), so their elapsed time is this kernel's
-// execution; otherwise a plain launch.
 template <typename K, typename... Args>
 static void launch_timed(K kernel, unsigned g, Args... args)
 {
-    const LaunchTimer t = take_softmax_timer();
-    if (t.start)
-        hipExtLaunchKernelGGL(kernel, dim3(g), dim3(kSmBlock), 0, stream(), t.start, t.stop, 0, args...);
-    else
-        hipLaunchKernelGGL(kernel, dim3(g), dim3(kSmBlock), 0, stream(), args...);
+    NH_LAUNCH(kernel, dim3(g), dim3(kSmBlock), 0, stream(), args...);
 }
 
 template <typename T, bool LOG, int VPL>
@@ -267,7 +260,7 @@ static int launch_softmax(const T *x, T *y, int64_t rows, int64_t cols)
         else if (ncv <= 512) launch_wave<T, LOG, 8>(x, y, rows, cols, g);
         else launch_wave<T, LOG, 16>(x, y, rows, cols, g);
     } else {
-        hipLaunchKernelGGL((k_softmax_block<T, LOG>), dim3(unsigned(rows)), dim3(kSmBlock), 0, stream(), x, y, cols);
+        NH_LAUNCH((k_softmax_block<T, LOG>), dim3(unsigned(rows)), dim3(kSmBlock), 0, stream(), x, y, cols);
     }
     return check_launch();
 }

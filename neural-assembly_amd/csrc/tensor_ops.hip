@@ -100,7 +100,7 @@ int tensor_concat_2d(const double *a, const double *b, int64_t rows_a, int64_t c
         *out_rows = rows_a + rows_b;
         *out_cols = cols_a;
     } else {
-        hipLaunchKernelGGL(k_concat_cols, dim3(t_grid(na + nb)), dim3(256), 0, stream(),
+        NH_LAUNCH(k_concat_cols, dim3(t_grid(na + nb)), dim3(256), 0, stream(),
                            static_cast<const double *>(sa.dev), static_cast<const double *>(sb.dev), O, rows_a,
                            cols_a, cols_b);
         if (check_launch() != NEURAL_OK) return -1;
@@ -133,7 +133,7 @@ int tensor_split_2d(const double *in, int64_t rows, int64_t cols, int64_t axis, 
             return -1;
         *rows_a = split_index; *cols_a = cols; *rows_b = rows - split_index; *cols_b = cols;
     } else {
-        hipLaunchKernelGGL(k_split_cols, dim3(t_grid(n)), dim3(256), 0, stream(), I, static_cast<double *>(sa.dev),
+        NH_LAUNCH(k_split_cols, dim3(t_grid(n)), dim3(256), 0, stream(), I, static_cast<double *>(sa.dev),
                            static_cast<double *>(sb.dev), rows, cols, split_index);
         if (check_launch() != NEURAL_OK) return -1;
         *rows_a = rows; *cols_a = split_index; *rows_b = rows; *cols_b = cols - split_index;
@@ -153,7 +153,7 @@ int tensor_pad_2d(const double *in, int64_t in_rows, int64_t in_cols, int64_t pa
     const int64_t R = in_rows + pad_top + pad_bottom, C = in_cols + pad_left + pad_right;
     Staged si, so;
     if (si.open(in, size_t(in_rows * in_cols) * 8, true) || so.open(out, size_t(R * C) * 8, false)) return -1;
-    hipLaunchKernelGGL(k_pad, dim3(t_grid(R * C)), dim3(256), 0, stream(), static_cast<const double *>(si.dev),
+    NH_LAUNCH(k_pad, dim3(t_grid(R * C)), dim3(256), 0, stream(), static_cast<const double *>(si.dev),
                        static_cast<double *>(so.dev), in_rows, in_cols, pad_top, pad_left, R, C, pad_value);
     if (check_launch() != NEURAL_OK) return -1;
     *out_rows = R;
@@ -172,7 +172,7 @@ int tensor_transpose2d_array(const double *in, int64_t rows, int64_t cols, doubl
     if (si.open(in, bytes, true) || so.open(out, bytes, false)) return -1;
     const int64_t gx = ceil_div(cols, kTile), gy = ceil_div(rows, kTile);
     if (gx > 0x7fffffff || gy > 65535) return -1;
-    hipLaunchKernelGGL(k_transpose, dim3(unsigned(gx), unsigned(gy)), dim3(256), 0, stream(),
+    NH_LAUNCH(k_transpose, dim3(unsigned(gx), unsigned(gy)), dim3(256), 0, stream(),
                        static_cast<const double *>(si.dev), static_cast<double *>(so.dev), rows, cols);
     if (check_launch() != NEURAL_OK) return -1;
     if (so.finish(true) || si.finish(false)) return -1;

@@ -256,9 +256,9 @@ static int stats(const double *data, int64_t b, int64_t F, double *mean, double 
     }
     ColState *part = static_cast<ColState *>(dev_alloc(size_t(nchunks * F) * sizeof(ColState)));
     if (!part) return -1;
-    hipLaunchKernelGGL(k_colstats, dim3(unsigned(fgroups), unsigned(nchunks)), dim3(kTBlock), 0, stream(),
+    NH_LAUNCH(k_colstats, dim3(unsigned(fgroups), unsigned(nchunks)), dim3(kTBlock), 0, stream(),
                        static_cast<const double *>(sx.dev), b, F, chunk, part);
-    hipLaunchKernelGGL(k_colstats_final, dim3(unsigned(F)), dim3(kRBlock), 0, stream(), part, nchunks, b, douts[0],
+    NH_LAUNCH(k_colstats_final, dim3(unsigned(F)), dim3(kRBlock), 0, stream(), part, nchunks, b, douts[0],
                        douts[1], douts[2], douts[3]);
     const int rc = check_launch();
     dev_free(part);
@@ -293,16 +293,16 @@ static int feat_apply(const double *data, double *out, int64_t b, int64_t F, con
         const int64_t stride = int64_t(g) * kTBlock * kTUnroll;
         const int64_t d1 = (2 * int64_t(kTBlock)) % F, dS = (2 * stride) % F;
         if (d1 == 0 && dS == 0)
-            hipLaunchKernelGGL((k_feat_map2<MODE, true>), dim3(g), dim3(kTBlock), 0, stream(),
+            NH_LAUNCH((k_feat_map2<MODE, true>), dim3(g), dim3(kTBlock), 0, stream(),
                                reinterpret_cast<const f64x2 *>(X), reinterpret_cast<f64x2 *>(O), n2, F, A, C, eps, d1,
                                dS);
         else
-            hipLaunchKernelGGL((k_feat_map2<MODE, false>), dim3(g), dim3(kTBlock), 0, stream(),
+            NH_LAUNCH((k_feat_map2<MODE, false>), dim3(g), dim3(kTBlock), 0, stream(),
                                reinterpret_cast<const f64x2 *>(X), reinterpret_cast<f64x2 *>(O), n2, F, A, C, eps, d1,
                                dS);
     } else {
         const unsigned g = t_grid(n);
-        hipLaunchKernelGGL(k_feat_map1<MODE>, dim3(g), dim3(kTBlock), 0, stream(), X, O, n, F, A, C, eps,
+        NH_LAUNCH(k_feat_map1<MODE>, dim3(g), dim3(kTBlock), 0, stream(), X, O, n, F, A, C, eps,
                            (int64_t(g) * kTBlock) % F);
     }
     if (check_launch() != NEURAL_OK) return -1;

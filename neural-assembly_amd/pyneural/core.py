@@ -280,7 +280,8 @@ _SIGS = {
     "neural_cross_entropy_loss": (_i, [_vp, _vp, _dp]),
     # HIP runtime controls
     "neural_hip_set_stream": (_i, [_vp]),
-    "neural_hip_time_next_softmax": (_i, [_vp, _vp]),
+    "neural_hip_time_next_launch": (_i, [_vp, _vp, _i]),
+    "neural_hip_time_cancel": (_i, []),
     "neural_hip_reset_stream": (_i, []),
     "neural_hip_get_stream": (_vp, []),
     "neural_hip_synchronize": (_i, []),

@@ -74,10 +74,11 @@ def test_softmax_errors(pn):
     assert pn.core._lib.neural_softmax(c._ptr, a._ptr) == pn.NeuralError.SHAPE_MISMATCH
 
 
-def test_softmax_timed_launch(pn):
-    """neural_hip_time_next_softmax: the events ride on the next softmax launch
-    (elapsed time > 0, output unchanged), are used once, and a null event is
-    rejected."""
+def test_timed_launch(pn):
+    """neural_hip_time_next_launch: the events ride on the chosen launch of the
+    calling thread (elapsed time > 0, outputs unchanged), are used once, can
+    skip launches (the combine launch of a whole-tensor sum is skip = 1) and
+    be cancelled; null events and negative skips are rejected."""
     import ctypes
     from pathlib import Path
     import torch
@@ -93,21 +94,57 @@ def test_softmax_timed_launch(pn):
     assert lib.neural_softmax(y_plain._ptr, tx._ptr) == 0
     s = torch.cuda.current_stream()
     lib.neural_hip_set_stream(ctypes.c_void_p(s.cuda_stream))
+    ev = []
     try:
-        e0, e1 = ctypes.c_void_p(), ctypes.c_void_p()
-        assert hip.hipEventCreate(ctypes.byref(e0)) == 0 and hip.hipEventCreate(ctypes.byref(e1)) == 0
-        assert lib.neural_hip_time_next_softmax(e0, e1) == 0
+        def pair():
+            e0, e1 = ctypes.c_void_p(), ctypes.c_void_p()
+            assert hip.hipEventCreate(ctypes.byref(e0)) == 0 and hip.hipEventCreate(ctypes.byref(e1)) == 0
+            ev.extend([e0, e1])
+            return e0, e1
+
+        def elapsed(e0, e1):
+            ms = ctypes.c_float()
+            assert hip.hipEventElapsedTime(ctypes.byref(ms), e0, e1) == 0
+            return ms.value
+
+        e0, e1 = pair()
+        assert lib.neural_hip_time_next_launch(e0, e1, 0) == 0
         y = pn.Tensor.create(tx.shape, tx.dtype)
         assert lib.neural_softmax(y._ptr, tx._ptr) == 0
         torch.cuda.synchronize()
+        assert elapsed(e0, e1) > 0.0
+        assert np.array_equal(y.numpy(), y_plain.numpy())
+        assert lib.neural_softmax(y._ptr, tx._ptr) == 0  # nothing armed: a plain launch
+        assert np.array_equal(y.numpy(), y_plain.numpy())
+        # a whole-tensor sum of 2^24 values is a segment launch and a combine launch
+        big = pn.Tensor.from_numpy(rng.uniform(-1, 1, 1 << 24).astype(np.float32))
+        r0 = ctypes.c_double()
+        assert lib.neural_sum(big._ptr, ctypes.byref(r0)) == 0
+        a0, a1 = pair()
+        b0, b1 = pair()
+        assert lib.neural_hip_time_next_launch(a0, a1, 0) == 0
+        r1 = ctypes.c_double()
+        assert lib.neural_sum(big._ptr, ctypes.byref(r1)) == 0
+        assert lib.neural_hip_time_next_launch(b0, b1, 1) == 0
+        r2 = ctypes.c_double()
+        assert lib.neural_sum(big._ptr, ctypes.byref(r2)) == 0
+        torch.cuda.synchronize()
+        seg_ms, comb_ms = elapsed(a0, a1), elapsed(b0, b1)
+        assert seg_ms > 0.0 and comb_ms > 0.0 and comb_ms < seg_ms, (seg_ms, comb_ms)
+        assert r0.value == r1.value == r2.value
+        # cancel: armed events are dropped unused
+        c0, c1 = pair()
+        assert lib.neural_hip_time_next_launch(c0, c1, 0) == 0
+        assert lib.neural_hip_time_cancel() == 0
+        assert lib.neural_softmax(y._ptr, tx._ptr) == 0
+        torch.cuda.synchronize()
         ms = ctypes.c_float()
-        assert hip.hipEventElapsedTime(ctypes.byref(ms), e0, e1) == 0
-        assert ms.value > 0.0
-        assert np.array_equal(y.numpy(), y_plain.numpy())
-        assert lib.neural_softmax(y._ptr, tx._ptr) == 0  # no events pending: a plain launch
-        assert np.array_equal(y.numpy(), y_plain.numpy())
-        assert lib.neural_hip_time_next_softmax(None, e1) == pn.NeuralError.NULL_POINTER
-        hip.hipEventDestroy(e0)
-        hip.hipEventDestroy(e1)
+        assert hip.hipEventElapsedTime(ctypes.byref(ms), c0, c1) != 0  # never recorded
+        hip.hipGetLastError()  # clear that error so the next library call does not report it
+        assert lib.neural_hip_time_next_launch(None, e1, 0) == pn.NeuralError.NULL_POINTER
+        assert lib.neural_hip_time_next_launch(e0, e1, -1) == pn.NeuralError.INVALID_ARGUMENT
     finally:
+        lib.neural_hip_time_cancel()
         lib.neural_hip_reset_stream()
+        for e in ev:
+            hip.hipEventDestroy(e)
