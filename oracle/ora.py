@@ -15,6 +15,7 @@ import numpy as np
 
 HERE = Path(__file__).resolve().parent
 ORACLE_SO = HERE / "liboracle.so"
+CPU_SO = HERE / "libcpu_baseline.so"
 REF_SO = HERE / "_ref" / "libneural_ref.so"
 
 ADD, SUB, MUL, DIV, MAX = 0, 1, 2, 3, 4
@@ -72,6 +73,55 @@ def ref():
         _ref.opt_state_bytes.argtypes = [ctypes.c_void_p]
         _ref.opt_state_export.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
     return _ref
+
+
+_cpu = None
+
+
+def cpu():
+    """The reference's host SIMD loops (cpu_baseline.c): AVX-256 ew_add /
+    ew_mul / reduce_sum, the AVX-512 simd.asm path, the SSE L2 norm and the
+    node_relu pass structure, for bench.py's CPU baseline."""
+    global _cpu
+    if _cpu is None:
+        if not CPU_SO.exists():
+            raise RuntimeError(f"{CPU_SO} missing: run `make -C oracle`")
+        c = ctypes.CDLL(str(CPU_SO))
+        P, I64 = ctypes.c_void_p, ctypes.c_int64
+        for n in ("cpu_ew_add_avx", "cpu_ew_mul_avx", "cpu_simd_add_avx512", "cpu_simd_mul_avx512"):
+            getattr(c, n).argtypes = [P, P, P, I64]
+            getattr(c, n).restype = None
+        for n in ("cpu_reduce_sum_avx", "cpu_simd_sum_avx512"):
+            getattr(c, n).argtypes = [P, I64]
+            getattr(c, n).restype = ctypes.c_float
+        c.cpu_l2_sse.argtypes = [P, ctypes.c_uint64]
+        c.cpu_l2_sse.restype = ctypes.c_float
+        c.cpu_relu_node.argtypes = [P, P, I64]
+        c.cpu_relu_node.restype = ctypes.c_int
+        _cpu = c
+    return _cpu
+
+
+def cpu_binary(name, a, b, out=None):
+    """cpu_ew_add_avx / cpu_ew_mul_avx / cpu_simd_add_avx512 / cpu_simd_mul_avx512."""
+    out = np.empty_like(a) if out is None else out
+    getattr(cpu(), name)(a.ctypes.data, b.ctypes.data, out.ctypes.data, a.size)
+    return out
+
+
+def cpu_sum(name, x):
+    """cpu_reduce_sum_avx / cpu_simd_sum_avx512 (float result)."""
+    return getattr(cpu(), name)(x.ctypes.data, x.size)
+
+
+def cpu_l2(x):
+    return cpu().cpu_l2_sse(x.ctypes.data, x.size)
+
+
+def cpu_relu_node(x, out=None):
+    out = np.empty_like(x) if out is None else out
+    assert cpu().cpu_relu_node(x.ctypes.data, out.ctypes.data, x.size) == 0
+    return out
 
 
 def _p(a):
