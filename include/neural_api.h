@@ -280,6 +280,19 @@ double quantization_snr_f32(const float *original, int64_t n, const QuantParams 
 int    calibrate_minmax_f32_dev(const float *data, int64_t n, int symmetric, QuantParams *dev_params);
 int    quantize_tensor_f32_dev(const float *data, int8_t *out, int64_t n, const QuantParams *dev_params);
 int    dequantize_tensor_f32_dev(const int8_t *data, float *out, int64_t n, const QuantParams *dev_params);
+/* NEW, no counterpart in the reference: calibrate_minmax_f32_dev for callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same result, bit for bit; data and
+ * dev_params must be device pointers (host pointers: -1,
+ * NEURAL_ERR_INVALID_ARGUMENT).  Allocates nothing and never initialises the
+ * library: before neural_init() it returns -1 with NEURAL_ERR_INVALID_CONFIG.
+ * The segment summaries use a static 64 KiB device buffer per GPU (held until
+ * the process ends); a launch whose summaries would not fit it returns -1
+ * with NEURAL_ERR_TENSOR_TOO_LARGE (never on MI355X: at most 4 per CU).
+ * Calls enqueued on one stream are ordered; calls that overlap on one GPU
+ * (e.g. captured graphs replayed concurrently on two streams) race on the
+ * buffer. */
+int    calibrate_minmax_f32_dev_noalloc(const float *data, int64_t n, int symmetric, QuantParams *dev_params);
 
 /* ---- Training ops: training_ops.asm:544-696 (neural_api.asm:2786-2791) -------- */
 int   neural_tensor_has_nan(const float *data, uint64_t n);      /* training_ops.asm:544 */

@@ -70,6 +70,13 @@ namespace nh {
 // Runtime
 // ---------------------------------------------------------------------------
 int          ensure_init();              // NEURAL_OK or error code (lazy init)
+// NEURAL_OK when the runtime was initialised earlier (makes its device
+// current on this thread); NEURAL_ERR_INVALID_CONFIG otherwise.  Never
+// initialises, so it allocates nothing.
+int          ensure_ready();
+// Per-device set-up of static device buffers, run by ensure_init with the
+// device current (defined beside the buffer it resolves).
+int          setup_static_scratch(int device);
 hipStream_t  stream();                   // active stream
 // A pair of events armed by neural_hip_time_next_launch on the calling
 // thread: the launch `skip` launches later carries them (see NH_LAUNCH).

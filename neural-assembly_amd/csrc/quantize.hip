@@ -14,6 +14,9 @@
 //              out-of-range) and the wrap-around add of the reference build.
 //   dequantize: ((double)q - (double)zp) * scale.
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <mutex>
 
 #include "quant_common.hpp"
 #include "reduce_impl.hpp"
@@ -389,6 +392,53 @@ static double quant_snr(const T *d, int64_t n, const QuantParams *p)
     return 10.0 * std::log10(sig / noise);
 }
 
+// ---- calibration without allocation ----------------------------------------------------
+
+// Segment summaries of calibrate_minmax_f32_dev_noalloc live in this static
+// device array, one copy per GPU, kept until the process ends.  Host code
+// never passes the array's name to a kernel (on the host it is only a
+// stand-in for the symbol); it uses the device address that
+// hipGetSymbolAddress returned for that GPU at initialisation.
+constexpr size_t kScratchBytes = size_t(64) << 10;  // 4096 summaries of 16 bytes: 16 per CU on 256 CUs
+constexpr int kMaxScratchDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+static void *g_scratch_ptr[kMaxScratchDevices];
+static std::mutex g_scratch_mu;
+
+int setup_static_scratch(int device)
+{
+    if (device < 0 || device >= kMaxScratchDevices) return NEURAL_ERR_INTERNAL;
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+        if (std::getenv("NEURAL_HIP_VERBOSE"))
+            std::fprintf(stderr, "libneural_hip: hipGetSymbolAddress(scratch) failed: %s\n", hipGetErrorString(e));
+        return NEURAL_ERR_INTERNAL;
+    }
+    g_scratch_ptr[device] = p;
+    return NEURAL_OK;
+}
+
+static int calibrate_noalloc(const float *data, int64_t n, int symmetric, QuantParams *dev_params)
+{
+    if (!data || !dev_params) return set_error(NEURAL_ERR_NULL_POINTER);
+    if (n <= 0) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
+    NH_TRY(ensure_ready());
+    int dev = -1;
+    NH_HIP(hipGetDevice(&dev));
+    void *scr = (dev >= 0 && dev < kMaxScratchDevices) ? g_scratch_ptr[dev] : nullptr;
+    if (!scr) return set_error(NEURAL_ERR_INVALID_CONFIG);
+    // host buffers would need staging copies, i.e. an allocation
+    if (!is_device_ptr(data) || !is_device_ptr(dev_params)) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
+    RedMinMax<float> red;
+    red.symmetric = symmetric ? 1 : 0;
+    // Held while the two launches are enqueued: later calls on the stream run
+    // after this call's combine has read the summaries.
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    NH_TRY(launch_reduce(data, 1, n, n, red, dev_params, scr, kScratchBytes));
+    return NEURAL_OK;
+}
+
 }  // namespace nh
 
 using namespace nh;
@@ -400,6 +450,12 @@ extern "C" {
 int calibrate_minmax(const double *d, int64_t n, int sym, QuantParams *o) { return calibrate(d, n, sym, o, false); }
 int calibrate_minmax_f32(const float *d, int64_t n, int sym, QuantParams *o) { return calibrate(d, n, sym, o, false); }
 int calibrate_minmax_f32_dev(const float *d, int64_t n, int sym, QuantParams *o) { return calibrate(d, n, sym, o, true); }
+int calibrate_minmax_f32_dev_noalloc(const float *d, int64_t n, int sym, QuantParams *o)
+{
+    if (calibrate_noalloc(d, n, sym, o) != NEURAL_OK) return -1;
+    set_error(NEURAL_OK);
+    return 0;
+}
 
 int quantize_tensor(const double *d, int8_t *o, int64_t n, const QuantParams *p) { return quantize(d, o, n, p, false); }
 int quantize_tensor_f32(const float *d, int8_t *o, int64_t n, const QuantParams *p) { return quantize(d, o, n, p, false); }

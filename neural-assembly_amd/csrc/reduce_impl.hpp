@@ -233,8 +233,13 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_combine(const T *__restrict_
 // or one block per row.  Few long rows: ~4 blocks per CU spread over the rows,
 // each block one contiguous segment of a multiple of 16 KiB, then the
 // one-block-per-row combine.
+//
+// The segment summaries go to the shared workspace (under WsGuard), or to
+// `scratch` (scratch_bytes long) when the caller brings its own buffer; a
+// grid whose summaries do not fit it returns NEURAL_ERR_TENSOR_TOO_LARGE.
 template <typename T, class Red>
-int launch_reduce(const T *x, int64_t rows, int64_t cols, int64_t ld, const Red &red, void *out)
+int launch_reduce(const T *x, int64_t rows, int64_t cols, int64_t ld, const Red &red, void *out,
+                  void *scratch = nullptr, size_t scratch_bytes = 0)
 {
     static_assert(sizeof(typename Red::B) <= 64, "segment summary must fit a 64-byte partial slot");
     if (rows <= 0 || cols <= 0) return NEURAL_OK;
@@ -258,8 +263,11 @@ int launch_reduce(const T *x, int64_t rows, int64_t cols, int64_t ld, const Red 
         }
     }
     if (gx > 1) {
-        WsGuard wg;
-        auto *part = static_cast<typename Red::B *>(workspace().partials);
+        if (scratch && size_t(gx * rows) * sizeof(typename Red::B) > scratch_bytes)
+            return set_error(NEURAL_ERR_TENSOR_TOO_LARGE);
+        std::unique_lock<std::recursive_mutex> wg(workspace_mutex(), std::defer_lock);
+        if (!scratch) wg.lock();
+        auto *part = static_cast<typename Red::B *>(scratch ? scratch : workspace().partials);
         const dim3 grid{unsigned(gx), unsigned(rows), 1u};
         NH_LAUNCH((k_reduce_seg<T, Red>), grid, dim3(kRBlock), 0, stream(), x, cols, ld, chunk, red, part,
                            vec);

@@ -121,6 +121,9 @@ int ensure_init()
                 r.init_rc = NEURAL_ERR_OUT_OF_MEMORY;
                 return set_error(r.init_rc);
             }
+            // A failure here only disables the allocation-free entry point
+            // (it then reports NEURAL_ERR_INVALID_CONFIG); the rest works.
+            if (setup_static_scratch(r.device) != NEURAL_OK) (void)hipGetLastError();
             r.inited = true;
             t_device_set = true;
         }
@@ -128,6 +131,17 @@ int ensure_init()
     if (r.init_rc != NEURAL_OK) return set_error(r.init_rc);
     if (!t_device_set) {
         (void)hipSetDevice(r.device);
+        t_device_set = true;
+    }
+    return NEURAL_OK;
+}
+
+int ensure_ready()
+{
+    Runtime &r = R();
+    if (!r.inited) return set_error(NEURAL_ERR_INVALID_CONFIG);
+    if (!t_device_set) {
+        if (hipSetDevice(r.device) != hipSuccess) return set_error(NEURAL_ERR_INTERNAL);
         t_device_set = true;
     }
     return NEURAL_OK;

@@ -250,6 +250,7 @@ _SIGS = {
     "quantization_error_f32": (_d, [_vp, _i64, _qp]),
     "quantization_snr_f32": (_d, [_vp, _i64, _qp]),
     "calibrate_minmax_f32_dev": (_i, [_vp, _i64, _i, _vp]),
+    "calibrate_minmax_f32_dev_noalloc": (_i, [_vp, _i64, _i, _vp]),
     "quantize_tensor_f32_dev": (_i, [_vp, _vp, _i64, _vp]),
     "dequantize_tensor_f32_dev": (_i, [_vp, _vp, _i64, _vp]),
     # training ops

@@ -234,3 +234,17 @@ def test_header_matches_reference_signatures():
         if not ok:
             bad.append((n, ret, params, ref[n]["restype"], ref[n]["argtypes"]))
     assert not bad, bad
+
+
+def test_noalloc_entry_refuses_before_init(lib):
+    """calibrate_minmax_f32_dev_noalloc never initialises the library (that
+    would allocate): in a process that has not called neural_init it returns
+    -1 with NEURAL_ERR_INVALID_CONFIG, without touching a device."""
+    import subprocess
+    import sys
+    code = ("import ctypes,sys; l=ctypes.CDLL(sys.argv[1]); f=l.calibrate_minmax_f32_dev_noalloc; "
+            "f.argtypes=[ctypes.c_void_p,ctypes.c_int64,ctypes.c_int,ctypes.c_void_p]; "
+            "x=(ctypes.c_float*8)(); p=(ctypes.c_double*5)(); "
+            "print(f(ctypes.addressof(x),8,1,ctypes.addressof(p)), l.neural_get_last_error())")
+    out = subprocess.run([sys.executable, "-c", code, str(LIB)], capture_output=True, text=True, timeout=120)
+    assert out.stdout.split() == ["-1", "10"], (out.stdout, out.stderr)
