@@ -74,6 +74,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline legs")
     ap.add_argument("--no-configs", action="store_true", help="only the cfg2 step")
+    ap.add_argument("--configs", default="cfg1,cfg3,cfg4,cfg5", help="comma-separated configs to run besides cfg2")
     ap.add_argument("--detail", default=None, help="write every per-op figure (JSON) to this file")
     ap.add_argument("--suite", action="store_true", help="also time the other kernel families (detail file)")
     ap.add_argument("--calib", action="store_true",
@@ -412,12 +413,24 @@ def main():
 # ------------------------------------------------------------------------------- configs
 
 def run_configs(torch, pn, lib, clock, dev, args, detail):
-    W = pn.Tensor.from_torch
     out = {}
     cpu_on = not args.no_cpu
-
-    # ---- cfg1: a, b ~ U[-1,1] f32 (seed 0), 64M (headline) and 1M (as specified)
+    want = set(args.configs.split(","))
     g = torch.Generator(device=dev)
+    if "cfg1" in want:
+        _cfg1(torch, pn, lib, clock, dev, g, cpu_on, out, detail)
+    if "cfg3" in want:
+        _cfg3(torch, pn, lib, clock, dev, g, cpu_on, out, detail)
+    if "cfg4" in want:
+        _cfg4(torch, pn, lib, clock, dev, g, cpu_on, out, detail)
+    if "cfg5" in want:
+        _cfg5(torch, pn, lib, clock, dev, g, cpu_on, out, detail)
+    return out
+
+
+def _cfg1(torch, pn, lib, clock, dev, g, cpu_on, out, detail):
+    """cfg1: a, b ~ U[-1,1] f32 (seed 0), 64M (the headline size) and 1M (as specified)."""
+    W = pn.Tensor.from_torch
     g.manual_seed(0)
     a = torch.rand(N1, device=dev, generator=g) * 2 - 1
     bb = torch.rand(N1, device=dev, generator=g) * 2 - 1
@@ -457,7 +470,10 @@ def run_configs(torch, pn, lib, clock, dev, args, detail):
     del a, bb, c, one, one_i
     torch.cuda.empty_cache()
 
-    # ---- cfg3: activations on [64,64,128,128], N(0,4) with 1% at +-30
+
+def _cfg3(torch, pn, lib, clock, dev, g, cpu_on, out, detail):
+    """cfg3: the ten activations on [64,64,128,128], N(0,4) with 1% at +-30."""
+    W = pn.Tensor.from_torch
     g.manual_seed(4)
     x4 = torch.randn(*ACT_SHAPE, device=dev, generator=g, dtype=torch.float64) * 4
     ne = x4.numel()
@@ -488,7 +504,10 @@ def run_configs(torch, pn, lib, clock, dev, args, detail):
     del x4
     torch.cuda.empty_cache()
 
-    # ---- cfg4: int8 quantization of 268M Laplace(0,1) f32, 0.1% outliers at +-50
+
+
+def _cfg4(torch, pn, lib, clock, dev, g, cpu_on, out, detail):
+    """cfg4: int8 quantization of 268M Laplace(0,1) f32, 0.1% outliers at +-50."""
     g.manual_seed(5)
     q_in = torch.empty(NQ, device=dev).exponential_(generator=g)
     q_in *= torch.randint(0, 2, (NQ,), device=dev, generator=g).float() * 2 - 1
@@ -525,7 +544,11 @@ def run_configs(torch, pn, lib, clock, dev, args, detail):
     del q_in, q8, dq, dq64, psym, paff
     torch.cuda.empty_cache()
 
-    # ---- cfg5: NaN/Inf/L2 scan + AdamW over 100M f32 params (f64 moments)
+
+
+def _cfg5(torch, pn, lib, clock, dev, g, cpu_on, out, detail):
+    """cfg5: NaN/Inf/L2 scan + AdamW over 100M f32 params (f64 moments)."""
+    W = pn.Tensor.from_torch
     g.manual_seed(6)
     p = torch.randn(NA, device=dev, generator=g) * 0.02
     gr = torch.randn(NA, device=dev, generator=g) * 1e-3
@@ -554,7 +577,6 @@ def run_configs(torch, pn, lib, clock, dev, args, detail):
         detail["cfg5"]["cpu"] = cpu
     del p, gr, clean, tp, tg, tcl, opt
     torch.cuda.empty_cache()
-    return out
 
 
 def _kc(clock, fn):

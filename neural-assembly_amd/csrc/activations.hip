@@ -125,21 +125,21 @@ NH_DEV double gelu_d(double x)
 // softplus = log(u), u = 1.0 + exp(x) rounded as in the reference.
 NH_DEV double softplus_d(double x) { return log_ge1(1.0 + exp(x)); }
 
-// mish = x * tanh(log u) with tanh(log u) = (u^2 - 1)/(u^2 + 1):
-//   t = u - 1 <= 1:  t(2 + t) / (t(2 + t) + 2)     (t exact: the reference's rounding of u)
-//   t > 1:           1 - 2 / (u^2 + 1)             (u^2 = inf gives 1)
+// mish = x * tanh(log u), u = 1 + e^x, tanh(log u) = (u^2 - 1)/(u^2 + 1), from
+// one exponential s = e^{-|x|} and one division, no branch (a wave holds both
+// signs):
+//   x <= 0:  t = (1 + s) - 1, the reference's rounding of u kept exactly;
+//            g = t(2 + t) / (t(2 + t) + 2)
+//   x > 0:   with t = 1/s:  g = (1 + 2s) / (1 + 2s + 2s^2)  (no overflow for
+//            large x; u's rounding moves g by ~1e-16 here, where g ~ 1)
 NH_DEV double mish_d(double x)
 {
-    const double u = 1.0 + exp(x);
-    const double t = u - 1.0;
-    double g;
-    if (t <= 1.0) {
-        const double a = t * (2.0 + t);
-        g = a / (a + 2.0);
-    } else {
-        g = 1.0 - 2.0 / (u * u + 1.0);
-    }
-    return x * g;
+    const double s = exp(-__builtin_fabs(x));
+    const bool pos = x > 0.0;
+    const double t = (1.0 + s) - 1.0;
+    const double num = pos ? __builtin_fma(2.0, s, 1.0) : t * (2.0 + t);
+    const double den = num + (pos ? 2.0 * (s * s) : 2.0);
+    return x * (num / den);
 }
 
 // ---- f32 outputs ----------------------------------------------------------------
@@ -201,13 +201,17 @@ struct GeluF32 {
     }
 };
 
+// softplus = max(x, 0) + log1p(s), s = e^{-|x|} as one hardware exp2 (as in
+// mish: within ~8e-7 relative for |x| <= 20; for x > 0 the error of s is
+// damped by the + x); no branch.
 struct SoftplusF32 {
     static constexpr bool kHeadTail = true;
     NH_DEV float head(float x, bool &need) const
     {
         need = x < -20.0f;  // 1 + exp(x) keeps < 31 bits of exp(x) in the reference
-        if (x >= 709.78271484375f) return __builtin_inff();  // the reference's double exp overflows
-        return __builtin_fmaxf(x, 0.0f) + log1p_01(expf(-__builtin_fabsf(x)));
+        const float s = __builtin_amdgcn_exp2f(-1.44269504f * __builtin_fabsf(x));
+        const float y = __builtin_fmaxf(x, 0.0f) + log1p_01(s);
+        return x >= 709.78271484375f ? __builtin_inff() : y;  // the reference's double exp overflows there
     }
     NH_DEV float tail(float x) const
     {
@@ -231,13 +235,24 @@ NH_DEV float mish_from_t(float x, float t)
     return x * g;
 }
 
+// The head is the branch-free form of mish_d in float: s = e^{-|x|} as one
+// hardware exp2 (the product |x| log2 e rounds to within 9.5e-7 of the
+// exponent for |x| <= 20, so s and, for x <= 0, g ~ s are within ~8e-7
+// relative; for x > 0, g ~ 1 - 2s^2 hides s's error).  Near 0, g is 0.6
+// to a few float ulps, so x * g rounds like the reference's x * 0.6 except
+// where x * 0.6 lies within g's error of a rounding midpoint: for denormal
+// outputs k ulps long that needs k > 2.8e5 (0.6 k is at least 0.1 ulp from a
+// midpoint), an error below 4e-6 relative.
 struct MishF32 {
     static constexpr bool kHeadTail = true;
     NH_DEV float head(float x, bool &need) const
     {
         need = x < -20.0f;
-        if (__builtin_fabsf(x) < 0x1p-30f) return float(double(x) * 0.6);  // tanh(log 2) = 0.6 in double
-        return mish_from_t(x, expf(x));
+        const float s = __builtin_amdgcn_exp2f(-1.44269504f * __builtin_fabsf(x));
+        const bool pos = x > 0.0f;
+        const float num = pos ? __builtin_fmaf(2.0f, s, 1.0f) : s * (s + 2.0f);
+        const float den = num + (pos ? 2.0f * (s * s) : 2.0f);
+        return x * (num * rcp_f32(den));
     }
     NH_DEV float tail(float x) const { return mish_from_t(x, float((1.0 + exp(double(x))) - 1.0)); }
 };

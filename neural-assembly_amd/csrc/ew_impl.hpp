@@ -109,66 +109,86 @@ __global__ __launch_bounds__(kBlock) void k_map1_flat_scalar(const T *a, T *o, i
 // ---- flat unary f32 with a rare expensive path ------------------------------
 // F supplies head(x, need) -- the cheap evaluation, run for every element,
 // which also says whether the element needs the expensive one -- and
-// tail(x).  Per tile, each wave queues its `need` elements in LDS (ballot +
-// prefix count keeps them in lane/element order), runs tail() over the queue
-// 64 at a time, and reads the results back, so the tail costs one pass per 64
-// queued elements instead of one pass per element position that any lane
+// tail(x).  Per tile each lane keeps a bit mask of its elements that need the
+// tail (no cross-lane work per element).  A wave with any such element counts
+// them with five ballots (an exclusive prefix sum over the lanes via mbcnt),
+// packs them into its LDS queue in (lane, element) order, runs tail() over the
+// queue 64 at a time and puts the results back, so the tail costs one pass per
+// 64 queued elements instead of one pass per element position that any lane
 // needs.  The tile loop is block-uniform; the wave's queue holds a full tile.
-constexpr int kTailUnroll = 2;  // 4 blows past 240 VGPRs (occupancy 1)
+// 16-byte vectors per lane per tile.  Measured on the cfg3 input: 2 (8
+// elements per lane) beats 4, whose twice as many live values and the
+// inlined double tail cut residency (gelu 87 -> 380 us, mish 82 -> 254 us).
+constexpr int kTailUnroll = 2;
+
+// Exclusive prefix sum over the wave of c in [0, 32), and the wave's total,
+// from one ballot per bit of c.
+NH_DEV int wave_excl_prefix_small(int c, int &total)
+{
+    int pre = 0;
+    total = 0;
+#pragma unroll
+    for (int b = 0; b < 5; b++) {
+        const uint64_t m = __ballot((c >> b) & 1);
+        pre += int(__builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u))) << b;
+        total += __popcll(m) << b;
+    }
+    return pre;
+}
 
 template <typename F>
 __global__ __launch_bounds__(kBlock) void k_map1_f32_tail(const float *__restrict__ a, float *__restrict__ o,
                                                           int64_t n, F f)
 {
-    constexpr int kUnroll = kTailUnroll;
-    constexpr int kPerLane = kUnroll * 4;
-    __shared__ float queue[kBlock / 64][64 * kPerLane];
+    constexpr int U = kTailUnroll;
+    constexpr int PL = U * 4;  // elements per lane per tile
+    static_assert(PL < 32, "the per-lane count must fit wave_excl_prefix_small");
+    __shared__ float queue[kBlock / 64][64 * PL];
     float *wq = queue[threadIdx.x >> 6];
     const int lane = threadIdx.x & 63;
-    const uint64_t below = __lanemask_lt();
     const int64_t nv = n / 4;
     const f32x4 *av = reinterpret_cast<const f32x4 *>(a);
     f32x4 *ov = reinterpret_cast<f32x4 *>(o);
-    const int64_t tile = int64_t(kBlock) * kUnroll;
+    const int64_t tile = int64_t(kBlock) * U;
     for (int64_t t0 = int64_t(blockIdx.x) * tile; t0 < nv; t0 += int64_t(gridDim.x) * tile) {
-        f32x4 r[kUnroll];
+        f32x4 x[U], r[U];
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) {
+        for (int u = 0; u < U; u++) {
             const int64_t i = t0 + int64_t(u) * kBlock + threadIdx.x;
-            if (i < nv) r[u] = ld_nt(av + i);
+            x[u] = i < nv ? ld_nt(av + i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
-        int cnt = 0;  // wave-uniform queue length
-        int slot[kPerLane];
+        uint32_t nm = 0;  // bit u*4+k: element k of vector u needs the tail
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) {
+        for (int u = 0; u < U; u++) {
             const bool valid = t0 + int64_t(u) * kBlock + threadIdx.x < nv;
 #pragma unroll
             for (int k = 0; k < 4; k++) {
                 bool need = false;
-                const float x = r[u][k];
-                const float y = valid ? f.head(x, need) : 0.0f;
-                need = need && valid;
-                const uint64_t m = __ballot(need);
-                slot[u * 4 + k] = need ? cnt + __popcll(m & below) : -1;
-                if (need) wq[cnt + __popcll(m & below)] = x;
-                cnt += __popcll(m);
-                r[u][k] = y;
+                r[u][k] = f.head(x[u][k], need);
+                nm |= (need && valid) ? (1u << (u * 4 + k)) : 0u;
             }
         }
-        if (cnt > 0) {
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            for (int j = lane; j < cnt; j += 64) wq[j] = f.tail(wq[j]);
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            __builtin_amdgcn_wave_barrier();
+        if (__ballot(nm != 0u)) {  // wave-uniform
+            int total;
+            int pos = wave_excl_prefix_small(__popc(nm), total);
+            const int first = pos;
 #pragma unroll
-            for (int e = 0; e < kPerLane; e++)
-                if (slot[e] >= 0) r[e / 4][e % 4] = wq[slot[e]];
+            for (int e = 0; e < PL; e++)
+                if ((nm >> e) & 1u) wq[pos++] = x[e / 4][e % 4];
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            for (int j = lane; j < total; j += 64) wq[j] = f.tail(wq[j]);
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            pos = first;
+#pragma unroll
+            for (int e = 0; e < PL; e++)
+                if ((nm >> e) & 1u) r[e / 4][e % 4] = wq[pos++];
             __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
             __builtin_amdgcn_wave_barrier();
         }
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) {
+        for (int u = 0; u < U; u++) {
             const int64_t i = t0 + int64_t(u) * kBlock + threadIdx.x;
             if (i < nv) st_nt(ov + i, r[u]);
         }

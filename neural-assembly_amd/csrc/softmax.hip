@@ -83,15 +83,15 @@ NH_DEV void softmax_row_f32(f32x4 (&v)[VPL], f32x4 *__restrict__ yr, int64_t ncv
             }
         }
         s = wave_dsum(s);
-        const double lse = log(s);
+        // y = (x - m) - lse in float: x - m <= 0 and lse >= 0, so the two
+        // terms never cancel and two float roundings (plus lse's) leave y
+        // within ~2e-7 relative of the double expression; NaN / Inf rows give
+        // the same NaNs as the double form.
+        const float lse = float(log(s));
+        const float mf = float(md);
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
-            if (in_row(k)) {
-                f32x4 o;
-#pragma unroll
-                for (int j = 0; j < 4; j++) o[j] = float((double(v[k][j]) - md) - lse);
-                st_nt(yr + lane + k * 64, o);
-            }
+            if (in_row(k)) st_nt(yr + lane + k * 64, (v[k] - mf) - lse);
         }
     }
 }

@@ -133,3 +133,107 @@ def test_elu_selu_f32_small_negative(pn, ora, name, alpha):
         code = 6 if name == "elu" else 7  # NEURAL_ACT_ELU / NEURAL_ACT_SELU (neural_api.h)
         assert lib.neural_bias_add_act(o2._ptr, tx._ptr, tb._ptr, code, ctypes.c_double(alpha)) == 0
         rel_close(o2.numpy(), want[: x2.size].reshape(x2.shape), 1e-5, 0.0, name + " fused")
+
+
+# ---- cfg3 at its full size ------------------------------------------------------------------
+
+CFG3_SHAPE = (64, 64, 128, 128)
+WIN = 1 << 19
+
+
+def _torch_formula(torch, name, x):
+    """The reference's double formula (activations_c.c:124-158) in torch
+    float64, the operation order kept; used as the full-tensor check of the
+    f32 outputs (REL32), whose 1e-5 bar is far above libm's last-ulp
+    differences."""
+    if name == "tanh":
+        return torch.tanh(x)
+    if name == "gelu":
+        return 0.5 * x * (1.0 + torch.tanh(0.7978845608028654 * (x + 0.044715 * x * x * x)))
+    if name == "leaky_relu":
+        return torch.where(x >= 0, x, 0.01 * x)
+    if name == "elu":
+        return torch.where(x > 0, x, 1.0 * (torch.exp(x) - 1.0))
+    if name == "selu":
+        lam, alp = 1.0507009873554804934193349852946, 1.6732632423543772848170429916717
+        return torch.where(x > 0, lam * x, lam * alp * (torch.exp(x) - 1.0))
+    if name == "swish":
+        return x / (1.0 + torch.exp(-x))
+    if name == "mish":
+        return x * torch.tanh(torch.log(1.0 + torch.exp(x)))
+    if name == "hardswish":
+        return torch.where(x <= -3.0, torch.zeros_like(x), torch.where(x >= 3.0, x, x * (x + 3.0) / 6.0))
+    if name == "softplus":
+        return torch.log(1.0 + torch.exp(x))
+    if name == "hardtanh":
+        return torch.clamp(x, -1.0, 1.0)
+    raise ValueError(name)
+
+
+@pytest.fixture(scope="module")
+def cfg3_input():
+    """BASELINE cfg3: N(0,4) over [64,64,128,128] in double, 1% of the
+    elements (chosen without replacement) set to +-30."""
+    import torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4)
+    x = torch.randn(*CFG3_SHAPE, device="cuda", generator=g, dtype=torch.float64) * 4
+    n = x.numel()
+    sat = torch.randperm(n, device="cuda", generator=g)[: n // 100]
+    x.view(-1)[sat] = 30.0 * (torch.randint(0, 2, (sat.numel(),), device="cuda", generator=g).double() * 2 - 1)
+    torch.cuda.synchronize()
+    yield x
+    del x, sat
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("dt_name", ["f32", "f64"])
+def test_activations_cfg3_full_size(pn, ora, cfg3_input, dt_name):
+    """All ten activations on the full cfg3 tensor (67,108,864 elements,
+    NCHW contiguous).  Windows of 2^19 elements at the start, the middle and
+    the end against the oracle (glibc libm, the reference's formulas):
+    piecewise bit-exact, f32 REL32, f64 REL64.  f32 outputs are also checked
+    over the whole tensor against the double formula evaluated by torch."""
+    import ctypes
+    import torch
+    lib = pn.core._lib
+    dt = torch.float32 if dt_name == "f32" else torch.float64
+    x = cfg3_input.to(dt).contiguous()
+    y = torch.empty_like(x)
+    tx, ty = pn.Tensor.from_torch(x), pn.Tensor.from_torch(y)
+    n = x.numel()
+    starts = [0, n // 2 - WIN // 2 + 3, n - WIN]
+    xf = x.view(-1)
+    xwin = [xf[s:s + WIN].cpu().numpy() for s in starts]
+    assert sum(int((np.abs(w) == 30.0).sum()) for w in xwin) > 10000
+    x64 = x.double() if dt_name == "f32" else None
+    for name in ["tanh", "gelu", "leaky_relu", "elu", "selu", "swish", "mish", "hardswish", "softplus", "hardtanh"]:
+        fn = getattr(lib, "act_" + name)
+        rc = fn(ty._ptr, tx._ptr, ctypes.c_double(ALPHA[name])) if name in ALPHA else fn(ty._ptr, tx._ptr)
+        assert rc == 0, name
+        torch.cuda.synchronize()
+        yf = y.view(-1)
+        for s, xw in zip(starts, xwin):
+            got = yf[s:s + WIN].cpu().numpy()
+            want = ora.act(name, xw, ALPHA.get(name, 0.0))
+            if name in EXACT:
+                same_bits(got, want)
+            elif dt_name == "f32":
+                rel_close(got, want, 1e-5, 0.0, f"{name} window {s}")
+            else:
+                rel_close(got, want, 1e-12, 1e-15, f"{name} window {s}")
+        if dt_name == "f32":
+            ref = _torch_formula(torch, name, x64).float()
+            if name in EXACT:
+                assert torch.equal(y, ref), name
+            else:
+                yd = y.double()
+                rd = ref.double()
+                fin = torch.isfinite(rd)
+                assert torch.equal(torch.isnan(yd), torch.isnan(rd)), name
+                assert torch.equal(yd[~fin & ~torch.isnan(rd)], rd[~fin & ~torch.isnan(rd)]), name
+                err = (yd[fin] - rd[fin]).abs() - 1e-5 * rd[fin].abs()
+                assert float(err.max()) <= 0.0, (name, float(err.max()))
+                del yd, rd, fin, err
+            del ref
+    del x, y, x64

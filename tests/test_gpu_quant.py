@@ -82,6 +82,40 @@ def test_f64_reference_api(pn, ora, rng):
         same_bits(_quant(pn, x, p), ora.quantize(x, want))
 
 
+@pytest.mark.parametrize("n", [1, 3, 4, 255, 256, 257, 1027, 4 * 256 * 4 + 8, (1 << 20) + 5])
+def test_f64_quantize_dequantize_sizes(pn, ora, n):
+    """The double API's kernels regroup a wave's 256 elements through lane
+    shuffles (16-byte accesses contiguous per instruction): every size around
+    a unit (4), a wave (256) and a 4-unit tile, host and device buffers,
+    bit-exact against the oracle."""
+    import torch
+    rng = np.random.default_rng(n)
+    x = rng.laplace(0, 1, n)
+    x[rng.integers(0, n, max(1, n // 100))] = 50.0
+    for sym in (True, False):
+        p = _calib(pn, x, sym)
+        want = ora.calibrate(x, sym)
+        _params_equal(p, want)
+        q = _quant(pn, x, p)
+        same_bits(q, ora.quantize(x, want))
+        d = np.empty(n)
+        assert pn.core._lib.dequantize_tensor(q.ctypes.data, d.ctypes.data, n, ctypes.byref(p)) == 0
+        same_bits(d, ora.dequantize(q, want))
+    # device pointers, an offset of 16 bytes (still 16-byte aligned) so the
+    # wave-contiguous kernels run on a start that is not a multiple of 256
+    xd = torch.from_numpy(np.concatenate([np.zeros(2), x])).cuda()
+    qd = torch.zeros(n + 4, dtype=torch.int8, device="cuda")
+    dd = torch.full((n + 2,), -7.0, dtype=torch.float64, device="cuda")
+    assert pn.core._lib.quantize_tensor(xd.data_ptr() + 16, qd.data_ptr() + 4, n, ctypes.byref(p)) == 0
+    assert pn.core._lib.dequantize_tensor(qd.data_ptr() + 4, dd.data_ptr() + 16, n, ctypes.byref(p)) == 0
+    torch.cuda.synchronize()
+    qh, dh = qd.cpu().numpy(), dd.cpu().numpy()
+    same_bits(qh[4:], ora.quantize(x, want))
+    assert not qh[:4].any()
+    same_bits(dh[2:], ora.dequantize(qh[4:].copy(), want))
+    assert (dh[:2] == -7.0).all()
+
+
 def test_special_values(pn, ora):
     x = np.array([0.3, np.nan, np.inf, -np.inf, 1e30, -1e30, 0.0, -0.0, 2.5, -2.5] * 7, dtype=np.float64)
     for zp in (-1, 0, 5, -128, 127):
