@@ -1,37 +1,34 @@
 """
-Checkpoint save / resume (reference ``pyneural/checkpoint.py``): the NEURCKPT
-binary format, version 3, with versions 1 and 2 still readable.
+Checkpoints in the NEURCKPT container (the reference's
+``pyneural/checkpoint.py``: written as version 3, versions 1 and 2 read).
 
-Layout, little-endian (reference checkpoint.py:4-35):
+Byte layout, little-endian (documented at checkpoint.py:4-35 of the
+reference; kept so that files move between the two implementations):
 
-    "NEURCKPT" | u32 version (3) | u32 num_tensors
-    u32 epoch | f64 best_loss | f64 lr
-    v2+: u8 has_optimizer | u8 opt_type (0 none, 1 sgd, 2 adam, 3 adamw) | u16 0
-         f64 momentum | f64 beta1 | f64 beta2 | f64 epsilon | f64 weight_decay
-    v3:  u64 blob_size | the optimizer's OPTS state blob (hyper-parameters, step
-         count and the float64 moments, optimizers_c.c:391-562)
+    "NEURCKPT" | u32 version | u32 tensor count | u32 epoch | f64 best_loss | f64 lr
+    v2+: u8 has_optimizer | u8 kind (0 none, 1 sgd, 2 adam, 3 adamw) | u16 0
+         f64 x 5: momentum, beta1, beta2, epsilon, weight_decay (zeros where
+         the kind has no such field)
+    v3:  u64 blob length | the OPTS state blob of opt_state_export
+         (optimizers_c.c:391-562: hyper-parameters, step count, f64 moments)
     per tensor: u32 ndim | ndim x u64 shape | u32 dtype (0 f32, 1 f64) | raw data
 
-Parameters and optimizer moments live in HBM here: each parameter comes down
-with one device-to-host copy straight into a write buffer and goes back with
-one host-to-device copy; the moments travel inside the state blob
-(opt_state_export / opt_state_import).  Files are byte-compatible with the
-reference's: the blob layout is the reference's and the tensors are raw
-little-endian IEEE data.
+Here the parameters and the moments live in device memory.  Every tensor
+goes through one host staging buffer that is reused for the whole file (a
+device-to-host copy into it, then one write; on load one read into it, then
+one host-to-device copy), and the moments travel inside the state blob.
 
-``model`` is anything with ``parameters()`` (the reference's Module) or a
-plain sequence of Tensors.
+``model`` is anything with ``parameters()`` or a plain sequence of Tensors.
 """
 
 from __future__ import annotations
 
-import ctypes
 import struct
 from pathlib import Path
 
 import numpy as np
 
-from .core import _lib, NeuralDtype
+from .core import _lib, NeuralDtype, NeuralException
 
 MAGIC = b"NEURCKPT"
 VERSION = 3
@@ -41,211 +38,172 @@ OPT_SGD = 1
 OPT_ADAM = 2
 OPT_ADAMW = 3
 
-_OPT_NAMES = {OPT_SGD: "sgd", OPT_ADAM: "adam", OPT_ADAMW: "adamw"}
+_PREFIX = struct.Struct("<8sIIIdd")  # magic, version, count, epoch, best_loss, lr
+_OPT_HEAD = struct.Struct("<BBH")
+_OPT_FIELDS = ("momentum", "beta1", "beta2", "epsilon", "weight_decay")
+_OPT_VALUES = struct.Struct("<" + "d" * len(_OPT_FIELDS))
+_U64 = struct.Struct("<Q")
+_U32 = struct.Struct("<I")
+
+# optimizer kind <- lower-cased class name, and the payload fields it records
+_KINDS = {
+    "sgd": (OPT_SGD, ("momentum",)),
+    "adam": (OPT_ADAM, ("beta1", "beta2", "epsilon")),
+    "adamw": (OPT_ADAMW, ("beta1", "beta2", "epsilon", "weight_decay")),
+}
+_KIND_NAMES = {code: name for name, (code, _) in _KINDS.items()}
 
 
-def _params(model):
-    if hasattr(model, "parameters"):
-        return list(model.parameters())
-    return list(model)
+def _parameter_list(model) -> list:
+    return list(model.parameters()) if hasattr(model, "parameters") else list(model)
 
 
-def _optimizer_payload(optimizer):
-    """(opt_type, momentum, beta1, beta2, epsilon, weight_decay) keyed on the
-    optimizer's class name, as checkpoint.py:56-76 of the reference."""
-    if optimizer is None:
-        return OPT_NONE, 0.0, 0.0, 0.0, 0.0, 0.0
-    name = optimizer.__class__.__name__.lower()
-    momentum = float(getattr(optimizer, "momentum", 0.0))
-    beta1 = float(getattr(optimizer, "beta1", 0.0))
-    beta2 = float(getattr(optimizer, "beta2", 0.0))
-    epsilon = float(getattr(optimizer, "epsilon", 0.0))
-    weight_decay = float(getattr(optimizer, "weight_decay", 0.0))
-    if name == "sgd":
-        return OPT_SGD, momentum, 0.0, 0.0, 0.0, 0.0
-    if name == "adam":
-        return OPT_ADAM, 0.0, beta1, beta2, epsilon, 0.0
-    if name == "adamw":
-        return OPT_ADAMW, 0.0, beta1, beta2, epsilon, weight_decay
-    return OPT_NONE, 0.0, 0.0, 0.0, 0.0, 0.0
+def _describe_optimizer(optimizer):
+    """(kind code, payload values) for the optimizer object."""
+    entry = _KINDS.get(type(optimizer).__name__.lower()) if optimizer is not None else None
+    if entry is None:
+        return OPT_NONE, (0.0,) * len(_OPT_FIELDS)
+    code, recorded = entry
+    return code, tuple(float(getattr(optimizer, f, 0.0)) if f in recorded else 0.0 for f in _OPT_FIELDS)
 
 
-def _apply_optimizer_payload(optimizer, opt_type, payload) -> None:
-    """Set the hyper-parameter attributes the optimizer object exposes."""
-    if optimizer is None or opt_type == OPT_NONE:
-        return
-    for attr, value in zip(("momentum", "beta1", "beta2", "epsilon", "weight_decay"), payload):
-        if hasattr(optimizer, attr):
-            setattr(optimizer, attr, value)
+class _Staging:
+    """One growable host buffer shared by every tensor of a file."""
+
+    def __init__(self):
+        self._buf = np.empty(0, dtype=np.uint8)
+
+    def view(self, nbytes: int) -> np.ndarray:
+        if self._buf.size < nbytes:
+            self._buf = np.empty(max(nbytes, 2 * self._buf.size), dtype=np.uint8)
+        return self._buf[:nbytes]
 
 
-def _export_state(optimizer):
-    """The optimizer's OPTS blob as a ctypes buffer (empty bytes when there is
-    none); the moments come down from the device inside opt_state_export."""
-    if optimizer is None or not getattr(optimizer, "_ptr", None):
-        return b""
-    nbytes = int(_lib.opt_state_bytes(optimizer._ptr))
-    if nbytes <= 0:
-        return b""
-    buf = (ctypes.c_uint8 * nbytes)()
-    if int(_lib.opt_state_export(optimizer._ptr, ctypes.cast(buf, ctypes.c_void_p), nbytes)) != 0:
-        return b""
-    return buf
+class _Source:
+    """Sequential reads that name what was missing when the file ends early."""
+
+    def __init__(self, f):
+        self._f = f
+
+    def unpack(self, fmt: struct.Struct, what: str) -> tuple:
+        raw = self._f.read(fmt.size)
+        if len(raw) < fmt.size:
+            raise IOError(f"checkpoint truncated in the {what}")
+        return fmt.unpack(raw)
+
+    def fill(self, buf, what: str) -> None:
+        if self._f.readinto(memoryview(buf)) < len(buf):
+            raise IOError(f"checkpoint truncated in the {what}")
 
 
-def _import_state(optimizer, blob) -> None:
-    """Load an OPTS blob into the optimizer handle.  As in the reference
-    (checkpoint.py:108-120), a blob the handle refuses is ignored."""
-    if not blob or optimizer is None or not getattr(optimizer, "_ptr", None):
-        return
-    buf = (ctypes.c_uint8 * len(blob)).from_buffer(blob)
-    _lib.opt_state_import(optimizer._ptr, ctypes.cast(buf, ctypes.c_void_p), len(blob))
-
-
-def _tensor_meta(tensor):
+def _tensor_header(tensor):
     ndim = int(_lib.neural_tensor_ndim(tensor._ptr))
-    shape_ptr = _lib.neural_tensor_shape(tensor._ptr)
-    shape = tuple(int(shape_ptr[i]) for i in range(ndim))
-    dtype = int(_lib.neural_tensor_dtype(tensor._ptr))
-    return ndim, shape, dtype
+    dims = _lib.neural_tensor_shape(tensor._ptr)
+    return tuple(int(dims[k]) for k in range(ndim)), int(_lib.neural_tensor_dtype(tensor._ptr))
 
 
-def _elem_size(dtype: int) -> int:
+def _itemsize(dtype: int) -> int:
     return 4 if dtype == NeuralDtype.FLOAT32 else 8
 
 
-def _write_tensor(f, tensor) -> None:
-    ndim, shape, dtype = _tensor_meta(tensor)
-    f.write(struct.pack("<I", ndim))
-    for s in shape:
-        f.write(struct.pack("<Q", s))
-    f.write(struct.pack("<I", dtype))
-    src = tensor if tensor.is_contiguous else tensor.contiguous()
-    nbytes = int(_lib.neural_tensor_bytes(src._ptr))
-    if nbytes:
-        buf = np.empty(nbytes, dtype=np.uint8)
-        rc = _lib.neural_tensor_download(src._ptr, buf.ctypes.data, nbytes)
-        if rc != 0:
-            raise IOError(f"tensor download failed (error {rc})")
-        f.write(memoryview(buf))
-
-
-def _read_tensor_into(f, tensor) -> None:
-    raw = f.read(4)
-    if len(raw) < 4:
-        raise IOError("Truncated checkpoint: expected ndim")
-    ndim = struct.unpack("<I", raw)[0]
-    shape = []
-    for _ in range(ndim):
-        raw = f.read(8)
-        if len(raw) < 8:
-            raise IOError("Truncated checkpoint: expected shape")
-        shape.append(struct.unpack("<Q", raw)[0])
-    raw = f.read(4)
-    if len(raw) < 4:
-        raise IOError("Truncated checkpoint: expected dtype")
-    dtype = struct.unpack("<I", raw)[0]
-    t_ndim, t_shape, t_dtype = _tensor_meta(tensor)
-    if t_ndim != ndim or t_shape != tuple(shape) or t_dtype != dtype:
-        raise ValueError(
-            f"Checkpoint shape mismatch: file has ({ndim}, {shape}, dtype={dtype}) "
-            f"but model has ({t_ndim}, {t_shape}, dtype={t_dtype})")
-    numel = 1
-    for s in shape:
-        numel *= s
-    total = numel * _elem_size(dtype)
-    if total == 0:
+def _dump_tensor(f, tensor, staging: _Staging) -> None:
+    shape, dtype = _tensor_header(tensor)
+    f.write(_U32.pack(len(shape)) + b"".join(_U64.pack(s) for s in shape) + _U32.pack(dtype))
+    dense = tensor if tensor.is_contiguous else tensor.contiguous()
+    nbytes = int(_lib.neural_tensor_bytes(dense._ptr))
+    if nbytes == 0:
         return
-    buf = np.empty(total, dtype=np.uint8)
-    got = f.readinto(memoryview(buf))
-    if got < total:
-        raise IOError("Truncated checkpoint: expected tensor data")
-    if not tensor.is_contiguous:
-        raise ValueError("checkpoint load needs contiguous parameter tensors")
-    rc = _lib.neural_tensor_upload(tensor._ptr, buf.ctypes.data, total)
+    buf = staging.view(nbytes)
+    rc = _lib.neural_tensor_download(dense._ptr, buf.ctypes.data, nbytes)
     if rc != 0:
-        raise IOError(f"tensor upload failed (error {rc})")
+        raise IOError(f"device-to-host copy of a parameter failed (error {rc})")
+    f.write(memoryview(buf))
+
+
+def _restore_tensor(src: _Source, index: int, tensor, staging: _Staging) -> None:
+    (ndim,) = src.unpack(_U32, "tensor header")
+    shape = tuple(src.unpack(_U64, "tensor shape")[0] for _ in range(ndim))
+    (dtype,) = src.unpack(_U32, "tensor dtype")
+    have_shape, have_dtype = _tensor_header(tensor)
+    if (shape, dtype) != (have_shape, have_dtype):
+        raise ValueError(f"tensor {index}: shape mismatch (file {list(shape)} dtype {dtype}, "
+                         f"model {list(have_shape)} dtype {have_dtype})")
+    nbytes = int(np.prod(shape, dtype=np.int64)) * _itemsize(dtype)
+    if nbytes == 0:
+        return
+    buf = staging.view(nbytes)
+    src.fill(buf, "tensor data")
+    if not tensor.is_contiguous:
+        raise ValueError(f"tensor {index}: loading needs a contiguous parameter")
+    rc = _lib.neural_tensor_upload(tensor._ptr, buf.ctypes.data, nbytes)
+    if rc != 0:
+        raise IOError(f"host-to-device copy of parameter {index} failed (error {rc})")
 
 
 def save_checkpoint(filepath, model, optimizer=None, epoch: int = 0, best_loss: float = float("inf"),
                     lr: float = 0.0) -> None:
-    """Write parameters, training metadata and optimizer state (reference
-    checkpoint.py:196-240)."""
-    params = _params(model)
+    """Write the parameters, the training position and the optimizer state
+    (the interface of the reference's checkpoint.py:196-240)."""
+    params = _parameter_list(model)
+    kind, payload = _describe_optimizer(optimizer)
+    export = getattr(optimizer, "state_bytes", None)
+    blob = export() if (export is not None and getattr(optimizer, "_ptr", None)) else b""
+    staging = _Staging()
     with open(filepath, "wb") as f:
-        f.write(MAGIC)
-        f.write(struct.pack("<I", VERSION))
-        f.write(struct.pack("<I", len(params)))
-        f.write(struct.pack("<I", epoch))
-        f.write(struct.pack("<d", best_loss))
-        f.write(struct.pack("<d", lr))
-        opt_type, momentum, beta1, beta2, epsilon, weight_decay = _optimizer_payload(optimizer)
-        f.write(struct.pack("<BBH", 1 if opt_type != OPT_NONE else 0, opt_type, 0))
-        f.write(struct.pack("<ddddd", momentum, beta1, beta2, epsilon, weight_decay))
-        blob = _export_state(optimizer)
-        f.write(struct.pack("<Q", len(blob)))
-        if len(blob):
-            f.write(memoryview(blob))
+        f.write(_PREFIX.pack(MAGIC, VERSION, len(params), epoch, best_loss, lr))
+        f.write(_OPT_HEAD.pack(int(kind != OPT_NONE), kind, 0) + _OPT_VALUES.pack(*payload))
+        f.write(_U64.pack(len(blob)))
+        f.write(blob)
         for p in params:
-            _write_tensor(f, p)
+            _dump_tensor(f, p, staging)
 
 
 def load_checkpoint(filepath, model, optimizer=None, strict_optimizer: bool = False) -> dict:
-    """Read a v1/v2/v3 checkpoint into existing parameters (and optimizer);
-    returns {'epoch', 'best_loss', 'lr', 'optimizer_type'} (reference
-    checkpoint.py:243-349, same checks and exceptions)."""
-    path = Path(filepath)
-    if not path.exists():
-        raise FileNotFoundError(f"Checkpoint not found: {filepath}")
-    params = _params(model)
+    """Read a version 1, 2 or 3 checkpoint into existing parameters (and the
+    optimizer); returns {'epoch', 'best_loss', 'lr', 'optimizer_type'} (the
+    interface of the reference's checkpoint.py:243-349)."""
+    if not Path(filepath).exists():
+        raise FileNotFoundError(f"no checkpoint at {filepath}")
+    params = _parameter_list(model)
+    staging = _Staging()
     with open(filepath, "rb") as f:
-        magic = f.read(8)
+        src = _Source(f)
+        magic, version, count, epoch, best_loss, lr = src.unpack(_PREFIX, "file header")
         if magic != MAGIC:
-            raise ValueError(f"Invalid checkpoint magic: {magic!r} (expected {MAGIC!r})")
-        ver = struct.unpack("<I", f.read(4))[0]
-        if ver not in (1, 2, VERSION):
-            raise ValueError(f"Unsupported checkpoint version {ver} (expected 1, 2, or {VERSION})")
-        num_tensors = struct.unpack("<I", f.read(4))[0]
-        if num_tensors != len(params):
-            raise ValueError(f"Parameter count mismatch: checkpoint has {num_tensors}, model has {len(params)}")
-        epoch = struct.unpack("<I", f.read(4))[0]
-        best_loss = struct.unpack("<d", f.read(8))[0]
-        lr = struct.unpack("<d", f.read(8))[0]
-
-        optimizer_type = OPT_NONE
-        blob = bytearray()
-        if ver >= 2:
-            hdr = f.read(4)
-            if len(hdr) < 4:
-                raise IOError("Truncated checkpoint: expected optimizer header")
-            has_optimizer, optimizer_type, _ = struct.unpack("<BBH", hdr)
-            vals = f.read(40)
-            if len(vals) < 40:
-                raise IOError("Truncated checkpoint: expected optimizer payload")
-            payload = struct.unpack("<ddddd", vals)
-            if has_optimizer and optimizer is not None:
-                if strict_optimizer:
-                    cls = optimizer.__class__.__name__.lower()
-                    expected = _OPT_NAMES.get(optimizer_type, "unknown")
-                    if expected != "unknown" and cls != expected:
-                        raise ValueError(f"Optimizer type mismatch: checkpoint={expected}, provided={cls}")
-                _apply_optimizer_payload(optimizer, optimizer_type, payload)
-        if ver >= 3:
-            raw = f.read(8)
-            if len(raw) < 8:
-                raise IOError("Truncated checkpoint: expected optimizer state blob size")
-            blob_size = struct.unpack("<Q", raw)[0]
-            if blob_size > 0:
-                blob = bytearray(blob_size)
-                if f.readinto(blob) < blob_size:
-                    raise IOError("Truncated checkpoint: expected optimizer state blob")
-
-        if optimizer is not None and hasattr(optimizer, "lr"):
-            optimizer.lr = lr
-        if optimizer is not None and blob:
-            _import_state(optimizer, blob)
-
-        for p in params:
-            _read_tensor_into(f, p)
-
-    return {"epoch": epoch, "best_loss": best_loss, "lr": lr, "optimizer_type": optimizer_type}
+            raise ValueError(f"not a NEURCKPT file (magic {magic!r})")
+        if version not in (1, 2, VERSION):
+            raise ValueError(f"checkpoint version {version} cannot be read (versions 1 to {VERSION})")
+        if count != len(params):
+            raise ValueError(f"parameter count mismatch: the file holds {count}, the model has {len(params)}")
+        kind = OPT_NONE
+        blob = b""
+        if version >= 2:
+            present, kind, _ = src.unpack(_OPT_HEAD, "optimizer header")
+            payload = src.unpack(_OPT_VALUES, "optimizer payload")
+            if present and optimizer is not None:
+                stored = _KIND_NAMES.get(kind)
+                given = type(optimizer).__name__.lower()
+                if strict_optimizer and stored is not None and stored != given:
+                    raise ValueError(f"Optimizer type mismatch: the checkpoint holds {stored}, got {given}")
+                if kind != OPT_NONE:
+                    for field, value in zip(_OPT_FIELDS, payload):
+                        if hasattr(optimizer, field):
+                            setattr(optimizer, field, value)
+        if version >= 3:
+            (size,) = src.unpack(_U64, "optimizer state blob size")
+            if size:
+                data = bytearray(size)
+                src.fill(data, "optimizer state blob")
+                blob = bytes(data)
+        if optimizer is not None:
+            if hasattr(optimizer, "lr"):
+                optimizer.lr = lr
+            load = getattr(optimizer, "load_state_bytes", None)
+            if blob and load is not None and getattr(optimizer, "_ptr", None):
+                try:
+                    load(blob)
+                except NeuralException:
+                    pass  # a blob the handle refuses is skipped, as the reference does
+        for index, p in enumerate(params):
+            _restore_tensor(src, index, p, staging)
+    return {"epoch": epoch, "best_loss": best_loss, "lr": lr, "optimizer_type": kind}
