@@ -164,6 +164,18 @@ int          result_to_host(void *dst, const void *dev_src, size_t bytes);
 // and a host memcpy, no copy command (measured: 14.9 -> 11.3 us for a
 // launch-and-return round trip).
 int          host_result_fetch(void *dst, size_t bytes);
+// Ticketed variant: the storing kernel also writes a 64-bit ticket into the
+// last 8 bytes of the host area (after a system-scope fence), and the host
+// spins on it instead of synchronising the stream, then copies `bytes` (<=
+// 248) of the result.  A ticket that has not shown after ~2 s falls back to a
+// stream synchronisation (which reports any fault).  next_ticket() gives the
+// slot and a fresh value; callers hold WsGuard.
+struct Ticket {
+    unsigned long long *slot = nullptr;  // device address of the host word; null: no ticket
+    unsigned long long value = 0;
+};
+Ticket       next_ticket();
+int          host_result_wait(unsigned long long ticket, void *dst, size_t bytes);
 
 }  // namespace nh
 

@@ -414,9 +414,11 @@ static int calibrate(const T *data, int64_t n, int symmetric, QuantParams *out, 
     RedMinMax<T> red;
     red.symmetric = symmetric ? 1 : 0;
     WsGuard wg;
-    void *res = out_on_device ? static_cast<void *>(out) : workspace().host_result_dev;
-    if (launch_reduce_full(static_cast<const T *>(s.dev), n, red, res) != NEURAL_OK) return -1;
-    if (!out_on_device && host_result_fetch(out, sizeof(QuantParams)) != NEURAL_OK) return -1;
+    if (out_on_device) {
+        if (launch_reduce_full(static_cast<const T *>(s.dev), n, red, out) != NEURAL_OK) return -1;
+    } else if (reduce_full_to_host(static_cast<const T *>(s.dev), n, red, out, sizeof(QuantParams)) != NEURAL_OK) {
+        return -1;
+    }
     if (s.finish(false) != NEURAL_OK) return -1;
     set_error(NEURAL_OK);
     return 0;
@@ -468,8 +470,7 @@ static int qerr(const T *data, int64_t n, const QuantParams *p, double *sig, dou
     red.zp = p->zero_point;
     WsGuard wg;
     QErrOut st;
-    if (launch_reduce_full(static_cast<const T *>(s.dev), n, red, workspace().host_result_dev) != NEURAL_OK) return -1;
-    if (host_result_fetch(&st, sizeof(st)) != NEURAL_OK) return -1;
+    if (reduce_full_to_host(static_cast<const T *>(s.dev), n, red, &st, sizeof(st)) != NEURAL_OK) return -1;
     if (s.finish(false) != NEURAL_OK) return -1;
     *sig = st.sig;
     *noise = st.noise;

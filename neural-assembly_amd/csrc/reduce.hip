@@ -218,12 +218,9 @@ static int full_to_host(const NeuralTensor *t, Out *host_out)
     Contig c;
     NH_TRY(c.open(t));
     WsGuard wg;
-    void *res = workspace().host_result_dev;
     if (t->dtype == NEURAL_DTYPE_FLOAT32)
-        NH_TRY(launch_reduce_full(static_cast<const float *>(c.p), n, RedOf<float>{}, res));
-    else
-        NH_TRY(launch_reduce_full(static_cast<const double *>(c.p), n, RedOf<double>{}, res));
-    return host_result_fetch(host_out, sizeof(Out));
+        return reduce_full_to_host(static_cast<const float *>(c.p), n, RedOf<float>{}, host_out, sizeof(Out));
+    return reduce_full_to_host(static_cast<const double *>(c.p), n, RedOf<double>{}, host_out, sizeof(Out));
 }
 
 template <typename T> using SumF64 = RedSum<T, SUM_OUT_F64>;
@@ -398,11 +395,10 @@ float simd_sum_f32(const float *a, uint64_t n)
     Staged sa;
     if (sa.open(a, size_t(n) * 4, true) != NEURAL_OK) return 0.0f;
     WsGuard wg;
-    void *res = workspace().host_result_dev;
     double s = 0.0;
-    if (launch_reduce_full(static_cast<const float *>(sa.dev), int64_t(n), SumF64<float>{}, res) != NEURAL_OK)
+    if (reduce_full_to_host(static_cast<const float *>(sa.dev), int64_t(n), SumF64<float>{}, &s, sizeof(s)) !=
+        NEURAL_OK)
         return 0.0f;
-    if (host_result_fetch(&s, sizeof(s)) != NEURAL_OK) return 0.0f;
     set_error(NEURAL_OK);
     return float(s);
 }

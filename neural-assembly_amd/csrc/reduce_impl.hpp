@@ -184,10 +184,21 @@ NH_DEV typename Red::B ordered_combine(const Red &red, const typename Red::B *p,
 
 // ---- kernels --------------------------------------------------------------------------------
 
+// A result that only the host reads is stored into coherent host memory; the
+// storing lane then writes the ticket after a system-scope fence, so a host
+// that sees the ticket sees the result (host_result_wait).
+NH_DEV void publish(const Ticket &tk)
+{
+    if (tk.slot) {
+        __threadfence_system();
+        __hip_atomic_store(tk.slot, tk.value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
 // One group (wave or block) per row; RPB = 256 / TPR rows per block.
 template <typename T, class Red, int TPR>
 __global__ __launch_bounds__(kRBlock) void k_reduce_rows(const T *__restrict__ x, int64_t rows, int64_t cols,
-                                                         int64_t ld, Red red, void *out, bool vec)
+                                                         int64_t ld, Red red, void *out, bool vec, Ticket tk)
 {
     constexpr int RPB = kRBlock / TPR;
     const int64_t r = int64_t(blockIdx.x) * RPB + threadIdx.x / TPR;
@@ -197,7 +208,10 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_rows(const T *__restrict__ x
     // reductions of its result, then other streams) this measured faster for
     // the whole sequence than non-temporal ones
     const typename Red::B b = seg_reduce<T, Red, TPR, false>(red, xr, 0, cols, vec);
-    if (Grp<TPR>::lane() == 0) red.store(out, r, b, xr, cols);
+    if (Grp<TPR>::lane() == 0) {
+        red.store(out, r, b, xr, cols);
+        publish(tk);  // tickets are used with a single row only
+    }
 }
 
 // gridDim.x blocks per row (blockIdx.y = row), each reducing one contiguous
@@ -219,11 +233,14 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_seg(const T *__restrict__ x,
 template <typename T, class Red>
 __global__ __launch_bounds__(kRBlock) void k_reduce_combine(const T *__restrict__ x, int64_t cols, int64_t ld,
                                                             int gx, Red red, const typename Red::B *partials,
-                                                            void *out)
+                                                            void *out, Ticket tk)
 {
     const int64_t r = blockIdx.x;
     const typename Red::B tot = ordered_combine(red, partials + r * gx, gx);
-    if (threadIdx.x == 0) red.store(out, r, tot, x + r * ld, cols);
+    if (threadIdx.x == 0) {
+        red.store(out, r, tot, x + r * ld, cols);
+        publish(tk);  // tickets are used with a single row only
+    }
 }
 
 // ---- launch policy --------------------------------------------------------------------------
@@ -239,8 +256,9 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_combine(const T *__restrict_
 // grid whose summaries do not fit it returns NEURAL_ERR_TENSOR_TOO_LARGE.
 template <typename T, class Red>
 int launch_reduce(const T *x, int64_t rows, int64_t cols, int64_t ld, const Red &red, void *out,
-                  void *scratch = nullptr, size_t scratch_bytes = 0)
+                  void *scratch = nullptr, size_t scratch_bytes = 0, Ticket tk = Ticket{})
 {
+    if (tk.slot && rows != 1) return set_error(NEURAL_ERR_INTERNAL);
     static_assert(sizeof(typename Red::B) <= 64, "segment summary must fit a 64-byte partial slot");
     if (rows <= 0 || cols <= 0) return NEURAL_OK;
     constexpr int VN = Vec16<T>::n;
@@ -272,14 +290,14 @@ int launch_reduce(const T *x, int64_t rows, int64_t cols, int64_t ld, const Red 
         NH_LAUNCH((k_reduce_seg<T, Red>), grid, dim3(kRBlock), 0, stream(), x, cols, ld, chunk, red, part,
                            vec);
         NH_LAUNCH((k_reduce_combine<T, Red>), dim3(unsigned(rows)), dim3(kRBlock), 0, stream(), x, cols, ld,
-                           int(gx), red, part, out);
+                           int(gx), red, part, out, tk);
     } else if (cols <= 2048) {
         const unsigned g = unsigned(ceil_div(rows, kRBlock / 64));
         NH_LAUNCH((k_reduce_rows<T, Red, 64>), dim3(g), dim3(kRBlock), 0, stream(), x, rows, cols, ld, red,
-                           out, vec);
+                           out, vec, tk);
     } else {
         NH_LAUNCH((k_reduce_rows<T, Red, kRBlock>), dim3(unsigned(rows)), dim3(kRBlock), 0, stream(), x,
-                           rows, cols, ld, red, out, vec);
+                           rows, cols, ld, red, out, vec, tk);
     }
     return check_launch();
 }
@@ -289,6 +307,17 @@ template <typename T, class Red>
 int launch_reduce_full(const T *x, int64_t n, const Red &red, void *out)
 {
     return launch_reduce(x, 1, n, n, red, out);
+}
+
+// Whole contiguous array reduced into workspace().host_result, then the
+// result copied to dst (bytes <= 248) once the storing kernel's ticket shows
+// in host memory.  The caller holds WsGuard.
+template <typename T, class Red>
+int reduce_full_to_host(const T *x, int64_t n, const Red &red, void *dst, size_t bytes)
+{
+    const Ticket tk = next_ticket();
+    NH_TRY(launch_reduce(x, 1, n, n, red, workspace().host_result_dev, nullptr, 0, tk));
+    return host_result_wait(tk.value, dst, bytes);
 }
 
 // ---- shared reducers ---------------------------------------------------------------------

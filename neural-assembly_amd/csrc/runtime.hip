@@ -224,6 +224,44 @@ int host_result_fetch(void *dst, size_t bytes)
     return NEURAL_OK;
 }
 
+namespace {
+constexpr size_t kTicketOffset = 248;  // last 8 bytes of the 256-byte host result area
+unsigned long long g_ticket = 0;       // last ticket handed out (under WsGuard)
+}  // namespace
+
+Ticket next_ticket()
+{
+    Ticket t;
+    t.slot = reinterpret_cast<unsigned long long *>(static_cast<char *>(workspace().host_result_dev) + kTicketOffset);
+    t.value = ++g_ticket;
+    return t;
+}
+
+int host_result_wait(unsigned long long ticket, void *dst, size_t bytes)
+{
+    if (bytes > kTicketOffset) return set_error(NEURAL_ERR_INTERNAL);
+    const char *area = static_cast<const char *>(workspace().host_result);
+    const volatile unsigned long long *word =
+        reinterpret_cast<const volatile unsigned long long *>(area + kTicketOffset);
+    // Spin on the ticket for a while (a kernel that ends normally stores it
+    // within microseconds of finishing), then fall back to the stream wait,
+    // which also surfaces a fault.
+    bool seen = false;
+    for (long spins = 0; spins < (1L << 26); spins++) {
+        if (__atomic_load_n(word, __ATOMIC_ACQUIRE) == ticket) {
+            seen = true;
+            break;
+        }
+        __builtin_ia32_pause();
+    }
+    if (!seen) {
+        NH_TRY(sync());
+        if (__atomic_load_n(word, __ATOMIC_ACQUIRE) != ticket) return set_error(NEURAL_ERR_INTERNAL);
+    }
+    std::memcpy(dst, area, bytes);
+    return NEURAL_OK;
+}
+
 int result_to_host(void *dst, const void *dev_src, size_t bytes)
 {
     WsGuard wg;

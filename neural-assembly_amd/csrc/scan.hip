@@ -48,8 +48,7 @@ template <typename T>
 static int scan_dev(const T *x, int64_t n, ScanOut *st)
 {
     WsGuard wg;
-    NH_TRY(launch_reduce_full(x, n, RedScan<T>{}, workspace().host_result_dev));
-    return host_result_fetch(st, sizeof(*st));
+    return reduce_full_to_host(x, n, RedScan<T>{}, st, sizeof(*st));
 }
 
 static int scan_raw(const float *data, uint64_t n, ScanOut *st)
