@@ -83,15 +83,19 @@ def parse():
 
 
 def traffic_from_profile():
-    """HBM bytes per log-softmax launch from the committed rocprofv3 --pmc
-    summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration)."""
+    """HBM bytes per launch ("<config>.<op>" -> bytes) from the committed
+    rocprofv3 --pmc summary profiles/bench_pmc_traffic.txt (FETCH_SIZE +
+    WRITE_SIZE, scaled by a 256 MiB copy measured in the same runs)."""
     p = ROOT / "profiles" / "bench_pmc_traffic.json"
     if not p.exists():
-        return None
+        return {}
     try:
         return {k: float(v) for k, v in json.loads(p.read_text())["traffic_bytes_per_launch"].items()}
     except Exception:
-        return None
+        return {}
+
+
+TRAFFIC = traffic_from_profile()
 
 
 class TimingEvent:
@@ -214,7 +218,7 @@ class Config:
             "ops": {k: [o["kernel_us"], o["pct_hbm"]] for k, o in self.ops.items()},
             "GBps": round(self.aggregate_gbs(), 1),
             "roofline": {"kernel": dom, "us": d["kernel_us"], "bytes": d["bytes"], "achieved": d["GB/s"],
-                         "frac": round(d["GB/s"] / HBM_PEAK_GBS, 4)},
+                         "frac": round(d["GB/s"] / HBM_PEAK_GBS, 4), "traffic": TRAFFIC.get(f"{self.name}.{dom}")},
         }
         if cpu:
             c = {"GBps": cpu["value"], "kind": cpu["kind"], "cores": cpu["cores"]}
@@ -340,7 +344,6 @@ def main():
     detail["cfg2_step"] = cfg2.detail()
     dom = max(cfg2.ops, key=lambda k: cfg2.ops[k]["kernel_us"])
     d = cfg2.ops[dom]
-    traffic = traffic_from_profile()
 
     cpu2 = None
     if not args.no_cpu:
@@ -374,7 +377,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(d["GB/s"] / HBM_PEAK_GBS, 4),
-            "traffic": (traffic or {}).get(dom),
+            "traffic": TRAFFIC.get(f"cfg2.{dom}"),
             "avg_launch_us": d["kernel_us"],
             "algorithmic_bytes": d["bytes"],
             "min_frac_in_step": round(min(o["GB/s"] for o in cfg2.ops.values()) / HBM_PEAK_GBS, 4),

@@ -34,42 +34,6 @@ namespace nh {
 constexpr double kGelu = 0.7978845608028654;
 constexpr double kSeluL = 1.0507009873554804934193349852946;
 constexpr double kSeluA = 1.6732632423543772848170429916717;
-// ln 2 split so that k * kLn2Hi is exact for |k| < 2^20 (32 significant bits).
-constexpr double kLn2Hi = 0x1.62e42fee00000p-1;
-constexpr double kLn2Lo = 0x1.a39ef35793c76p-33;
-constexpr double kSqrtHalf = 0x1.6a09e667f3bcdp-1;
-
-// Natural log of u >= 1 (also +inf and NaN, returned unchanged) to about
-// 3 ulp: u = m * 2^k with m in [sqrt(1/2), sqrt(2)), log m = 2 atanh(s),
-// s = (m - 1) / (m + 1), |s| <= 0.1716, atanh by its odd power series through
-// s^19 (truncation below 2.4e-17 relative).
-NH_DEV double log_ge1(double u)
-{
-    int k;
-    double m = frexp(u, &k);
-    if (m < kSqrtHalf) {
-        m += m;
-        k -= 1;
-    }
-    const double f = m - 1.0;  // exact (Sterbenz)
-    const double s = f / (m + 1.0);
-    const double s2 = s * s;
-    double q = 1.0 / 19.0;
-    q = __builtin_fma(q, s2, 1.0 / 17.0);
-    q = __builtin_fma(q, s2, 1.0 / 15.0);
-    q = __builtin_fma(q, s2, 1.0 / 13.0);
-    q = __builtin_fma(q, s2, 1.0 / 11.0);
-    q = __builtin_fma(q, s2, 1.0 / 9.0);
-    q = __builtin_fma(q, s2, 1.0 / 7.0);
-    q = __builtin_fma(q, s2, 1.0 / 5.0);
-    q = __builtin_fma(q, s2, 1.0 / 3.0);
-    const double s_2 = s + s;
-    const double lm = __builtin_fma(s_2 * s2, q, s_2);  // 2s (1 + s^2/3 + s^4/5 + ...)
-    const double dk = double(k);
-    const double r = __builtin_fma(dk, kLn2Hi, __builtin_fma(dk, kLn2Lo, lm));
-    return (u < __builtin_inf()) ? r : u;
-}
-
 // tanh(x) = (E - 1) / (E + 1), E = exp(2|x|), with |x| clamped to 22 (where
 // the double result is already +-1); |x| < 2^-7 uses the Taylor series through
 // x^7 (truncation below 3e-19 relative; zeros keep their sign, denormals are
@@ -107,9 +71,13 @@ NH_DEV double rcp_1_2(double d)
 // Both sides share one reciprocal and no branch: a wave holds both signs.
 // An ulp of error in eps matters to rint only where eps * 2^53 is large, i.e.
 // where one multiple of 2^-53 is far below 1e-12 of the result.
+// The exponent is clamped at -40 (w >= 4.2e-18): beyond it the result is
+// already exactly 2 (z > 0) or 0 (z < 0, eps * 2^53 < 0.08 rounds to 0), and
+// cfg3's +-30 inputs (z = +-987) would otherwise drive exp into underflow.
 NH_DEV double one_plus_tanh(double z)
 {
-    const double w = exp(-2.0 * __builtin_fabs(z));
+    const double a = -2.0 * __builtin_fabs(z);
+    const double w = exp(a > -40.0 ? a : -40.0);
     const double r = rcp_1_2(1.0 + w);
     const double eps = (w + w) * r;
     const double q = eps < 0.5 ? __builtin_rint(eps * 0x1p53) * 0x1p-53 : eps;
