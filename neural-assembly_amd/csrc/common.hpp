@@ -255,6 +255,42 @@ NH_DEV float exp_d2f(double y)
     return __builtin_ldexpf(__builtin_amdgcn_exp2f(float(t - n)), int(n));
 }
 
+// ln 2 split so that k * kLn2Hi is exact for |k| < 2^20 (32 significant bits).
+constexpr double kLn2Hi = 0x1.62e42fee00000p-1;
+constexpr double kLn2Lo = 0x1.a39ef35793c76p-33;
+constexpr double kSqrtHalf = 0x1.6a09e667f3bcdp-1;
+
+// Natural log of u >= 1 (also +inf and NaN, returned unchanged) to about
+// 3 ulp: u = m * 2^k with m in [sqrt(1/2), sqrt(2)), log m = 2 atanh(s),
+// s = (m - 1) / (m + 1), |s| <= 0.1716, atanh by its odd power series through
+// s^19 (truncation below 2.4e-17 relative).
+NH_DEV double log_ge1(double u)
+{
+    int k;
+    double m = frexp(u, &k);
+    if (m < kSqrtHalf) {
+        m += m;
+        k -= 1;
+    }
+    const double f = m - 1.0;  // exact (Sterbenz)
+    const double s = f / (m + 1.0);
+    const double s2 = s * s;
+    double q = 1.0 / 19.0;
+    q = __builtin_fma(q, s2, 1.0 / 17.0);
+    q = __builtin_fma(q, s2, 1.0 / 15.0);
+    q = __builtin_fma(q, s2, 1.0 / 13.0);
+    q = __builtin_fma(q, s2, 1.0 / 11.0);
+    q = __builtin_fma(q, s2, 1.0 / 9.0);
+    q = __builtin_fma(q, s2, 1.0 / 7.0);
+    q = __builtin_fma(q, s2, 1.0 / 5.0);
+    q = __builtin_fma(q, s2, 1.0 / 3.0);
+    const double s_2 = s + s;
+    const double lm = __builtin_fma(s_2 * s2, q, s_2);  // 2s (1 + s^2/3 + s^4/5 + ...)
+    const double dk = double(k);
+    const double r = __builtin_fma(dk, kLn2Hi, __builtin_fma(dk, kLn2Lo, lm));
+    return (u < __builtin_inf()) ? r : u;
+}
+
 // 128-bit vector types (clang ext vectors: element access by index, and
 // accepted by the non-temporal load/store builtins).
 typedef float f32x4 __attribute__((ext_vector_type(4)));

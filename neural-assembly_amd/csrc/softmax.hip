@@ -87,7 +87,7 @@ NH_DEV void softmax_row_f32(f32x4 (&v)[VPL], f32x4 *__restrict__ yr, int64_t ncv
         // terms never cancel and two float roundings (plus lse's) leave y
         // within ~2e-7 relative of the double expression; NaN / Inf rows give
         // the same NaNs as the double form.
-        const float lse = float(log(s));
+        const float lse = float(log_ge1(s));  // s >= 1: the row maximum contributes exp(0) = 1
         const float mf = float(md);
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
@@ -163,7 +163,7 @@ __global__ __launch_bounds__(kSmBlock) void k_softmax_wave_f64(const double *__r
         }
     }
     s = wave_sum(s);
-    const double lse = LOG ? log(s) : 0.0;
+    const double lse = LOG ? log_ge1(s) : 0.0;  // s >= 1 (the maximum contributes 1)
 #pragma unroll
     for (int k = 0; k < VPL; k++) {
         const int64_t c = lane + int64_t(k) * 64;
