@@ -66,8 +66,9 @@ NH_DEV double rcp_1_2(double d)
 // 1 + tanh(z) as the reference's double tanh leaves it, from w = exp(-2|z|):
 //   z >= 0:  1 + (1 - w)/(1 + w) = 2/(1 + w)                     (no cancellation)
 //   z < 0:   eps = 1 - |tanh z| = 2w/(1 + w); while tanh z is in [-1, -0.5]
-//            it is a multiple of 2^-53, so 1 + tanh z = rint(eps * 2^53) * 2^-53
-//            (round-half-even on the multiple = round-half-even on tanh z).
+//            it is a multiple of 2^-53, so 1 + tanh z is eps rounded to a
+//            multiple of 2^-53 (round-half-even on the multiple =
+//            round-half-even on tanh z).
 // Both sides share one reciprocal and no branch: a wave holds both signs.
 // An ulp of error in eps matters to rint only where eps * 2^53 is large, i.e.
 // where one multiple of 2^-53 is far below 1e-12 of the result.
@@ -80,7 +81,9 @@ NH_DEV double one_plus_tanh(double z)
     const double w = exp(a > -40.0 ? a : -40.0);
     const double r = rcp_1_2(1.0 + w);
     const double eps = (w + w) * r;
-    const double q = eps < 0.5 ? __builtin_rint(eps * 0x1p53) * 0x1p-53 : eps;
+    // eps rounded to a multiple of 2^-53, ties to even: 0.5 + eps (in [0.5, 1),
+    // ulp 2^-53) rounds exactly so, and subtracting 0.5 is exact
+    const double q = eps < 0.5 ? (eps + 0.5) - 0.5 : eps;
     return z >= 0.0 ? r + r : q;
 }
 

@@ -16,11 +16,14 @@
 // passes read only those copies.  A one-block step after each pass picks the
 // byte on the device, so the host waits once per call.
 // Equal keys are equal doubles except for the zero key: the reference's qsort
-// (glibc's merge sort, which is stable) keeps equal elements in input order,
-// so a selected zero takes the sign of the j-th zero of the input, j the
-// rank's position among the zeros; two more launches find it (zero counts per
-// chunk, then one wave walks the chunk that holds it).  The parameter
-// arithmetic then runs on the host in the reference's expressions.
+// (glibc's merge sort, stable while its n * 8-byte copy fits in about a
+// quarter of physical memory) keeps equal elements in input order, so a
+// selected zero takes the sign of the j-th zero of the input, j the rank's
+// position among the zeros; two more launches find it (zero counts per chunk,
+// then one wave walks the chunk that holds it).  Beyond that size glibc falls
+// back to an unstable in-place sort and the reference's zero sign no longer
+// follows input order.  The parameter arithmetic then runs on the host in the
+// reference's expressions.
 //
 // Divergences (the reference's behaviour is undefined there): a NaN
 // percentile returns -1 (the reference indexes out of bounds); NaN data sort

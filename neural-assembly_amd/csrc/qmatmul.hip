@@ -39,18 +39,20 @@ constexpr int kQPad = 5;     // LDS row stride in 8-byte words (4 used): spreads
 __global__ __launch_bounds__(256) void k_qpad_a(const int8_t *__restrict__ A, int8_t *__restrict__ Ap, int64_t M,
                                                 int64_t K, int64_t Kp, int64_t units)
 {
-    const int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    const int64_t i = t / units, u = t - i * units;
-    if (i >= M) return;  // rows M .. Mp - 1 of Ap were zeroed by the caller
-    int8_t b[16];
+    // grid-stride over the M * units 16-byte units of the real rows (rows
+    // M .. Mp - 1 of Ap were zeroed by the caller)
+    for (int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x; t < M * units; t += int64_t(gridDim.x) * 256) {
+        const int64_t i = t / units, u = t - i * units;
+        int8_t b[16];
 #pragma unroll
-    for (int q = 0; q < 16; q++) {
-        const int64_t k = 16 * u + q;
-        b[q] = k < K ? A[i * K + k] : int8_t(0);
+        for (int q = 0; q < 16; q++) {
+            const int64_t k = 16 * u + q;
+            b[q] = k < K ? A[i * K + k] : int8_t(0);
+        }
+        int4 v;
+        __builtin_memcpy(&v, b, 16);
+        *reinterpret_cast<int4 *>(Ap + i * Kp + 16 * u) = v;
     }
-    int4 v;
-    __builtin_memcpy(&v, b, 16);
-    *reinterpret_cast<int4 *>(Ap + i * Kp + 16 * u) = v;
 }
 
 // Sum of the four signed bytes of w.
@@ -83,20 +85,22 @@ __global__ __launch_bounds__(256) void k_qpad_bt(const int8_t *__restrict__ B, i
                                                  int32_t *__restrict__ colB, int64_t K, int64_t N, int64_t Kp)
 {
     const int64_t j = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    const int64_t u = blockIdx.y;
     if (j >= N) return;
-    int8_t b[16];
-    int32_t s = 0;
+    // 16-byte K units blockIdx.y, blockIdx.y + gridDim.y, ... (gridDim.y <= 65535)
+    for (int64_t u = blockIdx.y; u < Kp / 16; u += gridDim.y) {
+        int8_t b[16];
+        int32_t s = 0;
 #pragma unroll
-    for (int q = 0; q < 16; q++) {
-        const int64_t k = 16 * u + q;
-        b[q] = k < K ? B[k * N + j] : int8_t(0);
-        s += b[q];
+        for (int q = 0; q < 16; q++) {
+            const int64_t k = 16 * u + q;
+            b[q] = k < K ? B[k * N + j] : int8_t(0);
+            s += b[q];
+        }
+        int4 v;
+        __builtin_memcpy(&v, b, 16);
+        *reinterpret_cast<int4 *>(Bt + j * Kp + 16 * u) = v;
+        atomicAdd(colB + j, s);
     }
-    int4 v;
-    __builtin_memcpy(&v, b, 16);
-    *reinterpret_cast<int4 *>(Bt + j * Kp + 16 * u) = v;
-    atomicAdd(colB + j, s);
 }
 
 __global__ __launch_bounds__(256) void k_qgemm(const int8_t *__restrict__ Ap, const int8_t *__restrict__ Bt,
@@ -176,8 +180,9 @@ static int qmatmul(const int8_t *A, const int8_t *B, double *C, int64_t M, int64
     if (M <= 0 || K <= 0 || N <= 0) return -1;
     if (ensure_init() != NEURAL_OK) return -1;
     const int64_t Mp = round_up(M, kQT), Np = round_up(N, kQT), Kp = round_up(K, kQK);
-    // grid limits: row tiles in y of the product, 16-byte K units in y of the B pass
-    if (Mp / kQT > 65535 || Kp / 16 > 65535) {
+    // grid limit: the product's row tiles run in grid y (M <= 65535 * 128 =
+    // 8,388,480; the reference has no such limit)
+    if (Mp / kQT > 65535) {
         set_error(NEURAL_ERR_TENSOR_TOO_LARGE);
         return -1;
     }
@@ -194,16 +199,24 @@ static int qmatmul(const int8_t *A, const int8_t *B, double *C, int64_t M, int64
     int8_t *Ap = reinterpret_cast<int8_t *>(blk), *Bt = Ap + bytesA;
     int32_t *rowA = reinterpret_cast<int32_t *>(Bt + bytesB), *colB = rowA + Mp;
     int rc = NEURAL_OK;
-    // the padding rows and the sums start at zero (the copies write only real rows)
-    if (hipMemsetAsync(blk, 0, bytesA + bytesB + size_t(Mp + Np) * sizeof(int32_t), stream()) != hipSuccess)
+    // Only the padding rows (A rows M .. Mp-1, Bt rows N .. Np-1) and the
+    // row / column sums start at zero: the copies write every byte of the
+    // real rows, K padding included.
+    const size_t padA = size_t((Mp - M) * Kp), padB = size_t((Np - N) * Kp);
+    if ((padA && hipMemsetAsync(Ap + M * Kp, 0, padA, stream()) != hipSuccess) ||
+        (padB && hipMemsetAsync(Bt + N * Kp, 0, padB, stream()) != hipSuccess) ||
+        hipMemsetAsync(rowA, 0, size_t(Mp + Np) * sizeof(int32_t), stream()) != hipSuccess)
         rc = NEURAL_ERR_INTERNAL;
     const int64_t units = Kp / 16;
     if (rc == NEURAL_OK) {
-        NH_LAUNCH(k_qpad_a, dim3(unsigned(ceil_div(M * units, 256))), dim3(256), 0, stream(),
-                           static_cast<const int8_t *>(sa.dev), Ap, M, K, Kp, units);
+        int64_t ga = ceil_div(M * units, 256);
+        ga = ga > kMaxGridBlocks ? kMaxGridBlocks : ga;
+        NH_LAUNCH(k_qpad_a, dim3(unsigned(ga)), dim3(256), 0, stream(), static_cast<const int8_t *>(sa.dev), Ap, M,
+                  K, Kp, units);
         NH_LAUNCH(k_qrowsum, dim3(unsigned(ceil_div(M, 4))), dim3(256), 0, stream(), Ap, rowA, M, Kp);
-        NH_LAUNCH(k_qpad_bt, dim3(unsigned(ceil_div(N, 256)), unsigned(units)), dim3(256), 0, stream(),
-                           static_cast<const int8_t *>(sb.dev), Bt, colB, K, N, Kp);
+        const unsigned gy = unsigned(units < 65535 ? units : 65535);
+        NH_LAUNCH(k_qpad_bt, dim3(unsigned(ceil_div(N, 256)), gy), dim3(256), 0, stream(),
+                  static_cast<const int8_t *>(sb.dev), Bt, colB, K, N, Kp);
         const double cs = pa->scale * pb->scale;  // combined_scale, quantize.c:198
         NH_LAUNCH(k_qgemm, dim3(unsigned(Np / kQT), unsigned(Mp / kQT)), dim3(256), 0, stream(), Ap, Bt,
                            static_cast<double *>(sc.dev), rowA, colB, M, N, K, Kp, pa->zero_point, pb->zero_point, cs);

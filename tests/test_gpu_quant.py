@@ -270,6 +270,32 @@ def test_quantized_matmul_device_wrap_and_errors(pn, ora):
     assert lib.quantized_matmul(a.ctypes.data, b.ctypes.data, got.ctypes.data, m, k, n, None, ctypes.byref(qb)) == -1
 
 
+def test_quantized_matmul_long_k_and_size_limit(pn, ora):
+    """K past 65535 16-byte units (the B pass loops over its K units) is
+    computed like the reference; M beyond 65535 row tiles (8,388,480) is
+    refused with -1 and NEURAL_ERR_TENSOR_TOO_LARGE before any access."""
+    import torch
+    lib = pn.core._lib
+    rng = np.random.default_rng(33)
+    m, k, n = 2, (1 << 20) + 17, 3
+    a = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    b = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    pa, pb = ora.QuantParams(), ora.QuantParams()
+    pa.scale, pa.zero_point, pb.scale, pb.zero_point = 0.01, 3, 0.02, -5
+    qa, qb = pn.core.QuantParamsC(), pn.core.QuantParamsC()
+    ctypes.memmove(ctypes.byref(qa), ctypes.byref(pa), ctypes.sizeof(qa))
+    ctypes.memmove(ctypes.byref(qb), ctypes.byref(pb), ctypes.sizeof(qb))
+    got = np.empty((m, n))
+    assert lib.quantized_matmul(a.ctypes.data, b.ctypes.data, got.ctypes.data, m, k, n, ctypes.byref(qa),
+                                ctypes.byref(qb)) == 0
+    same_bits(got.reshape(-1), ora.quantized_matmul(a, b, m, k, n, pa, pb)[1].reshape(-1))
+    dummy = torch.zeros(16, dtype=torch.int8, device="cuda")
+    big_m = 65535 * 128 + 1
+    assert lib.quantized_matmul(dummy.data_ptr(), dummy.data_ptr(), dummy.data_ptr(), big_m, 1, 1, ctypes.byref(qa),
+                                ctypes.byref(qb)) == -1
+    assert lib.neural_get_last_error() == pn.NeuralError.TENSOR_TOO_LARGE
+
+
 # ---- calibrate_percentile (quantize.c:89-132): radix select on the device -----------
 
 def _qp_bits(p):
