@@ -183,6 +183,21 @@ int neural_reduce_mean(const NeuralTensor *in, int64_t axis, NeuralTensor *out);
  * a host or device pointer with rows entries. */
 int neural_reduce_max(const NeuralTensor *in, int64_t axis, NeuralTensor *out);
 int neural_reduce_argmax(const NeuralTensor *in, int64_t axis, int64_t *out_indices);
+/* NEW, no counterpart in the reference: the row sum, mean, max and argmax over
+ * the last dim from ONE read of `in`, each bit-identical to the matching
+ * neural_reduce_sum / _mean / _max (axis = last dim) and neural_reduce_argmax
+ * call.  Any output may be NULL (skipped), not all of them (NULL_POINTER);
+ * sum / mean / max: contiguous, `rows` elements, the input's dtype; argmax:
+ * `rows` int64 at a host or device pointer.  Outputs must not overlap. */
+int neural_row_stats(const NeuralTensor *in, NeuralTensor *sum, NeuralTensor *mean, NeuralTensor *max,
+                     int64_t *argmax);
+/* NEW, no counterpart in the reference: out = in + bias exactly as
+ * neural_bias_add, and the row statistics of out exactly as neural_row_stats,
+ * reading `in` once and writing `out` once (contiguous tensors whose rows the
+ * stand-alone reductions give one wave or block each; otherwise the two calls
+ * in sequence, same results). */
+int neural_bias_add_row_stats(NeuralTensor *out, const NeuralTensor *in, const NeuralTensor *bias,
+                              NeuralTensor *sum, NeuralTensor *mean, NeuralTensor *max, int64_t *argmax);
 
 /* ---- Activations -------------------------------------------------------------- */
 int neural_relu(NeuralTensor *out, const NeuralTensor *input);      /* neural_api.h:379, node_relu activations.asm:114-200 */

@@ -38,8 +38,9 @@ struct RedMaxChain {
         s.nanacc = fma_t(x, T(0), s.nanacc);
     }
     NH_DEV L lcomb(L a, L b) const { return {fmax_nn(a.m, b.m), a.nanacc + b.nanacc}; }
-    template <int TPR>
-    NH_DEV B finish(L s, const T *row, int64_t lo, int64_t hi) const
+    // `row` is the row itself or a view that yields its elements by index
+    template <int TPR, class R>
+    NH_DEV B finish(L s, const R &row, int64_t lo, int64_t hi) const
     {
         using G = Grp<TPR>;
         B b{s.m, 0, hi > lo ? 1 : 0};
@@ -106,12 +107,135 @@ struct RedArgmax {
     NH_DEV B finish(L s, const T *, int64_t, int64_t) const { return s; }
     NH_DEV B bident() const { return linit(); }
     NH_DEV B bcomb(B a, B b) const { return lcomb(a, b); }
-    NH_DEV void store(void *out, int64_t r, B b, const T *row, int64_t) const
+    template <class R>
+    NH_DEV void store(void *out, int64_t r, B b, const R &row, int64_t) const
     {
         const T first = row[0];
         static_cast<int64_t *>(out)[r] = (first != first || b.i < 0) ? 0 : b.i;
     }
 };
+
+// ---- row statistics in one pass (NEW: no counterpart in the reference) -------------
+// Sum, mean, running-max chain and argmax of every row from one walk: the
+// four reducers side by side, each fed exactly the values, in exactly the
+// order, that it is fed by itself, so every output is bit-identical to the
+// stand-alone reduce_sum / reduce_mean / reduce_max / reduce_argmax of the
+// same rows.  Null output pointers are skipped.
+template <typename T>
+struct RedStats {
+    using S = RedSum<T, SUM_OUT_T>;
+    using M = RedMaxChain<T, OUT_T>;
+    using A = RedArgmax<T>;
+    struct L { typename S::L s; typename M::L m; typename A::L a; };
+    struct B { typename S::B s; typename M::B m; typename A::B a; };
+    T *sum = nullptr, *mean = nullptr, *max = nullptr;
+    int64_t *argmax = nullptr;
+    int64_t cols = 1;
+
+    NH_DEV L linit() const { return {S{}.linit(), M{}.linit(), A{}.linit()}; }
+    NH_DEV void lacc(L &l, T x, int64_t i) const
+    {
+        S{}.lacc(l.s, x, i);
+        M{}.lacc(l.m, x, i);
+        A{}.lacc(l.a, x, i);
+    }
+    NH_DEV L lcomb(L a, L b) const { return {S{}.lcomb(a.s, b.s), M{}.lcomb(a.m, b.m), A{}.lcomb(a.a, b.a)}; }
+    template <int TPR, class R>
+    NH_DEV B finish(L l, const R &row, int64_t lo, int64_t hi) const
+    {
+        const T *none = nullptr;  // the sum and argmax summaries do not look at the row
+        return {S{}.template finish<TPR>(l.s, none, lo, hi), M{}.template finish<TPR>(l.m, row, lo, hi),
+                A{}.template finish<TPR>(l.a, none, lo, hi)};
+    }
+    NH_DEV B bident() const { return {S{}.bident(), M{}.bident(), A{}.bident()}; }
+    NH_DEV B bcomb(B a, B b) const { return {S{}.bcomb(a.s, b.s), M{}.bcomb(a.m, b.m), A{}.bcomb(a.a, b.a)}; }
+    template <class R>
+    NH_DEV void store(void *, int64_t r, B b, const R &row, int64_t) const
+    {
+        const T *none = nullptr;
+        if (sum) S{}.store(sum, r, b.s, none, cols);
+        if (mean) {
+            S m;
+            m.div = cols;
+            m.store(mean, r, b.s, none, cols);
+        }
+        if (max) M{}.store(max, r, b.m, none, cols);
+        if (argmax) A{}.store(argmax, r, b.a, row, cols);
+    }
+};
+
+// The bias add as the walk's prologue: y = x + b per element (the rounding
+// neural_bias_add does), stored non-temporally and then reduced.
+template <typename T>
+struct BiasPre {
+    static constexpr bool kActive = true;
+    using V = typename Vec16<T>::type;
+    const T *bias;  // [cols]
+    T *y;           // this row of the output
+    NH_DEV V vec(const V &v, int64_t i) const
+    {
+        const V b = reinterpret_cast<const V *>(bias)[i];
+        V r;
+#pragma unroll
+        for (int k = 0; k < Vec16<T>::n; k++) r[k] = v[k] + b[k];
+        st_nt(reinterpret_cast<V *>(y) + i, r);
+        return r;
+    }
+    NH_DEV T one(T x, int64_t j) const
+    {
+        const T r = x + bias[j];
+        y[j] = r;
+        return r;
+    }
+};
+
+// The output row as the rescans see it, recomputed from x and b (the same
+// values the prologue stored; no wait for those stores is needed).
+template <typename T>
+struct BiasRow {
+    const T *x, *bias;
+    NH_DEV T operator[](int64_t j) const { return x[j] + bias[j]; }
+};
+
+// One group of TPR lanes per row, as k_reduce_rows: the row of x is read
+// once, y = x + b written once, and the statistics of y stored.
+template <typename T, int TPR>
+__global__ __launch_bounds__(kRBlock) void k_bias_row_stats(const T *__restrict__ x, const T *__restrict__ bias,
+                                                            T *__restrict__ y, int64_t rows, int64_t cols,
+                                                            RedStats<T> red, bool vec)
+{
+    constexpr int RPB = kRBlock / TPR;
+    for (int64_t r = int64_t(blockIdx.x) * RPB + threadIdx.x / TPR; r < rows; r += int64_t(gridDim.x) * RPB) {
+        const T *xr = x + r * cols;
+        const BiasPre<T> pre{bias, y + r * cols};
+        const typename RedStats<T>::L l = seg_walk<T, RedStats<T>, TPR, true>(red, xr, 0, cols, vec, pre);
+        const BiasRow<T> row{xr, bias};
+        const typename RedStats<T>::B b = red.template finish<TPR>(l, row, 0, cols);
+        if (Grp<TPR>::lane() == 0) red.store(nullptr, r, b, row, cols);
+    }
+}
+
+// bias == nullptr: the statistics of x.  Otherwise y = x + bias and its
+// statistics in one pass where the stand-alone reductions would use one group
+// per row; where they would split rows into segments (few long rows) the
+// bias add runs first and the statistics are reduced from y, so the split,
+// and with it every result, stays the stand-alone one.
+template <typename T>
+static int row_stats_launch(const T *x, const T *bias, T *y, int64_t rows, int64_t cols, const RedStats<T> &red)
+{
+    if (!bias) return launch_reduce(x, rows, cols, cols, red, nullptr);
+    const ReducePlan plan = reduce_plan<T>(rows, cols);
+    if (plan.gx > 1) return NEURAL_ERR_NOT_IMPLEMENTED;  // the caller takes the two-pass route
+    const bool vec = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(bias) |
+                       reinterpret_cast<uintptr_t>(y)) & 15u) == 0 && cols % Vec16<T>::n == 0;
+    if (plan.tpr == 64)
+        NH_LAUNCH((k_bias_row_stats<T, 64>), dim3(rows_grid(rows, kRBlock / 64)), dim3(kRBlock), 0, stream(), x,
+                  bias, y, rows, cols, red, vec);
+    else
+        NH_LAUNCH((k_bias_row_stats<T, kRBlock>), dim3(rows_grid(rows, 1)), dim3(kRBlock), 0, stream(), x, bias,
+                  y, rows, cols, red, vec);
+    return check_launch();
+}
 
 // ---- column sums (reduce_sum axis=0) -------------------------------------------------
 // Stage 1: grid (column groups of 256, row chunks) writes double partials
@@ -281,6 +405,70 @@ static int reduce_sum_mean(const NeuralTensor *in, int64_t axis, NeuralTensor *o
     return set_error(NEURAL_OK);
 }
 
+// The optional outputs of a row-statistics call on `in` (rows of its last
+// dimension): sum / mean / max tensors of `rows` elements, contiguous, in the
+// input's dtype; argmax `rows` int64 (host or device).  At least one is given.
+struct StatsOut {
+    NeuralTensor *t[3] = {nullptr, nullptr, nullptr};  // sum, mean, max
+    void *dev[3] = {nullptr, nullptr, nullptr};
+    int64_t *argmax = nullptr;
+    Staged arg;
+
+    int open(const NeuralTensor *in, int64_t rows, NeuralTensor *sum, NeuralTensor *mean, NeuralTensor *max,
+             int64_t *argmax_out)
+    {
+        t[0] = sum;
+        t[1] = mean;
+        t[2] = max;
+        argmax = argmax_out;
+        if (!sum && !mean && !max && !argmax) return set_error(NEURAL_ERR_NULL_POINTER);
+        for (NeuralTensor *o : t) {
+            if (!o) continue;
+            NH_TRY(check_tensor(o));
+            if (o->dtype != in->dtype) return set_error(NEURAL_ERR_DTYPE_MISMATCH);
+            if (numel(o) != rows || !is_contiguous(o)) return set_error(NEURAL_ERR_SHAPE_MISMATCH);
+        }
+        return NEURAL_OK;
+    }
+    // device destinations (after the argument checks of the call)
+    int map(int64_t rows)
+    {
+        for (int k = 0; k < 3; k++)
+            if (t[k]) NH_TRY(dev_write(t[k], &dev[k], true));
+        if (argmax) NH_TRY(arg.open(argmax, size_t(rows) * sizeof(int64_t), false));
+        return NEURAL_OK;
+    }
+    template <typename T>
+    RedStats<T> reducer(int64_t cols) const
+    {
+        RedStats<T> r;
+        r.sum = static_cast<T *>(dev[0]);
+        r.mean = static_cast<T *>(dev[1]);
+        r.max = static_cast<T *>(dev[2]);
+        r.argmax = argmax ? static_cast<int64_t *>(arg.dev) : nullptr;
+        r.cols = cols;
+        return r;
+    }
+    int finish()
+    {
+        for (NeuralTensor *o : t)
+            if (o) NH_TRY(dev_written(o));
+        if (argmax) NH_TRY(arg.finish(true));
+        return NEURAL_OK;
+    }
+};
+
+// rows x cols of `in` over its last dimension (cols > 0).
+static int stats_shape(const NeuralTensor *in, int64_t &rows, int64_t &cols)
+{
+    NH_TRY(check_tensor(in));
+    if (in->ndim < 1) return set_error(NEURAL_ERR_DIM_MISMATCH);
+    cols = in->shape[in->ndim - 1];
+    if (cols <= 0) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
+    rows = numel(in) / cols;
+    return NEURAL_OK;
+}
+
 }  // namespace nh
 
 using namespace nh;
@@ -384,6 +572,79 @@ int neural_reduce_argmax(const NeuralTensor *in, int64_t axis, int64_t *out_indi
     else
         NH_TRY(launch_reduce(static_cast<const double *>(c.p), rows, cols, cols, RedArgmax<double>{}, so.dev));
     NH_TRY(so.finish(true));
+    return set_error(NEURAL_OK);
+}
+
+// neural_row_stats (NEW: no counterpart in the reference): the sum, mean,
+// max and argmax of every row over the last dimension from one read of the
+// input, each bit-identical to neural_reduce_sum / neural_reduce_mean /
+// neural_reduce_max (axis = last) and neural_reduce_argmax.
+int neural_row_stats(const NeuralTensor *in, NeuralTensor *sum, NeuralTensor *mean, NeuralTensor *max,
+                     int64_t *argmax)
+{
+    NH_TRY(ensure_init());
+    if (!in) return set_error(NEURAL_ERR_NULL_POINTER);
+    int64_t rows = 0, cols = 0;
+    NH_TRY(stats_shape(in, rows, cols));
+    StatsOut so;
+    NH_TRY(so.open(in, rows, sum, mean, max, argmax));
+    if (rows == 0) return set_error(NEURAL_OK);
+    Contig c;
+    NH_TRY(c.open(in));
+    NH_TRY(so.map(rows));
+    if (in->dtype == NEURAL_DTYPE_FLOAT32)
+        NH_TRY(row_stats_launch(static_cast<const float *>(c.p), static_cast<const float *>(nullptr),
+                                static_cast<float *>(nullptr), rows, cols, so.reducer<float>(cols)));
+    else
+        NH_TRY(row_stats_launch(static_cast<const double *>(c.p), static_cast<const double *>(nullptr),
+                                static_cast<double *>(nullptr), rows, cols, so.reducer<double>(cols)));
+    NH_TRY(so.finish());
+    return set_error(NEURAL_OK);
+}
+
+// neural_bias_add_row_stats (NEW: no counterpart in the reference): out =
+// in + bias as neural_bias_add computes it, and the row statistics of out as
+// neural_row_stats computes them, with one read of `in` and one write of
+// `out` (no re-read of out) wherever the stand-alone reductions would give
+// each row one group of lanes; otherwise the two calls in sequence.
+int neural_bias_add_row_stats(NeuralTensor *out, const NeuralTensor *in, const NeuralTensor *bias,
+                              NeuralTensor *sum, NeuralTensor *mean, NeuralTensor *max, int64_t *argmax)
+{
+    NH_TRY(ensure_init());
+    if (!out || !in || !bias) return set_error(NEURAL_ERR_NULL_POINTER);
+    NH_TRY(check_tensor(out));
+    NH_TRY(check_tensor(bias));
+    int64_t rows = 0, cols = 0;
+    NH_TRY(stats_shape(in, rows, cols));
+    if (bias->ndim < 1 || numel(bias) != cols) return set_error(NEURAL_ERR_SHAPE_MISMATCH);
+    if (out->ndim != in->ndim) return set_error(NEURAL_ERR_SHAPE_MISMATCH);
+    for (int64_t i = 0; i < in->ndim; i++)
+        if (out->shape[i] != in->shape[i]) return set_error(NEURAL_ERR_SHAPE_MISMATCH);
+    if (in->dtype != out->dtype || bias->dtype != out->dtype) return set_error(NEURAL_ERR_DTYPE_MISMATCH);
+    StatsOut so;
+    NH_TRY(so.open(in, rows, sum, mean, max, argmax));
+    if (rows == 0) return set_error(NEURAL_OK);
+    const bool fused = is_contiguous(in) && is_contiguous(out) && is_contiguous(bias) &&
+                       ((in->dtype == NEURAL_DTYPE_FLOAT32 ? reduce_plan<float>(rows, cols)
+                                                           : reduce_plan<double>(rows, cols)).gx == 1);
+    if (!fused) {
+        NH_TRY(neural_bias_add(out, in, bias));
+        return neural_row_stats(out, sum, mean, max, argmax);
+    }
+    const void *px = nullptr, *pb = nullptr;
+    void *py = nullptr;
+    NH_TRY(dev_read(in, &px));
+    NH_TRY(dev_read(bias, &pb));
+    NH_TRY(dev_write(out, &py, true));
+    NH_TRY(so.map(rows));
+    if (in->dtype == NEURAL_DTYPE_FLOAT32)
+        NH_TRY(row_stats_launch(static_cast<const float *>(px), static_cast<const float *>(pb),
+                                static_cast<float *>(py), rows, cols, so.reducer<float>(cols)));
+    else
+        NH_TRY(row_stats_launch(static_cast<const double *>(px), static_cast<const double *>(pb),
+                                static_cast<double *>(py), rows, cols, so.reducer<double>(cols)));
+    NH_TRY(dev_written(out));
+    NH_TRY(so.finish());
     return set_error(NEURAL_OK);
 }
 

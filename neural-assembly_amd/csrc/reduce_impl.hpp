@@ -105,11 +105,24 @@ struct Grp {
 
 // ---- the segment walk ---------------------------------------------------------------------
 
-// Reduce row elements [lo, hi) with a group of TPR lanes.  `vec` promises that
-// row is 16-byte aligned and lo is a multiple of the vector width.  NT: the
-// vector loads are non-temporal.
-template <typename T, class Red, int TPR, bool NT>
-NH_DEV typename Red::B seg_reduce(const Red &red, const T *__restrict__ row, int64_t lo, int64_t hi, bool vec)
+// No prologue: the walked values are the row's own.
+struct NoPre {
+    static constexpr bool kActive = false;
+    template <typename V> NH_DEV V vec(const V &v, int64_t) const { return v; }
+    template <typename T> NH_DEV T one(T x, int64_t) const { return x; }
+};
+
+// Walk row elements [lo, hi) with a group of TPR lanes and return the group's
+// combined lane state (the same in every lane of the group).  `vec` promises
+// that row is 16-byte aligned and lo is a multiple of the vector width.  NT:
+// the vector loads are non-temporal.  A prologue `pre` (Pre::kActive) maps
+// each loaded vector / element (by its index in the row) before it is reduced;
+// the fused producers use it to compute and store a value and reduce it in the
+// same pass.  The walk order does not depend on Red or Pre, so a fused
+// reduction accumulates exactly what the stand-alone one does.
+template <typename T, class Red, int TPR, bool NT, class Pre = NoPre>
+NH_DEV typename Red::L seg_walk(const Red &red, const T *__restrict__ row, int64_t lo, int64_t hi, bool vec,
+                                const Pre &pre = Pre{})
 {
     using L = typename Red::L;
     using G = Grp<TPR>;
@@ -128,6 +141,13 @@ NH_DEV typename Red::B seg_reduce(const Red &red, const T *__restrict__ row, int
                 const int64_t i = c + int64_t(u) * TPR;
                 if (i < v1) r[u] = NT ? ld_nt(xv + i) : xv[i];
             }
+            if constexpr (Pre::kActive) {
+#pragma unroll
+                for (int u = 0; u < kRUnroll; u++) {
+                    const int64_t i = c + int64_t(u) * TPR;
+                    if (i < v1) r[u] = pre.vec(r[u], i);
+                }
+            }
 #pragma unroll
             for (int u = 0; u < kRUnroll; u++) {
                 const int64_t i = c + int64_t(u) * TPR;
@@ -139,9 +159,15 @@ NH_DEV typename Red::B seg_reduce(const Red &red, const T *__restrict__ row, int
         }
         tail = v1 * VN > lo ? v1 * VN : lo;
     }
-    for (int64_t j = tail + lane; j < hi; j += TPR) red.lacc(st, row[j], j);
-    st = G::reduce(st, [&](const L &a, const L &b) { return red.lcomb(a, b); });
-    return red.template finish<TPR>(st, row, lo, hi);
+    for (int64_t j = tail + lane; j < hi; j += TPR) red.lacc(st, pre.one(row[j], j), j);
+    return G::reduce(st, [&](const L &a, const L &b) { return red.lcomb(a, b); });
+}
+
+// Reduce row elements [lo, hi) to the segment summary.
+template <typename T, class Red, int TPR, bool NT>
+NH_DEV typename Red::B seg_reduce(const Red &red, const T *__restrict__ row, int64_t lo, int64_t hi, bool vec)
+{
+    return red.template finish<TPR>(seg_walk<T, Red, TPR, NT>(red, row, lo, hi, vec), row, lo, hi);
 }
 
 // Ordered combine of n segment summaries p[0..n) by one block; result valid
@@ -201,16 +227,18 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_rows(const T *__restrict__ x
                                                          int64_t ld, Red red, void *out, bool vec, Ticket tk)
 {
     constexpr int RPB = kRBlock / TPR;
-    const int64_t r = int64_t(blockIdx.x) * RPB + threadIdx.x / TPR;
-    if (r >= rows) return;  // uniform per group (the grid covers whole blocks only when TPR == 256)
-    const T *xr = x + r * ld;
-    // default-policy loads: in a sequence (bias add, then several row
-    // reductions of its result, then other streams) this measured faster for
-    // the whole sequence than non-temporal ones
-    const typename Red::B b = seg_reduce<T, Red, TPR, false>(red, xr, 0, cols, vec);
-    if (Grp<TPR>::lane() == 0) {
-        red.store(out, r, b, xr, cols);
-        publish(tk);  // tickets are used with a single row only
+    // rows past the grid (more than kMaxGridBlocks * RPB) are taken in further
+    // rounds; r is uniform per group
+    for (int64_t r = int64_t(blockIdx.x) * RPB + threadIdx.x / TPR; r < rows; r += int64_t(gridDim.x) * RPB) {
+        const T *xr = x + r * ld;
+        // default-policy loads: in a sequence (bias add, then several row
+        // reductions of its result, then other streams) this measured faster
+        // for the whole sequence than non-temporal ones
+        const typename Red::B b = seg_reduce<T, Red, TPR, false>(red, xr, 0, cols, vec);
+        if (Grp<TPR>::lane() == 0) {
+            red.store(out, r, b, xr, cols);
+            publish(tk);  // tickets are used with a single row only
+        }
     }
 }
 
@@ -254,6 +282,46 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_combine(const T *__restrict_
 // The segment summaries go to the shared workspace (under WsGuard), or to
 // `scratch` (scratch_bytes long) when the caller brings its own buffer; a
 // grid whose summaries do not fit it returns NEURAL_ERR_TENSOR_TOO_LARGE.
+// The grid of a reduction of `rows` rows of `cols` elements of T: gx segments
+// of `chunk` elements per row (gx > 1: k_reduce_seg + k_reduce_combine), else
+// one group per row of `tpr` lanes (k_reduce_rows).  A pure function of the
+// shape and the CU count, shared by every reducer, so a fused reduction walks
+// exactly the segments the stand-alone one does.
+struct ReducePlan {
+    int64_t gx, chunk;
+    int tpr;
+};
+
+template <typename T>
+ReducePlan reduce_plan(int64_t rows, int64_t cols)
+{
+    constexpr int VN = Vec16<T>::n;
+    const int64_t want = int64_t(num_cus()) * 4;  // blocks that keep every CU streaming (measured: 4/CU >= 8/CU here)
+    constexpr int64_t kGran = int64_t(kRBlock) * kRUnroll * VN;
+    ReducePlan p{1, cols, cols <= 2048 ? 64 : kRBlock};
+    // (a single block per row is slower even for a 512 KiB row: 18.7 us vs
+    // 9.4 us for 32 segments + the combine launch, measured)
+    if (rows < want && cols > 2 * kGran) {
+        p.gx = ceil_div(want, rows);
+        p.chunk = ceil_div(ceil_div(cols, p.gx), kGran) * kGran;
+        p.gx = ceil_div(cols, p.chunk);
+        const int64_t cap = kMaxPartials / rows;
+        if (p.gx > cap) {
+            p.gx = cap;
+            p.chunk = ceil_div(ceil_div(cols, p.gx), kGran) * kGran;
+            p.gx = ceil_div(cols, p.chunk);
+        }
+    }
+    return p;
+}
+
+// Blocks of a row-per-group launch (rpb rows per block), capped at kMaxGridBlocks.
+inline unsigned rows_grid(int64_t rows, int rpb)
+{
+    const int64_t g = ceil_div(rows, rpb);
+    return unsigned(g < kMaxGridBlocks ? g : kMaxGridBlocks);
+}
+
 template <typename T, class Red>
 int launch_reduce(const T *x, int64_t rows, int64_t cols, int64_t ld, const Red &red, void *out,
                   void *scratch = nullptr, size_t scratch_bytes = 0, Ticket tk = Ticket{})
@@ -261,25 +329,9 @@ int launch_reduce(const T *x, int64_t rows, int64_t cols, int64_t ld, const Red 
     if (tk.slot && rows != 1) return set_error(NEURAL_ERR_INTERNAL);
     static_assert(sizeof(typename Red::B) <= 64, "segment summary must fit a 64-byte partial slot");
     if (rows <= 0 || cols <= 0) return NEURAL_OK;
-    constexpr int VN = Vec16<T>::n;
     const bool vec = ((reinterpret_cast<uintptr_t>(x) & 15u) == 0) && ((ld * int64_t(sizeof(T))) % 16 == 0);
-    const int64_t cus = num_cus();
-    const int64_t want = cus * 4;  // blocks that keep every CU streaming (measured: 4/CU >= 8/CU here)
-    constexpr int64_t kGran = int64_t(kRBlock) * kRUnroll * VN;
-    int64_t gx = 1, chunk = cols;
-    // (a single block per row is slower even for a 512 KiB row: 18.7 us vs
-    // 9.4 us for 32 segments + the combine launch, measured)
-    if (rows < want && cols > 2 * kGran) {
-        gx = ceil_div(want, rows);
-        chunk = ceil_div(ceil_div(cols, gx), kGran) * kGran;
-        gx = ceil_div(cols, chunk);
-        const int64_t cap = kMaxPartials / rows;
-        if (gx > cap) {
-            gx = cap;
-            chunk = ceil_div(ceil_div(cols, gx), kGran) * kGran;
-            gx = ceil_div(cols, chunk);
-        }
-    }
+    const ReducePlan plan = reduce_plan<T>(rows, cols);
+    const int64_t gx = plan.gx, chunk = plan.chunk;
     if (gx > 1) {
         if (scratch && size_t(gx * rows) * sizeof(typename Red::B) > scratch_bytes)
             return set_error(NEURAL_ERR_TENSOR_TOO_LARGE);
@@ -291,13 +343,12 @@ int launch_reduce(const T *x, int64_t rows, int64_t cols, int64_t ld, const Red 
                            vec);
         NH_LAUNCH((k_reduce_combine<T, Red>), dim3(unsigned(rows)), dim3(kRBlock), 0, stream(), x, cols, ld,
                            int(gx), red, part, out, tk);
-    } else if (cols <= 2048) {
-        const unsigned g = unsigned(ceil_div(rows, kRBlock / 64));
-        NH_LAUNCH((k_reduce_rows<T, Red, 64>), dim3(g), dim3(kRBlock), 0, stream(), x, rows, cols, ld, red,
-                           out, vec, tk);
+    } else if (plan.tpr == 64) {
+        NH_LAUNCH((k_reduce_rows<T, Red, 64>), dim3(rows_grid(rows, kRBlock / 64)), dim3(kRBlock), 0, stream(), x,
+                  rows, cols, ld, red, out, vec, tk);
     } else {
-        NH_LAUNCH((k_reduce_rows<T, Red, kRBlock>), dim3(unsigned(rows)), dim3(kRBlock), 0, stream(), x,
-                           rows, cols, ld, red, out, vec, tk);
+        NH_LAUNCH((k_reduce_rows<T, Red, kRBlock>), dim3(rows_grid(rows, 1)), dim3(kRBlock), 0, stream(), x, rows,
+                  cols, ld, red, out, vec, tk);
     }
     return check_launch();
 }

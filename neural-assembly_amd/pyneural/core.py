@@ -196,6 +196,8 @@ _SIGS = {
     "neural_reduce_mean": (_i, [_vp, _i64, _vp]),
     "neural_reduce_max": (_i, [_vp, _i64, _vp]),
     "neural_reduce_argmax": (_i, [_vp, _i64, _vp]),
+    "neural_row_stats": (_i, [_vp, _vp, _vp, _vp, _vp]),
+    "neural_bias_add_row_stats": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     # activations
     "neural_relu": (_i, [_vp, _vp]),
     "neural_sigmoid": (_i, [_vp, _vp]),

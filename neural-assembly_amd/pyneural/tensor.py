@@ -271,6 +271,30 @@ class Tensor:
         _check_error(_lib.neural_argmax(self._ptr, ctypes.byref(r)), "argmax")
         return r.value
 
+    def _row_outputs(self):
+        if not self.shape or self.shape[-1] <= 0:
+            raise NeuralException(NeuralError.INVALID_ARGUMENT, "row statistics need a non-empty last dimension")
+        rows = self.numel // self.shape[-1]
+        return [Tensor.create([rows], self.dtype) for _ in range(3)], np.empty(rows, dtype=np.int64)
+
+    def row_stats(self):
+        """(sum, mean, max, argmax) of every row over the last dimension from one
+        read of the tensor (neural_row_stats; no counterpart in the reference):
+        three Tensors of `rows` values and an int64 numpy array, equal bit for
+        bit to the separate row reductions."""
+        (s, m, mx), idx = self._row_outputs()
+        _check_error(_lib.neural_row_stats(self._ptr, s._ptr, m._ptr, mx._ptr, idx.ctypes.data), "row_stats")
+        return s, m, mx, idx
+
+    def bias_add_row_stats(self, bias: "Tensor"):
+        """(self + bias, and that result's row sum, mean, max, argmax) in one
+        pass (neural_bias_add_row_stats; no counterpart in the reference)."""
+        out = Tensor.create(self.shape, self.dtype)
+        (s, m, mx), idx = self._row_outputs()
+        rc = _lib.neural_bias_add_row_stats(out._ptr, self._ptr, bias._ptr, s._ptr, m._ptr, mx._ptr, idx.ctypes.data)
+        _check_error(rc, "bias_add_row_stats")
+        return out, s, m, mx, idx
+
     # ---- arithmetic (tensor.py:627-665 of the reference) ----------------------------
     def _binary(self, other, fn, label):
         if not isinstance(other, Tensor):
