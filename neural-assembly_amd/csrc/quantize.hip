@@ -265,7 +265,17 @@ __global__ __launch_bounds__(kQBlock) void k_quantize_scalar(const T *x, int8_t 
         q[i] = quant_one(double(x[i]), inv, zp);
 }
 
-template <typename T>
+// Units per lane per tile of the write-heavy dequantize streams.  Fewer bytes
+// written per lane per block write HBM faster here (a plain 2 GiB fill: 6.72
+// TB/s with one 16-byte store per lane per block, 5.72 TB/s with four).
+// Measured at 268M codes with the output rotating over three buffers (so no
+// cache absorbs a rewrite): i8 -> f32 228 / 216 / 245 us for 4 / 2 / 1 units,
+// i8 -> f64 448 / 394 / 387 us.  The read-heavy quantize keeps kQUnroll (one
+// unit: 217 -> 257 us).
+constexpr int kDqUnrollF32 = 2;
+constexpr int kDqUnrollF64 = 1;
+
+template <typename T, int U>
 __global__ __launch_bounds__(kQBlock) void k_dequantize(const int8_t *__restrict__ q, T *__restrict__ y, int64_t n,
                                                         QArgs qa)
 {
@@ -275,16 +285,16 @@ __global__ __launch_bounds__(kQBlock) void k_dequantize(const int8_t *__restrict
     const double dz = double(zp);
     const int64_t n4 = n / 4;
     const uint32_t *q4 = reinterpret_cast<const uint32_t *>(q);
-    const int64_t tile = int64_t(kQBlock) * kQUnroll;
+    const int64_t tile = int64_t(kQBlock) * U;
     for (int64_t base = int64_t(blockIdx.x) * tile + threadIdx.x; base < n4; base += int64_t(gridDim.x) * tile) {
-        uint32_t w[kQUnroll];
+        uint32_t w[U];
 #pragma unroll
-        for (int u = 0; u < kQUnroll; u++) {
+        for (int u = 0; u < U; u++) {
             const int64_t i = base + int64_t(u) * kQBlock;
             if (i < n4) w[u] = __builtin_nontemporal_load(q4 + i);
         }
 #pragma unroll
-        for (int u = 0; u < kQUnroll; u++) {
+        for (int u = 0; u < U; u++) {
             const int64_t i = base + int64_t(u) * kQBlock;
             if (i < n4) {
                 Quad<T> o;
@@ -309,6 +319,7 @@ __global__ __launch_bounds__(kQBlock) void k_dequantize(const int8_t *__restrict
 // covers: measured 2.6 TB/s).  Lane m loads the packed codes of unit m; two
 // lane shuffles hand lane l the codes of doubles 2l, 2l+1 and 128+2l,
 // 128+2l+1 of the wave's 256.  The loop is uniform per wave.
+template <int U>
 __global__ __launch_bounds__(kQBlock) void k_dequantize_f64w(const int8_t *__restrict__ q, double *__restrict__ y,
                                                              int64_t n, QArgs qa)
 {
@@ -321,16 +332,16 @@ __global__ __launch_bounds__(kQBlock) void k_dequantize_f64w(const int8_t *__res
     const int64_t n4 = n / 4;
     const uint32_t *q4 = reinterpret_cast<const uint32_t *>(q);
     f64x2 *yv = reinterpret_cast<f64x2 *>(y);
-    const int64_t tile = int64_t(kQBlock) * kQUnroll;
+    const int64_t tile = int64_t(kQBlock) * U;
     for (int64_t wb = int64_t(blockIdx.x) * tile + (threadIdx.x & ~63u); wb < n4; wb += int64_t(gridDim.x) * tile) {
-        uint32_t w[kQUnroll];
+        uint32_t w[U];
 #pragma unroll
-        for (int u = 0; u < kQUnroll; u++) {
+        for (int u = 0; u < U; u++) {
             const int64_t i = wb + int64_t(u) * kQBlock + lane;
             w[u] = i < n4 ? __builtin_nontemporal_load(q4 + i) : 0u;
         }
 #pragma unroll
-        for (int u = 0; u < kQUnroll; u++) {
+        for (int u = 0; u < U; u++) {
             const int64_t ub = wb + int64_t(u) * kQBlock;
             if (ub >= n4) break;  // uniform over the wave
             const uint32_t lo = uint32_t(__shfl(int(w[u]), lane >> 1, 64));
@@ -391,11 +402,11 @@ static int launch_dequantize(const int8_t *q, T *y, int64_t n, QArgs qa)
 {
     const bool vec = (reinterpret_cast<uintptr_t>(y) & 15u) == 0 && (reinterpret_cast<uintptr_t>(q) & 3u) == 0;
     if (vec && sizeof(T) == 8)
-        NH_LAUNCH(k_dequantize_f64w, dim3(q_grid(n / 4, kQBlock * kQUnroll)), dim3(kQBlock), 0, stream(), q,
-                  reinterpret_cast<double *>(y), n, qa);
+        NH_LAUNCH(k_dequantize_f64w<kDqUnrollF64>, dim3(q_grid(n / 4, kQBlock * kDqUnrollF64)), dim3(kQBlock), 0,
+                  stream(), q, reinterpret_cast<double *>(y), n, qa);
     else if (vec)
-        NH_LAUNCH((k_dequantize<T>), dim3(q_grid(n / 4, kQBlock * kQUnroll)), dim3(kQBlock), 0, stream(), q,
-                           y, n, qa);
+        NH_LAUNCH((k_dequantize<T, kDqUnrollF32>), dim3(q_grid(n / 4, kQBlock * kDqUnrollF32)), dim3(kQBlock), 0,
+                  stream(), q, y, n, qa);
     else
         NH_LAUNCH((k_dequantize_scalar<T>), dim3(q_grid(n, kQBlock)), dim3(kQBlock), 0, stream(), q, y, n,
                            qa);
