@@ -305,7 +305,8 @@ struct Plan {
     int count;
     int64_t chunk_sum, chunk_ew;
     int64_t blocks_sum, blocks_ew;
-    unsigned grid_ew;       // read-write passes: one residency wave at most
+    unsigned grid_ew;       // scale pass: one residency wave at most (it usually exits at once)
+    unsigned grid_value;    // clamp pass: one block per chunk (it always works)
     template <class F>
     void with_tab(F f) const
     {
@@ -379,6 +380,10 @@ static int make_plan(const std::vector<GradRef> &g, Plan &p)
     }
     const int64_t wave = int64_t(num_cus()) * (2048 / kCBlock);  // resident 256-lane blocks per residency wave
     p.grid_ew = unsigned(p.blocks_ew < wave ? p.blocks_ew : wave);
+    // measured at 100M f32: the clamp pass 135.5 -> 128.5 us with a block per
+    // chunk; the scale pass keeps one residency wave, since a pass that clips
+    // nothing (the common case) then costs ~3 us less per call
+    p.grid_value = unsigned(p.blocks_ew < kMaxGridBlocks ? p.blocks_ew : kMaxGridBlocks);
     return NEURAL_OK;
 }
 
@@ -436,7 +441,7 @@ int clip_value_list(NeuralTensor *const *grads, int64_t count, double lo, double
     NH_TRY(make_plan(g, p));
     p.with_tab([&](const auto &tab) {
         using Tab = std::decay_t<decltype(tab)>;
-        NH_LAUNCH(k_clip_value<Tab>, dim3(p.grid_ew), dim3(kCBlock), 0, stream(), tab, p.count, p.chunk_ew,
+        NH_LAUNCH(k_clip_value<Tab>, dim3(p.grid_value), dim3(kCBlock), 0, stream(), tab, p.count, p.chunk_ew,
                            p.blocks_ew, lo, hi);
     });
     NH_TRY(check_launch());
