@@ -65,6 +65,11 @@ ACT_ALPHA = {"leaky_relu": 0.01, "elu": 1.0}
 NQ = 268_435_456               # cfg4
 NA = 100_000_000               # cfg5
 REPS = 10                      # timed launches per op outside the step
+# Untimed back-to-back calls of each op before its timed launches.  When the
+# load switches (light f32 streams to FP64-heavy activations, say) the GPU's
+# clocks take some milliseconds to settle: on one box f64 tanh ran 193-216 us
+# per launch in the first ~10 ms of FP64 work and 171-175 us after it.
+WARM_MS = 20.0
 
 
 def parse():
@@ -155,9 +160,14 @@ class Clock:
 
     def kernel_us(self, fn, reps=REPS, skip=0, warm=3):
         """Average duration (us) of one launch of `fn` (the launch after `skip`
-        others), each of `reps` calls timed by its own event pair."""
-        for _ in range(warm):
+        others), each of `reps` calls timed by its own event pair, after at
+        least `warm` calls and WARM_MS of back-to-back calls."""
+        t0, k = time.perf_counter(), 0
+        while k < warm or (time.perf_counter() - t0) * 1e3 < WARM_MS:
             fn()
+            k += 1
+            if k % 8 == 0:
+                self.torch.cuda.synchronize()
         self.torch.cuda.synchronize()
         used = []
         for r in range(reps):

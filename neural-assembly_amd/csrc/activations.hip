@@ -303,6 +303,21 @@ struct HeadTailFn {
     }
 };
 
+// hardswish on f32 tensors: the reference's double x * (x + 3.0) / 6.0 with
+// the division by 6 replaced by the product with RN(1/6).  The double results
+// can differ in the last bit, but after the rounding to float they agree for
+// every float input (checked exhaustively against the reference expression
+// over (-3, 3) on the CPU, zero signs included): one FP64 multiply in place of
+// the division's ten instructions.
+struct HardswishF32Fn {
+    NH_DEV float operator()(float xf) const
+    {
+        const double x = double(xf);
+        const double d = (x * (x + 3.0)) * (1.0 / 6.0);
+        return xf <= -3.0f ? 0.0f : (xf >= 3.0f ? xf : float(d));
+    }
+};
+
 // f32 functor calling a float formula directly.
 struct TanhF32Fn {
     NH_DEV float operator()(float x) const { return tanhf(x); }
@@ -375,7 +390,7 @@ static int bias_add_act(NeuralTensor *out, const NeuralTensor *x, const NeuralTe
     case NEURAL_ACT_SELU: return binary_api(out, x, bias, add_act(HeadTailFn<SeluF32>{}, ActFn<ASelu>{}));
     case NEURAL_ACT_SWISH: return binary_api(out, x, bias, add_act(HeadTailFn<SwishF32>{}, ActFn<ASwish>{}));
     case NEURAL_ACT_MISH: return binary_api(out, x, bias, add_act(HeadTailFn<MishF32>{}, ActFn<AMish>{}));
-    case NEURAL_ACT_HARDSWISH: return binary_api(out, x, bias, add_act(ActFn<AHardswish>{}, ActFn<AHardswish>{}));
+    case NEURAL_ACT_HARDSWISH: return binary_api(out, x, bias, add_act(HardswishF32Fn{}, ActFn<AHardswish>{}));
     case NEURAL_ACT_SOFTPLUS:
         return binary_api(out, x, bias, add_act(HeadTailFn<SoftplusF32>{}, ActFn<ASoftplus>{}));
     case NEURAL_ACT_HARDTANH: return binary_api(out, x, bias, add_act(ActFn<AHardtanh>{}, ActFn<AHardtanh>{}));
@@ -396,7 +411,7 @@ int act_elu(void *out, const void *in, double alpha) { return act_elu_impl(out, 
 int act_selu(void *out, const void *in) { return act_selu_impl(out, in); }
 int act_swish(void *out, const void *in) { return act_swish_impl(out, in); }
 int act_mish(void *out, const void *in) { return act_mish_impl(out, in); }
-int act_hardswish(void *out, const void *in) { return act<AHardswish>(out, in); }
+int act_hardswish(void *out, const void *in) { return act2<AHardswish>(out, in, HardswishF32Fn{}); }
 int act_softplus(void *out, const void *in) { return act_softplus_impl(out, in); }
 int act_hardtanh(void *out, const void *in) { return act<AHardtanh>(out, in); }
 
@@ -410,7 +425,7 @@ int neural_elu(NeuralTensor *out, const NeuralTensor *in, double alpha) { return
 int neural_selu(NeuralTensor *out, const NeuralTensor *in) { return act_selu_impl(out, in); }
 int neural_swish(NeuralTensor *out, const NeuralTensor *in) { return act_swish_impl(out, in); }
 int neural_mish(NeuralTensor *out, const NeuralTensor *in) { return act_mish_impl(out, in); }
-int neural_hardswish(NeuralTensor *out, const NeuralTensor *in) { return act<AHardswish>(out, in); }
+int neural_hardswish(NeuralTensor *out, const NeuralTensor *in) { return act2<AHardswish>(out, in, HardswishF32Fn{}); }
 int neural_softplus(NeuralTensor *out, const NeuralTensor *in) { return act_softplus_impl(out, in); }
 int neural_hardtanh(NeuralTensor *out, const NeuralTensor *in) { return act<AHardtanh>(out, in); }
 
