@@ -138,10 +138,10 @@ int launch_fill(void *dst, int dtype, int64_t n, double value)
 {
     if (n <= 0) return NEURAL_OK;
     if (dtype == NEURAL_DTYPE_FLOAT32)
-        NH_LAUNCH((k_fill<float>), dim3(flat_grid(n, 4)), dim3(kBlock), 0, stream(),
+        NH_LAUNCH((k_fill<float>), dim3(flat_grid(n, 4, kUnroll)), dim3(kBlock), 0, stream(),
                            static_cast<float *>(dst), n, float(value));
     else
-        NH_LAUNCH((k_fill<double>), dim3(flat_grid(n, 2)), dim3(kBlock), 0, stream(),
+        NH_LAUNCH((k_fill<double>), dim3(flat_grid(n, 2, kUnroll)), dim3(kBlock), 0, stream(),
                            static_cast<double *>(dst), n, value);
     return check_launch();
 }

@@ -16,13 +16,21 @@ namespace nh {
 
 constexpr int kBlock = 256;
 constexpr int kUnroll = 4;
+// Flat kernels: U vectors per lane per tile, and a wave's 64 U vectors are
+// contiguous (lane l of wave w takes vectors w 64 U + u 64 + l): each wave
+// streams one contiguous span.
+constexpr int kFlatU = 2;
+
+// First vector of the calling lane in the flat tile that starts at vector t0.
+NH_DEV int64_t flat_lane0(int64_t t0) { return t0 + int64_t(threadIdx.x >> 6) * (64 * kFlatU) + (threadIdx.x & 63); }
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // ---- flat binary ----------------------------------------------------------
-// Grid-stride over tiles of 256*U vectors (U = 4); per tile every lane issues
-// its U loads per operand before any arithmetic or store.  All accesses are
-// non-temporal.  Block 0 also finishes the n % VN tail.
+// Grid-stride over tiles of 256 * kFlatU vectors (flat_lane0 layout); per
+// tile every lane issues its loads of both operands before any arithmetic or
+// store.  All accesses are non-temporal.  Block 0 also finishes the n % VN
+// tail.
 template <typename T, typename Op>
 __global__ __launch_bounds__(kBlock) void k_map2_flat(const T *__restrict__ a, const T *__restrict__ b,
                                                       T *__restrict__ o, int64_t n, Op op)
@@ -33,17 +41,17 @@ __global__ __launch_bounds__(kBlock) void k_map2_flat(const T *__restrict__ a, c
     const V *av = reinterpret_cast<const V *>(a);
     const V *bv = reinterpret_cast<const V *>(b);
     V *ov = reinterpret_cast<V *>(o);
-    const int64_t step = int64_t(gridDim.x) * (kBlock * kUnroll);
-    for (int64_t base = int64_t(blockIdx.x) * (kBlock * kUnroll) + threadIdx.x; base < nv; base += step) {
-        V ra[kUnroll], rb[kUnroll];
+    const int64_t step = int64_t(gridDim.x) * (kBlock * kFlatU);
+    for (int64_t base = flat_lane0(int64_t(blockIdx.x) * (kBlock * kFlatU)); base < nv; base += step) {
+        V ra[kFlatU], rb[kFlatU];
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) {
-            const int64_t i = base + int64_t(u) * kBlock;
+        for (int u = 0; u < kFlatU; u++) {
+            const int64_t i = base + int64_t(u) * 64;
             if (i < nv) { ra[u] = ld_nt(av + i); rb[u] = ld_nt(bv + i); }
         }
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) {
-            const int64_t i = base + int64_t(u) * kBlock;
+        for (int u = 0; u < kFlatU; u++) {
+            const int64_t i = base + int64_t(u) * 64;
             if (i < nv) {
                 V r;
 #pragma unroll
@@ -74,17 +82,17 @@ __global__ __launch_bounds__(kBlock) void k_map1_flat(const T *__restrict__ a, T
     const int64_t nv = n / VN;
     const V *av = reinterpret_cast<const V *>(a);
     V *ov = reinterpret_cast<V *>(o);
-    const int64_t step = int64_t(gridDim.x) * (kBlock * kUnroll);
-    for (int64_t base = int64_t(blockIdx.x) * (kBlock * kUnroll) + threadIdx.x; base < nv; base += step) {
-        V ra[kUnroll];
+    const int64_t step = int64_t(gridDim.x) * (kBlock * kFlatU);
+    for (int64_t base = flat_lane0(int64_t(blockIdx.x) * (kBlock * kFlatU)); base < nv; base += step) {
+        V ra[kFlatU];
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) {
-            const int64_t i = base + int64_t(u) * kBlock;
+        for (int u = 0; u < kFlatU; u++) {
+            const int64_t i = base + int64_t(u) * 64;
             if (i < nv) ra[u] = ld_nt(av + i);
         }
 #pragma unroll
-        for (int u = 0; u < kUnroll; u++) {
-            const int64_t i = base + int64_t(u) * kBlock;
+        for (int u = 0; u < kFlatU; u++) {
+            const int64_t i = base + int64_t(u) * 64;
             if (i < nv) {
                 V r;
 #pragma unroll
@@ -311,12 +319,12 @@ __global__ __launch_bounds__(kBlock) void k_map1_nd(const T *a, T *o, int64_t n,
 
 // ---- host-side launch helpers ---------------------------------------------------
 
-// One block per tile of the whole range (kMaxGridBlocks at most; the
-// grid-stride loop covers the rest).
-inline unsigned flat_grid(int64_t n, int vn)
+// One block per tile of u vectors per lane over the whole range
+// (kMaxGridBlocks at most; the grid-stride loop covers the rest).
+inline unsigned flat_grid(int64_t n, int vn, int u = kFlatU)
 {
     const int64_t nv = n / vn;
-    int64_t g = ceil_div(nv, int64_t(kBlock) * kUnroll);
+    int64_t g = ceil_div(nv, int64_t(kBlock) * u);
     const int64_t cap = kMaxGridBlocks;
     if (g > cap) g = cap;
     return unsigned(g < 1 ? 1 : g);
@@ -337,7 +345,7 @@ int launch_rowbcast(const T *a, const T *b, T *o, int64_t rows, int64_t cols, Op
     const int64_t ncv = cols / VN;
     if (rows <= 0 || ncv <= 0) return NEURAL_OK;
     const int64_t nv = rows * ncv;
-    const unsigned g = flat_grid(nv * VN, VN);
+    const unsigned g = flat_grid(nv * VN, VN, kUnroll);
     const int64_t d1 = int64_t(kBlock) % ncv;
     const int64_t dS = (int64_t(g) * kBlock * kUnroll) % ncv;
     if (dS == 0)
