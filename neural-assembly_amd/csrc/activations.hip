@@ -34,11 +34,25 @@ namespace nh {
 constexpr double kGelu = 0.7978845608028654;
 constexpr double kSeluL = 1.0507009873554804934193349852946;
 constexpr double kSeluA = 1.6732632423543772848170429916717;
+// 1 / d for normal d of moderate size (2^-1000 < |d| < 2^1000): the hardware
+// reciprocal refined by two Newton steps (each squares the relative error;
+// the result is within an ulp or two of the correctly rounded quotient, ~5
+// instructions instead of a division's ~12).
+NH_DEV double rcp_nr(double d)
+{
+    double r = __builtin_amdgcn_rcp(d);
+    double e = __builtin_fma(-d, r, 1.0);
+    r = __builtin_fma(r, e, r);
+    e = __builtin_fma(-d, r, 1.0);
+    return __builtin_fma(r, e, r);
+}
+
 // tanh(x) = (E - 1) / (E + 1), E = exp(2|x|), with |x| clamped to 22 (where
 // the double result is already +-1); |x| < 2^-7 uses the Taylor series through
 // x^7 (truncation below 3e-19 relative; zeros keep their sign, denormals are
 // returned unchanged).
-// E - 1 is exact, so the relative error is ~1 ulp(E) / (E - 1) < 1.5e-14.
+// E - 1 is exact, so the relative error is ~1 ulp(E) / (E - 1) < 1.5e-14 (plus
+// an ulp or two from the reciprocal).
 NH_DEV double tanh_d(double x)
 {
     const double a = __builtin_fabs(x);
@@ -47,20 +61,8 @@ NH_DEV double tanh_d(double x)
         __builtin_fma(x * x2, __builtin_fma(x2, __builtin_fma(x2, -17.0 / 315.0, 2.0 / 15.0), -1.0 / 3.0), x), x);
     const double c = a < 22.0 ? a : 22.0;
     const double e = exp(c + c);
-    const double big = __builtin_copysign((e - 1.0) / (e + 1.0), x);
+    const double big = __builtin_copysign((e - 1.0) * rcp_nr(e + 1.0), x);
     return (a < 0x1p-7 || x != x) ? small : big;
-}
-
-// 1 / d for d in [1, 2]: the hardware reciprocal refined by two Newton steps
-// (each squares the relative error; the result is within an ulp or two of
-// the correctly rounded quotient, ~5 instructions instead of a division's ~12).
-NH_DEV double rcp_1_2(double d)
-{
-    double r = __builtin_amdgcn_rcp(d);
-    double e = __builtin_fma(-d, r, 1.0);
-    r = __builtin_fma(r, e, r);
-    e = __builtin_fma(-d, r, 1.0);
-    return __builtin_fma(r, e, r);
 }
 
 // 1 + tanh(z) as the reference's double tanh leaves it, from w = exp(-2|z|):
@@ -79,7 +81,7 @@ NH_DEV double one_plus_tanh(double z)
 {
     const double a = -2.0 * __builtin_fabs(z);
     const double w = exp(a > -40.0 ? a : -40.0);
-    const double r = rcp_1_2(1.0 + w);
+    const double r = rcp_nr(1.0 + w);
     const double eps = (w + w) * r;
     // eps rounded to a multiple of 2^-53, ties to even: 0.5 + eps (in [0.5, 1),
     // ulp 2^-53) rounds exactly so, and subtracting 0.5 is exact
@@ -93,8 +95,38 @@ NH_DEV double gelu_d(double x)
     return 0.5 * x * one_plus_tanh(z);
 }
 
-// softplus = log(u), u = 1.0 + exp(x) rounded as in the reference.
-NH_DEV double softplus_d(double x) { return log_ge1(1.0 + exp(x)); }
+// softplus = log(u), u = 1.0 + exp(x) rounded as in the reference, from one
+// exponential t = e^{-|x|} <= 1:
+//   x <= 0:  u = 1 + t is the reference's u exactly;
+//   x > 0:   log(1 + e^x) = x + log(1 + t); the rounding of 1 + t moves that
+//            by at most 2^-53, below 1.6e-16 of a result > log 2;
+// log of u in [1, 2]: m = u, or u / 2 above sqrt 2 (then + ln 2), and
+// log m = 2 atanh(s), s = (m - 1) / (m + 1) in [-0.172, 0.172] (m - 1 exact),
+// by the series of log_ge1 -- no frexp, and a refined reciprocal for the
+// quotient.  The reference's double exp overflows above 709.78 (+inf).
+NH_DEV double softplus_d(double x)
+{
+    const double t = exp(-__builtin_fabs(x));
+    const double u = 1.0 + t;
+    const bool hi = u > 0x1.6a09e667f3bcdp+0;  // sqrt 2
+    const double m = hi ? 0.5 * u : u;
+    const double s = (m - 1.0) * rcp_nr(m + 1.0);
+    const double s2 = s * s;
+    double q = 1.0 / 19.0;
+    q = __builtin_fma(q, s2, 1.0 / 17.0);
+    q = __builtin_fma(q, s2, 1.0 / 15.0);
+    q = __builtin_fma(q, s2, 1.0 / 13.0);
+    q = __builtin_fma(q, s2, 1.0 / 11.0);
+    q = __builtin_fma(q, s2, 1.0 / 9.0);
+    q = __builtin_fma(q, s2, 1.0 / 7.0);
+    q = __builtin_fma(q, s2, 1.0 / 5.0);
+    q = __builtin_fma(q, s2, 1.0 / 3.0);
+    const double s_2 = s + s;
+    const double lm = __builtin_fma(s_2 * s2, q, s_2);
+    const double l = hi ? lm + 0x1.62e42fefa39efp-1 : lm;  // + ln 2
+    const double r = x <= 0.0 ? l : x + l;
+    return x > 0x1.62e42fefa39efp+9 ? __builtin_inf() : r;  // 709.782712893384
+}
 
 // mish = x * tanh(log u), u = 1 + e^x, tanh(log u) = (u^2 - 1)/(u^2 + 1), from
 // one exponential s = e^{-|x|} and one division, no branch (a wave holds both
