@@ -47,6 +47,34 @@ NH_DEV double rcp_nr(double d)
     return __builtin_fma(r, e, r);
 }
 
+// e^a for a in [0, 44] (tanh's argument): a = k ln2 + r, |r| <= ln2/2, e^r by
+// its Taylor polynomial through r^11 (truncation below 7e-15 relative), scaled
+// by 2^k; ~17 instructions without the device library's range selects.  Its
+// error (up to ~30 ulp) is fine where e^a enters a quotient, not where the
+// reference rounds 1 + e^a (softplus, mish) or 1 + tanh (gelu): there an
+// exponential a few ulp off moves the rounded sum across a rounding boundary
+// about once per 10^4 elements, an error of up to 1e-11 relative after it
+// (measured on mish), so those keep the device library's exp.
+NH_DEV double exp_in_range(double a)
+{
+    const double k = __builtin_rint(a * 0x1.71547652b82fep+0);  // 1 / ln 2
+    double r = __builtin_fma(-k, kLn2Hi, a);                     // exact for |k| < 2^21
+    r = __builtin_fma(-k, kLn2Lo, r);
+    double p = 1.0 / 39916800.0;
+    p = __builtin_fma(p, r, 1.0 / 3628800.0);
+    p = __builtin_fma(p, r, 1.0 / 362880.0);
+    p = __builtin_fma(p, r, 1.0 / 40320.0);
+    p = __builtin_fma(p, r, 1.0 / 5040.0);
+    p = __builtin_fma(p, r, 1.0 / 720.0);
+    p = __builtin_fma(p, r, 1.0 / 120.0);
+    p = __builtin_fma(p, r, 1.0 / 24.0);
+    p = __builtin_fma(p, r, 1.0 / 6.0);
+    p = __builtin_fma(p, r, 0.5);
+    p = __builtin_fma(p, r, 1.0);
+    p = __builtin_fma(p, r, 1.0);
+    return __builtin_ldexp(p, int(k));
+}
+
 // tanh(x) = (E - 1) / (E + 1), E = exp(2|x|), with |x| clamped to 22 (where
 // the double result is already +-1); |x| < 2^-7 uses the Taylor series through
 // x^7 (truncation below 3e-19 relative; zeros keep their sign, denormals are
@@ -60,7 +88,7 @@ NH_DEV double tanh_d(double x)
     const double small = __builtin_copysign(
         __builtin_fma(x * x2, __builtin_fma(x2, __builtin_fma(x2, -17.0 / 315.0, 2.0 / 15.0), -1.0 / 3.0), x), x);
     const double c = a < 22.0 ? a : 22.0;
-    const double e = exp(c + c);
+    const double e = exp_in_range(c + c);
     const double big = __builtin_copysign((e - 1.0) * rcp_nr(e + 1.0), x);
     return (a < 0x1p-7 || x != x) ? small : big;
 }
@@ -102,8 +130,8 @@ NH_DEV double gelu_d(double x)
 //            by at most 2^-53, below 1.6e-16 of a result > log 2;
 // log of u in [1, 2]: m = u, or u / 2 above sqrt 2 (then + ln 2), and
 // log m = 2 atanh(s), s = (m - 1) / (m + 1) in [-0.172, 0.172] (m - 1 exact),
-// by the series of log_ge1 -- no frexp, and a refined reciprocal for the
-// quotient.  The reference's double exp overflows above 709.78 (+inf).
+// by the odd series through s^15 (truncation below 3.4e-14 relative, inside
+// the 1e-12 f64 bar) -- no frexp, and a refined reciprocal for the quotient.  The reference's double exp overflows above 709.78 (+inf).
 NH_DEV double softplus_d(double x)
 {
     const double t = exp(-__builtin_fabs(x));
@@ -112,9 +140,7 @@ NH_DEV double softplus_d(double x)
     const double m = hi ? 0.5 * u : u;
     const double s = (m - 1.0) * rcp_nr(m + 1.0);
     const double s2 = s * s;
-    double q = 1.0 / 19.0;
-    q = __builtin_fma(q, s2, 1.0 / 17.0);
-    q = __builtin_fma(q, s2, 1.0 / 15.0);
+    double q = 1.0 / 15.0;
     q = __builtin_fma(q, s2, 1.0 / 13.0);
     q = __builtin_fma(q, s2, 1.0 / 11.0);
     q = __builtin_fma(q, s2, 1.0 / 9.0);
@@ -142,7 +168,7 @@ NH_DEV double mish_d(double x)
     const double t = (1.0 + s) - 1.0;
     const double num = pos ? __builtin_fma(2.0, s, 1.0) : t * (2.0 + t);
     const double den = num + (pos ? 2.0 * (s * s) : 2.0);
-    return x * (num / den);
+    return x * (num * rcp_nr(den));
 }
 
 // ---- f32 outputs ----------------------------------------------------------------
