@@ -144,7 +144,11 @@ __global__ __launch_bounds__(kDBlock) void k_jump_table(uint64_t *__restrict__ T
 // Generate the keep bits of segment j.  W is the anchor window, Wn receives
 // the window after the call.  keep = (r >> 1) >= thr, taken as the sign bit of
 // thr_m1 - (r >> 1) with thr_m1 = thr - 1 (mod 2^32; both sides fit in 32 bits,
-// and thr = 0 keeps every draw): no compare, so no chain through VCC.  One period of 31 draws
+// and thr = 0 keeps every draw): no compare, so no chain through VCC.  One
+// funnel shift (alignbit: (kb << 1) | (x >> 31)) moves each sign bit into the
+// period's word, first draw highest -- four instructions per draw with the
+// recurrence add -- and a bit reversal per period puts draw u at bit u.
+// One period of 31 draws
 // is unrolled (ring slots are then registers) and the period loop is not:
 // the fully unrolled segment is ~50 KB of straight-line code, and fetching it
 // cold made the kernel instruction-fetch bound (measured 4x slower).
@@ -157,17 +161,18 @@ NH_DEV void gen_segment(uint32_t (&w)[kLag], int64_t d0, int64_t n, uint32_t thr
     int word = 0;
 #pragma unroll 1
     for (int per = 0; per < kPeriods; per++) {
-        uint32_t pb = 0u;
+        uint32_t kb = 0u;  // keep bit of draw u at bit 30 - u
 #pragma unroll
         for (int u = 0; u < kLag; u++) {
             const uint32_t r = w[u] + w[(u + 28) % kLag];
             w[u] = r;
-            pb |= ((thr_m1 - (r >> 1)) >> (31 - u)) & (1u << u);
+            kb = __builtin_amdgcn_alignbit(kb, thr_m1 - (r >> 1), 31u);
             if constexpr (TAIL) {
                 const int64_t d = d0 + int64_t(per) * kLag + u;
                 if (d < n && d >= n - kLag) Wn[d - (n - kLag)] = r;
             }
         }
+        const uint32_t pb = __builtin_bitreverse32(kb) >> 1;  // draw u at bit u
         acc |= uint64_t(pb) << have;
         have += kLag;
         if (have >= 32) {
