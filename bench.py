@@ -837,43 +837,146 @@ def cpu_cfg5(p_dev, clean_dev, g_dev):
 # ------------------------------------------------------------------------- other families
 
 def suite(torch, pn, clock, dev):
-    """Kernel families outside BASELINE's configs (detail file only)."""
-    from pyneural.core import _lib
+    """Kernel families outside BASELINE's configs (detail file only): for each
+    op the kernel time of its main launch (`k`, HIP event pair on that launch)
+    and, where a call makes several launches or returns a result to the host,
+    the call time (`call`, all launches and gaps), in us, with the algorithmic
+    bytes of the main kernel."""
+    from pyneural.core import _lib, QuantParamsC
     W = pn.Tensor.from_torch
     res = {}
+
+    def put(name, nbytes, k=None, call=None):
+        e = {"bytes": int(nbytes)}
+        if k is not None:
+            e["k_us"] = round(k, 2)
+            e["k_pct"] = pct(nbytes, k)
+        if call is not None:
+            e["call_us"] = round(call, 2)
+            e["call_pct"] = pct(nbytes, call)
+        res[name] = e
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    # ---- bias add (>= 64M), fused bias + activation, row reductions at [16384,4096]
+    R, C = 16384, 4096
+    X = torch.randn(R, C, device=dev, generator=g) * 3
+    bias = torch.randn(C, device=dev, generator=g) * 3
+    Y = torch.empty_like(X)
+    rs = torch.empty(R, device=dev)
+    ri = torch.empty(R, dtype=torch.int64, device=dev)
+    tX, tb, tY, trs = W(X), W(bias), W(Y), W(rs)
+    torch.cuda.synchronize()
+    put("bias_add_f32_16384x4096", 8 * R * C, clock.kernel_us(lambda: _lib.neural_bias_add(tY._ptr, tX._ptr, tb._ptr)))
+    for nm, act in (("relu", 1), ("gelu", 4)):
+        put(f"bias_add_{nm}_f32_16384x4096", 8 * R * C, clock.kernel_us(
+            lambda act=act: _lib.neural_bias_add_act(tY._ptr, tX._ptr, tb._ptr, act, ctypes.c_double(0.0))))
+    put("row_sum_f32_16384x4096", 4 * R * C, clock.kernel_us(lambda: _lib.neural_reduce_sum(tY._ptr, 1, trs._ptr)))
+    put("row_max_f32_16384x4096", 4 * R * C, clock.kernel_us(lambda: _lib.neural_reduce_max(tY._ptr, 1, trs._ptr)))
+    put("row_argmax_f32_16384x4096", 4 * R * C,
+        clock.kernel_us(lambda: _lib.neural_reduce_argmax(tY._ptr, 1, ri.data_ptr())))
+    del X, Y, tX, tY, rs, ri, trs
+    torch.cuda.empty_cache()
+
+    # ---- dropout forward / backward, 64M f32, p = 0.5 (the forward is two launches)
     n = N1
-    a = torch.rand(n, device=dev) * 2 - 1
+    a = torch.rand(n, device=dev, generator=g) * 2 - 1
     c = torch.empty_like(a)
     dmask = torch.empty(n, dtype=torch.uint8, device=dev)
     torch.cuda.synchronize()
-    res["dropout_fwd_f32_64M"] = clock.call_us(
-        lambda: _lib.neural_dropout_forward(a.data_ptr(), c.data_ptr(), dmask.data_ptr(), n, ctypes.c_float(0.5)))
-    res["dropout_bwd_f32_64M"] = clock.kernel_us(
-        lambda: _lib.neural_dropout_backward(a.data_ptr(), c.data_ptr(), dmask.data_ptr(), n, ctypes.c_float(0.5)))
+    fwd = lambda: _lib.neural_dropout_forward(a.data_ptr(), c.data_ptr(), dmask.data_ptr(), n, ctypes.c_float(0.5))
+    put("dropout_fwd_keep_bits_f32_64M", 0, clock.kernel_us(fwd, skip=0))
+    put("dropout_fwd_apply_f32_64M", 9 * n, clock.kernel_us(fwd, skip=1))
+    put("dropout_fwd_f32_64M", 9 * n, None, clock.call_us(fwd))
+    put("dropout_bwd_f32_64M", 9 * n, clock.kernel_us(
+        lambda: _lib.neural_dropout_backward(a.data_ptr(), c.data_ptr(), dmask.data_ptr(), n, ctypes.c_float(0.5))))
     del a, c, dmask
-    X = torch.randn(16384, 4096, device=dev)
-    bias = torch.randn(4096, device=dev)
-    Y = torch.empty_like(X)
-    tX, tb, tY = W(X), W(bias), W(Y)
-    res["bias_add_f32_16384x4096"] = clock.kernel_us(lambda: _lib.neural_bias_add(tY._ptr, tX._ptr, tb._ptr))
-    res["bias_add_gelu_f32_16384x4096"] = clock.kernel_us(
-        lambda: _lib.neural_bias_add_act(tY._ptr, tX._ptr, tb._ptr, 4, ctypes.c_double(0.0)))
-    del X, Y, tX, tY
-    S = torch.randn(65536, 1024, device=dev) * 3
-    G = torch.empty_like(S)
-    tgt = torch.randint(0, 1024, (65536,), device=dev, dtype=torch.int64)
+    torch.cuda.empty_cache()
+
+    # ---- cross-entropy [65536,1024]: label-smoothed forward / fused (f64, f32), tensor CE loss (f32)
+    B, K = 65536, 1024
+    tgt = torch.randint(0, K, (B,), device=dev, dtype=torch.int64, generator=g)
     lossv = ctypes.c_double()
-    res["ls_ce_fused_f32_65536x1024"] = clock.call_us(
-        lambda: _lib.label_smoothing_ce_fused_f32(S.data_ptr(), tgt.data_ptr(), 65536, 1024, 0.1,
-                                                  ctypes.byref(lossv), G.data_ptr()))
-    del S, G
+    L64 = torch.randn(B, K, device=dev, dtype=torch.float64, generator=g) * 3
+    G64 = torch.empty_like(L64)
+    torch.cuda.synchronize()
+    f = lambda: _lib.label_smoothing_ce_forward(L64.data_ptr(), tgt.data_ptr(), B, K, 0.1, ctypes.byref(lossv))
+    put("ls_ce_forward_f64_65536x1024", 8 * B * K, clock.kernel_us(f), clock.call_us(f))
+    f = lambda: _lib.label_smoothing_ce_fused(L64.data_ptr(), tgt.data_ptr(), B, K, 0.1, ctypes.byref(lossv),
+                                              G64.data_ptr())
+    put("ls_ce_fused_f64_65536x1024", 16 * B * K, clock.kernel_us(f), clock.call_us(f))
+    del L64, G64
+    L32 = torch.randn(B, K, device=dev, generator=g) * 3
+    G32 = torch.empty_like(L32)
+    torch.cuda.synchronize()
+    f = lambda: _lib.label_smoothing_ce_fused_f32(L32.data_ptr(), tgt.data_ptr(), B, K, 0.1, ctypes.byref(lossv),
+                                                  G32.data_ptr())
+    put("ls_ce_fused_f32_65536x1024", 8 * B * K, clock.kernel_us(f), clock.call_us(f))
+    tv = W(tgt.float())
+    tL = W(L32)
+    f = lambda: _lib.neural_cross_entropy_loss(tL._ptr, tv._ptr, ctypes.byref(lossv))
+    put("ce_loss_f32_65536x1024", 4 * B * K, clock.kernel_us(f), clock.call_us(f))
+    del L32, G32, tL, tv, tgt
+    torch.cuda.empty_cache()
+
+    # ---- gradient clipping over one 100M f32 gradient (norm: sum of squares,
+    # decide, scale; each timed call clips by 0.999, so every call scales)
     na = NA
-    gr = torch.randn(na, device=dev) * 1e-3
+    gr = torch.randn(na, device=dev, generator=g) * 1e-3
     tg = W(gr)
     glist = (ctypes.c_void_p * 1)(tg._ptr)
-    res["clip_grad_value_f32_100M"] = clock.call_us(
-        lambda: _lib.neural_clip_grad_value_list(glist, 1, ctypes.c_double(-1e-3), ctypes.c_double(1e-3)))
-    return {k: round(v, 2) for k, v in res.items()}
+    tot = ctypes.c_double()
+    torch.cuda.synchronize()
+    _lib.neural_clip_grad_norm_list(glist, 1, ctypes.c_double(1e30), ctypes.byref(tot))
+    state = {"m": tot.value}
+
+    def clip_scaling():
+        state["m"] *= 0.999
+        return _lib.neural_clip_grad_norm_list(glist, 1, ctypes.c_double(state["m"]), ctypes.byref(tot))
+
+    put("clip_grad_norm_clipping_f32_100M", 12 * na, None, clock.call_us(clip_scaling))
+    put("clip_grad_norm_below_f32_100M", 4 * na, None, clock.call_us(
+        lambda: _lib.neural_clip_grad_norm_list(glist, 1, ctypes.c_double(1e30), ctypes.byref(tot))))
+    f = lambda: _lib.neural_clip_grad_value_list(glist, 1, ctypes.c_double(-1e-3), ctypes.c_double(1e-3))
+    put("clip_grad_value_f32_100M", 8 * na, clock.kernel_us(f), clock.call_us(f))
+    del gr, tg
+    torch.cuda.empty_cache()
+
+    # ---- per-feature transforms, [1M, 64] f64, device pointers
+    TB, TF = 1 << 20, 64
+    D = torch.randn(TB, TF, device=dev, dtype=torch.float64, generator=g) * 2 + 1
+    O = torch.empty_like(D)
+    st = [torch.empty(TF, device=dev, dtype=torch.float64) for _ in range(4)]
+    torch.cuda.synchronize()
+    f = lambda: _lib.transform_compute_stats(D.data_ptr(), TB, TF, *[t.data_ptr() for t in st])
+    put("transform_compute_stats_f64_1Mx64", 8 * TB * TF, clock.kernel_us(f), clock.call_us(f))
+    f = lambda: _lib.transform_normalize(D.data_ptr(), O.data_ptr(), TB, TF, st[0].data_ptr(), st[1].data_ptr(),
+                                         ctypes.c_double(1e-8))
+    put("transform_normalize_f64_1Mx64", 16 * TB * TF, clock.kernel_us(f), clock.call_us(f))
+    del D, O, st
+    torch.cuda.empty_cache()
+
+    # ---- the rest of the quantization API: percentile calibration (64M f64)
+    # and the int8 product (4096^3, device pointers)
+    P = torch.randn(1 << 26, device=dev, dtype=torch.float64, generator=g)
+    qp = QuantParamsC()
+    torch.cuda.synchronize()
+    put("calibrate_percentile_f64_64M", 8 * P.numel(), None, clock.call_us(
+        lambda: _lib.calibrate_percentile(P.data_ptr(), P.numel(), ctypes.c_double(0.01), 1, ctypes.byref(qp))))
+    del P
+    m = 4096
+    A8 = torch.randint(-128, 128, (m, m), dtype=torch.int8, device=dev, generator=g)
+    B8 = torch.randint(-128, 128, (m, m), dtype=torch.int8, device=dev, generator=g)
+    C8 = torch.empty(m, m, dtype=torch.float64, device=dev)
+    pa, pb = QuantParamsC(), QuantParamsC()
+    pa.scale, pa.zero_point, pb.scale, pb.zero_point = 0.013, -7, 0.37, 11
+    torch.cuda.synchronize()
+    us = clock.call_us(lambda: _lib.quantized_matmul(A8.data_ptr(), B8.data_ptr(), C8.data_ptr(), m, m, m,
+                                                     ctypes.byref(pa), ctypes.byref(pb)))
+    res["quantized_matmul_4096^3"] = {"call_us": round(us, 2), "int8_TOPS": round(2.0 * m ** 3 / us / 1e6, 1)}
+    del A8, B8, C8
+    torch.cuda.empty_cache()
+    return res
 
 
 if __name__ == "__main__":

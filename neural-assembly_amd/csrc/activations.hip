@@ -427,6 +427,7 @@ static int act_selu_impl(void *out, const void *in) { return act2<ASelu>(out, in
 // the result equals neural_bias_add followed by the activation bit for bit.
 template <class F32, class F64>
 struct OpAddAct {
+    using F32T = F32;
     F32 f32;
     F64 f64;
     NH_DEV float operator()(float x, float b) const { return f32(x + b); }

@@ -144,9 +144,14 @@ NH_DEV int wave_excl_prefix_small(int c, int &total)
     return pre;
 }
 
-template <typename F>
+// ROW: the input element is x + bias[column] in float (the rounding
+// neural_bias_add does), [rows, ncv] vectors with the bias vector of `ncv`;
+// a lane's column vector index is found once by a division and then advanced
+// by d1 = 256 mod ncv per vector and dS = grid stride mod ncv per tile.
+template <typename F, bool ROW = false>
 __global__ __launch_bounds__(kBlock) void k_map1_f32_tail(const float *__restrict__ a, float *__restrict__ o,
-                                                          int64_t n, F f)
+                                                          int64_t n, F f, const float *__restrict__ bias = nullptr,
+                                                          int64_t ncv = 1, int64_t d1 = 0, int64_t dS = 0)
 {
     constexpr int U = kTailUnroll;
     constexpr int PL = U * 4;  // elements per lane per tile
@@ -156,14 +161,26 @@ __global__ __launch_bounds__(kBlock) void k_map1_f32_tail(const float *__restric
     const int lane = threadIdx.x & 63;
     const int64_t nv = n / 4;
     const f32x4 *av = reinterpret_cast<const f32x4 *>(a);
+    const f32x4 *bv = reinterpret_cast<const f32x4 *>(bias);
     f32x4 *ov = reinterpret_cast<f32x4 *>(o);
     const int64_t tile = int64_t(kBlock) * U;
+    int64_t c = ROW ? (int64_t(blockIdx.x) * tile + threadIdx.x) % ncv : 0;
     for (int64_t t0 = int64_t(blockIdx.x) * tile; t0 < nv; t0 += int64_t(gridDim.x) * tile) {
         f32x4 x[U], r[U];
+        int64_t cc = c;
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int64_t i = t0 + int64_t(u) * kBlock + threadIdx.x;
             x[u] = i < nv ? ld_nt(av + i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            if constexpr (ROW) {
+                if (i < nv) x[u] = x[u] + bv[cc];
+                cc += d1;
+                cc = cc >= ncv ? cc - ncv : cc;
+            }
+        }
+        if constexpr (ROW) {
+            c += dS;
+            c = c >= ncv ? c - ncv : c;
         }
         uint32_t nm = 0;  // bit u*4+k: element k of vector u needs the tail
 #pragma unroll
@@ -375,7 +392,26 @@ int launch_map1_f32_tail(const float *a, float *o, int64_t n, F f)
     int64_t g = ceil_div(n / 4, int64_t(kBlock) * kTailUnroll);
     const int64_t cap = kMaxGridBlocks;
     g = g > cap ? cap : (g < 1 ? 1 : g);
-    NH_LAUNCH((k_map1_f32_tail<F>), dim3(unsigned(g)), dim3(kBlock), 0, stream(), a, o, n, f);
+    NH_LAUNCH((k_map1_f32_tail<F>), dim3(unsigned(g)), dim3(kBlock), 0, stream(), a, o, n, f, nullptr,
+              int64_t(1), int64_t(0), int64_t(0));
+    return check_launch();
+}
+
+// The same over x [rows, cols] + bias [cols] (cols % 4 == 0, all 16-byte aligned):
+// the fused bias add + activation for head/tail activations.
+template <typename F>
+int launch_rowbcast_f32_tail(const float *x, const float *bias, float *o, int64_t rows, int64_t cols, F f)
+{
+    const int64_t ncv = cols / 4;
+    if (rows <= 0 || ncv <= 0) return NEURAL_OK;
+    const int64_t n = rows * cols;
+    int64_t g = ceil_div(n / 4, int64_t(kBlock) * kTailUnroll);
+    const int64_t cap = kMaxGridBlocks;
+    g = g > cap ? cap : (g < 1 ? 1 : g);
+    const int64_t d1 = int64_t(kBlock) % ncv;
+    const int64_t dS = (g * kBlock * kTailUnroll) % ncv;
+    NH_LAUNCH((k_map1_f32_tail<F, true>), dim3(unsigned(g)), dim3(kBlock), 0, stream(), x, o, n, f, bias, ncv,
+              d1, dS);
     return check_launch();
 }
 
@@ -460,6 +496,12 @@ inline bool row_broadcast_case(const NeuralTensor *out, const NeuralTensor *a, c
     return C % vn == 0;
 }
 
+// Binary ops that apply a head/tail f32 functor to a + b (the fused bias add +
+// activation, whose f32 member declares kHeadTail) take the queued-tail kernel
+// in the row-broadcast case.
+template <typename Op, typename = void> struct RowHeadTail : std::false_type {};
+template <typename Op> struct RowHeadTail<Op, std::void_t<decltype(Op::F32T::kHeadTail)>> : std::true_type {};
+
 template <typename T, typename Op>
 int launch_binary(NeuralTensor *out, const NeuralTensor *a, const NeuralTensor *b, const void *pa,
                          const void *pb, void *po, Op op)
@@ -472,6 +514,8 @@ int launch_binary(NeuralTensor *out, const NeuralTensor *a, const NeuralTensor *
         return launch_map2_flat(A, B, O, n, op);
     if (row_broadcast_case(out, a, b) && aligned16(A) && aligned16(B) && aligned16(O)) {
         const int64_t C = out->shape[out->ndim - 1];
+        if constexpr (std::is_same<T, float>::value && RowHeadTail<Op>::value)
+            return launch_rowbcast_f32_tail(A, B, O, n / C, C, op.f32);
         return launch_rowbcast(A, B, O, n / C, C, op);
     }
     ND4 d;
