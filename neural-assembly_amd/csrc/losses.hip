@@ -382,22 +382,30 @@ static int ce_run(const T *x, const int64_t *tidx, const T *tval, int64_t rows, 
     }
     CeArgs a{tidx, tval, rows, cols, alpha, 1.0 / double(rows), row_loss, row_s, grad_dev, bad};
     int rc = launch_ce<T, MODE>(x, a);
+    // The loss sum's launch stores a ticket after the sum (and after the CE
+    // kernel, earlier on the stream, has set the flag or not): the host waits
+    // for the ticket instead of synchronising the stream.
+    const Ticket tk = want_loss ? next_ticket() : Ticket{};
     if (rc == NEURAL_OK && want_loss) {
+        void *dst = ws.host_result_dev;
         if (MODE == CE_ASM) {
-            rc = launch_reduce_full(row_loss, rows, RedCeLoss<sizeof(T) == 4>{}, ws.host_result_dev);
+            rc = launch_reduce(row_loss, 1, rows, rows, RedCeLoss<sizeof(T) == 4>{}, dst, nullptr, 0, tk);
         } else {
             const double st0 = alpha / double(cols), st1 = st0 + (1.0 - alpha);
-            rc = launch_reduce_full(row_loss, rows, RedLsLoss{row_s, st0 * double(cols - 1) + st1},
-                                    ws.host_result_dev);
+            rc = launch_reduce(row_loss, 1, rows, rows, RedLsLoss{row_s, st0 * double(cols - 1) + st1}, dst,
+                               nullptr, 0, tk);
         }
     }
     struct { double sum; int pad[30]; int bad; } res;  // result area layout: sum at 0, flag at word 32
     static_assert(sizeof(res) == 136, "");
-    if (rc == NEURAL_OK) rc = host_result_fetch(&res, sizeof(res));
+    if (rc == NEURAL_OK)
+        rc = want_loss ? host_result_wait(tk.value, &res, sizeof(res)) : host_result_fetch(&res, sizeof(res));
     if (row_loss) dev_free(row_loss);
     if (rc != NEURAL_OK) return rc;
     if (res.bad) {
-        static_cast<int *>(ws.host_result)[32] = 0;  // the stream is idle: host_result_fetch synchronised it
+        // every launch of this call has finished writing the area (the
+        // ticket, or the stream wait, comes after them)
+        static_cast<int *>(ws.host_result)[32] = 0;
         return NEURAL_ERR_INVALID_ARGUMENT;
     }
     if (want_loss && loss_host) *loss_host = res.sum / double(rows);
