@@ -25,11 +25,13 @@
 // anchor window W = r[A .. A+30] any later value is r[A + k] = sum_m c_m W[m]
 // with c = x^k mod P(x), P(x) = x^31 - x^28 - 1, coefficients mod 2^32.
 // The n draws of a call are cut into segments of L = 248 draws (8 periods
-// of 31).  c_j = x^(jL) mod P is a device table computed once.  Segment j's
-// starting window is w_j[t] = r[A + jL + t] = sum_m c_j[m] G[m + t] with
-// G = r[A .. A+61] (the anchor window and the 31 values after it): for 64
-// segments at a time a [64 x 32] x [32 x 32] product mod 2^32, done on the
-// matrix cores (int8 MFMA over signed byte limbs, below).  Thread j then runs
+// of 31), 64 segments per wave.  Segment j = 64 w + l starts at
+// A + jL; its starting window is reached in two linear steps: the 62 values
+// G_w = r[A + 64 w L ..] from R = r[A .. A+92] and e_w = x^(64 w L) mod P (a
+// device table, 128 bytes per wave), then w_j[t] = sum_m d_l[m] G_w[m + t]
+// with d_l = x^(lL) mod P, the same 64 rows for every wave: a [64 x 32] x
+// [32 x 32] product mod 2^32, done on the matrix cores (int8 MFMA over signed
+// byte limbs, below).  Thread j then runs
 // the recurrence for its 248 draws with the 31-value ring in registers and
 // packs keep bits into 8 words.  A second, streaming kernel reads x in
 // 16-byte vectors, the 4 keep bits of each vector, and writes out and the
@@ -184,64 +186,94 @@ NH_DEV void gen_segment(uint32_t (&w)[kLag], int64_t d0, int64_t n, uint32_t thr
     if (have > 0) bits[word] = uint32_t(acc);  // only when L is not a multiple of 32
 }
 
-// One thread per segment, 64 segments per wave.  X31 holds x^(31+i) mod P
-// for i < 31 (G[31 + i] = sum_m X31[i][m] W[m]).  Every wave of the grid
-// has table rows (the table covers a multiple of 256 segments >= nseg), so
-// all waves run the jump and reach every barrier; threads past nseg stop
-// before generating.
-__global__ __launch_bounds__(kDBlock) void k_dropout_bits(const uint64_t *__restrict__ TL,
-                                                           const uint32_t *__restrict__ X31,
+// x^(64 w L) mod P for w in [w0, w1): the jump of wave w's first segment,
+// 32 words per wave (word 31 = 0), square-and-multiply over the host-made
+// powers B[k] = x^(64 L 2^k) mod P.
+__global__ __launch_bounds__(kDBlock) void k_wave_jumps(uint32_t *__restrict__ E, int64_t w0, int64_t w1,
+                                                         const uint32_t *__restrict__ B)
+{
+    const int64_t w = w0 + int64_t(blockIdx.x) * kDBlock + threadIdx.x;
+    if (w >= w1) return;
+    uint32_t c[kLag];
+#pragma unroll
+    for (int i = 0; i < kLag; i++) c[i] = i == 0 ? 1u : 0u;
+    for (int k = 0; k < 63 && (w >> k) != 0; k++)
+        if ((w >> k) & 1) dpoly_mul(c, B + k * kLag);
+    uint32_t *row = E + w * 32;
+#pragma unroll
+    for (int i = 0; i < kLag; i++) row[i] = c[i];
+    row[kLag] = 0u;
+}
+
+// One thread per segment, 64 segments per wave, the jump in two steps:
+//   1. wave w's base values G_w[i] = r[A + 64 w L + i], i < 62, from
+//      R = r[A .. A+92] (the anchor window and the 62 values after it, by
+//      X62[i] = x^(31+i) mod P) and e_w = x^(64 w L) mod P (E, 128 bytes per
+//      wave): G_w[i] = sum_m e_w[m] R[i + m], one lane per i;
+//   2. lane l's window w[t] = r[A + (64 w + l) L + t] = sum_m d_l[m] G_w[m + t]
+//      with d_l = x^(l L) mod P, the same 64 rows for every wave (D, digits in
+//      the MFMA A-operand layout, 8 KB): a [64 x 32] x [32 x 32] product mod
+//      2^32 on the matrix cores, B = the Hankel digits of G_w.
+// The per-segment table reads of a single-step jump (128 bytes per segment)
+// become 128 bytes per 64 segments.  E covers every wave of the grid, so all
+// waves run the jump and reach every barrier; threads past nseg stop before
+// generating.
+__global__ __launch_bounds__(kDBlock) void k_dropout_bits(const uint64_t *__restrict__ D,
+                                                           const uint32_t *__restrict__ E,
+                                                           const uint32_t *__restrict__ X62,
                                                            const uint32_t *__restrict__ W, uint32_t *__restrict__ Wn,
                                                            int64_t n, int64_t nseg, uint32_t thr,
                                                            uint32_t *__restrict__ bits)
 {
-    __shared__ uint32_t sG[64];
-    __shared__ uint64_t sB[8][64];
+    __shared__ uint32_t sR[3 * kLag + 3];                // r[A .. A+92], 3 pad words
+    __shared__ uint32_t sGw[kDBlock / 64][64];          // per wave: G_w (62 values, 2 zeros)
     __shared__ uint32_t sX[kDBlock / 64][32 * kLag];  // per wave: one tile's 32 windows, row stride 31 (odd: no bank conflicts)
     const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     if (blockIdx.x == 0 && tid < kLag && n + tid < kLag)
         Wn[tid] = W[n + tid];  // calls shorter than 31 draws keep part of the old window
-    // G = r[A .. A+61] (G[62], G[63] = 0: they meet only padding coefficients)
-    if (tid < 64) {
+    if (tid < 3 * kLag + 3) {
         uint32_t g = 0u;
         if (tid < kLag) {
             g = W[tid];
-        } else if (tid < 2 * kLag) {
-            for (int m = 0; m < kLag; m++) g += X31[(tid - kLag) * kLag + m] * W[m];
+        } else if (tid < 3 * kLag) {
+            for (int m = 0; m < kLag; m++) g += X62[(tid - kLag) * kLag + m] * W[m];
         }
-        sG[tid] = g;
+        sR[tid] = g;
     }
     __syncthreads();
-    // B operands, the same for every wave: digits of H[m][t] = G[m + t]
-    if (tid < 64) {
-        const int t = tid & 31, h = tid >> 5;
+    const int64_t wave = int64_t(blockIdx.x) * (kDBlock / 64) + wv;
+    {
+        const uint32_t *e = E + wave * 32;  // uniform per wave
+        uint32_t g = 0u;
+        if (lane < 2 * kLag) {
+#pragma unroll
+            for (int m = 0; m < kLag; m++) g += e[m] * sR[lane + m];
+        }
+        sGw[wv][lane] = g;
+    }
+    __syncthreads();
+    // B operands of this wave: digits of H[m][t] = G_w[m + t]
+    long Bq[4][2];
+    {
+        const int t = lane & 31, h = lane >> 5;
 #pragma unroll
         for (int cc = 0; cc < 2; cc++) {
             uint64_t q[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
             for (int b = 0; b < 8; b++) {
                 uint32_t l[4];
-                limbs4(sG[16 * cc + 8 * h + b + t], l);
+                limbs4(sGw[wv][16 * cc + 8 * h + b + t], l);
 #pragma unroll
                 for (int p = 0; p < 4; p++) q[p] |= uint64_t(l[p]) << (8 * b);
             }
 #pragma unroll
-            for (int p = 0; p < 4; p++) sB[p * 2 + cc][tid] = q[p];
+            for (int p = 0; p < 4; p++) Bq[p][cc] = long(q[p]);
         }
     }
-    __syncthreads();
-    long Bq[4][2];
-#pragma unroll
-    for (int p = 0; p < 4; p++)
-#pragma unroll
-        for (int cc = 0; cc < 2; cc++) Bq[p][cc] = long(sB[p * 2 + cc][lane]);
-    const int64_t wave = (int64_t(blockIdx.x) * kDBlock + tid) >> 6;
-    const uint64_t *tw = TL + wave * kTabWordsPerWave;
-    uint32_t *X = sX[tid >> 6];
+    uint32_t *X = sX[wv];
     // Two 32-segment tiles, transposed through LDS one at a time; one
     // accumulator at a time (D_0 .. D_3 folded into `out` as they finish).
-    // Registers and LDS stay low enough for 5+ waves per SIMD, which the
-    // recurrence below needs to issue at full rate.
     uint32_t w[kLag];
 #pragma unroll
     for (int T = 0; T < 2; T++) {
@@ -249,7 +281,7 @@ __global__ __launch_bounds__(kDBlock) void k_dropout_bits(const uint64_t *__rest
 #pragma unroll
         for (int p = 0; p < 4; p++)
 #pragma unroll
-            for (int cc = 0; cc < 2; cc++) A[p][cc] = long(tw[T * 512 + (p * 2 + cc) * 64 + lane]);
+            for (int cc = 0; cc < 2; cc++) A[p][cc] = long(D[T * 512 + (p * 2 + cc) * 64 + lane]);
         uint32_t out[16];
 #pragma unroll
         for (int s = 0; s < 4; s++) {
@@ -438,10 +470,11 @@ struct Stream {
     bool ready = false;
     uint32_t *win[2] = {nullptr, nullptr};  // device windows (current, next)
     int cur = 0;
-    uint64_t *table = nullptr;              // c_j = x^(jL) mod P as MFMA digits, 16 words per segment
-    int64_t table_n = 0;                    // segments covered (a power of two >= 1024)
-    uint32_t *powers = nullptr;             // B[k] = x^(L 2^k) mod P, k < 63
-    uint32_t *x31 = nullptr;                // x^(31+i) mod P, i < 31
+    uint64_t *dig = nullptr;                // d_l = x^(lL) mod P, l < 64, as MFMA digits (1024 words)
+    uint32_t *ejump = nullptr;              // e_w = x^(64 w L) mod P, 32 words per wave
+    int64_t ejump_n = 0;                    // waves covered (a power of two >= 1024)
+    uint32_t *wpowers = nullptr;            // x^(64 L 2^k) mod P, k < 63
+    uint32_t *x62 = nullptr;                // x^(31+i) mod P, i < 62
     uint32_t *bits = nullptr;
     size_t bits_cap = 0;
     uint64_t drawn = 0;                     // draws since the last seed
@@ -470,48 +503,54 @@ int ensure_stream_locked(Stream &s)
         s.win[i] = static_cast<uint32_t *>(dev_alloc(kLag * sizeof(uint32_t)));
         if (!s.win[i]) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
     }
-    std::vector<uint32_t> B(size_t(63) * kLag);
-    HPoly p = hpoly_xpow(uint64_t(kSegL));
+    // x^(L 2^k) for the 64-row digit table, x^(64 L 2^k) for the wave jumps
+    std::vector<uint32_t> B(size_t(63) * kLag), B64(size_t(63) * kLag);
+    HPoly p = hpoly_xpow(uint64_t(kSegL)), p64 = hpoly_xpow(uint64_t(64 * kSegL));
     for (int k = 0; k < 63; k++) {
         std::memcpy(B.data() + size_t(k) * kLag, p.data(), kLag * sizeof(uint32_t));
+        std::memcpy(B64.data() + size_t(k) * kLag, p64.data(), kLag * sizeof(uint32_t));
         p = hpoly_mul(p, p);
+        p64 = hpoly_mul(p64, p64);
     }
-    s.powers = static_cast<uint32_t *>(dev_alloc(B.size() * sizeof(uint32_t)));
-    if (!s.powers) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
-    NH_HIP(hipMemcpy(s.powers, B.data(), B.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
-    std::vector<uint32_t> X(size_t(kLag) * kLag);
-    for (int i = 0; i < kLag; i++) {
+    uint32_t *powers = static_cast<uint32_t *>(dev_alloc(B.size() * sizeof(uint32_t)));
+    s.wpowers = static_cast<uint32_t *>(dev_alloc(B64.size() * sizeof(uint32_t)));
+    s.dig = static_cast<uint64_t *>(dev_alloc(kTabWordsPerWave * sizeof(uint64_t)));
+    if (!powers || !s.wpowers || !s.dig) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
+    NH_HIP(hipMemcpy(powers, B.data(), B.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
+    NH_HIP(hipMemcpy(s.wpowers, B64.data(), B64.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
+    NH_LAUNCH(k_jump_table, dim3(1), dim3(kDBlock), 0, stream(), s.dig, int64_t(0), int64_t(64), powers);
+    NH_TRY(check_launch());
+    dev_free(powers);  // stream-ordered: reused only by later work on the stream
+    std::vector<uint32_t> X(size_t(2 * kLag) * kLag);
+    for (int i = 0; i < 2 * kLag; i++) {
         const HPoly c = hpoly_xpow(uint64_t(kLag + i));
         std::memcpy(X.data() + size_t(i) * kLag, c.data(), kLag * sizeof(uint32_t));
     }
-    s.x31 = static_cast<uint32_t *>(dev_alloc(X.size() * sizeof(uint32_t)));
-    if (!s.x31) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
-    NH_HIP(hipMemcpy(s.x31, X.data(), X.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
+    s.x62 = static_cast<uint32_t *>(dev_alloc(X.size() * sizeof(uint32_t)));
+    if (!s.x62) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
+    NH_HIP(hipMemcpy(s.x62, X.data(), X.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
     s.ready = true;
     return set_seed_locked(s, 1u);  // glibc's initial state is srand(1)
 }
 
-// Grow the jump table to cover nseg segments (doubling; old entries kept).
-int ensure_table_locked(Stream &s, int64_t nseg)
+// Grow the wave-jump table to cover nwaves waves (doubling; old entries kept).
+int ensure_jumps_locked(Stream &s, int64_t nwaves)
 {
-    if (nseg <= s.table_n) return NEURAL_OK;
-    int64_t cap = s.table_n > 0 ? s.table_n : 1024;
-    while (cap < nseg) cap *= 2;
-    // 16 words per segment; a wave block's rows are contiguous, so the old
-    // table is a prefix of the new one
-    const size_t per_seg = kTabWordsPerWave / 64;
-    uint64_t *t = static_cast<uint64_t *>(dev_alloc(size_t(cap) * per_seg * sizeof(uint64_t)));
+    if (nwaves <= s.ejump_n) return NEURAL_OK;
+    int64_t cap = s.ejump_n > 0 ? s.ejump_n : 1024;
+    while (cap < nwaves) cap *= 2;
+    uint32_t *t = static_cast<uint32_t *>(dev_alloc(size_t(cap) * 32 * sizeof(uint32_t)));
     if (!t) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
-    if (s.table_n > 0)
-        NH_HIP(hipMemcpyAsync(t, s.table, size_t(s.table_n) * per_seg * sizeof(uint64_t), hipMemcpyDeviceToDevice,
+    if (s.ejump_n > 0)
+        NH_HIP(hipMemcpyAsync(t, s.ejump, size_t(s.ejump_n) * 32 * sizeof(uint32_t), hipMemcpyDeviceToDevice,
                               stream()));
-    const int64_t fresh = cap - s.table_n;
-    NH_LAUNCH(k_jump_table, dim3(unsigned(ceil_div(fresh, kDBlock))), dim3(kDBlock), 0, stream(), t,
-                       s.table_n, cap, s.powers);
+    const int64_t fresh = cap - s.ejump_n;
+    NH_LAUNCH(k_wave_jumps, dim3(unsigned(ceil_div(fresh, kDBlock))), dim3(kDBlock), 0, stream(), t, s.ejump_n,
+              cap, s.wpowers);
     NH_TRY(check_launch());
-    if (s.table) dev_free(s.table);
-    s.table = t;
-    s.table_n = cap;
+    if (s.ejump) dev_free(s.ejump);
+    s.ejump = t;
+    s.ejump_n = cap;
     return NEURAL_OK;
 }
 
@@ -548,7 +587,8 @@ static int dropout_fwd(const float *in, float *out, uint8_t *mask, uint64_t n, f
     NH_TRY(ensure_stream_locked(s));
     const int64_t nn = int64_t(n);
     const int64_t nseg = ceil_div(nn, kSegL);
-    NH_TRY(ensure_table_locked(s, nseg));
+    // every wave of the grid (ceil(nseg / 256) blocks of 4) has a wave jump
+    NH_TRY(ensure_jumps_locked(s, ceil_div(nseg, kDBlock) * (kDBlock / 64)));
     const size_t words = size_t(nseg) * kSegWords;
     if (words > s.bits_cap) {
         if (s.bits) dev_free(s.bits);
@@ -565,10 +605,8 @@ static int dropout_fwd(const float *in, float *out, uint8_t *mask, uint64_t n, f
     NH_TRY(xo.open(out, size_t(n) * 4, false));
     NH_TRY(xm.open(mask, size_t(n), false));
     uint32_t *W = s.win[s.cur], *Wn = s.win[s.cur ^ 1];
-    // the grid covers ceil(nseg / 256) * 256 <= table_n segments (table_n is a
-    // power of two >= 1024), so every wave reads existing table rows
-    NH_LAUNCH(k_dropout_bits, dim3(unsigned(ceil_div(nseg, kDBlock))), dim3(kDBlock), 0, stream(), s.table,
-                       s.x31, W, Wn, nn, nseg, thr, s.bits);
+    NH_LAUNCH(k_dropout_bits, dim3(unsigned(ceil_div(nseg, kDBlock))), dim3(kDBlock), 0, stream(), s.dig,
+              s.ejump, s.x62, W, Wn, nn, nseg, thr, s.bits);
     NH_TRY(check_launch());
     s.cur ^= 1;
     s.drawn += n;
