@@ -35,8 +35,9 @@
 // the recurrence for its 248 draws with the 31-value ring in registers and
 // packs keep bits into 8 words.  A second, streaming kernel reads x in
 // 16-byte vectors, the 4 keep bits of each vector, and writes out and the
-// mask bytes (9 B per element).  The window after the call (r at A + n ..
-// A + n + 30) is written by the threads that generate the last 31 draws.
+// mask bytes (9 B per element).  The stream values after the call (r at
+// A + n .. A + n + 92, the next call's R) are written by the threads that
+// generate draws n - 31 .. n + 61 (the call generates 62 draws past n).
 #include <cmath>
 #include <cstring>
 #include <mutex>
@@ -56,6 +57,9 @@ constexpr int kPeriods = 8;
 constexpr int64_t kSegL = int64_t(kLag) * kPeriods;   // 248 draws per thread segment (a multiple of 4)
 constexpr int kSegWords = int((kSegL + 31) / 32);      // keep-bit words per segment (8)
 constexpr int kDBlock = 256;
+// Stream values kept between calls: r[A .. A+92], the anchor window and the
+// 62 values after it (the first jump step reads all 93).
+constexpr int kWin = 3 * kLag;
 
 // ---- polynomials mod P(x) = x^31 - x^28 - 1 over Z / 2^32 ------------------------------
 
@@ -83,14 +87,23 @@ NH_DEV void dpoly_mul(uint32_t (&a)[kLag], const uint32_t *__restrict__ b)
 //
 // A 32-bit value is split into balanced base-256 digits, v = sum_p l_p 256^p
 // (mod 2^32) with l_p in [-128, 127], so that products of digits fit the
-// signed int8 inputs of v_mfma_i32_32x32x16_i8.  For C (segments x m) and
+// signed int8 inputs of v_mfma_i32_32x32x32_i8.  For C (segments x m) and
 // H (m x t): C H = sum_{p+q <= 3} 256^(p+q) C_p H_q (mod 2^32) -- the
 // digit products with p + q >= 4 vanish mod 2^32.  Each D_s = sum_{p+q=s}
 // C_p H_q is exact in int32 (32 (s+1) terms of magnitude <= 2^14).
-// Operand layout of the 32x32x16 int8 MFMA: lane l holds row l % 32 of A
-// and column l % 32 of B, k = 8 (l / 32) + b for byte b of the 64-bit
-// operand; the 16 results of lane l are D[8 (v/4) + 4 (l/32) + v % 4][l % 32].
+// Operand layout: lane l holds row l % 32 of A and column l % 32 of B, 16
+// bytes each; the tables below store them as two 8-byte halves, coefficient
+// m = 16 c + 8 (l / 32) + b in byte b of half c (m = 31 is padding, 0).  A
+// and B place the same m at the same (lane half, byte), so the product sums
+// every m once.  The 16 results of lane l are D[8 (v/4) + 4 (l/32) + v % 4][l % 32].
 typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Two 8-byte operand halves as the 16-byte operand of the K = 32 form.
+NH_DEV i32x4 pack_k32(uint64_t lo, uint64_t hi)
+{
+    return i32x4{int(uint32_t(lo)), int(uint32_t(lo >> 32)), int(uint32_t(hi)), int(uint32_t(hi >> 32))};
+}
 
 // Balanced base-256 digits of v, each as the low byte of l[p].
 __host__ __device__ inline void limbs4(uint32_t v, uint32_t (&l)[4])
@@ -144,19 +157,22 @@ __global__ __launch_bounds__(kDBlock) void k_jump_table(uint64_t *__restrict__ T
 }
 
 // Generate the keep bits of segment j.  W is the anchor window, Wn receives
-// the window after the call.  keep = (r >> 1) >= thr, taken as the sign bit of
-// thr_m1 - (r >> 1) with thr_m1 = thr - 1 (mod 2^32; both sides fit in 32 bits,
-// and thr = 0 keeps every draw): no compare, so no chain through VCC.  One
-// funnel shift (alignbit: (kb << 1) | (x >> 31)) moves each sign bit into the
-// period's word, first draw highest -- four instructions per draw with the
-// recurrence add -- and a bit reversal per period puts draw u at bit u.
-// One period of 31 draws
+// the window after the call.  keep = (r >> 1) >= thr = (r > 2 thr - 1) for
+// thr in [1, 2^31] (ALL: thr = 0, every draw kept): one subtraction
+// t2m1 - r whose borrow is the keep bit, and one add-with-carry kb + kb +
+// borrow that shifts it into the period's word, first draw highest -- three
+// instructions per draw with the recurrence add (a sign-bit and funnel-shift
+// form, add + shift + subtract + v_alignbit_b32, measured 1.6x slower in a
+// probe of the ring alone) -- and a bit reversal per period puts draw u at
+// bit u.  The pair goes through VCC, written as inline assembly because the
+// compiler turns the C form (kb + kb + (r > t2m1)) into a compare, a select
+// and shifts.  One period of 31 draws
 // is unrolled (ring slots are then registers) and the period loop is not:
 // the fully unrolled segment is ~50 KB of straight-line code, and fetching it
 // cold made the kernel instruction-fetch bound (measured 4x slower).
-template <bool TAIL>
-NH_DEV void gen_segment(uint32_t (&w)[kLag], int64_t d0, int64_t n, uint32_t thr_m1, uint32_t *__restrict__ bits,
-                        uint32_t *__restrict__ Wn)
+template <bool ALL>
+NH_DEV void gen_segment(uint32_t (&w)[kLag], int64_t d0, int64_t n, uint32_t t2m1, uint32_t *__restrict__ bits,
+                        uint32_t *__restrict__ Wn, bool tail, int klo)
 {
     uint64_t acc = 0u;  // pending keep bits; the low `have` are valid
     int have = 0;
@@ -168,10 +184,25 @@ NH_DEV void gen_segment(uint32_t (&w)[kLag], int64_t d0, int64_t n, uint32_t thr
         for (int u = 0; u < kLag; u++) {
             const uint32_t r = w[u] + w[(u + 28) % kLag];
             w[u] = r;
-            kb = __builtin_amdgcn_alignbit(kb, thr_m1 - (r >> 1), 31u);
-            if constexpr (TAIL) {
-                const int64_t d = d0 + int64_t(per) * kLag + u;
-                if (d < n && d >= n - kLag) Wn[d - (n - kLag)] = r;
+            if constexpr (ALL) {
+                kb = (kb << 1) | 1u;
+            } else {
+                uint32_t diff;
+                asm volatile("v_sub_co_u32 %1, vcc, %2, %3\n\tv_addc_co_u32 %0, vcc, %0, %0, vcc"
+                             : "+v"(kb), "=&v"(diff)
+                             : "s"(t2m1), "v"(r)
+                             : "vcc");
+            }
+        }
+        // the segments that hold draws n - 31 .. n + 61 store them (ring slot
+        // u now holds draw p0 + u) as the next call's 93 values; slots below
+        // klo carry over from this call's values (block 0 copies them)
+        const int64_t off = d0 + int64_t(per) * kLag - (n - kLag);  // slot 0's place in Wn
+        if (tail && off > -kLag && off < kWin) {
+#pragma unroll
+            for (int u = 0; u < kLag; u++) {
+                const int k = int(off) + u;
+                if (k >= klo && k < kWin) Wn[k] = w[u];
             }
         }
         const uint32_t pb = __builtin_bitreverse32(kb) >> 1;  // draw u at bit u
@@ -207,40 +238,38 @@ __global__ __launch_bounds__(kDBlock) void k_wave_jumps(uint32_t *__restrict__ E
 
 // One thread per segment, 64 segments per wave, the jump in two steps:
 //   1. wave w's base values G_w[i] = r[A + 64 w L + i], i < 62, from
-//      R = r[A .. A+92] (the anchor window and the 62 values after it, by
-//      X62[i] = x^(31+i) mod P) and e_w = x^(64 w L) mod P (E, 128 bytes per
-//      wave): G_w[i] = sum_m e_w[m] R[i + m], one lane per i;
+//      R = r[A .. A+92] (W: the 93 values the previous call, or the seed,
+//      left) and e_w = x^(64 w L) mod P (E, 128 bytes per wave):
+//      G_w[i] = sum_m e_w[m] R[i + m], one lane per i;
 //   2. lane l's window w[t] = r[A + (64 w + l) L + t] = sum_m d_l[m] G_w[m + t]
 //      with d_l = x^(l L) mod P, the same 64 rows for every wave (D, digits in
 //      the MFMA A-operand layout, 8 KB): a [64 x 32] x [32 x 32] product mod
 //      2^32 on the matrix cores, B = the Hankel digits of G_w.
 // The per-segment table reads of a single-step jump (128 bytes per segment)
-// become 128 bytes per 64 segments.  E covers every wave of the grid, so all
+// become 128 bytes per 64 segments; D is staged in LDS once per block.  The
+// segments cover draws 0 .. n + 61 (nseg of them), so that the next call's
+// 93 values are generated here.  E covers every wave of the grid, so all
 // waves run the jump and reach every barrier; threads past nseg stop before
 // generating.
+template <bool ALL>
 __global__ __launch_bounds__(kDBlock) void k_dropout_bits(const uint64_t *__restrict__ D,
                                                            const uint32_t *__restrict__ E,
-                                                           const uint32_t *__restrict__ X62,
                                                            const uint32_t *__restrict__ W, uint32_t *__restrict__ Wn,
-                                                           int64_t n, int64_t nseg, uint32_t thr,
+                                                           int64_t n, int64_t nseg, uint32_t t2m1,
                                                            uint32_t *__restrict__ bits)
 {
-    __shared__ uint32_t sR[3 * kLag + 3];                // r[A .. A+92], 3 pad words
-    __shared__ uint32_t sGw[kDBlock / 64][64];          // per wave: G_w (62 values, 2 zeros)
+    __shared__ uint64_t sD[kTabWordsPerWave];           // the 64-row digit table
+    __shared__ uint32_t sR[kWin];                        // r[A .. A+92]
+    __shared__ uint32_t sGd[kDBlock / 64][4][16];       // per wave: byte i of row p = digit p of G_w[i]
     __shared__ uint32_t sX[kDBlock / 64][32 * kLag];  // per wave: one tile's 32 windows, row stride 31 (odd: no bank conflicts)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    if (blockIdx.x == 0 && tid < kLag && n + tid < kLag)
-        Wn[tid] = W[n + tid];  // calls shorter than 31 draws keep part of the old window
-    if (tid < 3 * kLag + 3) {
-        uint32_t g = 0u;
-        if (tid < kLag) {
-            g = W[tid];
-        } else if (tid < 3 * kLag) {
-            for (int m = 0; m < kLag; m++) g += X62[(tid - kLag) * kLag + m] * W[m];
-        }
-        sR[tid] = g;
-    }
+    // the next call's values r[A + n + k] for n + k < 93 are this call's
+    const int klo = n < kWin ? int(kWin - n) : 0;
+    if (blockIdx.x == 0 && tid < klo) Wn[tid] = W[n + tid];
+    if (tid < kWin) sR[tid] = W[tid];
+#pragma unroll
+    for (int i = 0; i < kTabWordsPerWave / kDBlock; i++) sD[i * kDBlock + tid] = D[i * kDBlock + tid];
     __syncthreads();
     const int64_t wave = int64_t(blockIdx.x) * (kDBlock / 64) + wv;
     {
@@ -250,50 +279,64 @@ __global__ __launch_bounds__(kDBlock) void k_dropout_bits(const uint64_t *__rest
 #pragma unroll
             for (int m = 0; m < kLag; m++) g += e[m] * sR[lane + m];
         }
-        sGw[wv][lane] = g;
+        // its balanced digits, one byte per lane in each digit row
+        uint32_t l[4];
+        limbs4(g, l);
+        uint8_t *gd = reinterpret_cast<uint8_t *>(sGd[wv]);
+#pragma unroll
+        for (int p = 0; p < 4; p++) gd[p * 64 + lane] = uint8_t(l[p]);
     }
     __syncthreads();
-    // B operands of this wave: digits of H[m][t] = G_w[m + t]
-    long Bq[4][2];
+    // B operands of this wave: digits of H[m][t] = G_w[m + t], m = 16 c +
+    // 8 (lane / 32) + b: bytes o .. o + 7 of each digit row, o = 16 c +
+    // 8 (lane / 32) + t (<= 55), gathered as two byte-aligned dword pairs
+    uint64_t Bq[4][2];
     {
         const int t = lane & 31, h = lane >> 5;
 #pragma unroll
         for (int cc = 0; cc < 2; cc++) {
-            uint64_t q[4] = {0u, 0u, 0u, 0u};
+            const int o = 16 * cc + 8 * h + t;
+            const int qd = o >> 2, sh = o & 3;
 #pragma unroll
-            for (int b = 0; b < 8; b++) {
-                uint32_t l[4];
-                limbs4(sGw[wv][16 * cc + 8 * h + b + t], l);
-#pragma unroll
-                for (int p = 0; p < 4; p++) q[p] |= uint64_t(l[p]) << (8 * b);
+            for (int p = 0; p < 4; p++) {
+                const uint32_t *row = sGd[wv][p];
+                const uint32_t d0 = row[qd], d1 = row[qd + 1], d2 = row[qd + 2];
+                const uint32_t lo = __builtin_amdgcn_alignbyte(d1, d0, uint32_t(sh));
+                const uint32_t hi = __builtin_amdgcn_alignbyte(d2, d1, uint32_t(sh));
+                Bq[p][cc] = uint64_t(lo) | (uint64_t(hi) << 32);
             }
-#pragma unroll
-            for (int p = 0; p < 4; p++) Bq[p][cc] = long(q[p]);
         }
     }
     uint32_t *X = sX[wv];
-    // Two 32-segment tiles, transposed through LDS one at a time; one
-    // accumulator at a time (D_0 .. D_3 folded into `out` as they finish).
+    // Two 32-segment tiles, transposed through LDS one at a time.
     uint32_t w[kLag];
 #pragma unroll
     for (int T = 0; T < 2; T++) {
-        long A[4][2];
+        // K = 32 per instruction: both 16-coefficient chunks in one operand
+        // (bytes 0-7 chunk 0, bytes 8-15 chunk 1, the same for A and B, so
+        // the product sums all 32 coefficients whatever the unit's k order)
+        i32x4 A4[4], B4[4];
 #pragma unroll
-        for (int p = 0; p < 4; p++)
+        for (int p = 0; p < 4; p++) {
+            A4[p] = pack_k32(sD[T * 512 + (p * 2) * 64 + lane], sD[T * 512 + (p * 2 + 1) * 64 + lane]);
+            B4[p] = pack_k32(Bq[p][0], Bq[p][1]);
+        }
+        // Horner over the digit weight, s = 3, 2, 1, 0: d = (d << 8) + D_s,
+        // the shifted sum entering the next products as their accumulator
+        // (int32 accumulation wraps mod 2^32)
+        i32x16 d = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-            for (int cc = 0; cc < 2; cc++) A[p][cc] = long(D[T * 512 + (p * 2 + cc) * 64 + lane]);
+        for (int s = 3; s >= 0; s--) {
+            if (s < 3) {
+#pragma unroll
+                for (int v = 0; v < 16; v++) d[v] = int(uint32_t(d[v]) << 8);
+            }
+#pragma unroll
+            for (int p = 0; p <= s; p++) d = __builtin_amdgcn_mfma_i32_32x32x32_i8(A4[p], B4[s - p], d, 0, 0, 0);
+        }
         uint32_t out[16];
 #pragma unroll
-        for (int s = 0; s < 4; s++) {
-            i32x16 d = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-            for (int p = 0; p <= s; p++)
-#pragma unroll
-                for (int cc = 0; cc < 2; cc++)
-                    d = __builtin_amdgcn_mfma_i32_32x32x16_i8(A[p][cc], Bq[s - p][cc], d, 0, 0, 0);
-#pragma unroll
-            for (int v = 0; v < 16; v++) out[v] = s == 0 ? uint32_t(d[v]) : out[v] + (uint32_t(d[v]) << (8 * s));
-        }
+        for (int v = 0; v < 16; v++) out[v] = uint32_t(d[v]);
         // result (row, t) of lane l, value v: row 8(v/4) + 4(l/32) + v%4, t = l % 32 (t = 31 is padding)
         if ((lane & 31) < kLag) {
 #pragma unroll
@@ -310,8 +353,7 @@ __global__ __launch_bounds__(kDBlock) void k_dropout_bits(const uint64_t *__rest
     if (j >= nseg) return;
     const int64_t d0 = j * kSegL;
     uint32_t *b = bits + j * kSegWords;
-    if (d0 + kSegL > n - kLag) gen_segment<true>(w, d0, n, thr - 1u, b, Wn);
-    else gen_segment<false>(w, d0, n, thr - 1u, b, Wn);
+    gen_segment<ALL>(w, d0, n, t2m1, b, Wn, d0 + kSegL > n - kLag, klo);
 }
 
 constexpr int kDUnroll = 2;
@@ -445,11 +487,12 @@ HPoly hpoly_xpow(uint64_t k)
     return r;
 }
 
-// glibc srand(seed) followed by the 310 discarded values: the window
-// r[313 .. 343] that precedes the first rand() output r[344].
+// glibc srand(seed) followed by the 310 discarded values: r[313 .. 405], the
+// window that precedes the first rand() output r[344] and the 62 values after
+// it.
 void seed_window(uint32_t seed, uint32_t *win)
 {
-    uint32_t r[344];
+    uint32_t r[344 + 2 * kLag];
     const uint32_t s = seed == 0 ? 1u : seed;
     r[0] = s;
     int32_t word = int32_t(s);
@@ -461,20 +504,19 @@ void seed_window(uint32_t seed, uint32_t *win)
         r[i] = uint32_t(word);
     }
     for (int i = kLag; i < 34; i++) r[i] = r[i - kLag];
-    for (int i = 34; i < 344; i++) r[i] = r[i - kLag] + r[i - 3];
-    std::memcpy(win, r + 344 - kLag, kLag * sizeof(uint32_t));
+    for (int i = 34; i < 344 + 2 * kLag; i++) r[i] = r[i - kLag] + r[i - 3];
+    std::memcpy(win, r + 344 - kLag, kWin * sizeof(uint32_t));
 }
 
 struct Stream {
     std::mutex mu;
     bool ready = false;
-    uint32_t *win[2] = {nullptr, nullptr};  // device windows (current, next)
+    uint32_t *win[2] = {nullptr, nullptr};  // device stream values, kWin words (current, next)
     int cur = 0;
     uint64_t *dig = nullptr;                // d_l = x^(lL) mod P, l < 64, as MFMA digits (1024 words)
     uint32_t *ejump = nullptr;              // e_w = x^(64 w L) mod P, 32 words per wave
     int64_t ejump_n = 0;                    // waves covered (a power of two >= 1024)
     uint32_t *wpowers = nullptr;            // x^(64 L 2^k) mod P, k < 63
-    uint32_t *x62 = nullptr;                // x^(31+i) mod P, i < 62
     uint32_t *bits = nullptr;
     size_t bits_cap = 0;
     uint64_t drawn = 0;                     // draws since the last seed
@@ -488,7 +530,7 @@ Stream &S()
 
 int set_seed_locked(Stream &s, uint32_t seed)
 {
-    uint32_t w[kLag];
+    uint32_t w[kWin];
     seed_window(seed, w);
     NH_TRY(sync());
     NH_HIP(hipMemcpy(s.win[s.cur], w, sizeof(w), hipMemcpyHostToDevice));
@@ -500,7 +542,7 @@ int ensure_stream_locked(Stream &s)
 {
     if (s.ready) return NEURAL_OK;
     for (int i = 0; i < 2; i++) {
-        s.win[i] = static_cast<uint32_t *>(dev_alloc(kLag * sizeof(uint32_t)));
+        s.win[i] = static_cast<uint32_t *>(dev_alloc(kWin * sizeof(uint32_t)));
         if (!s.win[i]) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
     }
     // x^(L 2^k) for the 64-row digit table, x^(64 L 2^k) for the wave jumps
@@ -521,14 +563,6 @@ int ensure_stream_locked(Stream &s)
     NH_LAUNCH(k_jump_table, dim3(1), dim3(kDBlock), 0, stream(), s.dig, int64_t(0), int64_t(64), powers);
     NH_TRY(check_launch());
     dev_free(powers);  // stream-ordered: reused only by later work on the stream
-    std::vector<uint32_t> X(size_t(2 * kLag) * kLag);
-    for (int i = 0; i < 2 * kLag; i++) {
-        const HPoly c = hpoly_xpow(uint64_t(kLag + i));
-        std::memcpy(X.data() + size_t(i) * kLag, c.data(), kLag * sizeof(uint32_t));
-    }
-    s.x62 = static_cast<uint32_t *>(dev_alloc(X.size() * sizeof(uint32_t)));
-    if (!s.x62) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
-    NH_HIP(hipMemcpy(s.x62, X.data(), X.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
     s.ready = true;
     return set_seed_locked(s, 1u);  // glibc's initial state is srand(1)
 }
@@ -586,7 +620,7 @@ static int dropout_fwd(const float *in, float *out, uint8_t *mask, uint64_t n, f
     std::lock_guard<std::mutex> lock(s.mu);
     NH_TRY(ensure_stream_locked(s));
     const int64_t nn = int64_t(n);
-    const int64_t nseg = ceil_div(nn, kSegL);
+    const int64_t nseg = ceil_div(nn + 2 * kLag, kSegL);  // draws 0 .. n + 61
     // every wave of the grid (ceil(nseg / 256) blocks of 4) has a wave jump
     NH_TRY(ensure_jumps_locked(s, ceil_div(nseg, kDBlock) * (kDBlock / 64)));
     const size_t words = size_t(nseg) * kSegWords;
@@ -605,8 +639,14 @@ static int dropout_fwd(const float *in, float *out, uint8_t *mask, uint64_t n, f
     NH_TRY(xo.open(out, size_t(n) * 4, false));
     NH_TRY(xm.open(mask, size_t(n), false));
     uint32_t *W = s.win[s.cur], *Wn = s.win[s.cur ^ 1];
-    NH_LAUNCH(k_dropout_bits, dim3(unsigned(ceil_div(nseg, kDBlock))), dim3(kDBlock), 0, stream(), s.dig,
-              s.ejump, s.x62, W, Wn, nn, nseg, thr, s.bits);
+    // keep = r > 2 thr - 1 (thr >= 1), or every draw (thr = 0)
+    const uint32_t t2m1 = uint32_t(2 * uint64_t(thr) - 1u);
+    if (thr == 0)
+        NH_LAUNCH(k_dropout_bits<true>, dim3(unsigned(ceil_div(nseg, kDBlock))), dim3(kDBlock), 0, stream(), s.dig,
+                  s.ejump, W, Wn, nn, nseg, t2m1, s.bits);
+    else
+        NH_LAUNCH(k_dropout_bits<false>, dim3(unsigned(ceil_div(nseg, kDBlock))), dim3(kDBlock), 0, stream(),
+                  s.dig, s.ejump, W, Wn, nn, nseg, t2m1, s.bits);
     NH_TRY(check_launch());
     s.cur ^= 1;
     s.drawn += n;
