@@ -36,8 +36,8 @@
 // packs keep bits into 8 words.  A second, streaming kernel reads x in
 // 16-byte vectors, the 4 keep bits of each vector, and writes out and the
 // mask bytes (9 B per element).  The stream values after the call (r at
-// A + n .. A + n + 92, the next call's R) are written by the threads that
-// generate draws n - 31 .. n + 61 (the call generates 62 draws past n).
+// A + n .. A + n + 92, the next call's R) are one more jump of R, by
+// x^n and x^(n+31) mod P (made on the host, kept while n repeats).
 #include <cmath>
 #include <cstring>
 #include <mutex>
@@ -156,8 +156,8 @@ __global__ __launch_bounds__(kDBlock) void k_jump_table(uint64_t *__restrict__ T
     }
 }
 
-// Generate the keep bits of segment j.  W is the anchor window, Wn receives
-// the window after the call.  keep = (r >> 1) >= thr = (r > 2 thr - 1) for
+// Generate the keep bits of one segment from its starting window w.
+// keep = (r >> 1) >= thr = (r > 2 thr - 1) for
 // thr in [1, 2^31] (ALL: thr = 0, every draw kept): one subtraction
 // t2m1 - r whose borrow is the keep bit, and one add-with-carry kb + kb +
 // borrow that shifts it into the period's word, first draw highest -- three
@@ -171,8 +171,7 @@ __global__ __launch_bounds__(kDBlock) void k_jump_table(uint64_t *__restrict__ T
 // the fully unrolled segment is ~50 KB of straight-line code, and fetching it
 // cold made the kernel instruction-fetch bound (measured 4x slower).
 template <bool ALL>
-NH_DEV void gen_segment(uint32_t (&w)[kLag], int64_t d0, int64_t n, uint32_t t2m1, uint32_t *__restrict__ bits,
-                        uint32_t *__restrict__ Wn, bool tail, int klo)
+NH_DEV void gen_segment(uint32_t (&w)[kLag], uint32_t t2m1, uint32_t *__restrict__ bits)
 {
     uint64_t acc = 0u;  // pending keep bits; the low `have` are valid
     int have = 0;
@@ -192,17 +191,6 @@ NH_DEV void gen_segment(uint32_t (&w)[kLag], int64_t d0, int64_t n, uint32_t t2m
                              : "+v"(kb), "=&v"(diff)
                              : "s"(t2m1), "v"(r)
                              : "vcc");
-            }
-        }
-        // the segments that hold draws n - 31 .. n + 61 store them (ring slot
-        // u now holds draw p0 + u) as the next call's 93 values; slots below
-        // klo carry over from this call's values (block 0 copies them)
-        const int64_t off = d0 + int64_t(per) * kLag - (n - kLag);  // slot 0's place in Wn
-        if (tail && off > -kLag && off < kWin) {
-#pragma unroll
-            for (int u = 0; u < kLag; u++) {
-                const int k = int(off) + u;
-                if (k >= klo && k < kWin) Wn[k] = w[u];
             }
         }
         const uint32_t pb = __builtin_bitreverse32(kb) >> 1;  // draw u at bit u
@@ -246,16 +234,23 @@ __global__ __launch_bounds__(kDBlock) void k_wave_jumps(uint32_t *__restrict__ E
 //      the MFMA A-operand layout, 8 KB): a [64 x 32] x [32 x 32] product mod
 //      2^32 on the matrix cores, B = the Hankel digits of G_w.
 // The per-segment table reads of a single-step jump (128 bytes per segment)
-// become 128 bytes per 64 segments; D is staged in LDS once per block.  The
-// segments cover draws 0 .. n + 61 (nseg of them), so that the next call's
-// 93 values are generated here.  E covers every wave of the grid, so all
+// become 128 bytes per 64 segments; D is staged in LDS once per block.
+// E covers every wave of the grid, so all
 // waves run the jump and reach every barrier; threads past nseg stop before
 // generating.
+// x^n and x^(n+31) mod P for the call's n: the next call's 93 values are
+// Wn[i] = r[A + n + i] = sum_m c0[m] R[i + m] (i < 62) and
+// Wn[62 + q] = sum_m c1[m] R[31 + q + m] (q < 31), from R alone.
+struct NextJump {
+    uint32_t c0[kLag];
+    uint32_t c1[kLag];
+};
+
 template <bool ALL>
 __global__ __launch_bounds__(kDBlock) void k_dropout_bits(const uint64_t *__restrict__ D,
                                                            const uint32_t *__restrict__ E,
                                                            const uint32_t *__restrict__ W, uint32_t *__restrict__ Wn,
-                                                           int64_t n, int64_t nseg, uint32_t t2m1,
+                                                           NextJump nj, int64_t nseg, uint32_t t2m1,
                                                            uint32_t *__restrict__ bits)
 {
     __shared__ uint64_t sD[kTabWordsPerWave];           // the 64-row digit table
@@ -264,14 +259,26 @@ __global__ __launch_bounds__(kDBlock) void k_dropout_bits(const uint64_t *__rest
     __shared__ uint32_t sX[kDBlock / 64][32 * kLag];  // per wave: one tile's 32 windows, row stride 31 (odd: no bank conflicts)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // the next call's values r[A + n + k] for n + k < 93 are this call's
-    const int klo = n < kWin ? int(kWin - n) : 0;
-    if (blockIdx.x == 0 && tid < klo) Wn[tid] = W[n + tid];
     if (tid < kWin) sR[tid] = W[tid];
 #pragma unroll
     for (int i = 0; i < kTabWordsPerWave / kDBlock; i++) sD[i * kDBlock + tid] = D[i * kDBlock + tid];
     __syncthreads();
     const int64_t wave = int64_t(blockIdx.x) * (kDBlock / 64) + wv;
+    if (blockIdx.x == 0 && wv < 2) {
+        // the next call's 93 values (block 0, two waves; coefficients uniform)
+        uint32_t g = 0u;
+        if (wv == 0) {
+            if (lane < 2 * kLag) {
+#pragma unroll
+                for (int m = 0; m < kLag; m++) g += nj.c0[m] * sR[lane + m];
+                Wn[lane] = g;
+            }
+        } else if (lane < kLag) {
+#pragma unroll
+            for (int m = 0; m < kLag; m++) g += nj.c1[m] * sR[kLag + lane + m];
+            Wn[2 * kLag + lane] = g;
+        }
+    }
     {
         const uint32_t *e = E + wave * 32;  // uniform per wave
         uint32_t g = 0u;
@@ -351,9 +358,8 @@ __global__ __launch_bounds__(kDBlock) void k_dropout_bits(const uint64_t *__rest
     }
     const int64_t j = wave * 64 + lane;
     if (j >= nseg) return;
-    const int64_t d0 = j * kSegL;
     uint32_t *b = bits + j * kSegWords;
-    gen_segment<ALL>(w, d0, n, t2m1, b, Wn, d0 + kSegL > n - kLag, klo);
+    gen_segment<ALL>(w, t2m1, b);
 }
 
 constexpr int kDUnroll = 2;
@@ -520,6 +526,8 @@ struct Stream {
     uint32_t *bits = nullptr;
     size_t bits_cap = 0;
     uint64_t drawn = 0;                     // draws since the last seed
+    NextJump nj{};                          // x^n, x^(n+31) mod P for n = nj_n
+    int64_t nj_n = -1;
 };
 
 Stream &S()
@@ -620,7 +628,7 @@ static int dropout_fwd(const float *in, float *out, uint8_t *mask, uint64_t n, f
     std::lock_guard<std::mutex> lock(s.mu);
     NH_TRY(ensure_stream_locked(s));
     const int64_t nn = int64_t(n);
-    const int64_t nseg = ceil_div(nn + 2 * kLag, kSegL);  // draws 0 .. n + 61
+    const int64_t nseg = ceil_div(nn, kSegL);
     // every wave of the grid (ceil(nseg / 256) blocks of 4) has a wave jump
     NH_TRY(ensure_jumps_locked(s, ceil_div(nseg, kDBlock) * (kDBlock / 64)));
     const size_t words = size_t(nseg) * kSegWords;
@@ -638,15 +646,22 @@ static int dropout_fwd(const float *in, float *out, uint8_t *mask, uint64_t n, f
     NH_TRY(xi.open(in, size_t(n) * 4, true));
     NH_TRY(xo.open(out, size_t(n) * 4, false));
     NH_TRY(xm.open(mask, size_t(n), false));
+    if (nn != s.nj_n) {
+        // x^n and x^(n+31) mod P for the next call's values
+        const HPoly c0 = hpoly_xpow(uint64_t(nn)), c1 = hpoly_mul(c0, hpoly_xpow(uint64_t(kLag)));
+        std::memcpy(s.nj.c0, c0.data(), sizeof(s.nj.c0));
+        std::memcpy(s.nj.c1, c1.data(), sizeof(s.nj.c1));
+        s.nj_n = nn;
+    }
     uint32_t *W = s.win[s.cur], *Wn = s.win[s.cur ^ 1];
     // keep = r > 2 thr - 1 (thr >= 1), or every draw (thr = 0)
     const uint32_t t2m1 = uint32_t(2 * uint64_t(thr) - 1u);
     if (thr == 0)
         NH_LAUNCH(k_dropout_bits<true>, dim3(unsigned(ceil_div(nseg, kDBlock))), dim3(kDBlock), 0, stream(), s.dig,
-                  s.ejump, W, Wn, nn, nseg, t2m1, s.bits);
+                  s.ejump, W, Wn, s.nj, nseg, t2m1, s.bits);
     else
         NH_LAUNCH(k_dropout_bits<false>, dim3(unsigned(ceil_div(nseg, kDBlock))), dim3(kDBlock), 0, stream(),
-                  s.dig, s.ejump, W, Wn, nn, nseg, t2m1, s.bits);
+                  s.dig, s.ejump, W, Wn, s.nj, nseg, t2m1, s.bits);
     NH_TRY(check_launch());
     s.cur ^= 1;
     s.drawn += n;
