@@ -416,7 +416,7 @@ def main():
         del src, dst
 
     if args.suite:
-        detail["suite"] = suite(torch, pn, clock, dev)
+        detail["suite"] = suite(torch, pn, clock, dev, cpu=not args.no_cpu)
     pn.set_stream(None)
     if args.detail:
         detail["host"] = {"cpu": _cpu_model(), "nproc": os.cpu_count()}
@@ -836,15 +836,24 @@ def cpu_cfg5(p_dev, clean_dev, g_dev):
 
 # ------------------------------------------------------------------------- other families
 
-def suite(torch, pn, clock, dev):
+SUITE_CPU_SAMPLE = 1 << 22  # elements of each family's CPU leg
+
+
+def suite(torch, pn, clock, dev, cpu=True):
     """Kernel families outside BASELINE's configs (detail file only): for each
     op the kernel time of its main launch (`k`, HIP event pair on that launch)
     and, where a call makes several launches or returns a result to the host,
     the call time (`call`, all launches and gaps), in us, with the algorithmic
-    bytes of the main kernel."""
+    bytes of the main kernel.  With `cpu`, each op also carries its CPU leg
+    (`cpu`: one host thread, GB/s over the same bytes per element) on a bounded
+    sample (SUITE_CPU_SAMPLE elements, rows of it for the row ops) of the same
+    input: the reference's own C (oracle/_ref, kind "reference") where it
+    compiles, else the oracle's restatement of the reference loop ("port");
+    the oracle allocates each output, which those timings include."""
     from pyneural.core import _lib, QuantParamsC
     W = pn.Tensor.from_torch
     res = {}
+    ora, ref = _ref() if cpu else (None, None)
 
     def put(name, nbytes, k=None, call=None):
         e = {"bytes": int(nbytes)}
@@ -855,6 +864,13 @@ def suite(torch, pn, clock, dev):
             e["call_us"] = round(call, 2)
             e["call_pct"] = pct(nbytes, call)
         res[name] = e
+
+    def cpu_leg(name, nbytes, fn, kind, sample):
+        if not cpu or (kind.startswith("reference") and ref is None):
+            return
+        sec = _median_time(fn)
+        res[name]["cpu"] = {"GB/s": round(nbytes / sec / 1e9, 3), "ms": round(1e3 * sec, 2), "cores": 1,
+                            "kind": kind, "sample": sample}
 
     g = torch.Generator(device=dev)
     g.manual_seed(7)
@@ -875,6 +891,19 @@ def suite(torch, pn, clock, dev):
     put("row_max_f32_16384x4096", 4 * R * C, clock.kernel_us(lambda: _lib.neural_reduce_max(tY._ptr, 1, trs._ptr)))
     put("row_argmax_f32_16384x4096", 4 * R * C,
         clock.kernel_us(lambda: _lib.neural_reduce_argmax(tY._ptr, 1, ri.data_ptr())))
+    if cpu:
+        rows = SUITE_CPU_SAMPLE // C
+        Xh, bh = X[:rows].cpu().numpy(), bias.cpu().numpy()
+        Yh = ora.bias_add(Xh, bh)
+        smp = f"first {rows} rows"
+        cpu_leg("bias_add_f32_16384x4096", 8 * Xh.size, lambda: ora.bias_add(Xh, bh), "port", smp)
+        cpu_leg("bias_add_relu_f32_16384x4096", 8 * Xh.size, lambda: ora.relu(ora.bias_add(Xh, bh)), "port",
+                smp + ": bias add, then ReLU, as the reference runs them")
+        cpu_leg("bias_add_gelu_f32_16384x4096", 8 * Xh.size, lambda: ora.act("gelu", ora.bias_add(Xh, bh)), "port",
+                smp + ": bias add, then GELU (activations_c.c formula)")
+        cpu_leg("row_sum_f32_16384x4096", 4 * Yh.size, lambda: ora.rowsum_ref(Yh), "port", smp)
+        cpu_leg("row_max_f32_16384x4096", 4 * Yh.size, lambda: ora.rowmax_chain(Yh), "port", smp)
+        cpu_leg("row_argmax_f32_16384x4096", 4 * Yh.size, lambda: ora.rowargmax(Yh), "port", smp)
     del X, Y, tX, tY, rs, ri, trs
     torch.cuda.empty_cache()
 
@@ -890,6 +919,13 @@ def suite(torch, pn, clock, dev):
     put("dropout_fwd_f32_64M", 9 * n, None, clock.call_us(fwd))
     put("dropout_bwd_f32_64M", 9 * n, clock.kernel_us(
         lambda: _lib.neural_dropout_backward(a.data_ptr(), c.data_ptr(), dmask.data_ptr(), n, ctypes.c_float(0.5))))
+    if cpu:
+        xh = a[:SUITE_CPU_SAMPLE].cpu().numpy()
+        _, _, mh = ora.dropout_forward(xh, 0.5)
+        smp = f"first {xh.size:,} elements; glibc rand() per element"
+        cpu_leg("dropout_fwd_f32_64M", 9 * xh.size, lambda: ora.dropout_forward(xh, 0.5), "port", smp)
+        cpu_leg("dropout_bwd_f32_64M", 9 * xh.size, lambda: ora.dropout_backward(xh, mh, 0.5), "port",
+                f"first {xh.size:,} elements")
     del a, c, dmask
     torch.cuda.empty_cache()
 
@@ -905,6 +941,15 @@ def suite(torch, pn, clock, dev):
     f = lambda: _lib.label_smoothing_ce_fused(L64.data_ptr(), tgt.data_ptr(), B, K, 0.1, ctypes.byref(lossv),
                                               G64.data_ptr())
     put("ls_ce_fused_f64_65536x1024", 16 * B * K, clock.kernel_us(f), clock.call_us(f))
+    if cpu:
+        rows = SUITE_CPU_SAMPLE // K
+        Lh, th = L64[:rows].cpu().numpy(), tgt[:rows].cpu().numpy()
+        smp = f"first {rows} rows; metrics_losses.c compiled unchanged"
+        cpu_leg("ls_ce_forward_f64_65536x1024", 8 * Lh.size, lambda: ora.ls_ce_forward(Lh, th, 0.1, use_ref=True),
+                "reference", smp)
+        cpu_leg("ls_ce_fused_f64_65536x1024", 16 * Lh.size,
+                lambda: (ora.ls_ce_forward(Lh, th, 0.1, use_ref=True), ora.ls_ce_backward(Lh, th, 0.1, use_ref=True)),
+                "reference", smp + ": forward, then backward")
     del L64, G64
     L32 = torch.randn(B, K, device=dev, generator=g) * 3
     G32 = torch.empty_like(L32)
@@ -916,6 +961,16 @@ def suite(torch, pn, clock, dev):
     tL = W(L32)
     f = lambda: _lib.neural_cross_entropy_loss(tL._ptr, tv._ptr, ctypes.byref(lossv))
     put("ce_loss_f32_65536x1024", 4 * B * K, clock.kernel_us(f), clock.call_us(f))
+    if cpu:
+        rows = SUITE_CPU_SAMPLE // K
+        Lh, th = L32[:rows].cpu().numpy(), tgt[:rows].cpu().numpy()
+        Lw = Lh.astype("float64")
+        cpu_leg("ls_ce_fused_f32_65536x1024", 8 * Lh.size,
+                lambda: (ora.ls_ce_forward(Lw, th, 0.1, use_ref=True), ora.ls_ce_backward(Lw, th, 0.1, use_ref=True)),
+                "reference", f"first {rows} rows widened to double (the reference API is double-only); "
+                             "metrics_losses.c forward, then backward")
+        tvh = th.astype("float32")
+        cpu_leg("ce_loss_f32_65536x1024", 4 * Lh.size, lambda: ora.ce_loss(Lh, tvh), "port", f"first {rows} rows")
     del L32, G32, tL, tv, tgt
     torch.cuda.empty_cache()
 
@@ -939,6 +994,14 @@ def suite(torch, pn, clock, dev):
         lambda: _lib.neural_clip_grad_norm_list(glist, 1, ctypes.c_double(1e30), ctypes.byref(tot))))
     f = lambda: _lib.neural_clip_grad_value_list(glist, 1, ctypes.c_double(-1e-3), ctypes.c_double(1e-3))
     put("clip_grad_value_f32_100M", 8 * na, clock.kernel_us(f), clock.call_us(f))
+    if cpu:
+        gh = gr[:SUITE_CPU_SAMPLE].cpu().numpy()
+        nh = ora.clip_grad_norm([gh], 1e30)[0]
+        smp = f"first {gh.size:,} elements; the port clips a copy, which the timing includes"
+        cpu_leg("clip_grad_norm_clipping_f32_100M", 12 * gh.size, lambda: ora.clip_grad_norm([gh], 0.5 * nh), "port",
+                smp)
+        cpu_leg("clip_grad_norm_below_f32_100M", 4 * gh.size, lambda: ora.clip_grad_norm([gh], 1e30), "port", smp)
+        cpu_leg("clip_grad_value_f32_100M", 8 * gh.size, lambda: ora.clip_grad_value([gh], -1e-3, 1e-3), "port", smp)
     del gr, tg
     torch.cuda.empty_cache()
 
@@ -953,6 +1016,14 @@ def suite(torch, pn, clock, dev):
     f = lambda: _lib.transform_normalize(D.data_ptr(), O.data_ptr(), TB, TF, st[0].data_ptr(), st[1].data_ptr(),
                                          ctypes.c_double(1e-8))
     put("transform_normalize_f64_1Mx64", 16 * TB * TF, clock.kernel_us(f), clock.call_us(f))
+    if cpu:
+        Dh = D[:SUITE_CPU_SAMPLE // TF].cpu().numpy()
+        _, mu, sd, _, _ = ora.transform_stats(Dh, use_ref=True)
+        smp = f"first {Dh.shape[0]:,} rows; transforms.c compiled unchanged"
+        cpu_leg("transform_compute_stats_f64_1Mx64", 8 * Dh.size, lambda: ora.transform_stats(Dh, use_ref=True),
+                "reference", smp)
+        cpu_leg("transform_normalize_f64_1Mx64", 16 * Dh.size,
+                lambda: ora.transform_apply(0, Dh, mu, sd, 1e-8, use_ref=True), "reference", smp)
     del D, O, st
     torch.cuda.empty_cache()
 
@@ -963,6 +1034,11 @@ def suite(torch, pn, clock, dev):
     torch.cuda.synchronize()
     put("calibrate_percentile_f64_64M", 8 * P.numel(), None, clock.call_us(
         lambda: _lib.calibrate_percentile(P.data_ptr(), P.numel(), ctypes.c_double(0.01), 1, ctypes.byref(qp))))
+    if cpu:
+        Ph = P[:SUITE_CPU_SAMPLE].cpu().numpy()
+        cpu_leg("calibrate_percentile_f64_64M", 8 * Ph.size,
+                lambda: ora.calibrate_percentile(Ph, 0.01, True, use_ref=True), "reference",
+                f"first {Ph.size:,} values; quantize.c (qsort) compiled unchanged")
     del P
     m = 4096
     A8 = torch.randint(-128, 128, (m, m), dtype=torch.int8, device=dev, generator=g)
@@ -974,6 +1050,15 @@ def suite(torch, pn, clock, dev):
     us = clock.call_us(lambda: _lib.quantized_matmul(A8.data_ptr(), B8.data_ptr(), C8.data_ptr(), m, m, m,
                                                      ctypes.byref(pa), ctypes.byref(pb)))
     res["quantized_matmul_4096^3"] = {"call_us": round(us, 2), "int8_TOPS": round(2.0 * m ** 3 / us / 1e6, 1)}
+    if cpu and ref is not None:
+        mc = 256
+        Ah, Bh = A8[:mc, :mc].cpu().numpy(), B8[:mc, :mc].cpu().numpy()
+        qa, qb = ora.QuantParams(), ora.QuantParams()
+        qa.scale, qa.zero_point, qb.scale, qb.zero_point = 0.013, -7, 0.37, 11
+        sec = _median_time(lambda: ora.quantized_matmul(Ah, Bh, mc, mc, mc, qa, qb, use_ref=True))
+        res["quantized_matmul_4096^3"]["cpu"] = {
+            "int8_TOPS": round(2.0 * mc ** 3 / sec / 1e12, 4), "ms": round(1e3 * sec, 2), "cores": 1,
+            "kind": "reference", "sample": f"{mc}^3 corner of the same operands; quantize.c compiled unchanged"}
     del A8, B8, C8
     torch.cuda.empty_cache()
     return res
