@@ -24,7 +24,7 @@
 // Parallel generation on the device: the recurrence is linear, so for the
 // anchor window W = r[A .. A+30] any later value is r[A + k] = sum_m c_m W[m]
 // with c = x^k mod P(x), P(x) = x^31 - x^28 - 1, coefficients mod 2^32.
-// The n draws of a call are cut into segments of L = 248 draws (8 periods
+// The n draws of a call are cut into segments of L = 372 draws (12 periods
 // of 31), 64 segments per wave.  Segment j = 64 w + l starts at
 // A + jL; its starting window is reached in two linear steps: the 62 values
 // G_w = r[A + 64 w L ..] from R = r[A .. A+92] and e_w = x^(64 w L) mod P (a
@@ -32,8 +32,8 @@
 // with d_l = x^(lL) mod P, the same 64 rows for every wave: a [64 x 32] x
 // [32 x 32] product mod 2^32, done on the matrix cores (int8 MFMA over signed
 // byte limbs, below).  Thread j then runs
-// the recurrence for its 248 draws with the 31-value ring in registers and
-// packs keep bits into 8 words.  A second, streaming kernel reads x in
+// the recurrence for its 372 draws with the 31-value ring in registers and
+// packs keep bits into 12 words.  A second, streaming kernel reads x in
 // 16-byte vectors, the 4 keep bits of each vector, and writes out and the
 // mask bytes (9 B per element).  The stream values after the call (r at
 // A + n .. A + n + 92, the next call's R) are one more jump of R, by
@@ -49,13 +49,13 @@
 namespace nh {
 
 constexpr int kLag = 31;                       // r[i] = r[i-31] + r[i-3]
-// Segments of 8 periods: the jump (961 quarter-rate multiplies per segment)
-// then costs ~3/4 of the kernel, but 4 waves per SIMD hide the latencies one
-// wave cannot (measured on 64 M draws: 32 periods 68 us, 16 periods 47 us,
-// 8 periods 41 us).
-constexpr int kPeriods = 8;
-constexpr int64_t kSegL = int64_t(kLag) * kPeriods;   // 248 draws per thread segment (a multiple of 4)
-constexpr int kSegWords = int((kSegL + 31) / 32);      // keep-bit words per segment (8)
+// Segments of 12 periods (a multiple of 4 draws, for the 4-draw vectors of
+// the streaming pass): keep-bit kernel at 64 M draws with 4 / 8 / 12 / 16 /
+// 24 periods 20.9 / 17.4 / 16.9 / 20.5 / 20.0 us (shorter segments pay more
+// jumps, longer ones leave SIMDs with too few waves).
+constexpr int kPeriods = 12;
+constexpr int64_t kSegL = int64_t(kLag) * kPeriods;   // 372 draws per thread segment (a multiple of 4)
+constexpr int kSegWords = int((kSegL + 31) / 32);      // keep-bit words per segment (12)
 constexpr int kDBlock = 256;
 // Stream values kept between calls: r[A .. A+92], the anchor window and the
 // 62 values after it (the first jump step reads all 93).

@@ -38,7 +38,10 @@ def test_stream_across_calls(pn, ora, seed):
     assert _lib().neural_dropout_seed(ctypes.c_uint32(seed)) == 0
     ora.srand(seed)
     total = 0
-    for n in [1, 5, 30, 31, 32, 247, 248, 249, 496, 991, 992, 993, 100_003, 7, 65_536 * 3 + 1]:
+    # around the 31-draw period, the 372-draw thread segment, the 23,808-draw
+    # wave group and the 93 stream values carried between calls
+    for n in [1, 5, 30, 31, 32, 92, 93, 94, 371, 372, 373, 744, 23_807, 23_808, 23_809, 100_003, 7,
+              65_536 * 3 + 1]:
         x = rng.normal(0, 1, n).astype(np.float32)
         p = 0.5 if n % 2 else 0.3
         out, mask = _fwd_host(x, p)
