@@ -138,6 +138,11 @@ constexpr int kQBlock = 256;
 // (1 KiB read, 256 B written for f32).  Tiles of 256 lanes x U units, all
 // loads of a tile issued before its stores; accesses are non-temporal.
 constexpr int kQUnroll = 4;
+// f32 / f64 -> i8 (k_quantize): 2 units per lane with each wave's 128 units
+// contiguous (the flat streams' layout): quantize at 268M f32 210 us against
+// 215-217 us for 4 units per lane strided by the block (the same for 4 units
+// wave-contiguous), parity unchanged.
+constexpr int kQUnrollQ = 2;
 
 template <typename T>
 struct Quad;  // 4 consecutive elements
@@ -178,17 +183,18 @@ __global__ __launch_bounds__(kQBlock) void k_quantize(const T *__restrict__ x, i
     load_q(qa, inv, scale, zp);
     const int64_t n4 = n / 4;
     uint32_t *q4 = reinterpret_cast<uint32_t *>(q);
-    const int64_t tile = int64_t(kQBlock) * kQUnroll;
-    for (int64_t base = int64_t(blockIdx.x) * tile + threadIdx.x; base < n4; base += int64_t(gridDim.x) * tile) {
-        Quad<T> v[kQUnroll];
+    const int64_t tile = int64_t(kQBlock) * kQUnrollQ;
+    for (int64_t base = int64_t(blockIdx.x) * tile + (threadIdx.x >> 6) * (64 * kQUnrollQ) + (threadIdx.x & 63);
+         base < n4; base += int64_t(gridDim.x) * tile) {
+        Quad<T> v[kQUnrollQ];
 #pragma unroll
-        for (int u = 0; u < kQUnroll; u++) {
-            const int64_t i = base + int64_t(u) * kQBlock;
+        for (int u = 0; u < kQUnrollQ; u++) {
+            const int64_t i = base + int64_t(u) * 64;
             if (i < n4) v[u] = Quad<T>::load(x, i);
         }
 #pragma unroll
-        for (int u = 0; u < kQUnroll; u++) {
-            const int64_t i = base + int64_t(u) * kQBlock;
+        for (int u = 0; u < kQUnrollQ; u++) {
+            const int64_t i = base + int64_t(u) * 64;
             if (i < n4) {
                 uint32_t packed = 0;
 #pragma unroll
@@ -270,8 +276,8 @@ __global__ __launch_bounds__(kQBlock) void k_quantize_scalar(const T *x, int8_t 
 // TB/s with one 16-byte store per lane per block, 5.72 TB/s with four).
 // Measured at 268M codes with the output rotating over three buffers (so no
 // cache absorbs a rewrite): i8 -> f32 228 / 216 / 245 us for 4 / 2 / 1 units,
-// i8 -> f64 448 / 394 / 387 us.  The read-heavy quantize keeps kQUnroll (one
-// unit: 217 -> 257 us).
+// i8 -> f64 448 / 394 / 387 us.  The read-heavy quantize keeps more than one
+// unit (one unit: 217 -> 257 us).
 constexpr int kDqUnrollF32 = 2;
 constexpr int kDqUnrollF64 = 1;
 
@@ -390,7 +396,7 @@ static int launch_quantize(const T *x, int8_t *q, int64_t n, QArgs qa)
         NH_LAUNCH(k_quantize_f64w, dim3(q_grid(n / 4, kQBlock * kQUnroll)), dim3(kQBlock), 0, stream(),
                   reinterpret_cast<const double *>(x), q, n, qa);
     else if (vec)
-        NH_LAUNCH((k_quantize<T>), dim3(q_grid(n / 4, kQBlock * kQUnroll)), dim3(kQBlock), 0, stream(), x,
+        NH_LAUNCH((k_quantize<T>), dim3(q_grid(n / 4, kQBlock * kQUnrollQ)), dim3(kQBlock), 0, stream(), x,
                            q, n, qa);
     else
         NH_LAUNCH((k_quantize_scalar<T>), dim3(q_grid(n, kQBlock)), dim3(kQBlock), 0, stream(), x, q, n, qa);
