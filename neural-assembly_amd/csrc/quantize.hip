@@ -277,7 +277,8 @@ __global__ __launch_bounds__(kQBlock) void k_quantize_scalar(const T *x, int8_t 
 // Measured at 268M codes with the output rotating over three buffers (so no
 // cache absorbs a rewrite): i8 -> f32 228 / 216 / 245 us for 4 / 2 / 1 units,
 // i8 -> f64 448 / 394 / 387 us.  The read-heavy quantize keeps more than one
-// unit (one unit: 217 -> 257 us).
+// unit (one unit: 217 -> 257 us).  k_dequantize takes its U units per lane
+// wave-contiguous (i8 -> f32 215 -> 209 us against the block-strided layout).
 constexpr int kDqUnrollF32 = 2;
 constexpr int kDqUnrollF64 = 1;
 
@@ -292,16 +293,17 @@ __global__ __launch_bounds__(kQBlock) void k_dequantize(const int8_t *__restrict
     const int64_t n4 = n / 4;
     const uint32_t *q4 = reinterpret_cast<const uint32_t *>(q);
     const int64_t tile = int64_t(kQBlock) * U;
-    for (int64_t base = int64_t(blockIdx.x) * tile + threadIdx.x; base < n4; base += int64_t(gridDim.x) * tile) {
+    for (int64_t base = int64_t(blockIdx.x) * tile + (threadIdx.x >> 6) * (64 * U) + (threadIdx.x & 63); base < n4;
+         base += int64_t(gridDim.x) * tile) {
         uint32_t w[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int64_t i = base + int64_t(u) * kQBlock;
+            const int64_t i = base + int64_t(u) * 64;
             if (i < n4) w[u] = __builtin_nontemporal_load(q4 + i);
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int64_t i = base + int64_t(u) * kQBlock;
+            const int64_t i = base + int64_t(u) * 64;
             if (i < n4) {
                 Quad<T> o;
 #pragma unroll
