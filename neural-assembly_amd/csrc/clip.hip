@@ -186,16 +186,19 @@ NH_DEV void chunk_map(T *__restrict__ x, int64_t lo, int64_t hi, F f)
     if ((reinterpret_cast<uintptr_t>(x) & 15u) == 0) {
         V *xv = reinterpret_cast<V *>(x);
         const int64_t v0 = lo / VN, v1 = hi / VN;
-        for (int64_t c = v0 + threadIdx.x; c < v1; c += int64_t(kCBlock) * kCUnroll) {
+        // each wave's kCUnroll x 64 vectors contiguous (clip value at 100M f32:
+        // 126 us against 128 us with the units strided by the block)
+        for (int64_t c = v0 + (threadIdx.x >> 6) * (64 * kCUnroll) + (threadIdx.x & 63); c < v1;
+             c += int64_t(kCBlock) * kCUnroll) {
             V a[kCUnroll];
 #pragma unroll
             for (int u = 0; u < kCUnroll; u++) {
-                const int64_t i = c + int64_t(u) * kCBlock;
+                const int64_t i = c + int64_t(u) * 64;
                 if (i < v1) a[u] = ld_nt(xv + i);
             }
 #pragma unroll
             for (int u = 0; u < kCUnroll; u++) {
-                const int64_t i = c + int64_t(u) * kCBlock;
+                const int64_t i = c + int64_t(u) * 64;
                 if (i < v1) {
 #pragma unroll
                     for (int k = 0; k < VN; k++) a[u][k] = f(a[u][k]);
