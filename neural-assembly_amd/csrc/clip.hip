@@ -161,8 +161,12 @@ struct SumD {
     NH_DEV B bcomb(B a, B b) const { return a + b; }
 };
 
+// The decision to st (device, read by the scale pass) and, with a ticket, to
+// the mapped host result area, so the caller gets the norm without waiting
+// for the scale pass.
 __global__ __launch_bounds__(kRBlock) void k_clip_decide(const double *__restrict__ part, int nparts,
-                                                          double max_norm, ClipState *st)
+                                                          double max_norm, ClipState *st, ClipState *host_st,
+                                                          Ticket tk)
 {
     const double tot = ordered_combine(SumD{}, part, nparts);
     if (threadIdx.x == 0) {
@@ -173,6 +177,10 @@ __global__ __launch_bounds__(kRBlock) void k_clip_decide(const double *__restric
         c.scale = c.clip ? max_norm / c.norm : 1.0;
         c.pad = 0;
         *st = c;
+        if (tk.slot) {
+            *host_st = c;
+            publish(tk);
+        }
     }
 }
 
@@ -417,7 +425,9 @@ int clip_norm_list(NeuralTensor *const *grads, int64_t count, double max_norm, d
                            p.count, p.chunk_sum, part);
     });
     NH_TRY(check_launch());
-    NH_LAUNCH(k_clip_decide, dim3(1), dim3(kRBlock), 0, stream(), part, int(p.blocks_sum), max_norm, st);
+    const Ticket tk = total_norm ? next_ticket() : Ticket{};
+    NH_LAUNCH(k_clip_decide, dim3(1), dim3(kRBlock), 0, stream(), part, int(p.blocks_sum), max_norm, st,
+              static_cast<ClipState *>(workspace().host_result_dev), tk);
     NH_TRY(check_launch());
     p.with_tab([&](const auto &tab) {
         using Tab = std::decay_t<decltype(tab)>;
@@ -426,8 +436,10 @@ int clip_norm_list(NeuralTensor *const *grads, int64_t count, double max_norm, d
     });
     NH_TRY(check_launch());
     if (total_norm) {
+        // the scale pass may still run: later work on the stream (and any
+        // host read of the tensors, which synchronises) comes after it
         ClipState h;
-        NH_TRY(result_to_host(&h, st, sizeof(h)));
+        NH_TRY(host_result_wait(tk.value, &h, sizeof(h)));
         *total_norm = h.norm;
     }
     NH_TRY(written_all(g));
