@@ -12,14 +12,16 @@
 // (row 8 (v/4) + 4 (l/32) + v % 4, column l % 32)).
 //
 // Four launches: A copied into a zero-padded [Mp x Kp] buffer (rows of Kp
-// bytes, Mp a multiple of 128, Kp of 32); its row sums, one wave per row; B
-// transposed into a zero-padded [Np x Kp] buffer (so both operands are
-// k-contiguous) with its column sums (integer atomics spread over the grid:
-// the sums are exact and order-free); then the
-// product in 128 x 128 blocks (4 waves of 64 x 64, 2 x 2 MFMA tiles each),
-// 32-deep K steps through LDS, and the correction and scaling in the
-// epilogue.  The zero padding adds nothing to the products, so the K loop
-// needs no bounds checks.
+// bytes, Mp a multiple of 256, Kp of 64); its row sums, one wave per row; B
+// transposed into a zero-padded [Np x Kp] buffer (Np a multiple of 128; both
+// operands k-contiguous) with its column sums (integer atomics spread over the
+// grid: the sums are exact and order-free); then the product in 256 x 128
+// blocks (4 waves of 128 x 64, 4 x 2 tiles of v_mfma_i32_32x32x32_i8 each: 6
+// fragment reads from LDS per 8 products), 64-deep K
+// steps through two LDS buffers (the next step's global loads are in flight
+// while the current step multiplies; one barrier per step), and the
+// correction and scaling in the epilogue.  The zero padding adds nothing to
+// the products, so the K loop needs no bounds checks.
 #include <cstdint>
 
 #include "common.hpp"
@@ -29,28 +31,42 @@ namespace nh {
 namespace {
 
 typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kQT = 128;     // block tile (rows and columns)
-constexpr int kQK = 32;      // K step
-constexpr int kQPad = 5;     // LDS row stride in 8-byte words (4 used): spreads rows over banks
+constexpr int kQLimitTile = 128;  // the API's row limit: 65535 tiles of 128 rows
+constexpr int kQTM = 4, kQTN = 2;  // 32 x 32 tiles per wave: a wave computes 128 x 64
+constexpr int kQBM = 64 * kQTM;    // block tile rows (2 x 2 waves)
+constexpr int kQBN = 64 * kQTN;    // block tile columns
+constexpr int kQK = 64;            // K step (bytes of a row per LDS stage)
+constexpr int kQRow = 5;           // LDS row stride in 16-byte units (4 used): 8 lanes of a
+                                   // 16-byte read cover all 32 four-byte banks once
+constexpr int kQGroupRows = 2048;  // rows per group of the block order
 
 // A [M x K] -> Ap [Mp x Kp] zero-padded.  Thread (i, u) copies bytes
-// 16u .. 16u + 15 of row i.
+// 16u .. 16u + 15 of row i: one 16-byte load where those bytes lie inside the
+// row at a 16-byte aligned address, else byte by byte; rows M .. Mp - 1 are
+// written as zeros.  The same launch zeroes colB[0 .. Np) for the B pass's
+// atomics (that pass runs after this one on the stream).
 __global__ __launch_bounds__(256) void k_qpad_a(const int8_t *__restrict__ A, int8_t *__restrict__ Ap, int64_t M,
-                                                int64_t K, int64_t Kp, int64_t units)
+                                                int64_t Mp, int64_t K, int64_t Kp, int64_t units,
+                                                int32_t *__restrict__ colB, int64_t Np)
 {
-    // grid-stride over the M * units 16-byte units of the real rows (rows
-    // M .. Mp - 1 of Ap were zeroed by the caller)
-    for (int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x; t < M * units; t += int64_t(gridDim.x) * 256) {
+    const int64_t g0 = int64_t(blockIdx.x) * 256 + threadIdx.x, stride = int64_t(gridDim.x) * 256;
+    for (int64_t j = g0; j < Np; j += stride) colB[j] = 0;
+    for (int64_t t = g0; t < Mp * units; t += stride) {
         const int64_t i = t / units, u = t - i * units;
-        int8_t b[16];
+        const int8_t *src = A + i * K + 16 * u;
+        int4 v = int4{0, 0, 0, 0};
+        if (i < M) {
+            if (16 * u + 16 <= K && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+                v = *reinterpret_cast<const int4 *>(src);
+            } else {
+                int8_t b[16];
 #pragma unroll
-        for (int q = 0; q < 16; q++) {
-            const int64_t k = 16 * u + q;
-            b[q] = k < K ? A[i * K + k] : int8_t(0);
+                for (int q = 0; q < 16; q++) b[q] = 16 * u + q < K ? src[q] : int8_t(0);
+                __builtin_memcpy(&v, b, 16);
+            }
         }
-        int4 v;
-        __builtin_memcpy(&v, b, 16);
         *reinterpret_cast<int4 *>(Ap + i * Kp + 16 * u) = v;
     }
 }
@@ -80,12 +96,14 @@ __global__ __launch_bounds__(256) void k_qrowsum(const int8_t *__restrict__ Ap, 
 
 // B [K x N] -> Bt [Np x Kp] (row j = column j of B) zero-padded; colB[j] +=
 // the thread's 16 bytes.  Threads of a wave take consecutive j, so each of the
-// 16 reads is one contiguous span of B's row k.
+// 16 reads is one contiguous span of B's row k.  Rows N .. Np - 1 of Bt are
+// written as zeros.
 __global__ __launch_bounds__(256) void k_qpad_bt(const int8_t *__restrict__ B, int8_t *__restrict__ Bt,
-                                                 int32_t *__restrict__ colB, int64_t K, int64_t N, int64_t Kp)
+                                                 int32_t *__restrict__ colB, int64_t K, int64_t N, int64_t Np,
+                                                 int64_t Kp)
 {
     const int64_t j = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (j >= N) return;
+    if (j >= Np) return;
     // 16-byte K units blockIdx.y, blockIdx.y + gridDim.y, ... (gridDim.y <= 65535)
     for (int64_t u = blockIdx.y; u < Kp / 16; u += gridDim.y) {
         int8_t b[16];
@@ -93,66 +111,113 @@ __global__ __launch_bounds__(256) void k_qpad_bt(const int8_t *__restrict__ B, i
 #pragma unroll
         for (int q = 0; q < 16; q++) {
             const int64_t k = 16 * u + q;
-            b[q] = k < K ? B[k * N + j] : int8_t(0);
+            b[q] = k < K && j < N ? B[k * N + j] : int8_t(0);
             s += b[q];
         }
         int4 v;
         __builtin_memcpy(&v, b, 16);
         *reinterpret_cast<int4 *>(Bt + j * Kp + 16 * u) = v;
-        atomicAdd(colB + j, s);
+        if (j < N) atomicAdd(colB + j, s);
     }
 }
 
+// Block order: the hardware hands block h to XCD h % 8 (each XCD has its own
+// L2), so h is first renumbered to make each XCD's blocks consecutive, then
+// taken in groups of kQGroupRows rows of tiles, column by column within a
+// group: the blocks that share an XCD share few A row panels and B column
+// panels.
+__device__ __forceinline__ void qgemm_tile(int64_t &bi, int64_t &bj)
+{
+    constexpr int64_t G = kQGroupRows / kQBM;
+    const int64_t nbx = gridDim.x, nby = gridDim.y, nb = nbx * nby;
+    const int64_t h = int64_t(blockIdx.y) * nbx + blockIdx.x;
+    const int64_t L = (nb & 7) == 0 ? (h & 7) * (nb >> 3) + (h >> 3) : h;
+    const int64_t gsz = G * nbx, g = L / gsz, r = L - g * gsz;
+    const int64_t first = g * G, rows = nby - first < G ? nby - first : G;
+    bi = first + r % rows;
+    bj = r / rows;
+}
+
+// C block (kQBM x kQBN) of tile (bi, bj).  Ap [Mp x Kp] and Bt [Np x Kp]
+// zero-padded, Kp a multiple of kQK.
 __global__ __launch_bounds__(256) void k_qgemm(const int8_t *__restrict__ Ap, const int8_t *__restrict__ Bt,
                                                double *__restrict__ C, const int32_t *__restrict__ rowA,
                                                const int32_t *__restrict__ colB, int64_t M, int64_t N, int64_t K,
                                                int64_t Kp, int32_t za, int32_t zb, double cs)
 {
-    __shared__ long sA[kQT][kQPad];
-    __shared__ long sB[kQT][kQPad];
+    __shared__ i32x4 sA[2][kQBM * kQRow];
+    __shared__ i32x4 sB[2][kQBN * kQRow];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int64_t i0 = int64_t(blockIdx.y) * kQT, j0 = int64_t(blockIdx.x) * kQT;
-    const int wr = 64 * (w >> 1), wc = 64 * (w & 1);  // the wave's 64 x 64 quadrant
-    i32x16 acc[2][2];
+    int64_t bi, bj;
+    qgemm_tile(bi, bj);
+    const int64_t i0 = bi * kQBM, j0 = bj * kQBN;
+    const int wr = 32 * kQTM * (w >> 1), wc = 32 * kQTN * (w & 1);  // the wave's quadrant
+    i32x16 acc[kQTM][kQTN];
 #pragma unroll
-    for (int a = 0; a < 2; a++)
+    for (int a = 0; a < kQTM; a++)
 #pragma unroll
-        for (int b = 0; b < 2; b++) acc[a][b] = i32x16{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-    // tile loads: thread t copies 16 bytes of row t / 2 (half t % 2) of each tile
-    const int lr = tid >> 1, lh = tid & 1;
-    const int8_t *pa = Ap + (i0 + lr) * Kp + 16 * lh;
-    const int8_t *pb = Bt + (j0 + lr) * Kp + 16 * lh;
-    for (int64_t k0 = 0; k0 < Kp; k0 += kQK) {
-        const int4 va = *reinterpret_cast<const int4 *>(pa + k0);
-        const int4 vb = *reinterpret_cast<const int4 *>(pb + k0);
-        long a2[2], b2[2];
-        __builtin_memcpy(a2, &va, 16);
-        __builtin_memcpy(b2, &vb, 16);
-        sA[lr][2 * lh] = a2[0];
-        sA[lr][2 * lh + 1] = a2[1];
-        sB[lr][2 * lh] = b2[0];
-        sB[lr][2 * lh + 1] = b2[1];
-        __syncthreads();
+        for (int b = 0; b < kQTN; b++) acc[a][b] = i32x16{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    // stage loads: thread t copies 16-byte unit t % 4 of rows t / 4 + 64 q
+    const int lr = tid >> 2, lu = tid & 3;
+    const int8_t *pa = Ap + (i0 + lr) * Kp + 16 * lu;
+    const int8_t *pb = Bt + (j0 + lr) * Kp + 16 * lu;
+    const int64_t far = 64 * Kp;
+    i32x4 ra[kQTM], rb[kQTN];
 #pragma unroll
-        for (int kc = 0; kc < kQK / 16; kc++) {
-            long av[2], bv[2];
+    for (int q = 0; q < kQTM; q++) ra[q] = *reinterpret_cast<const i32x4 *>(pa + q * far);
 #pragma unroll
-            for (int t = 0; t < 2; t++) {
-                av[t] = sA[wr + 32 * t + (lane & 31)][2 * kc + (lane >> 5)];
-                bv[t] = sB[wc + 32 * t + (lane & 31)][2 * kc + (lane >> 5)];
-            }
+    for (int q = 0; q < kQTN; q++) rb[q] = *reinterpret_cast<const i32x4 *>(pb + q * far);
+    const int st = lr * kQRow + lu;
 #pragma unroll
-            for (int a = 0; a < 2; a++)
+    for (int q = 0; q < kQTM; q++) sA[0][st + 64 * kQRow * q] = ra[q];
 #pragma unroll
-                for (int b = 0; b < 2; b++) acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x16_i8(av[a], bv[b], acc[a][b], 0, 0, 0);
+    for (int q = 0; q < kQTN; q++) sB[0][st + 64 * kQRow * q] = rb[q];
+    __syncthreads();
+    // fragment reads: lane l takes row (column) l % 32 of a 32 x 32 tile and
+    // bytes 16 (l / 32) .. 16 (l / 32) + 15 of a 32-deep chunk, for A and B
+    // alike, so every k meets its partner in the product
+    const int fa = (wr + (lane & 31)) * kQRow + (lane >> 5);
+    const int fb = (wc + (lane & 31)) * kQRow + (lane >> 5);
+    const int64_t steps = Kp / kQK;
+    for (int64_t s = 0; s < steps; s++) {
+        const int cur = int(s & 1);
+        // the next step's slice (the last step reloads its own: in bounds, unused)
+        const int64_t k1 = (s + 1 < steps ? s + 1 : s) * kQK;
+#pragma unroll
+        for (int q = 0; q < kQTM; q++) ra[q] = *reinterpret_cast<const i32x4 *>(pa + q * far + k1);
+#pragma unroll
+        for (int q = 0; q < kQTN; q++) rb[q] = *reinterpret_cast<const i32x4 *>(pb + q * far + k1);
+        // keep the loads ahead of the products (the scheduler would sink them
+        // next to their LDS stores and wait on them there)
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int c = 0; c < kQK / 32; c++) {
+            i32x4 av[kQTM], bv[kQTN];
+#pragma unroll
+            for (int t = 0; t < kQTM; t++) av[t] = sA[cur][fa + t * 32 * kQRow + 2 * c];
+#pragma unroll
+            for (int t = 0; t < kQTN; t++) bv[t] = sB[cur][fb + t * 32 * kQRow + 2 * c];
+#pragma unroll
+            for (int a = 0; a < kQTM; a++)
+#pragma unroll
+                for (int b = 0; b < kQTN; b++) acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[a], bv[b], acc[a][b], 0, 0, 0);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        // the other buffer was last read in step s - 1, before the barrier
+        // that ended it; after the last step nothing reads it
+#pragma unroll
+        for (int q = 0; q < kQTM; q++) sA[cur ^ 1][st + 64 * kQRow * q] = ra[q];
+#pragma unroll
+        for (int q = 0; q < kQTN; q++) sB[cur ^ 1][st + 64 * kQRow * q] = rb[q];
         __syncthreads();
     }
+    // result v of lane l is (row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32)
+    // of the 32 x 32 tile
     const uint32_t kzz = uint32_t(K) * uint32_t(za) * uint32_t(zb);
 #pragma unroll
-    for (int a = 0; a < 2; a++)
+    for (int a = 0; a < kQTM; a++)
 #pragma unroll
-        for (int b = 0; b < 2; b++) {
+        for (int b = 0; b < kQTN; b++) {
             const int64_t col = j0 + wc + 32 * b + (lane & 31);
             if (col >= N) continue;
             const uint32_t cterm = uint32_t(za) * uint32_t(colB[col]);
@@ -161,7 +226,7 @@ __global__ __launch_bounds__(256) void k_qgemm(const int8_t *__restrict__ Ap, co
                 const int64_t row = i0 + wr + 32 * a + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
                 if (row < M) {
                     const uint32_t s = uint32_t(acc[a][b][v]) - uint32_t(zb) * uint32_t(rowA[row]) - cterm + kzz;
-                    C[row * N + col] = double(int32_t(s)) * cs;
+                    __builtin_nontemporal_store(double(int32_t(s)) * cs, C + row * N + col);
                 }
             }
         }
@@ -179,13 +244,13 @@ static int qmatmul(const int8_t *A, const int8_t *B, double *C, int64_t M, int64
     if (!A || !B || !C || !pa || !pb) return -1;
     if (M <= 0 || K <= 0 || N <= 0) return -1;
     if (ensure_init() != NEURAL_OK) return -1;
-    const int64_t Mp = round_up(M, kQT), Np = round_up(N, kQT), Kp = round_up(K, kQK);
-    // grid limit: the product's row tiles run in grid y (M <= 65535 * 128 =
-    // 8,388,480; the reference has no such limit)
-    if (Mp / kQT > 65535) {
+    // the API's limit: 65535 tiles of 128 rows (M <= 8,388,480; the reference
+    // has no such limit)
+    if (round_up(M, kQLimitTile) / kQLimitTile > 65535) {
         set_error(NEURAL_ERR_TENSOR_TOO_LARGE);
         return -1;
     }
+    const int64_t Mp = round_up(M, kQBM), Np = round_up(N, kQBN), Kp = round_up(K, kQK);
     Staged sa, sb, sc;
     if (sa.open(A, size_t(M * K), true) != NEURAL_OK || sb.open(B, size_t(K * N), true) != NEURAL_OK ||
         sc.open(C, size_t(M * N) * sizeof(double), false) != NEURAL_OK)
@@ -198,30 +263,22 @@ static int qmatmul(const int8_t *A, const int8_t *B, double *C, int64_t M, int64
     }
     int8_t *Ap = reinterpret_cast<int8_t *>(blk), *Bt = Ap + bytesA;
     int32_t *rowA = reinterpret_cast<int32_t *>(Bt + bytesB), *colB = rowA + Mp;
-    int rc = NEURAL_OK;
-    // Only the padding rows (A rows M .. Mp-1, Bt rows N .. Np-1) and the
-    // row / column sums start at zero: the copies write every byte of the
-    // real rows, K padding included.
-    const size_t padA = size_t((Mp - M) * Kp), padB = size_t((Np - N) * Kp);
-    if ((padA && hipMemsetAsync(Ap + M * Kp, 0, padA, stream()) != hipSuccess) ||
-        (padB && hipMemsetAsync(Bt + N * Kp, 0, padB, stream()) != hipSuccess) ||
-        hipMemsetAsync(rowA, 0, size_t(Mp + Np) * sizeof(int32_t), stream()) != hipSuccess)
-        rc = NEURAL_ERR_INTERNAL;
+    // The copies write every byte of Ap and Bt (padding rows and K padding
+    // as zeros) and the A pass zeroes colB; rowA is written for rows < M, the
+    // only ones the product reads.
     const int64_t units = Kp / 16;
-    if (rc == NEURAL_OK) {
-        int64_t ga = ceil_div(M * units, 256);
-        ga = ga > kMaxGridBlocks ? kMaxGridBlocks : ga;
-        NH_LAUNCH(k_qpad_a, dim3(unsigned(ga)), dim3(256), 0, stream(), static_cast<const int8_t *>(sa.dev), Ap, M,
-                  K, Kp, units);
-        NH_LAUNCH(k_qrowsum, dim3(unsigned(ceil_div(M, 4))), dim3(256), 0, stream(), Ap, rowA, M, Kp);
-        const unsigned gy = unsigned(units < 65535 ? units : 65535);
-        NH_LAUNCH(k_qpad_bt, dim3(unsigned(ceil_div(N, 256)), gy), dim3(256), 0, stream(),
-                  static_cast<const int8_t *>(sb.dev), Bt, colB, K, N, Kp);
-        const double cs = pa->scale * pb->scale;  // combined_scale, quantize.c:198
-        NH_LAUNCH(k_qgemm, dim3(unsigned(Np / kQT), unsigned(Mp / kQT)), dim3(256), 0, stream(), Ap, Bt,
-                           static_cast<double *>(sc.dev), rowA, colB, M, N, K, Kp, pa->zero_point, pb->zero_point, cs);
-        rc = check_launch();
-    }
+    int64_t ga = ceil_div(Mp * units, 256);
+    ga = ga > kMaxGridBlocks ? kMaxGridBlocks : ga;
+    NH_LAUNCH(k_qpad_a, dim3(unsigned(ga)), dim3(256), 0, stream(), static_cast<const int8_t *>(sa.dev), Ap, M, Mp,
+              K, Kp, units, colB, Np);
+    NH_LAUNCH(k_qrowsum, dim3(unsigned(ceil_div(M, 4))), dim3(256), 0, stream(), Ap, rowA, M, Kp);
+    const unsigned gy = unsigned(units < 65535 ? units : 65535);
+    NH_LAUNCH(k_qpad_bt, dim3(unsigned(ceil_div(Np, 256)), gy), dim3(256), 0, stream(),
+              static_cast<const int8_t *>(sb.dev), Bt, colB, K, N, Np, Kp);
+    const double cs = pa->scale * pb->scale;  // combined_scale, quantize.c:198
+    NH_LAUNCH(k_qgemm, dim3(unsigned(Np / kQBN), unsigned(Mp / kQBM)), dim3(256), 0, stream(), Ap, Bt,
+              static_cast<double *>(sc.dev), rowA, colB, M, N, K, Kp, pa->zero_point, pb->zero_point, cs);
+    const int rc = check_launch();
     dev_free(blk);
     if (rc != NEURAL_OK) return -1;
     if (sc.finish(true) != NEURAL_OK || sa.finish(false) != NEURAL_OK || sb.finish(false) != NEURAL_OK) return -1;
