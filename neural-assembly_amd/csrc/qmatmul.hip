@@ -11,17 +11,18 @@
 // l % 32 and k = 8 (l / 32) + b of a 16-deep slice; result v of lane l is
 // (row 8 (v/4) + 4 (l/32) + v % 4, column l % 32)).
 //
-// Four launches: A copied into a zero-padded [Mp x Kp] buffer (rows of Kp
-// bytes, Mp a multiple of 256, Kp of 64); its row sums, one wave per row; B
+// Two launches (one where A needs no padding): A copied into a zero-padded
+// [Mp x Kp] buffer (rows of Kp bytes, Mp a multiple of 256, Kp of 64) unless
+// A already is one (M a multiple of 256, K of 64, 16-byte aligned); B
 // transposed into a zero-padded [Np x Kp] buffer (Np a multiple of 128; both
-// operands k-contiguous) with its column sums (integer atomics spread over the
-// grid: the sums are exact and order-free); then the product in 256 x 128
-// blocks (4 waves of 128 x 64, 4 x 2 tiles of v_mfma_i32_32x32x32_i8 each: 6
-// fragment reads from LDS per 8 products), 64-deep K
-// steps through two LDS buffers (the next step's global loads are in flight
-// while the current step multiplies; one barrier per step), and the
-// correction and scaling in the epilogue.  The zero padding adds nothing to
-// the products, so the K loop needs no bounds checks.
+// operands k-contiguous); then the product in 256 x 128 blocks (4 waves of
+// 128 x 64, 4 x 2 tiles of v_mfma_i32_32x32x32_i8 each: 6 fragment reads from
+// LDS per 8 products), 64-deep K steps through two LDS buffers (the next
+// step's global loads are in flight while the current step multiplies; one
+// barrier per step).  The block also sums its rows of A and columns of B from
+// the bytes it stages (v_dot4_i32_i8 against ones; the zero padding adds
+// nothing) and applies the correction and scaling in the epilogue.  The K
+// loop needs no bounds checks.
 #include <cstdint>
 
 #include "common.hpp"
@@ -45,14 +46,11 @@ constexpr int kQGroupRows = 2048;  // rows per group of the block order
 // A [M x K] -> Ap [Mp x Kp] zero-padded.  Thread (i, u) copies bytes
 // 16u .. 16u + 15 of row i: one 16-byte load where those bytes lie inside the
 // row at a 16-byte aligned address, else byte by byte; rows M .. Mp - 1 are
-// written as zeros.  The same launch zeroes colB[0 .. Np) for the B pass's
-// atomics (that pass runs after this one on the stream).
+// written as zeros.
 __global__ __launch_bounds__(256) void k_qpad_a(const int8_t *__restrict__ A, int8_t *__restrict__ Ap, int64_t M,
-                                                int64_t Mp, int64_t K, int64_t Kp, int64_t units,
-                                                int32_t *__restrict__ colB, int64_t Np)
+                                                int64_t Mp, int64_t K, int64_t Kp, int64_t units)
 {
     const int64_t g0 = int64_t(blockIdx.x) * 256 + threadIdx.x, stride = int64_t(gridDim.x) * 256;
-    for (int64_t j = g0; j < Np; j += stride) colB[j] = 0;
     for (int64_t t = g0; t < Mp * units; t += stride) {
         const int64_t i = t / units, u = t - i * units;
         const int8_t *src = A + i * K + 16 * u;
@@ -71,54 +69,58 @@ __global__ __launch_bounds__(256) void k_qpad_a(const int8_t *__restrict__ A, in
     }
 }
 
-// Sum of the four signed bytes of w.
-__device__ __forceinline__ int32_t byte_sum(int32_t w)
+// B [K x N] -> Bt [Np x Kp] (row j = column j of B) zero-padded, rows
+// N .. Np - 1 as zeros.  A thread transposes a 16 x 4 byte block: 16 rows
+// k = 64 g + 16 (l % 4) + q of B times 4 columns 4 c .. 4 c + 3 (one 4-byte
+// load per row where N is a multiple of 4 and B 4-byte aligned, else byte
+// loads), into 16 bytes of each of 4 rows of Bt.  Lane l of a wave takes
+// column group c = 16 (wave) + l / 4 within its block: its loads read 64
+// contiguous bytes of 4 rows of B, and lanes 4 m .. 4 m + 3 write 64
+// contiguous bytes of each of their rows of Bt.
+__global__ __launch_bounds__(256) void k_qpad_bt(const int8_t *__restrict__ B, int8_t *__restrict__ Bt, int64_t K,
+                                                 int64_t N, int64_t Np, int64_t Kp, int vec)
 {
-    return int32_t(int8_t(w)) + int32_t(int8_t(w >> 8)) + int32_t(int8_t(w >> 16)) + (w >> 24);
-}
-
-// rowA[i] = sum of row i of Ap (its padding is zero), one wave per row.
-__global__ __launch_bounds__(256) void k_qrowsum(const int8_t *__restrict__ Ap, int32_t *__restrict__ rowA,
-                                                 int64_t M, int64_t Kp)
-{
-    const int64_t i = (int64_t(blockIdx.x) * 256 + threadIdx.x) >> 6;
-    const int lane = threadIdx.x & 63;
-    if (i >= M) return;  // uniform per wave
-    const int4 *row = reinterpret_cast<const int4 *>(Ap + i * Kp);
-    int32_t s = 0;
-    for (int64_t u = lane; u < Kp / 16; u += 64) {
-        const int4 v = row[u];
-        s += byte_sum(v.x) + byte_sum(v.y) + byte_sum(v.z) + byte_sum(v.w);
-    }
-    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
-    if (lane == 0) rowA[i] = s;
-}
-
-// B [K x N] -> Bt [Np x Kp] (row j = column j of B) zero-padded; colB[j] +=
-// the thread's 16 bytes.  Threads of a wave take consecutive j, so each of the
-// 16 reads is one contiguous span of B's row k.  Rows N .. Np - 1 of Bt are
-// written as zeros.
-__global__ __launch_bounds__(256) void k_qpad_bt(const int8_t *__restrict__ B, int8_t *__restrict__ Bt,
-                                                 int32_t *__restrict__ colB, int64_t K, int64_t N, int64_t Np,
-                                                 int64_t Kp)
-{
-    const int64_t j = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (j >= Np) return;
-    // 16-byte K units blockIdx.y, blockIdx.y + gridDim.y, ... (gridDim.y <= 65535)
-    for (int64_t u = blockIdx.y; u < Kp / 16; u += gridDim.y) {
-        int8_t b[16];
-        int32_t s = 0;
+    const int64_t c = int64_t(blockIdx.x) * 64 + (threadIdx.x >> 2);  // column group
+    if (4 * c >= Np) return;
+    const int ul = threadIdx.x & 3;
+    // 64-byte K groups blockIdx.y, blockIdx.y + gridDim.y, ... (gridDim.y <= 65535)
+    for (int64_t g = blockIdx.y; g < Kp / 64; g += gridDim.y) {
+        const int64_t k0 = 64 * g + 16 * ul;
+        uint32_t w[16];
 #pragma unroll
         for (int q = 0; q < 16; q++) {
-            const int64_t k = 16 * u + q;
-            b[q] = k < K && j < N ? B[k * N + j] : int8_t(0);
-            s += b[q];
+            const int64_t k = k0 + q;
+            w[q] = 0;
+            if (k < K) {
+                if (vec && 4 * c < N) {
+                    w[q] = *reinterpret_cast<const uint32_t *>(B + k * N + 4 * c);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (4 * c + e < N) w[q] |= uint32_t(uint8_t(B[k * N + 4 * c + e])) << (8 * e);
+                }
+            }
         }
-        int4 v;
-        __builtin_memcpy(&v, b, 16);
-        *reinterpret_cast<int4 *>(Bt + j * Kp + 16 * u) = v;
-        if (j < N) atomicAdd(colB + j, s);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            uint32_t o[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                o[r] = ((w[4 * r] >> (8 * e)) & 0xff) | (((w[4 * r + 1] >> (8 * e)) & 0xff) << 8) |
+                       (((w[4 * r + 2] >> (8 * e)) & 0xff) << 16) | (((w[4 * r + 3] >> (8 * e)) & 0xff) << 24);
+            *reinterpret_cast<uint4 *>(Bt + (4 * c + e) * Kp + k0) = uint4{o[0], o[1], o[2], o[3]};
+        }
     }
+}
+
+// acc + the sum of the 16 signed bytes of v (v_dot4_i32_i8 against ones;
+// wraps mod 2^32 like the reference's int32 sums).
+__device__ __forceinline__ int32_t byte_sum4(i32x4 v, int32_t acc)
+{
+    acc = __builtin_amdgcn_sdot4(v.x, 0x01010101, acc, false);
+    acc = __builtin_amdgcn_sdot4(v.y, 0x01010101, acc, false);
+    acc = __builtin_amdgcn_sdot4(v.z, 0x01010101, acc, false);
+    return __builtin_amdgcn_sdot4(v.w, 0x01010101, acc, false);
 }
 
 // Block order: the hardware hands block h to XCD h % 8 (each XCD has its own
@@ -141,12 +143,12 @@ __device__ __forceinline__ void qgemm_tile(int64_t &bi, int64_t &bj)
 // C block (kQBM x kQBN) of tile (bi, bj).  Ap [Mp x Kp] and Bt [Np x Kp]
 // zero-padded, Kp a multiple of kQK.
 __global__ __launch_bounds__(256) void k_qgemm(const int8_t *__restrict__ Ap, const int8_t *__restrict__ Bt,
-                                               double *__restrict__ C, const int32_t *__restrict__ rowA,
-                                               const int32_t *__restrict__ colB, int64_t M, int64_t N, int64_t K,
-                                               int64_t Kp, int32_t za, int32_t zb, double cs)
+                                               double *__restrict__ C, int64_t M, int64_t N, int64_t K, int64_t Kp,
+                                               int32_t za, int32_t zb, double cs)
 {
     __shared__ i32x4 sA[2][kQBM * kQRow];
     __shared__ i32x4 sB[2][kQBN * kQRow];
+    __shared__ int32_t sRow[kQBM], sCol[kQBN];  // sums of the block's rows of A, columns of B
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     int64_t bi, bj;
     qgemm_tile(bi, bj);
@@ -167,6 +169,19 @@ __global__ __launch_bounds__(256) void k_qgemm(const int8_t *__restrict__ Ap, co
     for (int q = 0; q < kQTM; q++) ra[q] = *reinterpret_cast<const i32x4 *>(pa + q * far);
 #pragma unroll
     for (int q = 0; q < kQTN; q++) rb[q] = *reinterpret_cast<const i32x4 *>(pb + q * far);
+    // partial sums of the thread's rows of A / columns of B over its units
+    int32_t ha[kQTM], hb[kQTN];
+    auto add_sums = [&]() {
+#pragma unroll
+        for (int q = 0; q < kQTM; q++) ha[q] = byte_sum4(ra[q], ha[q]);
+#pragma unroll
+        for (int q = 0; q < kQTN; q++) hb[q] = byte_sum4(rb[q], hb[q]);
+    };
+#pragma unroll
+    for (int q = 0; q < kQTM; q++) ha[q] = 0;
+#pragma unroll
+    for (int q = 0; q < kQTN; q++) hb[q] = 0;
+    add_sums();
     const int st = lr * kQRow + lu;
 #pragma unroll
     for (int q = 0; q < kQTM; q++) sA[0][st + 64 * kQRow * q] = ra[q];
@@ -181,7 +196,8 @@ __global__ __launch_bounds__(256) void k_qgemm(const int8_t *__restrict__ Ap, co
     const int64_t steps = Kp / kQK;
     for (int64_t s = 0; s < steps; s++) {
         const int cur = int(s & 1);
-        // the next step's slice (the last step reloads its own: in bounds, unused)
+        // the next step's slice (the last step reloads its own: in bounds, and
+        // its sum is taken out after the loop)
         const int64_t k1 = (s + 1 < steps ? s + 1 : s) * kQK;
 #pragma unroll
         for (int q = 0; q < kQTM; q++) ra[q] = *reinterpret_cast<const i32x4 *>(pa + q * far + k1);
@@ -203,6 +219,7 @@ __global__ __launch_bounds__(256) void k_qgemm(const int8_t *__restrict__ Ap, co
                 for (int b = 0; b < kQTN; b++) acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[a], bv[b], acc[a][b], 0, 0, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
+        add_sums();
         // the other buffer was last read in step s - 1, before the barrier
         // that ended it; after the last step nothing reads it
 #pragma unroll
@@ -211,6 +228,26 @@ __global__ __launch_bounds__(256) void k_qgemm(const int8_t *__restrict__ Ap, co
         for (int q = 0; q < kQTN; q++) sB[cur ^ 1][st + 64 * kQRow * q] = rb[q];
         __syncthreads();
     }
+    // the last step's reload was summed twice: take it out once (exact mod
+    // 2^32); then whole-row sums: lanes 4 m .. 4 m + 3 hold the four units
+    // of a row
+#pragma unroll
+    for (int q = 0; q < kQTM; q++) ha[q] -= byte_sum4(ra[q], 0);
+#pragma unroll
+    for (int q = 0; q < kQTN; q++) hb[q] -= byte_sum4(rb[q], 0);
+#pragma unroll
+    for (int q = 0; q < kQTM; q++) {
+        ha[q] += __shfl_xor(ha[q], 1, 64);
+        ha[q] += __shfl_xor(ha[q], 2, 64);
+        if (lu == 0) sRow[lr + 64 * q] = ha[q];
+    }
+#pragma unroll
+    for (int q = 0; q < kQTN; q++) {
+        hb[q] += __shfl_xor(hb[q], 1, 64);
+        hb[q] += __shfl_xor(hb[q], 2, 64);
+        if (lu == 0) sCol[lr + 64 * q] = hb[q];
+    }
+    __syncthreads();
     // result v of lane l is (row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32)
     // of the 32 x 32 tile
     const uint32_t kzz = uint32_t(K) * uint32_t(za) * uint32_t(zb);
@@ -220,12 +257,13 @@ __global__ __launch_bounds__(256) void k_qgemm(const int8_t *__restrict__ Ap, co
         for (int b = 0; b < kQTN; b++) {
             const int64_t col = j0 + wc + 32 * b + (lane & 31);
             if (col >= N) continue;
-            const uint32_t cterm = uint32_t(za) * uint32_t(colB[col]);
+            const uint32_t cterm = uint32_t(za) * uint32_t(sCol[wc + 32 * b + (lane & 31)]);
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                const int64_t row = i0 + wr + 32 * a + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                const int rl = wr + 32 * a + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                const int64_t row = i0 + rl;
                 if (row < M) {
-                    const uint32_t s = uint32_t(acc[a][b][v]) - uint32_t(zb) * uint32_t(rowA[row]) - cterm + kzz;
+                    const uint32_t s = uint32_t(acc[a][b][v]) - uint32_t(zb) * uint32_t(sRow[rl]) - cterm + kzz;
                     __builtin_nontemporal_store(double(int32_t(s)) * cs, C + row * N + col);
                 }
             }
@@ -255,29 +293,33 @@ static int qmatmul(const int8_t *A, const int8_t *B, double *C, int64_t M, int64
     if (sa.open(A, size_t(M * K), true) != NEURAL_OK || sb.open(B, size_t(K * N), true) != NEURAL_OK ||
         sc.open(C, size_t(M * N) * sizeof(double), false) != NEURAL_OK)
         return -1;
-    const size_t bytesA = size_t(Mp * Kp), bytesB = size_t(Np * Kp);
-    char *blk = static_cast<char *>(dev_alloc(bytesA + bytesB + size_t(Mp + Np) * sizeof(int32_t)));
+    // A serves as its own padded copy when it already has the padded shape
+    const bool copyA = Mp != M || Kp != K || (reinterpret_cast<uintptr_t>(sa.dev) & 15) != 0;
+    const size_t bytesA = copyA ? size_t(Mp * Kp) : 0, bytesB = size_t(Np * Kp);
+    char *blk = static_cast<char *>(dev_alloc(bytesA + bytesB));
     if (!blk) {
         set_error(NEURAL_ERR_OUT_OF_MEMORY);
         return -1;
     }
-    int8_t *Ap = reinterpret_cast<int8_t *>(blk), *Bt = Ap + bytesA;
-    int32_t *rowA = reinterpret_cast<int32_t *>(Bt + bytesB), *colB = rowA + Mp;
+    int8_t *Bt = reinterpret_cast<int8_t *>(blk) + bytesA;
+    const int8_t *Ap = copyA ? reinterpret_cast<int8_t *>(blk) : static_cast<const int8_t *>(sa.dev);
     // The copies write every byte of Ap and Bt (padding rows and K padding
-    // as zeros) and the A pass zeroes colB; rowA is written for rows < M, the
-    // only ones the product reads.
-    const int64_t units = Kp / 16;
-    int64_t ga = ceil_div(Mp * units, 256);
-    ga = ga > kMaxGridBlocks ? kMaxGridBlocks : ga;
-    NH_LAUNCH(k_qpad_a, dim3(unsigned(ga)), dim3(256), 0, stream(), static_cast<const int8_t *>(sa.dev), Ap, M, Mp,
-              K, Kp, units, colB, Np);
-    NH_LAUNCH(k_qrowsum, dim3(unsigned(ceil_div(M, 4))), dim3(256), 0, stream(), Ap, rowA, M, Kp);
-    const unsigned gy = unsigned(units < 65535 ? units : 65535);
+    // as zeros).
+    if (copyA) {
+        const int64_t units = Kp / 16;
+        int64_t ga = ceil_div(Mp * units, 256);
+        ga = ga > kMaxGridBlocks ? kMaxGridBlocks : ga;
+        NH_LAUNCH(k_qpad_a, dim3(unsigned(ga)), dim3(256), 0, stream(), static_cast<const int8_t *>(sa.dev),
+                  reinterpret_cast<int8_t *>(blk), M, Mp, K, Kp, units);
+    }
+    const int64_t groups = Kp / 64;
+    const unsigned gy = unsigned(groups < 65535 ? groups : 65535);
+    const int vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(sb.dev) & 3) == 0;
     NH_LAUNCH(k_qpad_bt, dim3(unsigned(ceil_div(Np, 256)), gy), dim3(256), 0, stream(),
-              static_cast<const int8_t *>(sb.dev), Bt, colB, K, N, Np, Kp);
+              static_cast<const int8_t *>(sb.dev), Bt, K, N, Np, Kp, vec);
     const double cs = pa->scale * pb->scale;  // combined_scale, quantize.c:198
     NH_LAUNCH(k_qgemm, dim3(unsigned(Np / kQBN), unsigned(Mp / kQBM)), dim3(256), 0, stream(), Ap, Bt,
-              static_cast<double *>(sc.dev), rowA, colB, M, N, K, Kp, pa->zero_point, pb->zero_point, cs);
+              static_cast<double *>(sc.dev), M, N, K, Kp, pa->zero_point, pb->zero_point, cs);
     const int rc = check_launch();
     dev_free(blk);
     if (rc != NEURAL_OK) return -1;

@@ -204,7 +204,7 @@ def _qmm_params(ora, za, zb):
 
 
 @pytest.mark.parametrize("m,k,n", [(1, 1, 1), (3, 5, 7), (128, 128, 128), (130, 257, 129), (64, 4096, 64),
-                                   (257, 33, 1000), (300, 1000, 500)])
+                                   (257, 33, 1000), (300, 1000, 500), (256, 64, 260), (512, 192, 3)])
 @pytest.mark.parametrize("za,zb", [(0, 0), (-128, 127), (17, -3)])
 def test_quantized_matmul_bit_exact(pn, ora, m, k, n, za, zb):
     rng = np.random.default_rng(m + 7 * k + 13 * n + za + 1000)
@@ -242,6 +242,25 @@ def test_quantized_matmul_device_wrap_and_errors(pn, ora):
                                 ctypes.byref(qb)) == 0
     torch.cuda.synchronize()
     same_bits(dc.cpu().numpy().reshape(-1), ora.quantized_matmul(a, b, m, k, n, pa, pb)[1].reshape(-1))
+    # A in the padded shape (256 x 128) used in place, or copied when it sits
+    # at an address that is not 16-byte aligned; B at an odd address (byte
+    # loads in the transpose) or aligned with N a multiple of 4 (4-byte loads)
+    m3, k3, n3 = 256, 128, 12
+    a3 = rng.integers(-128, 128, (m3, k3), dtype=np.int64).astype(np.int8)
+    b3 = rng.integers(-128, 128, (k3, n3), dtype=np.int64).astype(np.int8)
+    want3 = ora.quantized_matmul(a3, b3, m3, k3, n3, pa, pb)[1].reshape(-1)
+    for off in (0, 1):
+        ha = np.zeros(m3 * k3 + 16, dtype=np.int8)
+        hb = np.zeros(k3 * n3 + 16, dtype=np.int8)
+        ha[off:off + m3 * k3] = a3.reshape(-1)
+        hb[off:off + k3 * n3] = b3.reshape(-1)
+        da3, db3 = torch.from_numpy(ha).cuda(), torch.from_numpy(hb).cuda()
+        dc3 = torch.empty(m3, n3, dtype=torch.float64, device="cuda")
+        torch.cuda.synchronize()
+        assert lib.quantized_matmul(da3.data_ptr() + off, db3.data_ptr() + off, dc3.data_ptr(), m3, k3, n3,
+                                    ctypes.byref(qa), ctypes.byref(qb)) == 0
+        torch.cuda.synchronize()
+        same_bits(dc3.cpu().numpy().reshape(-1), want3)
     # a sum past int32 wraps mod 2^32, as in the compiled reference
     k2 = 40_000
     a2 = np.full((3, k2), -128, dtype=np.int8)
