@@ -129,28 +129,37 @@ NH_DEV double gelu_d(double x)
 //   x > 0:   log(1 + e^x) = x + log(1 + t); the rounding of 1 + t moves that
 //            by at most 2^-53, below 1.6e-16 of a result > log 2;
 // log of u in [1, 2]: m = u, or u / 2 above sqrt 2 (then + ln 2), and
-// log m = 2 atanh(s), s = (m - 1) / (m + 1) in [-0.172, 0.172] (m - 1 exact),
-// by the odd series through s^15 (truncation below 3.4e-14 relative, inside
-// the 1e-12 f64 bar) -- no frexp, and a refined reciprocal for the quotient.  The reference's double exp overflows above 709.78 (+inf).
+// log m = 2 atanh(s) = 2s + 2s^3 g(s^2), s = (m - 1) / (m + 1) in
+// [-0.172, 0.172] (m - 1 exact), g by a degree-5 polynomial in w = s^2 fitted
+// near-minimax on [0, 0.0295] (7e-16 relative on log m with an exact
+// quotient, against 3.4e-14 for the Taylor series through s^15 it replaces).
+// The quotient takes the hardware reciprocal with one Newton step: a seed
+// within 2^-22 leaves 5.8e-14 relative on log m (checked over 4e7 values of u
+// on the CPU), inside the 1e-12 f64 bar.  The reference's double exp
+// overflows above 709.78 (+inf).
+NH_DEV double rcp_nr1(double d)
+{
+    const double r = __builtin_amdgcn_rcp(d);
+    return __builtin_fma(r, __builtin_fma(-d, r, 1.0), r);
+}
+
 NH_DEV double softplus_d(double x)
 {
     const double t = exp(-__builtin_fabs(x));
     const double u = 1.0 + t;
     const bool hi = u > 0x1.6a09e667f3bcdp+0;  // sqrt 2
-    const double m = hi ? 0.5 * u : u;
-    const double s = (m - 1.0) * rcp_nr(m + 1.0);
-    const double s2 = s * s;
-    double q = 1.0 / 15.0;
-    q = __builtin_fma(q, s2, 1.0 / 13.0);
-    q = __builtin_fma(q, s2, 1.0 / 11.0);
-    q = __builtin_fma(q, s2, 1.0 / 9.0);
-    q = __builtin_fma(q, s2, 1.0 / 7.0);
-    q = __builtin_fma(q, s2, 1.0 / 5.0);
-    q = __builtin_fma(q, s2, 1.0 / 3.0);
+    const double m = u * (hi ? 0.5 : 1.0);     // exact
+    const double s = (m - 1.0) * rcp_nr1(m + 1.0);
+    const double w = s * s;
+    double q = 0x1.58e1eaa5792a2p-4;
+    q = __builtin_fma(q, w, 0x1.732185997e49ap-4);
+    q = __builtin_fma(q, w, 0x1.c722e0b18874dp-4);
+    q = __builtin_fma(q, w, 0x1.2492408227507p-3);
+    q = __builtin_fma(q, w, 0x1.999999a4af1eap-3);
+    q = __builtin_fma(q, w, 0x1.5555555552c78p-2);
     const double s_2 = s + s;
-    const double lm = __builtin_fma(s_2 * s2, q, s_2);
-    const double l = hi ? lm + 0x1.62e42fefa39efp-1 : lm;  // + ln 2
-    const double r = x <= 0.0 ? l : x + l;
+    const double l = __builtin_fma(s_2 * w, q, s_2) + (hi ? 0x1.62e42fefa39efp-1 : 0.0);  // + ln 2
+    const double r = __builtin_fmax(x, 0.0) + l;  // x <= 0: l exactly
     return x > 0x1.62e42fefa39efp+9 ? __builtin_inf() : r;  // 709.782712893384
 }
 
