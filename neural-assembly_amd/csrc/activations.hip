@@ -20,10 +20,10 @@
 //   1.0 + tanh(z)       (gelu, z << 0): tanh(z) rounds to a multiple of 2^-53 in
 //                       [-1, -0.5], so 1 + tanh(z) is that multiple; it is
 //                       rebuilt as rint(eps * 2^53) * 2^-53 from eps = 1 - |tanh z|
-//                       computed to double accuracy.
+//                       computed to ~2^-48 relative (a few 2^-53 steps at most).
 //
-// Everything else matches the reference's value to a few double ulps (libm
-// differences aside), far inside the 1e-5 (f32) / 1e-12 + 1e-15 (f64) bars.
+// Everything else matches the reference's value to ~1e-14 relative or better
+// (libm differences aside), far inside the 1e-5 (f32) / 1e-12 + 1e-15 (f64) bars.
 // f32 tensors use the float-output paths below.
 #include <cmath>
 
@@ -35,16 +35,15 @@ constexpr double kGelu = 0.7978845608028654;
 constexpr double kSeluL = 1.0507009873554804934193349852946;
 constexpr double kSeluA = 1.6732632423543772848170429916717;
 // 1 / d for normal d of moderate size (2^-1000 < |d| < 2^1000): the hardware
-// reciprocal refined by two Newton steps (each squares the relative error;
-// the result is within an ulp or two of the correctly rounded quotient, ~5
-// instructions instead of a division's ~12).
-NH_DEV double rcp_nr(double d)
+// reciprocal refined by one Newton step, 3 instructions instead of a
+// division's ~12.  The seed measured within 2^-24.4 relative on the GPU (16 M
+// values in [1, 4]); the step squares that, so the result is within ~2^-48
+// (~30 ulp), and a quotient built on it stays ~1e-14 relative or better,
+// far inside the 1e-12 f64 bar.
+NH_DEV double rcp_nr1(double d)
 {
-    double r = __builtin_amdgcn_rcp(d);
-    double e = __builtin_fma(-d, r, 1.0);
-    r = __builtin_fma(r, e, r);
-    e = __builtin_fma(-d, r, 1.0);
-    return __builtin_fma(r, e, r);
+    const double r = __builtin_amdgcn_rcp(d);
+    return __builtin_fma(r, __builtin_fma(-d, r, 1.0), r);
 }
 
 // e^a for a in [0, 44] (tanh's argument): a = k ln2 + r, |r| <= ln2/2, e^r by
@@ -80,7 +79,7 @@ NH_DEV double exp_in_range(double a)
 // x^7 (truncation below 3e-19 relative; zeros keep their sign, denormals are
 // returned unchanged).
 // E - 1 is exact, so the relative error is ~1 ulp(E) / (E - 1) < 1.5e-14 (plus
-// an ulp or two from the reciprocal).
+// ~2^-48 from the reciprocal).
 NH_DEV double tanh_d(double x)
 {
     const double a = __builtin_fabs(x);
@@ -89,7 +88,7 @@ NH_DEV double tanh_d(double x)
         __builtin_fma(x * x2, __builtin_fma(x2, __builtin_fma(x2, -17.0 / 315.0, 2.0 / 15.0), -1.0 / 3.0), x), x);
     const double c = a < 22.0 ? a : 22.0;
     const double e = exp_in_range(c + c);
-    const double big = __builtin_copysign((e - 1.0) * rcp_nr(e + 1.0), x);
+    const double big = __builtin_copysign((e - 1.0) * rcp_nr1(e + 1.0), x);
     return (a < 0x1p-7 || x != x) ? small : big;
 }
 
@@ -109,7 +108,7 @@ NH_DEV double one_plus_tanh(double z)
 {
     const double a = -2.0 * __builtin_fabs(z);
     const double w = exp(a > -40.0 ? a : -40.0);
-    const double r = rcp_nr(1.0 + w);
+    const double r = rcp_nr1(1.0 + w);
     const double eps = (w + w) * r;
     // eps rounded to a multiple of 2^-53, ties to even: 0.5 + eps (in [0.5, 1),
     // ulp 2^-53) rounds exactly so, and subtracting 0.5 is exact
@@ -133,16 +132,10 @@ NH_DEV double gelu_d(double x)
 // [-0.172, 0.172] (m - 1 exact), g by a degree-5 polynomial in w = s^2 fitted
 // near-minimax on [0, 0.0295] (7e-16 relative on log m with an exact
 // quotient, against 3.4e-14 for the Taylor series through s^15 it replaces).
-// The quotient takes the hardware reciprocal with one Newton step: a seed
-// within 2^-22 leaves 5.8e-14 relative on log m (checked over 4e7 values of u
-// on the CPU), inside the 1e-12 f64 bar.  The reference's double exp
+// The quotient's reciprocal has one Newton step: even a seed within only
+// 2^-22 would leave 5.8e-14 relative on log m (checked over 4e7 values of u
+// on the CPU).  The reference's double exp
 // overflows above 709.78 (+inf).
-NH_DEV double rcp_nr1(double d)
-{
-    const double r = __builtin_amdgcn_rcp(d);
-    return __builtin_fma(r, __builtin_fma(-d, r, 1.0), r);
-}
-
 NH_DEV double softplus_d(double x)
 {
     const double t = exp(-__builtin_fabs(x));
@@ -177,7 +170,7 @@ NH_DEV double mish_d(double x)
     const double t = (1.0 + s) - 1.0;
     const double num = pos ? __builtin_fma(2.0, s, 1.0) : t * (2.0 + t);
     const double den = num + (pos ? 2.0 * (s * s) : 2.0);
-    return x * (num * rcp_nr(den));
+    return x * (num * rcp_nr1(den));
 }
 
 // ---- f32 outputs ----------------------------------------------------------------
