@@ -20,7 +20,7 @@
 //   1.0 + tanh(z)       (gelu, z << 0): tanh(z) rounds to a multiple of 2^-53 in
 //                       [-1, -0.5], so 1 + tanh(z) is that multiple; it is
 //                       rebuilt as rint(eps * 2^53) * 2^-53 from eps = 1 - |tanh z|
-//                       computed to ~2^-48 relative (a few 2^-53 steps at most).
+//                       computed to a few ulp (a few 2^-53 steps at most).
 //
 // Everything else matches the reference's value to ~1e-14 relative or better
 // (libm differences aside), far inside the 1e-5 (f32) / 1e-12 + 1e-15 (f64) bars.
@@ -34,15 +34,28 @@ namespace nh {
 constexpr double kGelu = 0.7978845608028654;
 constexpr double kSeluL = 1.0507009873554804934193349852946;
 constexpr double kSeluA = 1.6732632423543772848170429916717;
-// 1 / d for normal d of moderate size (2^-1000 < |d| < 2^1000): the hardware
-// reciprocal refined by one Newton step, 3 instructions instead of a
-// division's ~12.  The seed measured within 2^-24.4 relative on the GPU (16 M
-// values in [1, 4]); the step squares that, so the result is within ~2^-48
-// (~30 ulp), and a quotient built on it stays ~1e-14 relative or better,
-// far inside the 1e-12 f64 bar.
+// 1 / d for normal d of moderate size (2^-1000 < |d| < 2^1000) from the
+// hardware reciprocal seed.  AMD does not publish a bound for the f64 seed;
+// a GPU probe measured 2^-24.4 relative over 16 M values in [1, 4].
+//   rcp_nr2: two Newton steps (5 instructions instead of a division's ~12):
+//            a seed even as coarse as 2^-12 ends within ~2^-48, and a seed
+//            within 2^-22 ends at the rounding error of the last FMA (~1 ulp).
+//            Used by tanh, gelu and mish, whose quotients feed the result
+//            directly.
+//   rcp_nr1: one Newton step (3 instructions): the seed's error squared, so
+//            ~2^-44 for a 2^-22 seed.  Used only by softplus, where the
+//            reciprocal enters the atanh series of log m through s = (m - 1) /
+//            (m + 1), |s| <= 0.172: checked on the CPU over 4e7 values of u
+//            with a seed perturbed by 2^-22, the log stays within 5.8e-14.
 NH_DEV double rcp_nr1(double d)
 {
     const double r = __builtin_amdgcn_rcp(d);
+    return __builtin_fma(r, __builtin_fma(-d, r, 1.0), r);
+}
+NH_DEV double rcp_nr2(double d)
+{
+    double r = __builtin_amdgcn_rcp(d);
+    r = __builtin_fma(r, __builtin_fma(-d, r, 1.0), r);
     return __builtin_fma(r, __builtin_fma(-d, r, 1.0), r);
 }
 
@@ -79,7 +92,7 @@ NH_DEV double exp_in_range(double a)
 // x^7 (truncation below 3e-19 relative; zeros keep their sign, denormals are
 // returned unchanged).
 // E - 1 is exact, so the relative error is ~1 ulp(E) / (E - 1) < 1.5e-14 (plus
-// ~2^-48 from the reciprocal).
+// ~1 ulp from the reciprocal).
 NH_DEV double tanh_d(double x)
 {
     const double a = __builtin_fabs(x);
@@ -88,7 +101,7 @@ NH_DEV double tanh_d(double x)
         __builtin_fma(x * x2, __builtin_fma(x2, __builtin_fma(x2, -17.0 / 315.0, 2.0 / 15.0), -1.0 / 3.0), x), x);
     const double c = a < 22.0 ? a : 22.0;
     const double e = exp_in_range(c + c);
-    const double big = __builtin_copysign((e - 1.0) * rcp_nr1(e + 1.0), x);
+    const double big = __builtin_copysign((e - 1.0) * rcp_nr2(e + 1.0), x);
     return (a < 0x1p-7 || x != x) ? small : big;
 }
 
@@ -108,7 +121,7 @@ NH_DEV double one_plus_tanh(double z)
 {
     const double a = -2.0 * __builtin_fabs(z);
     const double w = exp(a > -40.0 ? a : -40.0);
-    const double r = rcp_nr1(1.0 + w);
+    const double r = rcp_nr2(1.0 + w);
     const double eps = (w + w) * r;
     // eps rounded to a multiple of 2^-53, ties to even: 0.5 + eps (in [0.5, 1),
     // ulp 2^-53) rounds exactly so, and subtracting 0.5 is exact
@@ -170,7 +183,7 @@ NH_DEV double mish_d(double x)
     const double t = (1.0 + s) - 1.0;
     const double num = pos ? __builtin_fma(2.0, s, 1.0) : t * (2.0 + t);
     const double den = num + (pos ? 2.0 * (s * s) : 2.0);
-    return x * (num * rcp_nr1(den));
+    return x * (num * rcp_nr2(den));
 }
 
 // ---- f32 outputs ----------------------------------------------------------------
@@ -180,8 +193,9 @@ NH_DEV double mish_d(double x)
 // above take over only where the quantization shows:
 //   softplus, mish: x < -20, where 1 + exp(x) keeps fewer than 31 bits of exp(x)
 //                   (above it the quantization is < 5.4e-8 relative);
-//   gelu:           z < -10.5, where 1 + tanh(z) < 1.5e-9 is a small multiple of
-//                   2^-53 (above it the quantization is < 7.4e-8 relative);
+//   gelu:           z < -8, where 1 + tanh(z) < 2.3e-7 is a multiple of 2^-53
+//                   (quantization < 4.9e-10 relative) and the float head's
+//                   error would approach the bar;
 //   swish:          x < -80, where exp(-x) leaves float's range.
 // Inputs of magnitude below 2^-30 (where outputs can be denormal, so a second
 // rounding would show) take the double formula's linear term exactly.
@@ -214,11 +228,13 @@ struct GeluF32 {
         // z in float: x + 0.044715 x^3 adds terms of one sign (no
         // cancellation), so z is within ~3 ulp (3.6e-7 relative) of the
         // reference's double z; w = exp(-2|z|) = 2^a with a rounded to float:
-        // |a| <= 30.3 where the head is used, so w (and 1 + tanh z = 2w / (1 + w)
-        // for z < 0) is off by at most 2 |dz| + 9.5e-7 <= 8.5e-6 relative at
-        // the tail threshold, inside the 1e-5 f32 bar.
+        // |a| <= 23.1 where the head is used, so w (and 1 + tanh z = 2w / (1 + w)
+        // for z < 0) is off by at most 2 |dz| + 9.5e-7 <= 6.7e-6 relative at
+        // the tail threshold z = -8, a third inside the 1e-5 f32 bar.  Below
+        // it (1 + tanh z < 2.3e-7, where the bound would grow towards the bar)
+        // the double tail takes over.
         const float z = float(kGelu) * (xf + 0.044715f * xf * xf * xf);
-        need = z < -10.5f;  // 1 + tanh(z) < 1.5e-9: a small multiple of 2^-53 in the reference
+        need = z < -8.0f;
         const float w = __builtin_amdgcn_exp2f(-2.0f * 1.44269504f * __builtin_fabsf(z));
         const float r = rcp_f32(1.0f + w);
         const float onept = z >= 0.0f ? 2.0f * r : (w + w) * r;
@@ -228,8 +244,9 @@ struct GeluF32 {
     {
         const double x = double(xf);
         const double z = kGelu * (x + 0.044715 * x * x * x);
-        const double w = exp(z + z);               // < 7.6e-10
-        const double eps = (w + w) * (1.0 - w);   // 2w / (1 + w) to 6e-19 relative
+        // 1 + tanh z, a multiple of 2^-53 in the reference (tanh z in [-1, -0.5])
+        const double w = exp(z + z);               // < 1.2e-7 (z < -8 within float's error)
+        const double eps = (w + w) * (1.0 - w);   // 2w / (1 + w) to 2 w^3 < 3.4e-21 absolute
         return float(0.5 * x * (__builtin_rint(eps * 0x1p53) * 0x1p-53));
     }
 };

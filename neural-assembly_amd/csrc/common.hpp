@@ -138,6 +138,9 @@ struct Staged {
 int64_t      numel(const NeuralTensor *t);
 size_t       elem_size(int dtype);
 bool         is_contiguous(const NeuralTensor *t);
+// True when a and b may address the same bytes: one shared storage, or
+// element spans (through the strides) whose addresses intersect.
+bool         tensors_may_overlap(const NeuralTensor *a, const NeuralTensor *b);
 int          check_tensor(const NeuralTensor *t);   // null / dtype validation
 // Make the device copy current and return its element-0 address.
 int          dev_read(const NeuralTensor *t, const void **p);

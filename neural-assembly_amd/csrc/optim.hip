@@ -15,7 +15,9 @@
 // OPTS state blob (optimizers_c.c:84-100,391-562): 80-byte header, then
 // int64 sizes, then f64 velocities (SGD) or all m followed by all v.
 #include <cmath>
+#include <climits>
 #include <cstdlib>
+#include <new>
 #include <vector>
 
 #include "common.hpp"
@@ -285,7 +287,7 @@ void *opt_adamw_create(double lr, double beta1, double beta2, double epsilon, do
 }
 
 // opt_step (optimizers_c.c:353-368): NULL -> 1; n < 0 or n != first-call count -> 3.
-int opt_step(void *opt, void **params, void **grads, int64_t n)
+static int opt_step_impl(void *opt, void **params, void **grads, int64_t n)
 {
     if (!opt || !params || !grads) return set_error(NEURAL_ERR_NULL_POINTER);
     NH_TRY(ensure_init());
@@ -324,6 +326,20 @@ int opt_step(void *opt, void **params, void **grads, int64_t n)
         NH_TRY(step_param(o, size_t(i), static_cast<NeuralTensor *>(params[i]),
                           static_cast<const NeuralTensor *>(grads[i]), a));
     return set_error(NEURAL_OK);
+}
+
+// C++ exceptions (a failed vector growth) end as an error code at the C
+// boundary, never as an abort.
+int opt_step(void *opt, void **params, void **grads, int64_t n)
+{
+    try {
+        return opt_step_impl(opt, params, grads, n);
+    } catch (const std::bad_alloc &) {
+        free_moments(static_cast<OptHandle *>(opt));
+        return set_error(NEURAL_ERR_OUT_OF_MEMORY);
+    } catch (...) {
+        return set_error(NEURAL_ERR_INTERNAL);
+    }
 }
 
 void opt_free(void *opt)
@@ -424,7 +440,7 @@ int opt_state_export(void *opt, void *buffer, int64_t size)
     return set_error(NEURAL_OK);
 }
 
-int opt_state_import(void *opt, const void *buffer, int64_t size)
+static int opt_state_import_impl(void *opt, const void *buffer, int64_t size)
 {
     if (!opt || !buffer || size <= 0) return set_error(NEURAL_ERR_NULL_POINTER);
     NH_TRY(ensure_init());
@@ -447,22 +463,40 @@ int opt_state_import(void *opt, const void *buffer, int64_t size)
     o->wd = h.weight_decay;
     o->t = h.t;
     if (h.n_params == 0) return set_error(NEURAL_OK);
+    // Counts whose byte sizes overflow int64 end, in the reference, in a
+    // calloc that fails (NEURAL_ERR_OUT_OF_MEMORY); counts that fit but run
+    // past the blob are NEURAL_ERR_INVALID_ARGUMENT.  No product below can
+    // overflow.
+    constexpr int64_t kMaxCount = INT64_MAX / int64_t(sizeof(double));
+    const auto remaining = [&]() { return size - int64_t(p - base); };
+    if (h.n_params > kMaxCount) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
     const int64_t sizes_bytes = h.n_params * int64_t(sizeof(int64_t));
-    if ((p - base) + sizes_bytes > size) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
+    if (sizes_bytes > remaining()) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
+    try {
+        o->sizes.resize(size_t(h.n_params));
+    } catch (...) {
+        o->sizes.clear();
+        return set_error(NEURAL_ERR_OUT_OF_MEMORY);
+    }
     o->n_params = h.n_params;
-    o->sizes.resize(size_t(h.n_params));
     std::memcpy(o->sizes.data(), p, size_t(sizes_bytes));
     p += sizes_bytes;
     auto load = [&](std::vector<double *> &bufs) -> int {
         for (int64_t i = 0; i < o->n_params; i++) {
             const int64_t n = o->sizes[size_t(i)];
             if (n < 0) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
+            if (n > kMaxCount) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
+            const int64_t bytes = n * int64_t(sizeof(double));
+            if (bytes > remaining()) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
             double *d = static_cast<double *>(dev_alloc(size_t(n > 0 ? n : 1) * sizeof(double)));
             if (!d) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
-            bufs.push_back(d);
+            try {
+                bufs.push_back(d);
+            } catch (...) {
+                dev_free(d);
+                return set_error(NEURAL_ERR_OUT_OF_MEMORY);
+            }
             if (n == 0) continue;
-            const int64_t bytes = n * int64_t(sizeof(double));
-            if ((p - base) + bytes > size) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
             NH_HIP(hipMemcpyAsync(d, p, size_t(bytes), hipMemcpyHostToDevice, stream()));
             p += bytes;
         }
@@ -481,6 +515,21 @@ int opt_state_import(void *opt, const void *buffer, int64_t size)
     }
     NH_TRY(sync());
     return set_error(NEURAL_OK);
+}
+
+int opt_state_import(void *opt, const void *buffer, int64_t size)
+{
+    try {
+        return opt_state_import_impl(opt, buffer, size);
+    } catch (const std::bad_alloc &) {
+        (void)sync();
+        free_moments(static_cast<OptHandle *>(opt));
+        return set_error(NEURAL_ERR_OUT_OF_MEMORY);
+    } catch (...) {
+        (void)sync();
+        free_moments(static_cast<OptHandle *>(opt));
+        return set_error(NEURAL_ERR_INTERNAL);
+    }
 }
 
 }  // extern "C"

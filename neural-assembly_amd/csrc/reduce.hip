@@ -65,7 +65,7 @@ struct RedMaxChain {
             int64_t lz = -1;
             for (int64_t j = from + G::lane(); j < hi; j += TPR) lz = (row[j] == T(0)) ? j : lz;
             lz = G::max_i64(lz);
-            b.v = row[lz];
+            if (lz >= 0) b.v = row[lz];
         }
         return b;
     }
@@ -624,7 +624,10 @@ int neural_bias_add_row_stats(NeuralTensor *out, const NeuralTensor *in, const N
     StatsOut so;
     NH_TRY(so.open(in, rows, sum, mean, max, argmax));
     if (rows == 0) return set_error(NEURAL_OK);
+    // In place (out sharing bytes with in or bias) the one-pass kernel would
+    // overwrite values its rare-case rescans read again: two calls instead.
     const bool fused = is_contiguous(in) && is_contiguous(out) && is_contiguous(bias) &&
+                       !tensors_may_overlap(out, in) && !tensors_may_overlap(out, bias) &&
                        ((in->dtype == NEURAL_DTYPE_FLOAT32 ? reduce_plan<float>(rows, cols)
                                                            : reduce_plan<double>(rows, cols)).gx == 1);
     if (!fused) {

@@ -576,6 +576,21 @@ NeuralTensor *create_owned(const uint64_t *shape, uint64_t ndim, int dtype, bool
 
 }  // namespace
 
+bool nh::tensors_may_overlap(const NeuralTensor *a, const NeuralTensor *b)
+{
+    if (!a || !b) return false;
+    if (a->st == b->st) return true;
+    int64_t alo, ahi, blo, bhi;
+    span_of(a, &alo, &ahi);
+    span_of(b, &blo, &bhi);
+    if (ahi <= alo || bhi <= blo) return false;
+    const uintptr_t a0 = reinterpret_cast<uintptr_t>(a->data) + uintptr_t(alo);
+    const uintptr_t a1 = reinterpret_cast<uintptr_t>(a->data) + uintptr_t(ahi);
+    const uintptr_t b0 = reinterpret_cast<uintptr_t>(b->data) + uintptr_t(blo);
+    const uintptr_t b1 = reinterpret_cast<uintptr_t>(b->data) + uintptr_t(bhi);
+    return a0 < b1 && b0 < a1;
+}
+
 extern "C" {
 
 int neural_init(void) { return ensure_init(); }

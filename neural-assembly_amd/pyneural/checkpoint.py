@@ -140,14 +140,26 @@ def _restore_tensor(src: _Source, index: int, tensor, staging: _Staging) -> None
         raise IOError(f"host-to-device copy of parameter {index} failed (error {rc})")
 
 
+def _optimizer_blob(optimizer) -> bytes:
+    """The optimizer's OPTS state blob, or b"" when it has none or its export
+    fails: the checkpoint is then written without moments, as the reference
+    does (checkpoint.py:99-114)."""
+    export = getattr(optimizer, "state_bytes", None)
+    if export is None or not getattr(optimizer, "_ptr", None):
+        return b""
+    try:
+        return export()
+    except NeuralException:
+        return b""
+
+
 def save_checkpoint(filepath, model, optimizer=None, epoch: int = 0, best_loss: float = float("inf"),
                     lr: float = 0.0) -> None:
     """Write the parameters, the training position and the optimizer state
     (the interface of the reference's checkpoint.py:196-240)."""
     params = _parameter_list(model)
     kind, payload = _describe_optimizer(optimizer)
-    export = getattr(optimizer, "state_bytes", None)
-    blob = export() if (export is not None and getattr(optimizer, "_ptr", None)) else b""
+    blob = _optimizer_blob(optimizer)
     staging = _Staging()
     with open(filepath, "wb") as f:
         f.write(_PREFIX.pack(MAGIC, VERSION, len(params), epoch, best_loss, lr))

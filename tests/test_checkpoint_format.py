@@ -97,3 +97,26 @@ def test_errors(tmp_path):
     p.write_bytes(full[:-1])
     with pytest.raises(IOError, match="state blob"):
         ck.load_checkpoint(p, [])
+
+
+class Adam:
+    """An optimizer whose state export fails (a handle the library refuses)."""
+
+    def __init__(self):
+        self.beta1, self.beta2, self.epsilon, self.weight_decay, self.lr = 0.9, 0.999, 1e-8, 0.0, 1e-3
+        self._ptr = 1
+
+    def state_bytes(self):
+        from pyneural.core import NeuralException
+        raise NeuralException(3, "opt_state_export failed")
+
+
+def test_save_when_state_export_fails(tmp_path):
+    """A failing export writes the checkpoint with an empty state blob, as the
+    reference's _export_optimizer_state_blob does (checkpoint.py:99-114),
+    instead of raising out of save_checkpoint."""
+    p = tmp_path / "e.ckpt"
+    ck.save_checkpoint(p, [], Adam(), epoch=2, best_loss=1.5, lr=1e-3)
+    assert p.read_bytes() == _v3_bytes(2, 1.5, 1e-3, 1, 2, (0.0, 0.9, 0.999, 1e-8, 0.0))
+    info = ck.load_checkpoint(p, [], Adam())
+    assert info == {"epoch": 2, "best_loss": 1.5, "lr": 1e-3, "optimizer_type": 2}

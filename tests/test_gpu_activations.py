@@ -141,6 +141,21 @@ CFG3_SHAPE = (64, 64, 128, 128)
 WIN = 1 << 19
 
 
+def test_gelu_f32_every_float_around_tail_threshold(pn, ora):
+    """Every float x whose GELU argument z = sqrt(2/pi)(x + 0.044715 x^3) lies
+    in [-11, -7] (x in [-5.75, -4.55], about 2.5 M values): the float head
+    above z = -8 and the double tail below it both within REL32 of the
+    reference formula (activations_c.c:124-131) evaluated by the oracle."""
+    lo = np.float32(4.55).view(np.uint32)
+    hi = np.float32(5.75).view(np.uint32)
+    x = (np.arange(lo, hi + 1, dtype=np.uint32) | np.uint32(0x80000000)).view(np.float32)
+    got = _run(pn, "gelu", x)
+    want = ora.act("gelu", x, 0.0)
+    rel_close(got, want, 1e-5, 0.0, "gelu f32 around z = -8")
+    z = np.sqrt(2.0 / np.pi) * (x.astype(np.float64) + 0.044715 * x.astype(np.float64) ** 3)
+    assert z.min() < -11.0 and z.max() > -7.0
+
+
 def _torch_formula(torch, name, x):
     """The reference's double formula (activations_c.c:124-158) in torch
     float64, the operation order kept; used as the full-tensor check of the

@@ -147,3 +147,41 @@ def test_step_errors(pn):
     sgd = pn.SGD()
     with pytest.raises(pn.NeuralException):
         sgd.load_state_bytes(opt.state_bytes())  # type mismatch -> INVALID_ARGUMENT
+
+
+def test_state_import_overflowing_counts(pn):
+    """Blobs whose counts overflow int64 byte sizes (n_params = 2^61, a
+    parameter of 2^61 + 1 values) or run past the blob end come back as error
+    codes, as the reference's calloc failure does (optimizers_c.c:480-562),
+    never as an abort; the optimizer stays usable afterwards."""
+    import struct
+
+    lib = pn.core._lib
+    E = pn.NeuralError
+    opt = pn.AdamW()
+    a, g = pn.Tensor.create([6]), pn.Tensor.create([6])
+    opt.step([a], [g])
+    good = opt.state_bytes()
+    hdr = bytearray(good[:80])
+
+    def blob(n_params, sizes, tail=b""):
+        h = bytearray(hdr)
+        struct.pack_into("<q", h, 16, n_params)
+        return bytes(h) + b"".join(struct.pack("<q", s) for s in sizes) + tail
+
+    def imp(b):
+        buf = ctypes.create_string_buffer(b, len(b))
+        return lib.opt_state_import(opt._ptr, buf, len(b))
+
+    assert imp(blob(1 << 61, [])) == E.OUT_OF_MEMORY
+    assert imp(blob((1 << 60) + 1, [])) == E.OUT_OF_MEMORY
+    assert imp(blob((1 << 63) - 1, [])) == E.OUT_OF_MEMORY
+    assert imp(blob(1 << 40, [])) == E.INVALID_ARGUMENT       # fits int64, runs past the blob
+    assert imp(blob(1, [(1 << 61) + 1], b"\0" * 8)) == E.OUT_OF_MEMORY
+    assert imp(blob(2, [6, (1 << 62) + 3], b"\0" * 64)) == E.OUT_OF_MEMORY
+    assert imp(blob(1, [1 << 40], b"\0" * 8)) == E.INVALID_ARGUMENT
+    assert imp(blob(1, [-1], b"")) == E.INVALID_ARGUMENT
+    # a good blob still loads and the optimizer still steps
+    assert imp(good) == 0
+    assert opt.state_bytes() == good
+    opt.step([a], [g])

@@ -98,6 +98,42 @@ def test_bias_add_row_stats_equal_separate_calls(pn, ora, rows, cols, dt):
     same_bits(idx, ora.rowargmax(yv))
 
 
+@pytest.mark.parametrize("cols", [300, 4096])
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_bias_add_row_stats_in_place(pn, ora, cols, dt):
+    """out == in (the in-place bias add of a linear layer): rows whose maximum
+    after the add is a zero (signed zeros mixed), rows with NaN before and
+    after the zeros, and rows with +-Inf give the two separate calls' bits."""
+    rows = 64
+    rng = np.random.default_rng(cols + 3)
+    b = rng.normal(0, 3, cols).astype(dt)
+    b[7] = -0.0
+    x = (-np.abs(rng.normal(0, 3, (rows, cols))) - b).astype(dt)  # x + b <= 0 (rounded)
+    for r in range(0, rows, 4):
+        z = rng.choice(np.arange(8, cols), size=5, replace=False)
+        x[r, z] = -b[z]                                # +0 after the add: the row's maximum is 0
+        x[r, 7] = -0.0                                 # -0 + -0 = -0: zeros of both signs tie
+        if r % 8 == 0:
+            x[r, z[2]] = np.nan                        # NaN: the chain restarts after it
+        x[r + 1, rng.integers(0, cols)] = np.inf
+        x[r + 2, rng.integers(0, cols)] = -np.inf
+        x[r + 3, cols - 1] = np.nan                    # NaN last: row max NaN
+    y_ref = x + b
+    lib = pn.core._lib
+    want = _separate(pn, pn.Tensor.from_numpy(y_ref), rows)
+    t = pn.Tensor.from_numpy(x)
+    tb = pn.Tensor.from_numpy(b)
+    outs, idx = _fused_outputs(pn, rows, t.dtype)
+    rc = lib.neural_bias_add_row_stats(t._ptr, t._ptr, tb._ptr, outs[0]._ptr, outs[1]._ptr, outs[2]._ptr,
+                                       idx.ctypes.data)
+    pn.core._check_error(rc, "neural_bias_add_row_stats in place")
+    same_bits(t.numpy(), y_ref)
+    for got, w in zip([o.numpy() for o in outs] + [idx], want):
+        same_bits(got, w)
+    same_bits(outs[2].numpy(), ora.rowmax_chain(y_ref))
+    same_bits(idx, ora.rowargmax(y_ref))
+
+
 def test_row_stats_subsets_and_device_indices(pn, ora):
     """Any subset of the outputs; argmax into device memory; repeated calls
     give the same bits."""
