@@ -16,12 +16,15 @@ its own 1M size, cfg3 in f32 and f64, cfg4, cfg5): per op the kernel time and
 its % of 8 TB/s, per config the aggregate GB/s, a roofline object for its
 dominant kernel and a CPU baseline timed on this host in this run.
 
-Kernel times come from HIP event pairs that the library attaches to one
-launch (neural_hip_time_next_launch -> hipExtLaunchKernelGGL), so each pair
-brackets that kernel's own execution on its stream; the events are created
-with hipEventDisableSystemFence.  Call times (all kernels of a call plus the
-gaps, the host wait where a result returns to the host) are HIP events around
-back-to-back calls and go to the --detail file.
+Kernel times come from HIP event pairs that the library attaches to launches
+(neural_hip_time_launches -> hipExtLaunchKernelGGL): a pair on one launch
+brackets that kernel's own execution on its stream; a pair spanning every
+launch of a multi-launch call (the library's launch counter gives how many)
+brackets the whole op, gaps included.  Each figure is the median of 20 such
+pairs.  Ops whose result returns to the host (neural_sum, neural_argmax, the
+NaN/Inf/L2 scan) are also timed per call on the host clock (launch, kernels,
+host wait, return).  A float4 streaming copy measured in the same run gives
+the achievable 1:1 stream rate; every op also carries its % of it.
 
 CPU baselines, one thread (the reference never dispatches to its thread pool):
   cfg2  the oracle's C restatement of the whole step (port);
@@ -34,7 +37,8 @@ CPU baselines, one thread (the reference never dispatches to its thread pool):
   cfg5  the reference's optimizers_c.c AdamW (oracle/_ref) and the
         training_ops.asm scans (has_nan, has_inf: scalar; L2: SSE 4-lane) on a
         sample.
-CPU GB/s use the same algorithmic bytes per element as the GPU op.
+CPU GB/s use the same algorithmic bytes per element as the GPU op; each CPU
+figure is the median of 5 runs after one warm-up run.
 
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--detail FILE] [--suite]
 """
@@ -64,7 +68,11 @@ ACTS = ["tanh", "gelu", "leaky_relu", "elu", "selu", "swish", "mish", "hardswish
 ACT_ALPHA = {"leaky_relu": 0.01, "elu": 1.0}
 NQ = 268_435_456               # cfg4
 NA = 100_000_000               # cfg5
-REPS = 10                      # timed launches per op outside the step
+REPS = 20                      # event-paired launches per op (median reported)
+CPU_REPS = 5                   # timed CPU runs per leg after one warm-up (median reported)
+VALU_CYCLES = 4                # cycles a wave64 VALU instruction occupies a 16-lane SIMD
+CLOCK_GHZ = 2.4                # MI355X peak engine clock
+N_SIMD = 256 * 4
 # Untimed back-to-back calls of each op before its timed launches.  When the
 # load switches (light f32 streams to FP64-heavy activations, say) the GPU's
 # clocks take some milliseconds to settle: on one box f64 tanh ran 193-216 us
@@ -101,6 +109,22 @@ def traffic_from_profile():
 
 
 TRAFFIC = traffic_from_profile()
+
+
+def valu_from_profile():
+    """Per-launch VALU instruction counts of the cfg3 f64 activations
+    ("<op>" -> {"valu": wave instructions, "fp64_flops": FLOPs}) from the
+    committed rocprofv3 --pmc summary profiles/cfg3_f64_valu_pmc.json."""
+    p = ROOT / "profiles" / "cfg3_f64_valu_pmc.json"
+    if not p.exists():
+        return {}
+    try:
+        return json.loads(p.read_text())["per_launch"]
+    except Exception:
+        return {}
+
+
+VALU = valu_from_profile()
 
 
 class TimingEvent:
@@ -147,21 +171,19 @@ class TimingEvent:
 
 
 class Clock:
-    """Kernel and call timing on the library's launch stream."""
+    """Kernel, op and call timing on the library's launch stream."""
 
     def __init__(self, torch, lib, stream):
         self.torch, self.lib, self.stream = torch, lib, stream
-        self.pairs = [(TimingEvent(), TimingEvent()) for _ in range(64)]
+        self.pairs = [(TimingEvent(), TimingEvent()) for _ in range(REPS)]
 
-    def arm(self, pair, skip=0):
-        rc = self.lib.neural_hip_time_next_launch(pair[0].ev, pair[1].ev, skip)
+    def arm(self, pair, skip=0, count=1):
+        rc = self.lib.neural_hip_time_launches(pair[0].ev, pair[1].ev, skip, count)
         if rc != 0:
-            raise RuntimeError(f"neural_hip_time_next_launch failed: {rc}")
+            raise RuntimeError(f"neural_hip_time_launches failed: {rc}")
 
-    def kernel_us(self, fn, reps=REPS, skip=0, warm=3):
-        """Average duration (us) of one launch of `fn` (the launch after `skip`
-        others), each of `reps` calls timed by its own event pair, after at
-        least `warm` calls and WARM_MS of back-to-back calls."""
+    def warm(self, fn, warm=3):
+        """At least `warm` calls and WARM_MS of back-to-back calls."""
         t0, k = time.perf_counter(), 0
         while k < warm or (time.perf_counter() - t0) * 1e3 < WARM_MS:
             fn()
@@ -169,28 +191,44 @@ class Clock:
             if k % 8 == 0:
                 self.torch.cuda.synchronize()
         self.torch.cuda.synchronize()
-        used = []
-        for r in range(reps):
-            p = self.pairs[r % len(self.pairs)]
-            self.arm(p, skip)
-            fn()
-            used.append(p)
-            if len(used) == len(self.pairs):
-                break
-        self.torch.cuda.synchronize()
-        return 1e3 * statistics.mean(a.elapsed_time(b) for a, b in used)
 
-    def call_us(self, fn, reps=REPS):
-        """Average time (us) of `reps` back-to-back calls."""
+    def launches(self, fn):
+        """Kernel launches one call of fn makes (after a first call, which
+        may allocate and clear state)."""
         fn()
+        c0 = self.lib.neural_hip_launch_count()
+        fn()
+        n = self.lib.neural_hip_launch_count() - c0
         self.torch.cuda.synchronize()
-        e0, e1 = TimingEvent(), TimingEvent()
-        e0.record(self.stream)
-        for _ in range(reps):
+        return int(n)
+
+    def kernel_us(self, fn, reps=REPS, skip=0, count=1, warm=3):
+        """Median duration (us) over `reps` calls of fn, each with its own
+        event pair on the launches skip .. skip + count - 1 of the call."""
+        self.warm(fn, warm)
+        for r in range(reps):
+            self.arm(self.pairs[r], skip, count)
             fn()
-        e1.record(self.stream)
         self.torch.cuda.synchronize()
-        return 1e3 * e0.elapsed_time(e1) / reps
+        return 1e3 * statistics.median(a.elapsed_time(b) for a, b in self.pairs[:reps])
+
+    def op(self, fn, reps=REPS):
+        """(main kernel us, whole-op us, launches per call): the first launch,
+        and the span over every launch of the call."""
+        n = self.launches(fn)
+        k = self.kernel_us(fn, reps)
+        return k, (self.kernel_us(fn, reps, 0, n, warm=0) if n > 1 else k), n
+
+    def host_call_us(self, fn, reps=REPS):
+        """Median host-clock time (us) of one call of fn that returns its
+        result to the host (the call waits for it)."""
+        self.warm(fn)
+        ts = []
+        for _ in range(reps):
+            t = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t)
+        return 1e6 * statistics.median(ts)
 
 
 def gbs(nbytes, us):
@@ -201,35 +239,60 @@ def pct(nbytes, us):
     return round(100.0 * gbs(nbytes, us) / HBM_PEAK_GBS, 1)
 
 
+COPY = {}  # the same-run float4 copy: {"GBps": ..} (filled by measure_copy_peak)
+
+
+def pct_copy(gbps):
+    return round(100.0 * gbps / COPY["GBps"], 1) if COPY.get("GBps") else None
+
+
 class Config:
     """Per-op GPU figures of one BASELINE config and its compact summary."""
 
     def __init__(self, name, workload):
         self.name, self.workload = name, workload
-        self.ops = {}          # op -> dict(kernel_us, call_us, bytes, elems, kernel)
+        self.ops = {}          # op -> dict(kernel, bytes, elems, kernel_us, op_us, launches, host_call_us, ...)
 
-    def add(self, op, kernel, nbytes, elems, kernel_us, call_us=None):
-        self.ops[op] = {"kernel": kernel, "bytes": nbytes, "elems": elems, "kernel_us": round(kernel_us, 2),
-                        "call_us": round(call_us, 2) if call_us is not None else None,
-                        "GB/s": round(gbs(nbytes, kernel_us), 1), "pct_hbm": pct(nbytes, kernel_us),
-                        "Gelem/s": round(elems / kernel_us / 1e3, 2)}
+    def add(self, op, kernel, nbytes, elems, kernel_us, op_us=None, launches=1, host_call_us=None):
+        """kernel_us: the op's main (first) launch; op_us: every launch of the
+        call (default: kernel_us); host_call_us: the whole call on the host
+        clock, for ops that return a result to the host."""
+        op_us = kernel_us if op_us is None else op_us
+        e = {"kernel": kernel, "bytes": nbytes, "elems": elems, "launches": launches,
+             "kernel_us": round(kernel_us, 2), "op_us": round(op_us, 2),
+             "GB/s": round(gbs(nbytes, op_us), 1), "pct_hbm": pct(nbytes, op_us),
+             "pct_copy": pct_copy(gbs(nbytes, op_us)), "Gelem/s": round(elems / op_us / 1e3, 2)}
+        if host_call_us is not None:
+            e["host_call_us"] = round(host_call_us, 2)
+            e["host_call_pct_hbm"] = pct(nbytes, host_call_us)
+        self.ops[op] = e
 
     def aggregate_gbs(self):
-        return sum(o["bytes"] for o in self.ops.values()) / sum(o["kernel_us"] for o in self.ops.values()) / 1e3
+        return sum(o["bytes"] for o in self.ops.values()) / sum(o["op_us"] for o in self.ops.values()) / 1e3
 
     def summary(self, cpu=None):
-        """Compact form for the JSON line: ops as [kernel us, % of 8 TB/s];
-        the roofline of the dominant (longest) kernel, HBM-bound against
-        8 TB/s: achieved = algorithmic bytes / avg launch us."""
-        dom = max(self.ops, key=lambda k: self.ops[k]["kernel_us"])
+        """Compact form for the JSON line: ops as [op us, % of 8 TB/s] (op =
+        every launch of the call); the main kernel alone where an op makes
+        several launches; host-clock call times where a result returns to the
+        host; the roofline of the dominant (longest) op, HBM-bound against
+        8 TB/s: achieved = algorithmic bytes / median op us."""
+        dom = max(self.ops, key=lambda k: self.ops[k]["op_us"])
         d = self.ops[dom]
         s = {
             "w": self.workload,
-            "ops": {k: [o["kernel_us"], o["pct_hbm"]] for k, o in self.ops.items()},
+            "ops": {k: [o["op_us"], o["pct_hbm"]] for k, o in self.ops.items()},
             "GBps": round(self.aggregate_gbs(), 1),
-            "roofline": {"kernel": dom, "us": d["kernel_us"], "bytes": d["bytes"], "achieved": d["GB/s"],
+            "pct_of_copy": round(100.0 * self.aggregate_gbs() / COPY["GBps"], 1) if COPY.get("GBps") else None,
+            "roofline": {"kernel": dom, "us": d["op_us"], "bytes": d["bytes"], "achieved": d["GB/s"],
                          "frac": round(d["GB/s"] / HBM_PEAK_GBS, 4), "traffic": TRAFFIC.get(f"{self.name}.{dom}")},
         }
+        multi = {k: {"launches": o["launches"], "first_kernel_us": o["kernel_us"]}
+                 for k, o in self.ops.items() if o["launches"] > 1}
+        if multi:
+            s["multi_launch"] = multi
+        host = {k: [o["host_call_us"], o["host_call_pct_hbm"]] for k, o in self.ops.items() if "host_call_us" in o}
+        if host:
+            s["host_call"] = host
         if cpu:
             c = {"GBps": cpu["value"], "kind": cpu["kind"], "cores": cpu["cores"]}
             if "avx512" in cpu:
@@ -252,7 +315,10 @@ def _cpu_model() -> str:
     return "unknown CPU"
 
 
-def _median_time(fn, reps=3):
+def _median_time(fn, reps=CPU_REPS, warm=1):
+    """Median wall time (s) of `reps` runs of fn after `warm` untimed runs."""
+    for _ in range(warm):
+        fn()
     ts = []
     for _ in range(reps):
         t = time.perf_counter()
@@ -284,6 +350,7 @@ def main():
     dev = torch.device("cuda:0")
     clock = Clock(torch, _lib, stream)
     detail = {}
+    measure_copy_peak(torch, _lib, clock, dev)
 
     # ---------------------------------------------------------------- cfg2 step
     g = torch.Generator(device=dev)
@@ -341,21 +408,27 @@ def main():
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
     # The same steps again with an event pair on every kernel: each kernel's
-    # own duration inside the step sequence (cache state as in the step).
+    # own duration inside the step sequence (cache state as in the step);
+    # the mean over the steps (the roofline's average launch) and the median.
     inst = [[(TimingEvent(), TimingEvent()) for _ in step_ops] for _ in range(args.steps)]
     for s in range(args.steps):
         step(inst[s])
     torch.cuda.synchronize()
     cfg2 = Config("cfg2", "cfg2 step kernels, each timed inside the step sequence")
+    mean_us = {}
     for k, (name, kern, nbytes, elems, _) in enumerate(step_ops):
-        us = 1e3 * statistics.mean(inst[s][k][0].elapsed_time(inst[s][k][1]) for s in range(args.steps))
-        cfg2.add(name, kern, nbytes, elems, us)
-    kernel_sum_us = sum(o["kernel_us"] for o in cfg2.ops.values())
+        ts = [1e3 * inst[s][k][0].elapsed_time(inst[s][k][1]) for s in range(args.steps)]
+        mean_us[name] = statistics.mean(ts)
+        cfg2.add(name, kern, nbytes, elems, statistics.median(ts))
+    kernel_sum_us = sum(mean_us.values())
     detail["cfg2_step"] = cfg2.detail()
-    dom = max(cfg2.ops, key=lambda k: cfg2.ops[k]["kernel_us"])
+    detail["cfg2_step"]["mean_us"] = {k: round(v, 2) for k, v in mean_us.items()}
+    dom = max(mean_us, key=lambda k: mean_us[k])
     d = cfg2.ops[dom]
+    frac_by_kernel = {k: round(cfg2.ops[k]["bytes"] / (v * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) for k, v in mean_us.items()}
 
     fused = fused_step(torch, _lib, clock, stream, T, ridx, step_ops, args, ms_per_step, n1)
+    yres = y_residency(torch, pn, _lib, clock, Y, step_ops)
 
     cpu2 = None
     if not args.no_cpu:
@@ -379,21 +452,27 @@ def main():
             "step_bytes": step_bytes,
             "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 1),
             "elements_per_s": round((5 * n1 + 2 * n2) / (ms_per_step * 1e-3), 0),
-            "kernel_us_in_step": {k: o["kernel_us"] for k, o in cfg2.ops.items()},
+            "kernel_us_in_step": {k: round(v, 2) for k, v in mean_us.items()},
+            "kernel_median_us_in_step": {k: o["kernel_us"] for k, o in cfg2.ops.items()},
             "kernel_sum_us": round(kernel_sum_us, 1),
             "fused_step": fused,
+            "y_residency": yres,
+            "copy_peak": COPY,
         },
         "roofline": {
             "kernel": f"{dom}: {d['kernel']} [65536,1024] f32" if "softmax" in dom else f"{dom}: {d['kernel']}",
             "bound": "hbm",
-            "achieved": d["GB/s"],
+            "achieved": round(gbs(d["bytes"], mean_us[dom]), 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(d["GB/s"] / HBM_PEAK_GBS, 4),
+            "frac": frac_by_kernel[dom],
             "traffic": TRAFFIC.get(f"cfg2.{dom}"),
-            "avg_launch_us": d["kernel_us"],
+            "avg_launch_us": round(mean_us[dom], 2),
+            "median_launch_us": d["kernel_us"],
             "algorithmic_bytes": d["bytes"],
-            "min_frac_in_step": round(min(o["GB/s"] for o in cfg2.ops.values()) / HBM_PEAK_GBS, 4),
+            "frac_by_kernel": frac_by_kernel,
+            "min_frac_in_step": min(frac_by_kernel.values()),
+            "pct_of_copy": pct_copy(gbs(d["bytes"], mean_us[dom])),
         },
         "cpu_baseline": cpu2,
     }
@@ -424,6 +503,80 @@ def main():
         Path(args.detail).parent.mkdir(parents=True, exist_ok=True)
         Path(args.detail).write_text(json.dumps(detail, indent=1))
     print(json.dumps(line, separators=(",", ":")), flush=True)
+
+
+def measure_copy_peak(torch, lib, clock, dev):
+    """The library's float4 streaming copy (neural_hip_stream_copy: the flat
+    kernels' tiling, 16-byte non-temporal loads and stores) of 256 MiB (cfg1's
+    64M f32, cfg2's softmax input) and of 1 GiB into a second buffer: the
+    achievable rate of a 1:1 read/write stream in this run.  The faster of the
+    two is the reference every op's pct_of_copy refers to."""
+    res = {}
+    for n in (1 << 26, 1 << 28):
+        src = torch.empty(n, device=dev).uniform_()
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        f = lambda: lib.neural_hip_stream_copy(ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(src.data_ptr()),
+                                               4 * n)  # noqa: E731
+        if f() != 0:
+            raise RuntimeError("neural_hip_stream_copy failed")
+        us = clock.kernel_us(f)
+        torch.cuda.synchronize()
+        if not torch.equal(src, dst):
+            raise RuntimeError("stream copy: destination differs from source")
+        res[f"{4 * n >> 20}MiB"] = {"us": round(us, 2), "GBps": round(gbs(8 * n, us), 1), "pct_hbm": pct(8 * n, us)}
+        del src, dst
+        torch.cuda.empty_cache()
+    best = max(res.values(), key=lambda r: r["GBps"])
+    COPY.update({"kernel": "k_map1_flat<float, FnCopy>, median of %d launches" % REPS, "sizes": res,
+                 "GBps": best["GBps"], "pct_hbm": best["pct_hbm"]})
+
+
+def y_residency(torch, pn, lib, clock, Y, step_ops, reps=REPS):
+    """Where the step's row reductions read Y from.  A row sum of Y [8192,4096]
+    timed: right after the bias add that wrote it (as in the step); after the
+    bias add and then a 1 GiB read of another buffer (four times the 256 MB
+    memory-side cache: Y cannot stay resident, and the read leaves no dirty
+    lines behind); after the bias add and 1 GiB of writes (the timed read
+    then also competes with their write-back); right after another row sum of
+    Y.  Control: a row sum of a 64 MiB slice of Y right after a row sum of the
+    same slice (the slice fits the cache), whose rate shows what a
+    cache-served read looks like."""
+    dev = torch.device("cuda:0")
+    W = pn.Tensor.from_torch
+    scrub = torch.empty(1 << 16, 1 << 12, device=dev)
+    scrub_out = torch.empty(1 << 16, device=dev)
+    ys, ys_out = Y[:4096], torch.empty(4096, device=dev)
+    ts, tso, tys, tyso = W(scrub), W(scrub_out), W(ys), W(ys_out)
+    bias = step_ops[0][4]
+    rsum = step_ops[1][4]
+    res = {}
+
+    def read_scrub():
+        lib.neural_reduce_sum(ts._ptr, 1, tso._ptr)
+
+    def slice_sum():
+        lib.neural_reduce_sum(tys._ptr, 1, tyso._ptr)
+
+    phases = (("after_bias_add", lambda r: bias(), rsum),
+              ("after_bias_add_then_1GiB_read", lambda r: (bias(), read_scrub()), rsum),
+              ("after_bias_add_then_1GiB_write", lambda r: (bias(), scrub.fill_(float(r))), rsum),
+              ("after_row_sum", lambda r: (bias(), rsum()), rsum),
+              ("control_64MiB_slice_after_its_row_sum", lambda r: slice_sum(), slice_sum))
+    for name, pre, timed in phases:
+        for r in range(reps):
+            pre(r)
+            clock.arm(clock.pairs[r])
+            timed()
+        torch.cuda.synchronize()
+        res[name] = round(1e3 * statistics.median(a.elapsed_time(b) for a, b in clock.pairs[:reps]), 2)
+    ybytes = ROWS * COLS * 4
+    res["GBps"] = {k: round(gbs(ybytes if not k.startswith("control") else ybytes // 2, v), 1)
+                   for k, v in res.items()}
+    res["kernel"] = "k_reduce_rows (row sum of Y [8192,4096] f32, %d MB), median of %d" % (ybytes // 10 ** 6, reps)
+    del ts, tso, tys, tyso, scrub, scrub_out, ys_out
+    torch.cuda.empty_cache()
+    return res
 
 
 def fused_step(torch, lib, clock, stream, T, ridx, step_ops, args, ms_per_step, n1):
@@ -518,32 +671,41 @@ def _cfg1(torch, pn, lib, clock, dev, g, cpu_on, out, detail):
     for n, key in ((N1, "cfg1"), (N1_SMALL, "cfg1_1M")):
         ta, tb, tc = W(a[:n]), W(bb[:n]), W(c[:n])
         to = W(one)
+        t1 = W(a[:1])
         cf = Config(key, f"cfg1: f32 add, mul, ReLU, full sum, max over {n:,} elements U[-1,1]"
                     + (" (256 MiB MALL holds it: cache-resident, reported not judged)" if n < N1 else ""))
-        ops = [("add", "k_map2_flat", 12 * n, lambda: lib.neural_add(tc._ptr, ta._ptr, tb._ptr), 0),
-               ("mul", "k_map2_flat", 12 * n, lambda: lib.neural_mul(tc._ptr, ta._ptr, tb._ptr), 0),
-               ("relu", "k_map1_flat", 8 * n, lambda: lib.neural_relu(tc._ptr, ta._ptr), 0),
-               ("sum", "k_reduce_seg (+combine)", 4 * n, lambda: lib.neural_reduce_sum(ta._ptr, -1, to._ptr), 0),
-               ("max", "k_reduce_seg (+combine)", 4 * n, lambda: lib.neural_reduce_max(ta._ptr, -1, to._ptr), 0)]
-        for name, kern, nbytes, fn, skip in ops:
-            cf.add(name, kern, nbytes, n, clock.kernel_us(fn, skip=skip), clock.call_us(fn))
+        ops = [("add", "k_map2_flat", 12 * n, lambda: lib.neural_add(tc._ptr, ta._ptr, tb._ptr)),
+               ("mul", "k_map2_flat", 12 * n, lambda: lib.neural_mul(tc._ptr, ta._ptr, tb._ptr)),
+               ("relu", "k_map1_flat", 8 * n, lambda: lib.neural_relu(tc._ptr, ta._ptr)),
+               ("sum", "k_reduce_seg + k_reduce_combine", 4 * n, lambda: lib.neural_reduce_sum(ta._ptr, -1, to._ptr)),
+               ("max", "k_reduce_seg + k_reduce_combine", 4 * n, lambda: lib.neural_reduce_max(ta._ptr, -1, to._ptr))]
+        for name, kern, nbytes, fn in ops:
+            k, o, nl = clock.op(fn)
+            cf.add(name, kern, nbytes, n, k, o, nl)
         if n == N1:
+            # the reference's host-returning forms (neural_api.h:359,367): the
+            # whole call on the host clock, result in host memory
             r = ctypes.c_double()
             idx = ctypes.c_int64()
-            extra = {"sum_host_api_call_us": clock.call_us(lambda: lib.neural_sum(ta._ptr, ctypes.byref(r))),
-                     "argmax_host_api_call_us": clock.call_us(lambda: lib.neural_argmax(ta._ptr, ctypes.byref(idx))),
-                     "argmax_kernel_us": clock.kernel_us(
-                         lambda: lib.neural_reduce_argmax(ta._ptr, -1, ctypes.c_void_p(one_i.data_ptr())))}
+            s_fn = lambda: lib.neural_sum(ta._ptr, ctypes.byref(r))  # noqa: E731
+            a_fn = lambda: lib.neural_argmax(ta._ptr, ctypes.byref(idx))  # noqa: E731
+            for name, fn in (("neural_sum", s_fn), ("neural_argmax", a_fn)):
+                k, o, nl = clock.op(fn)
+                cf.add(name, "k_reduce_seg + k_reduce_combine (result to the host)", 4 * n, n, k, o, nl,
+                       host_call_us=clock.host_call_us(fn))
+            # the floor of any host-returning call: one empty-work launch and
+            # the host wait for its result (a 1-element sum)
+            floor = clock.host_call_us(lambda: lib.neural_sum(t1._ptr, ctypes.byref(r)))
         cpu = cpu_cfg1(a[:n], bb[:n], n) if (cpu_on and n == N1) else None
         out[key] = cf.summary(cpu)
         if n < N1:
-            out[key] = {"w": out[key]["w"], "ops_us": {k: o["kernel_us"] for k, o in cf.ops.items()}}
+            out[key] = {"w": out[key]["w"], "ops_us": {k: o["op_us"] for k, o in cf.ops.items()}}
         detail[key] = cf.detail()
         if n == N1:
-            detail[key]["extra"] = {k: round(v, 2) for k, v in extra.items()}
+            out[key]["host_return_floor_us"] = round(floor, 2)
             if cpu:
                 detail[key]["cpu"] = cpu
-        del ta, tb, tc, to
+        del ta, tb, tc, to, t1
     del a, bb, c, one, one_i
     torch.cuda.empty_cache()
 
@@ -571,9 +733,11 @@ def _cfg3(torch, pn, lib, clock, dev, g, cpu_on, out, detail):
             else:
                 f = (lambda fn_c=fn_c: fn_c(ty._ptr, tx._ptr))
             cf.add(nm, "k_map1_flat / k_map1_f32_tail" if dt_name == "f32" else "k_map1_flat", bpe * ne, ne,
-                   clock.kernel_us(f, reps=REPS))
+                   clock.kernel_us(f))
         cpu = cpu_cfg3(xx, dt_name, bpe) if cpu_on else None
         out[key] = cf.summary(cpu)
+        if dt_name == "f64":
+            compute_bound(cf, out[key])
         detail[key] = cf.detail()
         if cpu:
             detail[key]["cpu"] = cpu
@@ -581,6 +745,38 @@ def _cfg3(torch, pn, lib, clock, dev, g, cpu_on, out, detail):
     del x4
     torch.cuda.empty_cache()
 
+
+
+def compute_bound(cf, summ):
+    """FP64 and VALU-issue figures of the f64 activations beside their HBM
+    figure, from the per-launch instruction counts of a rocprofv3 --pmc run
+    (profiles/cfg3_f64_valu_pmc.json: SQ_INSTS_VALU, and FP64 FLOPs =
+    64 (2 FMA + ADD + MUL) from SQ_INSTS_VALU_{FMA,ADD,MUL}_F64) and this
+    run's launch times: FP64 TFLOP/s against 78.6 TFLOP/s, and the VALU issue
+    fraction = wave instructions x 4 cycles / (1024 SIMDs x 2.4 GHz x launch
+    time) (a wave64 VALU instruction, FP64 included, occupies a 16-lane SIMD
+    for 4 cycles).  The roofline's `bound` is whichever fraction is larger."""
+    per = {}
+    for op, o in cf.ops.items():
+        v = VALU.get(op)
+        if not v:
+            continue
+        t = o["op_us"] * 1e-6
+        per[op] = {"fp64_tflops": round(v["fp64_flops"] / t / 1e12, 2),
+                   "fp64_frac": round(v["fp64_flops"] / t / 1e12 / FP64_PEAK_TFLOPS, 4),
+                   "valu_issue_frac": round(v["valu"] * VALU_CYCLES / (N_SIMD * CLOCK_GHZ * 1e9 * t), 4),
+                   "hbm_frac": round(o["pct_hbm"] / 100.0, 4)}
+    if not per:
+        return
+    summ["compute"] = per
+    rf = summ["roofline"]
+    c = per.get(rf["kernel"])
+    if c:
+        rf["fp64_tflops"] = c["fp64_tflops"]
+        rf["fp64_frac"] = c["fp64_frac"]
+        rf["valu_issue_frac"] = c["valu_issue_frac"]
+        rf["bound"] = "hbm" if rf["frac"] >= c["valu_issue_frac"] else "valu"
+    summ["bound_by_op"] = {op: ("hbm" if c["hbm_frac"] >= c["valu_issue_frac"] else "valu") for op, c in per.items()}
 
 
 def _cfg4(torch, pn, lib, clock, dev, g, cpu_on, out, detail):
@@ -599,26 +795,30 @@ def _cfg4(torch, pn, lib, clock, dev, g, cpu_on, out, detail):
     paff = torch.zeros(5, dtype=torch.float64, device=dev)
     torch.cuda.synchronize()
     cf = Config("cfg4", "cfg4: minmax calibration, symmetric and affine quantize, dequantize; 268,435,456 f32")
-    cf.add("calibrate_sym", "k_reduce_seg (+combine)", 4 * NQ, NQ,
-           *_kc(clock, lambda: lib.calibrate_minmax_f32_dev(q_in.data_ptr(), NQ, 1, psym.data_ptr())))
-    cf.add("calibrate_aff", "k_reduce_seg (+combine)", 4 * NQ, NQ,
-           *_kc(clock, lambda: lib.calibrate_minmax_f32_dev(q_in.data_ptr(), NQ, 0, paff.data_ptr())))
+    cal = "k_reduce_seg + k_reduce_combine (params in device memory)"
+    cf.add("calibrate_sym", cal, 4 * NQ, NQ,
+           *clock.op(lambda: lib.calibrate_minmax_f32_dev(q_in.data_ptr(), NQ, 1, psym.data_ptr())))
+    cf.add("calibrate_aff", cal, 4 * NQ, NQ,
+           *clock.op(lambda: lib.calibrate_minmax_f32_dev(q_in.data_ptr(), NQ, 0, paff.data_ptr())))
     cf.add("quantize_sym", "k_quantize", 5 * NQ, NQ,
-           *_kc(clock, lambda: lib.quantize_tensor_f32_dev(q_in.data_ptr(), q8.data_ptr(), NQ, psym.data_ptr())))
+           *clock.op(lambda: lib.quantize_tensor_f32_dev(q_in.data_ptr(), q8.data_ptr(), NQ, psym.data_ptr())))
     cf.add("quantize_aff", "k_quantize", 5 * NQ, NQ,
-           *_kc(clock, lambda: lib.quantize_tensor_f32_dev(q_in.data_ptr(), q8.data_ptr(), NQ, paff.data_ptr())))
+           *clock.op(lambda: lib.quantize_tensor_f32_dev(q_in.data_ptr(), q8.data_ptr(), NQ, paff.data_ptr())))
     cf.add("dequantize_f32", "k_dequantize<float>", 5 * NQ, NQ,
-           *_kc(clock, lambda: lib.dequantize_tensor_f32_dev(q8.data_ptr(), dq.data_ptr(), NQ, paff.data_ptr())))
+           *clock.op(lambda: lib.dequantize_tensor_f32_dev(q8.data_ptr(), dq.data_ptr(), NQ, paff.data_ptr())))
     hp = pn.core.QuantParamsC()
     ctypes.memmove(ctypes.addressof(hp), paff.cpu().numpy().ctypes.data, 40)
     cf.add("dequantize_f64", "k_dequantize<double>", 9 * NQ, NQ,
-           *_kc(clock, lambda: lib.dequantize_tensor(q8.data_ptr(), dq64.data_ptr(), NQ, ctypes.byref(hp))))
+           *clock.op(lambda: lib.dequantize_tensor(q8.data_ptr(), dq64.data_ptr(), NQ, ctypes.byref(hp))))
     cpu = cpu_cfg4(q_in) if cpu_on else None
     out["cfg4"] = cf.summary(cpu)
     detail["cfg4"] = cf.detail()
     if cpu:
         detail["cfg4"]["cpu"] = cpu
-    del q_in, q8, dq, dq64, psym, paff
+    del q8, dq, dq64, psym, paff
+    torch.cuda.empty_cache()
+    out["cfg4"]["host_e2e"] = host_e2e_cfg4(torch, pn, q_in)
+    del q_in
     torch.cuda.empty_cache()
 
 
@@ -640,10 +840,11 @@ def _cfg5(torch, pn, lib, clock, dev, g, cpu_on, out, detail):
     cf = Config("cfg5", "cfg5: fused NaN/Inf/L2 scan + AdamW (lr 1e-3, wd 0.01) over 100M f32, f64 m/v")
     hn, hi, ss = ctypes.c_int(), ctypes.c_int(), ctypes.c_double()
     scan = lambda: lib.neural_tensor_scan(tg._ptr, ctypes.byref(hn), ctypes.byref(hi), ctypes.byref(ss))  # noqa: E731
-    cf.add("scan", "k_reduce_seg (+combine; flags + sum of squares to the host)", 4 * NA, NA, *_kc(clock, scan))
+    cf.add("scan", "k_reduce_seg + k_reduce_combine (flags + sum of squares to the host)", 4 * NA, NA,
+           *clock.op(scan), host_call_us=clock.host_call_us(scan))
     flags = (hn.value, hi.value)
     opt = pn.AdamW(1e-3, 0.9, 0.999, 1e-8, 0.01)
-    cf.add("adamw", "k_adam_f32<AdamW>", 44 * NA, NA, *_kc(clock, lambda: opt.step([tp], [tg])))
+    cf.add("adamw", "k_adam_f32<AdamW>", 44 * NA, NA, *clock.op(lambda: opt.step([tp], [tg])))
     lib.neural_tensor_scan(tcl._ptr, ctypes.byref(hn), ctypes.byref(hi), ctypes.byref(ss))
     clean_norm = ss.value ** 0.5
     cpu = cpu_cfg5(p, clean, gr) if cpu_on else None
@@ -652,13 +853,94 @@ def _cfg5(torch, pn, lib, clock, dev, g, cpu_on, out, detail):
     detail["cfg5"] = cf.detail()
     if cpu:
         detail["cfg5"]["cpu"] = cpu
+    out["cfg5"]["host_e2e"] = host_e2e_cfg5(torch, pn, lib, tg)
     del p, gr, clean, tp, tg, tcl, opt
     torch.cuda.empty_cache()
 
 
-def _kc(clock, fn):
-    """(kernel_us, call_us) of fn, for Config.add."""
-    return clock.kernel_us(fn), clock.call_us(fn)
+# ------------------------------------------------------------- host buffers, end to end
+
+def _host_timed(fn, reps=CPU_REPS):
+    """Median host-clock seconds of fn (one warm-up call first)."""
+    return _median_time(fn, reps=reps, warm=1)
+
+
+def host_e2e_cfg4(torch, pn, q_dev):
+    """The reference's Quantizer calls on host arrays as its Python makes them
+    (pyneural/quantize.py:76-151: float64 data, a fresh ctypes int8 / float64
+    output array per call), through this library: host-clock time per call,
+    PCIe copies (staged through HBM) and the output array's allocation
+    included; rates over the same algorithmic bytes as the device ops (8 B
+    read per value for the float64 API).  Reported beside the device-resident
+    figures, never as them."""
+    import numpy as np
+    x = q_dev.cpu().numpy().astype(np.float64)
+    n = x.size
+    qz = pn.Quantizer(symmetric=True)
+    qz.calibrate(x.ctypes.data, n)
+    codes = qz.quantize(x.ctypes.data, n)
+    t_cal = _host_timed(lambda: qz.calibrate(x.ctypes.data, n))
+    t_q = _host_timed(lambda: qz.quantize(x.ctypes.data, n))
+    t_dq = _host_timed(lambda: qz.dequantize(codes, n))
+    out = {"w": f"Quantizer(symmetric=True) on {n:,} float64 values in host memory (the reference's API dtype)",
+           "calibrate_ms": round(1e3 * t_cal, 2), "calibrate_GBps": round(8 * n / t_cal / 1e9, 2),
+           "quantize_ms": round(1e3 * t_q, 2), "quantize_GBps": round(9 * n / t_q / 1e9, 2),
+           "dequantize_ms": round(1e3 * t_dq, 2), "dequantize_GBps": round(9 * n / t_dq / 1e9, 2),
+           "timing": f"host clock per call, median of {CPU_REPS} after one warm-up"}
+    del x, codes
+    return out
+
+
+def host_e2e_cfg5(torch, pn, lib, tg):
+    """NaN/Inf/L2 checks of the 100M-element gradient right after a kernel
+    wrote it, as the reference's training.py:43-79 makes them (a host pointer
+    from neural_tensor_data(), then the raw-pointer entry points; check() is
+    has_nan then has_inf, each fetching the pointer again) and as this
+    package's NaNDetector makes them (one device scan of the tensor).  Host
+    clock per call, the rewrite of the gradient between calls excluded."""
+    from pyneural.training import NaNDetector
+    n = int(lib.neural_tensor_numel(tg._ptr))
+
+    def dirty():  # g = g * 1 in place: the device copy is newer than the host mirror
+        lib.neural_scalar_mul(tg._ptr, tg._ptr, ctypes.c_double(1.0))
+        torch.cuda.synchronize()
+
+    # the reference's tensors are library-owned (host mirror + device copy)
+    own = pn.Tensor.create([n])
+    pn.core._check_error(lib.neural_tensor_copy(own._ptr, tg._ptr), "copy")
+    tg = own
+
+    def ref_check():
+        p = lib.neural_tensor_data(tg._ptr)
+        lib.neural_tensor_has_nan(p, n)
+        p = lib.neural_tensor_data(tg._ptr)
+        lib.neural_tensor_has_inf(p, n)
+
+    def ref_norm():
+        lib.neural_tensor_grad_l2_norm(lib.neural_tensor_data(tg._ptr), n)
+
+    det = NaNDetector(raise_on_detect=False)
+
+    def timed(fn, reps=CPU_REPS):
+        ts = []
+        for r in range(reps + 1):
+            dirty()
+            t = time.perf_counter()
+            fn()
+            if r:
+                ts.append(time.perf_counter() - t)
+        return statistics.median(ts)
+
+    t_ref, t_norm, t_dev = timed(ref_check), timed(ref_norm), timed(lambda: det.check(tg))
+    return {"w": f"{n:,} f32 gradient resident on the device, rewritten by a kernel before each call",
+            "reference_check_ms": round(1e3 * t_ref, 2),
+            "reference_grad_l2_norm_ms": round(1e3 * t_norm, 2),
+            "pyneural_check_ms": round(1e3 * t_dev, 3),
+            "reference_check_GBps": round(4 * n / t_ref / 1e9, 2),
+            "note": "reference shape: neural_tensor_data() downloads the tensor (PCIe); the raw-pointer scan "
+                    "resolves the mirror to the tensor's device copy (one upload, no staging buffer, no re-upload "
+                    "by the next kernel)",
+            "timing": f"host clock per call, median of {CPU_REPS} after one warm-up"}
 
 
 # ----------------------------------------------------------------------------- CPU legs
@@ -696,7 +978,8 @@ def cpu_baseline_cfg2(X, b, S, step_bytes):
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"full cfg2 step on host (oracle/liboracle.so, gcc -O2 SSE2), median of 3 = {sec:.3f} s",
+        "sample": f"full cfg2 step on host (oracle/liboracle.so, gcc -O2 SSE2), median of {CPU_REPS} after one "
+                  f"warm-up = {sec:.3f} s",
         "nproc": os.cpu_count(),
         "cpu_model": _cpu_model(),
         "threads": "1 (the reference never dispatches to its thread pool: pool size 1, unused)",
@@ -719,7 +1002,7 @@ def cpu_cfg1(a_dev, b_dev, n):
         ops["sum"] = (4 * n, _median_time(lambda: ora.cpu_sum("cpu_reduce_sum_avx", a)))
     ops["max"] = (4 * n, _median_time(lambda: ora.max_chain(a)))
     e = _cpu_entry(ops, "port", "full 64M arrays: AVX-256 add/mul/sum (math_kernels.asm), node_relu 3 passes, "
-                   "scalar maxss max; oracle/cpu_baseline.c -O2, median of 3")
+                   "scalar maxss max; oracle/cpu_baseline.c -O2, median of 5 after one warm-up")
     if c.cpu_has_avx512f():
         ops5 = {"add": (12 * n, _median_time(lambda: ora.cpu_binary("cpu_simd_add_avx512", a, b, o))),
                 "mul": (12 * n, _median_time(lambda: ora.cpu_binary("cpu_simd_mul_avx512", a, b, o))),
@@ -771,7 +1054,7 @@ def cpu_cfg3(x_dev, dt_name, bpe):
         else:
             fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
             run = (lambda fn=fn: fn(ctypes.addressof(to), ctypes.addressof(ti)))
-        ops[nm] = (bpe * x.size, _median_time(run, reps=1))
+        ops[nm] = (bpe * x.size, _median_time(run))
     return _cpu_entry(ops, "reference", f"activations_c.c compiled unchanged (oracle/_ref, -O2 SSE2, glibc libm), "
                       f"first {CPU_ACT_SAMPLE:,} elements of the same {dt_name} input")
 
@@ -843,8 +1126,9 @@ def suite(torch, pn, clock, dev, cpu=True):
     """Kernel families outside BASELINE's configs (detail file only): for each
     op the kernel time of its main launch (`k`, HIP event pair on that launch)
     and, where a call makes several launches or returns a result to the host,
-    the call time (`call`, all launches and gaps), in us, with the algorithmic
-    bytes of the main kernel.  With `cpu`, each op also carries its CPU leg
+    the call time (`call`: the event span over all of the call's launches and
+    gaps, or, where the result returns to the host, the host-clock time of
+    the whole call), in us, with the algorithmic bytes of the main kernel.  With `cpu`, each op also carries its CPU leg
     (`cpu`: one host thread, GB/s over the same bytes per element) on a bounded
     sample (SUITE_CPU_SAMPLE elements, rows of it for the row ops) of the same
     input: the reference's own C (oracle/_ref, kind "reference") where it
@@ -916,7 +1200,7 @@ def suite(torch, pn, clock, dev, cpu=True):
     fwd = lambda: _lib.neural_dropout_forward(a.data_ptr(), c.data_ptr(), dmask.data_ptr(), n, ctypes.c_float(0.5))
     put("dropout_fwd_keep_bits_f32_64M", 0, clock.kernel_us(fwd, skip=0))
     put("dropout_fwd_apply_f32_64M", 9 * n, clock.kernel_us(fwd, skip=1))
-    put("dropout_fwd_f32_64M", 9 * n, None, clock.call_us(fwd))
+    put("dropout_fwd_f32_64M", 9 * n, None, clock.op(fwd)[1])
     put("dropout_bwd_f32_64M", 9 * n, clock.kernel_us(
         lambda: _lib.neural_dropout_backward(a.data_ptr(), c.data_ptr(), dmask.data_ptr(), n, ctypes.c_float(0.5))))
     if cpu:
@@ -937,10 +1221,10 @@ def suite(torch, pn, clock, dev, cpu=True):
     G64 = torch.empty_like(L64)
     torch.cuda.synchronize()
     f = lambda: _lib.label_smoothing_ce_forward(L64.data_ptr(), tgt.data_ptr(), B, K, 0.1, ctypes.byref(lossv))
-    put("ls_ce_forward_f64_65536x1024", 8 * B * K, clock.kernel_us(f), clock.call_us(f))
+    put("ls_ce_forward_f64_65536x1024", 8 * B * K, clock.kernel_us(f), clock.host_call_us(f))
     f = lambda: _lib.label_smoothing_ce_fused(L64.data_ptr(), tgt.data_ptr(), B, K, 0.1, ctypes.byref(lossv),
                                               G64.data_ptr())
-    put("ls_ce_fused_f64_65536x1024", 16 * B * K, clock.kernel_us(f), clock.call_us(f))
+    put("ls_ce_fused_f64_65536x1024", 16 * B * K, clock.kernel_us(f), clock.host_call_us(f))
     if cpu:
         rows = SUITE_CPU_SAMPLE // K
         Lh, th = L64[:rows].cpu().numpy(), tgt[:rows].cpu().numpy()
@@ -956,11 +1240,11 @@ def suite(torch, pn, clock, dev, cpu=True):
     torch.cuda.synchronize()
     f = lambda: _lib.label_smoothing_ce_fused_f32(L32.data_ptr(), tgt.data_ptr(), B, K, 0.1, ctypes.byref(lossv),
                                                   G32.data_ptr())
-    put("ls_ce_fused_f32_65536x1024", 8 * B * K, clock.kernel_us(f), clock.call_us(f))
+    put("ls_ce_fused_f32_65536x1024", 8 * B * K, clock.kernel_us(f), clock.host_call_us(f))
     tv = W(tgt.float())
     tL = W(L32)
     f = lambda: _lib.neural_cross_entropy_loss(tL._ptr, tv._ptr, ctypes.byref(lossv))
-    put("ce_loss_f32_65536x1024", 4 * B * K, clock.kernel_us(f), clock.call_us(f))
+    put("ce_loss_f32_65536x1024", 4 * B * K, clock.kernel_us(f), clock.host_call_us(f))
     if cpu:
         rows = SUITE_CPU_SAMPLE // K
         Lh, th = L32[:rows].cpu().numpy(), tgt[:rows].cpu().numpy()
@@ -989,11 +1273,11 @@ def suite(torch, pn, clock, dev, cpu=True):
         state["m"] *= 0.999
         return _lib.neural_clip_grad_norm_list(glist, 1, ctypes.c_double(state["m"]), ctypes.byref(tot))
 
-    put("clip_grad_norm_clipping_f32_100M", 12 * na, None, clock.call_us(clip_scaling))
-    put("clip_grad_norm_below_f32_100M", 4 * na, None, clock.call_us(
+    put("clip_grad_norm_clipping_f32_100M", 12 * na, None, clock.host_call_us(clip_scaling))
+    put("clip_grad_norm_below_f32_100M", 4 * na, None, clock.host_call_us(
         lambda: _lib.neural_clip_grad_norm_list(glist, 1, ctypes.c_double(1e30), ctypes.byref(tot))))
     f = lambda: _lib.neural_clip_grad_value_list(glist, 1, ctypes.c_double(-1e-3), ctypes.c_double(1e-3))
-    put("clip_grad_value_f32_100M", 8 * na, clock.kernel_us(f), clock.call_us(f))
+    put("clip_grad_value_f32_100M", 8 * na, clock.kernel_us(f), clock.op(f)[1])
     if cpu:
         gh = gr[:SUITE_CPU_SAMPLE].cpu().numpy()
         nh = ora.clip_grad_norm([gh], 1e30)[0]
@@ -1012,10 +1296,10 @@ def suite(torch, pn, clock, dev, cpu=True):
     st = [torch.empty(TF, device=dev, dtype=torch.float64) for _ in range(4)]
     torch.cuda.synchronize()
     f = lambda: _lib.transform_compute_stats(D.data_ptr(), TB, TF, *[t.data_ptr() for t in st])
-    put("transform_compute_stats_f64_1Mx64", 8 * TB * TF, clock.kernel_us(f), clock.call_us(f))
+    put("transform_compute_stats_f64_1Mx64", 8 * TB * TF, clock.kernel_us(f), clock.op(f)[1])
     f = lambda: _lib.transform_normalize(D.data_ptr(), O.data_ptr(), TB, TF, st[0].data_ptr(), st[1].data_ptr(),
                                          ctypes.c_double(1e-8))
-    put("transform_normalize_f64_1Mx64", 16 * TB * TF, clock.kernel_us(f), clock.call_us(f))
+    put("transform_normalize_f64_1Mx64", 16 * TB * TF, clock.kernel_us(f), clock.op(f)[1])
     if cpu:
         Dh = D[:SUITE_CPU_SAMPLE // TF].cpu().numpy()
         _, mu, sd, _, _ = ora.transform_stats(Dh, use_ref=True)
@@ -1032,7 +1316,7 @@ def suite(torch, pn, clock, dev, cpu=True):
     P = torch.randn(1 << 26, device=dev, dtype=torch.float64, generator=g)
     qp = QuantParamsC()
     torch.cuda.synchronize()
-    put("calibrate_percentile_f64_64M", 8 * P.numel(), None, clock.call_us(
+    put("calibrate_percentile_f64_64M", 8 * P.numel(), None, clock.host_call_us(
         lambda: _lib.calibrate_percentile(P.data_ptr(), P.numel(), ctypes.c_double(0.01), 1, ctypes.byref(qp))))
     if cpu:
         Ph = P[:SUITE_CPU_SAMPLE].cpu().numpy()
@@ -1047,8 +1331,8 @@ def suite(torch, pn, clock, dev, cpu=True):
     pa, pb = QuantParamsC(), QuantParamsC()
     pa.scale, pa.zero_point, pb.scale, pb.zero_point = 0.013, -7, 0.37, 11
     torch.cuda.synchronize()
-    us = clock.call_us(lambda: _lib.quantized_matmul(A8.data_ptr(), B8.data_ptr(), C8.data_ptr(), m, m, m,
-                                                     ctypes.byref(pa), ctypes.byref(pb)))
+    us = clock.op(lambda: _lib.quantized_matmul(A8.data_ptr(), B8.data_ptr(), C8.data_ptr(), m, m, m,
+                                                     ctypes.byref(pa), ctypes.byref(pb)))[1]
     res["quantized_matmul_4096^3"] = {"call_us": round(us, 2), "int8_TOPS": round(2.0 * m ** 3 / us / 1e6, 1)}
     if cpu and ref is not None:
         mc = 256

@@ -572,7 +572,23 @@ int upsample2d_nearest_forward(void *, int64_t, int64_t, int64_t, int64_t, int64
  * NEURAL_ERR_NULL_POINTER for a null event, NEURAL_ERR_INVALID_ARGUMENT for
  * skip < 0. */
 int   neural_hip_time_next_launch(void *start_event, void *stop_event, int skip);
+/* NEW (no reference counterpart; for measurement): the same over a span of
+ * launches: after `skip` launches, the next one records start_event when it
+ * starts executing and the launch `count` - 1 later records stop_event when it
+ * ends, so hipEventElapsedTime spans every kernel of a multi-launch call and
+ * the gaps between them (count = 1 is neural_hip_time_next_launch).  Returns
+ * NEURAL_ERR_INVALID_ARGUMENT for skip < 0 or count < 1. */
+int   neural_hip_time_launches(void *start_event, void *stop_event, int skip, int count);
 int   neural_hip_time_cancel(void);
+/* NEW (no reference counterpart; for measurement): kernel launches the
+ * calling thread has made so far (the difference around a call is the number
+ * of launches the call makes). */
+unsigned long long neural_hip_launch_count(void);
+/* NEW (no reference counterpart; a bandwidth reference for measurement):
+ * dst = src over `bytes` bytes with the library's flat streaming kernel
+ * (16-byte non-temporal loads and stores).  Device pointers only, 16-byte
+ * aligned, bytes a multiple of 16; otherwise NEURAL_ERR_INVALID_ARGUMENT. */
+int   neural_hip_stream_copy(void *dst, const void *src, uint64_t bytes);
 int   neural_hip_set_stream(void *hip_stream);
 int   neural_hip_reset_stream(void);
 void *neural_hip_get_stream(void);

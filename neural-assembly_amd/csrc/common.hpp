@@ -78,14 +78,18 @@ int          ensure_ready();
 // device current (defined beside the buffer it resolves).
 int          setup_static_scratch(int device);
 hipStream_t  stream();                   // active stream
-// A pair of events armed by neural_hip_time_next_launch on the calling
-// thread: the launch `skip` launches later carries them (see NH_LAUNCH).
+// A pair of events armed by neural_hip_time_launches on the calling thread:
+// after `skip` launches, the next launch carries `start` and the launch
+// `count` - 1 later carries `stop` (the same launch both when count is 1), so
+// the pair spans those launches and the gaps between them (see NH_LAUNCH).
 struct LaunchTimer {
     hipEvent_t start = nullptr, stop = nullptr;
     int skip = 0;
+    int count = 1;
 };
-// Counts this thread's launches down; returns the events once, for the launch
-// they were armed for, and null events otherwise.
+// Called once per launch: counts this thread's launches (launch_count) and
+// the armed span down, and returns the events this launch records (either or
+// both may be null).
 LaunchTimer  take_launch_timer();
 int          num_cus();
 int          set_error(int code);        // stores thread-local last error, returns code
@@ -122,17 +126,27 @@ struct WsGuard {
 bool         is_device_ptr(const void *p);
 
 // Stage a caller pointer into device memory.  For device pointers the
-// pointer itself is used; for host pointers a device block is allocated and
-// (when upload) filled.  finish() copies back (when download) and frees.
+// pointer itself is used.  A host pointer into the host mirror of a live
+// library tensor (what neural_tensor_data() returns) resolves to that
+// tensor's device copy: made current first if the host copy is
+// authoritative, so no temporary buffer and no second upload by the tensor's
+// next kernel.  Other host pointers get a device block, filled when upload.
+// finish() copies back to the host pointer (when download) and frees.
 struct Staged {
-    void  *dev = nullptr;
-    void  *host = nullptr;
-    size_t bytes = 0;
-    bool   owned = false;
+    void    *dev = nullptr;
+    void    *host = nullptr;
+    size_t   bytes = 0;
+    bool     owned = false;
+    Storage *mirror = nullptr;  // the tensor storage whose mirror `host` lies in
     int    open(const void *p, size_t nbytes, bool upload);
     int    finish(bool download);
     ~Staged();
 };
+
+// Owned tensors' host mirrors, for Staged::open (registered at creation,
+// removed when the storage is released).
+void         mirror_register(Storage *s);
+void         mirror_unregister(Storage *s);
 
 // Tensor coherence
 int64_t      numel(const NeuralTensor *t);
@@ -314,13 +328,14 @@ template <typename T> NH_DEV T ld_nt(const T *p) { return __builtin_nontemporal_
 template <typename T> NH_DEV void st_nt(T *p, T v) { __builtin_nontemporal_store(v, p); }
 
 // Every kernel launch goes through NH_LAUNCH.  When the calling thread has
-// armed an event pair (neural_hip_time_next_launch), the launch it was armed
-// for is made with hipExtLaunchKernelGGL, which records the events around
-// this kernel's own execution on its stream; every other launch is plain.
+// armed an event pair (neural_hip_time_launches), the launches that carry its
+// start and stop events are made with hipExtLaunchKernelGGL, which records
+// them at the start and the end of that kernel's own execution on its stream;
+// every other launch is plain.
 #define NH_LAUNCH(kernel, grid, block, shmem, strm, ...)                                            \
     do {                                                                                            \
         const nh::LaunchTimer t__ = nh::take_launch_timer();                                        \
-        if (t__.start)                                                                              \
+        if (t__.start || t__.stop)                                                                  \
             hipExtLaunchKernelGGL(kernel, grid, block, shmem, strm, t__.start, t__.stop, 0, __VA_ARGS__); \
         else                                                                                        \
             hipLaunchKernelGGL(kernel, grid, block, shmem, strm, __VA_ARGS__);                      \

@@ -37,6 +37,12 @@ struct FnRelu {
     NH_DEV double operator()(double x) const { return x > 0.0 ? x : 0.0; }
 };
 
+// Identity: the streaming copy the flat kernels' tiling gives for a 1:1
+// read / write stream (the bandwidth reference neural_hip_stream_copy times).
+struct FnCopy {
+    NH_DEV float operator()(float x) const { return x; }
+};
+
 // vec_add_relu_fusion (fusion.asm:200-226) and the bias + ReLU epilogue of
 // matmul_bias_relu_fusion (fusion.asm:110-190): addss, then maxss with +0.
 struct OpAddRelu {
@@ -361,6 +367,22 @@ int simd_fma_f32(float *dst, const float *a, const float *b, const float *c, uin
     NH_TRY(sa.finish(false));
     NH_TRY(sb.finish(false));
     NH_TRY(sc.finish(false));
+    return set_error(NEURAL_OK);
+}
+
+// neural_hip_stream_copy (NEW, no reference counterpart; a bandwidth
+// reference for measurement): dst = src over `bytes` bytes of device memory
+// through k_map1_flat (16-byte non-temporal loads and stores, the tiling of
+// every flat streaming kernel).  Both pointers must be device pointers,
+// 16-byte aligned, and bytes a multiple of 16.
+int neural_hip_stream_copy(void *dst, const void *src, uint64_t bytes)
+{
+    NH_TRY(ensure_init());
+    if (!dst || !src) return set_error(NEURAL_ERR_NULL_POINTER);
+    if (bytes % 16 != 0 || !aligned16(dst) || !aligned16(src) || !is_device_ptr(dst) || !is_device_ptr(src))
+        return set_error(NEURAL_ERR_INVALID_ARGUMENT);
+    NH_TRY(launch_map1_flat(static_cast<const float *>(src), static_cast<float *>(dst), int64_t(bytes / 4),
+                            FnCopy{}));
     return set_error(NEURAL_OK);
 }
 

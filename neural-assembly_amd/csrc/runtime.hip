@@ -7,6 +7,7 @@
 // neural_tensor_data() (see the memory-model note in include/neural_api.h).
 #include <cstdio>
 #include <cstdlib>
+#include <map>
 #include <mutex>
 #include <new>
 #include <unordered_map>
@@ -277,12 +278,59 @@ int result_to_host(void *dst, const void *dev_src, size_t bytes)
 // Staging of caller pointers
 // ---------------------------------------------------------------------------
 
+// Host mirrors of owned tensors by start address (the mirror of a storage
+// covers [host, host + hi)), for Staged::open.
+namespace {
+std::mutex g_mirror_mu;
+std::map<uintptr_t, Storage *> g_mirrors;
+}  // namespace
+
+void mirror_register(Storage *s)
+{
+    std::lock_guard<std::mutex> g(g_mirror_mu);
+    g_mirrors[reinterpret_cast<uintptr_t>(s->host)] = s;
+}
+
+void mirror_unregister(Storage *s)
+{
+    std::lock_guard<std::mutex> g(g_mirror_mu);
+    const auto it = g_mirrors.find(reinterpret_cast<uintptr_t>(s->host));
+    if (it != g_mirrors.end() && it->second == s) g_mirrors.erase(it);
+}
+
+// The owned storage whose host mirror holds all of [p, p + nbytes), or null.
+static Storage *mirror_lookup(const void *p, size_t nbytes)
+{
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    std::lock_guard<std::mutex> g(g_mirror_mu);
+    auto it = g_mirrors.upper_bound(a);
+    if (it == g_mirrors.begin()) return nullptr;
+    --it;
+    Storage *s = it->second;
+    const uintptr_t end = it->first + uintptr_t(s->hi);
+    return (a >= it->first && a < end && nbytes <= end - a) ? s : nullptr;
+}
+
 int Staged::open(const void *p, size_t nbytes, bool upload)
 {
     bytes = nbytes;
     host = const_cast<void *>(p);
     if (is_device_ptr(p)) {
         dev = const_cast<void *>(p);
+        owned = false;
+        return NEURAL_OK;
+    }
+    if (Storage *s = nbytes ? mirror_lookup(p, nbytes) : nullptr) {
+        // The device copy serves both reads and writes; bytes outside
+        // [p, p + nbytes) must be current on the device too, so a
+        // host-authoritative mirror is uploaded whole (dev_read's rule).
+        if (s->state == ST_HOST) {
+            const int64_t span = s->hi - s->lo;
+            if (span > 0) NH_HIP(hipMemcpyAsync(s->dev_block, s->host, size_t(span), hipMemcpyHostToDevice, stream()));
+            s->state = ST_SYNCED;
+        }
+        dev = static_cast<char *>(s->dev_block) + (static_cast<const char *>(p) - static_cast<const char *>(s->host));
+        mirror = s;
         owned = false;
         return NEURAL_OK;
     }
@@ -295,8 +343,17 @@ int Staged::open(const void *p, size_t nbytes, bool upload)
 
 int Staged::finish(bool download)
 {
-    if (owned && download && bytes)
+    // A mirror-backed output was written on the device; the caller may read
+    // it through the host pointer, so the written range goes back there too
+    // (the storage keeps its state: SYNCED stays in sync, DEVICE stays ahead).
+    if ((owned || mirror) && download && bytes)
         NH_HIP(hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, stream()));
+    if (mirror) {
+        if (download && bytes) NH_TRY(sync());
+        mirror = nullptr;
+        dev = nullptr;
+        return NEURAL_OK;
+    }
     if (owned) {
         NH_TRY(sync());
         dev_free(dev);
@@ -413,16 +470,23 @@ static void *host_map(NeuralTensor *t)
 }
 
 thread_local LaunchTimer t_timer;
+thread_local unsigned long long t_launches = 0;
 
 LaunchTimer take_launch_timer()
 {
-    if (!t_timer.start) return LaunchTimer{};
+    t_launches++;
+    if (!t_timer.start && !t_timer.stop) return LaunchTimer{};
     if (t_timer.skip > 0) {
         t_timer.skip--;
         return LaunchTimer{};
     }
-    const LaunchTimer t = t_timer;
-    t_timer = LaunchTimer{};
+    LaunchTimer t;
+    t.start = t_timer.start;  // null once the span's first launch has taken it
+    t_timer.start = nullptr;
+    if (--t_timer.count <= 0) {
+        t.stop = t_timer.stop;
+        t_timer = LaunchTimer{};
+    }
     return t;
 }
 
@@ -503,7 +567,10 @@ void storage_release(Storage *s)
     if (!s || --s->refs > 0) return;
     // Stream-ordered reuse makes an immediate return to the cache safe.
     if (s->dev_block) dev_free(s->dev_block);
-    if (s->host_owned) std::free(s->host);
+    if (s->host_owned) {
+        mirror_unregister(s);
+        std::free(s->host);
+    }
     delete s;
 }
 
@@ -563,6 +630,7 @@ NeuralTensor *create_owned(const uint64_t *shape, uint64_t ndim, int dtype, bool
     t->kind = KIND_OWNED;
     t->flags = NT_OWN_DATA | NT_OWN_META;
     t->st = s;
+    mirror_register(s);
     // tensor_create zero-fills every new tensor (tensor.asm:326-329); the
     // fill runs in HBM.
     (void)zero;
@@ -901,15 +969,21 @@ int neural_hip_reset_stream(void)
     return set_error(NEURAL_OK);
 }
 
-int neural_hip_time_next_launch(void *start_event, void *stop_event, int skip)
+int neural_hip_time_launches(void *start_event, void *stop_event, int skip, int count)
 {
     NH_TRY(ensure_init());
     if (!start_event || !stop_event) return set_error(NEURAL_ERR_NULL_POINTER);
-    if (skip < 0) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
+    if (skip < 0 || count < 1) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
     t_timer.start = static_cast<hipEvent_t>(start_event);
     t_timer.stop = static_cast<hipEvent_t>(stop_event);
     t_timer.skip = skip;
+    t_timer.count = count;
     return set_error(NEURAL_OK);
+}
+
+int neural_hip_time_next_launch(void *start_event, void *stop_event, int skip)
+{
+    return neural_hip_time_launches(start_event, stop_event, skip, 1);
 }
 
 int neural_hip_time_cancel(void)
@@ -917,6 +991,8 @@ int neural_hip_time_cancel(void)
     t_timer = LaunchTimer{};
     return set_error(NEURAL_OK);
 }
+
+unsigned long long neural_hip_launch_count(void) { return t_launches; }
 
 void *neural_hip_get_stream(void)
 {

@@ -284,6 +284,9 @@ _SIGS = {
     # HIP runtime controls
     "neural_hip_set_stream": (_i, [_vp]),
     "neural_hip_time_next_launch": (_i, [_vp, _vp, _i]),
+    "neural_hip_time_launches": (_i, [_vp, _vp, _i, _i]),
+    "neural_hip_launch_count": (ctypes.c_ulonglong, []),
+    "neural_hip_stream_copy": (_i, [_vp, _vp, _u64]),
     "neural_hip_time_cancel": (_i, []),
     "neural_hip_reset_stream": (_i, []),
     "neural_hip_get_stream": (_vp, []),

@@ -107,3 +107,59 @@ def test_torch_stream_interop(pn):
         same_bits(out.cpu().numpy(), a.cpu().numpy() + b.cpu().numpy())  # stream-ordered, no explicit sync
     finally:
         pn.set_stream(None)
+
+
+def test_raw_pointer_into_tensor_mirror(pn):
+    """The reference's Python hands neural_tensor_data() pointers to the
+    raw-pointer entry points (training.py:43-79).  Such a pointer resolves to
+    the tensor's device copy, under the rule every kernel follows: host
+    writes made through the pointer after neural_tensor_data() are seen by the
+    next call, device writes made after the pointer was handed out are seen
+    too (the reference has one copy of the data), partial ranges work, and an
+    output written through a mirror pointer lands both in the host mirror and
+    on the device."""
+    lib = pn.core._lib
+    n = 1 << 20
+    t = pn.Tensor.from_numpy(np.linspace(-1, 1, n, dtype=np.float32))
+    p = lib.neural_tensor_data(t._ptr)
+    assert lib.neural_tensor_has_nan(p, n) == 0 and lib.neural_tensor_has_inf(p, n) == 0
+    # a host write through a freshly fetched pointer (as the reference's
+    # tensor.py writes: neural_tensor_data() makes the host copy
+    # authoritative), then the raw call
+    p = lib.neural_tensor_data(t._ptr)
+    bad = np.array([np.nan], dtype=np.float32)
+    ctypes.memmove(p + 4 * 777, bad.ctypes.data, 4)
+    assert lib.neural_tensor_has_nan(p, n) == 1
+    assert lib.neural_tensor_has_nan(p + 4 * 778, n - 778) == 0   # range after the NaN
+    assert lib.neural_tensor_has_nan(p + 4 * 700, 100) == 1       # range around it
+    # the NaN reached the device copy: a kernel sees it without another upload
+    r = pn.Tensor.create([n])
+    pn.core._check_error(lib.neural_relu(r._ptr, t._ptr), "relu")
+    assert r.numpy()[777] == 0.0
+    # a device write after the pointer was handed out: the old pointer sees it
+    pn.core._check_error(lib.neural_tensor_fill(t._ptr, ctypes.c_double(float("inf"))), "fill")
+    assert lib.neural_tensor_has_inf(p, n) == 1 and lib.neural_tensor_has_nan(p, n) == 0
+    want_norm = np.float32(np.sqrt(np.float64(n) * 4.0))
+    pn.core._check_error(lib.neural_tensor_fill(t._ptr, ctypes.c_double(2.0)), "fill")
+    assert np.float32(lib.neural_tensor_grad_l2_norm(p, n)) == want_norm
+    # an output through a mirror pointer: host mirror and device copy agree
+    c = pn.Tensor.create([n])
+    pc = lib.neural_tensor_data(c._ptr)
+    a = np.arange(n, dtype=np.float32)
+    b = np.full(n, 0.5, dtype=np.float32)
+    assert lib.simd_add_f32(pc, a.ctypes.data, b.ctypes.data, n) == 0
+    host_view = np.ctypeslib.as_array(ctypes.cast(pc, ctypes.POINTER(ctypes.c_float)), shape=(n,))
+    same_bits(host_view.copy(), a + b)
+    same_bits(c.numpy(), a + b)
+    s = pn.Tensor.create([n])
+    pn.core._check_error(lib.neural_add(s._ptr, c._ptr, c._ptr), "add")
+    same_bits(s.numpy(), (a + b) * 2)
+    # host buffers that are not mirrors (below, between and above the live
+    # mirrors' addresses) are staged as before
+    for m in (7, 1000, 1 << 16, 3 << 20):
+        x = np.ones(m, dtype=np.float32)
+        x[m // 2] = np.nan
+        assert lib.neural_tensor_has_nan(x.ctypes.data, m) == 1
+        y = np.empty(m, dtype=np.float32)
+        assert lib.simd_add_f32(y.ctypes.data, x.ctypes.data, x.ctypes.data, m) == 0
+        same_bits(y, x + x)
