@@ -85,28 +85,58 @@ struct RedMaxChain {
 
 // Argmax: idx = 0, m = x0, update iff x_j > m (main.asm:3245-3292,3598-3640):
 // the first index of the largest non-NaN value, or 0 when x0 is NaN or no
-// element exceeds -inf.  Lane state {best value, its first index}; ties go to
-// the smaller index, so the combine is order-free.
+// element exceeds -inf.  Lane state {best value, its first index relative to
+// the segment start} (8 bytes for f32: two dwords through every butterfly
+// step); segment summary {row index, value}.  Ties go to the smaller index,
+// so the combine is order-free.
+template <typename T> struct ArgLane;
+template <> struct ArgLane<float> { float v; int32_t i; };
+template <> struct ArgLane<double> { double v; int32_t i, pad; };
+
 template <typename T>
 struct RedArgmax {
-    struct L { int64_t i; T v; int32_t pad[sizeof(T) == 4 ? 1 : 2]; };
-    using B = L;
-    NH_DEV L linit() const { return {-1, -inf_t<T>(), {}}; }
+    static constexpr bool kRelIndex = true;
+    static constexpr bool kStoreReadsFirst = true;
+    using L = ArgLane<T>;
+    struct B { int64_t i; T v; int32_t pad[sizeof(T) == 4 ? 1 : 2]; };
+    NH_DEV L linit() const
+    {
+        L l{};
+        l.v = -inf_t<T>();
+        l.i = -1;
+        return l;
+    }
     NH_DEV void lacc(L &s, T x, int64_t i) const
     {
         const bool up = x > s.v;
         s.v = up ? x : s.v;
-        s.i = up ? i : s.i;
+        s.i = up ? int32_t(i) : s.i;
     }
     NH_DEV L lcomb(L a, L b) const
     {
         if (b.v > a.v || (b.v == a.v && b.i >= 0 && (a.i < 0 || b.i < a.i))) return b;
         return a;
     }
-    template <int TPR>
-    NH_DEV B finish(L s, const T *, int64_t, int64_t) const { return s; }
-    NH_DEV B bident() const { return linit(); }
-    NH_DEV B bcomb(B a, B b) const { return lcomb(a, b); }
+    template <int TPR, class R>
+    NH_DEV B finish(L s, const R &, int64_t lo, int64_t) const
+    {
+        B b{};
+        b.i = s.i >= 0 ? lo + s.i : -1;
+        b.v = s.v;
+        return b;
+    }
+    NH_DEV B bident() const
+    {
+        B b{};
+        b.i = -1;
+        b.v = -inf_t<T>();
+        return b;
+    }
+    NH_DEV B bcomb(B a, B b) const
+    {
+        if (b.v > a.v || (b.v == a.v && b.i >= 0 && (a.i < 0 || b.i < a.i))) return b;
+        return a;
+    }
     template <class R>
     NH_DEV void store(void *out, int64_t r, B b, const R &row, int64_t) const
     {
@@ -123,29 +153,35 @@ struct RedArgmax {
 // same rows.  Null output pointers are skipped.
 template <typename T>
 struct RedStats {
+    static constexpr bool kRelIndex = true;
+    static constexpr bool kStoreReadsFirst = true;
     using S = RedSum<T, SUM_OUT_T>;
     using M = RedMaxChain<T, OUT_T>;
     using A = RedArgmax<T>;
-    struct L { typename S::L s; typename M::L m; typename A::L a; };
+    // Lane state: the double sum and the argmax lane, whose best value is also
+    // the max chain's NaN-ignoring lane maximum (x > v and fmax(v, x) agree
+    // except on the sign of a zero, which the chain's zero rescan decides).
+    // A NaN makes the double sum NaN, so a NaN sum stands for the chain's NaN
+    // sentinel (it also fires for +Inf with -Inf; the rescan then finds no NaN
+    // and changes nothing).  4 dwords for f32 instead of 8.
+    struct L { double s; typename A::L a; };
     struct B { typename S::B s; typename M::B m; typename A::B a; };
     T *sum = nullptr, *mean = nullptr, *max = nullptr;
     int64_t *argmax = nullptr;
     int64_t cols = 1;
 
-    NH_DEV L linit() const { return {S{}.linit(), M{}.linit(), A{}.linit()}; }
+    NH_DEV L linit() const { return {0.0, A{}.linit()}; }
     NH_DEV void lacc(L &l, T x, int64_t i) const
     {
-        S{}.lacc(l.s, x, i);
-        M{}.lacc(l.m, x, i);
+        l.s += double(x);
         A{}.lacc(l.a, x, i);
     }
-    NH_DEV L lcomb(L a, L b) const { return {S{}.lcomb(a.s, b.s), M{}.lcomb(a.m, b.m), A{}.lcomb(a.a, b.a)}; }
+    NH_DEV L lcomb(L a, L b) const { return {a.s + b.s, A{}.lcomb(a.a, b.a)}; }
     template <int TPR, class R>
     NH_DEV B finish(L l, const R &row, int64_t lo, int64_t hi) const
     {
-        const T *none = nullptr;  // the sum and argmax summaries do not look at the row
-        return {S{}.template finish<TPR>(l.s, none, lo, hi), M{}.template finish<TPR>(l.m, row, lo, hi),
-                A{}.template finish<TPR>(l.a, none, lo, hi)};
+        const typename M::L ml{l.a.v, l.s != l.s ? qnan_t<T>() : T(0)};
+        return {l.s, M{}.template finish<TPR>(ml, row, lo, hi), A{}.template finish<TPR>(l.a, row, lo, hi)};
     }
     NH_DEV B bident() const { return {S{}.bident(), M{}.bident(), A{}.bident()}; }
     NH_DEV B bcomb(B a, B b) const { return {S{}.bcomb(a.s, b.s), M{}.bcomb(a.m, b.m), A{}.bcomb(a.a, b.a)}; }
@@ -172,9 +208,9 @@ struct BiasPre {
     using V = typename Vec16<T>::type;
     const T *bias;  // [cols]
     T *y;           // this row of the output
-    NH_DEV V vec(const V &v, int64_t i) const
+    NH_DEV V load(int64_t i) const { return reinterpret_cast<const V *>(bias)[i]; }
+    NH_DEV V vec(const V &v, const V &b, int64_t i) const
     {
-        const V b = reinterpret_cast<const V *>(bias)[i];
         V r;
 #pragma unroll
         for (int k = 0; k < Vec16<T>::n; k++) r[k] = v[k] + b[k];
@@ -208,10 +244,11 @@ __global__ __launch_bounds__(kRBlock) void k_bias_row_stats(const T *__restrict_
     for (int64_t r = int64_t(blockIdx.x) * RPB + threadIdx.x / TPR; r < rows; r += int64_t(gridDim.x) * RPB) {
         const T *xr = x + r * cols;
         const BiasPre<T> pre{bias, y + r * cols};
-        const typename RedStats<T>::L l = seg_walk<T, RedStats<T>, TPR, true>(red, xr, 0, cols, vec, pre);
+        T y0 = T(0);  // y[r][0] as lane 0 computed it
+        const typename RedStats<T>::L l = seg_walk<T, RedStats<T>, TPR, true>(red, xr, 0, cols, vec, pre, &y0);
         const BiasRow<T> row{xr, bias};
         const typename RedStats<T>::B b = red.template finish<TPR>(l, row, 0, cols);
-        if (Grp<TPR>::lane() == 0) red.store(nullptr, r, b, row, cols);
+        if (Grp<TPR>::lane() == 0) red.store(nullptr, r, b, FirstOnly<T>{y0}, cols);
     }
 }
 

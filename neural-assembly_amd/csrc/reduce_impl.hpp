@@ -31,6 +31,8 @@
 // L and B are trivially copyable, a multiple of 4 bytes, B at most 64 bytes.
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace nh {
@@ -67,9 +69,24 @@ NH_DEV S shfl_down_obj(const S &s, int off)
     return r;
 }
 
+template <int CTRL, typename S>
+NH_DEV S dpp_obj(const S &s)
+{
+    constexpr int W = sizeof(S) / 4;
+    int w[W];
+    __builtin_memcpy(w, &s, sizeof(S));
+#pragma unroll
+    for (int k = 0; k < W; k++) w[k] = dpp_i<CTRL>(w[k]);
+    S r;
+    __builtin_memcpy(&r, w, sizeof(S));
+    return r;
+}
+
 // Group of TPR lanes (64 = one wave, 256 = the whole block).  reduce() leaves
-// the same value in every lane of the group: the butterfly pairs are fixed and
-// each pair computes comb(a, b) and comb(b, a), equal for commutative comb.
+// the same value in every lane of the group: the pairs are fixed and each
+// pair computes comb(a, b) and comb(b, a), equal for commutative comb.  Within
+// a wave: quad swaps (xor 1, xor 2), the half-row and row mirrors as DPP
+// operand moves (no LDS traffic), then lane exchanges across 16 and 32.
 template <int TPR>
 struct Grp {
     static_assert(TPR == 64 || TPR == kRBlock, "a group is one wave or one block");
@@ -77,8 +94,12 @@ struct Grp {
     template <typename S, typename C>
     NH_DEV static S reduce(S s, C comb)
     {
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) s = comb(s, shfl_xor_obj(s, off));
+        s = comb(s, dpp_obj<kDppXor1>(s));
+        s = comb(s, dpp_obj<kDppXor2>(s));
+        s = comb(s, dpp_obj<kDppHalfMirror>(s));
+        s = comb(s, dpp_obj<kDppMirror>(s));
+        s = comb(s, shfl_xor_obj(s, 16));
+        s = comb(s, shfl_xor_obj(s, 32));
         if constexpr (TPR == 64) {
             return s;
         } else {
@@ -105,10 +126,24 @@ struct Grp {
 
 // ---- the segment walk ---------------------------------------------------------------------
 
-// No prologue: the walked values are the row's own.
+// Reducers that declare `static constexpr bool kRelIndex = true` receive the
+// element's index relative to the segment start `lo` (it fits 32 bits: every
+// launch checks that segments hold fewer than 2^31 elements), computed in
+// 32-bit arithmetic; their finish() turns lane indices back into row indices.
+// Others receive the index in the row.
+template <class Red, typename = void> struct RelIndex { static constexpr bool value = false; };
+template <class Red> struct RelIndex<Red, std::void_t<decltype(Red::kRelIndex)>> {
+    static constexpr bool value = Red::kRelIndex;
+};
+
+// No prologue: the walked values are the row's own.  A prologue's load(i)
+// fetches what vec() needs beside the row's vector i (the fused bias add: the
+// bias vector); the walk issues those loads together with the row's loads,
+// before it waits for any of them.
 struct NoPre {
     static constexpr bool kActive = false;
-    template <typename V> NH_DEV V vec(const V &v, int64_t) const { return v; }
+    NH_DEV int load(int64_t) const { return 0; }
+    template <typename V> NH_DEV V vec(const V &v, int, int64_t) const { return v; }
     template <typename T> NH_DEV T one(T x, int64_t) const { return x; }
 };
 
@@ -120,12 +155,15 @@ struct NoPre {
 // the fused producers use it to compute and store a value and reduce it in the
 // same pass.  The walk order does not depend on Red or Pre, so a fused
 // reduction accumulates exactly what the stand-alone one does.
+// `first` (optional) receives the first value the lane walked: for the
+// group's lane 0 that is element lo (after the prologue).
 template <typename T, class Red, int TPR, bool NT, class Pre = NoPre>
 NH_DEV typename Red::L seg_walk(const Red &red, const T *__restrict__ row, int64_t lo, int64_t hi, bool vec,
-                                const Pre &pre = Pre{})
+                                const Pre &pre = Pre{}, T *first = nullptr)
 {
     using L = typename Red::L;
     using G = Grp<TPR>;
+    constexpr bool kRel = RelIndex<Red>::value;
     L st = red.linit();
     const int lane = G::lane();
     int64_t tail = lo;
@@ -136,6 +174,7 @@ NH_DEV typename Red::L seg_walk(const Red &red, const T *__restrict__ row, int64
         const int64_t v0 = lo / VN, v1 = hi / VN;
         for (int64_t c = v0 + lane; c < v1; c += int64_t(TPR) * kRUnroll) {
             V r[kRUnroll];
+            decltype(pre.load(0)) aux[kRUnroll];
 #pragma unroll
             for (int u = 0; u < kRUnroll; u++) {
                 const int64_t i = c + int64_t(u) * TPR;
@@ -145,30 +184,59 @@ NH_DEV typename Red::L seg_walk(const Red &red, const T *__restrict__ row, int64
 #pragma unroll
                 for (int u = 0; u < kRUnroll; u++) {
                     const int64_t i = c + int64_t(u) * TPR;
-                    if (i < v1) r[u] = pre.vec(r[u], i);
+                    if (i < v1) aux[u] = pre.load(i);
+                }
+#pragma unroll
+                for (int u = 0; u < kRUnroll; u++) {
+                    const int64_t i = c + int64_t(u) * TPR;
+                    if (i < v1) r[u] = pre.vec(r[u], aux[u], i);
                 }
             }
+            if (first && c == v0 + lane) *first = r[0][0];
+            const int32_t rb = kRel ? int32_t(c - v0) * VN : 0;  // lo is a multiple of VN here
 #pragma unroll
             for (int u = 0; u < kRUnroll; u++) {
                 const int64_t i = c + int64_t(u) * TPR;
                 if (i < v1) {
 #pragma unroll
-                    for (int k = 0; k < VN; k++) red.lacc(st, r[u][k], i * VN + k);
+                    for (int k = 0; k < VN; k++) {
+                        if constexpr (kRel) red.lacc(st, r[u][k], rb + (u * TPR * VN + k));
+                        else red.lacc(st, r[u][k], i * VN + k);
+                    }
                 }
             }
         }
         tail = v1 * VN > lo ? v1 * VN : lo;
     }
-    for (int64_t j = tail + lane; j < hi; j += TPR) red.lacc(st, pre.one(row[j], j), j);
+    for (int64_t j = tail + lane; j < hi; j += TPR) {
+        const T x = pre.one(row[j], j);
+        if (first && j == tail + lane && tail == lo) *first = x;
+        red.lacc(st, x, kRel ? j - lo : j);
+    }
     return G::reduce(st, [&](const L &a, const L &b) { return red.lcomb(a, b); });
 }
 
-// Reduce row elements [lo, hi) to the segment summary.
+// Reduce row elements [lo, hi) to the segment summary (`first`: see seg_walk).
 template <typename T, class Red, int TPR, bool NT>
-NH_DEV typename Red::B seg_reduce(const Red &red, const T *__restrict__ row, int64_t lo, int64_t hi, bool vec)
+NH_DEV typename Red::B seg_reduce(const Red &red, const T *__restrict__ row, int64_t lo, int64_t hi, bool vec,
+                                  T *first = nullptr)
 {
-    return red.template finish<TPR>(seg_walk<T, Red, TPR, NT>(red, row, lo, hi, vec), row, lo, hi);
+    return red.template finish<TPR>(seg_walk<T, Red, TPR, NT>(red, row, lo, hi, vec, NoPre{}, first), row, lo, hi);
 }
+
+// Reducers whose store() reads only element 0 of the row (argmax: x0 NaN
+// gives index 0) declare kStoreReadsFirst; the row kernels then hand them the
+// value their lane 0 walked first instead of a pointer, so no lane waits on a
+// load of row[0] after the reduction.
+template <class Red, typename = void> struct StoreReadsFirst { static constexpr bool value = false; };
+template <class Red> struct StoreReadsFirst<Red, std::void_t<decltype(Red::kStoreReadsFirst)>> {
+    static constexpr bool value = Red::kStoreReadsFirst;
+};
+template <typename T>
+struct FirstOnly {
+    T v;
+    NH_DEV T operator[](int64_t) const { return v; }
+};
 
 // Ordered combine of n segment summaries p[0..n) by one block; result valid
 // in thread 0.  Each thread folds a contiguous run, then an ordered tree
@@ -234,10 +302,19 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_rows(const T *__restrict__ x
         // default-policy loads: in a sequence (bias add, then several row
         // reductions of its result, then other streams) this measured faster
         // for the whole sequence than non-temporal ones
-        const typename Red::B b = seg_reduce<T, Red, TPR, false>(red, xr, 0, cols, vec);
-        if (Grp<TPR>::lane() == 0) {
-            red.store(out, r, b, xr, cols);
-            publish(tk);  // tickets are used with a single row only
+        if constexpr (StoreReadsFirst<Red>::value) {
+            T x0 = T(0);
+            const typename Red::B b = seg_reduce<T, Red, TPR, false>(red, xr, 0, cols, vec, &x0);
+            if (Grp<TPR>::lane() == 0) {
+                red.store(out, r, b, FirstOnly<T>{x0}, cols);
+                publish(tk);  // tickets are used with a single row only
+            }
+        } else {
+            const typename Red::B b = seg_reduce<T, Red, TPR, false>(red, xr, 0, cols, vec);
+            if (Grp<TPR>::lane() == 0) {
+                red.store(out, r, b, xr, cols);
+                publish(tk);  // tickets are used with a single row only
+            }
         }
     }
 }
@@ -332,6 +409,7 @@ int launch_reduce(const T *x, int64_t rows, int64_t cols, int64_t ld, const Red 
     const bool vec = ((reinterpret_cast<uintptr_t>(x) & 15u) == 0) && ((ld * int64_t(sizeof(T))) % 16 == 0);
     const ReducePlan plan = reduce_plan<T>(rows, cols);
     const int64_t gx = plan.gx, chunk = plan.chunk;
+    if (RelIndex<Red>::value && chunk >= (int64_t(1) << 31)) return set_error(NEURAL_ERR_TENSOR_TOO_LARGE);
     if (gx > 1) {
         if (scratch && size_t(gx * rows) * sizeof(typename Red::B) > scratch_bytes)
             return set_error(NEURAL_ERR_TENSOR_TOO_LARGE);
