@@ -50,6 +50,32 @@ NH_DEV bool loss_target(const int64_t *ti, const T *tv, int64_t r, int64_t cols,
 // within 1e-5.  Exact-difference double range reduction was measured ~20%
 // slower for the tensor loss kernel.
 NH_DEV double row_exp_d(double x, double m) { return exp(x - m); }
+
+// e^y for the one-wave-per-row forward's f64 rows, from a 64-entry table of
+// 2^(j/64) that each block keeps in LDS: y = (64 k + j) ln2 / 64 + r with
+// |r| <= ln2 / 128, e^r by its Taylor polynomial through r^5 (truncation
+// below 4e-17 relative), scaled by 2^k with ldexp (exact, or rounded once
+// into the denormal range).  About 3 ulp against the device library's ~1,
+// in 17 instructions instead of ~24: the 1e-12 bars of the losses and
+// gradients are 3e3 times wider.  y below -1100 is taken as -1100 (e^y is 0
+// either way), +inf and overflow give +inf, a NaN stays NaN (through r).
+constexpr double kLn2_64Hi = kLn2Hi / 64.0;  // n * kLn2_64Hi exact for |n| < 2^20
+constexpr double kLn2_64Lo = kLn2Lo / 64.0;
+NH_DEV double exp_tab(double y, const double *tab)
+{
+    y = y < -1100.0 ? -1100.0 : y;  // NaN compares false and stays
+    const double n = __builtin_rint(y * 92.332482616893658);  // 64 / ln 2
+    double r = __builtin_fma(-n, kLn2_64Hi, y);
+    r = __builtin_fma(-n, kLn2_64Lo, r);
+    const int ni = int(n);  // |n| <= 2^17 for finite y <= 1100; a NaN's r carries it
+    double p = 1.0 / 120.0;
+    p = __builtin_fma(p, r, 1.0 / 24.0);
+    p = __builtin_fma(p, r, 1.0 / 6.0);
+    p = __builtin_fma(p, r, 0.5);
+    p = __builtin_fma(p, r, 1.0);
+    p = __builtin_fma(p, r, 1.0);
+    return __builtin_ldexp(tab[ni & 63] * p, ni >> 6);  // 2^floor(n / 64); beyond 2^1023: +inf
+}
 NH_DEV double row_exp_f(float x, double m)
 {
     return double(__builtin_amdgcn_exp2f((x - float(m)) * 1.4426950408889634f));
@@ -107,6 +133,16 @@ __global__ __launch_bounds__(256) void k_ce_wave(const T *__restrict__ x, CeArgs
     using V = typename Vec16<T>::type;
     constexpr int VN = Vec16<T>::n;
     const int lane = threadIdx.x & 63;
+    // The f64 forward takes exp_tab (2^(j/64) by the device library's exp2,
+    // in LDS): 85-90 -> 84-87 us at [65536,1024] (A/B in one run).  The modes
+    // that keep every e for the gradient keep the library's exp: with the
+    // table their longer-lived registers made the fused pass 177 -> 182 us.
+    constexpr bool kTab = sizeof(T) == 8 && MODE == CE_LS_FWD;
+    __shared__ double etab[kTab ? 64 : 1];
+    if constexpr (kTab) {
+        if (threadIdx.x < 64) etab[threadIdx.x] = exp2(double(threadIdx.x) * (1.0 / 64.0));
+        __syncthreads();
+    }
     const int64_t r = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
     if (r >= a.rows) return;  // uniform per wave
     const int64_t cols = a.cols;
@@ -150,7 +186,8 @@ __global__ __launch_bounds__(256) void k_ce_wave(const T *__restrict__ x, CeArgs
 #pragma unroll
         for (int j = 0; j < VN; j++)
             if (FULL || c0 + j < cols) {
-                const double e = sizeof(T) == 8 ? row_exp_d(double(v[k][j]), m) : row_exp_f(float(v[k][j]), m);
+                const double e = kTab ? exp_tab(double(v[k][j]) - m, etab)
+                                      : (sizeof(T) == 8 ? row_exp_d(double(v[k][j]), m) : row_exp_f(float(v[k][j]), m));
                 if constexpr (KEEP) ev[k][j] = T(e);
                 if constexpr (MODE == CE_ASM) et = c0 + j == t ? Acc(e) : et;
                 sl += Acc(e);
