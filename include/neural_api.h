@@ -584,6 +584,11 @@ int   neural_hip_time_cancel(void);
  * calling thread has made so far (the difference around a call is the number
  * of launches the call makes). */
 unsigned long long neural_hip_launch_count(void);
+/* NEW (no reference counterpart; diagnostics): device allocations the
+ * library has requested so far from its caching allocator (every request)
+ * and, among them, those that called hipMalloc (cache misses); either
+ * pointer may be NULL.  Process-wide counts. */
+int   neural_hip_alloc_stats(unsigned long long *dev_allocs, unsigned long long *hip_mallocs);
 /* NEW (no reference counterpart; a bandwidth reference for measurement):
  * dst = src over `bytes` bytes with the library's flat streaming kernel
  * (16-byte non-temporal loads and stores).  Device pointers only, 16-byte

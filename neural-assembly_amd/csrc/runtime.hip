@@ -5,6 +5,7 @@
 // messages) and the tensor exports of neural_api.asm:297-967,2293-2426.
 // Tensor bytes live in HBM; the host copy is a mirror synchronised at
 // neural_tensor_data() (see the memory-model note in include/neural_api.h).
+#include <atomic>
 #include <cstdio>
 #include <cstdlib>
 #include <map>
@@ -152,8 +153,13 @@ hipStream_t stream() { return R().active; }
 int num_cus() { return R().cus; }
 Workspace &workspace() { return R().ws; }
 
+// Allocation counters for neural_hip_alloc_stats: every dev_alloc call, and
+// the hipMalloc calls among them (cache misses).
+static std::atomic<unsigned long long> g_dev_allocs{0}, g_hip_mallocs{0};
+
 void *dev_alloc(size_t bytes)
 {
+    g_dev_allocs.fetch_add(1, std::memory_order_relaxed);
     Runtime &r = R();
     const size_t cls = size_class(bytes);
     std::lock_guard<std::mutex> g(r.mu);
@@ -165,6 +171,7 @@ void *dev_alloc(size_t bytes)
         return p;
     }
     void *p = nullptr;
+    g_hip_mallocs.fetch_add(1, std::memory_order_relaxed);
     if (hipMalloc(&p, cls) != hipSuccess) {
         (void)hipGetLastError();
         // Give cached blocks back and retry once; outstanding work may still
@@ -993,6 +1000,13 @@ int neural_hip_time_cancel(void)
 }
 
 unsigned long long neural_hip_launch_count(void) { return t_launches; }
+
+int neural_hip_alloc_stats(unsigned long long *dev_allocs, unsigned long long *hip_mallocs)
+{
+    if (dev_allocs) *dev_allocs = g_dev_allocs.load(std::memory_order_relaxed);
+    if (hip_mallocs) *hip_mallocs = g_hip_mallocs.load(std::memory_order_relaxed);
+    return set_error(NEURAL_OK);
+}
 
 void *neural_hip_get_stream(void)
 {

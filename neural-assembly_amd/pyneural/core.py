@@ -286,6 +286,7 @@ _SIGS = {
     "neural_hip_time_next_launch": (_i, [_vp, _vp, _i]),
     "neural_hip_time_launches": (_i, [_vp, _vp, _i, _i]),
     "neural_hip_launch_count": (ctypes.c_ulonglong, []),
+    "neural_hip_alloc_stats": (_i, [ctypes.POINTER(ctypes.c_ulonglong), ctypes.POINTER(ctypes.c_ulonglong)]),
     "neural_hip_stream_copy": (_i, [_vp, _vp, _u64]),
     "neural_hip_time_cancel": (_i, []),
     "neural_hip_reset_stream": (_i, []),

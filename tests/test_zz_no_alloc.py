@@ -26,6 +26,13 @@ def _bytes(t):
     return b[0:12] + b[16:36]
 
 
+def _alloc_stats(lib):
+    """(allocator requests, hipMalloc calls) the library has made so far."""
+    a, m = ctypes.c_ulonglong(), ctypes.c_ulonglong()
+    assert lib.neural_hip_alloc_stats(ctypes.byref(a), ctypes.byref(m)) == 0
+    return a.value, m.value
+
+
 @pytest.mark.parametrize("sym", [1, 0])
 def test_noalloc_matches_allocating_entry_point(pn, sym):
     import torch
@@ -44,8 +51,11 @@ def test_noalloc_matches_allocating_entry_point(pn, sym):
         want, got = _params_dev(torch), _params_dev(torch)
         got.fill_(np.nan)
         assert lib.calibrate_minmax_f32_dev(x.data_ptr(), n, sym, want.data_ptr()) == 0
+        torch.cuda.synchronize()
+        before = _alloc_stats(lib)
         assert lib.calibrate_minmax_f32_dev_noalloc(x.data_ptr(), n, sym, got.data_ptr()) == 0
         torch.cuda.synchronize()
+        assert _alloc_stats(lib) == before, f"the allocation-free entry point allocated (n = {n})"
         assert _bytes(got) == _bytes(want), (n, sym, got.cpu(), want.cpu())
     # a second round over the same sizes in reverse order: the buffer holds the
     # previous (smaller) call's summaries
