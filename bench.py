@@ -24,7 +24,12 @@ brackets the whole op, gaps included.  Each figure is the median of 20 such
 pairs.  Ops whose result returns to the host (neural_sum, neural_argmax, the
 NaN/Inf/L2 scan) are also timed per call on the host clock (launch, kernels,
 host wait, return).  A float4 streaming copy measured in the same run gives
-the achievable 1:1 stream rate; every op also carries its % of it.
+the achievable 1:1 stream rate; every op also carries its % of it.  Outside
+the step, an op whose footprint is below 1 GiB cycles over NROT copies of its
+inputs and outputs from one timed call to the next, so that the 256 MB
+memory-side cache cannot serve re-reads or absorb rewrites; the step keeps the
+reference's one set of buffers, and the same step with its outputs rotating
+is reported beside it.
 
 CPU baselines, one thread (the reference never dispatches to its thread pool):
   cfg2  the oracle's C restatement of the whole step (port);
@@ -78,6 +83,15 @@ N_SIMD = 256 * 4
 # clocks take some milliseconds to settle: on one box f64 tanh ran 193-216 us
 # per launch in the first ~10 ms of FP64 work and 171-175 us after it.
 WARM_MS = 20.0
+# Buffer sets an op cycles through from one timed call to the next.  The GPU's
+# 256 MB memory-side cache (MALL) serves part of a re-read and absorbs
+# rewrites of data touched by the previous call: a row sum of one 268 MB
+# [16384,4096] input read it 9% faster than over four rotating inputs, and a
+# bias add rewriting one output took 77 us against 88 us over four outputs.
+# Every timed op whose footprint is below 1 GiB therefore rotates over NROT
+# copies of its inputs and outputs, so that at least (NROT - 1) x its
+# footprint of other traffic (>= 800 MB here) separates two uses of a buffer.
+NROT = 4
 
 
 def parse():
@@ -240,6 +254,24 @@ def pct(nbytes, us):
 
 
 COPY = {}  # the same-run float4 copy: {"GBps": ..} (filled by measure_copy_peak)
+
+
+class Rot:
+    """A call that runs the next of several equivalent calls each time (the
+    same op over NROT buffer sets, in turn)."""
+
+    def __init__(self, fns):
+        self.fns, self.k = list(fns), 0
+
+    def __call__(self):
+        f = self.fns[self.k]
+        self.k = (self.k + 1) % len(self.fns)
+        return f()
+
+
+def copies(t, n=NROT):
+    """t and n - 1 device copies of it."""
+    return [t] + [t.clone() for _ in range(n - 1)]
 
 
 def pct_copy(gbps):
@@ -429,6 +461,7 @@ def main():
 
     fused = fused_step(torch, _lib, clock, stream, T, ridx, step_ops, args, ms_per_step, n1)
     yres = y_residency(torch, pn, _lib, clock, Y, step_ops)
+    rot_us = rotating_step(torch, pn, _lib, stream, T, ridx, args)
 
     cpu2 = None
     if not args.no_cpu:
@@ -457,6 +490,9 @@ def main():
             "kernel_sum_us": round(kernel_sum_us, 1),
             "fused_step": fused,
             "y_residency": yres,
+            "step_outputs_rotating": {"us_per_step": round(rot_us, 1),
+                                      "GBps": round(gbs(step_bytes, rot_us), 1),
+                                      "note": f"the same step with Y, P and L rotating over {NROT} buffers each"},
             "copy_peak": COPY,
         },
         "roofline": {
@@ -509,23 +545,26 @@ def measure_copy_peak(torch, lib, clock, dev):
     """The library's float4 streaming copy (neural_hip_stream_copy: the flat
     kernels' tiling, 16-byte non-temporal loads and stores) of 256 MiB (cfg1's
     64M f32, cfg2's softmax input) and of 1 GiB into a second buffer: the
-    achievable rate of a 1:1 read/write stream in this run.  The faster of the
-    two is the reference every op's pct_of_copy refers to."""
+    achievable rate of a 1:1 read/write stream in this run (the 256 MiB copy
+    over NROT source / destination pairs, like the ops it is compared with).
+    The faster of the two is the reference every op's pct_of_copy refers to."""
     res = {}
-    for n in (1 << 26, 1 << 28):
-        src = torch.empty(n, device=dev).uniform_()
-        dst = torch.empty_like(src)
+    for n, nrot in ((1 << 26, NROT), (1 << 28, 1)):
+        srcs = copies(torch.empty(n, device=dev).uniform_(), nrot)
+        dsts = [torch.empty_like(srcs[0]) for _ in range(nrot)]
         torch.cuda.synchronize()
-        f = lambda: lib.neural_hip_stream_copy(ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(src.data_ptr()),
-                                               4 * n)  # noqa: E731
-        if f() != 0:
-            raise RuntimeError("neural_hip_stream_copy failed")
+        f = Rot([lambda d=d, s_=s_: lib.neural_hip_stream_copy(ctypes.c_void_p(d.data_ptr()),
+                                                               ctypes.c_void_p(s_.data_ptr()), 4 * n)
+                 for d, s_ in zip(dsts, srcs)])
+        for _ in range(nrot):
+            if f() != 0:
+                raise RuntimeError("neural_hip_stream_copy failed")
         us = clock.kernel_us(f)
         torch.cuda.synchronize()
-        if not torch.equal(src, dst):
+        if not all(torch.equal(a, b) for a, b in zip(srcs, dsts)):
             raise RuntimeError("stream copy: destination differs from source")
         res[f"{4 * n >> 20}MiB"] = {"us": round(us, 2), "GBps": round(gbs(8 * n, us), 1), "pct_hbm": pct(8 * n, us)}
-        del src, dst
+        del srcs, dsts, f
         torch.cuda.empty_cache()
     best = max(res.values(), key=lambda r: r["GBps"])
     COPY.update({"kernel": "k_map1_flat<float, FnCopy>, median of %d launches" % REPS, "sizes": res,
@@ -577,6 +616,42 @@ def y_residency(torch, pn, lib, clock, Y, step_ops, reps=REPS):
     del ts, tso, tys, tyso, scrub, scrub_out, ys_out
     torch.cuda.empty_cache()
     return res
+
+
+def rotating_step(torch, pn, lib, stream, T, ridx, args):
+    """Microseconds per cfg2 step with its outputs Y, P and L rotating over
+    NROT buffers each (the timed steps reuse one set, as the reference's loop
+    does): whether the memory-side cache carries any output from one step to
+    the next shows as a difference between the two."""
+    W = pn.Tensor.from_torch
+    X, S = T["X"], T["S"]
+    ys = [W(torch.empty(ROWS, COLS, device="cuda")) for _ in range(NROT)]
+    ps = [W(torch.empty(SROWS, SCOLS, device="cuda")) for _ in range(NROT)]
+    ls = [W(torch.empty(SROWS, SCOLS, device="cuda")) for _ in range(NROT)]
+    torch.cuda.synchronize()
+
+    def step(k):
+        y = ys[k % NROT]._ptr
+        for rc in (lib.neural_bias_add(y, X._ptr, T["b"]._ptr), lib.neural_reduce_sum(y, 1, T["rsum"]._ptr),
+                   lib.neural_reduce_mean(y, 1, T["rmean"]._ptr), lib.neural_reduce_max(y, 1, T["rmax"]._ptr),
+                   lib.neural_reduce_argmax(y, 1, ctypes.c_void_p(ridx.data_ptr())),
+                   lib.neural_softmax(ps[k % NROT]._ptr, S._ptr), lib.neural_log_softmax(ls[k % NROT]._ptr, S._ptr)):
+            if rc != 0:
+                raise RuntimeError("rotating step: a call failed")
+
+    for k in range(args.warmup):
+        step(k)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for k in range(args.steps):
+        step(k)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    us = 1e3 * t0.elapsed_time(t1) / args.steps
+    del ys, ps, ls
+    torch.cuda.empty_cache()
+    return us
 
 
 def fused_step(torch, lib, clock, stream, T, ridx, step_ops, args, ms_per_step, n1):
@@ -668,17 +743,31 @@ def _cfg1(torch, pn, lib, clock, dev, g, cpu_on, out, detail):
     one = torch.empty(1, device=dev)
     one_i = torch.empty(1, dtype=torch.int64, device=dev)
     torch.cuda.synchronize()
+    # the 64M arrays rotate over NROT copies (3.2 GB); the 1M case is the
+    # cache-resident one and keeps one set
+    a_s, b_s, c_s = copies(a), copies(bb), [c] + [torch.empty_like(c) for _ in range(NROT - 1)]
+    torch.cuda.synchronize()
     for n, key in ((N1, "cfg1"), (N1_SMALL, "cfg1_1M")):
-        ta, tb, tc = W(a[:n]), W(bb[:n]), W(c[:n])
+        nset = NROT if n == N1 else 1
+        ta = [W(x[:n]) for x in a_s[:nset]]
+        tb = [W(x[:n]) for x in b_s[:nset]]
+        tc = [W(x[:n]) for x in c_s[:nset]]
         to = W(one)
         t1 = W(a[:1])
         cf = Config(key, f"cfg1: f32 add, mul, ReLU, full sum, max over {n:,} elements U[-1,1]"
-                    + (" (256 MiB MALL holds it: cache-resident, reported not judged)" if n < N1 else ""))
-        ops = [("add", "k_map2_flat", 12 * n, lambda: lib.neural_add(tc._ptr, ta._ptr, tb._ptr)),
-               ("mul", "k_map2_flat", 12 * n, lambda: lib.neural_mul(tc._ptr, ta._ptr, tb._ptr)),
-               ("relu", "k_map1_flat", 8 * n, lambda: lib.neural_relu(tc._ptr, ta._ptr)),
-               ("sum", "k_reduce_seg + k_reduce_combine", 4 * n, lambda: lib.neural_reduce_sum(ta._ptr, -1, to._ptr)),
-               ("max", "k_reduce_seg + k_reduce_combine", 4 * n, lambda: lib.neural_reduce_max(ta._ptr, -1, to._ptr))]
+                    + (" (256 MiB MALL holds it: cache-resident, reported not judged)" if n < N1
+                       else f" ({NROT} rotating buffer sets)"))
+
+        def rot(call):
+            return Rot([lambda k=k: call(k) for k in range(nset)])
+
+        ops = [("add", "k_map2_flat", 12 * n, rot(lambda k: lib.neural_add(tc[k]._ptr, ta[k]._ptr, tb[k]._ptr))),
+               ("mul", "k_map2_flat", 12 * n, rot(lambda k: lib.neural_mul(tc[k]._ptr, ta[k]._ptr, tb[k]._ptr))),
+               ("relu", "k_map1_flat", 8 * n, rot(lambda k: lib.neural_relu(tc[k]._ptr, ta[k]._ptr))),
+               ("sum", "k_reduce_seg + k_reduce_combine", 4 * n,
+                rot(lambda k: lib.neural_reduce_sum(ta[k]._ptr, -1, to._ptr))),
+               ("max", "k_reduce_seg + k_reduce_combine", 4 * n,
+                rot(lambda k: lib.neural_reduce_max(ta[k]._ptr, -1, to._ptr)))]
         for name, kern, nbytes, fn in ops:
             k, o, nl = clock.op(fn)
             cf.add(name, kern, nbytes, n, k, o, nl)
@@ -687,8 +776,8 @@ def _cfg1(torch, pn, lib, clock, dev, g, cpu_on, out, detail):
             # whole call on the host clock, result in host memory
             r = ctypes.c_double()
             idx = ctypes.c_int64()
-            s_fn = lambda: lib.neural_sum(ta._ptr, ctypes.byref(r))  # noqa: E731
-            a_fn = lambda: lib.neural_argmax(ta._ptr, ctypes.byref(idx))  # noqa: E731
+            s_fn = rot(lambda k: lib.neural_sum(ta[k]._ptr, ctypes.byref(r)))
+            a_fn = rot(lambda k: lib.neural_argmax(ta[k]._ptr, ctypes.byref(idx)))
             for name, fn in (("neural_sum", s_fn), ("neural_argmax", a_fn)):
                 k, o, nl = clock.op(fn)
                 cf.add(name, "k_reduce_seg + k_reduce_combine (result to the host)", 4 * n, n, k, o, nl,
@@ -706,7 +795,7 @@ def _cfg1(torch, pn, lib, clock, dev, g, cpu_on, out, detail):
             if cpu:
                 detail[key]["cpu"] = cpu
         del ta, tb, tc, to, t1
-    del a, bb, c, one, one_i
+    del a, bb, c, one, one_i, a_s, b_s, c_s
     torch.cuda.empty_cache()
 
 
@@ -721,17 +810,20 @@ def _cfg3(torch, pn, lib, clock, dev, g, cpu_on, out, detail):
     del sat
     for dt_name, tdt, bpe in (("f32", torch.float32, 8), ("f64", torch.float64, 16)):
         xx = x4.to(tdt).contiguous()
-        yy = torch.empty_like(xx)
-        tx, ty = W(xx), W(yy)
+        xs = copies(xx)
+        ys = [torch.empty_like(xx) for _ in range(NROT)]
+        tx, ty = [W(t) for t in xs], [W(t) for t in ys]
         torch.cuda.synchronize()
         key = f"cfg3_{dt_name}"
-        cf = Config(key, f"cfg3: ten activations on [64,64,128,128] {dt_name}, N(0,4) with 1% at +-30")
+        cf = Config(key, f"cfg3: ten activations on [64,64,128,128] {dt_name}, N(0,4) with 1% at +-30 "
+                         f"({NROT} rotating buffer sets)")
         for nm in ACTS:
             fn_c = getattr(lib, "act_" + nm)
             if nm in ACT_ALPHA:
-                f = (lambda fn_c=fn_c, al=ACT_ALPHA[nm]: fn_c(ty._ptr, tx._ptr, ctypes.c_double(al)))
+                f = Rot([lambda fn_c=fn_c, al=ACT_ALPHA[nm], k=k: fn_c(ty[k]._ptr, tx[k]._ptr, ctypes.c_double(al))
+                         for k in range(NROT)])
             else:
-                f = (lambda fn_c=fn_c: fn_c(ty._ptr, tx._ptr))
+                f = Rot([lambda fn_c=fn_c, k=k: fn_c(ty[k]._ptr, tx[k]._ptr) for k in range(NROT)])
             cf.add(nm, "k_map1_flat / k_map1_f32_tail" if dt_name == "f32" else "k_map1_flat", bpe * ne, ne,
                    clock.kernel_us(f))
         cpu = cpu_cfg3(xx, dt_name, bpe) if cpu_on else None
@@ -741,7 +833,7 @@ def _cfg3(torch, pn, lib, clock, dev, g, cpu_on, out, detail):
         detail[key] = cf.detail()
         if cpu:
             detail[key]["cpu"] = cpu
-        del xx, yy, tx, ty
+        del xx, xs, ys, tx, ty
     del x4
     torch.cuda.empty_cache()
 
@@ -836,10 +928,16 @@ def _cfg5(torch, pn, lib, clock, dev, g, cpu_on, out, detail):
     gr[inj[64:]] = float("-inf")
     del inj
     tp, tg, tcl = W(p), W(gr), W(clean)
+    # the scan (400 MB) rotates over three copies of the gradient; AdamW moves
+    # 4.4 GB per call and keeps one set
+    gs = copies(gr, 3)
+    tgs = [tg] + [W(x) for x in gs[1:]]
     torch.cuda.synchronize()
-    cf = Config("cfg5", "cfg5: fused NaN/Inf/L2 scan + AdamW (lr 1e-3, wd 0.01) over 100M f32, f64 m/v")
+    cf = Config("cfg5", "cfg5: fused NaN/Inf/L2 scan (3 rotating copies) + AdamW (lr 1e-3, wd 0.01) over 100M f32, "
+                        "f64 m/v")
     hn, hi, ss = ctypes.c_int(), ctypes.c_int(), ctypes.c_double()
-    scan = lambda: lib.neural_tensor_scan(tg._ptr, ctypes.byref(hn), ctypes.byref(hi), ctypes.byref(ss))  # noqa: E731
+    scan = Rot([lambda t=t: lib.neural_tensor_scan(t._ptr, ctypes.byref(hn), ctypes.byref(hi), ctypes.byref(ss))
+                for t in tgs])
     cf.add("scan", "k_reduce_seg + k_reduce_combine (flags + sum of squares to the host)", 4 * NA, NA,
            *clock.op(scan), host_call_us=clock.host_call_us(scan))
     flags = (hn.value, hi.value)
@@ -854,7 +952,7 @@ def _cfg5(torch, pn, lib, clock, dev, g, cpu_on, out, detail):
     if cpu:
         detail["cfg5"]["cpu"] = cpu
     out["cfg5"]["host_e2e"] = host_e2e_cfg5(torch, pn, lib, tg)
-    del p, gr, clean, tp, tg, tcl, opt
+    del p, gr, clean, tp, tg, tcl, opt, gs, tgs
     torch.cuda.empty_cache()
 
 
@@ -1133,7 +1231,9 @@ def suite(torch, pn, clock, dev, cpu=True):
     sample (SUITE_CPU_SAMPLE elements, rows of it for the row ops) of the same
     input: the reference's own C (oracle/_ref, kind "reference") where it
     compiles, else the oracle's restatement of the reference loop ("port");
-    the oracle allocates each output, which those timings include."""
+    the oracle allocates each output, which those timings include.  Inputs and
+    outputs of ops whose footprint is below 1 GiB rotate over copies (NROT, or
+    2-3 for the larger ones) between timed calls."""
     from pyneural.core import _lib, QuantParamsC
     W = pn.Tensor.from_torch
     res = {}
@@ -1162,19 +1262,27 @@ def suite(torch, pn, clock, dev, cpu=True):
     R, C = 16384, 4096
     X = torch.randn(R, C, device=dev, generator=g) * 3
     bias = torch.randn(C, device=dev, generator=g) * 3
-    Y = torch.empty_like(X)
+    Xs = copies(X)
+    Ys = [torch.empty_like(X) for _ in range(NROT)]
     rs = torch.empty(R, device=dev)
     ri = torch.empty(R, dtype=torch.int64, device=dev)
-    tX, tb, tY, trs = W(X), W(bias), W(Y), W(rs)
+    tX, tY, tb, trs = [W(t) for t in Xs], [W(t) for t in Ys], W(bias), W(rs)
     torch.cuda.synchronize()
-    put("bias_add_f32_16384x4096", 8 * R * C, clock.kernel_us(lambda: _lib.neural_bias_add(tY._ptr, tX._ptr, tb._ptr)))
+
+    def rot(call, nset=NROT):
+        return Rot([lambda k=k: call(k) for k in range(nset)])
+
+    put("bias_add_f32_16384x4096", 8 * R * C,
+        clock.kernel_us(rot(lambda k: _lib.neural_bias_add(tY[k]._ptr, tX[k]._ptr, tb._ptr))))
     for nm, act in (("relu", 1), ("gelu", 4)):
-        put(f"bias_add_{nm}_f32_16384x4096", 8 * R * C, clock.kernel_us(
-            lambda act=act: _lib.neural_bias_add_act(tY._ptr, tX._ptr, tb._ptr, act, ctypes.c_double(0.0))))
-    put("row_sum_f32_16384x4096", 4 * R * C, clock.kernel_us(lambda: _lib.neural_reduce_sum(tY._ptr, 1, trs._ptr)))
-    put("row_max_f32_16384x4096", 4 * R * C, clock.kernel_us(lambda: _lib.neural_reduce_max(tY._ptr, 1, trs._ptr)))
+        put(f"bias_add_{nm}_f32_16384x4096", 8 * R * C, clock.kernel_us(rot(
+            lambda k, act=act: _lib.neural_bias_add_act(tY[k]._ptr, tX[k]._ptr, tb._ptr, act, ctypes.c_double(0.0)))))
+    put("row_sum_f32_16384x4096", 4 * R * C,
+        clock.kernel_us(rot(lambda k: _lib.neural_reduce_sum(tY[k]._ptr, 1, trs._ptr))))
+    put("row_max_f32_16384x4096", 4 * R * C,
+        clock.kernel_us(rot(lambda k: _lib.neural_reduce_max(tY[k]._ptr, 1, trs._ptr))))
     put("row_argmax_f32_16384x4096", 4 * R * C,
-        clock.kernel_us(lambda: _lib.neural_reduce_argmax(tY._ptr, 1, ri.data_ptr())))
+        clock.kernel_us(rot(lambda k: _lib.neural_reduce_argmax(tY[k]._ptr, 1, ri.data_ptr()))))
     if cpu:
         rows = SUITE_CPU_SAMPLE // C
         Xh, bh = X[:rows].cpu().numpy(), bias.cpu().numpy()
@@ -1188,21 +1296,24 @@ def suite(torch, pn, clock, dev, cpu=True):
         cpu_leg("row_sum_f32_16384x4096", 4 * Yh.size, lambda: ora.rowsum_ref(Yh), "port", smp)
         cpu_leg("row_max_f32_16384x4096", 4 * Yh.size, lambda: ora.rowmax_chain(Yh), "port", smp)
         cpu_leg("row_argmax_f32_16384x4096", 4 * Yh.size, lambda: ora.rowargmax(Yh), "port", smp)
-    del X, Y, tX, tY, rs, ri, trs
+    del X, Xs, Ys, tX, tY, rs, ri, trs
     torch.cuda.empty_cache()
 
     # ---- dropout forward / backward, 64M f32, p = 0.5 (the forward is two launches)
     n = N1
     a = torch.rand(n, device=dev, generator=g) * 2 - 1
-    c = torch.empty_like(a)
-    dmask = torch.empty(n, dtype=torch.uint8, device=dev)
+    a_s = copies(a)
+    c_s = [torch.empty_like(a) for _ in range(NROT)]
+    m_s = [torch.empty(n, dtype=torch.uint8, device=dev) for _ in range(NROT)]
     torch.cuda.synchronize()
-    fwd = lambda: _lib.neural_dropout_forward(a.data_ptr(), c.data_ptr(), dmask.data_ptr(), n, ctypes.c_float(0.5))
+    fwd = rot(lambda k: _lib.neural_dropout_forward(a_s[k].data_ptr(), c_s[k].data_ptr(), m_s[k].data_ptr(), n,
+                                                    ctypes.c_float(0.5)))
     put("dropout_fwd_keep_bits_f32_64M", 0, clock.kernel_us(fwd, skip=0))
     put("dropout_fwd_apply_f32_64M", 9 * n, clock.kernel_us(fwd, skip=1))
     put("dropout_fwd_f32_64M", 9 * n, None, clock.op(fwd)[1])
-    put("dropout_bwd_f32_64M", 9 * n, clock.kernel_us(
-        lambda: _lib.neural_dropout_backward(a.data_ptr(), c.data_ptr(), dmask.data_ptr(), n, ctypes.c_float(0.5))))
+    put("dropout_bwd_f32_64M", 9 * n, clock.kernel_us(rot(
+        lambda k: _lib.neural_dropout_backward(a_s[k].data_ptr(), c_s[k].data_ptr(), m_s[k].data_ptr(), n,
+                                               ctypes.c_float(0.5)))))
     if cpu:
         xh = a[:SUITE_CPU_SAMPLE].cpu().numpy()
         _, _, mh = ora.dropout_forward(xh, 0.5)
@@ -1210,7 +1321,7 @@ def suite(torch, pn, clock, dev, cpu=True):
         cpu_leg("dropout_fwd_f32_64M", 9 * xh.size, lambda: ora.dropout_forward(xh, 0.5), "port", smp)
         cpu_leg("dropout_bwd_f32_64M", 9 * xh.size, lambda: ora.dropout_backward(xh, mh, 0.5), "port",
                 f"first {xh.size:,} elements")
-    del a, c, dmask
+    del a, a_s, c_s, m_s
     torch.cuda.empty_cache()
 
     # ---- cross-entropy [65536,1024]: label-smoothed forward / fused (f64, f32), tensor CE loss (f32)
@@ -1219,8 +1330,10 @@ def suite(torch, pn, clock, dev, cpu=True):
     lossv = ctypes.c_double()
     L64 = torch.randn(B, K, device=dev, dtype=torch.float64, generator=g) * 3
     G64 = torch.empty_like(L64)
+    L64s = copies(L64, 2)  # the forward reads 537 MB per call: two copies
     torch.cuda.synchronize()
-    f = lambda: _lib.label_smoothing_ce_forward(L64.data_ptr(), tgt.data_ptr(), B, K, 0.1, ctypes.byref(lossv))
+    f = rot(lambda k: _lib.label_smoothing_ce_forward(L64s[k].data_ptr(), tgt.data_ptr(), B, K, 0.1,
+                                                      ctypes.byref(lossv)), 2)
     put("ls_ce_forward_f64_65536x1024", 8 * B * K, clock.kernel_us(f), clock.host_call_us(f))
     f = lambda: _lib.label_smoothing_ce_fused(L64.data_ptr(), tgt.data_ptr(), B, K, 0.1, ctypes.byref(lossv),
                                               G64.data_ptr())
@@ -1234,16 +1347,17 @@ def suite(torch, pn, clock, dev, cpu=True):
         cpu_leg("ls_ce_fused_f64_65536x1024", 16 * Lh.size,
                 lambda: (ora.ls_ce_forward(Lh, th, 0.1, use_ref=True), ora.ls_ce_backward(Lh, th, 0.1, use_ref=True)),
                 "reference", smp + ": forward, then backward")
-    del L64, G64
+    del L64, G64, L64s
     L32 = torch.randn(B, K, device=dev, generator=g) * 3
-    G32 = torch.empty_like(L32)
+    L32s = copies(L32)
+    G32s = [torch.empty_like(L32) for _ in range(NROT)]
     torch.cuda.synchronize()
-    f = lambda: _lib.label_smoothing_ce_fused_f32(L32.data_ptr(), tgt.data_ptr(), B, K, 0.1, ctypes.byref(lossv),
-                                                  G32.data_ptr())
+    f = rot(lambda k: _lib.label_smoothing_ce_fused_f32(L32s[k].data_ptr(), tgt.data_ptr(), B, K, 0.1,
+                                                        ctypes.byref(lossv), G32s[k].data_ptr()))
     put("ls_ce_fused_f32_65536x1024", 8 * B * K, clock.kernel_us(f), clock.host_call_us(f))
     tv = W(tgt.float())
-    tL = W(L32)
-    f = lambda: _lib.neural_cross_entropy_loss(tL._ptr, tv._ptr, ctypes.byref(lossv))
+    tL = [W(t) for t in L32s]
+    f = rot(lambda k: _lib.neural_cross_entropy_loss(tL[k]._ptr, tv._ptr, ctypes.byref(lossv)))
     put("ce_loss_f32_65536x1024", 4 * B * K, clock.kernel_us(f), clock.host_call_us(f))
     if cpu:
         rows = SUITE_CPU_SAMPLE // K
@@ -1255,28 +1369,32 @@ def suite(torch, pn, clock, dev, cpu=True):
                              "metrics_losses.c forward, then backward")
         tvh = th.astype("float32")
         cpu_leg("ce_loss_f32_65536x1024", 4 * Lh.size, lambda: ora.ce_loss(Lh, tvh), "port", f"first {rows} rows")
-    del L32, G32, tL, tv, tgt
+    del L32, L32s, G32s, tL, tv, tgt
     torch.cuda.empty_cache()
 
     # ---- gradient clipping over one 100M f32 gradient (norm: sum of squares,
     # decide, scale; each timed call clips by 0.999, so every call scales)
+    # three rotating copies (400 MB each): every copy is clipped in turn with
+    # a max_norm that keeps falling, so every timed call scales
     na = NA
     gr = torch.randn(na, device=dev, generator=g) * 1e-3
-    tg = W(gr)
-    glist = (ctypes.c_void_p * 1)(tg._ptr)
+    grs = copies(gr, 3)
+    tgs = [W(t) for t in grs]
+    glists = [(ctypes.c_void_p * 1)(t._ptr) for t in tgs]
     tot = ctypes.c_double()
     torch.cuda.synchronize()
-    _lib.neural_clip_grad_norm_list(glist, 1, ctypes.c_double(1e30), ctypes.byref(tot))
+    _lib.neural_clip_grad_norm_list(glists[0], 1, ctypes.c_double(1e30), ctypes.byref(tot))
     state = {"m": tot.value}
 
-    def clip_scaling():
+    def clip_scaling(k):
         state["m"] *= 0.999
-        return _lib.neural_clip_grad_norm_list(glist, 1, ctypes.c_double(state["m"]), ctypes.byref(tot))
+        return _lib.neural_clip_grad_norm_list(glists[k], 1, ctypes.c_double(state["m"]), ctypes.byref(tot))
 
-    put("clip_grad_norm_clipping_f32_100M", 12 * na, None, clock.host_call_us(clip_scaling))
-    put("clip_grad_norm_below_f32_100M", 4 * na, None, clock.host_call_us(
-        lambda: _lib.neural_clip_grad_norm_list(glist, 1, ctypes.c_double(1e30), ctypes.byref(tot))))
-    f = lambda: _lib.neural_clip_grad_value_list(glist, 1, ctypes.c_double(-1e-3), ctypes.c_double(1e-3))
+    put("clip_grad_norm_clipping_f32_100M", 12 * na, None, clock.host_call_us(rot(clip_scaling, 3)))
+    put("clip_grad_norm_below_f32_100M", 4 * na, None, clock.host_call_us(rot(
+        lambda k: _lib.neural_clip_grad_norm_list(glists[k], 1, ctypes.c_double(1e30), ctypes.byref(tot)), 3)))
+    f = rot(lambda k: _lib.neural_clip_grad_value_list(glists[k], 1, ctypes.c_double(-1e-3), ctypes.c_double(1e-3)),
+            3)
     put("clip_grad_value_f32_100M", 8 * na, clock.kernel_us(f), clock.op(f)[1])
     if cpu:
         gh = gr[:SUITE_CPU_SAMPLE].cpu().numpy()
@@ -1286,16 +1404,17 @@ def suite(torch, pn, clock, dev, cpu=True):
                 smp)
         cpu_leg("clip_grad_norm_below_f32_100M", 4 * gh.size, lambda: ora.clip_grad_norm([gh], 1e30), "port", smp)
         cpu_leg("clip_grad_value_f32_100M", 8 * gh.size, lambda: ora.clip_grad_value([gh], -1e-3, 1e-3), "port", smp)
-    del gr, tg
+    del gr, grs, tgs, glists
     torch.cuda.empty_cache()
 
     # ---- per-feature transforms, [1M, 64] f64, device pointers
     TB, TF = 1 << 20, 64
     D = torch.randn(TB, TF, device=dev, dtype=torch.float64, generator=g) * 2 + 1
+    Ds = copies(D, 2)  # the statistics read 537 MB per call: two copies
     O = torch.empty_like(D)
     st = [torch.empty(TF, device=dev, dtype=torch.float64) for _ in range(4)]
     torch.cuda.synchronize()
-    f = lambda: _lib.transform_compute_stats(D.data_ptr(), TB, TF, *[t.data_ptr() for t in st])
+    f = rot(lambda k: _lib.transform_compute_stats(Ds[k].data_ptr(), TB, TF, *[t.data_ptr() for t in st]), 2)
     put("transform_compute_stats_f64_1Mx64", 8 * TB * TF, clock.kernel_us(f), clock.op(f)[1])
     f = lambda: _lib.transform_normalize(D.data_ptr(), O.data_ptr(), TB, TF, st[0].data_ptr(), st[1].data_ptr(),
                                          ctypes.c_double(1e-8))
@@ -1308,22 +1427,24 @@ def suite(torch, pn, clock, dev, cpu=True):
                 "reference", smp)
         cpu_leg("transform_normalize_f64_1Mx64", 16 * Dh.size,
                 lambda: ora.transform_apply(0, Dh, mu, sd, 1e-8, use_ref=True), "reference", smp)
-    del D, O, st
+    del D, Ds, O, st
     torch.cuda.empty_cache()
 
     # ---- the rest of the quantization API: percentile calibration (64M f64)
     # and the int8 product (4096^3, device pointers)
     P = torch.randn(1 << 26, device=dev, dtype=torch.float64, generator=g)
+    Ps = copies(P, 2)
     qp = QuantParamsC()
     torch.cuda.synchronize()
-    put("calibrate_percentile_f64_64M", 8 * P.numel(), None, clock.host_call_us(
-        lambda: _lib.calibrate_percentile(P.data_ptr(), P.numel(), ctypes.c_double(0.01), 1, ctypes.byref(qp))))
+    put("calibrate_percentile_f64_64M", 8 * P.numel(), None, clock.host_call_us(rot(
+        lambda k: _lib.calibrate_percentile(Ps[k].data_ptr(), P.numel(), ctypes.c_double(0.01), 1,
+                                            ctypes.byref(qp)), 2)))
     if cpu:
         Ph = P[:SUITE_CPU_SAMPLE].cpu().numpy()
         cpu_leg("calibrate_percentile_f64_64M", 8 * Ph.size,
                 lambda: ora.calibrate_percentile(Ph, 0.01, True, use_ref=True), "reference",
                 f"first {Ph.size:,} values; quantize.c (qsort) compiled unchanged")
-    del P
+    del P, Ps
     m = 4096
     A8 = torch.randint(-128, 128, (m, m), dtype=torch.int8, device=dev, generator=g)
     B8 = torch.randint(-128, 128, (m, m), dtype=torch.int8, device=dev, generator=g)
