@@ -1234,6 +1234,7 @@ def suite(torch, pn, clock, dev, cpu=True):
     the oracle allocates each output, which those timings include.  Inputs and
     outputs of ops whose footprint is below 1 GiB rotate over copies (NROT, or
     2-3 for the larger ones) between timed calls."""
+    import numpy as np
     from pyneural.core import _lib, QuantParamsC
     W = pn.Tensor.from_torch
     res = {}
@@ -1299,18 +1300,34 @@ def suite(torch, pn, clock, dev, cpu=True):
     del X, Xs, Ys, tX, tY, rs, ri, trs
     torch.cuda.empty_cache()
 
-    # ---- dropout forward / backward, 64M f32, p = 0.5 (the forward is two launches)
+    # ---- dropout forward / backward, 64M f32, p = 0.5
     n = N1
     a = torch.rand(n, device=dev, generator=g) * 2 - 1
     a_s = copies(a)
     c_s = [torch.empty_like(a) for _ in range(NROT)]
     m_s = [torch.empty(n, dtype=torch.uint8, device=dev) for _ in range(NROT)]
     torch.cuda.synchronize()
+    # Repeated calls with one (n, p), as a training loop makes them: each call's
+    # apply pass also makes the next call's keep bits, so a call is one launch.
+    # A call whose (n, p) differs from the previous call's (here p alternates
+    # between 0.5 and the next float up, a different threshold) runs the
+    # keep-bit pass first, then the plain apply pass.
     fwd = rot(lambda k: _lib.neural_dropout_forward(a_s[k].data_ptr(), c_s[k].data_ptr(), m_s[k].data_ptr(), n,
                                                     ctypes.c_float(0.5)))
-    put("dropout_fwd_keep_bits_f32_64M", 0, clock.kernel_us(fwd, skip=0))
-    put("dropout_fwd_apply_f32_64M", 9 * n, clock.kernel_us(fwd, skip=1))
-    put("dropout_fwd_f32_64M", 9 * n, None, clock.op(fwd)[1])
+    alt_p = [0.5, float(np.nextafter(np.float32(0.5), np.float32(1)))]
+
+    def alt_call(k):
+        alt_p.reverse()
+        return _lib.neural_dropout_forward(a_s[k].data_ptr(), c_s[k].data_ptr(), m_s[k].data_ptr(), n,
+                                           ctypes.c_float(alt_p[0]))
+
+    alt = rot(alt_call)
+    clock.warm(fwd)
+    k, o, nl = clock.op(fwd)
+    put("dropout_fwd_f32_64M", 9 * n, k if nl == 1 else None, o)
+    put("dropout_fwd_new_p_f32_64M", 9 * n, None, clock.op(alt)[1])
+    put("dropout_fwd_keep_bits_f32_64M", 0, clock.kernel_us(alt, skip=0))
+    put("dropout_fwd_apply_f32_64M", 9 * n, clock.kernel_us(alt, skip=1))
     put("dropout_bwd_f32_64M", 9 * n, clock.kernel_us(rot(
         lambda k: _lib.neural_dropout_backward(a_s[k].data_ptr(), c_s[k].data_ptr(), m_s[k].data_ptr(), n,
                                                ctypes.c_float(0.5)))))

@@ -41,6 +41,7 @@
 #include <cmath>
 #include <cstring>
 #include <mutex>
+#include <utility>
 #include <vector>
 
 #include "common.hpp"
@@ -246,12 +247,12 @@ struct NextJump {
     uint32_t c1[kLag];
 };
 
+// The work of block `bid` of the keep-bit pass (a block-uniform index: every
+// thread of the block reaches every barrier).
 template <bool ALL>
-__global__ __launch_bounds__(kDBlock) void k_dropout_bits(const uint64_t *__restrict__ D,
-                                                           const uint32_t *__restrict__ E,
-                                                           const uint32_t *__restrict__ W, uint32_t *__restrict__ Wn,
-                                                           NextJump nj, int64_t nseg, uint32_t t2m1,
-                                                           uint32_t *__restrict__ bits)
+NH_DEV void dropout_bits_block(unsigned bid, const uint64_t *__restrict__ D, const uint32_t *__restrict__ E,
+                               const uint32_t *__restrict__ W, uint32_t *__restrict__ Wn, const NextJump &nj,
+                               int64_t nseg, uint32_t t2m1, uint32_t *__restrict__ bits)
 {
     __shared__ uint64_t sD[kTabWordsPerWave];           // the 64-row digit table
     __shared__ uint32_t sR[kWin];                        // r[A .. A+92]
@@ -263,8 +264,8 @@ __global__ __launch_bounds__(kDBlock) void k_dropout_bits(const uint64_t *__rest
 #pragma unroll
     for (int i = 0; i < kTabWordsPerWave / kDBlock; i++) sD[i * kDBlock + tid] = D[i * kDBlock + tid];
     __syncthreads();
-    const int64_t wave = int64_t(blockIdx.x) * (kDBlock / 64) + wv;
-    if (blockIdx.x == 0 && wv < 2) {
+    const int64_t wave = int64_t(bid) * (kDBlock / 64) + wv;
+    if (bid == 0 && wv < 2) {
         // the next call's 93 values (block 0, two waves; coefficients uniform)
         uint32_t g = 0u;
         if (wv == 0) {
@@ -362,6 +363,16 @@ __global__ __launch_bounds__(kDBlock) void k_dropout_bits(const uint64_t *__rest
     gen_segment<ALL>(w, t2m1, b);
 }
 
+template <bool ALL>
+__global__ __launch_bounds__(kDBlock) void k_dropout_bits(const uint64_t *__restrict__ D,
+                                                           const uint32_t *__restrict__ E,
+                                                           const uint32_t *__restrict__ W, uint32_t *__restrict__ Wn,
+                                                           NextJump nj, int64_t nseg, uint32_t t2m1,
+                                                           uint32_t *__restrict__ bits)
+{
+    dropout_bits_block<ALL>(blockIdx.x, D, E, W, Wn, nj, nseg, t2m1, bits);
+}
+
 constexpr int kDUnroll = 2;
 
 // Keep bit of draw d: segment d / L, bit d % L of its words.  I = uint32_t
@@ -375,14 +386,15 @@ NH_DEV uint32_t keep_bits(const uint32_t *__restrict__ bits, I d)
     return bits[size_t(seg) * kSegWords + size_t(bi >> 5)] >> (bi & 31);
 }
 
-// out = keep ? x * scale : +0, mask = keep; 4 elements per lane-unit.
+// out = keep ? x * scale : +0, mask = keep; 4 elements per lane-unit; block
+// `a` of `na` blocks striding over the n4 vectors.
 template <typename I>
-__global__ __launch_bounds__(kDBlock) void k_dropout_apply(const f32x4 *__restrict__ x, f32x4 *__restrict__ out,
-                                                            uint32_t *__restrict__ mask, const uint32_t *__restrict__ bits,
-                                                            int64_t n4, float scale)
+NH_DEV void dropout_apply_block(unsigned a, unsigned na, const f32x4 *__restrict__ x, f32x4 *__restrict__ out,
+                                uint32_t *__restrict__ mask, const uint32_t *__restrict__ bits, int64_t n4,
+                                float scale)
 {
     const int64_t tile = int64_t(kDBlock) * kDUnroll;
-    for (int64_t base = int64_t(blockIdx.x) * tile + threadIdx.x; base < n4; base += int64_t(gridDim.x) * tile) {
+    for (int64_t base = int64_t(a) * tile + threadIdx.x; base < n4; base += int64_t(na) * tile) {
         f32x4 v[kDUnroll];
         uint32_t kb[kDUnroll];
 #pragma unroll
@@ -409,6 +421,37 @@ __global__ __launch_bounds__(kDBlock) void k_dropout_apply(const f32x4 *__restri
                 st_nt(mask + q, m);
             }
         }
+    }
+}
+
+template <typename I>
+__global__ __launch_bounds__(kDBlock) void k_dropout_apply(const f32x4 *__restrict__ x, f32x4 *__restrict__ out,
+                                                            uint32_t *__restrict__ mask, const uint32_t *__restrict__ bits,
+                                                            int64_t n4, float scale)
+{
+    dropout_apply_block<I>(blockIdx.x, gridDim.x, x, out, mask, bits, n4, scale);
+}
+
+// The apply pass of this call with the keep-bit pass of the next call's
+// draws folded in, for a caller that repeats (n, p) (a training loop): `nb`
+// keep-bit blocks for the draws after this call's, at block indices 0,
+// period, 2 period, ... so that their arithmetic spreads over the stream
+// instead of running before it; the other `na` blocks stream.  The next
+// call finds its keep bits ready and launches only this kernel again.
+template <bool ALL, typename I>
+__global__ __launch_bounds__(kDBlock) void k_dropout_apply_ahead(
+    const f32x4 *__restrict__ x, f32x4 *__restrict__ out, uint32_t *__restrict__ mask,
+    const uint32_t *__restrict__ bits, int64_t n4, float scale, unsigned na,
+    const uint64_t *__restrict__ D, const uint32_t *__restrict__ E, const uint32_t *__restrict__ W,
+    uint32_t *__restrict__ Wn, NextJump nj, int64_t nseg, uint32_t t2m1, uint32_t *__restrict__ next_bits,
+    unsigned nb, unsigned period)
+{
+    const unsigned b = blockIdx.x, q = b / period, r = b - q * period;
+    if (r == 0 && q < nb) {
+        dropout_bits_block<ALL>(q, D, E, W, Wn, nj, nseg, t2m1, next_bits);
+    } else {
+        const unsigned before = q + 1 < nb ? q + 1 : nb;  // keep-bit blocks at indices <= b
+        dropout_apply_block<I>(b - before, na, x, out, mask, bits, n4, scale);
     }
 }
 
@@ -528,6 +571,20 @@ struct Stream {
     uint64_t drawn = 0;                     // draws since the last seed
     NextJump nj{};                          // x^n, x^(n+31) mod P for n = nj_n
     int64_t nj_n = -1;
+    // Keep bits made ahead by the previous call's apply pass for the draws
+    // that follow it, valid for a call of ahead_n draws at threshold
+    // ahead_t2m1 (ahead_all: every draw kept) on stream ahead_stream; the
+    // window after those draws is then in win[cur ^ 1].
+    uint32_t *ahead_bits = nullptr;
+    size_t ahead_cap = 0;
+    bool ahead_valid = false;
+    int64_t ahead_n = -1;
+    uint32_t ahead_t2m1 = 0;
+    bool ahead_all = false;
+    hipStream_t ahead_stream = nullptr;
+    int64_t last_n = -1;                    // the previous call's draws and threshold
+    uint32_t last_t2m1 = 0;
+    bool last_all = false;
 };
 
 Stream &S()
@@ -536,13 +593,24 @@ Stream &S()
     return *s;
 }
 
+// Wait for a pass that made keep bits ahead on another stream (it writes
+// ahead_bits and win[cur ^ 1]), and drop those bits.
+int drop_ahead_locked(Stream &s)
+{
+    if (s.ahead_valid && s.ahead_stream != stream()) NH_HIP(hipStreamSynchronize(s.ahead_stream));
+    s.ahead_valid = false;
+    return NEURAL_OK;
+}
+
 int set_seed_locked(Stream &s, uint32_t seed)
 {
     uint32_t w[kWin];
     seed_window(seed, w);
+    NH_TRY(drop_ahead_locked(s));
     NH_TRY(sync());
     NH_HIP(hipMemcpy(s.win[s.cur], w, sizeof(w), hipMemcpyHostToDevice));
     s.drawn = 0;
+    s.last_n = -1;
     return NEURAL_OK;
 }
 
@@ -632,15 +700,27 @@ static int dropout_fwd(const float *in, float *out, uint8_t *mask, uint64_t n, f
     // every wave of the grid (ceil(nseg / 256) blocks of 4) has a wave jump
     NH_TRY(ensure_jumps_locked(s, ceil_div(nseg, kDBlock) * (kDBlock / 64)));
     const size_t words = size_t(nseg) * kSegWords;
+    const int64_t th = cvtsd2si(double(p) * 2147483647.0);
+    const uint32_t thr = th <= 0 ? 0u : (th >= (int64_t(1) << 31) ? 0x80000000u : uint32_t(th));
+    const float scale = drop_scale(p);
+    // keep = r > 2 thr - 1 (thr >= 1), or every draw (thr = 0)
+    const uint32_t t2m1 = uint32_t(2 * uint64_t(thr) - 1u);
+    const bool all = thr == 0;
+    const bool hit = s.ahead_valid && s.ahead_n == nn && s.ahead_t2m1 == t2m1 && s.ahead_all == all &&
+                     s.ahead_stream == stream();
+    if (!hit) NH_TRY(drop_ahead_locked(s));
+    s.ahead_valid = false;
+    if (hit) {
+        // this call's keep bits were made by the previous call's apply pass
+        std::swap(s.bits, s.ahead_bits);
+        std::swap(s.bits_cap, s.ahead_cap);
+    }
     if (words > s.bits_cap) {
         if (s.bits) dev_free(s.bits);
         s.bits = static_cast<uint32_t *>(dev_alloc(words * sizeof(uint32_t)));
         s.bits_cap = s.bits ? words : 0;
         if (!s.bits) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
     }
-    const int64_t th = cvtsd2si(double(p) * 2147483647.0);
-    const uint32_t thr = th <= 0 ? 0u : (th >= (int64_t(1) << 31) ? 0x80000000u : uint32_t(th));
-    const float scale = drop_scale(p);
 
     Staged xi, xo, xm;
     NH_TRY(xi.open(in, size_t(n) * 4, true));
@@ -653,16 +733,19 @@ static int dropout_fwd(const float *in, float *out, uint8_t *mask, uint64_t n, f
         std::memcpy(s.nj.c1, c1.data(), sizeof(s.nj.c1));
         s.nj_n = nn;
     }
-    uint32_t *W = s.win[s.cur], *Wn = s.win[s.cur ^ 1];
-    // keep = r > 2 thr - 1 (thr >= 1), or every draw (thr = 0)
-    const uint32_t t2m1 = uint32_t(2 * uint64_t(thr) - 1u);
-    if (thr == 0)
-        NH_LAUNCH(k_dropout_bits<true>, dim3(unsigned(ceil_div(nseg, kDBlock))), dim3(kDBlock), 0, stream(), s.dig,
-                  s.ejump, W, Wn, s.nj, nseg, t2m1, s.bits);
-    else
-        NH_LAUNCH(k_dropout_bits<false>, dim3(unsigned(ceil_div(nseg, kDBlock))), dim3(kDBlock), 0, stream(),
-                  s.dig, s.ejump, W, Wn, s.nj, nseg, t2m1, s.bits);
-    NH_TRY(check_launch());
+    const unsigned nbits_blocks = unsigned(ceil_div(nseg, kDBlock));
+    if (!hit) {
+        uint32_t *W = s.win[s.cur], *Wn = s.win[s.cur ^ 1];
+        if (all)
+            NH_LAUNCH(k_dropout_bits<true>, dim3(nbits_blocks), dim3(kDBlock), 0, stream(), s.dig, s.ejump, W, Wn,
+                      s.nj, nseg, t2m1, s.bits);
+        else
+            NH_LAUNCH(k_dropout_bits<false>, dim3(nbits_blocks), dim3(kDBlock), 0, stream(), s.dig, s.ejump, W, Wn,
+                      s.nj, nseg, t2m1, s.bits);
+        NH_TRY(check_launch());
+    }
+    // win[cur ^ 1] now holds (or, after a hit, already held) the window after
+    // this call's draws
     s.cur ^= 1;
     s.drawn += n;
     const float *X = static_cast<const float *>(xi.dev);
@@ -671,7 +754,50 @@ static int dropout_fwd(const float *in, float *out, uint8_t *mask, uint64_t n, f
     int64_t done = 0;
     if (aligned16(X) && aligned16(O) && (reinterpret_cast<uintptr_t>(M) & 3u) == 0) {
         const int64_t n4 = nn / 4;
-        if (n4 > 0) {
+        // A second call in a row with these draws and threshold: make the next
+        // call's keep bits during this apply pass.
+        bool ahead = n4 > 0 && nn == s.last_n && t2m1 == s.last_t2m1 && all == s.last_all &&
+                     int64_t(d_grid(ceil_div(n4, kDUnroll))) + nbits_blocks < (int64_t(1) << 31);
+        if (ahead && words > s.ahead_cap) {
+            if (s.ahead_bits) dev_free(s.ahead_bits);
+            s.ahead_bits = static_cast<uint32_t *>(dev_alloc(words * sizeof(uint32_t)));
+            s.ahead_cap = s.ahead_bits ? words : 0;
+            ahead = s.ahead_bits != nullptr;  // without the buffer, the plain pass
+        }
+        if (ahead) {
+            const unsigned na = d_grid(ceil_div(n4, kDUnroll));
+            const unsigned total = na + nbits_blocks;
+            const unsigned period = total / nbits_blocks;
+            uint32_t *W = s.win[s.cur], *Wn = s.win[s.cur ^ 1];
+            const auto *xv = reinterpret_cast<const f32x4 *>(X);
+            auto *ov = reinterpret_cast<f32x4 *>(O);
+            auto *mv = reinterpret_cast<uint32_t *>(M);
+            if (nn < (int64_t(1) << 32)) {
+                if (all)
+                    NH_LAUNCH((k_dropout_apply_ahead<true, uint32_t>), dim3(total), dim3(kDBlock), 0, stream(), xv,
+                              ov, mv, s.bits, n4, scale, na, s.dig, s.ejump, W, Wn, s.nj, nseg, t2m1,
+                              s.ahead_bits, nbits_blocks, period);
+                else
+                    NH_LAUNCH((k_dropout_apply_ahead<false, uint32_t>), dim3(total), dim3(kDBlock), 0, stream(), xv,
+                              ov, mv, s.bits, n4, scale, na, s.dig, s.ejump, W, Wn, s.nj, nseg, t2m1,
+                              s.ahead_bits, nbits_blocks, period);
+            } else {
+                if (all)
+                    NH_LAUNCH((k_dropout_apply_ahead<true, int64_t>), dim3(total), dim3(kDBlock), 0, stream(), xv,
+                              ov, mv, s.bits, n4, scale, na, s.dig, s.ejump, W, Wn, s.nj, nseg, t2m1,
+                              s.ahead_bits, nbits_blocks, period);
+                else
+                    NH_LAUNCH((k_dropout_apply_ahead<false, int64_t>), dim3(total), dim3(kDBlock), 0, stream(), xv,
+                              ov, mv, s.bits, n4, scale, na, s.dig, s.ejump, W, Wn, s.nj, nseg, t2m1,
+                              s.ahead_bits, nbits_blocks, period);
+            }
+            NH_TRY(check_launch());
+            s.ahead_valid = true;
+            s.ahead_n = nn;
+            s.ahead_t2m1 = t2m1;
+            s.ahead_all = all;
+            s.ahead_stream = stream();
+        } else if (n4 > 0) {
             if (nn < (int64_t(1) << 32))
                 NH_LAUNCH(k_dropout_apply<uint32_t>, dim3(d_grid(ceil_div(n4, kDUnroll))), dim3(kDBlock), 0,
                                    stream(), reinterpret_cast<const f32x4 *>(X), reinterpret_cast<f32x4 *>(O),
@@ -684,6 +810,9 @@ static int dropout_fwd(const float *in, float *out, uint8_t *mask, uint64_t n, f
         }
         done = n4 * 4;
     }
+    s.last_n = nn;
+    s.last_t2m1 = t2m1;
+    s.last_all = all;
     if (done < nn) {
         NH_LAUNCH(k_dropout_apply1, dim3(d_grid(nn - done)), dim3(kDBlock), 0, stream(), X, O, M, s.bits,
                            done, nn, scale);

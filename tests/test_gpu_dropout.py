@@ -102,13 +102,89 @@ def test_large_stream(pn, ora):
     out, mask = _fwd_host(x[:1000], 0.25)
     _, wout, wmask = ora.dropout_forward(x[:1000], 0.25)
     same_bits(mask, wmask)
-    # just above the size where the keep bits are made on a second stream,
-    # with a length that is not a multiple of the chunking
+    # a length that is not a multiple of the segment or the wave group
     m = (1 << 23) + 1003
     out, mask = _fwd_host(x[:m], 0.6)
     _, wout, wmask = ora.dropout_forward(x[:m], 0.6)
     same_bits(mask, wmask)
     same_bits(out, wout)
+
+
+def test_repeated_calls_made_ahead(pn, ora):
+    """A call that repeats the previous call's draws and threshold makes the
+    next call's keep bits during its apply pass; the next call with the same
+    (n, p) on the same stream uses them.  Every path around that is checked
+    against the C library's rand(): streaks of identical calls (with tails of
+    1-3 elements and a single-vector call), a change of p or n inside a streak,
+    alternating sizes, p = 0 and p = 1 streaks, a reseed inside a streak, an
+    unaligned call that takes made-ahead bits, and a change of stream."""
+    import torch
+    lib = _lib()
+    rng = np.random.default_rng(11)
+    lib.neural_dropout_seed(ctypes.c_uint32(31337))
+    ora.srand(31337)
+    total = [0]
+
+    def call(x, p, dev=None):
+        if dev is None:
+            out, mask = _fwd_host(x, p)
+        else:
+            xd, od, md, off = dev
+            n = x.size
+            assert lib.neural_dropout_forward(xd.data_ptr() + 4 * off, od.data_ptr() + 4 * off, md.data_ptr() + off,
+                                              n, ctypes.c_float(p)) == 0
+            out, mask = od.cpu().numpy()[off:off + n], md.cpu().numpy()[off:off + n]
+        _, wout, wmask = ora.dropout_forward(x, p)
+        same_bits(mask, wmask)
+        same_bits(out, wout)
+        total[0] += x.size
+
+    xs = {n: rng.normal(0, 1, n).astype(np.float32) for n in (4, 5, 1000, 71_431, 1 << 20, 23_808 * 3 + 7)}
+    for n in (4, 5, 1000, 71_431, 23_808 * 3 + 7, 1 << 20):
+        for _ in range(4):
+            call(xs[n], 0.5)
+    for p in (0.5, 0.5, 0.25, 0.25, 0.25, 0.5, 0.5):          # p changes inside streaks
+        call(xs[1 << 20], p)
+    for n in (1000, 71_431, 1000, 71_431, 1000, 1000, 1000):   # alternating sizes, then a streak
+        call(xs[n], 0.3)
+    for p in (0.0, 0.0, 0.0, 1.0, 1.0, 1.0):                    # keep everything / nothing
+        call(xs[71_431], p)
+    call(xs[71_431], 0.7)
+    call(xs[71_431], 0.7)                                       # makes bits ahead
+    lib.neural_dropout_seed(ctypes.c_uint32(99))               # ... which the reseed drops
+    ora.srand(99)
+    total[0] = 0                                                # draws count from the last seed
+    call(xs[71_431], 0.7)
+    call(xs[71_431], 0.7)
+    call(xs[71_431], 0.7)
+    # device buffers: an aligned streak, then an unaligned call with the same
+    # (n, p), which uses the bits made ahead and makes none
+    n = 71_431
+    xd = torch.from_numpy(np.concatenate([xs[n], xs[n]])).cuda()
+    od = torch.empty(2 * n, device="cuda")
+    md = torch.empty(2 * n, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    call(xs[n], 0.4, (xd, od, md, 0))
+    call(xs[n], 0.4, (xd, od, md, 0))
+    call(xs[n], 0.4, (xd, od, md, 0))
+    call(np.concatenate([xs[n], xs[n]])[1:n + 1], 0.4, (xd, od, md, 1))
+    call(xs[n], 0.4, (xd, od, md, 0))
+    call(xs[n], 0.4, (xd, od, md, 0))
+    # a change of stream inside a streak
+    s = torch.cuda.Stream()
+    try:
+        call(xs[n], 0.4, (xd, od, md, 0))                       # makes bits ahead on the library's stream
+        lib.neural_hip_set_stream(ctypes.c_void_p(s.cuda_stream))
+        with torch.cuda.stream(s):
+            call(xs[n], 0.4, (xd, od, md, 0))
+            call(xs[n], 0.4, (xd, od, md, 0))
+            call(xs[n], 0.4, (xd, od, md, 0))
+            torch.cuda.synchronize()
+    finally:
+        lib.neural_hip_reset_stream()
+    call(xs[n], 0.4, (xd, od, md, 0))
+    call(xs[n], 0.4, (xd, od, md, 0))
+    assert lib.neural_dropout_draws() == total[0]
 
 
 def test_backward(pn, ora):

@@ -4,8 +4,9 @@ torch's IEEE-exact ops; reductions with torch's float64 sums under the REDUCE
 bound (1e-5 * sum|x|) and exactly for max / argmax (planted past 2^31);
 quantize, dequantize, AdamW and dropout windows (the first and last elements)
 bit for bit against the CPU oracle run on the same window -- elementwise
-functions, so a window's results do not depend on the rest.  Dropout runs once
-past 2^32 draws, where the apply kernel switches to 64-bit draw indices; its
+functions, so a window's results do not depend on the rest.  Dropout runs
+three calls in a row past 2^32 draws, where the apply kernels switch to 64-bit
+draw indices (the third call on keep bits made by the second); its
 windows come from the oracle's jump-ahead of the glibc stream (pinned against
 rand() itself in test_oracle_dropout.py).
 
@@ -208,21 +209,26 @@ def test_dropout_past_int32(pn, ora, lib, n):
     torch.cuda.synchronize()
     seed = 2024
     assert lib.neural_dropout_seed(ctypes.c_uint32(seed)) == 0
-    assert lib.neural_dropout_forward(x.data_ptr(), out.data_ptr(), mask.data_ptr(), n, ctypes.c_float(0.3)) == 0
-    torch.cuda.synchronize()
-    assert lib.neural_dropout_draws() == n
-    for start in (0, n - W):
-        xs = x[start:start + W].cpu().numpy()
-        wout, wmask = ora.dropout_window(seed, start, xs, 0.3)
-        same_bits(mask[start:start + W].cpu().numpy(), wmask)
-        same_bits(out[start:start + W].cpu().numpy(), wout)
-    # the stream continues past the call
+    # three calls in a row: the second makes the third's keep bits during its
+    # apply pass, and the third uses them (and makes the next ones)
+    for call in range(3):
+        assert lib.neural_dropout_forward(x.data_ptr(), out.data_ptr(), mask.data_ptr(), n, ctypes.c_float(0.3)) == 0
+        torch.cuda.synchronize()
+        if call == 1:
+            continue
+        for start in (0, n - W):
+            xs = x[start:start + W].cpu().numpy()
+            wout, wmask = ora.dropout_window(seed, call * n + start, xs, 0.3)
+            same_bits(mask[start:start + W].cpu().numpy(), wmask)
+            same_bits(out[start:start + W].cpu().numpy(), wout)
+    assert lib.neural_dropout_draws() == 3 * n
+    # the stream continues past the calls
     nxt = torch.empty(1000, device="cuda")
     m2 = torch.empty(1000, dtype=torch.uint8, device="cuda")
     assert lib.neural_dropout_forward(x.data_ptr(), nxt.data_ptr(), m2.data_ptr(), 1000, ctypes.c_float(0.3)) == 0
     torch.cuda.synchronize()
-    same_bits(m2.cpu().numpy(), ora.dropout_window(seed, n, x[:1000].cpu().numpy(), 0.3)[1])
-    # backward over the whole mask
+    same_bits(m2.cpu().numpy(), ora.dropout_window(seed, 3 * n, x[:1000].cpu().numpy(), 0.3)[1])
+    # backward over the whole mask (the third call's)
     gi = torch.empty_like(x)
     assert lib.neural_dropout_backward(x.data_ptr(), gi.data_ptr(), mask.data_ptr(), n, ctypes.c_float(0.3)) == 0
     torch.cuda.synchronize()
