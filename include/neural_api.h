@@ -195,7 +195,9 @@ int neural_row_stats(const NeuralTensor *in, NeuralTensor *sum, NeuralTensor *me
  * neural_bias_add, and the row statistics of out exactly as neural_row_stats,
  * reading `in` once and writing `out` once (contiguous tensors whose rows the
  * stand-alone reductions give one wave or block each; otherwise the two calls
- * in sequence, same results). */
+ * in sequence, same results).  `out` may be `in` (the in-place bias add of a
+ * linear layer) or overlap `in` or `bias`: such calls take the two-call route.
+ * The statistics outputs must not overlap `out`, `in`, `bias` or each other. */
 int neural_bias_add_row_stats(NeuralTensor *out, const NeuralTensor *in, const NeuralTensor *bias,
                               NeuralTensor *sum, NeuralTensor *mean, NeuralTensor *max, int64_t *argmax);
 
