@@ -573,15 +573,20 @@ struct Stream {
     int64_t nj_n = -1;
     // Keep bits made ahead by the previous call's apply pass for the draws
     // that follow it, valid for a call of ahead_n draws at threshold
-    // ahead_t2m1 (ahead_all: every draw kept) on stream ahead_stream; the
-    // window after those draws is then in win[cur ^ 1].
+    // ahead_t2m1 (ahead_all: every draw kept); the window after those draws
+    // is then in win[cur ^ 1].
     uint32_t *ahead_bits = nullptr;
     size_t ahead_cap = 0;
     bool ahead_valid = false;
     int64_t ahead_n = -1;
     uint32_t ahead_t2m1 = 0;
     bool ahead_all = false;
-    hipStream_t ahead_stream = nullptr;
+    // Recorded after the last launch of every forward call, on done_stream:
+    // a call on another stream waits for it first, since every call writes
+    // the windows and keep-bit buffers the previous one used.
+    hipEvent_t done = nullptr;
+    hipStream_t done_stream = nullptr;
+    bool done_valid = false;
     int64_t last_n = -1;                    // the previous call's draws and threshold
     uint32_t last_t2m1 = 0;
     bool last_all = false;
@@ -593,12 +598,12 @@ Stream &S()
     return *s;
 }
 
-// Wait for a pass that made keep bits ahead on another stream (it writes
-// ahead_bits and win[cur ^ 1]), and drop those bits.
-int drop_ahead_locked(Stream &s)
+// Order the current stream after the previous forward call when that call ran
+// on another stream: a wait on the event recorded after its last launch,
+// which stays valid if the caller has destroyed that stream since.
+int order_after_last_locked(Stream &s)
 {
-    if (s.ahead_valid && s.ahead_stream != stream()) NH_HIP(hipStreamSynchronize(s.ahead_stream));
-    s.ahead_valid = false;
+    if (s.done_valid && s.done_stream != stream()) NH_HIP(hipStreamWaitEvent(stream(), s.done, 0));
     return NEURAL_OK;
 }
 
@@ -606,7 +611,8 @@ int set_seed_locked(Stream &s, uint32_t seed)
 {
     uint32_t w[kWin];
     seed_window(seed, w);
-    NH_TRY(drop_ahead_locked(s));
+    s.ahead_valid = false;
+    if (s.done_valid) NH_HIP(hipEventSynchronize(s.done));
     NH_TRY(sync());
     NH_HIP(hipMemcpy(s.win[s.cur], w, sizeof(w), hipMemcpyHostToDevice));
     s.drawn = 0;
@@ -634,6 +640,7 @@ int ensure_stream_locked(Stream &s)
     s.wpowers = static_cast<uint32_t *>(dev_alloc(B64.size() * sizeof(uint32_t)));
     s.dig = static_cast<uint64_t *>(dev_alloc(kTabWordsPerWave * sizeof(uint64_t)));
     if (!powers || !s.wpowers || !s.dig) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
+    if (!s.done) NH_HIP(hipEventCreateWithFlags(&s.done, hipEventDisableTiming));
     NH_HIP(hipMemcpy(powers, B.data(), B.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
     NH_HIP(hipMemcpy(s.wpowers, B64.data(), B64.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
     NH_LAUNCH(k_jump_table, dim3(1), dim3(kDBlock), 0, stream(), s.dig, int64_t(0), int64_t(64), powers);
@@ -706,9 +713,8 @@ static int dropout_fwd(const float *in, float *out, uint8_t *mask, uint64_t n, f
     // keep = r > 2 thr - 1 (thr >= 1), or every draw (thr = 0)
     const uint32_t t2m1 = uint32_t(2 * uint64_t(thr) - 1u);
     const bool all = thr == 0;
-    const bool hit = s.ahead_valid && s.ahead_n == nn && s.ahead_t2m1 == t2m1 && s.ahead_all == all &&
-                     s.ahead_stream == stream();
-    if (!hit) NH_TRY(drop_ahead_locked(s));
+    NH_TRY(order_after_last_locked(s));
+    const bool hit = s.ahead_valid && s.ahead_n == nn && s.ahead_t2m1 == t2m1 && s.ahead_all == all;
     s.ahead_valid = false;
     if (hit) {
         // this call's keep bits were made by the previous call's apply pass
@@ -796,7 +802,6 @@ static int dropout_fwd(const float *in, float *out, uint8_t *mask, uint64_t n, f
             s.ahead_n = nn;
             s.ahead_t2m1 = t2m1;
             s.ahead_all = all;
-            s.ahead_stream = stream();
         } else if (n4 > 0) {
             if (nn < (int64_t(1) << 32))
                 NH_LAUNCH(k_dropout_apply<uint32_t>, dim3(d_grid(ceil_div(n4, kDUnroll))), dim3(kDBlock), 0,
@@ -818,6 +823,9 @@ static int dropout_fwd(const float *in, float *out, uint8_t *mask, uint64_t n, f
                            done, nn, scale);
         NH_TRY(check_launch());
     }
+    NH_HIP(hipEventRecord(s.done, stream()));
+    s.done_stream = stream();
+    s.done_valid = true;
     NH_TRY(xo.finish(true));
     NH_TRY(xm.finish(true));
     NH_TRY(xi.finish(false));
