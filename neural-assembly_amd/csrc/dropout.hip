@@ -581,12 +581,8 @@ struct Stream {
     int64_t ahead_n = -1;
     uint32_t ahead_t2m1 = 0;
     bool ahead_all = false;
-    // Recorded after the last launch of every forward call, on done_stream:
-    // a call on another stream waits for it first, since every call writes
-    // the windows and keep-bit buffers the previous one used.
-    hipEvent_t done = nullptr;
-    hipStream_t done_stream = nullptr;
-    bool done_valid = false;
+    // (A change of the library's stream synchronises the old one first, so
+    // calls on different streams never overlap on these buffers.)
     int64_t last_n = -1;                    // the previous call's draws and threshold
     uint32_t last_t2m1 = 0;
     bool last_all = false;
@@ -598,21 +594,11 @@ Stream &S()
     return *s;
 }
 
-// Order the current stream after the previous forward call when that call ran
-// on another stream: a wait on the event recorded after its last launch,
-// which stays valid if the caller has destroyed that stream since.
-int order_after_last_locked(Stream &s)
-{
-    if (s.done_valid && s.done_stream != stream()) NH_HIP(hipStreamWaitEvent(stream(), s.done, 0));
-    return NEURAL_OK;
-}
-
 int set_seed_locked(Stream &s, uint32_t seed)
 {
     uint32_t w[kWin];
     seed_window(seed, w);
     s.ahead_valid = false;
-    if (s.done_valid) NH_HIP(hipEventSynchronize(s.done));
     NH_TRY(sync());
     NH_HIP(hipMemcpy(s.win[s.cur], w, sizeof(w), hipMemcpyHostToDevice));
     s.drawn = 0;
@@ -640,7 +626,6 @@ int ensure_stream_locked(Stream &s)
     s.wpowers = static_cast<uint32_t *>(dev_alloc(B64.size() * sizeof(uint32_t)));
     s.dig = static_cast<uint64_t *>(dev_alloc(kTabWordsPerWave * sizeof(uint64_t)));
     if (!powers || !s.wpowers || !s.dig) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
-    if (!s.done) NH_HIP(hipEventCreateWithFlags(&s.done, hipEventDisableTiming));
     NH_HIP(hipMemcpy(powers, B.data(), B.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
     NH_HIP(hipMemcpy(s.wpowers, B64.data(), B64.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
     NH_LAUNCH(k_jump_table, dim3(1), dim3(kDBlock), 0, stream(), s.dig, int64_t(0), int64_t(64), powers);
@@ -713,7 +698,6 @@ static int dropout_fwd(const float *in, float *out, uint8_t *mask, uint64_t n, f
     // keep = r > 2 thr - 1 (thr >= 1), or every draw (thr = 0)
     const uint32_t t2m1 = uint32_t(2 * uint64_t(thr) - 1u);
     const bool all = thr == 0;
-    NH_TRY(order_after_last_locked(s));
     const bool hit = s.ahead_valid && s.ahead_n == nn && s.ahead_t2m1 == t2m1 && s.ahead_all == all;
     s.ahead_valid = false;
     if (hit) {
@@ -823,9 +807,6 @@ static int dropout_fwd(const float *in, float *out, uint8_t *mask, uint64_t n, f
                            done, nn, scale);
         NH_TRY(check_launch());
     }
-    NH_HIP(hipEventRecord(s.done, stream()));
-    s.done_stream = stream();
-    s.done_valid = true;
     NH_TRY(xo.finish(true));
     NH_TRY(xm.finish(true));
     NH_TRY(xi.finish(false));

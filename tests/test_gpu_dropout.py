@@ -113,8 +113,8 @@ def test_large_stream(pn, ora):
 def test_repeated_calls_made_ahead(pn, ora):
     """A call that repeats the previous call's draws and threshold makes the
     next call's keep bits during its apply pass; the next call with the same
-    (n, p) uses them, also on another stream (which first waits for the
-    previous call's kernels).  Every path around that is checked
+    (n, p) uses them, also after a change of stream (which synchronises the
+    old stream).  Every path around that is checked
     against the C library's rand(): streaks of identical calls (with tails of
     1-3 elements and a single-vector call), a change of p or n inside a streak,
     alternating sizes, p = 0 and p = 1 streaks, a reseed inside a streak, an
