@@ -303,9 +303,11 @@ static int gather(NeuralTensor *const *grads, int64_t count, std::vector<GradRef
         if (!is_contiguous(t)) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
         const int64_t n = numel(t);
         if (n == 0) continue;
+        // more tensors than the sum pass has partials: refused before the
+        // list grows further
+        if (int64_t(out.size()) >= kMaxPartials) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
         out.push_back({t, nullptr, n, t->dtype});
     }
-    if (int64_t(out.size()) > kMaxPartials) return set_error(NEURAL_ERR_INVALID_ARGUMENT);
     for (GradRef &g : out) NH_TRY(dev_write(g.t, &g.d, false));
     return NEURAL_OK;
 }

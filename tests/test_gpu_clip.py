@@ -189,6 +189,15 @@ def test_errors(pn):
     norm = ctypes.c_double(-1.0)
     assert _lib.neural_clip_grad_norm_list(None, 0, ctypes.c_double(1.0), ctypes.byref(norm)) == 0
     assert norm.value == 0.0
+    # at most 16384 non-empty tensors per call (the sum pass's partials);
+    # NULL entries do not count
+    big = torch.ones(16385, device="cuda")
+    views = [pn.Tensor.from_torch(big[i:i + 1]) for i in range(16385)]
+    torch.cuda.synchronize()
+    arr = (ctypes.c_void_p * 16386)(*([v._ptr for v in views[:16384]] + [None, views[16384]._ptr]))
+    assert _lib.neural_clip_grad_norm_list(arr, 16386, ctypes.c_double(1e30), ctypes.byref(norm)) == 3
+    assert _lib.neural_clip_grad_norm_list(arr, 16385, ctypes.c_double(1e30), ctypes.byref(norm)) == 0
+    assert norm.value == 128.0  # sqrt(16384 ones)
 
 
 def test_cfg5_scale(pn, ora):
