@@ -83,6 +83,33 @@ def test_steps_bit_exact(pn, ora, kind, dt, n):
         same_bits(gv2, v2)
 
 
+def test_adamw_cfg5_ten_steps(pn, ora):
+    """cfg5's AdamW as BASELINE specifies it (params N(0, 0.02), grads
+    N(0, 1e-3) with 32 NaN, 32 +Inf and 32 -Inf injected, lr 1e-3, wd 0.01),
+    on 4 M f32 parameters: after step t = 10 (9 prior steps, a fresh gradient
+    each step) params and the f64 moments equal the oracle's bit for bit."""
+    n = 1 << 22
+    rng = np.random.default_rng(6)
+    p = rng.normal(0, 0.02, n).astype(np.float32)
+    tp = pn.Tensor.from_numpy(p)
+    opt = pn.AdamW(LR, B1, B2, EPS, WD)
+    rp = p.copy()
+    m, v = np.zeros(n), np.zeros(n)
+    for t in range(1, 11):
+        g = rng.normal(0, 1e-3, n).astype(np.float32)
+        idx = rng.choice(n, 96, replace=False)
+        g[idx[:32]] = np.nan
+        g[idx[32:64]] = np.inf
+        g[idx[64:]] = -np.inf
+        tg = pn.Tensor.from_numpy(g)
+        opt.step([tp], [tg])
+        ora.adamw_step(rp, g, m, v, LR, B1, B2, EPS, WD, t)
+    same_bits(tp.numpy(), rp)
+    gm, gv = _blob_moments(opt.state_bytes(), [n], 2)
+    same_bits(gm, m)
+    same_bits(gv, v)
+
+
 def test_state_roundtrip_and_reference_blob(pn, ora):
     p, g = _data(1000, np.float32, 3)
     tp, tg = pn.Tensor.from_numpy(p), pn.Tensor.from_numpy(g)
