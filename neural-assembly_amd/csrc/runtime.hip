@@ -582,6 +582,32 @@ void storage_release(Storage *s)
 }
 
 // Byte span [lo, hi) reachable from element 0 through the strides.
+// A caller's shape (and byte strides, when given) as the library can hold
+// it: every dimension below 2^63, the element count and its bytes, and each
+// dimension's byte extent and their sums (the storage span) all within
+// int64 -- so no count, index or span computed later can wrap.
+// NEURAL_ERR_TENSOR_TOO_LARGE otherwise.
+static int check_shape(const uint64_t *shape, uint64_t ndim, int dtype, const int64_t *strides)
+{
+    int64_t n = 1, lo = 0, hi = 0;
+    for (uint64_t i = 0; i < ndim; i++) {
+        if (shape[i] > uint64_t(INT64_MAX)) return NEURAL_ERR_TENSOR_TOO_LARGE;
+        if (__builtin_mul_overflow(n, int64_t(shape[i]), &n)) return NEURAL_ERR_TENSOR_TOO_LARGE;
+        if (strides && shape[i] > 0) {
+            int64_t ext;
+            if (__builtin_mul_overflow(int64_t(shape[i]) - 1, strides[i], &ext)) return NEURAL_ERR_TENSOR_TOO_LARGE;
+            if (ext < 0 ? __builtin_add_overflow(lo, ext, &lo) : __builtin_add_overflow(hi, ext, &hi))
+                return NEURAL_ERR_TENSOR_TOO_LARGE;
+        }
+    }
+    int64_t bytes;
+    if (__builtin_mul_overflow(n, int64_t(elem_size(dtype)), &bytes)) return NEURAL_ERR_TENSOR_TOO_LARGE;
+    if (strides && (__builtin_add_overflow(hi, int64_t(elem_size(dtype)), &hi) ||
+                    __builtin_sub_overflow(hi, lo, &hi)))
+        return NEURAL_ERR_TENSOR_TOO_LARGE;
+    return NEURAL_OK;
+}
+
 void span_of(const NeuralTensor *t, int64_t *lo, int64_t *hi)
 {
     int64_t a = 0, b = 0;
@@ -602,6 +628,7 @@ NeuralTensor *create_owned(const uint64_t *shape, uint64_t ndim, int dtype, bool
         set_error(NEURAL_ERR_INVALID_DTYPE);
         return nullptr;
     }
+    if (const int rc = check_shape(shape, ndim, dtype, nullptr)) { set_error(rc); return nullptr; }
     NeuralTensor *t = alloc_desc(int64_t(ndim), dtype);
     if (!t) { set_error(NEURAL_ERR_OUT_OF_MEMORY); return nullptr; }
     int64_t n = 1;
@@ -742,6 +769,7 @@ NeuralTensor *neural_tensor_from_buffer(void *buffer, const uint64_t *shape, uin
         set_error(NEURAL_ERR_INVALID_DTYPE);
         return nullptr;
     }
+    if (const int rc = check_shape(shape, ndim, dtype, strides)) { set_error(rc); return nullptr; }
     NeuralTensor *t = alloc_desc(int64_t(ndim), dtype);
     if (!t) { set_error(NEURAL_ERR_OUT_OF_MEMORY); return nullptr; }
     for (uint64_t i = 0; i < ndim; i++) t->shape[i] = int64_t(shape[i]);
@@ -899,6 +927,11 @@ int neural_tensor_copy(NeuralTensor *dst, const NeuralTensor *src)
 NeuralTensor *neural_tensor_reshape(NeuralTensor *t, const uint64_t *new_shape, uint64_t new_ndim)
 {
     if (!t || (new_ndim > 0 && !new_shape)) { set_error(NEURAL_ERR_NULL_POINTER); return nullptr; }
+    // a count that does not fit int64 cannot match the tensor's
+    if (check_shape(new_shape, new_ndim, t->dtype, nullptr) != NEURAL_OK) {
+        set_error(NEURAL_ERR_SHAPE_MISMATCH);
+        return nullptr;
+    }
     int64_t n = 1;
     for (uint64_t i = 0; i < new_ndim; i++) n *= int64_t(new_shape[i]);
     if (n != numel(t)) { set_error(NEURAL_ERR_SHAPE_MISMATCH); return nullptr; }

@@ -163,3 +163,40 @@ def test_raw_pointer_into_tensor_mirror(pn):
         y = np.empty(m, dtype=np.float32)
         assert lib.simd_add_f32(y.ctypes.data, x.ctypes.data, x.ctypes.data, m) == 0
         same_bits(y, x + x)
+
+
+def test_shape_limits(pn):
+    """Shapes whose element count, byte size or strided span does not fit
+    int64 are refused with TENSOR_TOO_LARGE before anything is allocated (a
+    wrapped count would size a buffer smaller than the kernels index); a
+    tensor larger than the device is OUT_OF_MEMORY; the library keeps working
+    afterwards."""
+    import torch
+    lib = pn.core._lib
+    E = pn.NeuralError
+
+    def create(*shape, dtype=0):
+        arr = (ctypes.c_uint64 * len(shape))(*shape)
+        return lib.neural_tensor_create(arr, len(shape), dtype)
+
+    assert not create(1 << 40, 1 << 40) and lib.neural_get_last_error() == E.TENSOR_TOO_LARGE
+    assert not create(1 << 32, 1 << 32, 4) and lib.neural_get_last_error() == E.TENSOR_TOO_LARGE
+    assert not create(1 << 63) and lib.neural_get_last_error() == E.TENSOR_TOO_LARGE
+    assert not create(1 << 62, dtype=1) and lib.neural_get_last_error() == E.TENSOR_TOO_LARGE  # bytes overflow
+    assert not create(1 << 38) and lib.neural_get_last_error() == E.OUT_OF_MEMORY              # 1 TiB of f32
+    buf = torch.zeros(16, device="cuda")
+    torch.cuda.synchronize()
+    shp = (ctypes.c_uint64 * 1)(4)
+    bad_stride = (ctypes.c_int64 * 1)(1 << 62)
+    assert not lib.neural_tensor_from_buffer(ctypes.c_void_p(buf.data_ptr()), shp, 1, 0, bad_stride)
+    assert lib.neural_get_last_error() == E.TENSOR_TOO_LARGE
+    t = pn.Tensor.from_numpy(np.arange(16, dtype=np.float32))
+    wrap = (ctypes.c_uint64 * 2)(1 << 32, 1 << 32)   # 2^64 wraps to 0 in int64 arithmetic
+    assert not lib.neural_tensor_reshape(t._ptr, wrap, 2)
+    assert lib.neural_get_last_error() == E.SHAPE_MISMATCH
+    ok = (ctypes.c_uint64 * 2)(4, 4)
+    v = lib.neural_tensor_reshape(t._ptr, ok, 2)
+    assert v
+    lib.neural_tensor_free(v)
+    u = pn.Tensor.from_numpy(np.ones(8, dtype=np.float32))
+    same_bits(u.numpy(), np.ones(8, dtype=np.float32))
