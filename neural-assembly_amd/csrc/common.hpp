@@ -139,9 +139,16 @@ struct Staged {
     bool     owned = false;
     Storage *mirror = nullptr;  // the tensor storage whose mirror `host` lies in
     int    open(const void *p, size_t nbytes, bool upload);
+    // count elements of es bytes; a count beyond kMaxRawCount (whose bytes
+    // could wrap size_t) is NEURAL_ERR_TENSOR_TOO_LARGE
+    int    open_n(const void *p, uint64_t count, size_t es, bool upload);
     int    finish(bool download);
     ~Staged();
 };
+
+// Largest element count a raw-pointer entry point accepts: 2^56 elements of
+// up to 8 bytes stay far inside size_t.
+constexpr uint64_t kMaxRawCount = uint64_t(1) << 56;
 
 // Owned tensors' host mirrors, for Staged::open (registered at creation,
 // removed when the storage is released).

@@ -713,8 +713,8 @@ static int dropout_fwd(const float *in, float *out, uint8_t *mask, uint64_t n, f
     }
 
     Staged xi, xo, xm;
-    NH_TRY(xi.open(in, size_t(n) * 4, true));
-    NH_TRY(xo.open(out, size_t(n) * 4, false));
+    NH_TRY(xi.open_n(in, n, 4, true));
+    NH_TRY(xo.open_n(out, n, 4, false));
     NH_TRY(xm.open(mask, size_t(n), false));
     if (nn != s.nj_n) {
         // x^n and x^(n+31) mod P for the next call's values
@@ -821,9 +821,9 @@ static int dropout_bwd(const float *go, float *gi, const uint8_t *mask, uint64_t
     const int64_t nn = int64_t(n);
     const float scale = drop_scale(p);
     Staged sg, so, sm;
-    NH_TRY(sg.open(go, size_t(n) * 4, true));
+    NH_TRY(sg.open_n(go, n, 4, true));
     NH_TRY(sm.open(mask, size_t(n), true));
-    NH_TRY(so.open(gi, size_t(n) * 4, false));
+    NH_TRY(so.open_n(gi, n, 4, false));
     const float *G = static_cast<const float *>(sg.dev);
     float *O = static_cast<float *>(so.dev);
     const uint8_t *M = static_cast<const uint8_t *>(sm.dev);

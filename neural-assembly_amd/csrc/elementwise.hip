@@ -273,6 +273,7 @@ static int raw_binary_f32(float *dst, const float *a, const float *b, uint64_t n
     NH_TRY(ensure_init());
     if (!dst || !a || !b) return set_error(NEURAL_ERR_NULL_POINTER);
     if (n == 0) return set_error(NEURAL_OK);
+    if (n > kMaxRawCount) return set_error(NEURAL_ERR_TENSOR_TOO_LARGE);
     const size_t bytes = size_t(n) * 4;
     Staged sa, sb, so;
     NH_TRY(sa.open(a, bytes, true));
@@ -353,6 +354,7 @@ int simd_fma_f32(float *dst, const float *a, const float *b, const float *c, uin
     NH_TRY(ensure_init());
     if (!dst || !a || !b || !c) return set_error(NEURAL_ERR_NULL_POINTER);
     if (n == 0) return set_error(NEURAL_OK);
+    if (n > kMaxRawCount) return set_error(NEURAL_ERR_TENSOR_TOO_LARGE);
     const size_t bytes = size_t(n) * 4;
     Staged sa, sb, sc, so;
     NH_TRY(sa.open(a, bytes, true));

@@ -459,11 +459,13 @@ static int ls_ce(const T *logits, const int64_t *targets, int64_t batch, int64_t
     if ((MODE != CE_LS_BWD && !loss_out) || (MODE != CE_LS_FWD && !grad_out)) return -1;
     if (batch <= 0 || classes <= 0) return -1;
     if (!(smoothing >= 0.0 && smoothing <= 1.0)) return -1;
-    const size_t n = size_t(batch) * size_t(classes);
+    int64_t n;
+    if (__builtin_mul_overflow(batch, classes, &n)) return -1;
     Staged sx, st, sg;
-    if (sx.open(logits, n * sizeof(T), true) != NEURAL_OK || st.open(targets, size_t(batch) * 8, true) != NEURAL_OK)
+    if (sx.open_n(logits, uint64_t(n), sizeof(T), true) != NEURAL_OK ||
+        st.open_n(targets, uint64_t(batch), 8, true) != NEURAL_OK)
         return -1;
-    if (MODE != CE_LS_FWD && sg.open(grad_out, n * sizeof(T), false) != NEURAL_OK) return -1;
+    if (MODE != CE_LS_FWD && sg.open_n(grad_out, uint64_t(n), sizeof(T), false) != NEURAL_OK) return -1;
     const int rc = ce_run<T, MODE>(static_cast<const T *>(sx.dev), static_cast<const int64_t *>(st.dev), nullptr,
                                    batch, classes, smoothing, loss_out, static_cast<T *>(sg.dev));
     if (rc != NEURAL_OK) return -1;

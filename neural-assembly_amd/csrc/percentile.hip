@@ -484,7 +484,7 @@ static int calibrate_pct(const double *data, int64_t n, double percentile, int s
     if (lo_idx < 0) lo_idx = 0;
     if (hi_idx >= n) hi_idx = n - 1;
     Staged s;
-    if (s.open(data, size_t(n) * sizeof(double), true) != NEURAL_OK) return -1;
+    if (s.open_n(data, uint64_t(n), sizeof(double), true) != NEURAL_OK) return -1;
     const double *x = static_cast<const double *>(s.dev);
     const int64_t ranks[2] = {lo_idx, hi_idx};
     uint64_t key[2];

@@ -429,7 +429,7 @@ static int calibrate(const T *data, int64_t n, int symmetric, QuantParams *out, 
     if (ensure_init() != NEURAL_OK) return -1;
     if (!data || n <= 0 || !out) return -1;
     Staged s;
-    if (s.open(data, size_t(n) * sizeof(T), true) != NEURAL_OK) return -1;
+    if (s.open_n(data, uint64_t(n), sizeof(T), true) != NEURAL_OK) return -1;
     RedMinMax<T> red;
     red.symmetric = symmetric ? 1 : 0;
     WsGuard wg;
@@ -449,7 +449,7 @@ static int quantize(const T *data, int8_t *out, int64_t n, const QuantParams *p,
     if (ensure_init() != NEURAL_OK) return -1;
     if (!data || !out || n <= 0 || !p) return -1;
     Staged si, so;
-    if (si.open(data, size_t(n) * sizeof(T), true) != NEURAL_OK || so.open(out, size_t(n), false) != NEURAL_OK)
+    if (si.open_n(data, uint64_t(n), sizeof(T), true) != NEURAL_OK || so.open_n(out, uint64_t(n), 1, false) != NEURAL_OK)
         return -1;
     QArgs qa{0.0, 0, nullptr};
     if (p_on_device) qa.dev = p;
@@ -466,7 +466,7 @@ static int dequantize(const int8_t *data, T *out, int64_t n, const QuantParams *
     if (ensure_init() != NEURAL_OK) return -1;
     if (!data || !out || n <= 0 || !p) return -1;
     Staged si, so;
-    if (si.open(data, size_t(n), true) != NEURAL_OK || so.open(out, size_t(n) * sizeof(T), false) != NEURAL_OK)
+    if (si.open_n(data, uint64_t(n), 1, true) != NEURAL_OK || so.open_n(out, uint64_t(n), sizeof(T), false) != NEURAL_OK)
         return -1;
     QArgs qa{0.0, 0, nullptr};
     if (p_on_device) qa.dev = p;
@@ -482,7 +482,7 @@ static int qerr(const T *data, int64_t n, const QuantParams *p, double *sig, dou
 {
     if (ensure_init() != NEURAL_OK) return -1;
     Staged s;
-    if (s.open(data, size_t(n) * sizeof(T), true) != NEURAL_OK) return -1;
+    if (s.open_n(data, uint64_t(n), sizeof(T), true) != NEURAL_OK) return -1;
     RedQErr<T> red;
     red.scale = p->scale;
     red.inv = 1.0 / p->scale;

@@ -694,7 +694,7 @@ float simd_sum_f32(const float *a, uint64_t n)
 {
     if (ensure_init() != NEURAL_OK || !a || n == 0) return 0.0f;
     Staged sa;
-    if (sa.open(a, size_t(n) * 4, true) != NEURAL_OK) return 0.0f;
+    if (sa.open_n(a, n, 4, true) != NEURAL_OK) return 0.0f;
     WsGuard wg;
     double s = 0.0;
     if (reduce_full_to_host(static_cast<const float *>(sa.dev), int64_t(n), SumF64<float>{}, &s, sizeof(s)) !=
@@ -742,7 +742,7 @@ extern "C" float simd_dot_f32(const float *a, const float *b, uint64_t n)
 {
     if (ensure_init() != NEURAL_OK || !a || !b || n == 0) return 0.0f;
     Staged sa, sb;
-    if (sa.open(a, size_t(n) * 4, true) != NEURAL_OK || sb.open(b, size_t(n) * 4, true) != NEURAL_OK) return 0.0f;
+    if (sa.open_n(a, n, 4, true) != NEURAL_OK || sb.open_n(b, n, 4, true) != NEURAL_OK) return 0.0f;
     WsGuard wg;
     Workspace &ws = workspace();
     int64_t g = ceil_div(int64_t(n), kRBlock);

@@ -348,6 +348,12 @@ int Staged::open(const void *p, size_t nbytes, bool upload)
     return NEURAL_OK;
 }
 
+int Staged::open_n(const void *p, uint64_t count, size_t es, bool upload)
+{
+    if (count > kMaxRawCount) return set_error(NEURAL_ERR_TENSOR_TOO_LARGE);
+    return open(p, size_t(count) * es, upload);
+}
+
 int Staged::finish(bool download)
 {
     // A mirror-backed output was written on the device; the caller may read

@@ -55,7 +55,7 @@ static int scan_raw(const float *data, uint64_t n, ScanOut *st)
 {
     NH_TRY(ensure_init());
     Staged s;
-    NH_TRY(s.open(data, size_t(n) * 4, true));
+    NH_TRY(s.open_n(data, n, 4, true));
     NH_TRY(scan_dev(static_cast<const float *>(s.dev), int64_t(n), st));
     NH_TRY(s.finish(false));
     return NEURAL_OK;

@@ -77,6 +77,12 @@ inline unsigned t_grid(int64_t n)
 
 using namespace nh;
 
+// a * b as an element count the raw-pointer paths can stage (no wrap).
+static bool count_of(int64_t a, int64_t b, int64_t *out)
+{
+    return !__builtin_mul_overflow(a, b, out) && uint64_t(*out) <= kMaxRawCount;
+}
+
 extern "C" {
 
 int tensor_concat_2d(const double *a, const double *b, int64_t rows_a, int64_t cols_a, int64_t rows_b,
@@ -88,7 +94,8 @@ int tensor_concat_2d(const double *a, const double *b, int64_t rows_a, int64_t c
     if (axis == 0 && cols_a != cols_b) return -1;
     if (axis == 1 && rows_a != rows_b) return -1;
     if (ensure_init() != NEURAL_OK) return -1;
-    const int64_t na = rows_a * cols_a, nb = rows_b * cols_b;
+    int64_t na, nb;
+    if (!count_of(rows_a, cols_a, &na) || !count_of(rows_b, cols_b, &nb)) return -1;
     Staged sa, sb, so;
     if (sa.open(a, size_t(na) * 8, true) || sb.open(b, size_t(nb) * 8, true) || so.open(out, size_t(na + nb) * 8, false))
         return -1;
@@ -120,7 +127,8 @@ int tensor_split_2d(const double *in, int64_t rows, int64_t cols, int64_t axis, 
     const int64_t lim = axis == 0 ? rows : cols;
     if (split_index <= 0 || split_index >= lim) return -1;
     if (ensure_init() != NEURAL_OK) return -1;
-    const int64_t n = rows * cols;
+    int64_t n;
+    if (!count_of(rows, cols, &n)) return -1;
     const int64_t na = axis == 0 ? split_index * cols : rows * split_index;
     const int64_t nb = n - na;
     Staged si, sa, sb;
@@ -150,9 +158,13 @@ int tensor_pad_2d(const double *in, int64_t in_rows, int64_t in_cols, int64_t pa
     if (in_rows <= 0 || in_cols <= 0) return -1;
     if (pad_top < 0 || pad_bottom < 0 || pad_left < 0 || pad_right < 0) return -1;
     if (ensure_init() != NEURAL_OK) return -1;
-    const int64_t R = in_rows + pad_top + pad_bottom, C = in_cols + pad_left + pad_right;
+    int64_t R, C, nin, nout;
+    if (__builtin_add_overflow(in_rows, pad_top, &R) || __builtin_add_overflow(R, pad_bottom, &R) ||
+        __builtin_add_overflow(in_cols, pad_left, &C) || __builtin_add_overflow(C, pad_right, &C) ||
+        !count_of(in_rows, in_cols, &nin) || !count_of(R, C, &nout))
+        return -1;
     Staged si, so;
-    if (si.open(in, size_t(in_rows * in_cols) * 8, true) || so.open(out, size_t(R * C) * 8, false)) return -1;
+    if (si.open(in, size_t(nin) * 8, true) || so.open(out, size_t(nout) * 8, false)) return -1;
     NH_LAUNCH(k_pad, dim3(t_grid(R * C)), dim3(256), 0, stream(), static_cast<const double *>(si.dev),
                        static_cast<double *>(so.dev), in_rows, in_cols, pad_top, pad_left, R, C, pad_value);
     if (check_launch() != NEURAL_OK) return -1;
@@ -167,7 +179,9 @@ int tensor_transpose2d_array(const double *in, int64_t rows, int64_t cols, doubl
     if (!in || !out) return -1;
     if (rows <= 0 || cols <= 0) return -1;
     if (ensure_init() != NEURAL_OK) return -1;
-    const size_t bytes = size_t(rows * cols) * 8;
+    int64_t n;
+    if (!count_of(rows, cols, &n)) return -1;
+    const size_t bytes = size_t(n) * 8;
     Staged si, so;
     if (si.open(in, bytes, true) || so.open(out, bytes, false)) return -1;
     const int64_t gx = ceil_div(cols, kTile), gy = ceil_div(rows, kTile);

@@ -250,12 +250,14 @@ static int stats(const double *data, int64_t b, int64_t F, double *mean, double 
     const int64_t chunk = ceil_div(b, nchunks);
     nchunks = ceil_div(b, chunk);
     Staged sx, so[4];
-    if (sx.open(data, size_t(b * F) * sizeof(double), true) != NEURAL_OK) return -1;
+    int64_t bf;
+    if (__builtin_mul_overflow(b, F, &bf)) return -1;
+    if (sx.open_n(data, uint64_t(bf), sizeof(double), true) != NEURAL_OK) return -1;
     double *outs[4] = {mean, std, mn, mx};
     double *douts[4] = {nullptr, nullptr, nullptr, nullptr};
     for (int k = 0; k < 4; k++) {
         if (!outs[k]) continue;
-        if (so[k].open(outs[k], size_t(F) * sizeof(double), false) != NEURAL_OK) return -1;
+        if (so[k].open_n(outs[k], uint64_t(F), sizeof(double), false) != NEURAL_OK) return -1;
         douts[k] = static_cast<double *>(so[k].dev);
     }
     ColState *part = static_cast<ColState *>(dev_alloc(size_t(nchunks * F) * sizeof(ColState)));
@@ -280,12 +282,13 @@ static int feat_apply(const double *data, double *out, int64_t b, int64_t F, con
     if (!data || !out || !p0 || !p1) return -1;
     if (b <= 0 || F <= 0) return -1;
     if (ensure_init() != NEURAL_OK) return -1;
-    const int64_t n = b * F;
+    int64_t n;
+    if (__builtin_mul_overflow(b, F, &n)) return -1;
     Staged sx, so, s0, s1;
-    if (sx.open(data, size_t(n) * sizeof(double), true) != NEURAL_OK ||
-        so.open(out, size_t(n) * sizeof(double), false) != NEURAL_OK ||
-        s0.open(p0, size_t(F) * sizeof(double), true) != NEURAL_OK ||
-        s1.open(p1, size_t(F) * sizeof(double), true) != NEURAL_OK)
+    if (sx.open_n(data, uint64_t(n), sizeof(double), true) != NEURAL_OK ||
+        so.open_n(out, uint64_t(n), sizeof(double), false) != NEURAL_OK ||
+        s0.open_n(p0, uint64_t(F), sizeof(double), true) != NEURAL_OK ||
+        s1.open_n(p1, uint64_t(F), sizeof(double), true) != NEURAL_OK)
         return -1;
     const double *X = static_cast<const double *>(sx.dev);
     double *O = static_cast<double *>(so.dev);

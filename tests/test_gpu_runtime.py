@@ -200,3 +200,32 @@ def test_shape_limits(pn):
     lib.neural_tensor_free(v)
     u = pn.Tensor.from_numpy(np.ones(8, dtype=np.float32))
     same_bits(u.numpy(), np.ones(8, dtype=np.float32))
+
+
+def test_raw_counts_beyond_limit(pn):
+    """Raw-pointer entry points refuse element counts whose byte size could
+    wrap (n = 2^62 + 1: times 4 or 8 it would wrap to a few bytes, so a
+    staging buffer of that size would meet kernels indexing 2^62 elements)
+    before staging anything, with their usual error returns; products of two
+    dimensions that overflow likewise."""
+    lib = pn.core._lib
+    E = pn.NeuralError
+    big = (1 << 62) + 1
+    buf = np.zeros(64, dtype=np.float64)
+    p = buf.ctypes.data
+    out8 = np.zeros(64, dtype=np.int8)
+    assert lib.neural_tensor_has_nan(p, big) == 0 and lib.neural_get_last_error() == E.TENSOR_TOO_LARGE
+    assert lib.simd_add_f32(p, p, p, big) == E.TENSOR_TOO_LARGE
+    assert lib.simd_sum_f32(p, big) == 0.0 and lib.neural_get_last_error() == E.TENSOR_TOO_LARGE
+    qp = pn.core.QuantParamsC()
+    assert lib.calibrate_minmax(p, big, 1, ctypes.byref(qp)) == -1
+    assert lib.quantize_tensor(p, out8.ctypes.data, big, ctypes.byref(qp)) == -1
+    assert lib.neural_dropout_forward(p, p, out8.ctypes.data, big, ctypes.c_float(0.5)) == E.TENSOR_TOO_LARGE
+    loss = ctypes.c_double()
+    tgt = np.zeros(64, dtype=np.int64)
+    assert lib.label_smoothing_ce_forward(p, tgt.ctypes.data, 1 << 40, 1 << 40, 0.1, ctypes.byref(loss)) == -1
+    assert lib.tensor_transpose2d_array(p, 1 << 40, 1 << 40, p) == -1
+    assert lib.transform_compute_stats(p, 1 << 40, 1 << 40, p, None, None, None) == -1
+    # the library still works
+    x = np.arange(64, dtype=np.float32)
+    assert lib.simd_sum_f32(x.ctypes.data, 64) == float(x.sum())
