@@ -398,7 +398,8 @@ static int resolve_axis(const NeuralTensor *in, int64_t axis, int &kind, int64_t
     if (axis == nd - 1) {
         kind = 1;
         cols = in->shape[nd - 1];
-        rows = cols > 0 ? numel(in) / cols : 0;
+        rows = 1;  // the leading dims' product (rows of zero length still count)
+        for (int64_t i = 0; i + 1 < nd; i++) rows *= in->shape[i];
         return NEURAL_OK;
     }
     // Other axes: the reference falls back to the full sum (math_kernels.asm:979-991).
@@ -426,7 +427,8 @@ static int reduce_sum_mean(const NeuralTensor *in, int64_t axis, NeuralTensor *o
     NH_TRY(resolve_axis(in, axis, kind, rows, cols));
     const int64_t nout = kind == 0 ? 1 : (kind == 1 ? rows : cols);
     if (numel(out) != nout || !is_contiguous(out)) return set_error(NEURAL_ERR_SHAPE_MISMATCH);
-    if (numel(in) == 0) return neural_tensor_fill(out, 0.0);
+    // empty input: sums of no elements are 0, their means 0 / 0
+    if (numel(in) == 0) return neural_tensor_fill(out, mean ? __builtin_nan("") : 0.0);
     Contig c;
     NH_TRY(c.open(in));
     void *dst = nullptr;
