@@ -461,7 +461,7 @@ def main():
 
     fused = fused_step(torch, _lib, clock, stream, T, ridx, step_ops, args, ms_per_step, n1)
     yres = y_residency(torch, pn, _lib, clock, Y, step_ops)
-    rot_us = rotating_step(torch, pn, _lib, stream, T, ridx, args)
+    rot_us = rotating_step(torch, pn, _lib, stream, T, ridx, args, X, S)
 
     cpu2 = None
     if not args.no_cpu:
@@ -490,9 +490,12 @@ def main():
             "kernel_sum_us": round(kernel_sum_us, 1),
             "fused_step": fused,
             "y_residency": yres,
-            "step_outputs_rotating": {"us_per_step": round(rot_us, 1),
-                                      "GBps": round(gbs(step_bytes, rot_us), 1),
+            "step_outputs_rotating": {"us_per_step": round(rot_us[0], 1),
+                                      "GBps": round(gbs(step_bytes, rot_us[0]), 1),
                                       "note": f"the same step with Y, P and L rotating over {NROT} buffers each"},
+            "step_all_rotating": {"us_per_step": round(rot_us[1], 1),
+                                  "GBps": round(gbs(step_bytes, rot_us[1]), 1),
+                                  "note": f"the same step with X, S, Y, P and L rotating over {NROT} buffers each"},
             "copy_peak": COPY,
         },
         "roofline": {
@@ -618,38 +621,45 @@ def y_residency(torch, pn, lib, clock, Y, step_ops, reps=REPS):
     return res
 
 
-def rotating_step(torch, pn, lib, stream, T, ridx, args):
-    """Microseconds per cfg2 step with its outputs Y, P and L rotating over
-    NROT buffers each (the timed steps reuse one set, as the reference's loop
-    does): whether the memory-side cache carries any output from one step to
-    the next shows as a difference between the two."""
+def rotating_step(torch, pn, lib, stream, T, ridx, args, X, S):
+    """Microseconds per cfg2 step (a) with its outputs Y, P and L rotating
+    over NROT buffers each and (b) with its inputs X and S rotating as well
+    (copies of the same values), against the timed steps' one set of buffers:
+    whether the memory-side cache carries any buffer from one step to the next
+    shows as a difference between them."""
     W = pn.Tensor.from_torch
-    X, S = T["X"], T["S"]
     ys = [W(torch.empty(ROWS, COLS, device="cuda")) for _ in range(NROT)]
     ps = [W(torch.empty(SROWS, SCOLS, device="cuda")) for _ in range(NROT)]
     ls = [W(torch.empty(SROWS, SCOLS, device="cuda")) for _ in range(NROT)]
+    xs = [W(X.clone()) for _ in range(NROT)]
+    ss = [W(S.clone()) for _ in range(NROT)]
     torch.cuda.synchronize()
 
-    def step(k):
-        y = ys[k % NROT]._ptr
-        for rc in (lib.neural_bias_add(y, X._ptr, T["b"]._ptr), lib.neural_reduce_sum(y, 1, T["rsum"]._ptr),
-                   lib.neural_reduce_mean(y, 1, T["rmean"]._ptr), lib.neural_reduce_max(y, 1, T["rmax"]._ptr),
-                   lib.neural_reduce_argmax(y, 1, ctypes.c_void_p(ridx.data_ptr())),
-                   lib.neural_softmax(ps[k % NROT]._ptr, S._ptr), lib.neural_log_softmax(ls[k % NROT]._ptr, S._ptr)):
-            if rc != 0:
-                raise RuntimeError("rotating step: a call failed")
+    def timed(inputs_rotate):
+        def step(k):
+            r = k % NROT
+            y = ys[r]._ptr
+            x, s_ = (xs[r], ss[r]) if inputs_rotate else (T["X"], T["S"])
+            for rc in (lib.neural_bias_add(y, x._ptr, T["b"]._ptr), lib.neural_reduce_sum(y, 1, T["rsum"]._ptr),
+                       lib.neural_reduce_mean(y, 1, T["rmean"]._ptr), lib.neural_reduce_max(y, 1, T["rmax"]._ptr),
+                       lib.neural_reduce_argmax(y, 1, ctypes.c_void_p(ridx.data_ptr())),
+                       lib.neural_softmax(ps[r]._ptr, s_._ptr), lib.neural_log_softmax(ls[r]._ptr, s_._ptr)):
+                if rc != 0:
+                    raise RuntimeError("rotating step: a call failed")
 
-    for k in range(args.warmup):
-        step(k)
-    torch.cuda.synchronize()
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0.record(stream)
-    for k in range(args.steps):
-        step(k)
-    t1.record(stream)
-    torch.cuda.synchronize()
-    us = 1e3 * t0.elapsed_time(t1) / args.steps
-    del ys, ps, ls
+        for k in range(args.warmup):
+            step(k)
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for k in range(args.steps):
+            step(k)
+        t1.record(stream)
+        torch.cuda.synchronize()
+        return 1e3 * t0.elapsed_time(t1) / args.steps
+
+    us = (timed(False), timed(True))
+    del ys, ps, ls, xs, ss
     torch.cuda.empty_cache()
     return us
 
