@@ -128,7 +128,7 @@ template <> NH_DEV double wave_fmax_t<double>(double v)
 // element needs a bounds check (per-element checks around the exp turn into
 // exec-mask branches).
 template <typename T, int VPL, int MODE, bool FULL>
-__global__ __launch_bounds__(256) void k_ce_wave(const T *__restrict__ x, CeArgs a, bool vec)
+__global__ __launch_bounds__(256) void k_ce_wave(const T *__restrict__ x, CeArgs a, bool vec, int64_t r_base)
 {
     using V = typename Vec16<T>::type;
     constexpr int VN = Vec16<T>::n;
@@ -143,7 +143,7 @@ __global__ __launch_bounds__(256) void k_ce_wave(const T *__restrict__ x, CeArgs
         if (threadIdx.x < 64) etab[threadIdx.x] = exp2(double(threadIdx.x) * (1.0 / 64.0));
         __syncthreads();
     }
-    const int64_t r = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int64_t r = r_base + int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
     if (r >= a.rows) return;  // uniform per wave
     const int64_t cols = a.cols;
     const T *xr = x + r * cols;
@@ -279,10 +279,10 @@ __global__ __launch_bounds__(256) void k_ce_wave(const T *__restrict__ x, CeArgs
 // Block per row (any width): max, sum of exp, then the outputs, each a pass
 // over the row.
 template <typename T, int MODE>
-__global__ __launch_bounds__(256) void k_ce_block(const T *__restrict__ x, CeArgs a)
+__global__ __launch_bounds__(256) void k_ce_block(const T *__restrict__ x, CeArgs a, int64_t r_base)
 {
     using G = Grp<256>;
-    const int64_t r = blockIdx.x;
+    const int64_t r = r_base + blockIdx.x;
     const int64_t cols = a.cols;
     const T *xr = x + r * cols;
     T mx = -inf_t<T>();
@@ -330,11 +330,12 @@ __global__ __launch_bounds__(256) void k_ce_block(const T *__restrict__ x, CeArg
 template <typename T, int MODE, int VPL>
 static void launch_ce_wave(const T *x, const CeArgs &a, bool vec)
 {
-    const dim3 g(unsigned(ceil_div(a.rows, 4)));
-    if (vec && a.cols == int64_t(64) * VPL * Vec16<T>::n)
-        NH_LAUNCH((k_ce_wave<T, VPL, MODE, true>), g, dim3(256), 0, stream(), x, a, vec);
-    else
-        NH_LAUNCH((k_ce_wave<T, VPL, MODE, false>), g, dim3(256), 0, stream(), x, a, vec);
+    for_row_launches(a.rows, 4, [&](unsigned g, int64_t base) {
+        if (vec && a.cols == int64_t(64) * VPL * Vec16<T>::n)
+            NH_LAUNCH((k_ce_wave<T, VPL, MODE, true>), dim3(g), dim3(256), 0, stream(), x, a, vec, base);
+        else
+            NH_LAUNCH((k_ce_wave<T, VPL, MODE, false>), dim3(g), dim3(256), 0, stream(), x, a, vec, base);
+    });
 }
 
 template <typename T, int MODE>
@@ -349,7 +350,10 @@ static int launch_ce(const T *x, const CeArgs &a)
     else if (per <= 4) launch_ce_wave<T, MODE, 4>(x, a, vec);
     else if (per <= 8) launch_ce_wave<T, MODE, 8>(x, a, vec);
     else if (per <= 16) launch_ce_wave<T, MODE, 16>(x, a, vec);
-    else NH_LAUNCH((k_ce_block<T, MODE>), dim3(unsigned(a.rows)), dim3(256), 0, stream(), x, a);
+    else
+        for_row_launches(a.rows, 1, [&](unsigned g, int64_t base) {
+            NH_LAUNCH((k_ce_block<T, MODE>), dim3(g), dim3(256), 0, stream(), x, a, base);
+        });
     return check_launch();
 }
 

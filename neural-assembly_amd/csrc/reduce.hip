@@ -276,43 +276,44 @@ static int row_stats_launch(const T *x, const T *bias, T *y, int64_t rows, int64
 
 // ---- column sums (reduce_sum axis=0) -------------------------------------------------
 // Stage 1: grid (column groups of 256, row chunks) writes double partials
-// [chunks][cols]; stage 2 adds the chunks in order per column.
+// [chunks][cols]; stage 2 adds the chunks in order per column.  Both step
+// through column groups by the grid's width (capped at kMaxGridBlocks).
 
 __global__ __launch_bounds__(256) void k_colsum_stage1_f32(const float *x, int64_t rows, int64_t cols,
                                                            int64_t chunk, double *part)
 {
-    const int64_t c = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (c >= cols) return;
     const int64_t r0 = int64_t(blockIdx.y) * chunk;
     int64_t r1 = r0 + chunk;
     if (r1 > rows) r1 = rows;
-    double s = 0.0;
-    for (int64_t r = r0; r < r1; r++) s += double(x[r * cols + c]);
-    part[int64_t(blockIdx.y) * cols + c] = s;
+    for (int64_t c = int64_t(blockIdx.x) * 256 + threadIdx.x; c < cols; c += int64_t(gridDim.x) * 256) {
+        double s = 0.0;
+        for (int64_t r = r0; r < r1; r++) s += double(x[r * cols + c]);
+        part[int64_t(blockIdx.y) * cols + c] = s;
+    }
 }
 
 __global__ __launch_bounds__(256) void k_colsum_stage1_f64(const double *x, int64_t rows, int64_t cols,
                                                            int64_t chunk, double *part)
 {
-    const int64_t c = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (c >= cols) return;
     const int64_t r0 = int64_t(blockIdx.y) * chunk;
     int64_t r1 = r0 + chunk;
     if (r1 > rows) r1 = rows;
-    double s = 0.0;
-    for (int64_t r = r0; r < r1; r++) s += x[r * cols + c];
-    part[int64_t(blockIdx.y) * cols + c] = s;
+    for (int64_t c = int64_t(blockIdx.x) * 256 + threadIdx.x; c < cols; c += int64_t(gridDim.x) * 256) {
+        double s = 0.0;
+        for (int64_t r = r0; r < r1; r++) s += x[r * cols + c];
+        part[int64_t(blockIdx.y) * cols + c] = s;
+    }
 }
 
 template <typename T>
 __global__ __launch_bounds__(256) void k_colsum_stage2(const double *part, int64_t nchunks, int64_t cols,
                                                        int64_t div, T *out)
 {
-    const int64_t c = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (c >= cols) return;
-    double s = 0.0;
-    for (int64_t k = 0; k < nchunks; k++) s += part[k * cols + c];
-    out[c] = T(div > 1 ? s / double(div) : s);
+    for (int64_t c = int64_t(blockIdx.x) * 256 + threadIdx.x; c < cols; c += int64_t(gridDim.x) * 256) {
+        double s = 0.0;
+        for (int64_t k = 0; k < nchunks; k++) s += part[k * cols + c];
+        out[c] = T(div > 1 ? s / double(div) : s);
+    }
 }
 
 static int colsum(const NeuralTensor *in, const void *src, int64_t rows, int64_t cols, bool mean, void *dst)
@@ -320,6 +321,7 @@ static int colsum(const NeuralTensor *in, const void *src, int64_t rows, int64_t
     if (cols <= 0) return NEURAL_OK;
     // ~4 row chunks per CU-worth of column groups, at least 64 rows per chunk.
     const int64_t cgroups = ceil_div(cols, 256);
+    const unsigned gx = unsigned(cgroups < kMaxGridBlocks ? cgroups : kMaxGridBlocks);
     int64_t nchunks = ceil_div(int64_t(num_cus()) * 4, cgroups);
     if (nchunks > ceil_div(rows, 64)) nchunks = ceil_div(rows, 64);
     if (nchunks < 1) nchunks = 1;
@@ -327,7 +329,7 @@ static int colsum(const NeuralTensor *in, const void *src, int64_t rows, int64_t
     const int64_t chunk = ceil_div(rows > 0 ? rows : 1, nchunks);
     double *part = static_cast<double *>(dev_alloc(size_t(nchunks * cols) * sizeof(double)));
     if (!part) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
-    const dim3 g1{unsigned(cgroups), unsigned(nchunks), 1u};
+    const dim3 g1{gx, unsigned(nchunks), 1u};
     if (in->dtype == NEURAL_DTYPE_FLOAT32)
         NH_LAUNCH(k_colsum_stage1_f32, g1, dim3(256), 0, stream(), static_cast<const float *>(src), rows,
                            cols, chunk, part);
@@ -336,10 +338,10 @@ static int colsum(const NeuralTensor *in, const void *src, int64_t rows, int64_t
                            cols, chunk, part);
     const int64_t div = mean ? rows : 1;
     if (in->dtype == NEURAL_DTYPE_FLOAT32)
-        NH_LAUNCH((k_colsum_stage2<float>), dim3(unsigned(cgroups)), dim3(256), 0, stream(), part, nchunks,
+        NH_LAUNCH((k_colsum_stage2<float>), dim3(gx), dim3(256), 0, stream(), part, nchunks,
                            cols, div, static_cast<float *>(dst));
     else
-        NH_LAUNCH((k_colsum_stage2<double>), dim3(unsigned(cgroups)), dim3(256), 0, stream(), part,
+        NH_LAUNCH((k_colsum_stage2<double>), dim3(gx), dim3(256), 0, stream(), part,
                            nchunks, cols, div, static_cast<double *>(dst));
     const int rc = check_launch();
     dev_free(part);

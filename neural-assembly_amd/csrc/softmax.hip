@@ -98,11 +98,11 @@ NH_DEV void softmax_row_f32(f32x4 (&v)[VPL], f32x4 *__restrict__ yr, int64_t ncv
 
 template <bool LOG, int VPL, bool FULL, int RPW>
 __global__ __launch_bounds__(kSmBlock) void k_softmax_wave_f32(const float *__restrict__ x, float *__restrict__ y,
-                                                               int64_t rows, int64_t cols)
+                                                               int64_t rows, int64_t cols, int64_t r_base)
 {
     using V = f32x4;
     const int lane = threadIdx.x & 63;
-    const int64_t r0 = (int64_t(blockIdx.x) * (kSmBlock / 64) + (threadIdx.x >> 6)) * RPW;
+    const int64_t r0 = r_base + (int64_t(blockIdx.x) * (kSmBlock / 64) + (threadIdx.x >> 6)) * RPW;
     if (r0 >= rows) return;  // uniform per wave
     const int64_t ncv = cols / 4;
     V v[RPW][VPL];
@@ -123,11 +123,11 @@ __global__ __launch_bounds__(kSmBlock) void k_softmax_wave_f32(const float *__re
 
 template <bool LOG, int VPL>
 __global__ __launch_bounds__(kSmBlock) void k_softmax_wave_f64(const double *__restrict__ x, double *__restrict__ y,
-                                                               int64_t rows, int64_t cols)
+                                                               int64_t rows, int64_t cols, int64_t r_base)
 {
     using V = f64x2;
     const int lane = threadIdx.x & 63;
-    const int64_t r = int64_t(blockIdx.x) * (kSmBlock / 64) + (threadIdx.x >> 6);
+    const int64_t r = r_base + int64_t(blockIdx.x) * (kSmBlock / 64) + (threadIdx.x >> 6);
     if (r >= rows) return;  // uniform per wave
     const V *xr = reinterpret_cast<const V *>(x + r * cols);
     V *yr = reinterpret_cast<V *>(y + r * cols);
@@ -206,9 +206,10 @@ NH_DEV float row_exp(float x, float m) { return exp_diff_f32(x, double(m)); }
 NH_DEV double row_exp(double x, double m) { return exp(x - m); }
 
 template <typename T, bool LOG>
-__global__ __launch_bounds__(kSmBlock) void k_softmax_block(const T *__restrict__ x, T *__restrict__ y, int64_t cols)
+__global__ __launch_bounds__(kSmBlock) void k_softmax_block(const T *__restrict__ x, T *__restrict__ y, int64_t cols,
+                                                            int64_t r_base)
 {
-    const int64_t r = blockIdx.x;
+    const int64_t r = r_base + blockIdx.x;
     const T *xr = x + r * cols;
     T *yr = y + r * cols;
     T m = neg_inf<T>();
@@ -233,17 +234,19 @@ static void launch_timed(K kernel, unsigned g, Args... args)
 }
 
 template <typename T, bool LOG, int VPL>
-static void launch_wave(const T *x, T *y, int64_t rows, int64_t cols, unsigned g)
+static void launch_wave(const T *x, T *y, int64_t rows, int64_t cols)
 {
-    if constexpr (sizeof(T) == 4) {
-        // (two rows per wave measured slower on MI355X: 89.7 vs 86.2 us at [65536,1024])
-        if (cols == int64_t(VPL) * 256)
-            launch_timed(k_softmax_wave_f32<LOG, VPL, true, 1>, g, x, y, rows, cols);
-        else
-            launch_timed(k_softmax_wave_f32<LOG, VPL, false, 1>, g, x, y, rows, cols);
-    } else {
-        launch_timed(k_softmax_wave_f64<LOG, VPL>, g, x, y, rows, cols);
-    }
+    for_row_launches(rows, kSmBlock / 64, [&](unsigned g, int64_t base) {
+        if constexpr (sizeof(T) == 4) {
+            // (two rows per wave measured slower on MI355X: 89.7 vs 86.2 us at [65536,1024])
+            if (cols == int64_t(VPL) * 256)
+                launch_timed(k_softmax_wave_f32<LOG, VPL, true, 1>, g, x, y, rows, cols, base);
+            else
+                launch_timed(k_softmax_wave_f32<LOG, VPL, false, 1>, g, x, y, rows, cols, base);
+        } else {
+            launch_timed(k_softmax_wave_f64<LOG, VPL>, g, x, y, rows, cols, base);
+        }
+    });
 }
 
 template <typename T, bool LOG>
@@ -252,15 +255,16 @@ static int launch_softmax(const T *x, T *y, int64_t rows, int64_t cols)
     constexpr int VN = Vec16<T>::n;
     const bool vec = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15u) == 0 && cols % VN == 0;
     const int64_t ncv = cols / VN;
-    const unsigned g = unsigned(ceil_div(rows, kSmBlock / 64));
     if (vec && ncv <= 64 * 16) {
-        if (ncv <= 64) launch_wave<T, LOG, 1>(x, y, rows, cols, g);
-        else if (ncv <= 128) launch_wave<T, LOG, 2>(x, y, rows, cols, g);
-        else if (ncv <= 256) launch_wave<T, LOG, 4>(x, y, rows, cols, g);
-        else if (ncv <= 512) launch_wave<T, LOG, 8>(x, y, rows, cols, g);
-        else launch_wave<T, LOG, 16>(x, y, rows, cols, g);
+        if (ncv <= 64) launch_wave<T, LOG, 1>(x, y, rows, cols);
+        else if (ncv <= 128) launch_wave<T, LOG, 2>(x, y, rows, cols);
+        else if (ncv <= 256) launch_wave<T, LOG, 4>(x, y, rows, cols);
+        else if (ncv <= 512) launch_wave<T, LOG, 8>(x, y, rows, cols);
+        else launch_wave<T, LOG, 16>(x, y, rows, cols);
     } else {
-        NH_LAUNCH((k_softmax_block<T, LOG>), dim3(unsigned(rows)), dim3(kSmBlock), 0, stream(), x, y, cols);
+        for_row_launches(rows, 1, [&](unsigned g, int64_t base) {
+            NH_LAUNCH((k_softmax_block<T, LOG>), dim3(g), dim3(kSmBlock), 0, stream(), x, y, cols, base);
+        });
     }
     return check_launch();
 }

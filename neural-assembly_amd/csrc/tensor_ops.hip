@@ -48,20 +48,27 @@ __global__ __launch_bounds__(256) void k_pad(const double *in, double *o, int64_
     }
 }
 
-// out[c, r] = in[r, c]; block (32 x 8) moves a 32x32 tile.
+// out[c, r] = in[r, c]; block (32 x 8) moves 32x32 tiles, stepping through
+// the tile grid by the launch grid (capped in both dimensions).
 __global__ __launch_bounds__(256) void k_transpose(const double *in, double *o, int64_t rows, int64_t cols)
 {
     __shared__ double tile[kTile][kTile + 1];
-    const int64_t c0 = int64_t(blockIdx.x) * kTile, r0 = int64_t(blockIdx.y) * kTile;
     const int tx = threadIdx.x % kTile, ty = threadIdx.x / kTile;
-    for (int k = ty; k < kTile; k += 8) {
-        const int64_t r = r0 + k, c = c0 + tx;
-        if (r < rows && c < cols) tile[k][tx] = in[r * cols + c];
-    }
-    __syncthreads();
-    for (int k = ty; k < kTile; k += 8) {
-        const int64_t c = c0 + k, r = r0 + tx;
-        if (c < cols && r < rows) o[c * rows + r] = tile[tx][k];
+    const int64_t tcols = (cols + kTile - 1) / kTile, trows = (rows + kTile - 1) / kTile;
+    for (int64_t by = blockIdx.y; by < trows; by += gridDim.y) {
+        for (int64_t bx = blockIdx.x; bx < tcols; bx += gridDim.x) {
+            const int64_t c0 = bx * kTile, r0 = by * kTile;
+            for (int k = ty; k < kTile; k += 8) {
+                const int64_t r = r0 + k, c = c0 + tx;
+                if (r < rows && c < cols) tile[k][tx] = in[r * cols + c];
+            }
+            __syncthreads();
+            for (int k = ty; k < kTile; k += 8) {
+                const int64_t c = c0 + k, r = r0 + tx;
+                if (c < cols && r < rows) o[c * rows + r] = tile[tx][k];
+            }
+            __syncthreads();  // the tile is rewritten by the next step
+        }
     }
 }
 
@@ -184,8 +191,9 @@ int tensor_transpose2d_array(const double *in, int64_t rows, int64_t cols, doubl
     const size_t bytes = size_t(n) * 8;
     Staged si, so;
     if (si.open(in, bytes, true) || so.open(out, bytes, false)) return -1;
-    const int64_t gx = ceil_div(cols, kTile), gy = ceil_div(rows, kTile);
-    if (gx > 0x7fffffff || gy > 65535) return -1;
+    int64_t gx = ceil_div(cols, kTile), gy = ceil_div(rows, kTile);
+    if (gx > 65535) gx = 65535;
+    if (gy > 65535) gy = 65535;
     NH_LAUNCH(k_transpose, dim3(unsigned(gx), unsigned(gy)), dim3(256), 0, stream(),
                        static_cast<const double *>(si.dev), static_cast<double *>(so.dev), rows, cols);
     if (check_launch() != NEURAL_OK) return -1;

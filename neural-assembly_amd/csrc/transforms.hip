@@ -66,14 +66,16 @@ NH_DEV void cs_comb(ColState &a, const ColState &b)
     if (b.mxv > a.mxv || (b.mxv == a.mxv && b.mxi < a.mxi)) { a.mxv = b.mxv; a.mxi = b.mxi; }
 }
 
-__global__ __launch_bounds__(kTBlock) void k_colstats(const double *__restrict__ x, int64_t b, int64_t F,
-                                                       int64_t chunk, ColState *__restrict__ part)
+// Feature group fg (64 features, or all F < 64 with 64 / F rows per wave
+// step) over row chunk blockIdx.y.
+NH_DEV void colstats_group(const double *__restrict__ x, int64_t b, int64_t F, int64_t chunk,
+                           ColState *__restrict__ part, int64_t fg, ColState *sh)
 {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int Wf = F >= 64 ? 64 : int(F);
     const int R = 64 / Wf;  // rows per wave step
     const int ro = lane / Wf;
-    const int64_t f = int64_t(blockIdx.x) * 64 + lane % Wf;
+    const int64_t f = fg * 64 + lane % Wf;
     const bool active = ro < R && f < F;
     const int64_t r0 = int64_t(blockIdx.y) * chunk;
     const int64_t r1 = r0 + chunk < b ? r0 + chunk : b;
@@ -90,7 +92,6 @@ __global__ __launch_bounds__(kTBlock) void k_colstats(const double *__restrict__
         }
         for (; r < r1; r += step) cs_acc(s, x[r * F + f], r);
     }
-    __shared__ ColState sh[kTBlock];
     sh[threadIdx.x] = s;
     __syncthreads();
     if (threadIdx.x < Wf && f < F) {
@@ -100,6 +101,16 @@ __global__ __launch_bounds__(kTBlock) void k_colstats(const double *__restrict__
                 if (ww | rr) cs_comb(t, sh[ww * 64 + rr * Wf + threadIdx.x]);
         part[f * int64_t(gridDim.y) + blockIdx.y] = t;  // chunks of one feature contiguous
     }
+    __syncthreads();  // sh is rewritten by the block's next feature group
+}
+
+// Feature groups step by the grid's width (capped at kMaxGridBlocks).
+__global__ __launch_bounds__(kTBlock) void k_colstats(const double *__restrict__ x, int64_t b, int64_t F,
+                                                       int64_t chunk, ColState *__restrict__ part)
+{
+    __shared__ ColState sh[kTBlock];
+    const int64_t fgroups = (F + 63) / 64;
+    for (int64_t fg = blockIdx.x; fg < fgroups; fg += gridDim.x) colstats_group(x, b, F, chunk, part, fg, sh);
 }
 
 struct ColRed {
@@ -113,22 +124,26 @@ struct ColRed {
 };
 
 // One block per feature folds its chunk partials (an ordered tree: loads
-// issued together, not one dependent load per chunk).
+// issued together, not one dependent load per chunk); features step by the
+// grid's width (capped at kMaxGridBlocks).
 __global__ __launch_bounds__(kRBlock) void k_colstats_final(const ColState *__restrict__ part, int64_t nchunks,
-                                                             int64_t b, double *mean, double *std, double *mn,
-                                                             double *mx)
+                                                             int64_t b, int64_t F, double *mean, double *std,
+                                                             double *mn, double *mx)
 {
-    const int64_t f = blockIdx.x;
-    const ColState t = ordered_combine(ColRed{}, part + f * nchunks, int(nchunks));
-    if (threadIdx.x != 0) return;
-    const double m = t.sum / double(b);
-    const double m2 = m * m;
-    double var = t.sum2 / double(b) - m2;
-    if (var < 0.0) var = 0.0;
-    if (mean) mean[f] = m;
-    if (std) std[f] = sqrt(var);
-    if (mn) mn[f] = t.mnv;
-    if (mx) mx[f] = t.mxv;
+    for (int64_t f = blockIdx.x; f < F; f += gridDim.x) {
+        const ColState t = ordered_combine(ColRed{}, part + f * nchunks, int(nchunks));
+        if (threadIdx.x == 0) {
+            const double m = t.sum / double(b);
+            const double m2 = m * m;
+            double var = t.sum2 / double(b) - m2;
+            if (var < 0.0) var = 0.0;
+            if (mean) mean[f] = m;
+            if (std) std[f] = sqrt(var);
+            if (mn) mn[f] = t.mnv;
+            if (mx) mx[f] = t.mxv;
+        }
+        __syncthreads();  // the combine's LDS is reused by the next feature
+    }
 }
 
 enum { MAP_NORMALIZE = 0, MAP_UNNORMALIZE = 1, MAP_MINMAX = 2 };
@@ -262,9 +277,11 @@ static int stats(const double *data, int64_t b, int64_t F, double *mean, double 
     }
     ColState *part = static_cast<ColState *>(dev_alloc(size_t(nchunks * F) * sizeof(ColState)));
     if (!part) return -1;
-    NH_LAUNCH(k_colstats, dim3(unsigned(fgroups), unsigned(nchunks)), dim3(kTBlock), 0, stream(),
+    const unsigned gx = unsigned(fgroups < kMaxGridBlocks ? fgroups : kMaxGridBlocks);
+    const unsigned gf = unsigned(F < kMaxGridBlocks ? F : kMaxGridBlocks);
+    NH_LAUNCH(k_colstats, dim3(gx, unsigned(nchunks)), dim3(kTBlock), 0, stream(),
                        static_cast<const double *>(sx.dev), b, F, chunk, part);
-    NH_LAUNCH(k_colstats_final, dim3(unsigned(F)), dim3(kRBlock), 0, stream(), part, nchunks, b, douts[0],
+    NH_LAUNCH(k_colstats_final, dim3(gf), dim3(kRBlock), 0, stream(), part, nchunks, b, F, douts[0],
                        douts[1], douts[2], douts[3]);
     const int rc = check_launch();
     dev_free(part);
