@@ -180,7 +180,9 @@ int neural_reduce_sum(const NeuralTensor *in, int64_t axis, NeuralTensor *out);
 int neural_reduce_mean(const NeuralTensor *in, int64_t axis, NeuralTensor *out);
 /* NEW row max (running maxss over the row, activations.asm:888-895) and row
  * argmax (main.asm:3245-3270) over the last dim; indices are int64 written to
- * a host or device pointer with rows entries. */
+ * a host or device pointer with rows entries.  axis is -1 or ndim - 1, both
+ * the last dim (unlike neural_reduce_sum, -1 is not the whole tensor: that is
+ * neural_max / neural_argmax); other axes return NEURAL_ERR_DIM_MISMATCH. */
 int neural_reduce_max(const NeuralTensor *in, int64_t axis, NeuralTensor *out);
 int neural_reduce_argmax(const NeuralTensor *in, int64_t axis, int64_t *out_indices);
 /* NEW, no counterpart in the reference: the row sum, mean, max and argmax over
