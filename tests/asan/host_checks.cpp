@@ -11,17 +11,19 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <thread>
 #include <vector>
 
 #include "neural_api.h"
 
 namespace {
 
-int g_checks = 0, g_fail = 0;
+std::atomic<int> g_checks{0}, g_fail{0};
 
 #define CHECK(cond)                                                                   \
     do {                                                                              \
@@ -546,6 +548,84 @@ void check_hooks()
     CHECK(neural_get_last_error() == NEURAL_ERR_NOT_IMPLEMENTED);
 }
 
+// One of several host threads on the library's one stream: it creates, uses
+// and frees its own tensors, buffers and optimizer, and checks results it can
+// predict exactly, so a mix-up between threads (a shared workspace, the
+// allocator's cache, the mirror registry, the dropout stream) would show.
+void thread_body(int tid, int iters)
+{
+    const float v = float(tid) + 1.5f;
+    for (int it = 0; it < iters; it++) {
+        const uint64_t n = 1000 + uint64_t(tid) * 4099 + uint64_t(it) * 37;
+        NeuralTensor *a = make({n}), *b = make({n}), *o = make({n});
+        CHECK(a && b && o);
+        if (!a || !b || !o) continue;
+        CHECK(neural_tensor_fill(a, double(v) - 0.5) == 0);
+        CHECK(neural_tensor_fill(b, 0.5) == 0);
+        CHECK(neural_add(o, a, b) == 0);
+        double s = 0;
+        CHECK(neural_sum(o, &s) == 0 && s == double(n) * double(v));
+        float *m = static_cast<float *>(neural_tensor_data(o));
+        CHECK(m != nullptr);
+        if (m) {
+            m[n / 2] = 100.0f;
+            int64_t idx = -1;
+            CHECK(neural_argmax(o, &idx) == 0 && idx == int64_t(n / 2));
+            CHECK(neural_tensor_has_inf(m, n) == 0);  // a pointer into the mirror
+        }
+        std::vector<float> h(n);
+        CHECK(neural_tensor_download(o, h.data(), n * 4) == 0);
+        CHECK(h[0] == v && h[n / 2] == 100.0f && h[n - 1] == v);
+        QuantParams qp;
+        CHECK(calibrate_minmax_f32(h.data(), int64_t(n), 0, &qp) == 0 && qp.max_val == 100.0 && qp.min_val == double(v));
+        std::vector<int8_t> q(n);
+        CHECK(quantize_tensor_f32(h.data(), q.data(), int64_t(n), &qp) == 0 && q[n / 2] == 127);
+        // row sums of a [rows, 64] tensor of one value
+        const uint64_t rows = n / 64;
+        NeuralTensor *x = make({rows, 64}), *rs = make({rows});
+        CHECK(x && rs);
+        if (x && rs) {
+            CHECK(neural_tensor_fill(x, double(v)) == 0);
+            CHECK(neural_reduce_sum(x, 1, rs) == 0);
+            std::vector<float> r(rows);
+            CHECK(neural_tensor_download(rs, r.data(), rows * 4) == 0);
+            bool ok = true;
+            for (float e : r) ok = ok && e == 64.0f * v;
+            CHECK(ok);
+        }
+        neural_tensor_free(x);
+        neural_tensor_free(rs);
+        // the global norm of (a, b), then an optimizer of its own
+        NeuralTensor *L[2] = {a, b};
+        double norm = 0;
+        CHECK(neural_clip_grad_norm_list(L, 2, 1e30, &norm) == 0);
+        const double want = std::sqrt(double(n) * (double(v - 0.5f) * double(v - 0.5f) + 0.25));
+        CHECK(std::fabs(norm - want) <= 1e-12 * want);
+        void *opt = opt_adamw_create(1e-3, 0.9, 0.999, 1e-8, 0.01);
+        void *P[1] = {a}, *G[1] = {b};
+        CHECK(opt != nullptr && opt_step(opt, P, G, 1) == 0 && opt_step(opt, P, G, 1) == 0);
+        opt_free(opt);
+        // dropout draws from the one shared stream, under its lock
+        std::vector<float> y(n);
+        std::vector<uint8_t> mask(n);
+        CHECK(neural_dropout_forward(h.data(), y.data(), mask.data(), n, 0.25f) == 0);
+        bool ok = true;
+        for (uint64_t i = 0; i < n; i++) ok = ok && (mask[i] ? y[i] == h[i] * (1.0f / 0.75f) : y[i] == 0.0f);
+        CHECK(ok);
+        neural_tensor_free(a);
+        neural_tensor_free(b);
+        neural_tensor_free(o);
+    }
+}
+
+void check_threads()
+{
+    section("threads");
+    std::vector<std::thread> ts;
+    for (int t = 0; t < 4; t++) ts.emplace_back(thread_body, t, 25);
+    for (auto &t : ts) t.join();
+}
+
 }  // namespace
 
 int main()
@@ -562,7 +642,8 @@ int main()
     check_dropout();
     check_optimizers();
     check_hooks();
+    check_threads();
     neural_shutdown();
-    std::printf("host checks: %d passed, %d failed\n", g_checks - g_fail, g_fail);
+    std::printf("host checks: %d passed, %d failed\n", g_checks - g_fail, g_fail.load());
     return g_fail ? 1 : 0;
 }
