@@ -1,6 +1,7 @@
 // Host-side memory checks of libneural_hip: this program is built with
-// AddressSanitizer and linked against libneural_hip_asan.so (the library's
-// host code instrumented, its device code as usual), then walks the C ABI
+// AddressSanitizer and UndefinedBehaviorSanitizer and linked against
+// libneural_hip_asan.so (the library's host code instrumented for both, its
+// device code as usual), then walks the C ABI
 // through the paths whose host code handles caller memory: tensor
 // descriptors, shapes and strides, host mirrors and raw pointers into them,
 // staging of host buffers, the optimizer state blob (including corrupt
