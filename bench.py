@@ -28,8 +28,8 @@ the achievable 1:1 stream rate; every op also carries its % of it.  Outside
 the step, an op whose footprint is below 1 GiB cycles over NROT copies of its
 inputs and outputs from one timed call to the next, so that the 256 MB
 memory-side cache cannot serve re-reads or absorb rewrites; the step keeps the
-reference's one set of buffers, and the same step with its outputs rotating
-is reported beside it.
+reference's one set of buffers, and the same step with its outputs rotating,
+and with its inputs and outputs rotating, is reported beside it.
 
 CPU baselines, one thread (the reference never dispatches to its thread pool):
   cfg2  the oracle's C restatement of the whole step (port);
@@ -104,8 +104,6 @@ def parse():
     ap.add_argument("--configs", default="cfg1,cfg3,cfg4,cfg5", help="comma-separated configs to run besides cfg2")
     ap.add_argument("--detail", default=None, help="write every per-op figure (JSON) to this file")
     ap.add_argument("--suite", action="store_true", help="also time the other kernel families (detail file)")
-    ap.add_argument("--calib", action="store_true",
-                    help="also run a plain 256 MiB device copy (the PMC byte-counter calibration kernel)")
     return ap.parse_args()
 
 
@@ -522,16 +520,6 @@ def main():
 
     if not args.no_configs:
         line["configs"] = run_configs(torch, pn, _lib, clock, dev, args, detail)
-
-    if args.calib:
-        # Known-size copy: FETCH_SIZE / WRITE_SIZE of this dispatch calibrate the
-        # byte counters (256 MiB read + 256 MiB written).
-        src = torch.empty(64 << 20, device=dev).uniform_()
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
 
     if args.suite:
         detail["suite"] = suite(torch, pn, clock, dev, cpu=not args.no_cpu)
