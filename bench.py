@@ -1238,7 +1238,7 @@ def suite(torch, pn, clock, dev, cpu=True):
     res = {}
     ora, ref = _ref() if cpu else (None, None)
 
-    def put(name, nbytes, k=None, call=None):
+    def put(name, nbytes, k=None, call=None, op=None):
         e = {"bytes": int(nbytes)}
         if k is not None:
             e["k_us"] = round(k, 2)
@@ -1246,6 +1246,9 @@ def suite(torch, pn, clock, dev, cpu=True):
         if call is not None:
             e["call_us"] = round(call, 2)
             e["call_pct"] = pct(nbytes, call)
+        if op is not None:  # every launch of a call that leaves its result on the device
+            e["op_us"] = round(op, 2)
+            e["op_pct"] = pct(nbytes, op)
         res[name] = e
 
     def cpu_leg(name, nbytes, fn, kind, sample):
@@ -1350,6 +1353,12 @@ def suite(torch, pn, clock, dev, cpu=True):
     f = rot(lambda k: _lib.label_smoothing_ce_forward(L64s[k].data_ptr(), tgt.data_ptr(), B, K, 0.1,
                                                       ctypes.byref(lossv)), 2)
     put("ls_ce_forward_f64_65536x1024", 8 * B * K, clock.kernel_us(f), clock.host_call_us(f))
+    # the NEW form that leaves the loss in device memory: no host wait
+    dloss = torch.zeros(1, dtype=torch.float64, device=dev)
+    f = rot(lambda k: _lib.label_smoothing_ce_forward_dev(L64s[k].data_ptr(), tgt.data_ptr(), B, K, 0.1,
+                                                          dloss.data_ptr()), 2)
+    kk, op, _ = clock.op(f)
+    put("ls_ce_forward_dev_f64_65536x1024", 8 * B * K, kk, op=op)
     f = lambda: _lib.label_smoothing_ce_fused(L64.data_ptr(), tgt.data_ptr(), B, K, 0.1, ctypes.byref(lossv),
                                               G64.data_ptr())
     put("ls_ce_fused_f64_65536x1024", 16 * B * K, clock.kernel_us(f), clock.host_call_us(f))
@@ -1370,6 +1379,10 @@ def suite(torch, pn, clock, dev, cpu=True):
     f = rot(lambda k: _lib.label_smoothing_ce_fused_f32(L32s[k].data_ptr(), tgt.data_ptr(), B, K, 0.1,
                                                         ctypes.byref(lossv), G32s[k].data_ptr()))
     put("ls_ce_fused_f32_65536x1024", 8 * B * K, clock.kernel_us(f), clock.host_call_us(f))
+    f = rot(lambda k: _lib.label_smoothing_ce_fused_f32_dev(L32s[k].data_ptr(), tgt.data_ptr(), B, K, 0.1,
+                                                            dloss.data_ptr(), G32s[k].data_ptr()))
+    kk, op, _ = clock.op(f)
+    put("ls_ce_fused_f32_dev_65536x1024", 8 * B * K, kk, op=op)
     tv = W(tgt.float())
     tL = [W(t) for t in L32s]
     f = rot(lambda k: _lib.neural_cross_entropy_loss(tL[k]._ptr, tv._ptr, ctypes.byref(lossv)))

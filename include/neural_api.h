@@ -384,6 +384,22 @@ int label_smoothing_ce_fused(const double *logits, const int64_t *targets, int64
  * f32 paths do), gradient rounded to float. */
 int label_smoothing_ce_fused_f32(const float *logits, const int64_t *targets, int64_t batch_size,
                                  int64_t num_classes, double smoothing, double *loss_out, float *grad_out);
+/* NEW, no counterpart in the reference (for GPU training loops that read the
+ * loss only now and then): the forward, fused and f32 fused forms with the
+ * mean loss left in device memory (*loss_dev, one double) instead of
+ * returned to the host.  The call returns once its launches are enqueued on
+ * the library's stream; the loss and gradient bits equal the host-returning
+ * forms'.  Every pointer must be device memory, aligned to its element
+ * (targets and loss_dev to 8 bytes).  Returns 0, or -1 on NULL, a host or
+ * misaligned pointer, batch or num_classes <= 0, or smoothing outside
+ * [0, 1]; a target outside [0, K) cannot be reported without waiting: it
+ * makes the loss NaN and leaves that row's gradient unwritten. */
+int label_smoothing_ce_forward_dev(const double *logits, const int64_t *targets, int64_t batch_size,
+                                   int64_t num_classes, double smoothing, double *loss_dev);
+int label_smoothing_ce_fused_dev(const double *logits, const int64_t *targets, int64_t batch_size,
+                                 int64_t num_classes, double smoothing, double *loss_dev, double *grad_dev);
+int label_smoothing_ce_fused_f32_dev(const float *logits, const int64_t *targets, int64_t batch_size,
+                                     int64_t num_classes, double smoothing, double *loss_dev, float *grad_dev);
 /* Cross-entropy of softmax(prediction) (replaces neural_api.h:674,
  * neural_api.asm:2546 -> losses.asm:315-613, intended semantics): prediction
  * [batch, K], target [batch] holding class indices as values of the same

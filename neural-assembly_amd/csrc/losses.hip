@@ -359,11 +359,14 @@ static int launch_ce(const T *x, const CeArgs &a)
 
 // Sum of the per-row losses of the tensor CE (losses.asm intended semantics):
 // the rows hold p_t, the loss term is -log(p_t + 1e-7), rounded to float for
-// f32 logits as the reference's float loss.
+// f32 logits as the reference's float loss.  div != 0: the stored value is
+// the sum / div (the mean, for a loss left in device memory), the division
+// the host makes otherwise.
 template <bool F32>
 struct RedCeLoss {
     using L = double;
     using B = double;
+    double div = 0.0;
     NH_DEV L linit() const { return 0.0; }
     NH_DEV void lacc(L &s, double p, int64_t) const
     {
@@ -374,17 +377,21 @@ struct RedCeLoss {
     template <int TPR> NH_DEV B finish(L s, const double *, int64_t, int64_t) const { return s; }
     NH_DEV B bident() const { return 0.0; }
     NH_DEV B bcomb(B a, B b) const { return a + b; }
-    NH_DEV void store(void *out, int64_t r, B s, const double *, int64_t) const { static_cast<double *>(out)[r] = s; }
+    NH_DEV void store(void *out, int64_t r, B s, const double *, int64_t) const
+    {
+        static_cast<double *>(out)[r] = div != 0.0 ? s / div : s;
+    }
 };
 
 // Sum of the label-smoothed row losses: row r holds A_r = sum_c st_c (x_c - m)
 // and s_r = sum_c exp(x_c - m); its loss is log(s_r) * S - A_r with
-// S = sum_c st_c = st0 (cols - 1) + st1.
+// S = sum_c st_c = st0 (cols - 1) + st1.  div as in RedCeLoss.
 struct RedLsLoss {
     using L = double;
     using B = double;
     const double *s;
     double S;
+    double div = 0.0;
     NH_DEV L linit() const { return 0.0; }
     NH_DEV void lacc(L &acc, double A, int64_t i) const
     {
@@ -396,46 +403,63 @@ struct RedLsLoss {
     template <int TPR> NH_DEV B finish(L v, const double *, int64_t, int64_t) const { return v; }
     NH_DEV B bident() const { return 0.0; }
     NH_DEV B bcomb(B a, B b) const { return a + b; }
-    NH_DEV void store(void *out, int64_t r, B v, const double *, int64_t) const { static_cast<double *>(out)[r] = v; }
+    NH_DEV void store(void *out, int64_t r, B v, const double *, int64_t) const
+    {
+        static_cast<double *>(out)[r] = div != 0.0 ? v / div : v;
+    }
 };
 
 // Runs MODE over [rows, cols] logits already on the device; sums the per-row
 // losses into *loss_host (mean over rows) when wanted.  Returns NEURAL_OK,
 // NEURAL_ERR_INVALID_ARGUMENT for a target out of range, or an error code.
+// With loss_dev (device memory) instead, the mean loss is stored there by the
+// last launch and the call returns once everything is enqueued: nothing is
+// waited for, and a target out of range shows only as a NaN loss.
 template <typename T, int MODE>
 static int ce_run(const T *x, const int64_t *tidx, const T *tval, int64_t rows, int64_t cols, double alpha,
-                  double *loss_host, T *grad_dev)
+                  double *loss_host, T *grad_dev, double *loss_dev = nullptr)
 {
     WsGuard wg;
     Workspace &ws = workspace();
-    // The loss sum (word 0) and the out-of-range flag (int word 32) are stored
-    // into the mapped host area.  The flag is zero at init and between calls
-    // (a call that finds it set clears it on the host).
-    int *bad = static_cast<int *>(ws.host_result_dev) + 32;
+    const bool on_dev = loss_dev != nullptr;
     const bool want_loss = MODE != CE_LS_BWD;
     constexpr bool kLs = MODE == CE_LS_FWD || MODE == CE_LS_FUSED;
+    // The loss sum (word 0) and the out-of-range flag (int word 32) are stored
+    // into the mapped host area.  The flag is zero at init and between calls
+    // (a call that finds it set clears it on the host).  A call that leaves
+    // its loss on the device points the flag at a spare word of its own row
+    // buffer, which nothing reads.
+    int *bad = static_cast<int *>(ws.host_result_dev) + 32;
     double *row_loss = nullptr, *row_s = nullptr;
     if (want_loss) {
-        // one block: [rows] row values, then [rows] exp sums (label-smoothed)
-        row_loss = static_cast<double *>(dev_alloc(size_t(rows) * sizeof(double) * (kLs ? 2 : 1)));
+        // one block: [rows] row values, then [rows] exp sums (label-smoothed),
+        // then the spare flag word for a device-resident loss
+        const size_t words = size_t(rows) * (kLs ? 2 : 1);
+        row_loss = static_cast<double *>(dev_alloc((words + (on_dev ? 1 : 0)) * sizeof(double)));
         if (!row_loss) return set_error(NEURAL_ERR_OUT_OF_MEMORY);
         if (kLs) row_s = row_loss + rows;
+        if (on_dev) bad = reinterpret_cast<int *>(row_loss + words);
     }
     CeArgs a{tidx, tval, rows, cols, alpha, 1.0 / double(rows), row_loss, row_s, grad_dev, bad};
     int rc = launch_ce<T, MODE>(x, a);
     // The loss sum's launch stores a ticket after the sum (and after the CE
     // kernel, earlier on the stream, has set the flag or not): the host waits
     // for the ticket instead of synchronising the stream.
-    const Ticket tk = want_loss ? next_ticket() : Ticket{};
+    const Ticket tk = want_loss && !on_dev ? next_ticket() : Ticket{};
     if (rc == NEURAL_OK && want_loss) {
-        void *dst = ws.host_result_dev;
+        void *dst = on_dev ? static_cast<void *>(loss_dev) : ws.host_result_dev;
+        const double div = on_dev ? double(rows) : 0.0;
         if (MODE == CE_ASM) {
-            rc = launch_reduce(row_loss, 1, rows, rows, RedCeLoss<sizeof(T) == 4>{}, dst, nullptr, 0, tk);
+            rc = launch_reduce(row_loss, 1, rows, rows, RedCeLoss<sizeof(T) == 4>{div}, dst, nullptr, 0, tk);
         } else {
             const double st0 = alpha / double(cols), st1 = st0 + (1.0 - alpha);
-            rc = launch_reduce(row_loss, 1, rows, rows, RedLsLoss{row_s, st0 * double(cols - 1) + st1}, dst,
+            rc = launch_reduce(row_loss, 1, rows, rows, RedLsLoss{row_s, st0 * double(cols - 1) + st1, div}, dst,
                                nullptr, 0, tk);
         }
+    }
+    if (on_dev) {
+        if (row_loss) dev_free(row_loss);  // reused only by work enqueued after these launches
+        return rc;
     }
     struct { double sum; int pad[30]; int bad; } res;  // result area layout: sum at 0, flag at word 32
     static_assert(sizeof(res) == 136, "");
@@ -478,11 +502,60 @@ static int ls_ce(const T *logits, const int64_t *targets, int64_t batch, int64_t
     return 0;
 }
 
+// Label-smoothed CE on device pointers with the mean loss left in device
+// memory (*loss_dev): every launch enqueued, nothing waited for.
+template <typename T, int MODE>
+static int ls_ce_dev(const T *logits, const int64_t *targets, int64_t batch, int64_t classes, double smoothing,
+                     double *loss_dev, T *grad_dev)
+{
+    if (ensure_init() != NEURAL_OK) return -1;
+    if (!logits || !targets || !loss_dev || (MODE == CE_LS_FUSED && !grad_dev)) {
+        set_error(NEURAL_ERR_NULL_POINTER);
+        return -1;
+    }
+    int64_t n;
+    if (batch <= 0 || classes <= 0 || !(smoothing >= 0.0 && smoothing <= 1.0) ||
+        __builtin_mul_overflow(batch, classes, &n) || uint64_t(n) > kMaxRawCount) {
+        set_error(NEURAL_ERR_INVALID_ARGUMENT);
+        return -1;
+    }
+    const auto misaligned = [](const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) != 0; };
+    if (!is_device_ptr(logits) || !is_device_ptr(targets) || !is_device_ptr(loss_dev) ||
+        (grad_dev && !is_device_ptr(grad_dev)) || misaligned(logits, sizeof(T)) || misaligned(targets, 8) ||
+        misaligned(loss_dev, 8) || (grad_dev && misaligned(grad_dev, sizeof(T)))) {
+        set_error(NEURAL_ERR_INVALID_ARGUMENT);
+        return -1;
+    }
+    if (ce_run<T, MODE>(logits, targets, nullptr, batch, classes, smoothing, nullptr, grad_dev, loss_dev) !=
+        NEURAL_OK)
+        return -1;
+    set_error(NEURAL_OK);
+    return 0;
+}
+
 }  // namespace nh
 
 using namespace nh;
 
 extern "C" {
+
+int label_smoothing_ce_forward_dev(const double *logits, const int64_t *targets, int64_t batch_size,
+                                   int64_t num_classes, double smoothing, double *loss_dev)
+{
+    return ls_ce_dev<double, CE_LS_FWD>(logits, targets, batch_size, num_classes, smoothing, loss_dev, nullptr);
+}
+
+int label_smoothing_ce_fused_dev(const double *logits, const int64_t *targets, int64_t batch_size,
+                                 int64_t num_classes, double smoothing, double *loss_dev, double *grad_dev)
+{
+    return ls_ce_dev<double, CE_LS_FUSED>(logits, targets, batch_size, num_classes, smoothing, loss_dev, grad_dev);
+}
+
+int label_smoothing_ce_fused_f32_dev(const float *logits, const int64_t *targets, int64_t batch_size,
+                                     int64_t num_classes, double smoothing, double *loss_dev, float *grad_dev)
+{
+    return ls_ce_dev<float, CE_LS_FUSED>(logits, targets, batch_size, num_classes, smoothing, loss_dev, grad_dev);
+}
 
 int label_smoothing_ce_forward(const double *logits, const int64_t *targets, int64_t batch_size,
                                int64_t num_classes, double smoothing, double *loss_out)

@@ -280,6 +280,9 @@ _SIGS = {
     "label_smoothing_ce_backward": (_i, [_vp, _vp, _i64, _i64, _d, _vp]),
     "label_smoothing_ce_fused": (_i, [_vp, _vp, _i64, _i64, _d, _dp, _vp]),
     "label_smoothing_ce_fused_f32": (_i, [_vp, _vp, _i64, _i64, _d, _dp, _vp]),
+    "label_smoothing_ce_forward_dev": (_i, [_vp, _vp, _i64, _i64, _d, _vp]),
+    "label_smoothing_ce_fused_dev": (_i, [_vp, _vp, _i64, _i64, _d, _vp, _vp]),
+    "label_smoothing_ce_fused_f32_dev": (_i, [_vp, _vp, _i64, _i64, _d, _vp, _vp]),
     "neural_cross_entropy_loss": (_i, [_vp, _vp, _dp]),
     # HIP runtime controls
     "neural_hip_set_stream": (_i, [_vp]),

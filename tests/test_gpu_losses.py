@@ -203,3 +203,64 @@ def test_label_smoothing_module(pn, ora):
     m.backward_f64(ctypes.cast(g, ctypes.c_void_p))
     rel_close(np.frombuffer(g, dtype=np.float64).reshape(2, 4),
               ora.ls_ce_backward(np.array(logits).reshape(2, 4), np.array([2, 3]), 0.2)[1], 1e-12, 1e-15, "module")
+
+
+@pytest.mark.parametrize("k", [1000, 1024])
+def test_ls_ce_loss_left_in_device_memory(pn, k):
+    """The _dev forms (no reference counterpart): the host-returning forms'
+    loss and gradient bits, the loss stored in device memory; three calls
+    queue without waiting; a target out of range gives a NaN loss and does
+    not reach the next host-returning call; argument errors return -1."""
+    torch = pytest.importorskip("torch")
+    from conftest import same_bits
+    lib = pn.core._lib
+    b = 4096
+    x, t = _case(b, k, 91)  # finite logits: a NaN loss below can only come from the bad target
+    xt, tt = torch.from_numpy(x).cuda(), torch.from_numpy(t).cuda()
+    x32t = xt.float()
+    g_host, g_dev = torch.empty_like(xt), torch.full_like(xt, 7.0)
+    g32_host, g32_dev = torch.empty_like(x32t), torch.full_like(x32t, 7.0)
+    losses = torch.full((4,), 7.0, dtype=torch.float64, device="cuda")
+    torch.cuda.synchronize()
+    want = [ctypes.c_double() for _ in range(3)]
+    assert lib.label_smoothing_ce_forward(xt.data_ptr(), tt.data_ptr(), b, k, 0.1, ctypes.byref(want[0])) == 0
+    assert lib.label_smoothing_ce_fused(xt.data_ptr(), tt.data_ptr(), b, k, 0.1, ctypes.byref(want[1]),
+                                        g_host.data_ptr()) == 0
+    assert lib.label_smoothing_ce_fused_f32(x32t.data_ptr(), tt.data_ptr(), b, k, 0.1, ctypes.byref(want[2]),
+                                            g32_host.data_ptr()) == 0
+    pn.synchronize()
+    assert all(math.isfinite(w.value) for w in want)
+    p = losses.data_ptr()
+    assert lib.label_smoothing_ce_forward_dev(xt.data_ptr(), tt.data_ptr(), b, k, 0.1, p) == 0
+    assert lib.label_smoothing_ce_fused_dev(xt.data_ptr(), tt.data_ptr(), b, k, 0.1, p + 8, g_dev.data_ptr()) == 0
+    assert lib.label_smoothing_ce_fused_f32_dev(x32t.data_ptr(), tt.data_ptr(), b, k, 0.1, p + 16,
+                                                g32_dev.data_ptr()) == 0
+    pn.synchronize()
+    got = losses.cpu().numpy()
+    same_bits(got[:3], np.array([w.value for w in want]))
+    assert got[3] == 7.0  # nothing written past the three losses
+    same_bits(g_dev.cpu().numpy(), g_host.cpu().numpy())
+    same_bits(g32_dev.cpu().numpy(), g32_host.cpu().numpy())
+    # a target out of range: a NaN loss, and the next host-returning call is clean
+    t2 = t.copy()
+    t2[17] = k
+    tt2 = torch.from_numpy(t2).cuda()
+    torch.cuda.synchronize()
+    assert lib.label_smoothing_ce_forward_dev(xt.data_ptr(), tt2.data_ptr(), b, k, 0.1, p) == 0
+    pn.synchronize()
+    assert math.isnan(losses[0].item())
+    again = ctypes.c_double()
+    assert lib.label_smoothing_ce_forward(xt.data_ptr(), tt.data_ptr(), b, k, 0.1, ctypes.byref(again)) == 0
+    same_bits(np.array(again.value), np.array(want[0].value))
+    # argument errors: host memory, misalignment, NULL, sizes, smoothing
+    assert lib.label_smoothing_ce_forward_dev(x.ctypes.data, tt.data_ptr(), b, k, 0.1, p) == -1
+    assert lib.label_smoothing_ce_forward_dev(xt.data_ptr(), t.ctypes.data, b, k, 0.1, p) == -1
+    host_loss = np.zeros(1)
+    assert lib.label_smoothing_ce_forward_dev(xt.data_ptr(), tt.data_ptr(), b, k, 0.1, host_loss.ctypes.data) == -1
+    assert lib.label_smoothing_ce_forward_dev(xt.data_ptr(), tt.data_ptr(), b, k, 0.1, p + 4) == -1
+    assert lib.label_smoothing_ce_forward_dev(xt.data_ptr(), tt.data_ptr(), b, k, 0.1, None) == -1
+    assert lib.label_smoothing_ce_fused_dev(xt.data_ptr(), tt.data_ptr(), b, k, 0.1, p, None) == -1
+    assert lib.label_smoothing_ce_forward_dev(xt.data_ptr(), tt.data_ptr(), 0, k, 0.1, p) == -1
+    assert lib.label_smoothing_ce_forward_dev(xt.data_ptr(), tt.data_ptr(), b, k, 1.5, p) == -1
+    pn.synchronize()
+    assert math.isnan(losses[0].item()) and losses[3].item() == 7.0  # untouched by the refused calls
