@@ -192,6 +192,9 @@ def _c_matches(ctext, want):
     """A C type from the header is ABI-compatible with a ctypes binding: equal
     scalar widths; pointers bind as c_void_p, c_char_p (char *) or
     POINTER(T) where T is the pointee."""
+    # the multi-word spellings by their LP64 widths
+    ctext = re.sub(r"\bunsigned\s+long\s+long\b", "uint64_t", ctext)
+    ctext = re.sub(r"\blong\s+long\b", "int64_t", ctext)
     toks = [t for t in re.findall(r"[A-Za-z_][A-Za-z0-9_]*|\*", ctext) if t not in ("const", "struct", "unsigned")]
     npt = toks.count("*")
     base = [t for t in toks if t != "*"]
@@ -248,3 +251,24 @@ def test_noalloc_entry_refuses_before_init(lib):
             "print(f(ctypes.addressof(x),8,1,ctypes.addressof(p)), l.neural_get_last_error())")
     out = subprocess.run([sys.executable, "-c", code, str(LIB)], capture_output=True, text=True, timeout=120)
     assert out.stdout.split() == ["-1", "10"], (out.stdout, out.stderr)
+
+
+def test_python_bindings_match_header():
+    """Every binding in pyneural/core.py's table, the entry points without a
+    reference counterpart included, is declared in include/neural_api.h and
+    ABI-compatible with that declaration (argument count, scalar widths,
+    pointers where the header has pointers)."""
+    import sys
+    sys.path.insert(0, str(ROOT / "neural-assembly_amd"))
+    from pyneural.core import _SIGS
+    decls = _header_decls()
+    missing = [n for n in _SIGS if n not in decls]
+    assert not missing, missing
+    bad = []
+    for n, (res, args) in _SIGS.items():
+        ret, params = decls[n]
+        ok = _c_matches(ret, res) and len(params) == len(args) and \
+            all(_c_matches(p, a) for p, a in zip(params, args))
+        if not ok:
+            bad.append((n, ret, params, res, args))
+    assert not bad, bad
