@@ -167,6 +167,23 @@ class LabelSmoothingCrossEntropy(Module):
         _check_error(rc, "label_smoothing_ce_fused")
         return loss.value
 
+    def forward_f64_dev(self, logits_ptr, targets_ptr, batch_size, loss_ptr):
+        """Addition without a reference counterpart: device pointers only; the
+        mean loss goes into the double at loss_ptr (device memory) and the
+        call returns without waiting for it (label_smoothing_ce_forward_dev).
+        A target outside [0, K) makes that loss NaN."""
+        rc = _lib.label_smoothing_ce_forward_dev(logits_ptr, targets_ptr, batch_size, self.num_classes,
+                                                 self.smoothing, loss_ptr)
+        _check_error(rc, "label_smoothing_ce_forward_dev")
+        self._cached_logits, self._cached_targets, self._cached_batch_size = logits_ptr, targets_ptr, batch_size
+
+    def forward_backward_f64_dev(self, logits_ptr, targets_ptr, batch_size, grad_out_ptr, loss_ptr):
+        """forward_backward_f64 with the loss left in device memory, as
+        forward_f64_dev (label_smoothing_ce_fused_dev)."""
+        rc = _lib.label_smoothing_ce_fused_dev(logits_ptr, targets_ptr, batch_size, self.num_classes,
+                                               self.smoothing, loss_ptr, grad_out_ptr)
+        _check_error(rc, "label_smoothing_ce_fused_dev")
+
     def forward(self, logits_list, targets_list):
         bs = len(targets_list)
         nc = self.num_classes

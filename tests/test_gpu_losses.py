@@ -205,6 +205,26 @@ def test_label_smoothing_module(pn, ora):
               ora.ls_ce_backward(np.array(logits).reshape(2, 4), np.array([2, 3]), 0.2)[1], 1e-12, 1e-15, "module")
 
 
+def test_label_smoothing_module_device_loss(pn):
+    """The module's _dev methods: the host forms' loss and gradient, the loss
+    read from device memory after one synchronisation; a host pointer raises."""
+    torch = pytest.importorskip("torch")
+    m = pn.LabelSmoothingCrossEntropy(num_classes=37, smoothing=0.15)
+    x, t = _case(300, 37, 5)
+    xt, tt = torch.from_numpy(x).cuda(), torch.from_numpy(t).cuda()
+    g1, g2 = torch.empty_like(xt), torch.empty_like(xt)
+    loss = torch.zeros(2, dtype=torch.float64, device="cuda")
+    torch.cuda.synchronize()
+    want = m.forward_backward_f64(xt.data_ptr(), tt.data_ptr(), 300, g1.data_ptr())
+    m.forward_f64_dev(xt.data_ptr(), tt.data_ptr(), 300, loss.data_ptr())
+    m.forward_backward_f64_dev(xt.data_ptr(), tt.data_ptr(), 300, g2.data_ptr(), loss.data_ptr() + 8)
+    pn.synchronize()
+    assert loss.cpu().tolist() == [want, want]
+    assert torch.equal(g1, g2)
+    with pytest.raises(pn.NeuralException):
+        m.forward_f64_dev(x.ctypes.data, tt.data_ptr(), 300, loss.data_ptr())
+
+
 @pytest.mark.parametrize("k", [1000, 1024])
 def test_ls_ce_loss_left_in_device_memory(pn, k):
     """The _dev forms (no reference counterpart): the host-returning forms'
