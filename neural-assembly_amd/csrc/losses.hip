@@ -127,8 +127,15 @@ template <> NH_DEV double wave_fmax_t<double>(double v)
 // FULL: the row is exactly 64 * VPL * VN values and 16-byte aligned, so no
 // element needs a bounds check (per-element checks around the exp turn into
 // exec-mask branches).
-template <typename T, int VPL, int MODE, bool FULL>
-__global__ __launch_bounds__(256) void k_ce_wave(const T *__restrict__ x, CeArgs a, bool vec, int64_t r_base)
+//
+// WAVES: the minimum waves per SIMD the compiler must fit (1: its own
+// choice).  The f64 forward with rows of up to 1024 values takes 5 (83-84
+// VGPRs, no spills; 103 and 4 waves otherwise): 88.8-90.1 -> 82.9 us at
+// [65536,1024] (A/B in one run).  The fused and backward forms keep every
+// exp for the gradient and spill under that bound (fused f64 180 -> 331 us),
+// as do rows of 2048 doubles.
+template <typename T, int VPL, int MODE, bool FULL, int WAVES = 1>
+__global__ __launch_bounds__(256, WAVES) void k_ce_wave(const T *__restrict__ x, CeArgs a, bool vec, int64_t r_base)
 {
     using V = typename Vec16<T>::type;
     constexpr int VN = Vec16<T>::n;
@@ -330,11 +337,12 @@ __global__ __launch_bounds__(256) void k_ce_block(const T *__restrict__ x, CeArg
 template <typename T, int MODE, int VPL>
 static void launch_ce_wave(const T *x, const CeArgs &a, bool vec)
 {
+    constexpr int W = sizeof(T) == 8 && MODE == CE_LS_FWD && VPL <= 8 ? 5 : 1;
     for_row_launches(a.rows, 4, [&](unsigned g, int64_t base) {
         if (vec && a.cols == int64_t(64) * VPL * Vec16<T>::n)
-            NH_LAUNCH((k_ce_wave<T, VPL, MODE, true>), dim3(g), dim3(256), 0, stream(), x, a, vec, base);
+            NH_LAUNCH((k_ce_wave<T, VPL, MODE, true, W>), dim3(g), dim3(256), 0, stream(), x, a, vec, base);
         else
-            NH_LAUNCH((k_ce_wave<T, VPL, MODE, false>), dim3(g), dim3(256), 0, stream(), x, a, vec, base);
+            NH_LAUNCH((k_ce_wave<T, VPL, MODE, false, W>), dim3(g), dim3(256), 0, stream(), x, a, vec, base);
     });
 }
 
