@@ -549,6 +549,82 @@ void check_hooks()
     CHECK(neural_get_last_error() == NEURAL_ERR_NOT_IMPLEMENTED);
 }
 
+// Strided device views, device-side index outputs, and the edge sizes of
+// the quantization and transform entry points.
+void check_views_and_edges()
+{
+    section("views, device outputs, edge sizes");
+    // a [6, 8] f32 device buffer viewed as its transpose [8, 6] (byte strides)
+    float *d = nullptr;
+    CHECK(hipMalloc(&d, 48 * 4) == hipSuccess);
+    std::vector<float> h(48);
+    fill_host(h.data(), 48, 60);
+    CHECK(hipMemcpy(d, h.data(), 48 * 4, hipMemcpyHostToDevice) == hipSuccess);
+    const uint64_t s86[2] = {8, 6}, s68[2] = {6, 8};
+    const int64_t tstr[2] = {4, 32};
+    NeuralTensor *tv = neural_tensor_from_buffer(d, s86, 2, NEURAL_DTYPE_FLOAT32, tstr);
+    NeuralTensor *dv = neural_tensor_from_buffer(d, s68, 2, NEURAL_DTYPE_FLOAT32, nullptr);
+    NeuralTensor *o = make({8, 6}), *row = make({6});
+    CHECK(tv && dv && o && row);
+    CHECK(neural_tensor_is_contiguous(tv) == 0);
+    CHECK(neural_add(o, tv, tv) == 0);  // strided inputs through the N-D kernel
+    std::vector<float> back(48);
+    CHECK(neural_tensor_download(o, back.data(), 48 * 4) == 0);
+    CHECK(back[1] == 2.0f * h[8] && back[6] == 2.0f * h[1]);
+    NeuralTensor *c = neural_tensor_make_contiguous(tv);
+    CHECK(c != nullptr && c != tv);
+    if (c != tv) neural_tensor_free(c);
+    CHECK(neural_softmax(o, tv) != 0);         // rows must be contiguous
+    CHECK(neural_reduce_sum(tv, 0, row) == 0);  // a strided view is read through a contiguous copy
+    int64_t *didx = nullptr;
+    CHECK(hipMalloc(&didx, 6 * 8) == hipSuccess);
+    CHECK(neural_reduce_argmax(dv, 1, didx) == 0);
+    CHECK(neural_row_stats(dv, nullptr, nullptr, nullptr, didx) == 0);
+    int64_t hidx[6];
+    CHECK(neural_hip_synchronize() == 0 && hipMemcpy(hidx, didx, 48, hipMemcpyDeviceToHost) == hipSuccess);
+    CHECK(hidx[0] >= 0 && hidx[0] < 8 && hidx[5] >= 0 && hidx[5] < 8);
+    int hn = -1, hi = -1;
+    double ss = 0;
+    CHECK(neural_scan_nan_inf_l2(d, 48, &hn, &hi, &ss) == 0 && hn == 0 && hi == 0 && ss > 0);
+    CHECK(neural_tensor_grad_l2_norm(d + 3, 45) > 0.0f);  // a device pointer at an offset
+    neural_tensor_free(tv);
+    neural_tensor_free(dv);
+    neural_tensor_free(o);
+    neural_tensor_free(row);
+    CHECK(hipFree(didx) == hipSuccess && hipFree(d) == hipSuccess);
+    // percentile: n = 1 and 2, ties, zeros of both signs at the selected ranks
+    QuantParams p;
+    const double one[1] = {3.0}, two[2] = {-1.0, 1.0};
+    CHECK(calibrate_percentile(one, 1, 0.01, 0, &p) == 0);
+    CHECK(calibrate_percentile(two, 2, 0.25, 1, &p) == 0);
+    std::vector<double> z(1001, 0.0);
+    for (size_t i = 0; i < z.size(); i += 3) z[i] = -0.0;
+    z[500] = 7.0;
+    CHECK(calibrate_percentile(z.data(), int64_t(z.size()), 0.1, 0, &p) == 0);
+    CHECK(calibrate_percentile(z.data(), int64_t(z.size()), NAN, 0, &p) == -1);
+    // the int8 product at 1 x 1 x 1 and with a long K
+    QuantParams qa{0.5, 3, -1.0, 1.0, 0}, qb{0.25, -2, -1.0, 1.0, 0};
+    const int8_t a1 = 5, b1 = -7;
+    double c1 = 0;
+    CHECK(quantized_matmul(&a1, &b1, &c1, 1, 1, 1, &qa, &qb) == 0 && c1 == double((5 - 3) * (-7 + 2)) * 0.125);
+    std::vector<int8_t> A(3 * 40000, 1), B(40000 * 2, -1);
+    std::vector<double> C(6);
+    CHECK(quantized_matmul(A.data(), B.data(), C.data(), 3, 40000, 2, &qa, &qb) == 0);
+    // transforms on device pointers, one feature and one row
+    double *dx = nullptr, *dy = nullptr, *dm = nullptr, *ds = nullptr;
+    CHECK(hipMalloc(&dx, 64 * 8) == hipSuccess && hipMalloc(&dy, 64 * 8) == hipSuccess &&
+          hipMalloc(&dm, 64 * 8) == hipSuccess && hipMalloc(&ds, 64 * 8) == hipSuccess);
+    std::vector<double> hx(64);
+    fill_host(hx.data(), 64, 61);
+    CHECK(hipMemcpy(dx, hx.data(), 64 * 8, hipMemcpyHostToDevice) == hipSuccess);
+    CHECK(transform_compute_stats(dx, 64, 1, dm, ds, nullptr, nullptr) == 0);
+    CHECK(transform_compute_stats(dx, 1, 64, dm, ds, nullptr, nullptr) == 0);
+    CHECK(transform_normalize(dx, dy, 1, 64, dm, ds, 1e-8) == 0);
+    CHECK(neural_hip_synchronize() == 0);
+    CHECK(hipFree(dx) == hipSuccess && hipFree(dy) == hipSuccess && hipFree(dm) == hipSuccess &&
+          hipFree(ds) == hipSuccess);
+}
+
 // One of several host threads on the library's one stream: it creates, uses
 // and frees its own tensors, buffers and optimizer, and checks results it can
 // predict exactly, so a mix-up between threads (a shared workspace, the
@@ -643,6 +719,7 @@ int main()
     check_dropout();
     check_optimizers();
     check_hooks();
+    check_views_and_edges();
     check_threads();
     neural_shutdown();
     std::printf("host checks: %d passed, %d failed\n", g_checks - g_fail, g_fail.load());
