@@ -89,7 +89,11 @@ def test_ls_ce_vs_oracle(pn, ora, b, k, a):
     rel_close(gg, want_g, 1e-12, 2e-15 / b, "ls_ce grad")
     rc, fl, fg = _ls_gpu(pn, x, t, a, "fused")
     assert rc == 0
-    assert fl == gl  # same per-element terms, same reduction order
+    # the forward's exp comes from its LDS table (~3 ulp), the fused kernel's
+    # from the library (it keeps every e for the gradient): the row sums can
+    # differ in their last bits, so the losses agree to well inside the bar
+    _loss_close(fl, gl, bound, tol=1e-13)
+    # backward and fused share the exp, the sums and the gradient formula
     assert np.array_equal(fg.view(np.uint64), gg.view(np.uint64))
     if ora.ref() is not None:  # the reference's own C, when it travelled with the tree
         _loss_close(gl, ora.ls_ce_forward(x, t, a, use_ref=True)[1], bound)

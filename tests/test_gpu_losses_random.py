@@ -8,11 +8,13 @@ tail and the block-per-row kernel beyond them.  Smoothing is 0, 1 or uniform
 in (0, 1); N(0, 3) logits with +Inf, -Inf, NaN or a row of only -Inf planted
 in some cases.  Forward, backward and fused (host pointers, float64) are held
 to the bounds of the fixed-shape tests: loss |g - r| <= 1e-12 * sum|terms| / B
-against the oracle, gradient 1e-12 relative + 2e-15 / B, fused bits equal to
-the separate calls.  The float32 fused form on device pointers is held to
-2e-7 * sum|terms| / B for the loss and 1e-5 relative + 2e-7 / B for the
-gradient against the oracle on the widened logits.  The _dev forms must give
-the host-returning forms' loss and gradient bits.
+against the oracle, gradient 1e-12 relative + 2e-15 / B; the fused gradient's
+bits equal the backward's, the fused loss within 1e-13 * sum|terms| / B of
+the forward's (whose exp comes from a table, ~3 ulp).  The float32 fused
+form on device pointers is held to 2e-7 * sum|terms| / B for the loss and
+1e-5 relative + 2e-7 / B for the gradient against the oracle on the widened
+logits.  The _dev forms must give the host-returning forms' loss and
+gradient bits, each against the same mode.
 """
 
 import ctypes
@@ -74,7 +76,7 @@ def test_random_ls_ce_f64(pn, ora):
         rel_close(gg, want_g, 1e-12, 2e-15 / b, f"grad case {case} {b}x{k} a={a}")
         rc, fl, fg = _ls_gpu(pn, x, t, a, "fused")
         assert rc == 0
-        same_bits(np.array(fl), np.array(gl))
+        _loss_close(fl, gl, bound, tol=1e-13)  # the forward's exp is its LDS table's
         same_bits(fg, gg)
         # the _dev forms on device copies: the host forms' bits
         xt, tt = torch.from_numpy(x).cuda(), torch.from_numpy(t).cuda()
@@ -85,7 +87,7 @@ def test_random_ls_ce_f64(pn, ora):
         assert lib.label_smoothing_ce_forward_dev(xt.data_ptr(), tt.data_ptr(), b, k, a, p) == 0
         assert lib.label_smoothing_ce_fused_dev(xt.data_ptr(), tt.data_ptr(), b, k, a, p + 8, gd.data_ptr()) == 0
         pn.synchronize()
-        same_bits(losses.cpu().numpy(), np.array([gl, gl]))
+        same_bits(losses.cpu().numpy(), np.array([gl, fl]))
         same_bits(gd.cpu().numpy(), gg)
 
 
