@@ -96,6 +96,28 @@ def special_f64(n, rng, frac=0.01):
     return x
 
 
+def fmaf_exact(a, b, c):
+    """Correctly rounded float32 fma(a, b, c), elementwise.  a*b of two floats
+    is exact in double; the sum with c is rounded to odd in double (TwoSum's
+    error term says whether it was inexact and on which side), and a value
+    rounded to odd with at least two bits more than the target rounds to the
+    target as the exact value would.  Plain (double)a*b + c, rounded to
+    float afterwards, rounds twice and misses fmaf when the exact sum lies
+    just past a float tie."""
+    a64, b64, c64 = (np.asarray(v, dtype=np.float32).astype(np.float64) for v in (a, b, c))
+    with np.errstate(all="ignore"):
+        p = a64 * b64
+        s = p + c64
+        bb = s - p
+        err = (p - (s - bb)) + (c64 - bb)
+        inexact = np.isfinite(s) & (err != 0)
+        # truncate toward zero: step back one double when the exact value is smaller in magnitude
+        rz = np.where(inexact & (np.sign(err) != np.sign(s)), np.nextafter(s, 0.0), s)
+        bits = rz.view(np.uint64)
+        odd = np.where(inexact, bits | np.uint64(1), bits).view(np.float64)
+        return odd.astype(np.float32)
+
+
 _KEEP = []
 
 

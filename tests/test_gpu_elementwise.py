@@ -9,7 +9,7 @@ import ctypes
 import numpy as np
 import pytest
 
-from conftest import GPU, keep, rel_close, same_bits, special_f32, special_f64
+from conftest import GPU, fmaf_exact, keep, rel_close, same_bits, special_f32, special_f64
 
 pytestmark = GPU
 
@@ -156,8 +156,7 @@ def test_simd_raw_pointers(pn, ora, rng, n):
     assert lib.simd_mul_f32(out.ctypes.data, a.ctypes.data, b.ctypes.data, n) == 0
     same_bits(out, ora.ew(ora.MUL, a, b))
     assert lib.simd_fma_f32(out.ctypes.data, a.ctypes.data, b.ctypes.data, c.ctypes.data, n) == 0
-    fused = (a.astype(np.float64) * b.astype(np.float64) + c.astype(np.float64)).astype(np.float32)
-    same_bits(out, fused)  # a*b is exact in double, so the double sum rounds once like fmaf
+    same_bits(out, fmaf_exact(a, b, c))  # one rounding of the exact a*b + c
     e = float(np.sum(a.astype(np.float64) * b.astype(np.float64)))
     assert abs(lib.simd_dot_f32(a.ctypes.data, b.ctypes.data, n) - e) <= 1e-5 * float(np.sum(np.abs(a * b))) + 1e-30
     s = ora.sum_exact(a)
