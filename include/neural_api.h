@@ -376,8 +376,10 @@ int label_smoothing_ce_forward(const double *logits, const int64_t *targets, int
                                int64_t num_classes, double smoothing, double *loss_out);
 int label_smoothing_ce_backward(const double *logits, const int64_t *targets, int64_t batch_size,
                                 int64_t num_classes, double smoothing, double *grad_out);
-/* NEW: forward and backward in one pass over the logits (same results as the
- * two calls above). */
+/* NEW: forward and backward in one pass over the logits.  The gradient bits
+ * equal label_smoothing_ce_backward's; the loss agrees with
+ * label_smoothing_ce_forward's to a few ulps of the row terms (the f64
+ * forward takes exp from a table, this form the library's exp). */
 int label_smoothing_ce_fused(const double *logits, const int64_t *targets, int64_t batch_size,
                              int64_t num_classes, double smoothing, double *loss_out, double *grad_out);
 /* NEW: the same on f32 logits (widened exactly to double, as the reference's
@@ -388,8 +390,8 @@ int label_smoothing_ce_fused_f32(const float *logits, const int64_t *targets, in
  * loss only now and then): the forward, fused and f32 fused forms with the
  * mean loss left in device memory (*loss_dev, one double) instead of
  * returned to the host.  The call returns once its launches are enqueued on
- * the library's stream; the loss and gradient bits equal the host-returning
- * forms'.  Every pointer must be device memory, aligned to its element
+ * the library's stream; the loss and gradient bits equal those of the
+ * host-returning form of the same name without _dev.  Every pointer must be device memory, aligned to its element
  * (targets and loss_dev to 8 bytes).  Returns 0, or -1 on NULL, a host or
  * misaligned pointer, batch or num_classes <= 0, or smoothing outside
  * [0, 1]; a target outside [0, K) cannot be reported without waiting: it
