@@ -840,8 +840,8 @@ int ora_ce_loss_f32(const float *x, const float *tgt, int64_t batch, int64_t cla
         const float mx = ora_max_chain_f32(row, classes);
         float s = 0.0f;
         for (int64_t c = 0; c < classes; c++) s += (float)exp((double)row[c] - (double)mx);
-        const int32_t t = (int32_t)tgt[i];
         if (!(tgt[i] > -1.0f && tgt[i] < (float)classes)) return -1;
+        const int32_t t = (int32_t)tgt[i];  /* in range: truncation, as cvttss2si */
         const float et = (float)exp((double)row[t] - (double)mx);
         const float p = et / s;
         total += (float)(-log((double)p + 1e-7));
@@ -977,7 +977,7 @@ int ora_calibrate_percentile(const double *data, int64_t n, double percentile, i
         }
         out->scale = (cmax - cmin) / 255.0;
         if (out->scale < 1e-30) out->scale = 1e-30;
-        out->zero_point = (int32_t)round(-128.0 - cmin / out->scale);
+        out->zero_point = x86_round_to_i32(-128.0 - cmin / out->scale);
         if (out->zero_point < -128) out->zero_point = -128;
         if (out->zero_point > 127) out->zero_point = 127;
         out->min_val = cmin;
